@@ -1,0 +1,696 @@
+/*
+ * oracle.c -- CPU restatement of islhkafaa/neural-network's speculative
+ * decoding path (TEST INFRASTRUCTURE: the checker for libnnhip.so; the
+ * product never links it).  Citations are file:line in the reference tree.
+ *
+ * Scope: TransformerDecoder forward with fp32 or W8A32 Dense layers, fp32
+ * KV cache, RoPE, post-LN, SwiGLU, the fused attention arithmetic order,
+ * get_probs / sample_token, the accept / residual / bonus logic and cache
+ * rollback of generate_speculative, and generate_advanced.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* Philox4x32-10 (Random123 paper, Salmon et al. 2011).                */
+/* ------------------------------------------------------------------ */
+void or_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2],
+                      uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+  uint32_t k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+    uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+float or_uniform(uint64_t seed, uint32_t seq, uint32_t cycle, uint32_t slot) {
+  uint32_t ctr[4] = {slot, cycle, seq, 0u};
+  uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  uint32_t o[4];
+  or_philox4x32_10(ctr, key, o);
+  return (float)(o[0] >> 8) * (1.0f / 16777216.0f);
+}
+
+/* ------------------------------------------------------------------ */
+/* Model                                                               */
+/* ------------------------------------------------------------------ */
+typedef struct {
+  int64_t in, out;
+  float *w;        /* [in][out] fp32, Dense::weight_ (layer.cpp:151-160) */
+  float *b;        /* [out] */
+  int8_t *codes;   /* [in][out] int8 after quantisation */
+  float *scales;   /* [out] */
+} or_dense_t;
+
+typedef struct {
+  or_dense_t q, k, v, o, gate, up, down;
+  float *g1, *b1, *g2, *b2;
+} or_layer_t;
+
+struct or_model {
+  int vocab, d, H, F, L, max_seq;
+  float *emb;               /* [vocab][d] */
+  or_layer_t *layers;
+  or_dense_t lm;
+};
+
+struct or_cache {
+  int L, H, D, cap, len;
+  float *k, *v;             /* [L][H][cap][D] */
+};
+
+static void dense_init(or_dense_t *dn, int64_t in, int64_t out) {
+  dn->in = in; dn->out = out;
+  dn->w = (float *)calloc((size_t)(in * out), sizeof(float));
+  dn->b = (float *)calloc((size_t)out, sizeof(float));
+  dn->codes = NULL; dn->scales = NULL;
+}
+static void dense_free(or_dense_t *dn) {
+  free(dn->w); free(dn->b); free(dn->codes); free(dn->scales);
+}
+
+or_model *or_model_create(int vocab, int d, int H, int F, int L, int max_seq) {
+  if (vocab <= 0 || d <= 0 || H <= 0 || d % H != 0 || F <= 0 || L <= 0)
+    return NULL;
+  or_model *m = (or_model *)calloc(1, sizeof(or_model));
+  m->vocab = vocab; m->d = d; m->H = H; m->F = F; m->L = L;
+  m->max_seq = max_seq;
+  m->emb = (float *)calloc((size_t)vocab * d, sizeof(float));
+  m->layers = (or_layer_t *)calloc((size_t)L, sizeof(or_layer_t));
+  for (int l = 0; l < L; ++l) {
+    or_layer_t *ly = &m->layers[l];
+    dense_init(&ly->q, d, d); dense_init(&ly->k, d, d);
+    dense_init(&ly->v, d, d); dense_init(&ly->o, d, d);
+    dense_init(&ly->gate, d, F); dense_init(&ly->up, d, F);
+    dense_init(&ly->down, F, d);
+    ly->g1 = (float *)malloc(sizeof(float) * d);
+    ly->b1 = (float *)calloc((size_t)d, sizeof(float));
+    ly->g2 = (float *)malloc(sizeof(float) * d);
+    ly->b2 = (float *)calloc((size_t)d, sizeof(float));
+    for (int i = 0; i < d; ++i) { ly->g1[i] = 1.0f; ly->g2[i] = 1.0f; }
+  }
+  dense_init(&m->lm, d, vocab);
+  return m;
+}
+
+void or_model_free(or_model *m) {
+  if (!m) return;
+  for (int l = 0; l < m->L; ++l) {
+    or_layer_t *ly = &m->layers[l];
+    dense_free(&ly->q); dense_free(&ly->k); dense_free(&ly->v);
+    dense_free(&ly->o); dense_free(&ly->gate); dense_free(&ly->up);
+    dense_free(&ly->down);
+    free(ly->g1); free(ly->b1); free(ly->g2); free(ly->b2);
+  }
+  free(m->layers); free(m->emb); dense_free(&m->lm); free(m);
+}
+
+/* TransformerDecoder::parameters() order (layer.cpp:1140-1154): token_emb;
+ * per layer MHA q,k,v,o (w,b each, layer.cpp:491-502), SwiGLU gate,up,down
+ * (layer.cpp:1712-1721), LN1 gamma,beta, LN2 gamma,beta (layer.cpp:
+ * 1079-1090); lm_head w,b. */
+int or_model_num_params(const or_model *m) { return 1 + 18 * m->L + 2; }
+
+static float *param_ptr(const or_model *m, int idx, int64_t *rows,
+                        int64_t *cols) {
+  if (idx == 0) { *rows = m->vocab; *cols = m->d; return m->emb; }
+  int last = 1 + 18 * m->L;
+  if (idx == last) { *rows = m->d; *cols = m->vocab; return m->lm.w; }
+  if (idx == last + 1) { *rows = 1; *cols = m->vocab; return m->lm.b; }
+  if (idx < 0 || idx > last + 1) return NULL;
+  int l = (idx - 1) / 18, j = (idx - 1) % 18;
+  or_layer_t *ly = &m->layers[l];
+  or_dense_t *dn[7] = {&ly->q, &ly->k, &ly->v, &ly->o, &ly->gate, &ly->up,
+                       &ly->down};
+  if (j < 14) {
+    or_dense_t *x = dn[j / 2];
+    if (j % 2 == 0) { *rows = x->in; *cols = x->out; return x->w; }
+    *rows = 1; *cols = x->out; return x->b;
+  }
+  *rows = 1; *cols = m->d;
+  float *ln[4] = {ly->g1, ly->b1, ly->g2, ly->b2};
+  return ln[j - 14];
+}
+
+int or_model_param_shape(const or_model *m, int idx, int64_t *rows,
+                         int64_t *cols) {
+  return param_ptr(m, idx, rows, cols) ? 0 : -1;
+}
+
+int or_model_set_param(or_model *m, int idx, const float *data) {
+  int64_t r, c;
+  float *p = param_ptr(m, idx, &r, &c);
+  if (!p) return -1;
+  memcpy(p, data, sizeof(float) * (size_t)(r * c));
+  return 0;
+}
+
+/* QuantizedDense ctor, INT8 branch (quantization.cpp:36-66): per output
+ * column c, s_c = max_r |W[r,c]| / 127 (1 if 0); code = clamp(round(W/s),
+ * -127, 127) with round-half-away-from-zero. */
+void or_quantize_w8(const float *w, int64_t in, int64_t out, int8_t *codes,
+                    float *scales) {
+  for (int64_t c = 0; c < out; ++c) {
+    float mx = 0.0f;
+    for (int64_t r = 0; r < in; ++r) {
+      float a = fabsf(w[r * out + c]);
+      if (a > mx) mx = a;
+    }
+    float s = mx / 127.0f;
+    scales[c] = (s == 0.0f) ? 1.0f : s;
+  }
+  for (int64_t r = 0; r < in; ++r)
+    for (int64_t c = 0; c < out; ++c) {
+      float qf = roundf(w[r * out + c] / scales[c]);
+      qf = fmaxf(-127.0f, fminf(127.0f, qf));
+      codes[r * out + c] = (int8_t)qf;
+    }
+}
+
+static void dense_quantize(or_dense_t *dn) {
+  free(dn->codes); free(dn->scales);
+  dn->codes = (int8_t *)malloc((size_t)(dn->in * dn->out));
+  dn->scales = (float *)malloc(sizeof(float) * (size_t)dn->out);
+  or_quantize_w8(dn->w, dn->in, dn->out, dn->codes, dn->scales);
+}
+
+int or_model_quantize(or_model *m) {
+  for (int l = 0; l < m->L; ++l) {
+    or_layer_t *ly = &m->layers[l];
+    dense_quantize(&ly->q); dense_quantize(&ly->k); dense_quantize(&ly->v);
+    dense_quantize(&ly->o); dense_quantize(&ly->gate);
+    dense_quantize(&ly->up); dense_quantize(&ly->down);
+  }
+  dense_quantize(&m->lm);
+  return 0;
+}
+
+int or_model_get_quantized(const or_model *m, int layer, int which,
+                           int8_t *codes, float *scales) {
+  const or_dense_t *dn;
+  if (which == 7) dn = &m->lm;
+  else {
+    if (layer < 0 || layer >= m->L || which < 0 || which > 6) return -1;
+    const or_layer_t *ly = &m->layers[layer];
+    const or_dense_t *all[7] = {&ly->q, &ly->k, &ly->v, &ly->o, &ly->gate,
+                                &ly->up, &ly->down};
+    dn = all[which];
+  }
+  if (!dn->codes) return -1;
+  memcpy(codes, dn->codes, (size_t)(dn->in * dn->out));
+  memcpy(scales, dn->scales, sizeof(float) * (size_t)dn->out);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Ops                                                                 */
+/* ------------------------------------------------------------------ */
+
+/* Dense::forward (layer.cpp:162-171) and QuantizedDense::forward
+ * (quantization.cpp:127-147): y = x . W + b, W [in][out]; the quantised
+ * weight is dequantised to fp32 q*s (quantization.cpp:97-105) before the
+ * product.  Each output accumulates in fp32 in ascending k (the sgemm
+ * order of cpu_backend.cpp:366 is not fixed by the reference; this is the
+ * naive-loop order of cpu_backend.cpp:374-385). */
+void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
+              const float *w, const int8_t *codes, const float *scales,
+              const float *bias, float *y) {
+  float *wrow = (float *)malloc(sizeof(float) * (size_t)out);
+  for (int64_t i = 0; i < rows * out; ++i) y[i] = 0.0f;
+  for (int64_t k = 0; k < in; ++k) {
+    const float *wr;
+    if (codes) {
+      const int8_t *cr = codes + k * out;
+      for (int64_t n = 0; n < out; ++n) wrow[n] = (float)cr[n] * scales[n];
+      wr = wrow;
+    } else {
+      wr = w + k * out;
+    }
+    for (int64_t r = 0; r < rows; ++r) {
+      float xk = x[r * in + k];
+      float *yr = y + r * out;
+      for (int64_t n = 0; n < out; ++n) yr[n] += xk * wr[n];
+    }
+  }
+  if (bias)
+    for (int64_t r = 0; r < rows; ++r)
+      for (int64_t n = 0; n < out; ++n) y[r * out + n] = y[r * out + n] + bias[n];
+  free(wrow);
+}
+
+static void dense_fwd(const or_dense_t *dn, const float *x, int64_t rows,
+                      float *y) {
+  or_dense(x, rows, dn->in, dn->out, dn->w, dn->codes, dn->scales, dn->b, y);
+}
+
+/* Tensor::rope (tensor.cpp:1141-1173), x [H][S][D] in place. */
+void or_rope(float *x, int64_t H, int64_t S, int64_t D, int64_t s_past) {
+  for (int64_t h = 0; h < H; ++h)
+    for (int64_t s = 0; s < S; ++s) {
+      float m = (float)(s_past + s);
+      for (int64_t j = 0; j < D / 2; ++j) {
+        float theta = powf(10000.0f, -2.0f * (float)j / (float)D);
+        float omega = m * theta;
+        float c = cosf(omega), sn = sinf(omega);
+        float *p = x + (h * S + s) * D + 2 * j;
+        float xe = p[0], xo = p[1];
+        p[0] = xe * c - xo * sn;
+        p[1] = xe * sn + xo * c;
+      }
+    }
+}
+
+/* LayerNorm::forward (layer.cpp:242-261) with the backend sum of
+ * cpu_backend.cpp:389-459 (ascending index): mean = sum/N,
+ * var = sum((x-mean)^2)/N, y = (x-mean)/sqrt(var+eps)*gamma + beta. */
+void or_layernorm(const float *x, int64_t rows, int64_t n, const float *gamma,
+                  const float *beta, float eps, float *y) {
+  float N = (float)n;
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *xr = x + r * n;
+    float s = 0.0f;
+    for (int64_t i = 0; i < n; ++i) s += xr[i];
+    float mean = s / N;
+    float sq = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+      float df = xr[i] - mean;
+      sq += df * df;
+    }
+    float var = sq / N;
+    float sd = sqrtf(var + eps);
+    for (int64_t i = 0; i < n; ++i) {
+      float xh = (xr[i] - mean) / sd;
+      y[r * n + i] = xh * gamma[i] + beta[i];
+    }
+  }
+}
+
+/* Fused attention of MultiHeadAttention::forward (layer.cpp:842-952):
+ * score = dot/sqrt(D); masked positions (j > S_past + i) skip the max and
+ * get probability 0; p = exp(s - max) * (1/sum); out[d] = sum_j p_j v_j[d]
+ * in ascending j, skipping p == 0. */
+void or_attention(const float *q, const float *k, const float *v, int64_t H,
+                  int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
+                  int causal, float *out) {
+  int64_t S_past = S_total - S;
+  int64_t group = H / H_kv;
+  float scale = sqrtf((float)D);
+  float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
+  for (int64_t h = 0; h < H; ++h) {
+    int64_t hk = h / group;
+    for (int64_t i = 0; i < S; ++i) {
+      float mx = -INFINITY;
+      const float *qi = q + (h * S + i) * D;
+      for (int64_t j = 0; j < S_total; ++j) {
+        if (causal && j > S_past + i) { row[j] = -1e9f; continue; }
+        const float *kj = k + (hk * S_total + j) * D;
+        float dot = 0.0f;
+        for (int64_t dd = 0; dd < D; ++dd) dot += qi[dd] * kj[dd];
+        float sc = dot / scale;
+        row[j] = sc;
+        if (sc > mx) mx = sc;
+      }
+      float sum = 0.0f;
+      for (int64_t j = 0; j < S_total; ++j) {
+        if (causal && j > S_past + i) { row[j] = 0.0f; continue; }
+        float e = expf(row[j] - mx);
+        row[j] = e;
+        sum += e;
+      }
+      if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (int64_t j = 0; j < S_total; ++j) row[j] *= inv;
+      }
+      float *o = out + (i * H + h) * D;
+      for (int64_t dd = 0; dd < D; ++dd) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < S_total; ++j) {
+          if (row[j] == 0.0f) continue;
+          acc += row[j] * v[(hk * S_total + j) * D + dd];
+        }
+        o[dd] = acc;
+      }
+    }
+  }
+  free(row);
+}
+
+/* ------------------------------------------------------------------ */
+/* Cache and forward                                                   */
+/* ------------------------------------------------------------------ */
+or_cache *or_cache_create(const or_model *m) {
+  or_cache *c = (or_cache *)calloc(1, sizeof(or_cache));
+  c->L = m->L; c->H = m->H; c->D = m->d / m->H; c->cap = m->max_seq;
+  size_t n = (size_t)c->L * c->H * c->cap * c->D;
+  c->k = (float *)calloc(n, sizeof(float));
+  c->v = (float *)calloc(n, sizeof(float));
+  c->len = 0;
+  return c;
+}
+void or_cache_free(or_cache *c) {
+  if (!c) return;
+  free(c->k); free(c->v); free(c);
+}
+int or_cache_len(const or_cache *c) { return c->len; }
+/* KVCache::truncate (layer.cpp:67-149): keep the first len positions. */
+void or_cache_truncate(or_cache *c, int len) {
+  if (len < c->len) c->len = len;
+}
+
+/* TransformerDecoder::forward (layer.cpp:1161-1193) for B = 1:
+ * embedding gather with out-of-range ids -> row 0 (cpu_backend.cpp:
+ * 1020-1025), decoder layers (layer.cpp:1097-1114), lm_head. */
+int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
+               float *logits) {
+  int d = m->d, H = m->H, D = d / H, F = m->F;
+  int S_past = cache ? cache->len : 0;
+  if (S_past + S > m->max_seq) return -1;
+  int S_total = S_past + S;
+  size_t sd = (size_t)S * d;
+  float *x = (float *)malloc(sizeof(float) * sd);
+  float *q = (float *)malloc(sizeof(float) * sd);
+  float *kk = (float *)malloc(sizeof(float) * sd);
+  float *vv = (float *)malloc(sizeof(float) * sd);
+  float *qh = (float *)malloc(sizeof(float) * sd);
+  float *ctx = (float *)malloc(sizeof(float) * sd);
+  float *t1 = (float *)malloc(sizeof(float) * sd);
+  float *x1 = (float *)malloc(sizeof(float) * sd);
+  float *g = (float *)malloc(sizeof(float) * (size_t)S * F);
+  float *u = (float *)malloc(sizeof(float) * (size_t)S * F);
+  float *kt = NULL, *vt = NULL;
+  if (!cache) {
+    kt = (float *)malloc(sizeof(float) * sd);
+    vt = (float *)malloc(sizeof(float) * sd);
+  }
+  for (int s = 0; s < S; ++s) {
+    int64_t id = ids[s];
+    if (id < 0 || id >= m->vocab) id = 0;
+    memcpy(x + (size_t)s * d, m->emb + (size_t)id * d, sizeof(float) * d);
+  }
+  for (int l = 0; l < m->L; ++l) {
+    const or_layer_t *ly = &m->layers[l];
+    /* MultiHeadAttention::forward (layer.cpp:593-994) */
+    dense_fwd(&ly->q, x, S, q);
+    dense_fwd(&ly->k, x, S, kk);
+    dense_fwd(&ly->v, x, S, vv);
+    /* [S][H][D] -> [H][S][D] (transpose(1,2), layer.cpp:619-621) */
+    float *kh = cache ? (float *)malloc(sizeof(float) * sd) : kt;
+    float *vh = cache ? (float *)malloc(sizeof(float) * sd) : vt;
+    for (int h = 0; h < H; ++h)
+      for (int s = 0; s < S; ++s)
+        for (int e = 0; e < D; ++e) {
+          size_t src = (size_t)s * d + h * D + e;
+          size_t dst = ((size_t)h * S + s) * D + e;
+          qh[dst] = q[src]; kh[dst] = kk[src]; vh[dst] = vv[src];
+        }
+    or_rope(qh, H, S, D, S_past);
+    or_rope(kh, H, S, D, S_past);
+    if (cache) {
+      /* KV append (layer.cpp:758-807) */
+      size_t lay = (size_t)l * H * cache->cap * D;
+      for (int h = 0; h < H; ++h)
+        for (int s = 0; s < S; ++s) {
+          size_t dst = lay + ((size_t)h * cache->cap + S_past + s) * D;
+          memcpy(cache->k + dst, kh + ((size_t)h * S + s) * D,
+                 sizeof(float) * D);
+          memcpy(cache->v + dst, vh + ((size_t)h * S + s) * D,
+                 sizeof(float) * D);
+        }
+      /* gather the live cache rows of this layer as [H][S_total][D] */
+      float *K = (float *)malloc(sizeof(float) * (size_t)H * S_total * D);
+      float *V = (float *)malloc(sizeof(float) * (size_t)H * S_total * D);
+      for (int h = 0; h < H; ++h) {
+        memcpy(K + (size_t)h * S_total * D,
+               cache->k + lay + (size_t)h * cache->cap * D,
+               sizeof(float) * (size_t)S_total * D);
+        memcpy(V + (size_t)h * S_total * D,
+               cache->v + lay + (size_t)h * cache->cap * D,
+               sizeof(float) * (size_t)S_total * D);
+      }
+      or_attention(qh, K, V, H, H, S, S_total, D, 1, ctx);
+      free(K); free(V); free(kh); free(vh);
+    } else {
+      or_attention(qh, kh, vh, H, H, S, S, D, 1, ctx);
+    }
+    dense_fwd(&ly->o, ctx, S, t1);
+    /* x1 = LN1(x + attn) (layer.cpp:1102; dropout is identity in eval) */
+    for (size_t i = 0; i < sd; ++i) t1[i] = x[i] + t1[i];
+    or_layernorm(t1, S, d, ly->g1, ly->b1, 1e-5f, x1);
+    /* SwiGLU (layer.cpp:1704-1710): (g * sigmoid(g)) * u -> down;
+     * sigmoid = 1/(1+exp(-x)) (cpu_backend.cpp:483-489) */
+    dense_fwd(&ly->gate, x1, S, g);
+    dense_fwd(&ly->up, x1, S, u);
+    for (size_t i = 0; i < (size_t)S * F; ++i) {
+      float sg = 1.0f / (1.0f + expf(-g[i]));
+      float a = g[i] * sg;
+      g[i] = a * u[i];
+    }
+    dense_fwd(&ly->down, g, S, t1);
+    for (size_t i = 0; i < sd; ++i) t1[i] = x1[i] + t1[i];
+    or_layernorm(t1, S, d, ly->g2, ly->b2, 1e-5f, x);
+  }
+  dense_fwd(&m->lm, x, S, logits);
+  if (cache) cache->len = S_total;
+  free(x); free(q); free(kk); free(vv); free(qh); free(ctx); free(t1);
+  free(x1); free(g); free(u); free(kt); free(vt);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Sampling                                                            */
+/* ------------------------------------------------------------------ */
+
+/* First index of the maximum (strict >, layer.cpp:1413-1421;
+ * std::max_element, layer.cpp:1591-1593). */
+int or_argmax(const float *x, int V) {
+  int a = 0;
+  float mx = x[0];
+  for (int v = 1; v < V; ++v)
+    if (x[v] > mx) { mx = x[v]; a = v; }
+  return a;
+}
+
+typedef struct { float p; int i; } or_pi;
+static int cmp_desc(const void *a, const void *b) {
+  const or_pi *x = (const or_pi *)a, *y = (const or_pi *)b;
+  if (x->p > y->p) return -1;
+  if (x->p < y->p) return 1;
+  return (x->i < y->i) ? -1 : (x->i > y->i);
+}
+
+/* get_probs (layer.cpp:1410-1491).  T <= 0: one-hot at the first argmax.
+ * Else logits/T, max-subtract, exp, float sum in index order, divide; then
+ * sort descending, zero beyond top_k, zero after the cumulative sum first
+ * reaches top_p, final_sum in sorted order, divide again.  Ties in the sort
+ * are broken by index (std::sort leaves them unspecified; they change
+ * nothing unless top_k/top_p cut between equal probabilities). */
+void or_get_probs(const float *logits, int V, float T, int top_k, float top_p,
+                  float *probs) {
+  if (V <= 0) return;
+  if (T <= 0.0f) {
+    for (int v = 0; v < V; ++v) probs[v] = 0.0f;
+    probs[or_argmax(logits, V)] = 1.0f;
+    return;
+  }
+  float *sl = (float *)malloc(sizeof(float) * V);
+  for (int v = 0; v < V; ++v) sl[v] = logits[v] / T;
+  float mx = sl[0];
+  for (int v = 1; v < V; ++v) if (sl[v] > mx) mx = sl[v];
+  float sum = 0.0f;
+  for (int v = 0; v < V; ++v) { probs[v] = expf(sl[v] - mx); sum += probs[v]; }
+  for (int v = 0; v < V; ++v) probs[v] /= sum;
+  or_pi *ip = (or_pi *)malloc(sizeof(or_pi) * V);
+  for (int v = 0; v < V; ++v) { ip[v].p = probs[v]; ip[v].i = v; }
+  qsort(ip, (size_t)V, sizeof(or_pi), cmp_desc);
+  if (top_k > 0 && top_k < V)
+    for (int i = top_k; i < V; ++i) ip[i].p = 0.0f;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    float cs = 0.0f;
+    int cut = 0;
+    for (int i = 0; i < V; ++i) {
+      if (cut) ip[i].p = 0.0f;
+      else { cs += ip[i].p; if (cs >= top_p) cut = 1; }
+    }
+  }
+  float fs = 0.0f;
+  for (int v = 0; v < V; ++v) fs += ip[v].p;
+  for (int v = 0; v < V; ++v) probs[v] = 0.0f;
+  if (fs <= 0.0f) probs[ip[0].i] = 1.0f;
+  else for (int v = 0; v < V; ++v) probs[ip[v].i] = ip[v].p / fs;
+  free(ip); free(sl);
+}
+
+/* sample_token (layer.cpp:1493-1498) = std::discrete_distribution<size_t>
+ * over the probabilities widened to double (libstdc++ random.tcc:
+ * normalise by the double sum, partial_sum, last entry forced to 1.0,
+ * lower_bound of the uniform): the first v with cdf[v] >= u. */
+int or_sample(const float *probs, int V, double u) {
+  if (V < 2) return 0;
+  double sum = 0.0;
+  for (int v = 0; v < V; ++v) sum += (double)probs[v];
+  double c = 0.0;
+  for (int v = 0; v < V - 1; ++v) {
+    c += (double)probs[v] / sum;
+    if (c >= u) return v;
+  }
+  return V - 1;
+}
+
+/* Draws of the speculative loop: greedy mode (T <= 0) samples only one-hot
+ * vectors, where discrete_distribution returns the hot index; the oracle
+ * takes it directly and consumes no uniform. */
+static int draw(const float *probs, int V, int greedy, uint64_t seed,
+                uint32_t seq, uint32_t cycle, uint32_t slot) {
+  if (greedy) return or_argmax(probs, V);
+  return or_sample(probs, V, (double)or_uniform(seed, seq, cycle, slot));
+}
+
+/* generate_speculative (layer.cpp:1382-1661) for one sequence. */
+int or_generate_speculative(const or_model *t, const or_model *dm,
+                            const int32_t *prompt, int P, int max_new, int k,
+                            float T, int top_k, float top_p, uint64_t seed,
+                            uint32_t seq, int32_t *out, or_spec_stats *st) {
+  int V = t->vocab;
+  int greedy = T <= 0.0f;
+  if (dm->vocab != V || P <= 0 || k <= 0 || k > 63) return -2;
+  or_spec_stats local;
+  memset(&local, 0, sizeof(local));
+  or_cache *tc = or_cache_create(t), *dc = or_cache_create(dm);
+  float *tl = (float *)malloc(sizeof(float) * (size_t)(P > k + 1 ? P : k + 1) * V);
+  float *dl = (float *)malloc(sizeof(float) * (size_t)P * V);
+  float *q = (float *)malloc(sizeof(float) * (size_t)k * V);
+  float *p = (float *)malloc(sizeof(float) * (size_t)(k + 1) * V);
+  float *rec = (float *)malloc(sizeof(float) * V);
+  int32_t *cand = (int32_t *)malloc(sizeof(int32_t) * (k + 1));
+  int rc = 0;
+  int n = 0;
+  for (int i = 0; i < P; ++i) out[n++] = prompt[i];
+  /* prefill (layer.cpp:1400-1408) */
+  if (or_forward(t, tc, prompt, P, tl) || or_forward(dm, dc, prompt, P, dl)) {
+    rc = -1; goto done;
+  }
+  or_get_probs(tl + (size_t)(P - 1) * V, V, T, top_k, top_p, p);
+  out[n++] = draw(p, V, greedy, seed, seq, 0, 2 * k);
+  int ngen = 1;
+  uint32_t cycle = 0;
+  while (ngen < max_new) {
+    int M = k < max_new - ngen ? k : max_new - ngen;
+    ++cycle;
+    int tstart = tc->len, dstart = dc->len;
+    /* draft loop (layer.cpp:1541-1558) */
+    for (int j = 0; j < M; ++j) {
+      int32_t in = j == 0 ? out[n - 1] : cand[j - 1];
+      if (or_forward(dm, dc, &in, 1, dl)) { rc = -1; goto done; }
+      or_get_probs(dl, V, T, top_k, top_p, q + (size_t)j * V);
+      cand[j] = draw(q + (size_t)j * V, V, greedy, seed, seq, cycle, j);
+    }
+    /* verify (layer.cpp:1560-1579) */
+    int32_t tin[64];
+    tin[0] = out[n - 1];
+    for (int j = 0; j < M; ++j) tin[j + 1] = cand[j];
+    if (or_forward(t, tc, tin, M + 1, tl)) { rc = -1; goto done; }
+    for (int i = 0; i <= M; ++i)
+      or_get_probs(tl + (size_t)i * V, V, T, top_k, top_p, p + (size_t)i * V);
+    /* accept (layer.cpp:1581-1609) */
+    int all = 1, rej = 0;
+    for (int j = 0; j < M; ++j) {
+      int c = cand[j];
+      float qc = q[(size_t)j * V + c], pc = p[(size_t)j * V + c];
+      int acc;
+      if (greedy) {
+        acc = c == or_argmax(p + (size_t)j * V, V);
+      } else {
+        float r = or_uniform(seed, seq, cycle, k + j);
+        acc = r * qc < pc;
+        if (fabs((double)r - (double)pc / (double)qc) < 1e-6) local.ties++;
+      }
+      if (acc) { out[n++] = c; ngen++; local.accepted++; }
+      else { all = 0; rej = j; break; }
+    }
+    local.cycles++;
+    local.drafted += M;
+    if (!all) {
+      /* residual resample (layer.cpp:1611-1630) */
+      const float *pr = p + (size_t)rej * V, *qr = q + (size_t)rej * V;
+      float sr = 0.0f;
+      for (int v = 0; v < V; ++v) {
+        rec[v] = fmaxf(0.0f, pr[v] - qr[v]);
+        sr += rec[v];
+      }
+      int tok;
+      if (sr <= 0.0f) tok = draw(pr, V, greedy, seed, seq, cycle, 2 * k);
+      else {
+        for (int v = 0; v < V; ++v) rec[v] /= sr;
+        tok = draw(rec, V, greedy, seed, seq, cycle, 2 * k);
+      }
+      out[n++] = tok; ngen++; local.resampled++;
+      /* rollback (layer.cpp:1632-1637) and draft catch-up (:1639-1642) */
+      or_cache_truncate(tc, tstart + rej + 1);
+      or_cache_truncate(dc, dstart + rej + 1);
+      if (or_forward(dm, dc, &tok, 1, dl)) { rc = -1; goto done; }
+    } else if (ngen < max_new) {
+      /* bonus sample and draft catch-up (layer.cpp:1643-1655) */
+      int tok = draw(p + (size_t)M * V, V, greedy, seed, seq, cycle, 2 * k);
+      out[n++] = tok; ngen++; local.bonus++;
+      int32_t last = cand[M - 1];
+      if (or_forward(dm, dc, &last, 1, dl)) { rc = -1; goto done; }
+    }
+  }
+done:
+  if (st) *st = local;
+  or_cache_free(tc); or_cache_free(dc);
+  free(tl); free(dl); free(q); free(p); free(rec); free(cand);
+  return rc;
+}
+
+/* generate_advanced (layer.cpp:1240-1380) for one sequence.  Sampled mode
+ * draws u[seq][step][0]; greedy takes the first argmax. */
+int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
+                         int max_new, float T, int top_k, float top_p,
+                         uint64_t seed, uint32_t seq, int use_cache,
+                         int32_t *out) {
+  int V = m->vocab;
+  int total = P + max_new;
+  for (int i = 0; i < P; ++i) out[i] = prompt[i];
+  int n = P;
+  or_cache *c = use_cache ? or_cache_create(m) : NULL;
+  float *lg = (float *)malloc(sizeof(float) * (size_t)total * V);
+  float *pr = (float *)malloc(sizeof(float) * V);
+  int rc = 0;
+  for (int step = 0; step < max_new; ++step) {
+    int S;
+    const int32_t *in;
+    if (use_cache && step > 0) { S = 1; in = out + n - 1; }
+    else {
+      S = n;
+      int start = 0;
+      if (S > m->max_seq) { start = S - m->max_seq; S = m->max_seq; }
+      in = out + start;
+    }
+    if (or_forward(m, c, in, S, lg)) { rc = -1; break; }
+    const float *last = lg + (size_t)(S - 1) * V;
+    int tok;
+    if (T <= 0.0f) tok = or_argmax(last, V);
+    else {
+      or_get_probs(last, V, T, top_k, top_p, pr);
+      tok = or_sample(pr, V, (double)or_uniform(seed, seq, (uint32_t)step, 0));
+    }
+    out[n++] = tok;
+  }
+  or_cache_free(c);
+  free(lg); free(pr);
+  return rc;
+}

@@ -1,0 +1,114 @@
+/*
+ * oracle.h -- CPU restatement of the reference's speculative-decoding path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * product (libnnhip.so).  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  The product never links it.
+ *
+ * Every function restates the arithmetic of islhkafaa/neural-network's CPU
+ * backend path in plain C, in the same fp32 operation order where the
+ * reference fixes one (file:line citations at each definition in oracle.c).
+ * Compiled with -ffp-contract=off so that no multiply-add is fused, as in
+ * the reference's x86-64 build.
+ *
+ * Uniform source: the reference draws from std::mt19937 through libstdc++
+ * distributions.  The oracle and the device path instead share one
+ * counter-based Philox4x32-10 stream, addressed as u[seq][cycle][slot]:
+ *   slots 0..k-1   draft sampling of step j
+ *   slots k..2k-1  accept test of position j
+ *   slot  2k       residual resample or bonus sample
+ *   cycle 0, slot 2k: the first token after prefill.
+ * generate_advanced's sampled mode uses u[seq][step][0].
+ */
+#ifndef NN_ORACLE_H
+#define NN_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct or_model or_model;
+typedef struct or_cache or_cache;
+
+typedef struct {
+  int64_t cycles;       /* speculative cycles run after the first token */
+  int64_t drafted;      /* sum of M over cycles */
+  int64_t accepted;     /* accepted draft tokens */
+  int64_t ties;         /* accept tests with |r - p/q| < 1e-6 */
+  int64_t resampled;    /* cycles that ended in a residual resample */
+  int64_t bonus;        /* cycles that ended in a bonus sample */
+} or_spec_stats;
+
+/* Philox4x32-10 (Salmon et al., SC'11), the counter-based generator shared
+ * with the device path. */
+void or_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2],
+                      uint32_t out[4]);
+/* u[seq][cycle][slot] in [0,1): the top 24 bits of word 0, times 2^-24. */
+float or_uniform(uint64_t seed, uint32_t seq, uint32_t cycle, uint32_t slot);
+
+/* Model: TransformerDecoder(vocab, d, heads, d_ff, layers, max_seq_len). */
+or_model *or_model_create(int vocab, int d_model, int n_heads, int d_ff,
+                          int n_layers, int max_seq_len);
+void or_model_free(or_model *m);
+int or_model_num_params(const or_model *m);
+/* Shape of parameter idx in TransformerDecoder::parameters() order. */
+int or_model_param_shape(const or_model *m, int idx, int64_t *rows,
+                         int64_t *cols);
+int or_model_set_param(or_model *m, int idx, const float *data);
+/* Quantise every Dense (q,k,v,o,gate,up,down,lm_head) to symmetric int8
+ * per output channel; the embedding stays fp32. */
+int or_model_quantize(or_model *m);
+/* Read back int8 codes ([in,out] reference layout) and scales of a Dense.
+ * which: 0..6 = q,k,v,o,gate,up,down of layer `layer`; 7 = lm_head. */
+int or_model_get_quantized(const or_model *m, int layer, int which,
+                           int8_t *codes, float *scales);
+
+or_cache *or_cache_create(const or_model *m);
+void or_cache_free(or_cache *c);
+int or_cache_len(const or_cache *c);
+void or_cache_truncate(or_cache *c, int len);
+
+/* TransformerDecoder::forward for one sequence of S ids; logits [S][V].
+ * cache may be NULL.  Returns 0, or -1 when S_past + S > max_seq_len. */
+int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
+               float *logits);
+
+/* Unit restatements used by kernel-level parity tests. */
+void or_quantize_w8(const float *w, int64_t in, int64_t out, int8_t *codes,
+                    float *scales);
+void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
+              const float *w, const int8_t *codes, const float *scales,
+              const float *bias, float *y);
+void or_rope(float *x, int64_t heads, int64_t S, int64_t D, int64_t s_past);
+void or_layernorm(const float *x, int64_t rows, int64_t n, const float *gamma,
+                  const float *beta, float eps, float *y);
+/* Fused attention for one sequence: q [H][S][D] (already rotated),
+ * k/v [H_kv][S_total][D] (cache after append), out [S][H][D]. */
+void or_attention(const float *q, const float *k, const float *v, int64_t H,
+                  int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
+                  int causal, float *out);
+
+/* get_probs and sample_token of generate_speculative. */
+void or_get_probs(const float *logits, int V, float temperature, int top_k,
+                  float top_p, float *probs);
+int or_sample(const float *probs, int V, double u);
+int or_argmax(const float *x, int V);
+
+/* generate_speculative for one sequence; out receives P + max_new ids. */
+int or_generate_speculative(const or_model *target, const or_model *draft,
+                            const int32_t *prompt, int P, int max_new,
+                            int lookahead, float temperature, int top_k,
+                            float top_p, uint64_t seed, uint32_t seq_index,
+                            int32_t *out, or_spec_stats *stats);
+/* generate_advanced for one sequence; out receives P + max_new ids. */
+int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
+                         int max_new, float temperature, int top_k,
+                         float top_p, uint64_t seed, uint32_t seq_index,
+                         int use_kv_cache, int32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,228 @@
+"""ctypes view of oracle/liboracle.so (the CPU checker) for the tests.
+
+The oracle restates the reference's CPU path; see oracle/oracle.h.  This
+module also generates the seeded synthetic weights the tests share between
+the oracle and the device library.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+
+_lib = None
+
+
+class SpecStats(C.Structure):
+    _fields_ = [("cycles", C.c_int64), ("drafted", C.c_int64),
+                ("accepted", C.c_int64), ("ties", C.c_int64),
+                ("resampled", C.c_int64), ("bonus", C.c_int64)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.check_call(["make", "-s", "-C", ORACLE_DIR])
+        L = C.CDLL(LIB_PATH)
+        vp, i32, i64, f32, u32, u64 = (C.c_void_p, C.c_int, C.c_int64,
+                                       C.c_float, C.c_uint32, C.c_uint64)
+        fp = C.POINTER(C.c_float)
+        ip = C.POINTER(C.c_int32)
+        L.or_philox4x32_10.argtypes = [C.POINTER(u32), C.POINTER(u32),
+                                       C.POINTER(u32)]
+        L.or_uniform.argtypes = [u64, u32, u32, u32]
+        L.or_uniform.restype = f32
+        L.or_model_create.argtypes = [i32] * 6
+        L.or_model_create.restype = vp
+        L.or_model_free.argtypes = [vp]
+        L.or_model_num_params.argtypes = [vp]
+        L.or_model_param_shape.argtypes = [vp, i32, C.POINTER(i64),
+                                           C.POINTER(i64)]
+        L.or_model_set_param.argtypes = [vp, i32, fp]
+        L.or_model_quantize.argtypes = [vp]
+        L.or_model_get_quantized.argtypes = [vp, i32, i32,
+                                             C.POINTER(C.c_int8), fp]
+        L.or_cache_create.argtypes = [vp]
+        L.or_cache_create.restype = vp
+        L.or_cache_free.argtypes = [vp]
+        L.or_cache_len.argtypes = [vp]
+        L.or_cache_truncate.argtypes = [vp, i32]
+        L.or_forward.argtypes = [vp, vp, ip, i32, fp]
+        L.or_quantize_w8.argtypes = [fp, i64, i64, C.POINTER(C.c_int8), fp]
+        L.or_dense.argtypes = [fp, i64, i64, i64, fp, C.POINTER(C.c_int8),
+                               fp, fp, fp]
+        L.or_rope.argtypes = [fp, i64, i64, i64, i64]
+        L.or_layernorm.argtypes = [fp, i64, i64, fp, fp, f32, fp]
+        L.or_attention.argtypes = [fp, fp, fp, i64, i64, i64, i64, i64, i32,
+                                   fp]
+        L.or_get_probs.argtypes = [fp, i32, f32, i32, f32, fp]
+        L.or_sample.argtypes = [fp, i32, C.c_double]
+        L.or_argmax.argtypes = [fp, i32]
+        L.or_generate_speculative.argtypes = [vp, vp, ip, i32, i32, i32, f32,
+                                              i32, f32, u64, u32, ip,
+                                              C.POINTER(SpecStats)]
+        L.or_generate_advanced.argtypes = [vp, ip, i32, i32, f32, i32, f32,
+                                           u64, u32, i32, ip]
+        _lib = L
+    return _lib
+
+
+def fptr(a):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def iptr(a):
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def i8ptr(a):
+    assert a.dtype == np.int8 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
+
+
+def philox(ctr, key):
+    out = (C.c_uint32 * 4)()
+    lib().or_philox4x32_10((C.c_uint32 * 4)(*ctr), (C.c_uint32 * 2)(*key), out)
+    return list(out)
+
+
+def uniform(seed, seq, cycle, slot):
+    return lib().or_uniform(seed, seq, cycle, slot)
+
+
+# ----------------------------------------------------------------------------
+# Seeded synthetic decoder weights, TransformerDecoder::parameters() order:
+# Dense weights and the embedding ~ N(0, std), biases 0, LayerNorm gamma 1,
+# beta 0.  Shapes follow the reference ([in, out] Dense weights).
+# ----------------------------------------------------------------------------
+def param_shapes(vocab, d, H, F, L):
+    shapes = [("emb", (vocab, d))]
+    for l in range(L):
+        for nm, (i, o) in (("q", (d, d)), ("k", (d, d)), ("v", (d, d)),
+                           ("o", (d, d)), ("gate", (d, F)), ("up", (d, F)),
+                           ("down", (F, d))):
+            shapes.append((f"{nm}.w", (i, o)))
+            shapes.append((f"{nm}.b", (1, o)))
+        for nm in ("ln1.g", "ln1.b", "ln2.g", "ln2.b"):
+            shapes.append((nm, (1, d)))
+    shapes.append(("lm.w", (d, vocab)))
+    shapes.append(("lm.b", (1, vocab)))
+    return shapes
+
+
+def make_params(vocab, d, H, F, L, seed, std=0.02, bias_std=0.0):
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shp in param_shapes(vocab, d, H, F, L):
+        if name.endswith(".w") or name == "emb":
+            a = (rng.standard_normal(shp, dtype=np.float32) * np.float32(std))
+        elif name.endswith(".g"):
+            a = np.ones(shp, np.float32)
+        else:
+            a = (rng.standard_normal(shp, dtype=np.float32) *
+                 np.float32(bias_std)) if bias_std else np.zeros(shp,
+                                                                 np.float32)
+        out.append(np.ascontiguousarray(a, dtype=np.float32))
+    return out
+
+
+class Model:
+    """Oracle TransformerDecoder(vocab, d, heads, d_ff, layers, max_seq)."""
+
+    def __init__(self, vocab, d, H, F, L, max_seq, params, quantize=False):
+        self.vocab, self.d, self.H, self.F, self.L = vocab, d, H, F, L
+        self.max_seq = max_seq
+        self.h = lib().or_model_create(vocab, d, H, F, L, max_seq)
+        assert self.h
+        assert lib().or_model_num_params(self.h) == len(params)
+        for i, p in enumerate(params):
+            r, c = C.c_int64(), C.c_int64()
+            lib().or_model_param_shape(self.h, i, C.byref(r), C.byref(c))
+            assert r.value * c.value == p.size, (i, p.shape)
+            assert lib().or_model_set_param(self.h, i, fptr(p)) == 0
+        if quantize:
+            lib().or_model_quantize(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_model_free(self.h)
+            self.h = None
+
+    def quantized(self, layer, which, n_in, n_out):
+        codes = np.zeros((n_in, n_out), np.int8)
+        scales = np.zeros(n_out, np.float32)
+        assert lib().or_model_get_quantized(self.h, layer, which,
+                                            i8ptr(codes), fptr(scales)) == 0
+        return codes, scales
+
+    def forward(self, ids, cache=None):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((len(ids), self.vocab), np.float32)
+        rc = lib().or_forward(self.h, cache.h if cache is not None else None,
+                              iptr(ids),
+                              len(ids), fptr(out))
+        if rc != 0:
+            raise RuntimeError(
+                "Sequence length S plus past cached length exceeds max_seq_len")
+        return out
+
+
+class Cache:
+    def __init__(self, model):
+        self.h = lib().or_cache_create(model.h)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_cache_free(self.h)
+            self.h = None
+
+    def __len__(self):
+        return lib().or_cache_len(self.h)
+
+    def truncate(self, n):
+        lib().or_cache_truncate(self.h, n)
+
+
+def get_probs(logits, T, top_k=0, top_p=1.0):
+    logits = np.ascontiguousarray(logits, np.float32)
+    out = np.zeros_like(logits)
+    lib().or_get_probs(fptr(logits), logits.size, T, top_k, top_p, fptr(out))
+    return out
+
+
+def sample(probs, u):
+    probs = np.ascontiguousarray(probs, np.float32)
+    return lib().or_sample(fptr(probs), probs.size, float(u))
+
+
+def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,
+                         top_k=0, top_p=1.0):
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(len(prompt) + max_new, np.int32)
+    st = SpecStats()
+    rc = lib().or_generate_speculative(target.h, draft.h, iptr(prompt),
+                                       len(prompt), max_new, k, T, top_k,
+                                       top_p, seed, seq, iptr(out),
+                                       C.byref(st))
+    if rc != 0:
+        raise RuntimeError(f"or_generate_speculative failed: {rc}")
+    return out, st
+
+
+def generate_advanced(model, prompt, max_new, T, seed, seq=0, use_cache=True,
+                      top_k=0, top_p=1.0):
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(len(prompt) + max_new, np.int32)
+    rc = lib().or_generate_advanced(model.h, iptr(prompt), len(prompt),
+                                    max_new, T, top_k, top_p, seed, seq,
+                                    1 if use_cache else 0, iptr(out))
+    if rc != 0:
+        raise RuntimeError(f"or_generate_advanced failed: {rc}")
+    return out

@@ -1,0 +1,362 @@
+"""Pins the oracle (oracle/liboracle.so) before it is trusted as the checker.
+
+Each test anchors one oracle function on something outside the oracle: the
+reference's own known-answer tests (file:line under tests/ of the reference),
+the Random123 known-answer vectors, closed forms, float64 brute force, and
+the reference's integration invariants.  The reference itself cannot be built
+here (its CPU backend needs an external BLAS), so no output of it is used.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle_py as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+# --------------------------------------------------------------------------
+# Philox4x32-10 -- Random123 known-answer vectors
+# --------------------------------------------------------------------------
+def test_philox_kat():
+    for case in golden("philox4x32_10_kat.json")["vectors"]:
+        ctr = [int(x, 16) for x in case["ctr"]]
+        key = [int(x, 16) for x in case["key"]]
+        want = [int(x, 16) for x in case["out"]]
+        assert O.philox(ctr, key) == want
+
+
+def test_uniform_layout():
+    # u = top 24 bits of word 0 of Philox(ctr = {slot, cycle, seq, 0},
+    # key = {seed_lo, seed_hi}) times 2^-24
+    seed = 0x1234_5678_9ABC_DEF0
+    for seq, cyc, slot in [(0, 0, 0), (3, 7, 2), (31, 200, 10)]:
+        w = O.philox([slot, cyc, seq, 0], [seed & 0xFFFFFFFF, seed >> 32])[0]
+        assert O.uniform(seed, seq, cyc, slot) == np.float32((w >> 8) / 2**24)
+    us = np.array([O.uniform(7, s, 1, 0) for s in range(4000)])
+    assert 0.0 <= us.min() and us.max() < 1.0
+    assert abs(us.mean() - 0.5) < 0.02
+
+
+# --------------------------------------------------------------------------
+# int8 quantisation -- quantization_test.cpp:6-26 and the closed form
+# --------------------------------------------------------------------------
+def quantize(w):
+    w = np.ascontiguousarray(w, np.float32)
+    codes = np.zeros(w.shape, np.int8)
+    scales = np.zeros(w.shape[1], np.float32)
+    O.lib().or_quantize_w8(O.fptr(w), w.shape[0], w.shape[1], O.i8ptr(codes),
+                           O.fptr(scales))
+    return codes, scales
+
+
+def test_quantize_kat_reference():
+    kat = golden("reference_kats.json")["quantize_int8"]
+    codes, scales = quantize(np.array(kat["weight"], np.float32).reshape(2, 2))
+    np.testing.assert_allclose(scales, kat["scales"], atol=1e-5)
+    deq = codes.astype(np.float32) * scales[None, :]
+    np.testing.assert_allclose(deq.ravel()[0], kat["dequant"][0], atol=0.05)
+    np.testing.assert_allclose(deq.ravel()[1:], kat["dequant"][1:], atol=1e-5)
+
+
+def test_quantize_closed_form():
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((37, 19)) * 0.02).astype(np.float32)
+    w[:, 4] = 0.0                      # all-zero column -> scale 1
+    w[5, 7] = 0.5 * (np.abs(w[:, 7]).max() * 2)  # force a new max
+    codes, scales = quantize(w)
+    for c in range(w.shape[1]):
+        mx = np.float32(np.abs(w[:, c]).max())
+        s = np.float32(mx / np.float32(127.0))
+        assert scales[c] == (np.float32(1.0) if s == 0 else s)
+        q = np.trunc(w[:, c] / scales[c] + np.copysign(np.float32(0.5),
+                                                        w[:, c]))
+        np.testing.assert_array_equal(codes[:, c], np.clip(q, -127, 127))
+    assert np.abs(codes).max() == 127
+    # round half away from zero: 2.5 -> 3, -2.5 -> -3
+    w2 = np.array([[2.5, -2.5], [127.0, 127.0]], np.float32)
+    c2, s2 = quantize(w2)
+    assert list(s2) == [1.0, 1.0] and list(c2[0]) == [3, -3]
+
+
+def test_quantized_dense_forward_reference():
+    """quantization_test.cpp:47-87: int8 forward within 5% of fp32."""
+    kat = golden("reference_kats.json")["quantized_dense_forward"]
+    w = np.array(kat["weight"], np.float32).reshape(4, 3)
+    b = np.array(kat["bias"], np.float32)
+    x = np.array(kat["x"], np.float32).reshape(2, 4)
+    codes, scales = quantize(w)
+    y = np.zeros((2, 3), np.float32)
+    yq = np.zeros((2, 3), np.float32)
+    O.lib().or_dense(O.fptr(x), 2, 4, 3, O.fptr(w), None, None, O.fptr(b),
+                     O.fptr(y))
+    O.lib().or_dense(O.fptr(x), 2, 4, 3, None, O.i8ptr(codes), O.fptr(scales),
+                     O.fptr(b), O.fptr(yq))
+    np.testing.assert_allclose(y, x.astype(np.float64) @ w + b, rtol=1e-6)
+    rel = np.abs(y - yq) / np.maximum(1.0, np.abs(y))
+    assert rel.max() < 0.05
+
+
+def test_matmul_kat_reference():
+    """tensor_test.cpp:82-94: [[1,2,3],[4,5,6]] . [[7,8],[9,10],[11,12]]."""
+    kat = golden("reference_kats.json")["matmul"]
+    a = np.array(kat["a"], np.float32).reshape(2, 3)
+    b = np.array(kat["b"], np.float32).reshape(3, 2)
+    y = np.zeros((2, 2), np.float32)
+    O.lib().or_dense(O.fptr(a), 2, 3, 2, O.fptr(b), None, None, None,
+                     O.fptr(y))
+    assert y.ravel().tolist() == kat["out"]
+
+
+def test_dense_w8_vs_float64():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 96)).astype(np.float32)
+    w = (rng.standard_normal((96, 40)) * 0.02).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    codes, scales = quantize(w)
+    y = np.zeros((6, 40), np.float32)
+    O.lib().or_dense(O.fptr(x), 6, 96, 40, None, O.i8ptr(codes),
+                     O.fptr(scales), O.fptr(b), O.fptr(y))
+    ref = x.astype(np.float64) @ (codes.astype(np.float64) *
+                                  scales.astype(np.float64)) + b
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# RoPE -- rope_swiglu_test.cpp:10-48 and the rotation invariants
+# --------------------------------------------------------------------------
+def test_rope_kat_reference():
+    kat = golden("reference_kats.json")["rope"]
+    x = np.array(kat["x"], np.float32)
+    O.lib().or_rope(O.fptr(x), 1, 2, 4, 0)
+    np.testing.assert_allclose(x[:4], kat["x"][:4], atol=1e-5)
+    np.testing.assert_allclose(x[4:6], kat["out_s1_pair0"], atol=1e-4)
+
+
+def test_rope_closed_form():
+    rng = np.random.default_rng(9)
+    H, S, D, past = 3, 5, 16, 11
+    x = rng.standard_normal((H, S, D)).astype(np.float32)
+    y = x.copy()
+    O.lib().or_rope(O.fptr(y), H, S, D, past)
+    j = np.arange(D // 2)
+    theta = 10000.0 ** (-2.0 * j / D)
+    for s in range(S):
+        ang = (past + s) * theta
+        c, sn = np.cos(ang), np.sin(ang)
+        xe, xo = x[:, s, 0::2].astype(np.float64), x[:, s, 1::2]
+        np.testing.assert_allclose(y[:, s, 0::2], xe * c - xo * sn, atol=2e-5)
+        np.testing.assert_allclose(y[:, s, 1::2], xe * sn + xo * c, atol=2e-5)
+    # rotation preserves each pair's norm
+    n0 = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n1 = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+    np.testing.assert_allclose(n1, n0, rtol=1e-4)
+
+
+# --------------------------------------------------------------------------
+# LayerNorm -- layer_test.cpp:56-80
+# --------------------------------------------------------------------------
+def test_layernorm_kat_reference():
+    kat = golden("reference_kats.json")["layernorm"]
+    x = np.array(kat["x"], np.float32)
+    y = np.zeros_like(x)
+    g = np.ones(3, np.float32)
+    b = np.zeros(3, np.float32)
+    O.lib().or_layernorm(O.fptr(x), 2, 3, O.fptr(g), O.fptr(b), 1e-5,
+                         O.fptr(y))
+    np.testing.assert_allclose(y[:3], kat["out_row0"], atol=1e-3)
+    np.testing.assert_allclose(y[3:], kat["out_row0"], atol=1e-3)
+
+
+def test_layernorm_vs_float64():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((4, 200)) * 3 + 1).astype(np.float32)
+    g = rng.standard_normal(200).astype(np.float32)
+    b = rng.standard_normal(200).astype(np.float32)
+    y = np.zeros_like(x)
+    O.lib().or_layernorm(O.fptr(x), 4, 200, O.fptr(g), O.fptr(b), 1e-5,
+                         O.fptr(y))
+    xd = x.astype(np.float64)
+    m = xd.mean(1, keepdims=True)
+    v = ((xd - m) ** 2).mean(1, keepdims=True)
+    np.testing.assert_allclose(y, (xd - m) / np.sqrt(v + 1e-5) * g + b,
+                               rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# Attention -- float64 brute force with causal mask
+# --------------------------------------------------------------------------
+def attn_f64(q, k, v, causal):
+    H, S, D = q.shape
+    St = k.shape[1]
+    out = np.zeros((S, H, D))
+    for h in range(H):
+        sc = q[h].astype(np.float64) @ k[h].T.astype(np.float64) / math.sqrt(D)
+        if causal:
+            for i in range(S):
+                sc[i, St - S + i + 1:] = -np.inf
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        out[:, h] = p @ v[h].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("S,St", [(1, 1), (1, 9), (4, 4), (5, 37)])
+def test_attention_vs_float64(S, St):
+    rng = np.random.default_rng(S * 100 + St)
+    H, D = 3, 16
+    q = rng.standard_normal((H, S, D)).astype(np.float32)
+    k = rng.standard_normal((H, St, D)).astype(np.float32)
+    v = rng.standard_normal((H, St, D)).astype(np.float32)
+    out = np.zeros((S, H, D), np.float32)
+    O.lib().or_attention(O.fptr(q), O.fptr(k), O.fptr(v), H, H, S, St, D, 1,
+                         O.fptr(out))
+    np.testing.assert_allclose(out, attn_f64(q, k, v, True), rtol=1e-5,
+                               atol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# get_probs / sample_token
+# --------------------------------------------------------------------------
+def test_get_probs_closed_form():
+    rng = np.random.default_rng(2)
+    lg = (rng.standard_normal(500) * 2).astype(np.float32)
+    for T in (1.0, 0.7, 2.5):
+        p = O.get_probs(lg, T)
+        z = lg.astype(np.float64) / T
+        ref = np.exp(z - z.max())
+        ref /= ref.sum()
+        np.testing.assert_allclose(p, ref, rtol=2e-6, atol=1e-12)
+    g = O.get_probs(lg, 0.0)
+    assert g.sum() == 1.0 and g[int(np.argmax(lg))] == 1.0
+    tie = np.array([0.5, 2.0, 2.0, -1.0], np.float32)
+    assert O.get_probs(tie, 0.0)[1] == 1.0          # first index wins ties
+
+
+def test_get_probs_top_k_top_p():
+    lg = np.log(np.array([0.1, 0.4, 0.2, 0.3], np.float32))
+    p = O.get_probs(lg, 1.0, top_k=2)
+    np.testing.assert_allclose(p, [0, 4 / 7, 0, 3 / 7], rtol=1e-6)
+    p = O.get_probs(lg, 1.0, top_p=0.65)        # 0.4 + 0.3 >= 0.65 -> cut
+    np.testing.assert_allclose(p, [0, 4 / 7, 0, 3 / 7], rtol=1e-6)
+    p = O.get_probs(lg, 1.0, top_p=0.75)        # 0.4 + 0.3 + 0.2
+    np.testing.assert_allclose(p, [0, 4 / 9, 2 / 9, 3 / 9], rtol=1e-6)
+
+
+def test_sample_inverse_cdf_brute_force():
+    rng = np.random.default_rng(4)
+    p = rng.random(50).astype(np.float32)
+    p[[3, 17]] = 0
+    cdf = np.cumsum(p.astype(np.float64) / p.astype(np.float64).sum())
+    cdf[-1] = 1.0
+    for u in list(rng.random(300)) + [0.0, 1 - 2**-24]:
+        want = int(np.searchsorted(cdf, u, side="left"))
+        assert O.sample(p, u) == want
+    # a boundary value picks the first index whose cdf reaches it
+    q = np.array([0.25, 0.25, 0.5], np.float32)
+    assert O.sample(q, 0.25) == 0 and O.sample(q, 0.2500001) == 1
+
+
+# --------------------------------------------------------------------------
+# Whole-path invariants (transformer_test.cpp)
+# --------------------------------------------------------------------------
+def tiny_models(vocab=8, quantize=False, seed=11):
+    tp = O.make_params(vocab, 16, 2, 32, 2, seed, std=0.3)
+    dp = O.make_params(vocab, 16, 2, 32, 1, seed + 1, std=0.3)
+    return (O.Model(vocab, 16, 2, 32, 2, 64, tp, quantize),
+            O.Model(vocab, 16, 2, 32, 1, 64, dp, quantize))
+
+
+def test_causal_independence():
+    """transformer_test.cpp:153-176: a later token leaves earlier rows
+    bit-equal."""
+    t, _ = tiny_models()
+    a = t.forward([1, 2, 3, 4])
+    b = t.forward([1, 2, 3, 7])
+    np.testing.assert_array_equal(a[:3], b[:3])
+    assert not np.array_equal(a[3], b[3])
+
+
+def test_kv_cache_equals_no_cache():
+    """transformer_test.cpp:250-273 and cached vs uncached logits."""
+    t, _ = tiny_models(quantize=True)
+    full = t.forward([5, 1, 2, 7, 3, 0])
+    c = O.Cache(t)
+    parts = [t.forward([5, 1, 2], c), t.forward([7], c), t.forward([3, 0], c)]
+    np.testing.assert_allclose(np.concatenate(parts), full, rtol=1e-5,
+                               atol=1e-6)
+    assert len(c) == 6
+    c.truncate(4)
+    again = t.forward([3, 0], c)
+    np.testing.assert_array_equal(again, parts[2])
+    a = O.generate_advanced(t, [1, 2, 3], 6, 0.0, 42, use_cache=False)
+    b = O.generate_advanced(t, [1, 2, 3], 6, 0.0, 42, use_cache=True)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_max_seq_len_throws():
+    t, _ = tiny_models()
+    with pytest.raises(RuntimeError):
+        t.forward(list(range(8)) * 9)
+
+
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_greedy_spec_equals_ar(quant, k):
+    """transformer_test.cpp:307-346: greedy speculative == greedy AR."""
+    t, d = tiny_models(quantize=quant)
+    for prompt in ([1, 2, 3], [7, 0, 5, 5, 2]):
+        ar = O.generate_advanced(t, prompt, 12, 0.0, 42)
+        sp, st = O.generate_speculative(t, d, prompt, 12, k, 0.0, 42)
+        np.testing.assert_array_equal(sp, ar)
+        assert len(sp) == len(prompt) + 12
+        assert st.accepted + st.resampled + st.bonus + 1 == 12
+
+
+def test_sampled_same_seed_same_output():
+    """transformer_test.cpp:275-305 (same seed => same tokens)."""
+    t, d = tiny_models()
+    a, sa = O.generate_speculative(t, d, [1, 2, 3], 10, 3, 1.0, 42)
+    b, sb = O.generate_speculative(t, d, [1, 2, 3], 10, 3, 1.0, 42)
+    np.testing.assert_array_equal(a, b)
+    assert (sa.cycles, sa.accepted) == (sb.cycles, sb.accepted)
+    assert ((a >= 0) & (a < 8)).all()
+
+
+def test_speculative_sampling_preserves_target_distribution():
+    """Accept-with-r*q<p plus the max(0, p-q) residual must emit tokens
+    distributed as the target's p (the speculative-sampling theorem).  With
+    k=1 and max_new=2 the second token comes from one verify cycle; its
+    empirical law, conditioned on the first token, is compared with the
+    target softmax by a chi-square bound."""
+    t, d = tiny_models(vocab=6, seed=23)
+    prompt = [1, 4, 2]
+    counts = {}
+    n = 6000
+    for s in range(n):
+        out, _ = O.generate_speculative(t, d, prompt, 2, 1, 1.0, 1000 + s)
+        counts.setdefault(int(out[3]), np.zeros(6))[int(out[4])] += 1
+    worst = 0.0
+    for first, cnt in counts.items():
+        if cnt.sum() < 300:
+            continue
+        p = O.get_probs(t.forward(prompt + [first])[-1], 1.0).astype(
+            np.float64)
+        exp = p * cnt.sum()
+        keep = exp > 5
+        chi2 = (((cnt - exp) ** 2 / exp)[keep]).sum()
+        worst = max(worst, chi2)
+        # 5 degrees of freedom: P(chi2 > 25) ~ 1.4e-4
+        assert chi2 < 25.0, (first, cnt, exp)
+    # the draft must differ from the target for the test to mean anything
+    q = O.get_probs(d.forward(prompt + [3])[-1], 1.0)
+    p = O.get_probs(t.forward(prompt + [3])[-1], 1.0)
+    assert np.abs(p - q).sum() > 0.2
