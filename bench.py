@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Speculative-decoding benchmark on one MI355X.
+
+Workload (one "step"): sampled speculative decoding of 32 independent
+sequences with an int8 weight-quantised target (12 layers, d_model 1024,
+16 heads of 64, MLP 4096, vocab 32000) and draft (4 layers, d_model 512,
+8 heads, MLP 2048), prompts of 256 uniform random ids, k = 5, temperature
+1.0, 128 new tokens per sequence, Philox uniforms.  Weights are N(0, 0.02)
+from a seeded generator (synthetic; no checkpoints).
+
+value = committed tokens per second of the decode loop (accepted drafts plus
+one resample or bonus per cycle, prefill excluded), timed by HIP events on
+the library's stream around the cycle loop.  Also reported: the batch-1
+int8 greedy configuration (6L/512 target, 2L/256 draft, k=4, 256 new), the
+roofline of the dominant kernel, and the oracle timed on the host as the CPU
+baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "neural-network_amd", "python"))
+
+import nnhip  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+TARGET = dict(vocab=32000, d=1024, H=16, F=4096, L=12)
+DRAFT = dict(vocab=32000, d=512, H=8, F=2048, L=4)
+B, P, K_LOOK, NEW, TEMP = 32, 256, 5, 128, 1.0
+CFG2_T = dict(vocab=4096, d=512, H=8, F=2048, L=6)
+CFG2_D = dict(vocab=4096, d=256, H=4, F=1024, L=2)
+MAX_SEQ = 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_model(ctx, cfg, seed):
+    m = nnhip.Decoder(ctx, cfg["vocab"], cfg["d"], cfg["H"], cfg["F"],
+                      cfg["L"], MAX_SEQ)
+    m.init_normal(seed, 0.02)
+    m.quantize()
+    return m
+
+
+def weight_bytes(cfg):
+    """int8 codes + fp32 scales and biases of every Dense, per forward."""
+    d, F, V, L = cfg["d"], cfg["F"], cfg["vocab"], cfg["L"]
+    dense = L * (4 * d * d + 3 * d * F) + d * V
+    outs = L * (4 * d + 2 * F + d) + V
+    return dense + 8 * outs
+
+
+def kv_bytes(cfg, n_keys):
+    """fp32 K and V read by one forward over n_keys cached positions."""
+    return cfg["L"] * 2 * n_keys * cfg["d"] * 4
+
+
+def cycle_bytes(ctx_len, k, Bn):
+    """Algorithmic HBM bytes of one cycle at mean context ctx_len: verify
+    (weights once, k+1 rows of KV per sequence), k draft forwards and the
+    catch-up, and the logits written and read by sampling."""
+    v = weight_bytes(TARGET) + Bn * kv_bytes(TARGET, ctx_len + k + 1)
+    dr = (k + 1) * (weight_bytes(DRAFT) + Bn * kv_bytes(DRAFT, ctx_len + k))
+    lg = Bn * (2 * k + 1) * TARGET["vocab"] * 4 * 2
+    return v + dr + lg
+
+
+def attention_bytes(Bn, S, H, D, n_keys):
+    return 2 * Bn * H * n_keys * D * 4 + 2 * Bn * S * H * D * 4
+
+
+def run_cfg4(ctx, steps, warmup):
+    log("building cfg4 models (init + int8 quantisation on device)")
+    t = make_model(ctx, TARGET, 1234)
+    d = make_model(ctx, DRAFT, 5678)
+    rng = np.random.default_rng(2024)
+    prompts = rng.integers(0, TARGET["vocab"], (B, P)).astype(np.int32)
+    for i in range(warmup):
+        log(f"warmup {i}")
+        t.generate_speculative_batch(d, prompts, NEW, K_LOOK, TEMP, 42)
+    ctx.sync()
+    dec_ms, wall, toks, stats_all = 0.0, 0.0, 0, []
+    for i in range(steps):
+        t0 = time.perf_counter()
+        out, stats, tm = t.generate_speculative_batch(d, prompts, NEW, K_LOOK,
+                                                      TEMP, 42)
+        ctx.sync()
+        wall += time.perf_counter() - t0
+        dec_ms += tm.decode_ms
+        toks += B * (NEW - 1)
+        stats_all = stats
+        log(f"step {i}: decode {tm.decode_ms:.2f} ms prefill "
+            f"{tm.prefill_ms:.2f} ms cycles {tm.cycles_launched}")
+    cycles = max(s.cycles for s in stats_all)
+    acc = sum(s.accepted for s in stats_all)
+    drafted = sum(s.drafted for s in stats_all)
+    ties = sum(s.ties for s in stats_all)
+    res = dict(value=toks / (dec_ms / 1e3), wall_s=wall, decode_ms=dec_ms,
+               steps=steps, cycles=cycles, accepted=acc, drafted=drafted,
+               ties=ties, prefill_ms=tm.prefill_ms,
+               tokens_per_cycle_per_seq=(NEW - 1) / max(cycles, 1))
+    # algorithmic-byte roofline of the whole decode loop
+    ctx_mid = P + NEW // 2
+    bytes_total = cycles * cycle_bytes(ctx_mid, K_LOOK, B)
+    res["loop_bytes"] = bytes_total
+    res["loop_GBs"] = bytes_total / (dec_ms / steps / 1e3) / 1e9
+    res["models"] = (t, d, prompts)
+    return res
+
+
+def run_cfg2(ctx):
+    log("batch-1 int8 greedy configuration")
+    t = make_model(ctx, CFG2_T, 11)
+    d = make_model(ctx, CFG2_D, 12)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, 4096, (1, 128)).astype(np.int32)
+    t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
+    out, stats, tm = t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
+    t.free(); d.free()
+    return dict(tokens_per_s=255 / (tm.decode_ms / 1e3),
+                decode_ms=tm.decode_ms, cycles=stats[0].cycles,
+                accepted=stats[0].accepted)
+
+
+def roofline_attention(ctx):
+    """Verify-step attention at the cfg4 mid-run shape: 32 sequences x 16
+    heads, 6 queries, 320 cached keys (+6 new)."""
+    n_cached = P + NEW // 2
+    S = K_LOOK + 1
+    ms = nnhip.bench_attention(ctx, B, S, 16, 64, n_cached, iters=200, nbuf=4)
+    byt = attention_bytes(B, S, 16, 64, n_cached + S)
+    ach = byt / (ms / 1e3) / 1e9
+    return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
+                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4), traffic=None,
+                kernel="attn_kernel<6> (+combine)", bytes_per_launch=byt,
+                us_per_launch=round(ms * 1e3, 2))
+
+
+def cpu_baseline(models, sample_new=12):
+    """The oracle (single-threaded C restatement of the reference CPU path)
+    on sequence 0 of the same workload, with the device weights."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py as O
+    t, d, prompts = models
+    log("cpu baseline: copying weights to the host")
+    ot = O.Model(TARGET["vocab"], TARGET["d"], TARGET["H"], TARGET["F"],
+                 TARGET["L"], MAX_SEQ,
+                 [t.get_param(i) for i in range(t.num_params())], True)
+    od = O.Model(DRAFT["vocab"], DRAFT["d"], DRAFT["H"], DRAFT["F"],
+                 DRAFT["L"], MAX_SEQ,
+                 [d.get_param(i) for i in range(d.num_params())], True)
+    log("cpu baseline: running the oracle")
+    out, st = O.generate_speculative(ot, od, prompts[0], sample_new, K_LOOK,
+                                     TEMP, 42, seq=0)
+    toks = sample_new - 1
+    return dict(value=round(toks / (st.decode_ms / 1e3), 3),
+                unit="tokens/s", cores=1, kind="port",
+                sample=(f"sequence 0 of the workload, {sample_new} new tokens "
+                        f"after its 256-id prompt (decode loop only; prefill "
+                        f"{st.prefill_ms / 1e3:.1f} s excluded), 1 thread"))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batch1", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py measures one GPU only: every box in this setup has a "
+              "single MI355X (sharding is described in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    ctx = nnhip.Context(0)
+    r = run_cfg4(ctx, a.steps, a.warmup)
+    roof = roofline_attention(ctx)
+    b1 = None if a.no_batch1 else run_cfg2(ctx)
+    cpu = None if a.no_cpu_baseline else cpu_baseline(r["models"])
+    ms_step = r["wall_s"] / a.steps * 1e3
+    line = {
+        "metric": "accepted tokens/sec (batch 32, int8 target, k=5)",
+        "value": round(r["value"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x fp32 activations (fp32 KV)",
+        "data": "synthetic: seeded N(0,0.02) weights, uniform random prompts",
+        "config": {"workload": "sampled speculative decode, 32 sequences, "
+                               "target 12L/1024/16h/4096/V32000 int8, draft "
+                               "4L/512/8h/2048 int8, prompt 256, k=5, T=1.0, "
+                               "128 new", "batch": B, "lookahead": K_LOOK,
+                   "new_tokens": NEW, "prompt": P},
+        "decode_ms_per_step": round(r["decode_ms"] / a.steps, 2),
+        "prefill_ms": round(r["prefill_ms"], 2),
+        "cycles": r["cycles"],
+        "acceptance": round(r["accepted"] / max(r["drafted"], 1), 4),
+        "ties": r["ties"],
+        "loop_roofline": {"achieved_GBs": round(r["loop_GBs"], 1),
+                          "frac": round(r["loop_GBs"] / HBM_PEAK_GBS, 4)},
+        "roofline": roof,
+        "batch1": b1,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,236 @@
+/*
+ * nnhip.h -- C ABI of libnnhip.so, the MI355X (gfx950) HIP backend for the
+ * speculative-decoding path of islhkafaa/neural-network.
+ *
+ * Conventions: plain pointers and sizes only; every function returns 0 or a
+ * negative status (NNHIP_E*) and leaves a message for nnhip_last_error() on
+ * the calling thread (the reference throws std::runtime_error with the same
+ * text, e.g. tensor.cpp:393-402, layer.cpp:1176-1179).  A context owns one HIP
+ * stream; calls are ordered on it; functions that take host buffers return
+ * with the result in them.  A context is used by one host thread at a time.
+ *
+ * Host buffers are marked "host", device buffers (from nnhip_malloc) "dev".
+ * Token ids are int32 (the reference carries them as fp32, layer.cpp:1402).
+ */
+#ifndef NNHIP_H
+#define NNHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NNHIP_OK 0
+#define NNHIP_EARG (-1)          /* bad argument or shape                   */
+#define NNHIP_ECAPACITY (-2)     /* sequence would exceed max_seq_len        */
+#define NNHIP_EHIP (-3)          /* HIP runtime failure                      */
+#define NNHIP_EUNSUPPORTED (-4)  /* option the device path does not provide  */
+
+typedef struct nnhip_ctx nnhip_ctx;
+typedef struct nnhip_model nnhip_model;
+typedef struct nnhip_kvcache nnhip_kvcache;
+
+typedef struct {
+  int64_t cycles;     /* speculative cycles after the first token         */
+  int64_t drafted;    /* sum over cycles of M = min(k, tokens remaining)   */
+  int64_t accepted;   /* accepted draft tokens                             */
+  int64_t ties;       /* accept tests with |r - p/q| < 1e-6                */
+  int64_t resampled;  /* cycles ending in a residual resample              */
+  int64_t bonus;      /* cycles ending in a bonus sample                   */
+} nnhip_spec_stats;
+
+typedef struct {
+  double prefill_ms;        /* prompt forward of target + draft, first token */
+  double decode_ms;         /* the cycle loop                                 */
+  int64_t cycles_launched;  /* cycles enqueued (one may run after the end)    */
+} nnhip_spec_timing;
+
+/* ---- errors, lifecycle, memory -------------------------------------------
+ * Replace the device side of ExecutionBackend (include/backend/backend.hpp:
+ * 20-33): allocate, copy_host_to_device, copy_to_device,
+ * copy_device_to_host; DeviceBuffer (backend.hpp:9-18) is a dev pointer. */
+const char *nnhip_last_error(void);
+int nnhip_init(int device, nnhip_ctx **out);
+int nnhip_destroy(nnhip_ctx *ctx);
+/* "graphs" (1 = replay each speculative cycle as one HIP graph, default). */
+int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
+int nnhip_sync(nnhip_ctx *ctx);
+int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out);
+int nnhip_free(nnhip_ctx *ctx, void *dev);
+int nnhip_h2d(nnhip_ctx *ctx, void *dev_dst, const void *host_src,
+              size_t bytes);
+int nnhip_d2h(nnhip_ctx *ctx, void *host_dst, const void *dev_src,
+              size_t bytes);
+/* Stream-ordered timer: begin records an event, end records a second one,
+ * waits for it and returns the elapsed milliseconds. */
+int nnhip_timer_begin(nnhip_ctx *ctx);
+int nnhip_timer_end(nnhip_ctx *ctx, float *ms);
+
+/* ---- decoder --------------------------------------------------------------
+ * TransformerDecoder(vocab_size, embed_dim, num_heads, dim_feedforward,
+ * num_layers, max_seq_len) (include/nn/layer.hpp:300-302): post-LN layers of
+ * RoPE multi-head attention and SwiGLU, lm_head; weights resident on the
+ * device. */
+int nnhip_decoder_create(nnhip_ctx *ctx, int vocab, int d_model, int n_heads,
+                         int d_ff, int n_layers, int max_seq_len,
+                         nnhip_model **out);
+int nnhip_decoder_free(nnhip_model *m);
+/* TransformerDecoder::parameters() order (layer.cpp:1140-1154): token_emb;
+ * per layer q.w q.b k.w k.b v.w v.b o.w o.b gate.w gate.b up.w up.b down.w
+ * down.b ln1.g ln1.b ln2.g ln2.b; lm_head.w lm_head.b.  Dense weights are
+ * [in][out] row-major as in the reference (layer.cpp:151-160). */
+int nnhip_decoder_num_params(const nnhip_model *m, int *n);
+int nnhip_decoder_param_shape(const nnhip_model *m, int idx, int64_t *rows,
+                              int64_t *cols);
+/* Tensor::copy_from_host / to_host on parameters()[idx] (host buffers). */
+int nnhip_decoder_set_param(nnhip_model *m, int idx, const float *host);
+int nnhip_decoder_get_param(const nnhip_model *m, int idx, float *host);
+/* Seeded initialisation on the device: Dense weights and the embedding
+ * N(0, std) from Philox4x32-10 + Box-Muller, biases 0, LayerNorm gamma 1 and
+ * beta 0.  Replaces the random_device initialisers
+ * (include/nn/initialization.hpp:13-66), which are not reproducible. */
+int nnhip_decoder_init_normal(nnhip_model *m, uint64_t seed, float stdv);
+/* quantize_model + MultiHeadAttention::quantize + QuantizedDense ctor
+ * (quantization.cpp:7-87, 156-171; layer.cpp:545-558) applied to every Dense
+ * of the decoder (q, k, v, o, gate, up, down, lm_head); the embedding stays
+ * fp32.  bits: 8 (INT8).  INT4 returns NNHIP_EUNSUPPORTED. */
+int nnhip_decoder_quantize(nnhip_model *m, int bits);
+/* QuantizedDense::packed_weights / scales (quantization.hpp:31-33) of one
+ * Dense: which 0..6 = q,k,v,o,gate,up,down of `layer`, 7 = lm_head.  codes
+ * [in][out] int8 (host), scales [out] (host). */
+int nnhip_decoder_get_quantized(const nnhip_model *m, int layer, int which,
+                                int8_t *codes, float *scales);
+/* TransformerDecoder::forward(x, caches) (layer.cpp:1161-1193) for B
+ * sequences of S ids each: ids [B][S] (host), logits [B][S][V] (host).
+ * cache may be NULL (no cache: attention over the S ids only).  With a
+ * cache, sequence b continues at its own length, which grows by S. */
+int nnhip_decoder_forward(nnhip_model *m, nnhip_kvcache *cache,
+                          const int32_t *ids, int B, int S, float *logits);
+
+/* ---- KV cache --------------------------------------------------------------
+ * KVCache (layer.hpp:212-230) for `batch` sequences with one length each,
+ * capacity max_seq_len.  quantized != 0 (int8 cache) returns
+ * NNHIP_EUNSUPPORTED. */
+int nnhip_kvcache_create(nnhip_model *m, int batch, int quantized,
+                         nnhip_kvcache **out);
+int nnhip_kvcache_free(nnhip_kvcache *c);
+int nnhip_kvcache_length(const nnhip_kvcache *c, int b, int *len);
+/* KVCache::truncate(len) (layer.cpp:67-149) for sequence b: an O(1) length
+ * update; a longer len leaves the cache unchanged. */
+int nnhip_kvcache_truncate(nnhip_kvcache *c, int b, int len);
+
+/* ---- generation -----------------------------------------------------------
+ * TransformerDecoder::generate_speculative(draft, prompt, max_new_tokens,
+ * lookahead, temperature, top_k, top_p, seed, quantized_cache)
+ * (layer.hpp:318-323, layer.cpp:1382-1661).  out [P + max(max_new, 1)]
+ * (host) receives the prompt and the generated ids.  Uniforms come from the
+ * Philox stream u[seq][cycle][slot] (slot j < k: draft sample j, k + j:
+ * accept test j, 2k: resample or bonus; cycle 0 slot 2k: first token)
+ * instead of std::mt19937.  temperature <= 0 is greedy.  top_k in (0, V) or
+ * top_p in (0, 1) and quantized_cache != 0 return NNHIP_EUNSUPPORTED. */
+int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
+                               const int32_t *prompt, int P, int max_new,
+                               int lookahead, float temperature, int top_k,
+                               float top_p, uint64_t seed,
+                               int quantized_cache, int32_t *out,
+                               nnhip_spec_stats *stats);
+/* The same for B independent sequences of equal prompt length P (the
+ * reference is batch-1; this runs B of its loops in lockstep on one GPU
+ * with per-sequence cache lengths).  prompts [B][P], out
+ * [B][P + max(max_new, 1)], stats [B] (or NULL), timing (or NULL).
+ * Sequence b uses Philox sequence index seq0 + b. */
+int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
+                                     int B, const int32_t *prompts, int P,
+                                     int max_new, int lookahead,
+                                     float temperature, int top_k, float top_p,
+                                     uint64_t seed, uint32_t seq0,
+                                     int32_t *out, nnhip_spec_stats *stats,
+                                     nnhip_spec_timing *timing);
+/* TransformerDecoder::generate_advanced(prompt, max_new_tokens, temperature,
+ * top_k, top_p, seed, use_kv_cache) (layer.hpp:310-316, layer.cpp:
+ * 1240-1380); sampled mode draws u[seq][step][0]. */
+int nnhip_generate_advanced(nnhip_model *m, const int32_t *prompt, int P,
+                            int max_new, float temperature, int top_k,
+                            float top_p, uint64_t seed, int use_kv_cache,
+                            int32_t *out);
+int nnhip_generate_advanced_batch(nnhip_model *m, int B,
+                                  const int32_t *prompts, int P, int max_new,
+                                  float temperature, int top_k, float top_p,
+                                  uint64_t seed, uint32_t seq0,
+                                  int use_kv_cache, int32_t *out);
+
+/* ---- fused device ops (dev buffers, stream-ordered) ------------------------ */
+/* QuantizedDense ctor, INT8 (quantization.cpp:36-66): w [in][out] fp32 ->
+ * codes [out][in] int8 (transposed for coalesced GEMV loads), scales [out]. */
+int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
+                      int8_t *codes, float *scales);
+/* QuantizedDense::forward (quantization.cpp:127-147): y [rows][N] =
+ * x [rows][K] . (codes * scales)^T + bias.  path: 0 auto, 1 fp32 GEMV,
+ * 2 int8-digit MFMA GEMM (K % 128 == 0, N % 64 == 0). */
+int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
+                       const int8_t *codes, const float *scales,
+                       const float *bias, int N, float *y, int path);
+/* Dense::forward (layer.cpp:162-171) with w [N][K] fp32 (transposed). */
+int nnhip_linear_f32(nnhip_ctx *ctx, const float *x, int rows, int K,
+                     const float *w, const float *bias, int N, float *y);
+/* The MFMA path's exact integers: row exponents rexp [rows], digits
+ * limbs [3][rows64][K] (rows64 = rows rounded up to 64) and the int64 dot
+ * totals [rows][N] = sum_k (hi*65536 + mid*256 + lo) * code. */
+int nnhip_linear_limb_totals(nnhip_ctx *ctx, const float *x, int rows, int K,
+                             const int8_t *codes, int N, int64_t *totals,
+                             int32_t *rexp, int8_t *limbs);
+/* Tensor::rope (tensor.cpp:1126-1226) on q and k of qkv [B*S][3*H*D] rows
+ * ([q | k | v], head-major within each) at positions pos[b] + s, then the KV
+ * append of MultiHeadAttention::forward (layer.cpp:758-807) into kcache /
+ * vcache [B][H][cap][D]; q_out [B*S][H*D]. */
+int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                         int H, int D, const int32_t *pos, float *q_out,
+                         float *kcache, float *vcache, int cap);
+/* Fused causal attention of MultiHeadAttention::forward (layer.cpp:842-952)
+ * for S queries per sequence: q [B*S][H*D], kcache / vcache [B][Hkv][cap][D]
+ * holding pos0[b] + S valid entries; query s sees keys j <= pos0[b] + s.
+ * out [B*S][H*D]. */
+int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
+                       const float *vcache, int cap, const int32_t *pos0,
+                       int B, int S, int H, int Hkv, int D, float *out);
+/* LayerNorm::forward (layer.cpp:242-261), eps 1e-5, over rows of d. */
+int nnhip_layernorm(nnhip_ctx *ctx, const float *x, int rows, int d,
+                    const float *gamma, const float *beta, float *y);
+/* get_probs + sample_token (layer.cpp:1410-1498) per row: logits [B][V],
+ * u [B]; tok [B]; probs [B][V] or NULL (not written when temperature <= 0). */
+int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
+                      float temperature, const float *u, int32_t *tok,
+                      float *probs);
+/* Accept loop + residual resample of generate_speculative (layer.cpp:
+ * 1581-1630) for B sequences of k drafted positions: target and draft
+ * logits [B][k][V], draft ids [B][k], accept uniforms [B][k], resample
+ * uniforms [B].  n_accept [B]; next_tok [B] = resampled id, or -1 when all
+ * k are accepted (no target row k for a bonus sample). */
+int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
+                      const float *dlogits, const int32_t *dtok,
+                      const float *u_accept, const float *u_resample, int B,
+                      int k, int V, float temperature, int32_t *n_accept,
+                      int32_t *next_tok);
+
+/* ---- microbenchmarks -------------------------------------------------------
+ * Time one kernel on the context's stream with HIP events (one untimed
+ * launch first), rotating over nbuf device-generated input sets; *ms is the
+ * mean per launch.  No counterpart in the reference (it has no benchmarks);
+ * they time the verify-step attention and acceptance-sampling steps and the
+ * W8A32 Linear of the decode path in isolation. */
+int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
+                          int n_cached, int iters, int nbuf, float *ms);
+/* n_accept (host [B] or NULL): accepted counts on input set 0. */
+int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
+                            float temperature, int iters, int nbuf, float *ms,
+                            int32_t *n_accept);
+/* path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included). */
+int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
+                       int iters, int nbuf, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

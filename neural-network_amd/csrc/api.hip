@@ -1,0 +1,505 @@
+// extern "C" boundary of libnnhip.so (declared in include/nnhip.h).  Every
+// entry point converts exceptions into a status code plus a thread-local
+// message, the C form of the reference's std::runtime_error convention.
+#include "api_common.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace {
+thread_local std::string g_err;
+}  // namespace
+
+void nnhip::set_last_error(const std::string &msg) { g_err = msg; }
+
+using nnhip::guard;
+
+namespace {
+
+#define REQ(cond, msg) NNHIP_REQUIRE((cond), nnhip::kErrArg, (msg))
+
+void set_device(const nnhip_ctx *ctx) {
+  NNHIP_CHECK(hipSetDevice(ctx->c.device));
+}
+
+// Allocate-and-copy helpers for the host-buffer entry points.
+template <typename T>
+nnhip::DevBuf<T> upload(hipStream_t st, const T *host, size_t n) {
+  nnhip::DevBuf<T> d(n);
+  NNHIP_CHECK(hipMemcpyAsync(d.p, host, n * sizeof(T), hipMemcpyHostToDevice, st));
+  return d;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *nnhip_last_error(void) { return g_err.c_str(); }
+
+int nnhip_init(int device, nnhip_ctx **out) {
+  return guard([&] {
+    REQ(out, "nnhip_init: out is NULL");
+    int n = 0;
+    NNHIP_CHECK(hipGetDeviceCount(&n));
+    REQ(device >= 0 && device < n, "nnhip_init: no such device");
+    NNHIP_CHECK(hipSetDevice(device));
+    std::unique_ptr<nnhip_ctx> c(new nnhip_ctx);
+    c->c.device = device;
+    NNHIP_CHECK(hipStreamCreateWithFlags(&c->c.stream, hipStreamNonBlocking));
+    NNHIP_CHECK(hipEventCreate(&c->t0));
+    NNHIP_CHECK(hipEventCreate(&c->t1));
+    *out = c.release();
+  });
+}
+
+int nnhip_destroy(nnhip_ctx *ctx) {
+  return guard([&] {
+    if (!ctx) return;
+    set_device(ctx);
+    (void)hipStreamSynchronize(ctx->c.stream);
+    (void)hipEventDestroy(ctx->t0);
+    (void)hipEventDestroy(ctx->t1);
+    (void)hipStreamDestroy(ctx->c.stream);
+    delete ctx;
+  });
+}
+
+int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
+  return guard([&] {
+    REQ(ctx && key, "nnhip_set_option: NULL argument");
+    if (std::strcmp(key, "graphs") == 0) ctx->c.use_graphs = value != 0;
+    else throw nnhip::Error(nnhip::kErrArg, std::string("unknown option ") + key);
+  });
+}
+
+int nnhip_sync(nnhip_ctx *ctx) {
+  return guard([&] {
+    REQ(ctx, "nnhip_sync: NULL context");
+    NNHIP_CHECK(hipStreamSynchronize(ctx->c.stream));
+  });
+}
+
+int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out) {
+  return guard([&] {
+    REQ(ctx && out, "nnhip_malloc: NULL argument");
+    set_device(ctx);
+    *out = nullptr;
+    if (bytes) NNHIP_CHECK(hipMalloc(out, bytes));
+  });
+}
+
+int nnhip_free(nnhip_ctx *ctx, void *p) {
+  return guard([&] {
+    REQ(ctx, "nnhip_free: NULL context");
+    if (p) {
+      NNHIP_CHECK(hipStreamSynchronize(ctx->c.stream));
+      NNHIP_CHECK(hipFree(p));
+    }
+  });
+}
+
+int nnhip_h2d(nnhip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  return guard([&] {
+    REQ(ctx && (bytes == 0 || (dst && src)), "nnhip_h2d: NULL argument");
+    NNHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->c.stream));
+    NNHIP_CHECK(hipStreamSynchronize(ctx->c.stream));
+  });
+}
+
+int nnhip_d2h(nnhip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  return guard([&] {
+    REQ(ctx && (bytes == 0 || (dst && src)), "nnhip_d2h: NULL argument");
+    NNHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->c.stream));
+    NNHIP_CHECK(hipStreamSynchronize(ctx->c.stream));
+  });
+}
+
+int nnhip_timer_begin(nnhip_ctx *ctx) {
+  return guard([&] {
+    REQ(ctx, "nnhip_timer_begin: NULL context");
+    NNHIP_CHECK(hipEventRecord(ctx->t0, ctx->c.stream));
+  });
+}
+
+int nnhip_timer_end(nnhip_ctx *ctx, float *ms) {
+  return guard([&] {
+    REQ(ctx && ms, "nnhip_timer_end: NULL argument");
+    NNHIP_CHECK(hipEventRecord(ctx->t1, ctx->c.stream));
+    NNHIP_CHECK(hipEventSynchronize(ctx->t1));
+    NNHIP_CHECK(hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+  });
+}
+
+// ---- decoder ---------------------------------------------------------------
+int nnhip_decoder_create(nnhip_ctx *ctx, int vocab, int d_model, int n_heads,
+                         int d_ff, int n_layers, int max_seq_len,
+                         nnhip_model **out) {
+  return guard([&] {
+    REQ(ctx && out, "nnhip_decoder_create: NULL argument");
+    set_device(ctx);
+    std::unique_ptr<nnhip_model> m(new nnhip_model);
+    m->m.reset(new nnhip::Model(&ctx->c, vocab, d_model, n_heads, d_ff,
+                                n_layers, max_seq_len));
+    *out = m.release();
+  });
+}
+
+int nnhip_decoder_free(nnhip_model *m) {
+  return guard([&] {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->m->ctx->stream);
+    delete m;
+  });
+}
+
+int nnhip_decoder_num_params(const nnhip_model *m, int *n) {
+  return guard([&] {
+    REQ(m && n, "nnhip_decoder_num_params: NULL argument");
+    *n = m->m->num_params();
+  });
+}
+
+int nnhip_decoder_param_shape(const nnhip_model *m, int idx, int64_t *rows,
+                              int64_t *cols) {
+  return guard([&] {
+    REQ(m && rows && cols, "nnhip_decoder_param_shape: NULL argument");
+    m->m->param_shape(idx, rows, cols);
+  });
+}
+
+int nnhip_decoder_set_param(nnhip_model *m, int idx, const float *host) {
+  return guard([&] {
+    REQ(m && host, "nnhip_decoder_set_param: NULL argument");
+    m->m->set_param(idx, host);
+  });
+}
+
+int nnhip_decoder_get_param(const nnhip_model *m, int idx, float *host) {
+  return guard([&] {
+    REQ(m && host, "nnhip_decoder_get_param: NULL argument");
+    m->m->get_param(idx, host);
+  });
+}
+
+int nnhip_decoder_init_normal(nnhip_model *m, uint64_t seed, float stdv) {
+  return guard([&] {
+    REQ(m, "nnhip_decoder_init_normal: NULL model");
+    m->m->init_normal(seed, stdv);
+  });
+}
+
+int nnhip_decoder_quantize(nnhip_model *m, int bits) {
+  return guard([&] {
+    REQ(m, "nnhip_decoder_quantize: NULL model");
+    NNHIP_REQUIRE(bits == 8, nnhip::kErrUnsupported,
+                  "only INT8 weight quantization is implemented on the device");
+    m->m->quantize();
+  });
+}
+
+int nnhip_decoder_get_quantized(const nnhip_model *m, int layer, int which,
+                                int8_t *codes, float *scales) {
+  return guard([&] {
+    REQ(m && codes && scales, "nnhip_decoder_get_quantized: NULL argument");
+    m->m->get_quantized(layer, which, codes, scales);
+  });
+}
+
+int nnhip_decoder_forward(nnhip_model *mm, nnhip_kvcache *cache,
+                          const int32_t *ids, int B, int S, float *logits) {
+  return guard([&] {
+    REQ(mm && ids && logits && B > 0 && S > 0, "nnhip_decoder_forward: bad argument");
+    nnhip::Model &m = *mm->m;
+    hipStream_t st = m.ctx->stream;
+    nnhip::KVCache *kv = cache ? cache->c.get() : nullptr;
+    if (kv) {
+      REQ(kv->m == &m, "nnhip_decoder_forward: cache belongs to another model");
+      REQ(kv->B == B, "nnhip_decoder_forward: cache batch differs from B");
+      for (int b = 0; b < B; ++b)
+        NNHIP_REQUIRE(kv->host_len[b] + S <= m.max_seq, nnhip::kErrCapacity,
+                      "Sequence length S plus past cached length exceeds max_seq_len");
+    } else {
+      NNHIP_REQUIRE(S <= m.max_seq, nnhip::kErrCapacity,
+                    "Sequence length S plus past cached length exceeds max_seq_len");
+    }
+    auto d_ids = upload(st, ids, (size_t)B * S);
+    nnhip::DevBuf<float> d_log((size_t)B * S * m.V);
+    int max_keys = S;
+    if (kv) for (int b = 0; b < B; ++b) max_keys = std::max(max_keys, kv->host_len[b] + S);
+    m.forward(kv, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
+              max_keys, d_log.p, false);
+    NNHIP_CHECK(hipMemcpyAsync(logits, d_log.p, d_log.bytes(), hipMemcpyDeviceToHost, st));
+    if (kv) {
+      for (int b = 0; b < B; ++b) kv->host_len[b] += S;
+      NNHIP_CHECK(hipMemcpyAsync(kv->len.p, kv->host_len.data(), (size_t)B * 4,
+                                 hipMemcpyHostToDevice, st));
+    }
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+// ---- KV cache --------------------------------------------------------------
+int nnhip_kvcache_create(nnhip_model *m, int batch, int quantized,
+                         nnhip_kvcache **out) {
+  return guard([&] {
+    REQ(m && out, "nnhip_kvcache_create: NULL argument");
+    NNHIP_REQUIRE(!quantized, nnhip::kErrUnsupported,
+                  "the int8 KV cache is not implemented on the device");
+    std::unique_ptr<nnhip_kvcache> c(new nnhip_kvcache);
+    c->c.reset(new nnhip::KVCache(m->m.get(), batch, m->m->max_seq));
+    *out = c.release();
+  });
+}
+
+int nnhip_kvcache_free(nnhip_kvcache *c) {
+  return guard([&] {
+    if (!c) return;
+    (void)hipStreamSynchronize(c->c->m->ctx->stream);
+    delete c;
+  });
+}
+
+int nnhip_kvcache_length(const nnhip_kvcache *c, int b, int *len) {
+  return guard([&] {
+    REQ(c && len && b >= 0 && b < c->c->B, "nnhip_kvcache_length: bad argument");
+    *len = c->c->host_len[b];
+  });
+}
+
+int nnhip_kvcache_truncate(nnhip_kvcache *c, int b, int len) {
+  return guard([&] {
+    REQ(c && b >= 0 && b < c->c->B && len >= 0, "nnhip_kvcache_truncate: bad argument");
+    if (len < c->c->host_len[b]) {
+      c->c->host_len[b] = len;
+      c->c->sync_len_to_device();
+    }
+  });
+}
+
+// ---- generation ------------------------------------------------------------
+int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
+                               const int32_t *prompt, int P, int max_new,
+                               int lookahead, float temperature, int top_k,
+                               float top_p, uint64_t seed,
+                               int quantized_cache, int32_t *out,
+                               nnhip_spec_stats *stats) {
+  return guard([&] {
+    REQ(target && draft && prompt && out, "nnhip_generate_speculative: NULL argument");
+    NNHIP_REQUIRE(!quantized_cache, nnhip::kErrUnsupported,
+                  "the int8 KV cache is not implemented on the device");
+    nnhip::SpecStats st{};
+    nnhip::generate_speculative_batch(*target->m, *draft->m, 1, prompt, P,
+                                      max_new, lookahead, temperature, top_k,
+                                      top_p, seed, 0, out, &st, nullptr);
+    if (stats) std::memcpy(stats, &st, sizeof(st));
+  });
+}
+
+int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
+                                     int B, const int32_t *prompts, int P,
+                                     int max_new, int lookahead,
+                                     float temperature, int top_k, float top_p,
+                                     uint64_t seed, uint32_t seq0,
+                                     int32_t *out, nnhip_spec_stats *stats,
+                                     nnhip_spec_timing *timing) {
+  return guard([&] {
+    REQ(target && draft && prompts && out, "nnhip_generate_speculative_batch: NULL argument");
+    static_assert(sizeof(nnhip::SpecStats) == sizeof(nnhip_spec_stats), "stats layout");
+    static_assert(sizeof(nnhip::SpecTiming) == sizeof(nnhip_spec_timing), "timing layout");
+    nnhip::generate_speculative_batch(
+        *target->m, *draft->m, B, prompts, P, max_new, lookahead, temperature,
+        top_k, top_p, seed, seq0, out,
+        reinterpret_cast<nnhip::SpecStats *>(stats),
+        reinterpret_cast<nnhip::SpecTiming *>(timing));
+  });
+}
+
+int nnhip_generate_advanced(nnhip_model *m, const int32_t *prompt, int P,
+                            int max_new, float temperature, int top_k,
+                            float top_p, uint64_t seed, int use_kv_cache,
+                            int32_t *out) {
+  return guard([&] {
+    REQ(m && prompt && out, "nnhip_generate_advanced: NULL argument");
+    nnhip::generate_advanced_batch(*m->m, 1, prompt, P, max_new, temperature,
+                                   top_k, top_p, seed, 0, use_kv_cache != 0,
+                                   out);
+  });
+}
+
+int nnhip_generate_advanced_batch(nnhip_model *m, int B,
+                                  const int32_t *prompts, int P, int max_new,
+                                  float temperature, int top_k, float top_p,
+                                  uint64_t seed, uint32_t seq0,
+                                  int use_kv_cache, int32_t *out) {
+  return guard([&] {
+    REQ(m && prompts && out, "nnhip_generate_advanced_batch: NULL argument");
+    nnhip::generate_advanced_batch(*m->m, B, prompts, P, max_new, temperature,
+                                   top_k, top_p, seed, seq0, use_kv_cache != 0,
+                                   out);
+  });
+}
+
+// ---- fused device ops --------------------------------------------------------
+int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
+                      int8_t *codes, float *scales) {
+  return guard([&] {
+    REQ(ctx && w && codes && scales && in > 0 && out > 0, "nnhip_quantize_w8: bad argument");
+    hipStream_t st = ctx->c.stream;
+    nnhip::DevBuf<float> t((size_t)in * out);
+    nnhip::launch_transpose_into(st, w, in, out, t.p, 0, 1);
+    nnhip::launch_quantize_w8(st, t.p, out, in, codes, scales);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+namespace {
+struct LimbScratch {
+  nnhip::DevBuf<int8_t> limbs;
+  nnhip::DevBuf<int> rexp;
+  int mpad = 0;
+  void ensure(int rows, int K) {
+    const int mp = (rows + 63) / 64 * 64;
+    if ((size_t)3 * mp * K > limbs.n) limbs.alloc((size_t)3 * mp * K);
+    if ((size_t)mp > rexp.n) rexp.alloc(mp);
+    mpad = mp;
+  }
+};
+}  // namespace
+
+int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
+                       const int8_t *codes, const float *scales,
+                       const float *bias, int N, float *y, int path) {
+  return guard([&] {
+    REQ(ctx && x && codes && scales && bias && y && rows > 0 && K > 0 && N > 0,
+        "nnhip_linear_w8a32: bad argument");
+    hipStream_t st = ctx->c.stream;
+    const bool mfma_ok = K % 128 == 0 && N % 64 == 0;
+    bool mfma = path == 2 || (path == 0 && rows >= 16 && mfma_ok);
+    NNHIP_REQUIRE(!(path == 2 && !mfma_ok), nnhip::kErrArg,
+                  "MFMA path needs K % 128 == 0 and N % 64 == 0");
+    if (mfma) {
+      LimbScratch ls;
+      ls.ensure(rows, K);
+      nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
+      nnhip::launch_gemm_limb(st, ls.limbs.p, ls.mpad, ls.rexp.p, rows, K, N,
+                              codes, scales, bias, nullptr, 0, y, N,
+                              nnhip::kEpiBias);
+      NNHIP_CHECK(hipStreamSynchronize(st));
+    } else {
+      nnhip::launch_gemv(st, x, K, rows, K, N, codes, nullptr, scales, bias,
+                         nullptr, 0, y, N, nnhip::kEpiBias);
+    }
+  });
+}
+
+int nnhip_linear_f32(nnhip_ctx *ctx, const float *x, int rows, int K,
+                     const float *w, const float *bias, int N, float *y) {
+  return guard([&] {
+    REQ(ctx && x && w && bias && y && rows > 0 && K > 0 && N > 0,
+        "nnhip_linear_f32: bad argument");
+    nnhip::launch_gemv(ctx->c.stream, x, K, rows, K, N, nullptr, w, nullptr,
+                       bias, nullptr, 0, y, N, nnhip::kEpiBias);
+  });
+}
+
+int nnhip_linear_limb_totals(nnhip_ctx *ctx, const float *x, int rows, int K,
+                             const int8_t *codes, int N, int64_t *totals,
+                             int32_t *rexp, int8_t *limbs) {
+  return guard([&] {
+    REQ(ctx && x && codes && totals && rows > 0, "nnhip_linear_limb_totals: bad argument");
+    REQ(K % 128 == 0 && N % 64 == 0, "MFMA path needs K % 128 == 0 and N % 64 == 0");
+    hipStream_t st = ctx->c.stream;
+    LimbScratch ls;
+    ls.ensure(rows, K);
+    NNHIP_CHECK(hipMemsetAsync(ls.limbs.p, 0, ls.limbs.bytes(), st));
+    nnhip::DevBuf<float> dummy(N);
+    nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
+    nnhip::launch_gemm_limb(st, ls.limbs.p, ls.mpad, ls.rexp.p, rows, K, N,
+                            codes, dummy.p, dummy.p, nullptr, 0,
+                            reinterpret_cast<float *>(totals), N,
+                            nnhip::kEpiTotals);
+    if (rexp) NNHIP_CHECK(hipMemcpyAsync(rexp, ls.rexp.p, (size_t)rows * 4, hipMemcpyDeviceToDevice, st));
+    if (limbs) NNHIP_CHECK(hipMemcpyAsync(limbs, ls.limbs.p, ls.limbs.bytes(), hipMemcpyDeviceToDevice, st));
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                         int H, int D, const int32_t *pos, float *q_out,
+                         float *kcache, float *vcache, int cap) {
+  return guard([&] {
+    REQ(ctx && qkv && pos && q_out && kcache && vcache && B > 0 && S > 0 &&
+            H > 0 && D > 0 && D % 2 == 0 && cap > 0,
+        "nnhip_rope_kv_append: bad argument");
+    hipStream_t st = ctx->c.stream;
+    // RoPE factors for positions [0, cap) by the reference's float formula
+    const int half = D / 2;
+    std::vector<float> hc((size_t)cap * half), hs((size_t)cap * half);
+    for (int p = 0; p < cap; ++p)
+      for (int j = 0; j < half; ++j) {
+        const float theta = std::pow(10000.0f, -2.0f * (float)j / (float)D);
+        const float omega = (float)p * theta;
+        hc[(size_t)p * half + j] = std::cos(omega);
+        hs[(size_t)p * half + j] = std::sin(omega);
+      }
+    auto dc = upload(st, hc.data(), hc.size());
+    auto ds = upload(st, hs.data(), hs.size());
+    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
+                          q_out, kcache, vcache, cap, (int64_t)H * cap * D);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
+                       const float *vcache, int cap, const int32_t *pos0,
+                       int B, int S, int H, int Hkv, int D, float *out) {
+  return guard([&] {
+    REQ(ctx && q && kcache && vcache && pos0 && out && B > 0 && S > 0 &&
+            H > 0 && Hkv > 0 && cap > 0,
+        "nnhip_attention_kq: bad argument");
+    hipStream_t st = ctx->c.stream;
+    const int max_keys = cap;
+    const int64_t pe = nnhip::attention_partial_elems(B, S, H, D, max_keys);
+    nnhip::DevBuf<float> part(pe > 0 ? pe : 1);
+    nnhip::launch_attention(st, q, kcache, vcache, B, S, H, Hkv, D, cap,
+                            (int64_t)Hkv * cap * D, pos0, 0, nullptr, max_keys,
+                            part.p, pe, out);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+int nnhip_layernorm(nnhip_ctx *ctx, const float *x, int rows, int d,
+                    const float *gamma, const float *beta, float *y) {
+  return guard([&] {
+    REQ(ctx && x && gamma && beta && y && rows > 0 && d > 0, "nnhip_layernorm: bad argument");
+    nnhip::launch_layernorm(ctx->c.stream, x, rows, d, gamma, beta, y, nullptr,
+                            0, nullptr);
+  });
+}
+
+int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
+                      float temperature, const float *u, int32_t *tok,
+                      float *probs) {
+  return guard([&] {
+    REQ(ctx && logits && u && tok && B > 0 && V > 0, "nnhip_sample_rows: bad argument");
+    nnhip::launch_sample_rows(ctx->c.stream, logits, B, V, temperature, u, tok,
+                              probs);
+  });
+}
+
+int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
+                      const float *dlogits, const int32_t *dtok,
+                      const float *u_accept, const float *u_resample, int B,
+                      int k, int V, float temperature, int32_t *n_accept,
+                      int32_t *next_tok) {
+  return guard([&] {
+    REQ(ctx && tlogits && dlogits && dtok && u_accept && u_resample &&
+            n_accept && next_tok && B > 0 && k > 0 && V > 0,
+        "nnhip_spec_accept: bad argument");
+    nnhip::launch_accept_bench(ctx->c.stream, tlogits, dlogits, dtok, u_accept,
+                               u_resample, B, k, V, temperature, n_accept,
+                               next_tok);
+  });
+}
+
+}  // extern "C"

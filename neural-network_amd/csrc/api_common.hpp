@@ -1,0 +1,43 @@
+// Shared by the C ABI translation units: opaque handle types and the
+// exception-to-status guard.
+#pragma once
+
+#include "engine.hpp"
+#include "nnhip.h"
+
+#include <memory>
+#include <string>
+
+struct nnhip_ctx {
+  nnhip::Ctx c;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+struct nnhip_model {
+  std::unique_ptr<nnhip::Model> m;
+};
+struct nnhip_kvcache {
+  std::unique_ptr<nnhip::KVCache> c;
+};
+
+namespace nnhip {
+
+void set_last_error(const std::string &msg);
+
+template <typename F>
+int guard(F &&f) {
+  try {
+    f();
+    return NNHIP_OK;
+  } catch (const Error &e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc &) {
+    set_last_error("host allocation failed");
+    return NNHIP_EHIP;
+  } catch (const std::exception &e) {
+    set_last_error(e.what());
+    return NNHIP_EARG;
+  }
+}
+
+}  // namespace nnhip

@@ -1,0 +1,431 @@
+// Token embedding, RoPE + KV-cache append, k-query causal attention over the
+// device-resident KV cache, and LayerNorm for gfx950.
+//
+// Replaces the host loops of MultiHeadAttention::forward (layer.cpp:593-994):
+// RoPE (tensor.cpp:1126-1226), the O(S) KV concat (layer.cpp:758-807), the
+// fused ThreadPool attention (layer.cpp:842-952), plus Embedding
+// (cpu_backend.cpp:998-1033) and LayerNorm (layer.cpp:242-261).
+//
+// KV cache layout: per layer [B][H_kv][cap][D] fp32, so one (sequence, head)
+// is a contiguous [cap][D] slab; appending is a write at the sequence's own
+// length and truncation (KVCache::truncate, layer.cpp:67-149) is a length
+// update.  Each sequence carries its own length, so a batch is ragged.
+#include "nnhip_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace nnhip {
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kKeysPerSplit = 256;
+constexpr int kMaxQ = 8;       // queries per workgroup
+constexpr int kMaxD = 64;      // head dim handled by the attention kernel
+
+// Embedding gather (cpu_backend.cpp:1020-1025): ids outside [0, vocab) read
+// row 0.  Row t = b*S + s takes ids[b*stride_b + s].
+__global__ __launch_bounds__(256) void embed_kernel(
+    const float *__restrict__ emb, int vocab, int d,
+    const int32_t *__restrict__ ids, int S, int stride_b,
+    float *__restrict__ x) {
+  const int t = blockIdx.x;
+  const int b = t / S, s = t % S;
+  int id = ids[(int64_t)b * stride_b + s];
+  if (id < 0 || id >= vocab) id = 0;
+  const float *src = emb + (int64_t)id * d;
+  float *dst = x + (int64_t)t * d;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = src[i];
+}
+
+// verify input of one cycle: [generated.back(), c_0 .. c_{k-1}] per sequence
+// (layer.cpp:1560-1566).
+__global__ void build_verify_ids_kernel(const int32_t *__restrict__ cur,
+                                        const int32_t *__restrict__ cand, int B,
+                                        int k, int32_t *__restrict__ ids) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * (k + 1)) return;
+  int b = i / (k + 1), s = i % (k + 1);
+  ids[i] = s == 0 ? cur[b] : cand[b * k + s - 1];
+}
+
+// RoPE on q and k at position base[b] + off + s (tensor.cpp:1141-1173, with
+// the cos/sin table computed on the host by the same float formula), then
+// append rotated k and v to the cache.  qkv row t = b*S + s holds
+// [q(H*D) | k(H*D) | v(H*D)].
+__global__ __launch_bounds__(256) void rope_kv_kernel(
+    const float *__restrict__ qkv, int S, int H, int D,
+    const int32_t *__restrict__ base, int off,
+    const int32_t *__restrict__ active, const float *__restrict__ cosb,
+    const float *__restrict__ sinb, float *__restrict__ qrot,
+    float *__restrict__ kc, float *__restrict__ vc, int cap,
+    int64_t seq_stride) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.x;
+  const int b = t / S, s = t % S;
+  if (active && !active[b]) return;
+  const int pos = base[b] + off + s;
+  if (pos < 0 || pos >= cap) return;
+  const int E = H * D, half = D / 2;
+  const float *row = qkv + (int64_t)t * 3 * E;
+  for (int i = threadIdx.x; i < H * half; i += blockDim.x) {
+    const int h = i / half, j = i % half;
+    const float c = cosb[(int64_t)pos * half + j];
+    const float sn = sinb[(int64_t)pos * half + j];
+    const int e = h * D + 2 * j;
+    float xe = row[e], xo = row[e + 1];
+    qrot[(int64_t)t * E + e] = xe * c - xo * sn;
+    qrot[(int64_t)t * E + e + 1] = xe * sn + xo * c;
+    xe = row[E + e]; xo = row[E + e + 1];
+    float *kd = kc + b * seq_stride + ((int64_t)h * cap + pos) * D + 2 * j;
+    kd[0] = xe * c - xo * sn;
+    kd[1] = xe * sn + xo * c;
+    float *vd = vc + b * seq_stride + ((int64_t)h * cap + pos) * D + 2 * j;
+    vd[0] = row[2 * E + e];
+    vd[1] = row[2 * E + e + 1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K attention.  Grid (split, head, b * n_qblocks).  32 lane groups of 8
+// lanes; a group owns one key at a time (8 dims per lane) and keeps an online
+// softmax (max, sum, acc) per query; groups merge by shuffles, waves through
+// LDS.  Arithmetic: score = dot / sqrt(D), keys j > q_pos masked, p =
+// exp(score - max), out = (sum p v) * (1 / sum p), as layer.cpp:859-948.
+// ---------------------------------------------------------------------------
+template <int SQ>
+__global__ __launch_bounds__(256) void attn_kernel(
+    const float *__restrict__ q, const float *__restrict__ kc,
+    const float *__restrict__ vc, int S, int H, int Hkv, int D, int cap,
+    int64_t seq_stride, const int32_t *__restrict__ base, int off,
+    const int32_t *__restrict__ active, int nsplit, int nqb,
+    float *__restrict__ part, float *__restrict__ out) {
+  __shared__ float s_ml[4][SQ][2];
+  __shared__ float s_acc[4][SQ][kMaxD];
+  const int sp = blockIdx.x, h = blockIdx.y;
+  const int b = blockIdx.z / nqb, qb = blockIdx.z % nqb;
+  if (active && !active[b]) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = w * 8 + (lane >> 3), sub = lane & 7;
+  const int q0 = qb * kMaxQ;
+  const int nq = min(SQ, S - q0);
+  const int E = H * D;
+  const int hk = h / (H / Hkv);
+  const int pos0 = base[b] + off + q0;         // position of query q0
+  const int kend_all = min(pos0 + nq, cap);    // keys [0, kend_all) visible
+  const int kbeg = sp * kKeysPerSplit;
+  const int kend = min(kbeg + kKeysPerSplit, kend_all);
+  const float scale = sqrtf((float)D);
+  const int dl = D / 8;                        // dims per lane (<= 8)
+
+  float qv[SQ][8];
+#pragma unroll
+  for (int i = 0; i < SQ; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      int dd = sub * dl + e;
+      qv[i][e] = (i < nq && e < dl)
+                     ? q[((int64_t)b * S + q0 + i) * E + h * D + dd]
+                     : 0.f;
+    }
+  float m[SQ], l[SQ], acc[SQ][8];
+#pragma unroll
+  for (int i = 0; i < SQ; ++i) {
+    m[i] = -INFINITY; l[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+  }
+  const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
+  const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
+  for (int j = kbeg + g; j < kend; j += 32) {
+    float kv[8], vv[8];
+    if (dl == 8) {
+      const float4 *kp = reinterpret_cast<const float4 *>(kb + (int64_t)j * D + sub * 8);
+      const float4 *vp = reinterpret_cast<const float4 *>(vb + (int64_t)j * D + sub * 8);
+      float4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
+      kv[0] = k0.x; kv[1] = k0.y; kv[2] = k0.z; kv[3] = k0.w;
+      kv[4] = k1.x; kv[5] = k1.y; kv[6] = k1.z; kv[7] = k1.w;
+      vv[0] = v0.x; vv[1] = v0.y; vv[2] = v0.z; vv[3] = v0.w;
+      vv[4] = v1.x; vv[5] = v1.y; vv[6] = v1.z; vv[7] = v1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        kv[e] = e < dl ? kb[(int64_t)j * D + sub * dl + e] : 0.f;
+        vv[e] = e < dl ? vb[(int64_t)j * D + sub * dl + e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < SQ; ++i) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += qv[i][e] * kv[e];
+      dot += __shfl_xor(dot, 1, kWave);
+      dot += __shfl_xor(dot, 2, kWave);
+      dot += __shfl_xor(dot, 4, kWave);
+      if (i >= nq || j > pos0 + i) continue;   // causal mask
+      const float sc = dot / scale;
+      if (sc > m[i]) {
+        const float corr = expf(m[i] - sc);
+        l[i] *= corr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i][e] *= corr;
+        m[i] = sc;
+      }
+      const float p = expf(sc - m[i]);
+      l[i] += p;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[i][e] += p * vv[e];
+    }
+  }
+  // merge the 8 lane groups of this wave
+#pragma unroll
+  for (int o = 8; o <= 32; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < SQ; ++i) {
+      const float mo = __shfl_xor(m[i], o, kWave);
+      const float lo = __shfl_xor(l[i], o, kWave);
+      const float mn = fmaxf(m[i], mo);
+      const float a = (m[i] == -INFINITY) ? 0.f : expf(m[i] - mn);
+      const float c = (mo == -INFINITY) ? 0.f : expf(mo - mn);
+      l[i] = l[i] * a + lo * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ao = __shfl_xor(acc[i][e], o, kWave);
+        acc[i][e] = acc[i][e] * a + ao * c;
+      }
+      m[i] = mn;
+    }
+  }
+  if (lane < 8) {
+#pragma unroll
+    for (int i = 0; i < SQ; ++i) {
+      if (lane == 0) { s_ml[w][i][0] = m[i]; s_ml[w][i][1] = l[i]; }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < dl) s_acc[w][i][sub * dl + e] = acc[i][e];
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nq * D; t += blockDim.x) {
+    const int i = t / D, dd = t % D;
+    float mn = -INFINITY;
+    for (int ww = 0; ww < 4; ++ww) mn = fmaxf(mn, s_ml[ww][i][0]);
+    float ls = 0.f, as = 0.f;
+    for (int ww = 0; ww < 4; ++ww) {
+      const float mw = s_ml[ww][i][0];
+      const float f = (mw == -INFINITY) ? 0.f : expf(mw - mn);
+      ls += s_ml[ww][i][1] * f;
+      as += s_acc[ww][i][dd] * f;
+    }
+    const int64_t row = (int64_t)b * S + q0 + i;
+    if (nsplit == 1) {
+      const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+      out[row * E + h * D + dd] = as * inv;
+    } else {
+      const int64_t pi = (row * H + h) * nsplit + sp;
+      float *pp = part + pi * (D + 2);
+      if (dd == 0) { pp[0] = mn; pp[1] = ls; }
+      pp[2 + dd] = as;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void attn_combine_kernel(
+    const float *__restrict__ part, int S, int H, int D, int nsplit,
+    const int32_t *__restrict__ active, float *__restrict__ out) {
+  const int64_t rh = blockIdx.x;            // row * H + h
+  const int64_t row = rh / H;
+  const int h = (int)(rh % H);
+  if (active && !active[row / S]) return;
+  const float *pp = part + rh * nsplit * (D + 2);
+  float mn = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mn = fmaxf(mn, pp[s * (D + 2)]);
+  for (int dd = threadIdx.x; dd < D; dd += blockDim.x) {
+    float ls = 0.f, as = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = pp[s * (D + 2)];
+      const float f = (ms == -INFINITY) ? 0.f : expf(ms - mn);
+      ls += pp[s * (D + 2) + 1] * f;
+      as += pp[s * (D + 2) + 2 + dd] * f;
+    }
+    const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+    out[row * H * D + h * D + dd] = as * inv;
+  }
+}
+
+// LayerNorm (layer.cpp:242-261): mean = sum/N, var = sum((x-mean)^2)/N,
+// y = (x - mean) / sqrt(var + 1e-5) * gamma + beta.  Optionally also writes
+// the int8 digits of y for the next MFMA GEMM (same rule as act_quant).
+__global__ __launch_bounds__(256) void layernorm_kernel(
+    const float *__restrict__ hin, int d, const float *__restrict__ g,
+    const float *__restrict__ bt, float *__restrict__ y,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+#pragma clang fp contract(off)
+  __shared__ float sred[4];
+  constexpr int kPer = 16;                 // d <= 4096
+  const int64_t row = blockIdx.x;
+  const float *xr = hin + row * d;
+  float v[kPer];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int c = threadIdx.x + i * 256;
+    v[i] = c < d ? xr[c] : 0.f;
+    s += v[i];
+  }
+  auto block_sum = [&](float a) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, kWave);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = a;
+    __syncthreads();
+    return (sred[0] + sred[1]) + (sred[2] + sred[3]);
+  };
+  const float N = (float)d;
+  const float mean = block_sum(s) / N;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int c = threadIdx.x + i * 256;
+    if (c < d) { float df = v[i] - mean; sq += df * df; }
+  }
+  const float var = block_sum(sq) / N;
+  const float sd = sqrtf(var + 1e-5f);
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int c = threadIdx.x + i * 256;
+    if (c < d) {
+      float xh = (v[i] - mean) / sd;
+      v[i] = xh * g[c] + bt[c];
+      y[row * d + c] = v[i];
+      mx = fmaxf(mx, fabsf(v[i]));
+    }
+  }
+  if (!limbs) return;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+  int e = 0;
+  if (mx > 0.f) { int ex; (void)frexpf(mx, &ex); e = kLimbBits - ex; }
+  if (threadIdx.x == 0) rexp[row] = e;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int c = threadIdx.x + i * 256;
+    if (c < d) {
+      int X = (int)rintf(ldexpf(v[i], e));
+      int lo = (int)(int8_t)(X & 0xff);
+      int t = (X - lo) >> 8;
+      int mid = (int)(int8_t)(t & 0xff);
+      int hi = (t - mid) >> 8;
+      limbs[row * d + c] = (int8_t)hi;
+      limbs[((int64_t)mpad + row) * d + c] = (int8_t)mid;
+      limbs[((int64_t)2 * mpad + row) * d + c] = (int8_t)lo;
+    }
+  }
+}
+
+__global__ void add_scalar_kernel(int32_t *p, int n, int v) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] += v;
+}
+
+}  // namespace
+
+void launch_add_scalar(hipStream_t st, int32_t *p, int n, int v) {
+  hipLaunchKernelGGL(add_scalar_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                     st, p, n, v);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_embed(hipStream_t st, const float *emb, int vocab, int d,
+                  const int32_t *ids, int rows, float *x) {
+  // ids contiguous, one per row
+  hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, st, emb, vocab, d,
+                     ids, 1, 1, x);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
+                          const int32_t *ids, int B, int S, int stride_b,
+                          float *x) {
+  hipLaunchKernelGGL(embed_kernel, dim3(B * S), dim3(256), 0, st, emb, vocab,
+                     d, ids, S, stride_b, x);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
+                             const int32_t *cand, int B, int k, int32_t *ids) {
+  int n = B * (k + 1);
+  hipLaunchKernelGGL(build_verify_ids_kernel, dim3((n + 255) / 256), dim3(256),
+                     0, st, cur, cand, B, k, ids);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
+                    int D, const int32_t *base, int off, const int32_t *active,
+                    const float *cosb, const float *sinb, float *qrot,
+                    float *kc, float *vc, int cap, int64_t seq_stride) {
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(B * S), dim3(256), 0, st, qkv, S, H,
+                     D, base, off, active, cosb, sinb, qrot, kc, vc, cap,
+                     seq_stride);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys) {
+  int nsplit = (max_keys + kKeysPerSplit - 1) / kKeysPerSplit;
+  if (nsplit <= 1) return 0;
+  return (int64_t)B * S * H * nsplit * (D + 2);
+}
+
+void launch_attention(hipStream_t st, const float *q, const float *kc,
+                      const float *vc, int B, int S, int H, int Hkv, int D,
+                      int cap, int64_t seq_stride, const int32_t *base,
+                      int off, const int32_t *active, int max_keys,
+                      float *part, int64_t part_elems, float *out) {
+  NNHIP_REQUIRE(D % 8 == 0 && D <= kMaxD, kErrArg,
+                "attention: head dim must be a multiple of 8 and <= 64");
+  NNHIP_REQUIRE(Hkv > 0 && H % Hkv == 0, kErrArg, "attention: bad kv heads");
+  if (max_keys < 1) max_keys = 1;
+  const int nsplit = (max_keys + kKeysPerSplit - 1) / kKeysPerSplit;
+  NNHIP_REQUIRE(nsplit == 1 || part_elems >= attention_partial_elems(B, S, H, D, max_keys),
+                kErrArg, "attention: partial buffer too small");
+  const int nqb = (S + kMaxQ - 1) / kMaxQ;
+  const int sq = S < kMaxQ ? S : kMaxQ;
+  dim3 grid(nsplit, H, B * nqb);
+#define NNHIP_ATTN(SQV)                                                      \
+  hipLaunchKernelGGL((attn_kernel<SQV>), grid, dim3(256), 0, st, q, kc, vc, S, \
+                     H, Hkv, D, cap, seq_stride, base, off, active, nsplit,    \
+                     nqb, part, out)
+  switch (sq) {
+    case 1: NNHIP_ATTN(1); break;
+    case 2: NNHIP_ATTN(2); break;
+    case 3: NNHIP_ATTN(3); break;
+    case 4: NNHIP_ATTN(4); break;
+    case 5: NNHIP_ATTN(5); break;
+    case 6: NNHIP_ATTN(6); break;
+    case 7: NNHIP_ATTN(7); break;
+    default: NNHIP_ATTN(8); break;
+  }
+#undef NNHIP_ATTN
+  NNHIP_CHECK(hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S * H), dim3(64), 0, st,
+                       part, S, H, D, nsplit, active, out);
+    NNHIP_CHECK(hipGetLastError());
+  }
+}
+
+void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
+                      const float *g, const float *b, float *y,
+                      int8_t *limbs, int mpad, int *rexp) {
+  NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
+  hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,
+                     b, y, limbs, mpad, rexp);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+}  // namespace nnhip

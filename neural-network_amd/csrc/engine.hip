@@ -1,0 +1,592 @@
+// Host engine of libnnhip.so (see engine.hpp).
+#include "engine.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+
+namespace nnhip {
+
+namespace {
+
+constexpr int kLimbMinRows = 16;
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Table of RoPE factors for positions [0, max_seq) by the float formula of
+// Tensor::rope (tensor.cpp:1147-1153): theta = pow(10000, -2j/D),
+// omega = pos * theta, cos/sin(omega).
+void rope_tables(int max_seq, int D, std::vector<float> &c,
+                 std::vector<float> &s) {
+  const int half = D / 2;
+  c.resize((size_t)max_seq * half);
+  s.resize((size_t)max_seq * half);
+  for (int p = 0; p < max_seq; ++p) {
+    const float m = (float)p;
+    for (int j = 0; j < half; ++j) {
+      const float theta =
+          std::pow(10000.0f, -2.0f * (float)j / (float)D);
+      const float omega = m * theta;
+      c[(size_t)p * half + j] = std::cos(omega);
+      s[(size_t)p * half + j] = std::sin(omega);
+    }
+  }
+}
+
+struct ParamRef {
+  enum Kind { kEmb, kWeight, kBias, kVec } kind;
+  Linear *lin = nullptr;
+  DevBuf<float> *vec = nullptr;
+  int K = 0, N = 0;           // logical [K][N] (reference layout)
+  int64_t row_base = 0, row_stride = 1;
+};
+
+}  // namespace
+
+void Linear::init(int k, int n) {
+  K = k; N = n;
+  w.alloc((size_t)N * K);
+  b.alloc(N);
+  s.alloc(N);
+  quant = false;
+}
+
+Model::Model(Ctx *c, int vocab, int d_model, int heads, int d_ff,
+             int n_layers, int max_seq_len)
+    : ctx(c), V(vocab), d(d_model), H(heads), D(d_model / heads), F(d_ff),
+      L(n_layers), max_seq(max_seq_len) {
+  NNHIP_REQUIRE(vocab > 0 && d_model > 0 && heads > 0 && d_ff > 0 &&
+                    n_layers > 0 && max_seq_len > 0,
+                kErrArg, "decoder: sizes must be positive");
+  NNHIP_REQUIRE(d_model % heads == 0, kErrArg,
+                "embed_dim must be divisible by num_heads");
+  NNHIP_REQUIRE(D % 8 == 0 && D <= 64, kErrUnsupported,
+                "head dim must be a multiple of 8 and at most 64");
+  NNHIP_REQUIRE(d % 4 == 0 && F % 4 == 0 && d <= 4096 && F <= 4096, kErrUnsupported,
+                "d_model and d_ff must be multiples of 4 and at most 4096");
+  hipStream_t st = ctx->stream;
+  emb.alloc((size_t)V * d);
+  layers.resize(L);
+  for (auto &ly : layers) {
+    ly.qkv.init(d, 3 * d);
+    ly.o.init(d, d);
+    ly.gu.init(d, 2 * F);
+    ly.down.init(F, d);
+    ly.g1.alloc(d); ly.b1.alloc(d); ly.g2.alloc(d); ly.b2.alloc(d);
+  }
+  lm.init(d, V);
+  init_normal(0, 0.0f);  // zero weights, zero biases, gamma 1, beta 0
+  std::vector<float> hc, hs;
+  rope_tables(max_seq, D, hc, hs);
+  cosb.alloc(hc.size());
+  sinb.alloc(hs.size());
+  NNHIP_CHECK(hipMemcpyAsync(cosb.p, hc.data(), hc.size() * 4,
+                             hipMemcpyHostToDevice, st));
+  NNHIP_CHECK(hipMemcpyAsync(sinb.p, hs.data(), hs.size() * 4,
+                             hipMemcpyHostToDevice, st));
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+static ParamRef param_ref(Model &m, int idx) {
+  ParamRef r{};
+  const int last = 1 + 18 * m.L;
+  NNHIP_REQUIRE(idx >= 0 && idx <= last + 1, kErrArg, "parameter index out of range");
+  if (idx == 0) { r.kind = ParamRef::kEmb; r.K = m.V; r.N = m.d; return r; }
+  if (idx == last) { r.kind = ParamRef::kWeight; r.lin = &m.lm; r.K = m.d; r.N = m.V; return r; }
+  if (idx == last + 1) { r.kind = ParamRef::kBias; r.lin = &m.lm; r.K = 1; r.N = m.V; return r; }
+  LayerW &ly = m.layers[(idx - 1) / 18];
+  const int j = (idx - 1) % 18;
+  const int d = m.d, F = m.F;
+  switch (j / 2) {
+    case 0: case 1: case 2:
+      r.lin = &ly.qkv; r.K = d; r.N = d; r.row_base = (int64_t)(j / 2) * d; break;
+    case 3: r.lin = &ly.o; r.K = d; r.N = d; break;
+    case 4: r.lin = &ly.gu; r.K = d; r.N = F; r.row_base = 0; r.row_stride = 2; break;
+    case 5: r.lin = &ly.gu; r.K = d; r.N = F; r.row_base = 1; r.row_stride = 2; break;
+    case 6: r.lin = &ly.down; r.K = F; r.N = d; break;
+    default: {
+      DevBuf<float> *v4[4] = {&ly.g1, &ly.b1, &ly.g2, &ly.b2};
+      r.kind = ParamRef::kVec; r.vec = v4[j - 14]; r.K = 1; r.N = d;
+      return r;
+    }
+  }
+  if (j % 2 == 0) r.kind = ParamRef::kWeight;
+  else { r.kind = ParamRef::kBias; r.K = 1; }
+  return r;
+}
+
+void Model::param_shape(int idx, int64_t *rows, int64_t *cols) const {
+  ParamRef r = param_ref(const_cast<Model &>(*this), idx);
+  *rows = r.K; *cols = r.N;
+}
+
+void Model::set_param(int idx, const float *host) {
+  hipStream_t st = ctx->stream;
+  ParamRef r = param_ref(*this, idx);
+  const size_t n = (size_t)r.K * r.N;
+  if (r.kind == ParamRef::kEmb || r.kind == ParamRef::kVec) {
+    float *dst = r.kind == ParamRef::kEmb ? emb.p : r.vec->p;
+    NNHIP_CHECK(hipMemcpyAsync(dst, host, n * 4, hipMemcpyHostToDevice, st));
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    return;
+  }
+  DevBuf<float> stage(n);
+  NNHIP_CHECK(hipMemcpyAsync(stage.p, host, n * 4, hipMemcpyHostToDevice, st));
+  if (r.kind == ParamRef::kWeight)
+    launch_transpose_into(st, stage.p, r.K, r.N, r.lin->w.p, r.row_base,
+                          r.row_stride);
+  else
+    launch_transpose_into(st, stage.p, 1, r.N, r.lin->b.p, r.row_base,
+                          r.row_stride);
+  if (r.kind == ParamRef::kWeight && r.lin->quant)
+    launch_quantize_w8(st, r.lin->w.p, r.lin->N, r.lin->K, r.lin->q.p,
+                       r.lin->s.p);
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Model::get_param(int idx, float *host) const {
+  hipStream_t st = ctx->stream;
+  ParamRef r = param_ref(const_cast<Model &>(*this), idx);
+  const size_t n = (size_t)r.K * r.N;
+  if (r.kind == ParamRef::kEmb || r.kind == ParamRef::kVec) {
+    const float *src = r.kind == ParamRef::kEmb ? emb.p : r.vec->p;
+    NNHIP_CHECK(hipMemcpyAsync(host, src, n * 4, hipMemcpyDeviceToHost, st));
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    return;
+  }
+  DevBuf<float> stage(n);
+  if (r.kind == ParamRef::kWeight)
+    launch_transpose_out(st, r.lin->w.p, r.K, r.N, r.row_base, r.row_stride,
+                         stage.p);
+  else
+    launch_transpose_out(st, r.lin->b.p, 1, r.N, r.row_base, r.row_stride,
+                         stage.p);
+  NNHIP_CHECK(hipMemcpyAsync(host, stage.p, n * 4, hipMemcpyDeviceToHost, st));
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+// Seeded weights: Dense weights and the embedding N(0, std) (element (k, n)
+// of parameter idx is a function of (seed, idx, k*N + n) only), biases 0,
+// LayerNorm gamma 1 and beta 0 (layer.cpp:157-159, 203-209).
+void Model::init_normal(uint64_t seed, float stdv) {
+  hipStream_t st = ctx->stream;
+  for (int idx = 0; idx < num_params(); ++idx) {
+    ParamRef r = param_ref(*this, idx);
+    switch (r.kind) {
+      case ParamRef::kEmb:
+        launch_init_normal(st, emb.p, r.K, r.N, 0, 1, seed, idx, stdv, 0);
+        break;
+      case ParamRef::kWeight:
+        launch_init_normal(st, r.lin->w.p, r.K, r.N, r.row_base, r.row_stride,
+                           seed, idx, stdv, 1);
+        break;
+      case ParamRef::kBias:
+        launch_fill(st, r.lin->b.p, r.lin->N, 0.0f);
+        break;
+      case ParamRef::kVec: {
+        const int j = (idx - 1) % 18;
+        launch_fill(st, r.vec->p, r.N, (j == 14 || j == 16) ? 1.0f : 0.0f);
+        break;
+      }
+    }
+  }
+  if (quantized) quantize();
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+// quantize_model / MultiHeadAttention::quantize extended to the whole
+// decoder: every Dense (q, k, v, o, gate, up, down, lm_head) becomes a
+// symmetric per-output-channel int8 QuantizedDense (quantization.cpp:7-87);
+// the embedding stays fp32.
+void Model::quantize() {
+  hipStream_t st = ctx->stream;
+  auto q = [&](Linear &ln) {
+    if (!ln.q.p) ln.q.alloc((size_t)ln.N * ln.K);
+    launch_quantize_w8(st, ln.w.p, ln.N, ln.K, ln.q.p, ln.s.p);
+    ln.quant = true;
+  };
+  for (auto &ly : layers) { q(ly.qkv); q(ly.o); q(ly.gu); q(ly.down); }
+  q(lm);
+  quantized = true;
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Model::get_quantized(int layer, int which, int8_t *codes_kn,
+                          float *scales) const {
+  NNHIP_REQUIRE(quantized, kErrArg, "model is not quantized");
+  const Linear *ln;
+  int64_t base = 0, stride = 1;
+  int K = d, N = d;
+  if (which == 7) { ln = &lm; N = V; }
+  else {
+    NNHIP_REQUIRE(layer >= 0 && layer < L && which >= 0 && which < 7, kErrArg,
+                  "get_quantized: bad layer or index");
+    const LayerW &ly = layers[layer];
+    switch (which) {
+      case 0: case 1: case 2: ln = &ly.qkv; base = (int64_t)which * d; break;
+      case 3: ln = &ly.o; break;
+      case 4: ln = &ly.gu; N = F; base = 0; stride = 2; break;
+      case 5: ln = &ly.gu; N = F; base = 1; stride = 2; break;
+      default: ln = &ly.down; K = F; break;
+    }
+  }
+  std::vector<int8_t> all((size_t)ln->N * ln->K);
+  std::vector<float> sc(ln->N);
+  NNHIP_CHECK(hipMemcpy(all.data(), ln->q.p, all.size(), hipMemcpyDeviceToHost));
+  NNHIP_CHECK(hipMemcpy(sc.data(), ln->s.p, sc.size() * 4, hipMemcpyDeviceToHost));
+  for (int n = 0; n < N; ++n) {
+    const int64_t row = base + (int64_t)n * stride;
+    scales[n] = sc[row];
+    for (int k = 0; k < K; ++k) codes_kn[(int64_t)k * N + n] = all[row * ln->K + k];
+  }
+}
+
+void Model::reserve(int rows, int lrows, int max_keys) {
+  if (rows > ws.rows) {
+    const int r = std::max(rows, 64);
+    ws.rows = r;
+    ws.x.alloc((size_t)r * d); ws.qrot.alloc((size_t)r * d);
+    ws.ctx.alloc((size_t)r * d); ws.h.alloc((size_t)r * d);
+    ws.x1.alloc((size_t)r * d);
+    ws.qkv.alloc((size_t)r * 3 * d);
+    ws.ff.alloc((size_t)r * F);
+    ws.mpad = round_up(r, 64);
+    ws.limbs.alloc((size_t)kLimbs * ws.mpad * std::max(d, F));
+    ws.rexp.alloc(ws.mpad);
+    ws.ids.alloc(r);
+    ws.zeros.alloc(r);
+    NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->stream));
+  }
+  if (lrows > ws.lrows) {
+    ws.lrows = lrows;
+    ws.logits.alloc((size_t)lrows * V);
+  }
+  const int64_t pe = attention_partial_elems(1, rows, H, D, max_keys);
+  if (pe > ws.part_elems) {
+    ws.part.alloc(pe);
+    ws.part_elems = pe;
+  }
+}
+
+bool Model::use_limbs(const Linear &ln, int rows) const {
+  return ln.quant && rows >= kLimbMinRows && ln.K % 128 == 0 &&
+         ln.N % 64 == 0;
+}
+
+void Model::linear(const Linear &ln, const float *x, int64_t ldx, int rows,
+                   bool limbs_ready, const float *resid, int64_t ldr,
+                   float *y, int64_t ldy, int epi) {
+  hipStream_t st = ctx->stream;
+  if (use_limbs(ln, rows)) {
+    if (!limbs_ready)
+      launch_act_quant(st, x, ldx, rows, ln.K, ws.limbs.p, ws.mpad, ws.rexp.p);
+    launch_gemm_limb(st, ws.limbs.p, ws.mpad, ws.rexp.p, rows, ln.K, ln.N,
+                     ln.q.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi);
+  } else {
+    launch_gemv(st, x, ldx, rows, ln.K, ln.N, ln.quant ? ln.q.p : nullptr,
+                ln.quant ? nullptr : ln.w.p, ln.s.p, ln.b.p, resid, ldr, y,
+                ldy, epi);
+  }
+}
+
+void Model::forward(KVCache *cache, const int32_t *ids, int ids_stride, int B,
+                    int S, const int32_t *base, int off,
+                    const int32_t *active, int max_keys, float *logits,
+                    bool last_only) {
+  hipStream_t st = ctx->stream;
+  const int R = B * S;
+  std::unique_ptr<KVCache> tmp;
+  KVCache *kv = cache;
+  if (!kv) {
+    tmp.reset(new KVCache(this, B, S));
+    kv = tmp.get();
+    base = nullptr; off = 0; active = nullptr; max_keys = S;
+  }
+  reserve(R, logits ? (last_only ? B : R) : 0, max_keys);
+  const int32_t *bp = base ? base : ws.zeros.p;
+  launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p);
+  bool limbs_ready = false;
+  for (int l = 0; l < L; ++l) {
+    LayerW &ly = layers[l];
+    linear(ly.qkv, ws.x.p, d, R, limbs_ready, nullptr, 0, ws.qkv.p, 3 * d,
+           kEpiBias);
+    float *kc = kv->k.p + (int64_t)l * kv->layer_stride();
+    float *vc = kv->v.p + (int64_t)l * kv->layer_stride();
+    launch_rope_kv(st, ws.qkv.p, B, S, H, D, bp, off, active, cosb.p, sinb.p,
+                   ws.qrot.p, kc, vc, kv->cap, kv->seq_stride());
+    launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
+                     kv->seq_stride(), bp, off, active, max_keys, ws.part.p,
+                     ws.part_elems, ws.ctx.p);
+    linear(ly.o, ws.ctx.p, d, R, false, ws.x.p, d, ws.h.p, d, kEpiResid);
+    const bool l1 = use_limbs(ly.gu, R);
+    launch_layernorm(st, ws.h.p, R, d, ly.g1.p, ly.b1.p, ws.x1.p,
+                     l1 ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+    linear(ly.gu, ws.x1.p, d, R, l1, nullptr, 0, ws.ff.p, F, kEpiSwiGLU);
+    linear(ly.down, ws.ff.p, F, R, false, ws.x1.p, d, ws.h.p, d, kEpiResid);
+    limbs_ready = l + 1 < L && use_limbs(layers[l + 1].qkv, R);
+    launch_layernorm(st, ws.h.p, R, d, ly.g2.p, ly.b2.p, ws.x.p,
+                     limbs_ready ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+  }
+  if (logits) {
+    if (last_only)
+      linear(lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
+             nullptr, 0, logits, V, kEpiBias);
+    else
+      linear(lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
+  }
+  if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+KVCache::KVCache(Model *model, int batch, int capacity)
+    : m(model), B(batch), cap(capacity) {
+  NNHIP_REQUIRE(batch > 0 && capacity > 0, kErrArg, "kvcache: bad size");
+  const size_t n = (size_t)m->L * B * m->H * cap * m->D;
+  k.alloc(n);
+  v.alloc(n);
+  len.alloc(B);
+  host_len.assign(B, 0);
+  sync_len_to_device();
+}
+
+void KVCache::sync_len_to_device() {
+  NNHIP_CHECK(hipMemcpyAsync(len.p, host_len.data(), (size_t)B * 4,
+                             hipMemcpyHostToDevice, m->ctx->stream));
+  NNHIP_CHECK(hipStreamSynchronize(m->ctx->stream));
+}
+
+// ---------------------------------------------------------------------------
+// Speculative decoding for B independent sequences, entirely on the device
+// after the prompt upload: per cycle k draft forwards + k draft samplings,
+// one verify forward of k+1 tokens, one accept kernel and one draft catch-up
+// forward.  The per-sequence state (lengths, counters, candidates) stays in
+// device memory, so the cycle is a fixed kernel sequence that is captured
+// once into a HIP graph and replayed; the host only polls the count of
+// active sequences one cycle behind.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct SpecBuffers {
+  DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok,
+      out, n_active, vids, prompts;
+  DevBuf<float> qprob, dlog, tlog;
+  DevBuf<int64_t> stats;
+};
+
+void check_sampling_options(int V, int top_k, float top_p) {
+  NNHIP_REQUIRE(top_k <= 0 || top_k >= V, kErrUnsupported,
+                "top_k filtering is not implemented on the device path");
+  NNHIP_REQUIRE(top_p <= 0.0f || top_p >= 1.0f, kErrUnsupported,
+                "top_p filtering is not implemented on the device path");
+}
+
+}  // namespace
+
+void generate_speculative_batch(Model &t, Model &dm, int B,
+                                const int32_t *prompts, int P, int max_new,
+                                int k, float T, int top_k, float top_p,
+                                uint64_t seed, uint32_t seq0, int32_t *out,
+                                SpecStats *stats, SpecTiming *timing) {
+  NNHIP_REQUIRE(t.ctx == dm.ctx, kErrArg, "target and draft need one context");
+  NNHIP_REQUIRE(t.V == dm.V, kErrArg, "target and draft vocabularies differ");
+  NNHIP_REQUIRE(B > 0 && P > 0 && k > 0 && max_new >= 0, kErrArg,
+                "generate_speculative: bad sizes");
+  check_sampling_options(t.V, top_k, top_p);
+  // The target cache peaks at P + max_new + k; the draft cache also keeps a
+  // duplicate of every recovered token (layer.cpp:1639-1642 then :1542), up
+  // to one per generated token.
+  const int t_need = P + max_new + k + 1;
+  const int d_need = P + 2 * max_new + k + 2;
+  NNHIP_REQUIRE(t_need <= t.max_seq && d_need <= dm.max_seq, kErrCapacity,
+                "Sequence length S plus past cached length exceeds max_seq_len");
+  Ctx *ctx = t.ctx;
+  hipStream_t st = ctx->stream;
+  const int V = t.V;
+  const int out_stride = P + std::max(max_new, 1);
+
+  KVCache tc(&t, B, t_need), dc(&dm, B, d_need);
+  SpecBuffers bf;
+  bf.cur.alloc(B); bf.cand.alloc((size_t)B * k); bf.tlen.alloc(B);
+  bf.dlen.alloc(B); bf.gen.alloc(B); bf.cyc.alloc(B); bf.active.alloc(B);
+  bf.catchup.alloc(B); bf.catch_tok.alloc(B);
+  bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
+  bf.vids.alloc((size_t)B * (k + 1)); bf.prompts.alloc((size_t)B * P);
+  if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
+  bf.dlog.alloc((size_t)B * V);
+  bf.tlog.alloc((size_t)B * (k + 1) * V);
+  bf.stats.alloc((size_t)B * 6);
+  NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
+  NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 4, st));
+  NNHIP_CHECK(hipMemsetAsync(bf.cand.p, 0, bf.cand.bytes(), st));
+  NNHIP_CHECK(hipMemsetAsync(bf.out.p, 0, bf.out.bytes(), st));
+  NNHIP_CHECK(hipMemcpyAsync(bf.prompts.p, prompts, (size_t)B * P * 4,
+                             hipMemcpyHostToDevice, st));
+  NNHIP_CHECK(hipMemcpy2DAsync(bf.out.p, (size_t)out_stride * 4, prompts,
+                               (size_t)P * 4, (size_t)P * 4, B,
+                               hipMemcpyHostToDevice, st));
+
+  SpecState s{};
+  s.cur = bf.cur.p; s.cand = bf.cand.p; s.qprob = bf.qprob.p;
+  s.tlen = bf.tlen.p; s.dlen = bf.dlen.p; s.gen = bf.gen.p; s.cyc = bf.cyc.p;
+  s.active = bf.active.p; s.catchup = bf.catchup.p;
+  s.catch_tok = bf.catch_tok.p; s.out = bf.out.p; s.n_active = bf.n_active.p;
+  s.stats = bf.stats.p;
+  s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new; s.k = k;
+  s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;
+
+  // workspace for every shape the loop uses, before any graph capture
+  t.reserve(B * P, B * (k + 1), t_need);
+  t.reserve(B * (k + 1), B * (k + 1), t_need);
+  dm.reserve(B * P, B, d_need);
+
+  hipEvent_t e0, e1, e2;
+  NNHIP_CHECK(hipEventCreate(&e0));
+  NNHIP_CHECK(hipEventCreate(&e1));
+  NNHIP_CHECK(hipEventCreate(&e2));
+  NNHIP_CHECK(hipEventRecord(e0, st));
+  // prefill (layer.cpp:1400-1408); the draft's prefill logits are unused
+  t.forward(&tc, bf.prompts.p, P, B, P, nullptr, 0, nullptr, P, bf.dlog.p, true);
+  launch_first_token(st, s, bf.dlog.p, V);
+  dm.forward(&dc, bf.prompts.p, P, B, P, nullptr, 0, nullptr, P, nullptr, true);
+  NNHIP_CHECK(hipEventRecord(e1, st));
+
+  auto cycle = [&]() {
+    for (int j = 0; j < k; ++j) {
+      const int32_t *ids = j == 0 ? bf.cur.p : bf.cand.p + (j - 1);
+      dm.forward(&dc, ids, j == 0 ? 1 : k, B, 1, bf.dlen.p, j, bf.active.p,
+                 d_need, bf.dlog.p, false);
+      launch_draft_sample(st, s, j, bf.dlog.p, V);
+    }
+    launch_build_verify_ids(st, bf.cur.p, bf.cand.p, B, k, bf.vids.p);
+    t.forward(&tc, bf.vids.p, k + 1, B, k + 1, bf.tlen.p, 0, bf.active.p,
+              t_need, bf.tlog.p, false);
+    launch_accept(st, s, bf.tlog.p);
+    dm.forward(&dc, bf.catch_tok.p, 1, B, 1, bf.dlen.p, -1, bf.catchup.p,
+               d_need, nullptr, false);
+  };
+
+  int32_t *h_nact = nullptr;
+  NNHIP_CHECK(hipHostMalloc((void **)&h_nact, 2 * sizeof(int32_t)));
+  hipEvent_t ev[2];
+  NNHIP_CHECK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
+  NNHIP_CHECK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int64_t launched = 0;
+  try {
+    if (max_new > 1) {
+      if (ctx->use_graphs) {
+        NNHIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        try {
+          cycle();
+        } catch (...) {
+          hipGraph_t g2;
+          (void)hipStreamEndCapture(st, &g2);
+          if (g2) (void)hipGraphDestroy(g2);
+          throw;
+        }
+        NNHIP_CHECK(hipStreamEndCapture(st, &graph));
+        NNHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+      }
+      // each cycle commits at least one token per active sequence
+      const int max_cycles = max_new - 1;
+      for (int c = 0; c < max_cycles; ++c) {
+        if (exec) NNHIP_CHECK(hipGraphLaunch(exec, st));
+        else cycle();
+        ++launched;
+        NNHIP_CHECK(hipMemcpyAsync(&h_nact[c & 1], bf.n_active.p, 4,
+                                   hipMemcpyDeviceToHost, st));
+        NNHIP_CHECK(hipEventRecord(ev[c & 1], st));
+        if (c >= 1) {
+          NNHIP_CHECK(hipEventSynchronize(ev[(c - 1) & 1]));
+          if (h_nact[(c - 1) & 1] == 0) break;
+        }
+      }
+    }
+    NNHIP_CHECK(hipEventRecord(e2, st));
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  } catch (...) {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipHostFree(h_nact);
+    (void)hipEventDestroy(ev[0]); (void)hipEventDestroy(ev[1]);
+    (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); (void)hipEventDestroy(e2);
+    throw;
+  }
+  if (exec) NNHIP_CHECK(hipGraphExecDestroy(exec));
+  if (graph) NNHIP_CHECK(hipGraphDestroy(graph));
+  NNHIP_CHECK(hipHostFree(h_nact));
+  NNHIP_CHECK(hipEventDestroy(ev[0]));
+  NNHIP_CHECK(hipEventDestroy(ev[1]));
+  float ms_pre = 0.f, ms_dec = 0.f;
+  NNHIP_CHECK(hipEventElapsedTime(&ms_pre, e0, e1));
+  NNHIP_CHECK(hipEventElapsedTime(&ms_dec, e1, e2));
+  NNHIP_CHECK(hipEventDestroy(e0));
+  NNHIP_CHECK(hipEventDestroy(e1));
+  NNHIP_CHECK(hipEventDestroy(e2));
+  if (timing) {
+    timing->prefill_ms = ms_pre;
+    timing->decode_ms = ms_dec;
+    timing->cycles_launched = launched;
+  }
+  NNHIP_CHECK(hipMemcpy(out, bf.out.p, bf.out.bytes(), hipMemcpyDeviceToHost));
+  if (stats) {
+    std::vector<int64_t> hs((size_t)B * 6);
+    NNHIP_CHECK(hipMemcpy(hs.data(), bf.stats.p, hs.size() * 8,
+                          hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; ++b) {
+      const int64_t *x = &hs[(size_t)b * 6];
+      stats[b] = SpecStats{x[0], x[1], x[2], x[3], x[4], x[5]};
+    }
+  }
+}
+
+void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
+                             int max_new, float T, int top_k, float top_p,
+                             uint64_t seed, uint32_t seq0, bool use_cache,
+                             int32_t *out) {
+  NNHIP_REQUIRE(B > 0 && P > 0 && max_new >= 0, kErrArg,
+                "generate_advanced: bad sizes");
+  check_sampling_options(m.V, top_k, top_p);
+  hipStream_t st = m.ctx->stream;
+  const int total = P + max_new;
+  if (use_cache)
+    NNHIP_REQUIRE(total <= m.max_seq + 1, kErrCapacity,
+                  "Sequence length S plus past cached length exceeds max_seq_len");
+  DevBuf<int32_t> dout((size_t)B * std::max(total, 1)), cur(B), len(B);
+  DevBuf<float> lg((size_t)B * m.V);
+  NNHIP_CHECK(hipMemcpy(dout.p, prompts, (size_t)B * P * 4, hipMemcpyHostToDevice));
+  // prompts are [B][P]; re-lay them with stride `total`
+  if (total != P) {
+    std::vector<int32_t> h((size_t)B * total, 0);
+    for (int b = 0; b < B; ++b)
+      std::memcpy(&h[(size_t)b * total], prompts + (size_t)b * P, (size_t)P * 4);
+    NNHIP_CHECK(hipMemcpy(dout.p, h.data(), h.size() * 4, hipMemcpyHostToDevice));
+  }
+  NNHIP_CHECK(hipMemset(len.p, 0, (size_t)B * 4));
+  SpecState s{};
+  s.cur = cur.p; s.out = dout.p; s.B = B; s.out_stride = total; s.P = P;
+  s.max_new = max_new; s.k = 0; s.V = m.V; s.T = T; s.seed = seed;
+  s.seq0 = seq0;
+  std::unique_ptr<KVCache> cache;
+  if (use_cache) cache.reset(new KVCache(&m, B, std::max(total, 1)));
+  for (int step = 0; step < max_new; ++step) {
+    const int n = P + step;
+    if (use_cache && step > 0) {
+      m.forward(cache.get(), cur.p, 1, B, 1, len.p, 0, nullptr, n, lg.p, true);
+      launch_add_scalar(st, len.p, B, 1);
+    } else {
+      // the reference keeps the last max_seq_len tokens (layer.cpp:1271-1277)
+      int S = n, start = 0;
+      if (S > m.max_seq) { start = S - m.max_seq; S = m.max_seq; }
+      m.forward(cache.get(), dout.p + start, total, B, S, use_cache ? len.p : nullptr,
+                0, nullptr, S, lg.p, true);
+      if (use_cache) launch_add_scalar(st, len.p, B, S);
+    }
+    launch_ar_sample(st, s, step, lg.p, m.V);
+  }
+  NNHIP_CHECK(hipStreamSynchronize(st));
+  NNHIP_CHECK(hipMemcpy(out, dout.p, (size_t)B * total * 4, hipMemcpyDeviceToHost));
+}
+
+}  // namespace nnhip

@@ -1,0 +1,123 @@
+// Host engine of libnnhip.so: device-resident TransformerDecoder, ragged KV
+// caches, the forward pass and the on-device speculative loop.  Mirrors the
+// reference's TransformerDecoder / KVCache / QuantizedDense objects
+// (include/nn/layer.hpp:212-330, include/nn/quantization.hpp:15-43).
+#pragma once
+
+#include "nnhip_internal.hpp"
+
+#include <memory>
+
+namespace nnhip {
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool use_graphs = true;
+};
+
+// One Dense on the device, weight transposed to [N][K].  Fused layouts:
+// QKV rows [q | k | v]; gate/up interleaved (row 2n = gate n, 2n+1 = up n).
+struct Linear {
+  int K = 0, N = 0;
+  DevBuf<float> w;      // [N][K] fp32 master weight
+  DevBuf<int8_t> q;     // [N][K] int8 codes (after quantize)
+  DevBuf<float> s;      // [N] per-channel scales
+  DevBuf<float> b;      // [N] bias
+  bool quant = false;
+  void init(int k, int n);
+};
+
+struct LayerW {
+  Linear qkv, o, gu, down;
+  DevBuf<float> g1, b1, g2, b2;
+};
+
+struct Workspace {
+  int rows = 0, lrows = 0;
+  DevBuf<float> x, qkv, qrot, ctx, h, x1, ff, logits, part;
+  DevBuf<int8_t> limbs;
+  DevBuf<int> rexp;
+  DevBuf<int32_t> ids, zeros;
+  int mpad = 0;
+  int64_t part_elems = 0;
+};
+
+struct KVCache;
+
+struct Model {
+  Ctx *ctx = nullptr;
+  int V = 0, d = 0, H = 0, D = 0, F = 0, L = 0, max_seq = 0;
+  bool quantized = false;
+  DevBuf<float> emb;  // [V][d]
+  std::vector<LayerW> layers;
+  Linear lm;
+  DevBuf<float> cosb, sinb;  // [max_seq][D/2]
+  Workspace ws;
+
+  Model(Ctx *c, int vocab, int d_model, int heads, int d_ff, int n_layers,
+        int max_seq_len);
+  int num_params() const { return 1 + 18 * L + 2; }
+  void param_shape(int idx, int64_t *rows, int64_t *cols) const;
+  void set_param(int idx, const float *host);
+  void get_param(int idx, float *host) const;
+  void init_normal(uint64_t seed, float stdv);
+  void quantize();
+  void get_quantized(int layer, int which, int8_t *codes_kn,
+                     float *scales) const;
+
+  // Ensures workspace for `rows` rows of which `lrows` need logits.
+  void reserve(int rows, int lrows, int max_keys);
+
+  // TransformerDecoder::forward for B sequences of S new tokens each.
+  // Token of row (b, s): ids[b*ids_stride + s].  Positions start at
+  // base[b] + off (device array; nullptr = 0).  Sequences with
+  // active[b] == 0 neither write nor read the cache.  logits: nullptr (not
+  // needed), or [B*S][V] (all rows) or [B][V] (last_only).
+  void forward(KVCache *cache, const int32_t *ids, int ids_stride, int B,
+               int S, const int32_t *base, int off, const int32_t *active,
+               int max_keys, float *logits, bool last_only);
+
+  void linear(const Linear &ln, const float *x, int64_t ldx, int rows,
+              bool limbs_ready, const float *resid, int64_t ldr, float *y,
+              int64_t ldy, int epi);
+  bool use_limbs(const Linear &ln, int rows) const;
+};
+
+// Ragged KV cache for B sequences: per layer [B][H][cap][D], one length per
+// sequence (KVCache, layer.hpp:212-230, with per-sequence lengths).
+struct KVCache {
+  Model *m = nullptr;
+  int B = 0, cap = 0;
+  DevBuf<float> k, v;
+  DevBuf<int32_t> len;
+  std::vector<int32_t> host_len;
+  KVCache(Model *model, int batch, int capacity);
+  int64_t seq_stride() const { return (int64_t)m->H * cap * m->D; }
+  int64_t layer_stride() const { return (int64_t)B * seq_stride(); }
+  void sync_len_to_device();
+};
+
+struct SpecStats {
+  int64_t cycles, drafted, accepted, ties, resampled, bonus;
+};
+
+struct SpecTiming {
+  double prefill_ms, decode_ms;
+  int64_t cycles_launched;
+};
+
+// generate_speculative (layer.cpp:1382-1661) for B independent sequences.
+void generate_speculative_batch(Model &target, Model &draft, int B,
+                                const int32_t *prompts, int P, int max_new,
+                                int k, float T, int top_k, float top_p,
+                                uint64_t seed, uint32_t seq0, int32_t *out,
+                                SpecStats *stats, SpecTiming *timing);
+
+// generate_advanced (layer.cpp:1240-1380) for B independent sequences.
+void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
+                             int max_new, float T, int top_k, float top_p,
+                             uint64_t seed, uint32_t seq0, bool use_cache,
+                             int32_t *out);
+
+}  // namespace nnhip

@@ -1,0 +1,460 @@
+// W8A32 / fp32 Linear layers for gfx950.
+//
+// Replaces QuantizedDense::forward (quantization.cpp:127-147, dequantise the
+// whole weight then cblas_sgemm) and Dense::forward (layer.cpp:162-171).
+// Weights live on the device transposed to [N][K] (output channel major, K
+// contiguous) so that both kernels stream them with coalesced loads:
+//
+//  * gemv_kernel  -- rows <= 4 per pass (batch-1 draft / verify): fp32 VALU
+//    dot products, int8 codes dequantised in registers, per-channel scale
+//    and bias applied once per output in the epilogue.
+//  * gemm_limb_kernel -- rows >= 16 (batched verify, prefill): the fp32
+//    activations are split exactly into three int8 digits with a per-row
+//    power-of-two scale; each digit is multiplied with the int8 codes on the
+//    MFMA (v_mfma_i32_32x32x32_i8) with exact int32 accumulation, and the
+//    three int32 sums are recombined exactly in int64 before one rounding to
+//    fp32.  Result: an fp32 product whose only error is the 2^-23 (relative
+//    to the row maximum) digit truncation of x and one final rounding.
+#include "nnhip_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace nnhip {
+
+namespace {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // SwiGLU::forward (layer.cpp:1704-1710): (g * sigmoid(g)) * u, with
+  // sigmoid = 1 / (1 + exp(-g)) (cpu_backend.cpp:483-489).
+  float sg = 1.0f / (1.0f + expf(-g));
+  float a = __fmul_rn(g, sg);
+  return __fmul_rn(a, u);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV: y[r][n] = epi( sum_k x[r][k] * w[n][k] ), r < R (<= 4).
+// A workgroup of 4 waves covers NC columns for each of CG = 4/nks column
+// sets; wave (c, s) reduces K-slice s of column set c.  Each lane owns
+// 4-element groups of K at stride 256, keeps its slice of x for all R rows in
+// registers, and loops over the columns 4 at a time.
+// ---------------------------------------------------------------------------
+constexpr int kGemvNC = 8;  // columns per column set
+
+template <int R, bool Q8>
+__global__ __launch_bounds__(256) void gemv_kernel(
+    const float *__restrict__ x, int64_t ldx, int K, int N,
+    const int8_t *__restrict__ wq, const float *__restrict__ wf,
+    const float *__restrict__ scale, const float *__restrict__ bias,
+    const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
+    int64_t ldy, int epi, int nks) {
+  constexpr int kMaxIt = 4;  // slice <= 1024 elements
+  __shared__ float red[4][kGemvNC][R];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int cset = w / nks, slice = w % nks;
+  const int cg = 4 / nks;
+  const int slen = (((K + nks - 1) / nks) + 3) & ~3;
+  const int k0 = slice * slen;
+  const int iters = (slen + 255) / 256;
+  const int64_t ncol0 = (int64_t)blockIdx.x * cg * kGemvNC + cset * kGemvNC;
+
+  float xr[R][kMaxIt][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      int k = k0 + it * 256 + lane * 4;
+      bool ok = it < iters && k < k0 + slen && k < K;
+      float4 v = ok ? *reinterpret_cast<const float4 *>(x + r * ldx + k)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      xr[r][it][0] = v.x; xr[r][it][1] = v.y;
+      xr[r][it][2] = v.z; xr[r][it][3] = v.w;
+    }
+
+  for (int c0 = 0; c0 < kGemvNC; c0 += 4) {
+    float acc[4][R];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[c][r] = 0.f;
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      int k = k0 + it * 256 + lane * 4;
+      if (!(it < iters && k < k0 + slen && k < K)) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        int64_t n = ncol0 + c0 + c;
+        if (n >= N) continue;
+        float wv[4];
+        if (Q8) {
+          int pk = *reinterpret_cast<const int *>(wq + n * K + k);
+          wv[0] = (float)(int8_t)(pk & 0xff);
+          wv[1] = (float)(int8_t)((pk >> 8) & 0xff);
+          wv[2] = (float)(int8_t)((pk >> 16) & 0xff);
+          wv[3] = (float)(int8_t)((pk >> 24) & 0xff);
+        } else {
+          float4 f = *reinterpret_cast<const float4 *>(wf + n * K + k);
+          wv[0] = f.x; wv[1] = f.y; wv[2] = f.z; wv[3] = f.w;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[c][r] += xr[r][it][e] * wv[e];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float t = wave_sum(acc[c][r]);
+        if (lane == 0) red[w][c0 + c][r] = t;
+      }
+  }
+  __syncthreads();
+  // combine the nks slices and apply the epilogue
+  for (int t = threadIdx.x; t < cg * kGemvNC * R; t += blockDim.x) {
+    int r = t % R;
+    int cc = (t / R) % kGemvNC;
+    int cs = t / (R * kGemvNC);
+    int64_t n = (int64_t)blockIdx.x * cg * kGemvNC + cs * kGemvNC + cc;
+    if (n >= N) continue;
+    float a = 0.f;
+    for (int s = 0; s < nks; ++s) a += red[cs * nks + s][cc][r];
+    float v = Q8 ? a * scale[n] : a;
+    v = v + bias[n];
+    if (epi == kEpiSwiGLU) {
+      if (n & 1) continue;
+      float a1 = 0.f;
+      for (int s = 0; s < nks; ++s) a1 += red[cs * nks + s][cc + 1][r];
+      float u = (Q8 ? a1 * scale[n + 1] : a1) + bias[n + 1];
+      y[r * ldy + n / 2] = silu_mul(v, u);
+    } else if (epi == kEpiResid) {
+      y[r * ldy + n] = resid[r * ldr + n] + v;
+    } else {
+      y[r * ldy + n] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Activation digits for the MFMA GEMM.  Row m: e = 22 - exponent(max|x|), so
+// |x * 2^e| < 2^22; X = rint(x * 2^e) (exact scaling, ties to even) is split
+// into balanced base-256 digits hi, mid, lo in [-128, 127].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void act_quant_kernel(
+    const float *__restrict__ x, int64_t ldx, int K, int8_t *__restrict__ limbs,
+    int mpad, int *__restrict__ rexp) {
+  __shared__ float smax[4];
+  const int m = blockIdx.x;
+  const float *xr = x + m * ldx;
+  float mx = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(xr[k]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  int e = 0;
+  if (mx > 0.f) {
+    int ex;
+    (void)frexpf(mx, &ex);
+    e = kLimbBits - ex;
+  }
+  if (threadIdx.x == 0) rexp[m] = e;
+  int8_t *l0 = limbs + (int64_t)m * K;
+  int8_t *l1 = limbs + ((int64_t)mpad + m) * K;
+  int8_t *l2 = limbs + ((int64_t)2 * mpad + m) * K;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    int X = (int)rintf(ldexpf(xr[k], e));
+    int lo = (int)(int8_t)(X & 0xff);
+    int t = (X - lo) >> 8;
+    int mid = (int)(int8_t)(t & 0xff);
+    int hi = (t - mid) >> 8;
+    l0[k] = (int8_t)hi;
+    l1[k] = (int8_t)mid;
+    l2[k] = (int8_t)lo;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA GEMM over the activation digits.  Workgroup tile 64 x 64, four
+// waves of 32 x 32, three int32 accumulators (one per digit) per wave.
+// Within each 128-wide K chunk, lane (r, h) supplies bytes
+// [h*64 + s*16, h*64 + s*16 + 16) of its row for MFMA step s, identically for
+// the digit operand and the weight operand, so each MFMA contracts matching
+// k indices whatever order the hardware assigns to a lane's 16 bytes.
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void gemm_limb_kernel(
+    const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
+    int M, int K, int N, const int8_t *__restrict__ wq,
+    const float *__restrict__ scale, const float *__restrict__ bias,
+    const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
+    int64_t ldy, int epi) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int m0 = blockIdx.y * 64 + (w >> 1) * 32;
+  const int n0 = blockIdx.x * 64 + (w & 1) * 32;
+
+  v16i acc0 = {}, acc1 = {}, acc2 = {};
+  const int8_t *pb = wq + (int64_t)(n0 + r) * K + h * 64;
+  const int8_t *pa0 = limbs + (int64_t)(m0 + r) * K + h * 64;
+  const int8_t *pa1 = pa0 + (int64_t)mpad * K;
+  const int8_t *pa2 = pa1 + (int64_t)mpad * K;
+  for (int kb = 0; kb < K; kb += 128) {
+    v4i b[4], a0[4], a1[4], a2[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      b[s] = *reinterpret_cast<const v4i *>(pb + kb + s * 16);
+      a0[s] = *reinterpret_cast<const v4i *>(pa0 + kb + s * 16);
+      a1[s] = *reinterpret_cast<const v4i *>(pa1 + kb + s * 16);
+      a2[s] = *reinterpret_cast<const v4i *>(pa2 + kb + s * 16);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[s], b[s], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[s], b[s], acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2[s], b[s], acc2, 0, 0, 0);
+    }
+  }
+  const int n = n0 + r;
+  const float sc = scale[n], bi = bias[n];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int m = m0 + (j >> 2) * 8 + h * 4 + (j & 3);
+    long long tot = (long long)acc0[j] * 65536LL + (long long)acc1[j] * 256LL +
+                    (long long)acc2[j];
+    if (epi == kEpiTotals) {
+      if (m < M) reinterpret_cast<long long *>(y)[(int64_t)m * ldy + n] = tot;
+      continue;
+    }
+    float v = ldexpf((float)tot, -(m < M ? rexp[m] : 0));
+    v = __fadd_rn(__fmul_rn(v, sc), bi);
+    if (epi == kEpiSwiGLU) {
+      float u = __shfl_xor(v, 1, kWave);
+      if (m < M && !(n & 1)) y[(int64_t)m * ldy + n / 2] = silu_mul(v, u);
+    } else if (m < M) {
+      if (epi == kEpiResid) v = resid[(int64_t)m * ldr + n] + v;
+      y[(int64_t)m * ldy + n] = v;
+    }
+  }
+}
+
+// QuantizedDense ctor, INT8 (quantization.cpp:36-66), one output channel per
+// workgroup: s = max|w|/127 (1 if 0), code = clamp(round(w/s), +-127).
+__global__ __launch_bounds__(256) void quantize_w8_kernel(
+    const float *__restrict__ w, int K, int8_t *__restrict__ q,
+    float *__restrict__ scales) {
+  __shared__ float smax[4];
+  const int64_t n = blockIdx.x;
+  const float *wr = w + n * K;
+  float mx = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(wr[k]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+  float s = mx / 127.0f;
+  if (s == 0.0f) s = 1.0f;
+  if (threadIdx.x == 0) scales[n] = s;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    float qf = roundf(wr[k] / s);
+    qf = fmaxf(-127.0f, fminf(127.0f, qf));
+    q[n * K + k] = (int8_t)qf;
+  }
+}
+
+// dst[(row_base + n*row_stride)][k] = src[k][n]  (32x32 tiles through LDS)
+__global__ __launch_bounds__(256) void transpose_into_kernel(
+    const float *__restrict__ src, int K, int N, float *__restrict__ dst,
+    int64_t row_base, int64_t row_stride) {
+  __shared__ float tile[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    int k = k0 + i, n = n0 + tx;
+    tile[i][tx] = (k < K && n < N) ? src[(int64_t)k * N + n] : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    int n = n0 + i, k = k0 + tx;
+    if (k < K && n < N) dst[(row_base + n * row_stride) * K + k] = tile[tx][i];
+  }
+}
+
+__global__ __launch_bounds__(256) void transpose_out_kernel(
+    const float *__restrict__ src, int K, int N, int64_t row_base,
+    int64_t row_stride, float *__restrict__ dst) {
+  __shared__ float tile[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8) {
+    int n = n0 + i, k = k0 + tx;
+    tile[i][tx] = (k < K && n < N) ? src[(row_base + n * row_stride) * K + k] : 0.f;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    int k = k0 + i, n = n0 + tx;
+    if (k < K && n < N) dst[(int64_t)k * N + n] = tile[tx][i];
+  }
+}
+
+__device__ __forceinline__ void philox10(uint32_t c[4], uint32_t k0,
+                                         uint32_t k1) {
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    uint32_t hi0 = __umulhi(0xD2511F53u, c[0]), lo0 = 0xD2511F53u * c[0];
+    uint32_t hi1 = __umulhi(0xCD9E8D57u, c[2]), lo1 = 0xCD9E8D57u * c[2];
+    uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+    k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+  }
+}
+
+// Seeded N(0, std) for element (k, n) of parameter `param` (logical
+// [K][N] index k*N + n): Philox4x32-10 + Box-Muller.
+__global__ __launch_bounds__(256) void init_normal_kernel(
+    float *__restrict__ dst, int K, int N, int64_t row_base,
+    int64_t row_stride, uint64_t seed, uint32_t param, float stdv,
+    int transposed) {
+  int64_t total = (int64_t)K * N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t c[4] = {(uint32_t)i, (uint32_t)(i >> 32), param, 0x4E4E5744u};
+    philox10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    float u1 = ((float)(c[0] >> 8) + 1.0f) * (1.0f / 16777216.0f);
+    float u2 = (float)(c[1] >> 8) * (1.0f / 16777216.0f);
+    float z = sqrtf(-2.0f * logf(u1)) * cosf(6.2831853071795864f * u2);
+    int64_t k = i / N, n = i % N;
+    int64_t off = transposed ? (row_base + n * row_stride) * K + k : i;
+    dst[off] = z * stdv;
+  }
+}
+
+__global__ void fill_kernel(float *p, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+template <int R>
+void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
+                   const int8_t *wq, const float *wf, const float *scale,
+                   const float *bias, const float *resid, int64_t ldr,
+                   float *y, int64_t ldy, int epi) {
+  int nks = K >= 1024 ? 4 : (K >= 512 ? 2 : 1);
+  int cols = (4 / nks) * kGemvNC;
+  dim3 grid((N + cols - 1) / cols);
+  if (wq)
+    hipLaunchKernelGGL((gemv_kernel<R, true>), grid, dim3(256), 0, st, x, ldx,
+                       K, N, wq, wf, scale, bias, resid, ldr, y, ldy, epi,
+                       nks);
+  else
+    hipLaunchKernelGGL((gemv_kernel<R, false>), grid, dim3(256), 0, st, x,
+                       ldx, K, N, wq, wf, scale, bias, resid, ldr, y, ldy,
+                       epi, nks);
+}
+
+}  // namespace
+
+void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
+                 int N, const int8_t *wq, const float *wf, const float *scale,
+                 const float *bias, const float *resid, int64_t ldr, float *y,
+                 int64_t ldy, int epi) {
+  NNHIP_REQUIRE(K % 4 == 0 && K <= 4096, kErrArg, "gemv: K must be a multiple of 4 and <= 4096");
+  NNHIP_REQUIRE(epi != kEpiSwiGLU || N % 2 == 0, kErrArg, "gemv: SwiGLU needs even N");
+  for (int r0 = 0; r0 < rows; r0 += 4) {
+    int rr = rows - r0 < 4 ? rows - r0 : 4;
+    const float *xp = x + r0 * ldx;
+    const float *rp = resid ? resid + r0 * ldr : nullptr;
+    float *yp = y + r0 * ldy;
+    switch (rr) {
+      case 1: gemv_dispatch<1>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
+      case 2: gemv_dispatch<2>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
+      case 3: gemv_dispatch<3>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
+      default: gemv_dispatch<4>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
+    }
+  }
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
+                      int K, int8_t *limbs, int mpad, int *rexp) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(act_quant_kernel, dim3(rows), dim3(256), 0, st, x, ldx, K,
+                     limbs, mpad, rexp);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
+                      const int *rexp, int rows, int K, int N,
+                      const int8_t *wq, const float *scale, const float *bias,
+                      const float *resid, int64_t ldr, float *y, int64_t ldy,
+                      int epi) {
+  NNHIP_REQUIRE(K % 128 == 0 && N % 64 == 0, kErrArg,
+                "gemm_limb: K % 128 and N % 64 must be 0");
+  NNHIP_REQUIRE(mpad % 64 == 0 && rows <= mpad, kErrArg, "gemm_limb: bad mpad");
+  dim3 grid(N / 64, (rows + 63) / 64);
+  hipLaunchKernelGGL(gemm_limb_kernel, grid, dim3(256), 0, st, limbs, mpad,
+                     rexp, rows, K, N, wq, scale, bias, resid, ldr, y, ldy,
+                     epi);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
+                        int8_t *q_nk, float *scales) {
+  hipLaunchKernelGGL(quantize_w8_kernel, dim3(N), dim3(256), 0, st, w_nk, K,
+                     q_nk, scales);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_transpose_into(hipStream_t st, const float *src_kn, int K, int N,
+                           float *dst, int64_t row_base, int64_t row_stride) {
+  dim3 grid((N + 31) / 32, (K + 31) / 32);
+  hipLaunchKernelGGL(transpose_into_kernel, grid, dim3(256), 0, st, src_kn, K,
+                     N, dst, row_base, row_stride);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_transpose_out(hipStream_t st, const float *src, int K, int N,
+                          int64_t row_base, int64_t row_stride, float *dst_kn) {
+  dim3 grid((N + 31) / 32, (K + 31) / 32);
+  hipLaunchKernelGGL(transpose_out_kernel, grid, dim3(256), 0, st, src, K, N,
+                     row_base, row_stride, dst_kn);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_init_normal(hipStream_t st, float *dst, int K, int N,
+                        int64_t row_base, int64_t row_stride, uint64_t seed,
+                        uint32_t param, float stdv, int transposed) {
+  int64_t total = (int64_t)K * N;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(init_normal_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     st, dst, K, N, row_base, row_stride, seed, param, stdv,
+                     transposed);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_fill(hipStream_t st, float *p, int64_t n, float v) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p,
+                     n, v);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+}  // namespace nnhip

@@ -1,0 +1,171 @@
+// Internal declarations shared by the HIP kernels and the host engine of
+// libnnhip.so.  Nothing here is part of the C ABI (include/nnhip.h is).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace nnhip {
+
+// ---------------------------------------------------------------------------
+// Errors: every failure becomes a std::runtime_error carrying the message
+// that nnhip_last_error() returns at the C boundary.
+// ---------------------------------------------------------------------------
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+#define NNHIP_CHECK(expr)                                                     \
+  do {                                                                        \
+    hipError_t e_ = (expr);                                                   \
+    if (e_ != hipSuccess)                                                     \
+      throw ::nnhip::Error(-3, std::string(#expr) + ": " +                    \
+                                   hipGetErrorString(e_));                    \
+  } while (0)
+
+#define NNHIP_REQUIRE(cond, code, msg)                                        \
+  do {                                                                        \
+    if (!(cond)) throw ::nnhip::Error((code), (msg));                         \
+  } while (0)
+
+// Status codes of the C ABI.
+enum : int {
+  kOk = 0,
+  kErrArg = -1,        // bad argument / shape
+  kErrCapacity = -2,   // sequence would exceed max_seq_len
+  kErrHip = -3,        // HIP runtime failure
+  kErrUnsupported = -4 // option the device path does not implement
+};
+
+// ---------------------------------------------------------------------------
+// Device buffers
+// ---------------------------------------------------------------------------
+template <typename T>
+struct DevBuf {
+  T *p = nullptr;
+  size_t n = 0;
+  DevBuf() = default;
+  explicit DevBuf(size_t count) { alloc(count); }
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  DevBuf(DevBuf &&o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+  DevBuf &operator=(DevBuf &&o) noexcept {
+    if (this != &o) { release(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+    return *this;
+  }
+  ~DevBuf() { release(); }
+  void alloc(size_t count) {
+    release();
+    if (count) NNHIP_CHECK(hipMalloc(&p, count * sizeof(T)));
+    n = count;
+  }
+  void ensure(size_t count) { if (count > n) alloc(count); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr; n = 0;
+  }
+  size_t bytes() const { return n * sizeof(T); }
+};
+
+// ---------------------------------------------------------------------------
+// Kernel launch wrappers (defined in the .hip files).
+// ---------------------------------------------------------------------------
+enum Epi : int {
+  kEpiBias = 0,    // y = acc*s + b
+  kEpiResid = 1,   // y = resid + (acc*s + b)
+  kEpiSwiGLU = 2,  // columns (2n, 2n+1) = (gate n, up n): y[n] = silu(g)*u
+  kEpiTotals = 3   // limb GEMM only: write the exact int64 dot totals
+};
+
+// Activation limbs for the int8 MFMA GEMM: x[m][k] ~= X[m][k] * 2^-e[m] with
+// X = hi*65536 + mid*256 + lo, each digit an int8.
+static constexpr int kLimbs = 3;
+static constexpr int kLimbBits = 22;  // |X| < 2^22
+
+// linear.hip
+void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
+                 int N, const int8_t *wq, const float *wf, const float *scale,
+                 const float *bias, const float *resid, int64_t ldr, float *y,
+                 int64_t ldy, int epi);
+void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
+                      int K, int8_t *limbs, int mpad, int *rexp);
+void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
+                      const int *rexp, int rows, int K, int N,
+                      const int8_t *wq, const float *scale, const float *bias,
+                      const float *resid, int64_t ldr, float *y, int64_t ldy,
+                      int epi);
+void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
+                        int8_t *q_nk, float *scales);
+void launch_transpose_into(hipStream_t st, const float *src_kn, int K, int N,
+                           float *dst, int64_t row_base, int64_t row_stride);
+void launch_transpose_out(hipStream_t st, const float *src, int K, int N,
+                          int64_t row_base, int64_t row_stride, float *dst_kn);
+void launch_init_normal(hipStream_t st, float *dst, int K, int N,
+                        int64_t row_base, int64_t row_stride, uint64_t seed,
+                        uint32_t param, float stdv, int transposed);
+void launch_fill(hipStream_t st, float *p, int64_t n, float v);
+
+// attention.hip
+void launch_embed(hipStream_t st, const float *emb, int vocab, int d,
+                  const int32_t *ids, int rows, float *x);
+void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
+                          const int32_t *ids, int B, int S, int stride_b,
+                          float *x);
+void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
+                             const int32_t *cand, int B, int k, int32_t *ids);
+void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
+                    int D, const int32_t *base, int off, const int32_t *active,
+                    const float *cosb, const float *sinb, float *qrot,
+                    float *kc, float *vc, int cap, int64_t seq_stride);
+void launch_attention(hipStream_t st, const float *q, const float *kc,
+                      const float *vc, int B, int S, int H, int Hkv, int D,
+                      int cap, int64_t seq_stride, const int32_t *base,
+                      int off, const int32_t *active, int max_keys,
+                      float *part, int64_t part_elems, float *out);
+int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys);
+void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
+                      const float *g, const float *b, float *y,
+                      int8_t *limbs, int mpad, int *rexp);
+
+// sampling.hip
+struct SpecState {
+  int32_t *cur;        // [B] last committed token (generated.back())
+  int32_t *cand;       // [B][k] draft candidates of this cycle
+  float *qprob;        // [B][k][V] draft probabilities (sampled mode)
+  int32_t *tlen;       // [B] target cache length
+  int32_t *dlen;       // [B] draft cache length
+  int32_t *gen;        // [B] tokens generated so far
+  int32_t *cyc;        // [B] cycle counter (1-based) for the uniform stream
+  int32_t *active;     // [B] 1 while gen < max_new
+  int32_t *catchup;    // [B] 1 when the draft needs a catch-up forward
+  int32_t *catch_tok;  // [B] token of that catch-up forward
+  int32_t *out;        // [B][out_stride] prompt + generated ids
+  int32_t *n_active;   // [1]
+  int64_t *stats;      // [B][6] cycles, drafted, accepted, ties, resampled,
+                       //        bonus
+  int B, out_stride, P, max_new, k, V;
+  float T;
+  uint64_t seed;
+  uint32_t seq0;       // global index of sequence 0 (Philox key part)
+};
+void launch_first_token(hipStream_t st, const SpecState &s,
+                        const float *logits, int64_t ldl);
+void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
+                         const float *logits, int64_t ldl);
+void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits);
+void launch_ar_sample(hipStream_t st, const SpecState &s, int step,
+                      const float *logits, int64_t ldl);
+void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
+                        float T, const float *u, int32_t *tok, float *probs);
+void launch_add_scalar(hipStream_t st, int32_t *p, int n, int v);
+void launch_accept_bench(hipStream_t st, const float *tlog, const float *dlog,
+                         const int32_t *dtok, const float *u_acc,
+                         const float *u_res, int B, int k, int V, float T,
+                         int32_t *n_acc, int32_t *next_tok);
+
+}  // namespace nnhip

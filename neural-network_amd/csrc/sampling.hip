@@ -1,0 +1,506 @@
+// Softmax, sampling and the speculative accept / reject step for gfx950.
+//
+// Replaces the host side of generate_speculative (layer.cpp:1410-1655):
+// get_probs (:1410-1491), sample_token (:1493-1498), the accept loop
+// (:1581-1609), the residual resample (:1611-1630), the bonus sample
+// (:1643-1647) and the cache rollback (:1632-1637).  One workgroup of 1024
+// threads owns one sequence; a vocabulary row of probabilities is held in
+// LDS (up to 32768 entries, 132 KB), so every pass after the first read of
+// the logits is on-chip.  No host round trip happens per token.
+//
+// Uniforms: Philox4x32-10 keyed by the seed, counter {slot, cycle, seq, 0},
+// u = (word0 >> 8) * 2^-24 -- the stream the oracle uses.
+#include "nnhip_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace nnhip {
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxV = 32768;
+// Probability rows live in LDS at a padded address (one spare word every 32)
+// so that both the strided passes (v = tid + 1024 i) and the per-thread
+// contiguous chunks of the inverse CDF are free of bank conflicts.
+constexpr int kRowWords = kMaxV + kMaxV / 32;
+
+__device__ __forceinline__ int la(int v) { return v + (v >> 5); }
+
+__device__ __forceinline__ float uniform(uint64_t seed, uint32_t seq,
+                                         uint32_t cycle, uint32_t slot) {
+  uint32_t c0 = slot, c1 = cycle, c2 = seq, c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+    uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+    k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+  }
+  return (float)(c0 >> 8) * (1.0f / 16777216.0f);
+}
+
+struct Shared {
+  float f[kWaves];
+  double d[kWaves];
+  int i[kWaves];
+  float prow[kRowWords];
+};
+
+__device__ __forceinline__ float block_max(float v, Shared &sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.f[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh.f[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = fmaxf(r, sh.f[w]);
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, Shared &sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.f[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) r += sh.f[w];
+  return r;
+}
+
+__device__ __forceinline__ double block_sum_d(double v, Shared &sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.d[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) r += sh.d[w];
+  return r;
+}
+
+// exclusive prefix sum over threads in index order
+__device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  double incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    double t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  __syncthreads();
+  if (lane == 63) sh.d[w] = incl;
+  __syncthreads();
+  double pre = 0.0;
+  for (int i = 0; i < w; ++i) pre += sh.d[i];
+  return pre + incl - v;
+}
+
+__device__ __forceinline__ int block_min_i(int v, Shared &sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.i[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = sh.i[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = min(r, sh.i[w]);
+  return r;
+}
+
+// First index of the maximum (layer.cpp:1413-1421, std::max_element).
+__device__ int block_argmax(const float *__restrict__ row, int V, Shared &sh) {
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float x = row[v];
+    if (bi == 0x7fffffff || x > bv) { bv = x; bi = v; }
+  }
+  const float mx = block_max(bi == 0x7fffffff ? -INFINITY : bv, sh);
+  // lowest index holding the maximum (each thread scanned ascending v)
+  int cand = 0x7fffffff;
+  if (bi != 0x7fffffff && bv == mx) cand = bi;
+  if (cand != 0x7fffffff) {
+    for (int v = threadIdx.x; v < bi; v += kThreads)
+      if (row[v] == mx) { cand = v; break; }
+  }
+  const int r = block_min_i(cand, sh);
+  return r == 0x7fffffff ? 0 : r;
+}
+
+struct RowStats { float mx, sum, fs; };
+
+// get_probs (layer.cpp:1426-1489) for T > 0 without top-k / top-p:
+// s = l / T, e = exp(s - max), p1 = e / sum (float sum), p = p1 / final_sum.
+// Writes p into sh.prow and returns the three row constants.
+__device__ RowStats row_probs(const float *__restrict__ row, int V, float T,
+                              Shared &sh) {
+  float mx = -INFINITY;
+  for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float s = row[v] / T;
+    sh.prow[la(v)] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_max(mx, sh);
+  float s = 0.f;
+  for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float e = expf(sh.prow[la(v)] - mx);
+    sh.prow[la(v)] = e;
+    s += e;
+  }
+  const float sum = block_sum(s, sh);
+  float f = 0.f;
+  for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float p1 = sh.prow[la(v)] / sum;
+    sh.prow[la(v)] = p1;
+    f += p1;
+  }
+  const float fs = block_sum(f, sh);
+  for (int v = threadIdx.x; v < V; v += kThreads)
+    sh.prow[la(v)] = sh.prow[la(v)] / fs;
+  __syncthreads();
+  return RowStats{mx, sum, fs};
+}
+
+// Same statistics without materialising the row.
+__device__ RowStats row_stats(const float *__restrict__ row, int V, float T,
+                              Shared &sh) {
+  float mx = -INFINITY;
+  for (int v = threadIdx.x; v < V; v += kThreads) mx = fmaxf(mx, row[v] / T);
+  mx = block_max(mx, sh);
+  float s = 0.f;
+  for (int v = threadIdx.x; v < V; v += kThreads) s += expf(row[v] / T - mx);
+  const float sum = block_sum(s, sh);
+  float f = 0.f;
+  for (int v = threadIdx.x; v < V; v += kThreads)
+    f += expf(row[v] / T - mx) / sum;
+  const float fs = block_sum(f, sh);
+  return RowStats{mx, sum, fs};
+}
+
+__device__ __forceinline__ float prob_at(const float *row, int v, float T,
+                                         RowStats st) {
+  return (expf(row[v] / T - st.mx) / st.sum) / st.fs;
+}
+
+// sample_token (layer.cpp:1493-1498): std::discrete_distribution over
+// sh.prow widened to double -- normalise by the double sum, running sum,
+// last entry 1.0, first v with cdf[v] >= u.
+__device__ int block_sample(int V, float u, Shared &sh) {
+  const int C = (V + kThreads - 1) / kThreads;
+  const int b0 = threadIdx.x * C;
+  const int b1 = min(b0 + C, V);
+  double loc = 0.0;
+  for (int v = b0; v < b1; ++v) loc += (double)sh.prow[la(v)];
+  const double S = block_sum_d(loc, sh);
+  double part = 0.0;
+  for (int v = b0; v < b1; ++v) part += (double)sh.prow[la(v)] / S;
+  double c = block_excl_scan_d(part, sh);
+  int found = 0x7fffffff;
+  const double ud = (double)u;
+  for (int v = b0; v < b1 && v < V - 1; ++v) {
+    c += (double)sh.prow[la(v)] / S;
+    if (c >= ud) { found = v; break; }
+  }
+  const int r = block_min_i(found, sh);
+  return r == 0x7fffffff ? V - 1 : r;
+}
+
+__device__ int draw_row(const float *row, int V, float T, float u,
+                        Shared &sh) {
+  if (T <= 0.f) return block_argmax(row, V, sh);
+  row_probs(row, V, T, sh);
+  return block_sample(V, u, sh);
+}
+
+// ---------------------------------------------------------------------------
+// First token after the prefill (layer.cpp:1500-1510): cycle 0, slot 2k.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void first_token_kernel(
+    SpecState s, const float *__restrict__ logits, int64_t ldl) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  const float u = uniform(s.seed, s.seq0 + b, 0, 2 * s.k);
+  const int tok = draw_row(logits + b * ldl, s.V, s.T, u, sh);
+  if (threadIdx.x == 0) {
+    s.out[(int64_t)b * s.out_stride + s.P] = tok;
+    s.cur[b] = tok;
+    s.gen[b] = 1;
+    s.cyc[b] = 1;
+    s.tlen[b] = s.P;
+    s.dlen[b] = s.P;
+    s.catchup[b] = 0;
+    const int act = s.max_new > 1 ? 1 : 0;
+    s.active[b] = act;
+    if (act) atomicAdd(s.n_active, 1);
+  }
+}
+
+// One drafting step j (layer.cpp:1541-1558): q_j = get_probs(draft logits),
+// candidate = sample_token(q_j) with u[seq][cycle][j].
+__global__ __launch_bounds__(kThreads) void draft_sample_kernel(
+    SpecState s, int j, const float *__restrict__ logits, int64_t ldl) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  if (!s.active[b]) return;
+  const float *row = logits + b * ldl;
+  int tok;
+  if (s.T <= 0.f) {
+    tok = block_argmax(row, s.V, sh);
+  } else {
+    row_probs(row, s.V, s.T, sh);
+    float *qd = s.qprob + ((int64_t)b * s.k + j) * s.V;
+    for (int v = threadIdx.x; v < s.V; v += kThreads) qd[v] = sh.prow[la(v)];
+    tok = block_sample(s.V, uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+  }
+  if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
+}
+
+// Residual max(0, p - q) (layer.cpp:1611-1630) over sh.prow = p, q from
+// qrow (stored) or recomputed from draft logits; then sample it, or p when
+// the residual sums to zero (p is recomputed from tlog_row then).
+__device__ int residual_sample(const float *__restrict__ qrow,
+                               const float *__restrict__ dlog_row,
+                               RowStats qst, const float *__restrict__ tlog_row,
+                               int V, float T, float u, Shared &sh) {
+  float loc = 0.f;
+  for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float q = qrow ? qrow[v] : prob_at(dlog_row, v, T, qst);
+    const float r = fmaxf(0.0f, sh.prow[la(v)] - q);
+    sh.prow[la(v)] = r;
+    loc += r;
+  }
+  const float sr = block_sum(loc, sh);
+  if (sr <= 0.0f) {
+    row_probs(tlog_row, V, T, sh);
+  } else {
+    for (int v = threadIdx.x; v < V; v += kThreads)
+      sh.prow[la(v)] = sh.prow[la(v)] / sr;
+    __syncthreads();
+  }
+  return block_sample(V, u, sh);
+}
+
+// Accept / reject, resample or bonus, rollback (layer.cpp:1581-1655).
+// tlogits: [B][k+1][V], row i = verify position i.
+__global__ __launch_bounds__(kThreads) void accept_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  if (!s.active[b]) return;
+  const int V = s.V, k = s.k;
+  const bool greedy = s.T <= 0.f;
+  const int gen0 = s.gen[b];
+  const int M = min(k, s.max_new - gen0);
+  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const int tstart = s.tlen[b], dstart = s.dlen[b];
+  int32_t *out = s.out + (int64_t)b * s.out_stride;
+  int nout = s.P + gen0;
+  int rej = -1;
+  int64_t ties = 0;
+  for (int j = 0; j < M; ++j) {
+    const float *row = tlogits + ((int64_t)b * (k + 1) + j) * V;
+    const int c = s.cand[b * k + j];
+    bool acc;
+    if (greedy) {
+      acc = c == block_argmax(row, V, sh);
+    } else {
+      row_probs(row, V, s.T, sh);
+      const float pc = sh.prow[la(c)];
+      const float qc = s.qprob[((int64_t)b * k + j) * V + c];
+      const float r = uniform(s.seed, seq, cyc, k + j);
+      acc = __fmul_rn(r, qc) < pc;
+      if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
+    }
+    if (!acc) { rej = j; break; }
+    if (threadIdx.x == 0) out[nout] = c;
+    ++nout;
+  }
+  int gen = gen0 + (rej < 0 ? M : rej);
+  int tok = -1, catch_tok = -1;
+  const float u = uniform(s.seed, seq, cyc, 2 * k);
+  if (rej >= 0) {
+    const float *row = tlogits + ((int64_t)b * (k + 1) + rej) * V;
+    if (greedy) {
+      tok = block_argmax(row, V, sh);
+    } else {
+      tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, nullptr,
+                            RowStats{0.f, 1.f, 1.f}, row, V, s.T, u, sh);
+    }
+    catch_tok = tok;
+  } else if (gen < s.max_new) {
+    const float *row = tlogits + ((int64_t)b * (k + 1) + M) * V;
+    tok = draw_row(row, V, s.T, u, sh);
+    catch_tok = s.cand[b * k + M - 1];
+  }
+  if (threadIdx.x == 0) {
+    int64_t *st = s.stats + (int64_t)b * 6;
+    st[0] += 1;
+    st[1] += M;
+    st[2] += (rej < 0 ? M : rej);
+    st[3] += ties;
+    if (tok >= 0) {
+      out[nout] = tok;
+      ++gen;
+      s.cur[b] = tok;
+      if (rej >= 0) st[4] += 1; else st[5] += 1;
+    }
+    const int keep = rej >= 0 ? rej : M;
+    s.tlen[b] = tstart + keep + 1;
+    // The draft cache keeps [generated.back(), c_0 .. c_{rej-1}] after a
+    // rejection (layer.cpp:1636) or [generated.back(), c_0 .. c_{M-2}] after
+    // full acceptance, then takes the catch-up token (layer.cpp:1639-1653);
+    // dlen is the length after that catch-up, which writes at dlen - 1.
+    if (tok >= 0) s.dlen[b] = dstart + keep + (rej >= 0 ? 2 : 1);
+    s.catchup[b] = tok >= 0 ? 1 : 0;
+    s.catch_tok[b] = catch_tok;
+    s.gen[b] = gen;
+    s.cyc[b] = (int)cyc + 1;
+    if (gen >= s.max_new) {
+      s.active[b] = 0;
+      s.catchup[b] = 0;
+      atomicSub(s.n_active, 1);
+    }
+  }
+}
+
+// generate_advanced sampling step (layer.cpp:1294-1373): u[seq][step][0].
+__global__ __launch_bounds__(kThreads) void ar_sample_kernel(
+    SpecState s, int step, const float *__restrict__ logits, int64_t ldl) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  const float u = uniform(s.seed, s.seq0 + b, (uint32_t)step, 0);
+  const int tok = draw_row(logits + b * ldl, s.V, s.T, u, sh);
+  if (threadIdx.x == 0) {
+    s.out[(int64_t)b * s.out_stride + s.P + step] = tok;
+    s.cur[b] = tok;
+  }
+}
+
+// Acceptance microbenchmark: k target rows and k draft rows of logits per
+// sequence, draft ids, one accept uniform per position and one resample
+// uniform per sequence.  Rows are read only up to the first rejection.
+// next_tok = residual resample, or -1 when all k drafts are accepted (no
+// target row k is given for a bonus sample).
+__global__ __launch_bounds__(kThreads) void accept_bench_kernel(
+    const float *__restrict__ tlog, const float *__restrict__ dlog,
+    const int32_t *__restrict__ dtok, const float *__restrict__ u_acc,
+    const float *__restrict__ u_res, int k, int V, float T,
+    int32_t *__restrict__ n_acc, int32_t *__restrict__ next_tok) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  int rej = -1;
+  RowStats qst{0.f, 1.f, 1.f};
+  for (int j = 0; j < k; ++j) {
+    const float *tr = tlog + ((int64_t)b * k + j) * V;
+    const float *dr = dlog + ((int64_t)b * k + j) * V;
+    const int c = dtok[b * k + j];
+    bool acc;
+    if (T <= 0.f) {
+      acc = c == block_argmax(tr, V, sh);
+    } else {
+      qst = row_stats(dr, V, T, sh);
+      row_probs(tr, V, T, sh);
+      const float pc = sh.prow[la(c)];
+      const float qc = prob_at(dr, c, T, qst);
+      acc = __fmul_rn(u_acc[b * k + j], qc) < pc;
+    }
+    if (!acc) { rej = j; break; }
+  }
+  int tok = -1;
+  if (rej >= 0) {
+    const float *tr = tlog + ((int64_t)b * k + rej) * V;
+    if (T <= 0.f)
+      tok = block_argmax(tr, V, sh);
+    else
+      tok = residual_sample(nullptr, dlog + ((int64_t)b * k + rej) * V, qst,
+                            tr, V, T, u_res[b], sh);
+  }
+  if (threadIdx.x == 0) {
+    n_acc[b] = rej < 0 ? k : rej;
+    next_tok[b] = tok;
+  }
+}
+
+// get_probs + sample_token on independent rows with explicit uniforms.
+__global__ __launch_bounds__(kThreads) void sample_rows_kernel(
+    const float *__restrict__ logits, int V, float T,
+    const float *__restrict__ u, int32_t *__restrict__ tok,
+    float *__restrict__ probs) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  const float *row = logits + (int64_t)b * V;
+  int t;
+  if (T <= 0.f) {
+    t = block_argmax(row, V, sh);
+  } else {
+    row_probs(row, V, T, sh);
+    if (probs)
+      for (int v = threadIdx.x; v < V; v += kThreads)
+        probs[(int64_t)b * V + v] = sh.prow[la(v)];
+    t = block_sample(V, u[b], sh);
+  }
+  if (threadIdx.x == 0) tok[b] = t;
+}
+
+}  // namespace
+
+void launch_first_token(hipStream_t st, const SpecState &s,
+                        const float *logits, int64_t ldl) {
+  NNHIP_REQUIRE(s.V <= kMaxV, kErrUnsupported,
+                "sampling: vocabulary above 32768");
+  hipLaunchKernelGGL(first_token_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                     logits, ldl);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
+                         const float *logits, int64_t ldl) {
+  hipLaunchKernelGGL(draft_sample_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                     j, logits, ldl);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
+  hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                     tlogits);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_ar_sample(hipStream_t st, const SpecState &s, int step,
+                      const float *logits, int64_t ldl) {
+  NNHIP_REQUIRE(s.V <= kMaxV, kErrUnsupported,
+                "sampling: vocabulary above 32768");
+  hipLaunchKernelGGL(ar_sample_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                     step, logits, ldl);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
+                        float T, const float *u, int32_t *tok, float *probs) {
+  NNHIP_REQUIRE(V <= kMaxV, kErrUnsupported,
+                "sampling: vocabulary above 32768");
+  hipLaunchKernelGGL(sample_rows_kernel, dim3(B), dim3(kThreads), 0, st,
+                     logits, V, T, u, tok, probs);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_accept_bench(hipStream_t st, const float *tlog, const float *dlog,
+                         const int32_t *dtok, const float *u_acc,
+                         const float *u_res, int B, int k, int V, float T,
+                         int32_t *n_acc, int32_t *next_tok) {
+  NNHIP_REQUIRE(V <= kMaxV, kErrUnsupported,
+                "sampling: vocabulary above 32768");
+  hipLaunchKernelGGL(accept_bench_kernel, dim3(B), dim3(kThreads), 0, st, tlog,
+                     dlog, dtok, u_acc, u_res, k, V, T, n_acc, next_tok);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+}  // namespace nnhip

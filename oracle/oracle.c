@@ -8,9 +8,11 @@
  * get_probs / sample_token, the accept / residual / bonus logic and cache
  * rollback of generate_speculative, and generate_advanced.
  */
+#define _POSIX_C_SOURCE 199309L
 #include "oracle.h"
 
 #include <math.h>
+#include <time.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -558,6 +560,58 @@ static int draw(const float *probs, int V, int greedy, uint64_t seed,
   return or_sample(probs, V, (double)or_uniform(seed, seq, cycle, slot));
 }
 
+/* The accept loop and its ending (layer.cpp:1581-1630, 1643-1647) over
+ * probability rows p [M (+1)][V] (target) and q [M][V] (draft) for the
+ * candidates cand[M]: accept j while r_j * q_j[c_j] < p_j[c_j] (greedy: c_j
+ * is the first argmax of p_j); at the first rejection r, *tok is drawn with
+ * u_final from max(0, p_r - q_r) normalised by its float sum, or from p_r
+ * when that sum is <= 0; after full acceptance *tok is drawn from p_M when
+ * has_bonus, else -1.  Returns the number of accepted candidates. */
+int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
+                   int V, int greedy, int has_bonus, const float *u_accept,
+                   float u_final, int *tok, int64_t *ties) {
+  *tok = -1;
+  for (int j = 0; j < M; ++j) {
+    int c = cand[j];
+    const float *pj = p + (size_t)j * V, *qj = q + (size_t)j * V;
+    int acc;
+    if (greedy) {
+      acc = c == or_argmax(pj, V);
+    } else {
+      float r = u_accept[j];
+      acc = r * qj[c] < pj[c];
+      if (ties && fabs((double)r - (double)pj[c] / (double)qj[c]) < 1e-6)
+        (*ties)++;
+    }
+    if (acc) continue;
+    if (greedy) { *tok = or_argmax(pj, V); return j; }
+    float *rec = (float *)malloc(sizeof(float) * V);
+    float sr = 0.0f;
+    for (int v = 0; v < V; ++v) {
+      rec[v] = fmaxf(0.0f, pj[v] - qj[v]);
+      sr += rec[v];
+    }
+    if (sr <= 0.0f) *tok = or_sample(pj, V, (double)u_final);
+    else {
+      for (int v = 0; v < V; ++v) rec[v] /= sr;
+      *tok = or_sample(rec, V, (double)u_final);
+    }
+    free(rec);
+    return j;
+  }
+  if (has_bonus) {
+    const float *pm = p + (size_t)M * V;
+    *tok = greedy ? or_argmax(pm, V) : or_sample(pm, V, (double)u_final);
+  }
+  return M;
+}
+
+static double now_ms(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
+}
+
 /* generate_speculative (layer.cpp:1382-1661) for one sequence. */
 int or_generate_speculative(const or_model *t, const or_model *dm,
                             const int32_t *prompt, int P, int max_new, int k,
@@ -577,6 +631,7 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
   int32_t *cand = (int32_t *)malloc(sizeof(int32_t) * (k + 1));
   int rc = 0;
   int n = 0;
+  double t0 = now_ms(), t1 = t0;
   for (int i = 0; i < P; ++i) out[n++] = prompt[i];
   /* prefill (layer.cpp:1400-1408) */
   if (or_forward(t, tc, prompt, P, tl) || or_forward(dm, dc, prompt, P, dl)) {
@@ -586,6 +641,7 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
   out[n++] = draw(p, V, greedy, seed, seq, 0, 2 * k);
   int ngen = 1;
   uint32_t cycle = 0;
+  t1 = now_ms();
   while (ngen < max_new) {
     int M = k < max_new - ngen ? k : max_new - ngen;
     ++cycle;
@@ -604,52 +660,37 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
     if (or_forward(t, tc, tin, M + 1, tl)) { rc = -1; goto done; }
     for (int i = 0; i <= M; ++i)
       or_get_probs(tl + (size_t)i * V, V, T, top_k, top_p, p + (size_t)i * V);
-    /* accept (layer.cpp:1581-1609) */
-    int all = 1, rej = 0;
-    for (int j = 0; j < M; ++j) {
-      int c = cand[j];
-      float qc = q[(size_t)j * V + c], pc = p[(size_t)j * V + c];
-      int acc;
-      if (greedy) {
-        acc = c == or_argmax(p + (size_t)j * V, V);
-      } else {
-        float r = or_uniform(seed, seq, cycle, k + j);
-        acc = r * qc < pc;
-        if (fabs((double)r - (double)pc / (double)qc) < 1e-6) local.ties++;
-      }
-      if (acc) { out[n++] = c; ngen++; local.accepted++; }
-      else { all = 0; rej = j; break; }
-    }
+    /* accept, resample or bonus (layer.cpp:1581-1630, 1643-1647) */
+    float ua[64];
+    for (int j = 0; j < M; ++j) ua[j] = greedy ? 0.0f : or_uniform(seed, seq, cycle, k + j);
+    float uf = greedy ? 0.0f : or_uniform(seed, seq, cycle, 2 * k);
+    int tok = -1;
+    int64_t ties = 0;
+    int acc = or_accept_step(p, q, cand, M, V, greedy, ngen + M < max_new, ua,
+                             uf, &tok, &ties);
+    for (int j = 0; j < acc; ++j) out[n++] = cand[j];
+    ngen += acc;
+    local.accepted += acc;
+    local.ties += ties;
     local.cycles++;
     local.drafted += M;
-    if (!all) {
-      /* residual resample (layer.cpp:1611-1630) */
-      const float *pr = p + (size_t)rej * V, *qr = q + (size_t)rej * V;
-      float sr = 0.0f;
-      for (int v = 0; v < V; ++v) {
-        rec[v] = fmaxf(0.0f, pr[v] - qr[v]);
-        sr += rec[v];
-      }
-      int tok;
-      if (sr <= 0.0f) tok = draw(pr, V, greedy, seed, seq, cycle, 2 * k);
-      else {
-        for (int v = 0; v < V; ++v) rec[v] /= sr;
-        tok = draw(rec, V, greedy, seed, seq, cycle, 2 * k);
-      }
+    if (acc < M) {
+      int rej = acc;
       out[n++] = tok; ngen++; local.resampled++;
       /* rollback (layer.cpp:1632-1637) and draft catch-up (:1639-1642) */
       or_cache_truncate(tc, tstart + rej + 1);
       or_cache_truncate(dc, dstart + rej + 1);
       if (or_forward(dm, dc, &tok, 1, dl)) { rc = -1; goto done; }
-    } else if (ngen < max_new) {
+    } else if (tok >= 0) {
       /* bonus sample and draft catch-up (layer.cpp:1643-1655) */
-      int tok = draw(p + (size_t)M * V, V, greedy, seed, seq, cycle, 2 * k);
       out[n++] = tok; ngen++; local.bonus++;
       int32_t last = cand[M - 1];
       if (or_forward(dm, dc, &last, 1, dl)) { rc = -1; goto done; }
     }
   }
 done:
+  local.prefill_ms = t1 - t0;
+  local.decode_ms = now_ms() - t1;
   if (st) *st = local;
   or_cache_free(tc); or_cache_free(dc);
   free(tl); free(dl); free(q); free(p); free(rec); free(cand);

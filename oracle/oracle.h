@@ -39,6 +39,8 @@ typedef struct {
   int64_t ties;         /* accept tests with |r - p/q| < 1e-6 */
   int64_t resampled;    /* cycles that ended in a residual resample */
   int64_t bonus;        /* cycles that ended in a bonus sample */
+  double prefill_ms;    /* prompt forwards and first token (CLOCK_MONOTONIC) */
+  double decode_ms;     /* the cycle loop */
 } or_spec_stats;
 
 /* Philox4x32-10 (Salmon et al., SC'11), the counter-based generator shared
@@ -96,6 +98,10 @@ void or_get_probs(const float *logits, int V, float temperature, int top_k,
 int or_sample(const float *probs, int V, double u);
 int or_argmax(const float *x, int V);
 
+/* Accept loop, residual resample and bonus of one cycle (see oracle.c). */
+int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
+                   int V, int greedy, int has_bonus, const float *u_accept,
+                   float u_final, int *tok, int64_t *ties);
 /* generate_speculative for one sequence; out receives P + max_new ids. */
 int or_generate_speculative(const or_model *target, const or_model *draft,
                             const int32_t *prompt, int P, int max_new,

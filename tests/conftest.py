@@ -14,3 +14,12 @@ if TESTS not in sys.path:
 def pytest_configure(config):
     config.addinivalue_line(
         "markers", "gpu: needs an MI355X (gfx950) and the built libnnhip.so")
+
+
+@pytest.fixture(scope="session")
+def ctx():
+    """One device context (HIP stream) for all GPU tests of a session."""
+    import gpu_util
+    c = gpu_util.nnhip.Context(0)
+    yield c
+    c.close()

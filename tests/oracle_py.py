@@ -20,7 +20,8 @@ _lib = None
 class SpecStats(C.Structure):
     _fields_ = [("cycles", C.c_int64), ("drafted", C.c_int64),
                 ("accepted", C.c_int64), ("ties", C.c_int64),
-                ("resampled", C.c_int64), ("bonus", C.c_int64)]
+                ("resampled", C.c_int64), ("bonus", C.c_int64),
+                ("prefill_ms", C.c_double), ("decode_ms", C.c_double)]
 
 
 def lib():
@@ -63,6 +64,9 @@ def lib():
         L.or_get_probs.argtypes = [fp, i32, f32, i32, f32, fp]
         L.or_sample.argtypes = [fp, i32, C.c_double]
         L.or_argmax.argtypes = [fp, i32]
+        L.or_accept_step.argtypes = [fp, fp, ip, i32, i32, i32, i32, fp, f32,
+                                     C.POINTER(C.c_int),
+                                     C.POINTER(C.c_int64)]
         L.or_generate_speculative.argtypes = [vp, vp, ip, i32, i32, i32, f32,
                                               i32, f32, u64, u32, ip,
                                               C.POINTER(SpecStats)]
@@ -200,6 +204,20 @@ def get_probs(logits, T, top_k=0, top_p=1.0):
 def sample(probs, u):
     probs = np.ascontiguousarray(probs, np.float32)
     return lib().or_sample(fptr(probs), probs.size, float(u))
+
+
+def accept_step(p, q, cand, greedy, has_bonus, u_accept, u_final):
+    """or_accept_step: p [M(+1)][V], q [M][V] probability rows."""
+    p = np.ascontiguousarray(p, np.float32)
+    q = np.ascontiguousarray(q, np.float32)
+    cand = np.ascontiguousarray(cand, np.int32)
+    ua = np.ascontiguousarray(u_accept, np.float32)
+    tok, ties = C.c_int(), C.c_int64()
+    n = lib().or_accept_step(fptr(p), fptr(q), iptr(cand), len(cand),
+                             q.shape[-1], int(greedy), int(has_bonus),
+                             fptr(ua), float(u_final), C.byref(tok),
+                             C.byref(ties))
+    return n, tok.value, ties.value
 
 
 def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,

@@ -1,0 +1,211 @@
+"""Whole-path parity of libnnhip.so against the oracle (GPU).
+
+Forward logits within 1e-4 (row-relative) of the oracle, the reference's
+integration invariants on the device (greedy speculative == greedy
+autoregressive, cache == no cache, causal independence), and token streams
+identical to the oracle's generate_speculative given the same Philox
+uniforms: exactly in greedy mode, and in sampled mode up to a recorded
+accept / CDF tie.
+"""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from gpu_util import assert_rows_close, nnhip
+
+pytestmark = pytest.mark.gpu
+
+# Toy greedy configuration (target 2L/128/4h/512, draft 1L/64/2h/256, V 256)
+TOY_T = dict(vocab=256, d=128, H=4, F=512, L=2)
+TOY_D = dict(vocab=256, d=64, H=2, F=256, L=1)
+# int8 batch-1 configuration (target 6L/512/8h/2048, draft 2L/256/4h/1024)
+CFG2_T = dict(vocab=4096, d=512, H=8, F=2048, L=6)
+CFG2_D = dict(vocab=4096, d=256, H=4, F=1024, L=2)
+
+
+def build(ctx, cfg, seed, quantize, max_seq=1024, std=0.02):
+    params = O.make_params(cfg["vocab"], cfg["d"], cfg["H"], cfg["F"],
+                           cfg["L"], seed, std=std)
+    om = O.Model(cfg["vocab"], cfg["d"], cfg["H"], cfg["F"], cfg["L"],
+                 max_seq, params, quantize)
+    gm = nnhip.Decoder(ctx, cfg["vocab"], cfg["d"], cfg["H"], cfg["F"],
+                       cfg["L"], max_seq)
+    gm.set_params(params)
+    if quantize:
+        gm.quantize()
+    return om, gm, params
+
+
+def test_params_roundtrip_and_quantized_codes(ctx):
+    om, gm, params = build(ctx, TOY_T, 1, True)
+    for i in (0, 1, 2, 9, 10, 15, 16, len(params) - 2, len(params) - 1):
+        np.testing.assert_array_equal(gm.get_param(i).ravel(),
+                                      params[i].ravel())
+    d, F, V = TOY_T["d"], TOY_T["F"], TOY_T["vocab"]
+    for layer, which, n_in, n_out in ((0, 0, d, d), (1, 2, d, d),
+                                      (0, 4, d, F), (1, 5, d, F),
+                                      (0, 6, F, d), (0, 7, d, V)):
+        gc, gs = gm.get_quantized(layer, which, n_in, n_out)
+        oc, os_ = om.quantized(layer, which, n_in, n_out)
+        np.testing.assert_array_equal(gc, oc)
+        np.testing.assert_array_equal(gs, os_)
+    gm.free()
+
+
+def test_init_normal_rules(ctx):
+    gm = nnhip.Decoder(ctx, 512, 128, 4, 256, 2, 64)
+    gm.init_normal(7, 0.02)
+    a = gm.get_param(1)                      # q.w
+    assert abs(a.mean()) < 2e-3 and abs(a.std() - 0.02) < 1e-3
+    assert not gm.get_param(2).any()         # q.b = 0
+    assert (gm.get_param(15) == 1).all()     # ln1.gamma = 1
+    assert not gm.get_param(16).any()        # ln1.beta = 0
+    gm2 = nnhip.Decoder(ctx, 512, 128, 4, 256, 2, 64)
+    gm2.init_normal(7, 0.02)
+    np.testing.assert_array_equal(gm2.get_param(9), gm.get_param(9))
+    gm.free(); gm2.free()
+
+
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("S", [1, 7, 40])
+def test_forward_vs_oracle(ctx, quant, S):
+    om, gm, _ = build(ctx, TOY_T, 3, quant, std=0.05)
+    rng = np.random.default_rng(S)
+    ids = rng.integers(0, 256, (2, S)).astype(np.int32)
+    ids[1, 0] = 999                          # out of range -> row 0
+    got = gm.forward(ids)
+    for b in range(2):
+        want = om.forward(ids[b])
+        assert_rows_close(got[b], want, 1e-4, f"forward b={b}")
+    gm.free()
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_forward_cache_truncate_vs_oracle(ctx, quant):
+    om, gm, _ = build(ctx, TOY_T, 4, quant, std=0.05)
+    rng = np.random.default_rng(5)
+    seq = rng.integers(0, 256, 30).astype(np.int32)
+    gc = nnhip.KVCache(gm, 1)
+    oc = O.Cache(om)
+    for lo, hi in ((0, 20), (20, 21), (21, 26)):
+        g = gm.forward(seq[None, lo:hi], gc)[0]
+        o = om.forward(seq[lo:hi], oc)
+        assert_rows_close(g, o, 1e-4, f"cached [{lo},{hi})")
+    assert gc.length() == 26
+    gc.truncate(22)
+    oc.truncate(22)
+    g = gm.forward(seq[None, 26:30], gc)[0]
+    o = om.forward(seq[26:30], oc)
+    assert_rows_close(g, o, 1e-4, "after truncate")
+    gc.free()
+    gm.free()
+
+
+def test_causal_independence(ctx):
+    """transformer_test.cpp:153-176 on the device."""
+    _, gm, _ = build(ctx, TOY_T, 6, True)
+    a = gm.forward(np.array([[1, 2, 3, 4, 5]], np.int32))
+    b = gm.forward(np.array([[1, 2, 3, 4, 9]], np.int32))
+    np.testing.assert_array_equal(a[0, :4], b[0, :4])
+    gm.free()
+
+
+def test_capacity_and_unsupported_errors(ctx):
+    _, gt, _ = build(ctx, TOY_T, 7, False, max_seq=40)
+    _, gd, _ = build(ctx, TOY_D, 8, False, max_seq=40)
+    with pytest.raises(nnhip.NNHipError) as e:
+        gt.generate_speculative(gd, np.arange(30), 20, 4, 0.0)
+    assert e.value.code == nnhip.ECAPACITY
+    with pytest.raises(nnhip.NNHipError) as e:
+        gt.generate_speculative(gd, np.arange(3), 4, 2, 1.0, top_k=5)
+    assert e.value.code == nnhip.EUNSUPPORTED
+    with pytest.raises(nnhip.NNHipError) as e:
+        nnhip.KVCache(gt, 1, quantized=True)
+    assert e.value.code == nnhip.EUNSUPPORTED
+    gt.free(); gd.free()
+
+
+def spec_pair(ctx, tcfg, dcfg, seed, quant, std=0.02):
+    ot, gt, _ = build(ctx, tcfg, seed, quant, std=std)
+    od, gd, _ = build(ctx, dcfg, seed + 1, quant, std=std)
+    return ot, gt, od, gd
+
+
+@pytest.mark.parametrize("k", [1, 4])
+@pytest.mark.parametrize("graphs", [0, 1])
+def test_toy_greedy_matches_oracle_and_ar(ctx, k, graphs):
+    """Config: toy fp32 greedy (B=1, prompt 32, 64 new): the device token
+    stream equals the oracle's and the device greedy autoregressive one."""
+    ctx.set_option("graphs", graphs)
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 10, False, std=0.3)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, 256, 32).astype(np.int32)
+    got, st = gt.generate_speculative(gd, prompt, 64, k, 0.0)
+    want, ost = O.generate_speculative(ot, od, prompt, 64, k, 0.0, 42)
+    np.testing.assert_array_equal(got, want)
+    assert (st.cycles, st.accepted) == (ost.cycles, ost.accepted)
+    ar = gt.generate_advanced(prompt, 64, 0.0)
+    np.testing.assert_array_equal(got, ar)
+    ctx.set_option("graphs", 1)
+    gt.free(); gd.free()
+
+
+def test_toy_sampled_matches_oracle(ctx):
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 20, False, std=0.3)
+    rng = np.random.default_rng(21)
+    for seed in (1, 2, 3):
+        prompt = rng.integers(0, 256, 32).astype(np.int32)
+        got, st = gt.generate_speculative(gd, prompt, 64, 4, 1.0, seed=seed)
+        want, ost = O.generate_speculative(ot, od, prompt, 64, 4, 1.0, seed)
+        if not np.array_equal(got, want):
+            assert ost.ties > 0 or st.ties > 0, (seed, got, want)
+        else:
+            assert (st.cycles, st.accepted, st.resampled, st.bonus) == (
+                ost.cycles, ost.accepted, ost.resampled, ost.bonus)
+    gt.free(); gd.free()
+
+
+@pytest.mark.parametrize("T", [0.0, 1.0])
+def test_batch_matches_oracle_per_sequence(ctx, T):
+    """B independent sequences in lockstep = B oracle runs (seq index b)."""
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 30, True, std=0.2)
+    B = 6
+    rng = np.random.default_rng(31)
+    prompts = rng.integers(0, 256, (B, 24)).astype(np.int32)
+    got, stats, tm = gt.generate_speculative_batch(gd, prompts, 40, 3, T, 77)
+    assert tm.decode_ms > 0
+    for b in range(B):
+        want, ost = O.generate_speculative(ot, od, prompts[b], 40, 3, T, 77,
+                                           seq=b)
+        if not np.array_equal(got[b], want):
+            assert T > 0 and (ost.ties > 0 or stats[b].ties > 0), b
+        else:
+            assert stats[b].accepted == ost.accepted
+    gt.free(); gd.free()
+
+
+def test_batch_mfma_rows_match_oracle(ctx):
+    """B = 20 rows of drafting use the MFMA digit GEMM (rows >= 16)."""
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 40, True, std=0.2)
+    B = 20
+    rng = np.random.default_rng(41)
+    prompts = rng.integers(0, 256, (B, 16)).astype(np.int32)
+    got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
+    for b in (0, 7, 19):
+        want, _ = O.generate_speculative(ot, od, prompts[b], 24, 4, 0.0, 5,
+                                         seq=b)
+        np.testing.assert_array_equal(got[b], want)
+    gt.free(); gd.free()
+
+
+def test_cfg2_int8_greedy_full_size(ctx):
+    """int8 greedy at full size: target 6L/512/8h/2048/V4096, draft
+    2L/256/4h/1024, prompt 128, k=4, 256 new tokens; exact token stream."""
+    ot, gt, od, gd = spec_pair(ctx, CFG2_T, CFG2_D, 50, True)
+    rng = np.random.default_rng(51)
+    prompt = rng.integers(0, 4096, 128).astype(np.int32)
+    got, st = gt.generate_speculative(gd, prompt, 256, 4, 0.0)
+    want, ost = O.generate_speculative(ot, od, prompt, 256, 4, 0.0, 42)
+    np.testing.assert_array_equal(got, want)
+    assert st.accepted == ost.accepted and st.cycles == ost.cycles
+    gt.free(); gd.free()

@@ -1,0 +1,308 @@
+"""Kernel-level parity of libnnhip.so against the oracle (GPU).
+
+Each kernel runs through the C ABI on seeded inputs and is compared with the
+oracle function restating the same reference step: bit-exact for the int8
+codes, the MFMA digit integers and RoPE; within 1e-4 (row-relative) for fp32
+products, attention and probabilities; identical draws given the same
+uniforms except at a recorded tie.
+"""
+import numpy as np
+import pytest
+
+import oracle_py as O
+from gpu_util import assert_as_accurate, assert_rows_close, nnhip, row_rel_err
+
+pytestmark = pytest.mark.gpu
+
+call = nnhip.call
+
+
+def quantize_oracle(w):
+    codes = np.zeros(w.shape, np.int8)
+    scales = np.zeros(w.shape[1], np.float32)
+    O.lib().or_quantize_w8(O.fptr(w), w.shape[0], w.shape[1], O.i8ptr(codes),
+                           O.fptr(scales))
+    return codes, scales
+
+
+def dense_oracle(x, codes=None, scales=None, w=None, bias=None):
+    rows, K = x.shape
+    N = (codes if codes is not None else w).shape[1]
+    y = np.zeros((rows, N), np.float32)
+    O.lib().or_dense(O.fptr(x), rows, K, N,
+                     O.fptr(w) if w is not None else None,
+                     O.i8ptr(codes) if codes is not None else None,
+                     O.fptr(scales) if scales is not None else None,
+                     O.fptr(bias), O.fptr(y))
+    return y
+
+
+def test_quantize_w8_bit_exact(ctx):
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((300, 70)) * 0.02).astype(np.float32)
+    w[:, 3] = 0.0
+    w[:, 9] = np.float32(0.5) * np.arange(300, dtype=np.float32) - 50
+    codes_o, scales_o = quantize_oracle(w)
+    dw = ctx.array(w)
+    dc = ctx.array(shape=(70, 300), dtype=np.int8)
+    ds = ctx.array(shape=(70,))
+    call("nnhip_quantize_w8", ctx.h, dw.p, 300, 70, dc.p, ds.p)
+    np.testing.assert_array_equal(dc.numpy().T, codes_o)
+    np.testing.assert_array_equal(ds.numpy(), scales_o)
+
+
+GEMV_SHAPES = [(1, 64, 64), (1, 256, 768), (2, 512, 1536), (3, 1024, 1024),
+               (4, 1024, 4096), (5, 2048, 512), (8, 4096, 1024),
+               (1, 4096, 1024), (6, 128, 320)]
+
+
+@pytest.mark.parametrize("rows,K,N", GEMV_SHAPES)
+def test_gemv_w8a32(ctx, rows, K, N):
+    rng = np.random.default_rng(rows * 7 + K + N)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    codes, scales = quantize_oracle(w)
+    want = dense_oracle(x, codes, scales, bias=b)
+    dx, dc = ctx.array(x), ctx.array(np.ascontiguousarray(codes.T))
+    ds, db = ctx.array(scales), ctx.array(b)
+    dy = ctx.array(shape=(rows, N))
+    call("nnhip_linear_w8a32", ctx.h, dx.p, rows, K, dc.p, ds.p, db.p, N,
+         dy.p, 1)
+    got = dy.numpy()
+    assert_rows_close(got, want, 1e-4, "gemv w8a32")
+    exact = x.astype(np.float64) @ (codes.astype(np.float64) *
+                                    scales.astype(np.float64)) + b
+    assert_as_accurate(got, want, exact, what="gemv w8a32")
+
+
+@pytest.mark.parametrize("rows,K,N", [(1, 64, 192), (3, 128, 512),
+                                      (4, 512, 256), (7, 256, 64)])
+def test_gemv_f32(ctx, rows, K, N):
+    rng = np.random.default_rng(K + N)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    want = dense_oracle(x, w=w, bias=b)
+    dx, dw = ctx.array(x), ctx.array(np.ascontiguousarray(w.T))
+    db, dy = ctx.array(b), ctx.array(shape=(rows, N))
+    call("nnhip_linear_f32", ctx.h, dx.p, rows, K, dw.p, db.p, N, dy.p)
+    assert_rows_close(dy.numpy(), want, 1e-4, "gemv f32")
+
+
+def digits_reference(x):
+    """Restatement of the activation digit split: e = 22 - exponent of the
+    row max, X = rint(x * 2^e), balanced base-256 digits (hi, mid, lo)."""
+    mx = np.abs(x).max(axis=1)
+    e = np.where(mx > 0, 22 - np.frexp(mx)[1], 0).astype(np.int32)
+    X = np.rint(np.ldexp(x.astype(np.float64), e[:, None])).astype(np.int64)
+    lo = ((X + 128) & 255) - 128
+    t = (X - lo) >> 8
+    mid = ((t + 128) & 255) - 128
+    hi = (t - mid) >> 8
+    assert np.abs(hi).max() <= 127
+    np.testing.assert_array_equal(hi * 65536 + mid * 256 + lo, X)
+    return e, hi, mid, lo
+
+
+MFMA_SHAPES = [(16, 128, 64), (32, 512, 1536), (192, 1024, 3072),
+               (70, 4096, 1024), (8, 256, 256), (64, 2048, 512)]
+
+
+@pytest.mark.parametrize("rows,K,N", MFMA_SHAPES)
+def test_mfma_digits_int_bit_exact(ctx, rows, K, N):
+    """int8 x int8 -> int32 MFMA products: the exact integer totals
+    sum_k X[m,k] * code[n,k] must equal the CPU's int64 matmul."""
+    rng = np.random.default_rng(rows + K * 3 + N)
+    x = (rng.standard_normal((rows, K)) * 1.7).astype(np.float32)
+    x[0, :] *= 1e-3                        # a row with a different exponent
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    codes, _ = quantize_oracle(w)
+    e, hi, mid, lo = digits_reference(x)
+    rows64 = (rows + 63) // 64 * 64
+    dx, dc = ctx.array(x), ctx.array(np.ascontiguousarray(codes.T))
+    dt = ctx.array(shape=(rows, N), dtype=np.int64)
+    de = ctx.array(shape=(rows,), dtype=np.int32)
+    dl = ctx.array(shape=(3, rows64, K), dtype=np.int8)
+    call("nnhip_linear_limb_totals", ctx.h, dx.p, rows, K, dc.p, N, dt.p,
+         de.p, dl.p)
+    np.testing.assert_array_equal(de.numpy(), e)
+    limbs = dl.numpy()
+    np.testing.assert_array_equal(limbs[0, :rows], hi)
+    np.testing.assert_array_equal(limbs[1, :rows], mid)
+    np.testing.assert_array_equal(limbs[2, :rows], lo)
+    X = hi * 65536 + mid * 256 + lo
+    want = X @ codes.astype(np.int64)
+    np.testing.assert_array_equal(dt.numpy(), want)
+
+
+@pytest.mark.parametrize("rows,K,N", MFMA_SHAPES)
+def test_mfma_linear_vs_oracle(ctx, rows, K, N):
+    rng = np.random.default_rng(rows * 5 + K + N)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    codes, scales = quantize_oracle(w)
+    want = dense_oracle(x, codes, scales, bias=b)
+    dx, dc = ctx.array(x), ctx.array(np.ascontiguousarray(codes.T))
+    ds, db = ctx.array(scales), ctx.array(b)
+    dy = ctx.array(shape=(rows, N))
+    call("nnhip_linear_w8a32", ctx.h, dx.p, rows, K, dc.p, ds.p, db.p, N,
+         dy.p, 2)
+    got = dy.numpy()
+    assert_rows_close(got, want, 1e-4, "mfma w8a32")
+    exact = x.astype(np.float64) @ (codes.astype(np.float64) *
+                                    scales.astype(np.float64)) + b
+    assert_as_accurate(got, want, exact, what="mfma w8a32")
+
+
+def test_rope_kv_append(ctx):
+    rng = np.random.default_rng(11)
+    B, S, H, D, cap = 3, 5, 4, 64, 700
+    pos = np.array([0, 17, 640], np.int32)
+    qkv = rng.standard_normal((B * S, 3 * H * D)).astype(np.float32)
+    dq = ctx.array(qkv)
+    dpos = ctx.array(pos)
+    qo = ctx.array(shape=(B * S, H * D))
+    kc = ctx.array(np.zeros((B, H, cap, D), np.float32))
+    vc = ctx.array(np.zeros((B, H, cap, D), np.float32))
+    call("nnhip_rope_kv_append", ctx.h, dq.p, B, S, H, D, dpos.p, qo.p, kc.p,
+         vc.p, cap)
+    qg, kg, vg = qo.numpy(), kc.numpy(), vc.numpy()
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        for part, got in ((0, None), (1, None)):
+            x = np.ascontiguousarray(
+                rows[:, part * H * D:(part + 1) * H * D].reshape(S, H, D)
+                .transpose(1, 0, 2))
+            O.lib().or_rope(O.fptr(x), H, S, D, int(pos[b]))
+            if part == 0:
+                got = qg[b * S:(b + 1) * S].reshape(S, H, D).transpose(1, 0, 2)
+            else:
+                got = kg[b, :, pos[b]:pos[b] + S]
+            np.testing.assert_array_equal(got, x)
+        v = rows[:, 2 * H * D:].reshape(S, H, D).transpose(1, 0, 2)
+        np.testing.assert_array_equal(vg[b, :, pos[b]:pos[b] + S], v)
+
+
+ATTN_CASES = [(3, 1, 4, 64, [0, 37, 300]), (2, 6, 4, 64, [5, 380]),
+              (2, 8, 2, 32, [0, 900]), (2, 13, 2, 64, [0, 20]),
+              (16, 8, 8, 64, [2048] * 16)]
+
+
+@pytest.mark.parametrize("B,S,H,D,pos0", ATTN_CASES)
+def test_attention_kq(ctx, B, S, H, D, pos0):
+    rng = np.random.default_rng(B * 100 + S + D)
+    pos0 = np.array(pos0, np.int32)
+    cap = int(pos0.max()) + S
+    q = rng.standard_normal((B * S, H * D)).astype(np.float32)
+    k = rng.standard_normal((B, H, cap, D)).astype(np.float32)
+    v = rng.standard_normal((B, H, cap, D)).astype(np.float32)
+    dq, dk, dv = ctx.array(q), ctx.array(k), ctx.array(v)
+    dp, do = ctx.array(pos0), ctx.array(shape=(B * S, H * D))
+    call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
+         D, do.p)
+    got = do.numpy()
+    for b in range(B):
+        St = int(pos0[b]) + S
+        qb = np.ascontiguousarray(q[b * S:(b + 1) * S].reshape(S, H, D)
+                                  .transpose(1, 0, 2))
+        kb = np.ascontiguousarray(k[b, :, :St])
+        vb = np.ascontiguousarray(v[b, :, :St])
+        out = np.zeros((S, H, D), np.float32)
+        O.lib().or_attention(O.fptr(qb), O.fptr(kb), O.fptr(vb), H, H, S, St,
+                             D, 1, O.fptr(out))
+        assert_rows_close(got[b * S:(b + 1) * S].reshape(S, H * D),
+                          out.reshape(S, H * D), 1e-4, f"attention seq {b}")
+
+
+@pytest.mark.parametrize("rows,d", [(7, 64), (5, 1024), (3, 4096), (2, 100)])
+def test_layernorm(ctx, rows, d):
+    rng = np.random.default_rng(d)
+    x = (rng.standard_normal((rows, d)) * 2 + 0.5).astype(np.float32)
+    g = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    want = np.zeros_like(x)
+    O.lib().or_layernorm(O.fptr(x), rows, d, O.fptr(g), O.fptr(b), 1e-5,
+                         O.fptr(want))
+    dx, dg, db = ctx.array(x), ctx.array(g), ctx.array(b)
+    dy = ctx.array(shape=(rows, d))
+    call("nnhip_layernorm", ctx.h, dx.p, rows, d, dg.p, db.p, dy.p)
+    assert_rows_close(dy.numpy(), want, 1e-5, "layernorm")
+
+
+def cdf_tie(probs, u, tol=1e-6):
+    c = np.cumsum(probs.astype(np.float64) / probs.astype(np.float64).sum())
+    return bool(np.min(np.abs(c - u)) < tol)
+
+
+@pytest.mark.parametrize("V,T", [(256, 1.0), (4096, 0.7), (32000, 1.0),
+                                 (32000, 0.0), (1000, 2.5)])
+def test_sample_rows(ctx, V, T):
+    B = 24
+    rng = np.random.default_rng(V + int(T * 10))
+    lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    u = np.array([O.uniform(99, b, 3, 1) for b in range(B)], np.float32)
+    dl, du = ctx.array(lg), ctx.array(u)
+    dt = ctx.array(shape=(B,), dtype=np.int32)
+    dp = ctx.array(shape=(B, V))
+    call("nnhip_sample_rows", ctx.h, dl.p, B, V, T, du.p, dt.p, dp.p)
+    tok = dt.numpy()
+    mism = 0
+    for b in range(B):
+        p = O.get_probs(lg[b], T)
+        if T <= 0:
+            assert tok[b] == int(np.argmax(lg[b]))
+            continue
+        assert row_rel_err(dp.numpy()[b][None], p[None]) <= 1e-4
+        want = O.sample(p, u[b])
+        if tok[b] != want:
+            assert cdf_tie(p, u[b]), (b, tok[b], want)
+            mism += 1
+    assert mism <= 1
+
+
+def accept_case(ctx, B, k, V, T, corr, seed):
+    rng = np.random.default_rng(seed)
+    tl = (rng.standard_normal((B, k, V)) * 2).astype(np.float32)
+    dl = (corr * tl + (1 - corr) * rng.standard_normal((B, k, V)) * 2
+          ).astype(np.float32)
+    ua = rng.random((B, k)).astype(np.float32)
+    ur = rng.random(B).astype(np.float32)
+    dtok = np.zeros((B, k), np.int32)
+    for b in range(B):
+        for j in range(k):
+            q = O.get_probs(dl[b, j], T if T > 0 else 1.0)
+            dtok[b, j] = O.sample(q, rng.random())
+    dt_, dd, dk = ctx.array(tl), ctx.array(dl), ctx.array(dtok)
+    dua, dur = ctx.array(ua), ctx.array(ur)
+    dn = ctx.array(shape=(B,), dtype=np.int32)
+    dx = ctx.array(shape=(B,), dtype=np.int32)
+    call("nnhip_spec_accept", ctx.h, dt_.p, dd.p, dk.p, dua.p, dur.p, B, k, V,
+         T, dn.p, dx.p)
+    n_gpu, tok_gpu = dn.numpy(), dx.numpy()
+    ties = 0
+    for b in range(B):
+        p = np.stack([O.get_probs(tl[b, j], T) for j in range(k)])
+        q = np.stack([O.get_probs(dl[b, j], T) for j in range(k)])
+        n, tok, nt = O.accept_step(p, q, dtok[b], T <= 0, False, ua[b], ur[b])
+        if (n, tok) != (int(n_gpu[b]), int(tok_gpu[b])):
+            # allowed only where the oracle met an accept or CDF tie
+            j = min(n, int(n_gpu[b]))
+            r = ua[b, j] if j < k else 0
+            at_tie = nt > 0 or (j < k and abs(
+                r - p[j, dtok[b, j]] / q[j, dtok[b, j]]) < 1e-6)
+            if not at_tie and n == int(n_gpu[b]) and n < k:
+                rec = np.maximum(0, p[n] - q[n])
+                at_tie = cdf_tie(rec if rec.sum() > 0 else p[n], ur[b])
+            assert at_tie, (b, n, tok, n_gpu[b], tok_gpu[b])
+            ties += 1
+    return n_gpu, ties
+
+
+@pytest.mark.parametrize("T,corr", [(1.0, 0.0), (1.0, 0.97), (0.0, 0.9)])
+def test_spec_accept_vs_oracle(ctx, T, corr):
+    n, ties = accept_case(ctx, 48, 8, 32000, T, corr, seed=int(corr * 100))
+    assert ties <= 1
+    if corr > 0.9 and T > 0:
+        assert n.max() >= 3          # the correlated case accepts runs
