@@ -174,6 +174,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="launch each kernel of a cycle separately instead "
+                         "of replaying one HIP graph per cycle")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU only: every box in this setup has a "
@@ -181,6 +184,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     ctx = nnhip.Context(0)
+    if a.no_graphs:
+        ctx.set_option("graphs", 0)
     r = run_cfg4(ctx, a.steps, a.warmup)
     roof = roofline_attention(ctx)
     b1 = None if a.no_batch1 else run_cfg2(ctx)

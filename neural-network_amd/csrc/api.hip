@@ -380,9 +380,11 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
     if (mfma) {
       LimbScratch ls;
       ls.ensure(rows, K);
+      nnhip::DevBuf<int8_t> sw((size_t)N * K);
+      nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
       nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
       nnhip::launch_gemm_limb(st, ls.limbs.p, ls.mpad, ls.rexp.p, rows, K, N,
-                              codes, scales, bias, nullptr, 0, y, N,
+                              sw.p, scales, bias, nullptr, 0, y, N,
                               nnhip::kEpiBias);
       NNHIP_CHECK(hipStreamSynchronize(st));
     } else {
@@ -413,13 +415,19 @@ int nnhip_linear_limb_totals(nnhip_ctx *ctx, const float *x, int rows, int K,
     ls.ensure(rows, K);
     NNHIP_CHECK(hipMemsetAsync(ls.limbs.p, 0, ls.limbs.bytes(), st));
     nnhip::DevBuf<float> dummy(N);
+    nnhip::DevBuf<int8_t> sw((size_t)N * K);
+    nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
     nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
     nnhip::launch_gemm_limb(st, ls.limbs.p, ls.mpad, ls.rexp.p, rows, K, N,
-                            codes, dummy.p, dummy.p, nullptr, 0,
+                            sw.p, dummy.p, dummy.p, nullptr, 0,
                             reinterpret_cast<float *>(totals), N,
                             nnhip::kEpiTotals);
     if (rexp) NNHIP_CHECK(hipMemcpyAsync(rexp, ls.rexp.p, (size_t)rows * 4, hipMemcpyDeviceToDevice, st));
-    if (limbs) NNHIP_CHECK(hipMemcpyAsync(limbs, ls.limbs.p, ls.limbs.bytes(), hipMemcpyDeviceToDevice, st));
+    if (limbs)
+      for (int l = 0; l < 3; ++l)
+        nnhip::launch_swizzle_rows(st, ls.limbs.p + (size_t)l * ls.mpad * K,
+                                   ls.mpad, K, limbs + (size_t)l * ls.mpad * K,
+                                   true);
     NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }

@@ -303,28 +303,35 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
     }
   }
   if (!limbs) return;
+  // digits of y for the next MFMA GEMM, in the MFMA operand layout
+  __shared__ float srow[4096];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    int c = threadIdx.x + i * 256;
+    if (c < d) srow[c] = v[i];
+  }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-  int e = 0;
-  if (mx > 0.f) { int ex; (void)frexpf(mx, &ex); e = kLimbBits - ex; }
+  const int e = digit_exponent(mx);
   if (threadIdx.x == 0) rexp[row] = e;
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int64_t plane = (int64_t)mpad * d;
+  for (int p = threadIdx.x; p < d / 16; p += 256) {
+    const int k = p * 16;
+    v4i hi, mid, lo;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    int c = threadIdx.x + i * 256;
-    if (c < d) {
-      int X = (int)rintf(ldexpf(v[i], e));
-      int lo = (int)(int8_t)(X & 0xff);
-      int t = (X - lo) >> 8;
-      int mid = (int)(int8_t)(t & 0xff);
-      int hi = (t - mid) >> 8;
-      limbs[row * d + c] = (int8_t)hi;
-      limbs[((int64_t)mpad + row) * d + c] = (int8_t)mid;
-      limbs[((int64_t)2 * mpad + row) * d + c] = (int8_t)lo;
+    for (int q = 0; q < 4; ++q) {
+      const int3 t = digits4(srow + k + 4 * q, e);
+      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
     }
+    const int64_t off = mfma_operand_offset((int)row, k, d);
+    *reinterpret_cast<v4i *>(limbs + off) = hi;
+    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
+    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
   }
 }
 
@@ -423,6 +430,8 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,
                       int8_t *limbs, int mpad, int *rexp) {
   NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
+  NNHIP_REQUIRE(!limbs || (d % 128 == 0 && rows <= mpad), kErrArg,
+                "layernorm: digit output needs d % 128 == 0");
   hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,
                      b, y, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());

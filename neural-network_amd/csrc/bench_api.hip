@@ -117,7 +117,7 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     NNHIP_REQUIRE(ctx && ms && rows > 0 && K > 0 && N > 0 && iters > 0 && nbuf > 0,
                   nnhip::kErrArg, "nnhip_bench_linear: bad argument");
     hipStream_t st = ctx->c.stream;
-    std::vector<nnhip::DevBuf<int8_t>> W(nbuf);
+    std::vector<nnhip::DevBuf<int8_t>> W(nbuf), WS(nbuf);
     std::vector<nnhip::DevBuf<float>> S(nbuf);
     nnhip::DevBuf<float> wf((size_t)N * K), x((size_t)rows * K), y((size_t)rows * N), b(N);
     nnhip::launch_init_normal(st, x.p, 1, rows * K, 0, 1, 11, 0, 1.f, 0);
@@ -126,6 +126,10 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
       W[i].alloc((size_t)N * K); S[i].alloc(N);
       nnhip::launch_init_normal(st, wf.p, 1, N * K, 0, 1, 20 + i, 0, 0.02f, 0);
       nnhip::launch_quantize_w8(st, wf.p, N, K, W[i].p, S[i].p);
+      if (path == 2) {
+        WS[i].alloc((size_t)N * K);
+        nnhip::launch_swizzle_rows(st, W[i].p, N, K, WS[i].p, false);
+      }
     }
     const int mpad = (rows + 63) / 64 * 64;
     nnhip::DevBuf<int8_t> limbs((size_t)3 * mpad * K);
@@ -134,7 +138,7 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
       const int j = i % nbuf;
       if (path == 2) {
         nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
-        nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, W[j].p,
+        nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, WS[j].p,
                                 S[j].p, b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
       } else {
         nnhip::launch_gemv(st, x.p, K, rows, K, N, W[j].p, nullptr, S[j].p,

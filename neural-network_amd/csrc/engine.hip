@@ -139,9 +139,13 @@ void Model::set_param(int idx, const float *host) {
   else
     launch_transpose_into(st, stage.p, 1, r.N, r.lin->b.p, r.row_base,
                           r.row_stride);
-  if (r.kind == ParamRef::kWeight && r.lin->quant)
+  if (r.kind == ParamRef::kWeight && r.lin->quant) {
     launch_quantize_w8(st, r.lin->w.p, r.lin->N, r.lin->K, r.lin->q.p,
                        r.lin->s.p);
+    if (r.lin->qs.p)
+      launch_swizzle_rows(st, r.lin->q.p, r.lin->N, r.lin->K, r.lin->qs.p,
+                          false);
+  }
   NNHIP_CHECK(hipStreamSynchronize(st));
 }
 
@@ -204,6 +208,10 @@ void Model::quantize() {
   auto q = [&](Linear &ln) {
     if (!ln.q.p) ln.q.alloc((size_t)ln.N * ln.K);
     launch_quantize_w8(st, ln.w.p, ln.N, ln.K, ln.q.p, ln.s.p);
+    if (ln.K % 128 == 0 && ln.N % 64 == 0) {
+      if (!ln.qs.p) ln.qs.alloc((size_t)ln.N * ln.K);
+      launch_swizzle_rows(st, ln.q.p, ln.N, ln.K, ln.qs.p, false);
+    }
     ln.quant = true;
   };
   for (auto &ly : layers) { q(ly.qkv); q(ly.o); q(ly.gu); q(ly.down); }
@@ -270,7 +278,7 @@ void Model::reserve(int rows, int lrows, int max_keys) {
 }
 
 bool Model::use_limbs(const Linear &ln, int rows) const {
-  return ln.quant && rows >= kLimbMinRows && ln.K % 128 == 0 &&
+  return ln.quant && ln.qs.p && rows >= kLimbMinRows && ln.K % 128 == 0 &&
          ln.N % 64 == 0;
 }
 
@@ -282,7 +290,7 @@ void Model::linear(const Linear &ln, const float *x, int64_t ldx, int rows,
     if (!limbs_ready)
       launch_act_quant(st, x, ldx, rows, ln.K, ws.limbs.p, ws.mpad, ws.rexp.p);
     launch_gemm_limb(st, ws.limbs.p, ws.mpad, ws.rexp.p, rows, ln.K, ln.N,
-                     ln.q.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi);
+                     ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi);
   } else {
     launch_gemv(st, x, ldx, rows, ln.K, ln.N, ln.quant ? ln.q.p : nullptr,
                 ln.quant ? nullptr : ln.w.p, ln.s.p, ln.b.p, resid, ldr, y,

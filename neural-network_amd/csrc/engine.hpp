@@ -22,6 +22,7 @@ struct Linear {
   int K = 0, N = 0;
   DevBuf<float> w;      // [N][K] fp32 master weight
   DevBuf<int8_t> q;     // [N][K] int8 codes (after quantize)
+  DevBuf<int8_t> qs;    // the same codes in the MFMA operand layout
   DevBuf<float> s;      // [N] per-channel scales
   DevBuf<float> b;      // [N] bias
   bool quant = false;

@@ -25,6 +25,9 @@ namespace {
 
 constexpr int kWave = 64;
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -147,7 +150,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 // ---------------------------------------------------------------------------
 // Activation digits for the MFMA GEMM.  Row m: e = 22 - exponent(max|x|), so
 // |x * 2^e| < 2^22; X = rint(x * 2^e) (exact scaling, ties to even) is split
-// into balanced base-256 digits hi, mid, lo in [-128, 127].
+// into balanced base-256 digits hi, mid, lo in [-128, 127], written as three
+// planes in the MFMA operand layout (mfma_operand_offset).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void act_quant_kernel(
     const float *__restrict__ x, int64_t ldx, int K, int8_t *__restrict__ limbs,
@@ -162,91 +166,161 @@ __global__ __launch_bounds__(256) void act_quant_kernel(
   if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
-  int e = 0;
-  if (mx > 0.f) {
-    int ex;
-    (void)frexpf(mx, &ex);
-    e = kLimbBits - ex;
-  }
+  const int e = digit_exponent(mx);
   if (threadIdx.x == 0) rexp[m] = e;
-  int8_t *l0 = limbs + (int64_t)m * K;
-  int8_t *l1 = limbs + ((int64_t)mpad + m) * K;
-  int8_t *l2 = limbs + ((int64_t)2 * mpad + m) * K;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    int X = (int)rintf(ldexpf(xr[k], e));
-    int lo = (int)(int8_t)(X & 0xff);
-    int t = (X - lo) >> 8;
-    int mid = (int)(int8_t)(t & 0xff);
-    int hi = (t - mid) >> 8;
-    l0[k] = (int8_t)hi;
-    l1[k] = (int8_t)mid;
-    l2[k] = (int8_t)lo;
+  const int64_t plane = (int64_t)mpad * K;
+  for (int p = threadIdx.x; p < K / 16; p += blockDim.x) {
+    const int k = p * 16;
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = *reinterpret_cast<const float4 *>(xr + k + 4 * q);
+      v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+    }
+    v4i hi, mid, lo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int3 t = digits4(v + 4 * q, e);
+      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
+    }
+    const int64_t off = mfma_operand_offset(m, k, K);
+    *reinterpret_cast<v4i *>(limbs + off) = hi;
+    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
+    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
   }
 }
 
 // ---------------------------------------------------------------------------
-// int8 MFMA GEMM over the activation digits.  Workgroup tile 64 x 64, four
-// waves of 32 x 32, three int32 accumulators (one per digit) per wave.
-// Within each 128-wide K chunk, lane (r, h) supplies bytes
+// int8 MFMA GEMM over the activation digits.  Workgroup tile 32 rows x 64
+// columns; the four waves split K (chunks of 128, wave w takes chunks w,
+// w+4, ...) with the next chunk's loads issued before the current chunk's
+// MFMAs, and the three int32 accumulators per 32x32 sub-tile (one per digit)
+// are summed across waves with LDS integer atomics (exact, order-free).
+// Both operands are stored in the MFMA operand layout (mfma_operand_offset):
+// within each 128-wide K chunk, lane (r, h) supplies bytes
 // [h*64 + s*16, h*64 + s*16 + 16) of its row for MFMA step s, identically for
 // the digit operand and the weight operand, so each MFMA contracts matching
-// k indices whatever order the hardware assigns to a lane's 16 bytes.
+// k indices whatever order the hardware assigns to a lane's 16 bytes, and
+// every operand load of a wave is one contiguous 1 KB block.
+// Tiles are dealt to the 8 XCDs in contiguous runs (row tiles of one column
+// tile adjacent), so a weight tile is fetched from HBM into one XCD's L2.
 // ---------------------------------------------------------------------------
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int kGemmMT = 32, kGemmNT = 64;
 
 __global__ __launch_bounds__(256) void gemm_limb_kernel(
     const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
     int M, int K, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi) {
+    int64_t ldy, int epi, int ntm, int ntn) {
+  __shared__ int red[kLimbs][kGemmMT][kGemmNT];
+  const int T = ntm * ntn;
+  const int per = (T + 7) / 8;
+  const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (wi >= T) return;
+  const int tn = wi / ntm, tm = wi % ntm;
+  const int m0 = tm * kGemmMT, n0 = tn * kGemmNT;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
-  const int m0 = blockIdx.y * 64 + (w >> 1) * 32;
-  const int n0 = blockIdx.x * 64 + (w & 1) * 32;
+  for (int i = threadIdx.x; i < kLimbs * kGemmMT * kGemmNT; i += 256)
+    (&red[0][0][0])[i] = 0;
+  __syncthreads();
 
-  v16i acc0 = {}, acc1 = {}, acc2 = {};
-  const int8_t *pb = wq + (int64_t)(n0 + r) * K + h * 64;
-  const int8_t *pa0 = limbs + (int64_t)(m0 + r) * K + h * 64;
+  v16i acc[2][kLimbs];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int l = 0; l < kLimbs; ++l) acc[t][l] = v16i{};
+  const int nch = K / 128;
+  // tile bases in the operand layout: 32 rows x 128 k = 4 KB per chunk
+  const int8_t *pb0 = wq + (int64_t)(n0 >> 5) * nch * 4096 + lane * 16;
+  const int8_t *pb1 = pb0 + (int64_t)nch * 4096;
+  const int8_t *pa0 = limbs + (int64_t)(m0 >> 5) * nch * 4096 + lane * 16;
   const int8_t *pa1 = pa0 + (int64_t)mpad * K;
   const int8_t *pa2 = pa1 + (int64_t)mpad * K;
-  for (int kb = 0; kb < K; kb += 128) {
-    v4i b[4], a0[4], a1[4], a2[4];
+  v4i cb0[4], cb1[4], ca0[4], ca1[4], ca2[4];
+  auto load = [&](int c, v4i (&b0)[4], v4i (&b1)[4], v4i (&a0)[4],
+                  v4i (&a1)[4], v4i (&a2)[4]) {
+    const int kb = c * 4096;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      b[s] = *reinterpret_cast<const v4i *>(pb + kb + s * 16);
-      a0[s] = *reinterpret_cast<const v4i *>(pa0 + kb + s * 16);
-      a1[s] = *reinterpret_cast<const v4i *>(pa1 + kb + s * 16);
-      a2[s] = *reinterpret_cast<const v4i *>(pa2 + kb + s * 16);
+      b0[s] = *reinterpret_cast<const v4i *>(pb0 + kb + s * 1024);
+      b1[s] = *reinterpret_cast<const v4i *>(pb1 + kb + s * 1024);
+      a0[s] = *reinterpret_cast<const v4i *>(pa0 + kb + s * 1024);
+      a1[s] = *reinterpret_cast<const v4i *>(pa1 + kb + s * 1024);
+      a2[s] = *reinterpret_cast<const v4i *>(pa2 + kb + s * 1024);
     }
+  };
+  int c = w;
+  if (c < nch) load(c, cb0, cb1, ca0, ca1, ca2);
+  for (; c < nch; c += 4) {
+    v4i nb0[4], nb1[4], na0[4], na1[4], na2[4];
+    const bool more = c + 4 < nch;
+    if (more) load(c + 4, nb0, nb1, na0, na1, na2);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[s], b[s], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[s], b[s], acc1, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2[s], b[s], acc2, 0, 0, 0);
+      acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca0[s], cb0[s], acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca1[s], cb0[s], acc[0][1], 0, 0, 0);
+      acc[0][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca2[s], cb0[s], acc[0][2], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca0[s], cb1[s], acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca1[s], cb1[s], acc[1][1], 0, 0, 0);
+      acc[1][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca2[s], cb1[s], acc[1][2], 0, 0, 0);
+    }
+    if (more) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        cb0[s] = nb0[s]; cb1[s] = nb1[s];
+        ca0[s] = na0[s]; ca1[s] = na1[s]; ca2[s] = na2[s];
+      }
     }
   }
-  const int n = n0 + r;
-  const float sc = scale[n], bi = bias[n];
+  if (w < nch) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int m = m0 + (j >> 2) * 8 + h * 4 + (j & 3);
-    long long tot = (long long)acc0[j] * 65536LL + (long long)acc1[j] * 256LL +
-                    (long long)acc2[j];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int l = 0; l < kLimbs; ++l)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int row = (j >> 2) * 8 + h * 4 + (j & 3);
+          atomicAdd(&red[l][row][t * 32 + r], acc[t][l][j]);
+        }
+  }
+  __syncthreads();
+  // epilogue: thread -> (row, column pair)
+  for (int idx = threadIdx.x; idx < kGemmMT * kGemmNT / 2; idx += 256) {
+    const int row = idx / (kGemmNT / 2), cp = idx % (kGemmNT / 2);
+    const int m = m0 + row;
+    if (m >= M) continue;
+    const int c0 = 2 * cp;
+    long long tot[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      tot[e] = (long long)red[0][row][c0 + e] * 65536LL +
+               (long long)red[1][row][c0 + e] * 256LL +
+               (long long)red[2][row][c0 + e];
+    const int n = n0 + c0;
     if (epi == kEpiTotals) {
-      if (m < M) reinterpret_cast<long long *>(y)[(int64_t)m * ldy + n] = tot;
+      long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
+      yt[0] = tot[0]; yt[1] = tot[1];
       continue;
     }
-    float v = ldexpf((float)tot, -(m < M ? rexp[m] : 0));
-    v = __fadd_rn(__fmul_rn(v, sc), bi);
+    const int e = rexp[m];
+    float v[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      v[q] = ldexpf((float)tot[q], -e);
+      v[q] = __fadd_rn(__fmul_rn(v[q], scale[n + q]), bias[n + q]);
+    }
     if (epi == kEpiSwiGLU) {
-      float u = __shfl_xor(v, 1, kWave);
-      if (m < M && !(n & 1)) y[(int64_t)m * ldy + n / 2] = silu_mul(v, u);
-    } else if (m < M) {
-      if (epi == kEpiResid) v = resid[(int64_t)m * ldr + n] + v;
-      y[(int64_t)m * ldy + n] = v;
+      y[(int64_t)m * ldy + n / 2] = silu_mul(v[0], v[1]);
+    } else {
+      if (epi == kEpiResid) {
+        v[0] = resid[(int64_t)m * ldr + n] + v[0];
+        v[1] = resid[(int64_t)m * ldr + n + 1] + v[1];
+      }
+      y[(int64_t)m * ldy + n] = v[0];
+      y[(int64_t)m * ldy + n + 1] = v[1];
     }
   }
 }
@@ -274,6 +348,30 @@ __global__ __launch_bounds__(256) void quantize_w8_kernel(
     qf = fmaxf(-127.0f, fminf(127.0f, qf));
     q[n * K + k] = (int8_t)qf;
   }
+}
+
+// Row-major int8 [R][K] <-> MFMA operand layout, one 16-byte piece per
+// thread (piece p is the p-th 16 bytes of the operand layout).
+__global__ __launch_bounds__(256) void swizzle_rows_kernel(
+    const int8_t *__restrict__ src, int R, int K, int8_t *__restrict__ dst,
+    int inverse) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= (int64_t)R * K / 16) return;
+  const int nch = K / 128;
+  const int lane = (int)(p & 63);
+  int64_t q = p >> 6;
+  const int s = (int)(q & 3);
+  q >>= 2;
+  const int c = (int)(q % nch);
+  const int64_t t = q / nch;
+  const int64_t row = t * 32 + (lane & 31);
+  const int col = c * 128 + (lane >> 5) * 64 + s * 16;
+  if (inverse)
+    *reinterpret_cast<v4i *>(dst + row * K + col) =
+        *reinterpret_cast<const v4i *>(src + p * 16);
+  else
+    *reinterpret_cast<v4i *>(dst + p * 16) =
+        *reinterpret_cast<const v4i *>(src + row * K + col);
 }
 
 // dst[(row_base + n*row_stride)][k] = src[k][n]  (32x32 tiles through LDS)
@@ -393,6 +491,8 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
 void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
                       int K, int8_t *limbs, int mpad, int *rexp) {
   if (rows <= 0) return;
+  NNHIP_REQUIRE(K % 128 == 0 && ldx % 4 == 0 && rows <= mpad, kErrArg,
+                "act_quant: K % 128 and ldx % 4 must be 0");
   hipLaunchKernelGGL(act_quant_kernel, dim3(rows), dim3(256), 0, st, x, ldx, K,
                      limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
@@ -406,10 +506,11 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   NNHIP_REQUIRE(K % 128 == 0 && N % 64 == 0, kErrArg,
                 "gemm_limb: K % 128 and N % 64 must be 0");
   NNHIP_REQUIRE(mpad % 64 == 0 && rows <= mpad, kErrArg, "gemm_limb: bad mpad");
-  dim3 grid(N / 64, (rows + 63) / 64);
-  hipLaunchKernelGGL(gemm_limb_kernel, grid, dim3(256), 0, st, limbs, mpad,
-                     rexp, rows, K, N, wq, scale, bias, resid, ldr, y, ldy,
-                     epi);
+  const int ntm = (rows + kGemmMT - 1) / kGemmMT, ntn = N / kGemmNT;
+  const int per = (ntm * ntn + 7) / 8;
+  hipLaunchKernelGGL(gemm_limb_kernel, dim3(8 * per), dim3(256), 0, st, limbs,
+                     mpad, rexp, rows, K, N, wq, scale, bias, resid, ldr, y,
+                     ldy, epi, ntm, ntn);
   NNHIP_CHECK(hipGetLastError());
 }
 
@@ -417,6 +518,16 @@ void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
                         int8_t *q_nk, float *scales) {
   hipLaunchKernelGGL(quantize_w8_kernel, dim3(N), dim3(256), 0, st, w_nk, K,
                      q_nk, scales);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_swizzle_rows(hipStream_t st, const int8_t *src, int R, int K,
+                         int8_t *dst, bool inverse) {
+  NNHIP_REQUIRE(R % 32 == 0 && K % 128 == 0, kErrArg,
+                "swizzle: R % 32 and K % 128 must be 0");
+  const int64_t pieces = (int64_t)R * K / 16;
+  hipLaunchKernelGGL(swizzle_rows_kernel, dim3((unsigned)((pieces + 255) / 256)),
+                     dim3(256), 0, st, src, R, K, dst, inverse ? 1 : 0);
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -87,6 +87,50 @@ enum Epi : int {
 static constexpr int kLimbs = 3;
 static constexpr int kLimbBits = 22;  // |X| < 2^22
 
+// MFMA operand layout of an int8 [R][K] matrix (R % 32 == 0, K % 128 == 0):
+// element (m, k) lives at
+//   [m/32][k/128][(k%64)/16][lane = ((k%128)/64)*32 + m%32][k%16],
+// so the 16 bytes one lane feeds to one v_mfma_i32_32x32x32_i8 step are
+// contiguous and a wave's 64 lanes read one contiguous 1 KB block.  Used for
+// the weight codes of the MFMA path and for the activation digits (one
+// plane of R*K bytes per digit).
+__host__ __device__ inline int64_t mfma_operand_offset(int m, int k, int K) {
+  const int nch = K / 128;
+  const int c = k >> 7, kk = k & 127;
+  const int h = kk >> 6, s = (kk & 63) >> 4, byte = kk & 15;
+  const int lane = h * 32 + (m & 31);
+  return ((((int64_t)(m >> 5) * nch + c) * 4 + s) * 64 + lane) * 16 + byte;
+}
+
+// X = rint(x * 2^e) split into balanced base-256 digits, returned packed
+// four per int for 4 consecutive x as (hi, mid, lo).
+__device__ inline int3 digits4(const float *x, int e) {
+  int hi = 0, mid = 0, lo = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int X = (int)rintf(ldexpf(x[i], e));
+    const int l = (int)(int8_t)(X & 0xff);
+    const int t = (X - l) >> 8;
+    const int md = (int)(int8_t)(t & 0xff);
+    const int h = (t - md) >> 8;
+    lo |= (l & 0xff) << (8 * i);
+    mid |= (md & 0xff) << (8 * i);
+    hi |= (h & 0xff) << (8 * i);
+  }
+  return make_int3(hi, mid, lo);
+}
+
+// Row exponent e = 22 - exponent(max|x|) (0 for an all-zero row).
+__device__ inline int digit_exponent(float mx) {
+  int e = 0;
+  if (mx > 0.f) {
+    int ex;
+    (void)frexpf(mx, &ex);
+    e = kLimbBits - ex;
+  }
+  return e;
+}
+
 // linear.hip
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
@@ -101,6 +145,9 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       int epi);
 void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
                         int8_t *q_nk, float *scales);
+// row-major int8 [R][K] <-> MFMA operand layout (R % 32, K % 128 == 0)
+void launch_swizzle_rows(hipStream_t st, const int8_t *src, int R, int K,
+                         int8_t *dst, bool inverse);
 void launch_transpose_into(hipStream_t st, const float *src_kn, int K, int N,
                            float *dst, int64_t row_base, int64_t row_stride);
 void launch_transpose_out(hipStream_t st, const float *src, int K, int N,
