@@ -174,6 +174,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--groups", type=int, default=2,
+                    help="sequence groups driven on separate HIP streams")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch each kernel of a cycle separately instead "
                          "of replaying one HIP graph per cycle")
@@ -186,6 +188,7 @@ def main():
     ctx = nnhip.Context(0)
     if a.no_graphs:
         ctx.set_option("graphs", 0)
+    ctx.set_option("groups", a.groups)
     r = run_cfg4(ctx, a.steps, a.warmup)
     roof = roofline_attention(ctx)
     b1 = None if a.no_batch1 else run_cfg2(ctx)
@@ -204,6 +207,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 weights x fp32 activations (fp32 KV)",
         "data": "synthetic: seeded N(0,0.02) weights, uniform random prompts",
+        "groups": a.groups,
         "config": {"workload": "sampled speculative decode, 32 sequences, "
                                "target 12L/1024/16h/4096/V32000 int8, draft "
                                "4L/512/8h/2048 int8, prompt 256, k=5, T=1.0, "

@@ -54,7 +54,11 @@ typedef struct {
 const char *nnhip_last_error(void);
 int nnhip_init(int device, nnhip_ctx **out);
 int nnhip_destroy(nnhip_ctx *ctx);
-/* "graphs" (1 = replay each speculative cycle as one HIP graph, default). */
+/* "graphs": 1 = replay each speculative cycle as one HIP graph (default).
+ * "groups": split a batch into this many groups of sequences, each driven
+ * on its own HIP stream so that their kernels overlap (0 = 1 group).
+ * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids,
+ * 0 = always 32x32 tiles (default; process-wide). */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);
 int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out);

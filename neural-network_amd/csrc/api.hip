@@ -68,6 +68,8 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
   return guard([&] {
     REQ(ctx && key, "nnhip_set_option: NULL argument");
     if (std::strcmp(key, "graphs") == 0) ctx->c.use_graphs = value != 0;
+    else if (std::strcmp(key, "groups") == 0) ctx->c.groups = value;
+    else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
     else throw nnhip::Error(nnhip::kErrArg, std::string("unknown option ") + key);
   });
 }
@@ -226,7 +228,7 @@ int nnhip_decoder_forward(nnhip_model *mm, nnhip_kvcache *cache,
     nnhip::DevBuf<float> d_log((size_t)B * S * m.V);
     int max_keys = S;
     if (kv) for (int b = 0; b < B; ++b) max_keys = std::max(max_keys, kv->host_len[b] + S);
-    m.forward(kv, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
+    m.forward(0, kv, 0, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
               max_keys, d_log.p, false);
     NNHIP_CHECK(hipMemcpyAsync(logits, d_log.p, d_log.bytes(), hipMemcpyDeviceToHost, st));
     if (kv) {

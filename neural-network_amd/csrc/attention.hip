@@ -14,12 +14,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 namespace nnhip {
 
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kKeysPerSplit = 256;
+constexpr int kKeysPerSplit = 128;
 constexpr int kMaxQ = 8;       // queries per workgroup
 constexpr int kMaxD = 64;      // head dim handled by the attention kernel
 
@@ -87,21 +89,39 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split-K attention.  Grid (split, head, b * n_qblocks).  32 lane groups of 8
-// lanes; a group owns one key at a time (8 dims per lane) and keeps an online
-// softmax (max, sum, acc) per query; groups merge by shuffles, waves through
-// LDS.  Arithmetic: score = dot / sqrt(D), keys j > q_pos masked, p =
-// exp(score - max), out = (sum p v) * (1 / sum p), as layer.cpp:859-948.
+// Split-K attention.  Grid (split of 128 keys, head, b * n_qblocks).  Each of
+// the 32 lane groups (8 lanes, 8 dims per lane) loads 4 consecutive keys at
+// once, scores them for every query of the block, and keeps (max, sum, acc)
+// per query; groups merge by shuffles, waves through LDS, and the split's
+// partial state is written for attn_combine_kernel.  Arithmetic: score =
+// dot / sqrt(D), keys j > q_pos masked, p = exp(score - max), out =
+// (sum p v) * (1 / sum p), as layer.cpp:859-948.
 // ---------------------------------------------------------------------------
+constexpr int kKeysPerGroup = 4;
+
+// Sum over the 8 lanes of an aligned lane group with DPP: swap neighbours,
+// swap pairs, then mirror the two quads (row_half_mirror).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+           0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+           0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+           0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 template <int SQ>
 __global__ __launch_bounds__(256) void attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc,
     const float *__restrict__ vc, int S, int H, int Hkv, int D, int cap,
     int64_t seq_stride, const int32_t *__restrict__ base, int off,
-    const int32_t *__restrict__ active, int nsplit, int nqb,
-    float *__restrict__ part, float *__restrict__ out) {
-  __shared__ float s_ml[4][SQ][2];
-  __shared__ float s_acc[4][SQ][kMaxD];
+    const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
+    float *__restrict__ part) {
+  constexpr int kGroups = 32;
+  __shared__ float s_m[kGroups][SQ], s_l[kGroups][SQ], s_f[kGroups][SQ];
+  __shared__ float s_acc[kGroups][SQ][kMaxD];
+  __shared__ float s_M[SQ];
   const int sp = blockIdx.x, h = blockIdx.y;
   const int b = blockIdx.z / nqb, qb = blockIdx.z % nqb;
   if (active && !active[b]) return;
@@ -113,143 +133,195 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const int hk = h / (H / Hkv);
   const int pos0 = base[b] + off + q0;         // position of query q0
   const int kend_all = min(pos0 + nq, cap);    // keys [0, kend_all) visible
-  const int kbeg = sp * kKeysPerSplit;
-  const int kend = min(kbeg + kKeysPerSplit, kend_all);
+  const int ks = sp * kps;
+  const int kend = min(ks + kps, kend_all);
   const float scale = sqrtf((float)D);
   const int dl = D / 8;                        // dims per lane (<= 8)
+  const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
+  const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
 
-  float qv[SQ][8];
-#pragma unroll
-  for (int i = 0; i < SQ; ++i)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      int dd = sub * dl + e;
-      qv[i][e] = (i < nq && e < dl)
-                     ? q[((int64_t)b * S + q0 + i) * E + h * D + dd]
-                     : 0.f;
-    }
+  // the block's queries, read by every lane group through LDS broadcasts
+  __shared__ float s_q[SQ][kMaxD];
+  for (int t = threadIdx.x; t < SQ * kMaxD; t += blockDim.x) {
+    const int i = t / kMaxD, dd = t % kMaxD;
+    s_q[i][dd] = (i < nq && dd < D) ? q[((int64_t)b * S + q0 + i) * E + h * D + dd] : 0.f;
+  }
+  __syncthreads();
   float m[SQ], l[SQ], acc[SQ][8];
 #pragma unroll
   for (int i = 0; i < SQ; ++i) {
     m[i] = -INFINITY; l[i] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+    for (int x = 0; x < 8; ++x) acc[i][x] = 0.f;
   }
-  const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
-  const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
-  for (int j = kbeg + g; j < kend; j += 32) {
-    float kv[8], vv[8];
-    if (dl == 8) {
-      const float4 *kp = reinterpret_cast<const float4 *>(kb + (int64_t)j * D + sub * 8);
-      const float4 *vp = reinterpret_cast<const float4 *>(vb + (int64_t)j * D + sub * 8);
-      float4 k0 = kp[0], k1 = kp[1], v0 = vp[0], v1 = vp[1];
-      kv[0] = k0.x; kv[1] = k0.y; kv[2] = k0.z; kv[3] = k0.w;
-      kv[4] = k1.x; kv[5] = k1.y; kv[6] = k1.z; kv[7] = k1.w;
-      vv[0] = v0.x; vv[1] = v0.y; vv[2] = v0.z; vv[3] = v0.w;
-      vv[4] = v1.x; vv[5] = v1.y; vv[6] = v1.z; vv[7] = v1.w;
-    } else {
+
+  struct Blk { float k[kKeysPerGroup][8], v[kKeysPerGroup][8]; };
+  auto load = [&](int j0, Blk &bk) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kv[e] = e < dl ? kb[(int64_t)j * D + sub * dl + e] : 0.f;
-        vv[e] = e < dl ? vb[(int64_t)j * D + sub * dl + e] : 0.f;
+    for (int e = 0; e < kKeysPerGroup; ++e) {
+      const int j = j0 + e;
+      const bool ok = j < kend;
+      if (dl == 8) {
+        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
+        if (ok) {
+          const float4 *kp = reinterpret_cast<const float4 *>(kb + (int64_t)j * D + sub * 8);
+          const float4 *vp = reinterpret_cast<const float4 *>(vb + (int64_t)j * D + sub * 8);
+          k0 = kp[0]; k1 = kp[1]; v0 = vp[0]; v1 = vp[1];
+        }
+        bk.k[e][0] = k0.x; bk.k[e][1] = k0.y; bk.k[e][2] = k0.z; bk.k[e][3] = k0.w;
+        bk.k[e][4] = k1.x; bk.k[e][5] = k1.y; bk.k[e][6] = k1.z; bk.k[e][7] = k1.w;
+        bk.v[e][0] = v0.x; bk.v[e][1] = v0.y; bk.v[e][2] = v0.z; bk.v[e][3] = v0.w;
+        bk.v[e][4] = v1.x; bk.v[e][5] = v1.y; bk.v[e][6] = v1.z; bk.v[e][7] = v1.w;
+      } else {
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          bk.k[e][x] = (ok && x < dl) ? kb[(int64_t)j * D + sub * dl + x] : 0.f;
+          bk.v[e][x] = (ok && x < dl) ? vb[(int64_t)j * D + sub * dl + x] : 0.f;
+        }
       }
     }
+  };
+  // online softmax over one block of 4 keys starting at j0
+  auto consume = [&](int j0, const Blk &bk) {
 #pragma unroll
     for (int i = 0; i < SQ; ++i) {
-      float dot = 0.f;
+      float qv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dot += qv[i][e] * kv[e];
-      dot += __shfl_xor(dot, 1, kWave);
-      dot += __shfl_xor(dot, 2, kWave);
-      dot += __shfl_xor(dot, 4, kWave);
-      if (i >= nq || j > pos0 + i) continue;   // causal mask
-      const float sc = dot / scale;
-      if (sc > m[i]) {
-        const float corr = expf(m[i] - sc);
-        l[i] *= corr;
+      for (int x = 0; x < 8; ++x) qv[x] = x < dl ? s_q[i][sub * dl + x] : 0.f;
+      float sc[kKeysPerGroup];
+      float mb = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] *= corr;
-        m[i] = sc;
+      for (int e = 0; e < kKeysPerGroup; ++e) {
+        float dot = 0.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) dot += qv[x] * bk.k[e][x];
+        dot = group8_sum(dot);
+        const int j = j0 + e;
+        const bool valid = i < nq && j < kend && j <= pos0 + i;   // causal
+        sc[e] = valid ? dot / scale : -INFINITY;
+        mb = fmaxf(mb, sc[e]);
       }
-      const float p = expf(sc - m[i]);
-      l[i] += p;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[i][e] += p * vv[e];
-    }
-  }
-  // merge the 8 lane groups of this wave
-#pragma unroll
-  for (int o = 8; o <= 32; o <<= 1) {
-#pragma unroll
-    for (int i = 0; i < SQ; ++i) {
-      const float mo = __shfl_xor(m[i], o, kWave);
-      const float lo = __shfl_xor(l[i], o, kWave);
-      const float mn = fmaxf(m[i], mo);
+      if (mb == -INFINITY) continue;
+      const float mn = fmaxf(m[i], mb);
       const float a = (m[i] == -INFINITY) ? 0.f : expf(m[i] - mn);
-      const float c = (mo == -INFINITY) ? 0.f : expf(mo - mn);
-      l[i] = l[i] * a + lo * c;
+      l[i] *= a;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float ao = __shfl_xor(acc[i][e], o, kWave);
-        acc[i][e] = acc[i][e] * a + ao * c;
-      }
+      for (int x = 0; x < 8; ++x) acc[i][x] *= a;
       m[i] = mn;
+#pragma unroll
+      for (int e = 0; e < kKeysPerGroup; ++e) {
+        const float p = expf(sc[e] - mn);        // 0 for masked keys
+        l[i] += p;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc[i][x] += p * bk.v[e][x];
+      }
     }
+  };
+  // group g takes blocks g, g+32, ... of the split; the next block's loads
+  // are in flight while the current one is scored
+  constexpr int kStride = kGroups * kKeysPerGroup;
+  Blk ba, bb;
+  int j0 = ks + g * kKeysPerGroup;
+  if (j0 < kend) load(j0, ba);
+  while (j0 < kend) {
+    if (j0 + kStride < kend) load(j0 + kStride, bb);
+    consume(j0, ba);
+    j0 += kStride;
+    if (j0 >= kend) break;
+    if (j0 + kStride < kend) load(j0 + kStride, ba);
+    consume(j0, bb);
+    j0 += kStride;
   }
-  if (lane < 8) {
 #pragma unroll
-    for (int i = 0; i < SQ; ++i) {
-      if (lane == 0) { s_ml[w][i][0] = m[i]; s_ml[w][i][1] = l[i]; }
+  for (int i = 0; i < SQ; ++i) {
+    if (sub == 0) { s_m[g][i] = m[i]; s_l[g][i] = l[i]; }
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (e < dl) s_acc[w][i][sub * dl + e] = acc[i][e];
-    }
+    for (int x = 0; x < 8; ++x)
+      if (x < dl) s_acc[g][i][sub * dl + x] = acc[i][x];
+  }
+  __syncthreads();
+  // merge the 32 groups: per query the common max, per (group, query) the
+  // rescale factor, then per (query, dim) the weighted sums
+  if (threadIdx.x < nq) {
+    float mn = -INFINITY;
+    for (int gg = 0; gg < kGroups; ++gg) mn = fmaxf(mn, s_m[gg][threadIdx.x]);
+    s_M[threadIdx.x] = mn;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < kGroups * nq; t += blockDim.x) {
+    const int gg = t / nq, i = t % nq;
+    const float mg = s_m[gg][i];
+    s_f[gg][i] = (mg == -INFINITY) ? 0.f : expf(mg - s_M[i]);
   }
   __syncthreads();
   for (int t = threadIdx.x; t < nq * D; t += blockDim.x) {
     const int i = t / D, dd = t % D;
-    float mn = -INFINITY;
-    for (int ww = 0; ww < 4; ++ww) mn = fmaxf(mn, s_ml[ww][i][0]);
     float ls = 0.f, as = 0.f;
-    for (int ww = 0; ww < 4; ++ww) {
-      const float mw = s_ml[ww][i][0];
-      const float f = (mw == -INFINITY) ? 0.f : expf(mw - mn);
-      ls += s_ml[ww][i][1] * f;
-      as += s_acc[ww][i][dd] * f;
+    for (int gg = 0; gg < kGroups; ++gg) {
+      const float f = s_f[gg][i];
+      ls += s_l[gg][i] * f;
+      as += s_acc[gg][i][dd] * f;
     }
     const int64_t row = (int64_t)b * S + q0 + i;
-    if (nsplit == 1) {
-      const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-      out[row * E + h * D + dd] = as * inv;
-    } else {
-      const int64_t pi = (row * H + h) * nsplit + sp;
-      float *pp = part + pi * (D + 2);
-      if (dd == 0) { pp[0] = mn; pp[1] = ls; }
-      pp[2 + dd] = as;
-    }
+    const int64_t pi = (row * H + h) * nsplit + sp;
+    float *pp = part + pi * (D + 2);
+    if (dd == 0) { pp[0] = s_M[i]; pp[1] = ls; }
+    pp[2 + dd] = as;
   }
 }
 
-__global__ __launch_bounds__(64) void attn_combine_kernel(
+// Merges the splits of every head of one row (b, s), writes the context row
+// [H*D] and, when requested, its int8 digits for the output projection
+// (same rule as act_quant_kernel).
+__global__ __launch_bounds__(256) void attn_combine_kernel(
     const float *__restrict__ part, int S, int H, int D, int nsplit,
-    const int32_t *__restrict__ active, float *__restrict__ out) {
-  const int64_t rh = blockIdx.x;            // row * H + h
-  const int64_t row = rh / H;
-  const int h = (int)(rh % H);
+    const int32_t *__restrict__ active, float *__restrict__ out,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+  __shared__ float srow[4096];
+  __shared__ float sred[4];
+  const int64_t row = blockIdx.x;
   if (active && !active[row / S]) return;
-  const float *pp = part + rh * nsplit * (D + 2);
-  float mn = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mn = fmaxf(mn, pp[s * (D + 2)]);
-  for (int dd = threadIdx.x; dd < D; dd += blockDim.x) {
+  const int E = H * D;
+  float mx = 0.f;
+  for (int t = threadIdx.x; t < E; t += blockDim.x) {
+    const int h = t / D, dd = t % D;
+    const float *pp = part + (row * H + h) * nsplit * (D + 2);
+    float mn = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) mn = fmaxf(mn, pp[sp * (D + 2)]);
     float ls = 0.f, as = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = pp[s * (D + 2)];
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float ms = pp[sp * (D + 2)];
       const float f = (ms == -INFINITY) ? 0.f : expf(ms - mn);
-      ls += pp[s * (D + 2) + 1] * f;
-      as += pp[s * (D + 2) + 2 + dd] * f;
+      ls += pp[sp * (D + 2) + 1] * f;
+      as += pp[sp * (D + 2) + 2 + dd] * f;
     }
     const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-    out[row * H * D + h * D + dd] = as * inv;
+    const float v = as * inv;
+    out[row * E + t] = v;
+    if (limbs) { srow[t] = v; mx = fmaxf(mx, fabsf(v)); }
+  }
+  if (!limbs) return;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+  const int e = digit_exponent(mx);
+  if (threadIdx.x == 0) rexp[row] = e;
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int64_t plane = (int64_t)mpad * E;
+  for (int p = threadIdx.x; p < E / 16; p += blockDim.x) {
+    const int k = p * 16;
+    v4i hi, mid, lo;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int3 t = digits4(srow + k + 4 * qq, e);
+      hi[qq] = t.x; mid[qq] = t.y; lo[qq] = t.z;
+    }
+    const int64_t o2 = mfma_operand_offset((int)row, k, E);
+    *reinterpret_cast<v4i *>(limbs + o2) = hi;
+    *reinterpret_cast<v4i *>(limbs + plane + o2) = mid;
+    *reinterpret_cast<v4i *>(limbs + 2 * plane + o2) = lo;
   }
 }
 
@@ -382,9 +454,23 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
   NNHIP_CHECK(hipGetLastError());
 }
 
+// Splits of the key range: enough (sequence, head, query block, split)
+// workgroups to fill the GPU about 3 times over, each split a multiple of
+// 128 keys.
+static int attention_splits(int B, int S, int H, int max_keys, int *kps) {
+  const int nqb = (S + kMaxQ - 1) / kMaxQ;
+  const int units = std::max(1, B * H * nqb);
+  const int max_split = std::max(1, (std::max(max_keys, 1) + kKeysPerSplit - 1) / kKeysPerSplit);
+  int ns = std::min(max_split, std::max(1, (768 + units - 1) / units));
+  int k = (std::max(max_keys, 1) + ns - 1) / ns;
+  k = (k + kKeysPerSplit - 1) / kKeysPerSplit * kKeysPerSplit;
+  ns = (std::max(max_keys, 1) + k - 1) / k;
+  if (kps) *kps = k;
+  return ns;
+}
+
 int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys) {
-  int nsplit = (max_keys + kKeysPerSplit - 1) / kKeysPerSplit;
-  if (nsplit <= 1) return 0;
+  const int nsplit = attention_splits(B, S, H, max_keys, nullptr);
   return (int64_t)B * S * H * nsplit * (D + 2);
 }
 
@@ -392,13 +478,18 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
                       const float *vc, int B, int S, int H, int Hkv, int D,
                       int cap, int64_t seq_stride, const int32_t *base,
                       int off, const int32_t *active, int max_keys,
-                      float *part, int64_t part_elems, float *out) {
+                      float *part, int64_t part_elems, float *out,
+                      int8_t *limbs, int mpad, int *rexp) {
   NNHIP_REQUIRE(D % 8 == 0 && D <= kMaxD, kErrArg,
                 "attention: head dim must be a multiple of 8 and <= 64");
   NNHIP_REQUIRE(Hkv > 0 && H % Hkv == 0, kErrArg, "attention: bad kv heads");
+  NNHIP_REQUIRE(H * D <= 4096, kErrArg, "attention: H*D must be <= 4096");
+  NNHIP_REQUIRE(!limbs || ((H * D) % 128 == 0 && B * S <= mpad), kErrArg,
+                "attention: digit output needs H*D % 128 == 0");
   if (max_keys < 1) max_keys = 1;
-  const int nsplit = (max_keys + kKeysPerSplit - 1) / kKeysPerSplit;
-  NNHIP_REQUIRE(nsplit == 1 || part_elems >= attention_partial_elems(B, S, H, D, max_keys),
+  int kps = 0;
+  const int nsplit = attention_splits(B, S, H, max_keys, &kps);
+  NNHIP_REQUIRE(part_elems >= attention_partial_elems(B, S, H, D, max_keys),
                 kErrArg, "attention: partial buffer too small");
   const int nqb = (S + kMaxQ - 1) / kMaxQ;
   const int sq = S < kMaxQ ? S : kMaxQ;
@@ -406,7 +497,7 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
 #define NNHIP_ATTN(SQV)                                                      \
   hipLaunchKernelGGL((attn_kernel<SQV>), grid, dim3(256), 0, st, q, kc, vc, S, \
                      H, Hkv, D, cap, seq_stride, base, off, active, nsplit,    \
-                     nqb, part, out)
+                     nqb, kps, part)
   switch (sq) {
     case 1: NNHIP_ATTN(1); break;
     case 2: NNHIP_ATTN(2); break;
@@ -419,11 +510,9 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
   }
 #undef NNHIP_ATTN
   NNHIP_CHECK(hipGetLastError());
-  if (nsplit > 1) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S * H), dim3(64), 0, st,
-                       part, S, H, D, nsplit, active, out);
-    NNHIP_CHECK(hipGetLastError());
-  }
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S), dim3(256), 0, st, part,
+                     S, H, D, nsplit, active, out, limbs, mpad, rexp);
+  NNHIP_CHECK(hipGetLastError());
 }
 
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,

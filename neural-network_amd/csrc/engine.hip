@@ -44,6 +44,20 @@ struct ParamRef {
 
 }  // namespace
 
+hipStream_t Ctx::lane(int g) {
+  if (g == 0) return stream;
+  while ((int)extra.size() < g) {
+    hipStream_t st;
+    NNHIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    extra.push_back(st);
+  }
+  return extra[g - 1];
+}
+
+Ctx::~Ctx() {
+  for (hipStream_t st : extra) (void)hipStreamDestroy(st);
+}
+
 void Linear::init(int k, int n) {
   K = k; N = n;
   w.alloc((size_t)N * K);
@@ -250,7 +264,13 @@ void Model::get_quantized(int layer, int which, int8_t *codes_kn,
   }
 }
 
-void Model::reserve(int rows, int lrows, int max_keys) {
+Workspace &Model::ws(int g) {
+  if ((int)wss.size() <= g) wss.resize(g + 1);
+  return wss[g];
+}
+
+void Model::reserve(int g, int rows, int lrows, int max_keys) {
+  Workspace &ws = this->ws(g);
   if (rows > ws.rows) {
     const int r = std::max(rows, 64);
     ws.rows = r;
@@ -264,7 +284,7 @@ void Model::reserve(int rows, int lrows, int max_keys) {
     ws.rexp.alloc(ws.mpad);
     ws.ids.alloc(r);
     ws.zeros.alloc(r);
-    NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->stream));
+    NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->lane(g)));
   }
   if (lrows > ws.lrows) {
     ws.lrows = lrows;
@@ -282,66 +302,75 @@ bool Model::use_limbs(const Linear &ln, int rows) const {
          ln.N % 64 == 0;
 }
 
-void Model::linear(const Linear &ln, const float *x, int64_t ldx, int rows,
-                   bool limbs_ready, const float *resid, int64_t ldr,
-                   float *y, int64_t ldy, int epi) {
-  hipStream_t st = ctx->stream;
+void Model::linear(int g, const Linear &ln, const float *x, int64_t ldx,
+                   int rows, bool limbs_ready, const float *resid, int64_t ldr,
+                   float *y, int64_t ldy, int epi, const RopeArgs *ra) {
+  hipStream_t st = ctx->lane(g);
+  Workspace &ws = this->ws(g);
   if (use_limbs(ln, rows)) {
     if (!limbs_ready)
       launch_act_quant(st, x, ldx, rows, ln.K, ws.limbs.p, ws.mpad, ws.rexp.p);
     launch_gemm_limb(st, ws.limbs.p, ws.mpad, ws.rexp.p, rows, ln.K, ln.N,
-                     ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi);
+                     ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi, ra);
   } else {
     launch_gemv(st, x, ldx, rows, ln.K, ln.N, ln.quant ? ln.q.p : nullptr,
                 ln.quant ? nullptr : ln.w.p, ln.s.p, ln.b.p, resid, ldr, y,
-                ldy, epi);
+                ldy, epi, ra);
   }
 }
 
-void Model::forward(KVCache *cache, const int32_t *ids, int ids_stride, int B,
-                    int S, const int32_t *base, int off,
+void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
+                    int ids_stride, int B, int S, const int32_t *base, int off,
                     const int32_t *active, int max_keys, float *logits,
                     bool last_only) {
-  hipStream_t st = ctx->stream;
+  hipStream_t st = ctx->lane(g);
   const int R = B * S;
   std::unique_ptr<KVCache> tmp;
   KVCache *kv = cache;
   if (!kv) {
     tmp.reset(new KVCache(this, B, S));
     kv = tmp.get();
-    base = nullptr; off = 0; active = nullptr; max_keys = S;
+    b_off = 0; base = nullptr; off = 0; active = nullptr; max_keys = S;
   }
-  reserve(R, logits ? (last_only ? B : R) : 0, max_keys);
+  NNHIP_REQUIRE(b_off >= 0 && b_off + B <= kv->B, kErrArg,
+                "forward: sequence range outside the cache");
+  reserve(g, R, logits ? (last_only ? B : R) : 0, max_keys);
+  Workspace &ws = this->ws(g);
   const int32_t *bp = base ? base : ws.zeros.p;
   launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p);
   bool limbs_ready = false;
   for (int l = 0; l < L; ++l) {
     LayerW &ly = layers[l];
-    linear(ly.qkv, ws.x.p, d, R, limbs_ready, nullptr, 0, ws.qkv.p, 3 * d,
-           kEpiBias);
-    float *kc = kv->k.p + (int64_t)l * kv->layer_stride();
-    float *vc = kv->v.p + (int64_t)l * kv->layer_stride();
-    launch_rope_kv(st, ws.qkv.p, B, S, H, D, bp, off, active, cosb.p, sinb.p,
-                   ws.qrot.p, kc, vc, kv->cap, kv->seq_stride());
+    float *kc = kv->k.p + (int64_t)l * kv->layer_stride() + b_off * kv->seq_stride();
+    float *vc = kv->v.p + (int64_t)l * kv->layer_stride() + b_off * kv->seq_stride();
+    // q, k, v projection with RoPE and the KV append in its epilogue
+    RopeArgs ra;
+    ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
+    ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
+    ra.qrot = ws.qrot.p; ra.kc = kc; ra.vc = vc; ra.seq_stride = kv->seq_stride();
+    linear(g, ly.qkv, ws.x.p, d, R, limbs_ready, nullptr, 0, nullptr, 3 * d,
+           kEpiRope, &ra);
+    const bool lo = use_limbs(ly.o, R);
     launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
                      kv->seq_stride(), bp, off, active, max_keys, ws.part.p,
-                     ws.part_elems, ws.ctx.p);
-    linear(ly.o, ws.ctx.p, d, R, false, ws.x.p, d, ws.h.p, d, kEpiResid);
+                     ws.part_elems, ws.ctx.p, lo ? ws.limbs.p : nullptr,
+                     ws.mpad, ws.rexp.p);
+    linear(g, ly.o, ws.ctx.p, d, R, lo, ws.x.p, d, ws.h.p, d, kEpiResid);
     const bool l1 = use_limbs(ly.gu, R);
     launch_layernorm(st, ws.h.p, R, d, ly.g1.p, ly.b1.p, ws.x1.p,
                      l1 ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
-    linear(ly.gu, ws.x1.p, d, R, l1, nullptr, 0, ws.ff.p, F, kEpiSwiGLU);
-    linear(ly.down, ws.ff.p, F, R, false, ws.x1.p, d, ws.h.p, d, kEpiResid);
+    linear(g, ly.gu, ws.x1.p, d, R, l1, nullptr, 0, ws.ff.p, F, kEpiSwiGLU);
+    linear(g, ly.down, ws.ff.p, F, R, false, ws.x1.p, d, ws.h.p, d, kEpiResid);
     limbs_ready = l + 1 < L && use_limbs(layers[l + 1].qkv, R);
     launch_layernorm(st, ws.h.p, R, d, ly.g2.p, ly.b2.p, ws.x.p,
                      limbs_ready ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
   }
   if (logits) {
     if (last_only)
-      linear(lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
+      linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
              nullptr, 0, logits, V, kEpiBias);
     else
-      linear(lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
+      linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
   }
   if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
 }
@@ -433,19 +462,47 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                                (size_t)P * 4, (size_t)P * 4, B,
                                hipMemcpyHostToDevice, st));
 
-  SpecState s{};
-  s.cur = bf.cur.p; s.cand = bf.cand.p; s.qprob = bf.qprob.p;
-  s.tlen = bf.tlen.p; s.dlen = bf.dlen.p; s.gen = bf.gen.p; s.cyc = bf.cyc.p;
-  s.active = bf.active.p; s.catchup = bf.catchup.p;
-  s.catch_tok = bf.catch_tok.p; s.out = bf.out.p; s.n_active = bf.n_active.p;
-  s.stats = bf.stats.p;
-  s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new; s.k = k;
-  s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;
-
-  // workspace for every shape the loop uses, before any graph capture
-  t.reserve(B * P, B * (k + 1), t_need);
-  t.reserve(B * (k + 1), B * (k + 1), t_need);
-  dm.reserve(B * P, B, d_need);
+  // Sequences are independent: split the batch into G groups, each driven on
+  // its own lane (stream) so that the groups' kernels overlap on the GPU.
+  int G = ctx->groups > 0 ? ctx->groups : 1;
+  G = std::max(1, std::min(G, B));
+  std::vector<int> gb0(G + 1);
+  for (int g = 0; g <= G; ++g) gb0[g] = (int)((int64_t)B * g / G);
+  std::vector<SpecState> gs(G);
+  std::vector<hipStream_t> lanes(G);
+  for (int g = 0; g < G; ++g) {
+    const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
+    lanes[g] = ctx->lane(g);
+    SpecState &s = gs[g];
+    s.cur = bf.cur.p + b0; s.cand = bf.cand.p + (size_t)b0 * k;
+    s.qprob = bf.qprob.p ? bf.qprob.p + (size_t)b0 * k * V : nullptr;
+    s.tlen = bf.tlen.p + b0; s.dlen = bf.dlen.p + b0; s.gen = bf.gen.p + b0;
+    s.cyc = bf.cyc.p + b0; s.active = bf.active.p + b0;
+    s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;
+    s.out = bf.out.p + (size_t)b0 * out_stride; s.n_active = bf.n_active.p;
+    s.stats = bf.stats.p + (size_t)b0 * 6;
+    s.B = Bg; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
+    s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0 + b0;
+    // workspace for every shape the loop uses, before any graph capture
+    t.reserve(g, Bg * P, Bg * (k + 1), t_need);
+    t.reserve(g, Bg * (k + 1), Bg * (k + 1), t_need);
+    dm.reserve(g, Bg * P, Bg, d_need);
+  }
+  std::vector<hipEvent_t> evj(G);
+  hipEvent_t evf;
+  NNHIP_CHECK(hipEventCreateWithFlags(&evf, hipEventDisableTiming));
+  for (auto &e : evj) NNHIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  auto fork = [&]() {
+    if (G == 1) return;
+    NNHIP_CHECK(hipEventRecord(evf, st));
+    for (int g = 1; g < G; ++g) NNHIP_CHECK(hipStreamWaitEvent(lanes[g], evf, 0));
+  };
+  auto join = [&]() {
+    for (int g = 1; g < G; ++g) {
+      NNHIP_CHECK(hipEventRecord(evj[g], lanes[g]));
+      NNHIP_CHECK(hipStreamWaitEvent(st, evj[g], 0));
+    }
+  };
 
   hipEvent_t e0, e1, e2;
   NNHIP_CHECK(hipEventCreate(&e0));
@@ -453,24 +510,42 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   NNHIP_CHECK(hipEventCreate(&e2));
   NNHIP_CHECK(hipEventRecord(e0, st));
   // prefill (layer.cpp:1400-1408); the draft's prefill logits are unused
-  t.forward(&tc, bf.prompts.p, P, B, P, nullptr, 0, nullptr, P, bf.dlog.p, true);
-  launch_first_token(st, s, bf.dlog.p, V);
-  dm.forward(&dc, bf.prompts.p, P, B, P, nullptr, 0, nullptr, P, nullptr, true);
+  fork();
+  for (int g = 0; g < G; ++g) {
+    const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
+    const int32_t *pr = bf.prompts.p + (size_t)b0 * P;
+    float *dl = bf.dlog.p + (size_t)b0 * V;
+    t.forward(g, &tc, b0, pr, P, Bg, P, nullptr, 0, nullptr, P, dl, true);
+    launch_first_token(lanes[g], gs[g], dl, V);
+    dm.forward(g, &dc, b0, pr, P, Bg, P, nullptr, 0, nullptr, P, nullptr, true);
+  }
+  join();
   NNHIP_CHECK(hipEventRecord(e1, st));
 
   auto cycle = [&]() {
-    for (int j = 0; j < k; ++j) {
-      const int32_t *ids = j == 0 ? bf.cur.p : bf.cand.p + (j - 1);
-      dm.forward(&dc, ids, j == 0 ? 1 : k, B, 1, bf.dlen.p, j, bf.active.p,
-                 d_need, bf.dlog.p, false);
-      launch_draft_sample(st, s, j, bf.dlog.p, V);
+    fork();
+    for (int g = 0; g < G; ++g) {
+      const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
+      hipStream_t ls = lanes[g];
+      int32_t *cur = bf.cur.p + b0, *cand = bf.cand.p + (size_t)b0 * k;
+      int32_t *dlen = bf.dlen.p + b0, *act = bf.active.p + b0;
+      float *dl = bf.dlog.p + (size_t)b0 * V;
+      float *tl = bf.tlog.p + (size_t)b0 * (k + 1) * V;
+      int32_t *vids = bf.vids.p + (size_t)b0 * (k + 1);
+      for (int j = 0; j < k; ++j) {
+        const int32_t *ids = j == 0 ? cur : cand + (j - 1);
+        dm.forward(g, &dc, b0, ids, j == 0 ? 1 : k, Bg, 1, dlen, j, act,
+                   d_need, dl, false);
+        launch_draft_sample(ls, gs[g], j, dl, V);
+      }
+      launch_build_verify_ids(ls, cur, cand, Bg, k, vids);
+      t.forward(g, &tc, b0, vids, k + 1, Bg, k + 1, bf.tlen.p + b0, 0, act,
+                t_need, tl, false);
+      launch_accept(ls, gs[g], tl);
+      dm.forward(g, &dc, b0, bf.catch_tok.p + b0, 1, Bg, 1, dlen, -1,
+                 bf.catchup.p + b0, d_need, nullptr, false);
     }
-    launch_build_verify_ids(st, bf.cur.p, bf.cand.p, B, k, bf.vids.p);
-    t.forward(&tc, bf.vids.p, k + 1, B, k + 1, bf.tlen.p, 0, bf.active.p,
-              t_need, bf.tlog.p, false);
-    launch_accept(st, s, bf.tlog.p);
-    dm.forward(&dc, bf.catch_tok.p, 1, B, 1, bf.dlen.p, -1, bf.catchup.p,
-               d_need, nullptr, false);
+    join();
   };
 
   int32_t *h_nact = nullptr;
@@ -519,6 +594,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     (void)hipHostFree(h_nact);
     (void)hipEventDestroy(ev[0]); (void)hipEventDestroy(ev[1]);
     (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); (void)hipEventDestroy(e2);
+    (void)hipEventDestroy(evf);
+    for (auto &e : evj) (void)hipEventDestroy(e);
     throw;
   }
   if (exec) NNHIP_CHECK(hipGraphExecDestroy(exec));
@@ -532,6 +609,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   NNHIP_CHECK(hipEventDestroy(e0));
   NNHIP_CHECK(hipEventDestroy(e1));
   NNHIP_CHECK(hipEventDestroy(e2));
+  NNHIP_CHECK(hipEventDestroy(evf));
+  for (auto &e : evj) NNHIP_CHECK(hipEventDestroy(e));
   if (timing) {
     timing->prefill_ms = ms_pre;
     timing->decode_ms = ms_dec;
@@ -581,14 +660,15 @@ void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
   for (int step = 0; step < max_new; ++step) {
     const int n = P + step;
     if (use_cache && step > 0) {
-      m.forward(cache.get(), cur.p, 1, B, 1, len.p, 0, nullptr, n, lg.p, true);
+      m.forward(0, cache.get(), 0, cur.p, 1, B, 1, len.p, 0, nullptr, n, lg.p,
+                true);
       launch_add_scalar(st, len.p, B, 1);
     } else {
       // the reference keeps the last max_seq_len tokens (layer.cpp:1271-1277)
       int S = n, start = 0;
       if (S > m.max_seq) { start = S - m.max_seq; S = m.max_seq; }
-      m.forward(cache.get(), dout.p + start, total, B, S, use_cache ? len.p : nullptr,
-                0, nullptr, S, lg.p, true);
+      m.forward(0, cache.get(), 0, dout.p + start, total, B, S,
+                use_cache ? len.p : nullptr, 0, nullptr, S, lg.p, true);
       if (use_cache) launch_add_scalar(st, len.p, B, S);
     }
     launch_ar_sample(st, s, step, lg.p, m.V);

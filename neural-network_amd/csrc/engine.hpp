@@ -10,10 +10,17 @@
 
 namespace nnhip {
 
+// A context owns one HIP stream (lane 0) and, on demand, further lanes on
+// which independent groups of sequences run concurrently.  All lanes keep the
+// default stream priority.
 struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   bool use_graphs = true;
+  int groups = 0;                     // sequence groups per batch (0 = auto)
+  std::vector<hipStream_t> extra;     // lanes 1.. (created on first use)
+  hipStream_t lane(int g);
+  ~Ctx();
 };
 
 // One Dense on the device, weight transposed to [N][K].  Fused layouts:
@@ -54,7 +61,7 @@ struct Model {
   std::vector<LayerW> layers;
   Linear lm;
   DevBuf<float> cosb, sinb;  // [max_seq][D/2]
-  Workspace ws;
+  std::vector<Workspace> wss;  // one per lane
 
   Model(Ctx *c, int vocab, int d_model, int heads, int d_ff, int n_layers,
         int max_seq_len);
@@ -67,21 +74,24 @@ struct Model {
   void get_quantized(int layer, int which, int8_t *codes_kn,
                      float *scales) const;
 
-  // Ensures workspace for `rows` rows of which `lrows` need logits.
-  void reserve(int rows, int lrows, int max_keys);
+  Workspace &ws(int g);
+  // Ensures lane g's workspace for `rows` rows of which `lrows` need logits.
+  void reserve(int g, int rows, int lrows, int max_keys);
 
-  // TransformerDecoder::forward for B sequences of S new tokens each.
+  // TransformerDecoder::forward for B sequences of S new tokens each, on
+  // lane g, using cache sequences [b_off, b_off + B).
   // Token of row (b, s): ids[b*ids_stride + s].  Positions start at
   // base[b] + off (device array; nullptr = 0).  Sequences with
   // active[b] == 0 neither write nor read the cache.  logits: nullptr (not
   // needed), or [B*S][V] (all rows) or [B][V] (last_only).
-  void forward(KVCache *cache, const int32_t *ids, int ids_stride, int B,
-               int S, const int32_t *base, int off, const int32_t *active,
-               int max_keys, float *logits, bool last_only);
+  void forward(int g, KVCache *cache, int b_off, const int32_t *ids,
+               int ids_stride, int B, int S, const int32_t *base, int off,
+               const int32_t *active, int max_keys, float *logits,
+               bool last_only);
 
-  void linear(const Linear &ln, const float *x, int64_t ldx, int rows,
+  void linear(int g, const Linear &ln, const float *x, int64_t ldx, int rows,
               bool limbs_ready, const float *resid, int64_t ldr, float *y,
-              int64_t ldy, int epi);
+              int64_t ldy, int epi, const RopeArgs *ra = nullptr);
   bool use_limbs(const Linear &ln, int rows) const;
 };
 

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const int8_t *__restrict__ wq, const float *__restrict__ wf,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int nks) {
+    int64_t ldy, int epi, int nks, int64_t row0, RopeArgs ra) {
   constexpr int kMaxIt = 4;  // slice <= 1024 elements
   __shared__ float red[4][kGemvNC][R];
   const int lane = threadIdx.x & 63;
@@ -133,12 +133,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     for (int s = 0; s < nks; ++s) a += red[cs * nks + s][cc][r];
     float v = Q8 ? a * scale[n] : a;
     v = v + bias[n];
-    if (epi == kEpiSwiGLU) {
+    if (epi == kEpiSwiGLU || epi == kEpiRope) {
       if (n & 1) continue;
       float a1 = 0.f;
       for (int s = 0; s < nks; ++s) a1 += red[cs * nks + s][cc + 1][r];
       float u = (Q8 ? a1 * scale[n + 1] : a1) + bias[n + 1];
-      y[r * ldy + n / 2] = silu_mul(v, u);
+      if (epi == kEpiSwiGLU) y[r * ldy + n / 2] = silu_mul(v, u);
+      else rope_store_pair(ra, row0 + r, (int)n, v, u);
     } else if (epi == kEpiResid) {
       y[r * ldy + n] = resid[r * ldr + n] + v;
     } else {
@@ -205,79 +206,80 @@ __global__ __launch_bounds__(256) void act_quant_kernel(
 // Tiles are dealt to the 8 XCDs in contiguous runs (row tiles of one column
 // tile adjacent), so a weight tile is fetched from HBM into one XCD's L2.
 // ---------------------------------------------------------------------------
-constexpr int kGemmMT = 32, kGemmNT = 64;
+constexpr int kGemmMT = 32;
 
-__global__ __launch_bounds__(256) void gemm_limb_kernel(
+// NSUB 32-column sub-tiles per workgroup (tile 32 x 32*NSUB).
+template <int NSUB>
+__global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
     int M, int K, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn) {
-  __shared__ int red[kLimbs][kGemmMT][kGemmNT];
+    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
+  constexpr int NT = 32 * NSUB;
+  __shared__ int red[kLimbs][kGemmMT][NT];
   const int T = ntm * ntn;
   const int per = (T + 7) / 8;
   const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
   if (wi >= T) return;
   const int tn = wi / ntm, tm = wi % ntm;
-  const int m0 = tm * kGemmMT, n0 = tn * kGemmNT;
+  const int m0 = tm * kGemmMT, n0 = tn * NT;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
-  for (int i = threadIdx.x; i < kLimbs * kGemmMT * kGemmNT; i += 256)
+  for (int i = threadIdx.x; i < kLimbs * kGemmMT * NT; i += 256)
     (&red[0][0][0])[i] = 0;
   __syncthreads();
 
-  v16i acc[2][kLimbs];
+  v16i acc[NSUB][kLimbs];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < NSUB; ++t)
 #pragma unroll
     for (int l = 0; l < kLimbs; ++l) acc[t][l] = v16i{};
   const int nch = K / 128;
   // tile bases in the operand layout: 32 rows x 128 k = 4 KB per chunk
-  const int8_t *pb0 = wq + (int64_t)(n0 >> 5) * nch * 4096 + lane * 16;
-  const int8_t *pb1 = pb0 + (int64_t)nch * 4096;
-  const int8_t *pa0 = limbs + (int64_t)(m0 >> 5) * nch * 4096 + lane * 16;
-  const int8_t *pa1 = pa0 + (int64_t)mpad * K;
-  const int8_t *pa2 = pa1 + (int64_t)mpad * K;
-  v4i cb0[4], cb1[4], ca0[4], ca1[4], ca2[4];
-  auto load = [&](int c, v4i (&b0)[4], v4i (&b1)[4], v4i (&a0)[4],
-                  v4i (&a1)[4], v4i (&a2)[4]) {
+  const int8_t *pb = wq + (int64_t)(n0 >> 5) * nch * 4096 + lane * 16;
+  const int8_t *pa = limbs + (int64_t)(m0 >> 5) * nch * 4096 + lane * 16;
+  const int64_t plane = (int64_t)mpad * K;
+  struct Frag { v4i b[NSUB][4], a[kLimbs][4]; };
+  auto load = [&](int c, Frag &f) {
     const int kb = c * 4096;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      b0[s] = *reinterpret_cast<const v4i *>(pb0 + kb + s * 1024);
-      b1[s] = *reinterpret_cast<const v4i *>(pb1 + kb + s * 1024);
-      a0[s] = *reinterpret_cast<const v4i *>(pa0 + kb + s * 1024);
-      a1[s] = *reinterpret_cast<const v4i *>(pa1 + kb + s * 1024);
-      a2[s] = *reinterpret_cast<const v4i *>(pa2 + kb + s * 1024);
+#pragma unroll
+      for (int t = 0; t < NSUB; ++t)
+        f.b[t][s] = *reinterpret_cast<const v4i *>(pb + (int64_t)t * nch * 4096 + kb + s * 1024);
+#pragma unroll
+      for (int l = 0; l < kLimbs; ++l)
+        f.a[l][s] = *reinterpret_cast<const v4i *>(pa + l * plane + kb + s * 1024);
     }
   };
+  auto mma = [&](const Frag &f) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < NSUB; ++t)
+#pragma unroll
+        for (int l = 0; l < kLimbs; ++l)
+          acc[t][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[l][s], f.b[t][s], acc[t][l], 0, 0, 0);
+  };
+  // ping-pong over the wave's chunks w, w+4, w+8, ...: the loads of the next
+  // chunk are in flight while the current chunk's MFMAs run
+  Frag fa, fb;
   int c = w;
-  if (c < nch) load(c, cb0, cb1, ca0, ca1, ca2);
-  for (; c < nch; c += 4) {
-    v4i nb0[4], nb1[4], na0[4], na1[4], na2[4];
-    const bool more = c + 4 < nch;
-    if (more) load(c + 4, nb0, nb1, na0, na1, na2);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca0[s], cb0[s], acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca1[s], cb0[s], acc[0][1], 0, 0, 0);
-      acc[0][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca2[s], cb0[s], acc[0][2], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca0[s], cb1[s], acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca1[s], cb1[s], acc[1][1], 0, 0, 0);
-      acc[1][2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ca2[s], cb1[s], acc[1][2], 0, 0, 0);
-    }
-    if (more) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        cb0[s] = nb0[s]; cb1[s] = nb1[s];
-        ca0[s] = na0[s]; ca1[s] = na1[s]; ca2[s] = na2[s];
-      }
-    }
+  if (c < nch) load(c, fa);
+  while (c < nch) {
+    if (c + 4 < nch) load(c + 4, fb);
+    mma(fa);
+    c += 4;
+    if (c >= nch) break;
+    if (c + 4 < nch) load(c + 4, fa);
+    mma(fb);
+    c += 4;
   }
   if (w < nch) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NSUB; ++t)
 #pragma unroll
       for (int l = 0; l < kLimbs; ++l)
 #pragma unroll
@@ -288,8 +290,8 @@ __global__ __launch_bounds__(256) void gemm_limb_kernel(
   }
   __syncthreads();
   // epilogue: thread -> (row, column pair)
-  for (int idx = threadIdx.x; idx < kGemmMT * kGemmNT / 2; idx += 256) {
-    const int row = idx / (kGemmNT / 2), cp = idx % (kGemmNT / 2);
+  for (int idx = threadIdx.x; idx < kGemmMT * NT / 2; idx += 256) {
+    const int row = idx / (NT / 2), cp = idx % (NT / 2);
     const int m = m0 + row;
     if (m >= M) continue;
     const int c0 = 2 * cp;
@@ -314,6 +316,8 @@ __global__ __launch_bounds__(256) void gemm_limb_kernel(
     }
     if (epi == kEpiSwiGLU) {
       y[(int64_t)m * ldy + n / 2] = silu_mul(v[0], v[1]);
+    } else if (epi == kEpiRope) {
+      rope_store_pair(ra, m, n, v[0], v[1]);
     } else {
       if (epi == kEpiResid) {
         v[0] = resid[(int64_t)m * ldr + n] + v[0];
@@ -451,38 +455,45 @@ template <int R>
 void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
                    const int8_t *wq, const float *wf, const float *scale,
                    const float *bias, const float *resid, int64_t ldr,
-                   float *y, int64_t ldy, int epi) {
+                   float *y, int64_t ldy, int epi, int64_t row0,
+                   const RopeArgs &ra) {
   int nks = K >= 1024 ? 4 : (K >= 512 ? 2 : 1);
   int cols = (4 / nks) * kGemvNC;
   dim3 grid((N + cols - 1) / cols);
   if (wq)
     hipLaunchKernelGGL((gemv_kernel<R, true>), grid, dim3(256), 0, st, x, ldx,
                        K, N, wq, wf, scale, bias, resid, ldr, y, ldy, epi,
-                       nks);
+                       nks, row0, ra);
   else
     hipLaunchKernelGGL((gemv_kernel<R, false>), grid, dim3(256), 0, st, x,
                        ldx, K, N, wq, wf, scale, bias, resid, ldr, y, ldy,
-                       epi, nks);
+                       epi, nks, row0, ra);
 }
 
 }  // namespace
 
+// 1: allow 32x64 GEMM tiles for large grids; 0: always 32x32 (default,
+// measured faster on every decode shape).
+int g_gemm_wide = 0;
+
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
-                 int64_t ldy, int epi) {
+                 int64_t ldy, int epi, const RopeArgs *ra) {
   NNHIP_REQUIRE(K % 4 == 0 && K <= 4096, kErrArg, "gemv: K must be a multiple of 4 and <= 4096");
   NNHIP_REQUIRE(epi != kEpiSwiGLU || N % 2 == 0, kErrArg, "gemv: SwiGLU needs even N");
+  NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg, "gemv: RoPE epilogue needs its arguments");
+  const RopeArgs rz = ra ? *ra : RopeArgs{};
   for (int r0 = 0; r0 < rows; r0 += 4) {
     int rr = rows - r0 < 4 ? rows - r0 : 4;
     const float *xp = x + r0 * ldx;
     const float *rp = resid ? resid + r0 * ldr : nullptr;
-    float *yp = y + r0 * ldy;
+    float *yp = y ? y + r0 * ldy : nullptr;
     switch (rr) {
-      case 1: gemv_dispatch<1>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
-      case 2: gemv_dispatch<2>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
-      case 3: gemv_dispatch<3>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
-      default: gemv_dispatch<4>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi); break;
+      case 1: gemv_dispatch<1>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
+      case 2: gemv_dispatch<2>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
+      case 3: gemv_dispatch<3>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
+      default: gemv_dispatch<4>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
     }
   }
   NNHIP_CHECK(hipGetLastError());
@@ -502,15 +513,28 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi) {
+                      int epi, const RopeArgs *ra) {
   NNHIP_REQUIRE(K % 128 == 0 && N % 64 == 0, kErrArg,
                 "gemm_limb: K % 128 and N % 64 must be 0");
+  NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg,
+                "gemm_limb: RoPE epilogue needs its arguments");
+  const RopeArgs rz = ra ? *ra : RopeArgs{};
   NNHIP_REQUIRE(mpad % 64 == 0 && rows <= mpad, kErrArg, "gemm_limb: bad mpad");
-  const int ntm = (rows + kGemmMT - 1) / kGemmMT, ntn = N / kGemmNT;
-  const int per = (ntm * ntn + 7) / 8;
-  hipLaunchKernelGGL(gemm_limb_kernel, dim3(8 * per), dim3(256), 0, st, limbs,
-                     mpad, rexp, rows, K, N, wq, scale, bias, resid, ldr, y,
-                     ldy, epi, ntm, ntn);
+  // 32x64 tiles when they alone give enough workgroups to fill the chip,
+  // otherwise 32x32 tiles (twice the workgroups, two resident per CU)
+  const int ntm = (rows + kGemmMT - 1) / kGemmMT;
+  const bool wide = ntm * (N / 64) >= 512 && g_gemm_wide != 0;
+  if (wide) {
+    const int ntn = N / 64, per = (ntm * ntn + 7) / 8;
+    hipLaunchKernelGGL(gemm_limb_kernel<2>, dim3(8 * per), dim3(256), 0, st,
+                       limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
+                       ldr, y, ldy, epi, ntm, ntn, rz);
+  } else {
+    const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
+    hipLaunchKernelGGL(gemm_limb_kernel<1>, dim3(8 * per), dim3(256), 0, st,
+                       limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
+                       ldr, y, ldy, epi, ntm, ntn, rz);
+  }
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -79,8 +79,48 @@ enum Epi : int {
   kEpiBias = 0,    // y = acc*s + b
   kEpiResid = 1,   // y = resid + (acc*s + b)
   kEpiSwiGLU = 2,  // columns (2n, 2n+1) = (gate n, up n): y[n] = silu(g)*u
-  kEpiTotals = 3   // limb GEMM only: write the exact int64 dot totals
+  kEpiTotals = 3,  // limb GEMM only: write the exact int64 dot totals
+  kEpiRope = 4     // QKV projection: RoPE on q and k, k and v into the cache
 };
+
+// Arguments of the kEpiRope epilogue: row m = b*S + s sits at position
+// base[b] + off + s; columns [0, E) are q (rotated into qrot [rows][E]),
+// [E, 2E) are k (rotated into the cache), [2E, 3E) are v (into the cache),
+// E = H*D; cache rows [b][h][pos][D] with seq_stride floats per sequence.
+struct RopeArgs {
+  int S = 1, H = 1, D = 2, off = 0, cap = 0;
+  const int32_t *base = nullptr, *active = nullptr;
+  const float *cosb = nullptr, *sinb = nullptr;
+  float *qrot = nullptr, *kc = nullptr, *vc = nullptr;
+  int64_t seq_stride = 0;
+};
+
+// Tensor::rope (tensor.cpp:1141-1173) on one pair (x_2j, x_2j+1) of output
+// column n (even) of row m, then the KV append of layer.cpp:758-807.
+__device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
+                                       float xe, float xo) {
+  const int b = (int)(m / ra.S), s = (int)(m % ra.S);
+  if (ra.active && !ra.active[b]) return;
+  const int pos = ra.base[b] + ra.off + s;
+  if (pos < 0 || pos >= ra.cap) return;
+  const int E = ra.H * ra.D;
+  const int part = n / E, nn = n % E;
+  const int h = nn / ra.D, j = (nn % ra.D) >> 1;
+  if (part == 2) {
+    float *vd = ra.vc + b * ra.seq_stride + ((int64_t)h * ra.cap + pos) * ra.D + 2 * j;
+    vd[0] = xe; vd[1] = xo;
+    return;
+  }
+  const int half = ra.D >> 1;
+  const float c = ra.cosb[(int64_t)pos * half + j];
+  const float sn = ra.sinb[(int64_t)pos * half + j];
+  const float r0 = __fsub_rn(__fmul_rn(xe, c), __fmul_rn(xo, sn));
+  const float r1 = __fadd_rn(__fmul_rn(xe, sn), __fmul_rn(xo, c));
+  float *dst = part == 0
+                   ? ra.qrot + m * E + nn
+                   : ra.kc + b * ra.seq_stride + ((int64_t)h * ra.cap + pos) * ra.D + 2 * j;
+  dst[0] = r0; dst[1] = r1;
+}
 
 // Activation limbs for the int8 MFMA GEMM: x[m][k] ~= X[m][k] * 2^-e[m] with
 // X = hi*65536 + mid*256 + lo, each digit an int8.
@@ -132,17 +172,18 @@ __device__ inline int digit_exponent(float mx) {
 }
 
 // linear.hip
+extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
-                 int64_t ldy, int epi);
+                 int64_t ldy, int epi, const RopeArgs *ra = nullptr);
 void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
                       int K, int8_t *limbs, int mpad, int *rexp);
 void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi);
+                      int epi, const RopeArgs *ra = nullptr);
 void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
                         int8_t *q_nk, float *scales);
 // row-major int8 [R][K] <-> MFMA operand layout (R % 32, K % 128 == 0)
@@ -173,7 +214,9 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
                       const float *vc, int B, int S, int H, int Hkv, int D,
                       int cap, int64_t seq_stride, const int32_t *base,
                       int off, const int32_t *active, int max_keys,
-                      float *part, int64_t part_elems, float *out);
+                      float *part, int64_t part_elems, float *out,
+                      int8_t *limbs = nullptr, int mpad = 0,
+                      int *rexp = nullptr);
 int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys);
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,

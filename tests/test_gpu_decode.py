@@ -165,9 +165,12 @@ def test_toy_sampled_matches_oracle(ctx):
     gt.free(); gd.free()
 
 
+@pytest.mark.parametrize("groups", [1, 3])
 @pytest.mark.parametrize("T", [0.0, 1.0])
-def test_batch_matches_oracle_per_sequence(ctx, T):
-    """B independent sequences in lockstep = B oracle runs (seq index b)."""
+def test_batch_matches_oracle_per_sequence(ctx, T, groups):
+    """B independent sequences in lockstep = B oracle runs (seq index b),
+    also when the batch is split into groups on separate streams."""
+    ctx.set_option("groups", groups)
     ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 30, True, std=0.2)
     B = 6
     rng = np.random.default_rng(31)
@@ -181,6 +184,7 @@ def test_batch_matches_oracle_per_sequence(ctx, T):
             assert T > 0 and (ost.ties > 0 or stats[b].ties > 0), b
         else:
             assert stats[b].accepted == ost.accepted
+    ctx.set_option("groups", 0)
     gt.free(); gd.free()
 
 
