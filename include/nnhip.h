@@ -58,7 +58,10 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * "groups": split a batch into this many groups of sequences, each driven
  * on its own HIP stream so that their kernels overlap (0 = 1 group).
  * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids,
- * 0 = always 32x32 tiles (default; process-wide). */
+ * 0 = always 32x32 tiles (default; process-wide).
+ * "attn_waves": number of (key split) waves an attention launch aims for;
+ * the key range of each sequence is split accordingly (default 4096;
+ * process-wide). */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);
 int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out);

@@ -15,13 +15,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 
 namespace nnhip {
 
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kKeysPerSplit = 128;
 constexpr int kMaxQ = 8;       // queries per workgroup
 constexpr int kMaxD = 64;      // head dim handled by the attention kernel
 
@@ -89,214 +89,286 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split-K attention.  Grid (split of 128 keys, head, b * n_qblocks).  Each of
-// the 32 lane groups (8 lanes, 8 dims per lane) loads 4 consecutive keys at
-// once, scores them for every query of the block, and keeps (max, sum, acc)
-// per query; groups merge by shuffles, waves through LDS, and the split's
-// partial state is written for attn_combine_kernel.  Arithmetic: score =
-// dot / sqrt(D), keys j > q_pos masked, p = exp(score - max), out =
-// (sum p v) * (1 / sum p), as layer.cpp:859-948.
+// Split-K attention, one wave per (key split, head, sequence, query block).
+// Arithmetic as layer.cpp:859-948: score = q.k / sqrt(D), keys j > q_pos
+// masked, softmax, out = (sum p v) / (sum p).  The exponentials are taken in
+// base 2: the dot product is scaled by log2(e)/sqrt(D) and p = 2^(s - max),
+// which is the same function.
+//
+// A split is walked in chunks of 32 keys; a chunk's K and V rows are all
+// requested before any arithmetic.
+//  * Scores: lane group g (8 lanes, D/8 dims per lane) owns keys c0+g+8t,
+//    t < 4.  Each lane forms partial dot products for all SQP (power of two
+//    >= queries) queries and a reduce-scatter over the 8 lanes (DPP
+//    row_half_mirror, quad xor 2, quad xor 1) leaves lane `sub` with the full
+//    score of query g8(sub) & (SQP-1): log2(SQP) exchange-adds instead of
+//    3 * SQP.  For that, position p of a lane's query registers holds query
+//    p ^ (g8(sub) & (SQP-1)) with g8(s) = s ^ 3 * bit2(s).
+//  * Softmax: per-query running max across chunks (online rescale), chunk
+//    probabilities written to LDS as [key][query].
+//  * PV: lane (r, dq) owns dims 4dq..4dq+3 of keys c0 + r + kpi*t, with
+//    kpi = 256 / D key rows per wave instruction; the SQP probabilities of a
+//    key are one broadcast LDS read.
+// The split's (max, sum, acc) per query goes to `part` for the combine.
 // ---------------------------------------------------------------------------
-constexpr int kKeysPerGroup = 4;
+constexpr int kChunk = 32;
 
-// Sum over the 8 lanes of an aligned lane group with DPP: swap neighbours,
-// swap pairs, then mirror the two quads (row_half_mirror).
-__device__ __forceinline__ float group8_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-           0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-           0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-           0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-  return v;
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+             0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-template <int SQ>
-__global__ __launch_bounds__(256) void attn_kernel(
+// max / sum over the 8 lanes l, l^8, ..., l^56 (same `sub`, all groups)
+__device__ __forceinline__ float groups_max(float v) {
+  v = fmaxf(v, dppf<0x128>(v));                // row_ror:8
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+__device__ __forceinline__ float groups_sum(float v) {
+  v += dppf<0x128>(v);
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+}
+
+// Dims of a lane in the score phase (DL = D/8 of them): for DL = 8 the two
+// float4 runs 4*sub.. and 32+4*sub.. (a wave instruction then reads whole
+// 128-byte halves of 8 key rows), for DL = 4 the run 4*sub.., otherwise
+// DL*sub + x.  `p` is the row start; every load is unconditional.
+template <int DL>
+__device__ __forceinline__ void load_lane_dims(const float *p, int sub,
+                                               float (&x)[8]) {
+  if constexpr (DL == 8) {
+    const float4 a = *reinterpret_cast<const float4 *>(p + 4 * sub);
+    const float4 c = *reinterpret_cast<const float4 *>(p + 32 + 4 * sub);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+  } else if constexpr (DL == 4) {
+    const float4 a = *reinterpret_cast<const float4 *>(p + 4 * sub);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+#pragma unroll
+    for (int i = 4; i < 8; ++i) x[i] = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = i < DL ? p[DL * sub + i] : 0.f;
+  }
+}
+
+template <int SQP, int DL>
+__global__ __launch_bounds__(kWave) void attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc,
-    const float *__restrict__ vc, int S, int H, int Hkv, int D, int cap,
+    const float *__restrict__ vc, int S, int H, int Hkv, int cap,
     int64_t seq_stride, const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
-    float *__restrict__ part) {
-  constexpr int kGroups = 32;
-  __shared__ float s_m[kGroups][SQ], s_l[kGroups][SQ], s_f[kGroups][SQ];
-  __shared__ float s_acc[kGroups][SQ][kMaxD];
-  __shared__ float s_M[SQ];
+    float qscale, float *__restrict__ part) {
+  constexpr int D = DL * 8;
+  constexpr int NQ4 = D / 4, KPI = kWave / NQ4;   // PV: key rows per wave op
+  constexpr int TPV = (kChunk + KPI - 1) / KPI;   // PV keys per lane
+  // chunk probabilities [kChunk][SQP], later the PV partials [KPI][SQP][D]
+  __shared__ float4 s_buf4[(KPI * SQP * D > kChunk * SQP ? KPI * SQP * D
+                                                         : kChunk * SQP) / 4];
+  __shared__ float s_alpha[SQP];
+  float *s_buf = reinterpret_cast<float *>(s_buf4);
   const int sp = blockIdx.x, h = blockIdx.y;
   const int b = blockIdx.z / nqb, qb = blockIdx.z % nqb;
   if (active && !active[b]) return;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int g = w * 8 + (lane >> 3), sub = lane & 7;
+  const int lane = threadIdx.x, g = lane >> 3, sub = lane & 7;
+  const int g8 = sub ^ (((sub >> 2) & 1) * 3);
+  const int myq = g8 & (SQP - 1);
+  const bool uniq = g8 < SQP;                 // one lane per (group, query)
   const int q0 = qb * kMaxQ;
-  const int nq = min(SQ, S - q0);
+  const int nq = min(SQP, S - q0);
   const int E = H * D;
   const int hk = h / (H / Hkv);
-  const int pos0 = base[b] + off + q0;         // position of query q0
-  const int kend_all = min(pos0 + nq, cap);    // keys [0, kend_all) visible
+  const int pos0 = base[b] + off + q0;
+  const int kend_all = min(pos0 + nq, cap);
   const int ks = sp * kps;
   const int kend = min(ks + kps, kend_all);
-  const float scale = sqrtf((float)D);
-  const int dl = D / 8;                        // dims per lane (<= 8)
   const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
   const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
+  const int r = min(lane / NQ4, KPI - 1), dq = lane % NQ4;
+  const bool pv_lane = lane < KPI * NQ4;
 
-  // the block's queries, read by every lane group through LDS broadcasts
-  __shared__ float s_q[SQ][kMaxD];
-  for (int t = threadIdx.x; t < SQ * kMaxD; t += blockDim.x) {
-    const int i = t / kMaxD, dd = t % kMaxD;
-    s_q[i][dd] = (i < nq && dd < D) ? q[((int64_t)b * S + q0 + i) * E + h * D + dd] : 0.f;
-  }
-  __syncthreads();
-  float m[SQ], l[SQ], acc[SQ][8];
+  float qv[SQP][8];
 #pragma unroll
-  for (int i = 0; i < SQ; ++i) {
-    m[i] = -INFINITY; l[i] = 0.f;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) acc[i][x] = 0.f;
+  for (int p = 0; p < SQP; ++p) {
+    const int qi = p ^ myq;
+    load_lane_dims<DL>(q + ((int64_t)b * S + q0 + min(qi, nq - 1)) * E + h * D,
+                       sub, qv[p]);
   }
+  float acc[SQP][4];
+#pragma unroll
+  for (int i = 0; i < SQP; ++i)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[i][x] = 0.f;
+  float m_run = -INFINITY, l_loc = 0.f;
 
-  struct Blk { float k[kKeysPerGroup][8], v[kKeysPerGroup][8]; };
-  auto load = [&](int j0, Blk &bk) {
+  for (int c0 = ks; c0 < kend; c0 += kChunk) {
+    // every K and V row of the chunk is requested up front; rows past the
+    // split end re-read the last valid row and are masked
+    float kr[4][8];
+    float4 vv[TPV];
 #pragma unroll
-    for (int e = 0; e < kKeysPerGroup; ++e) {
-      const int j = j0 + e;
-      const bool ok = j < kend;
-      if (dl == 8) {
-        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0, v0 = k0, v1 = k0;
-        if (ok) {
-          const float4 *kp = reinterpret_cast<const float4 *>(kb + (int64_t)j * D + sub * 8);
-          const float4 *vp = reinterpret_cast<const float4 *>(vb + (int64_t)j * D + sub * 8);
-          k0 = kp[0]; k1 = kp[1]; v0 = vp[0]; v1 = vp[1];
-        }
-        bk.k[e][0] = k0.x; bk.k[e][1] = k0.y; bk.k[e][2] = k0.z; bk.k[e][3] = k0.w;
-        bk.k[e][4] = k1.x; bk.k[e][5] = k1.y; bk.k[e][6] = k1.z; bk.k[e][7] = k1.w;
-        bk.v[e][0] = v0.x; bk.v[e][1] = v0.y; bk.v[e][2] = v0.z; bk.v[e][3] = v0.w;
-        bk.v[e][4] = v1.x; bk.v[e][5] = v1.y; bk.v[e][6] = v1.z; bk.v[e][7] = v1.w;
+    for (int t = 0; t < 4; ++t)
+      load_lane_dims<DL>(kb + (int64_t)min(c0 + g + 8 * t, kend - 1) * D, sub,
+                         kr[t]);
+#pragma unroll
+    for (int t = 0; t < TPV; ++t)
+      vv[t] = *reinterpret_cast<const float4 *>(
+          vb + (int64_t)min(c0 + r + KPI * t, kend - 1) * D + dq * 4);
+    // scores of this lane's query for keys c0 + g + 8t
+    float sc[4], cm = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float pr[SQP];
+#pragma unroll
+      for (int p = 0; p < SQP; ++p) {
+        float s = 0.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x)
+          if (x < DL) s += qv[p][x] * kr[t][x];
+        pr[p] = s;
+      }
+      // bit 2 of g8 (partner sub ^ 7)
+      if constexpr (SQP == 8) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) pr[p] += dppf<0x141>(pr[p + 4]);
       } else {
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          bk.k[e][x] = (ok && x < dl) ? kb[(int64_t)j * D + sub * dl + x] : 0.f;
-          bk.v[e][x] = (ok && x < dl) ? vb[(int64_t)j * D + sub * dl + x] : 0.f;
+        for (int p = 0; p < SQP; ++p) pr[p] += dppf<0x141>(pr[p]);
+      }
+      // bit 1 (partner sub ^ 2)
+      if constexpr (SQP >= 4) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) pr[p] += dppf<0x4E>(pr[p + 2]);
+      } else {
+#pragma unroll
+        for (int p = 0; p < SQP; ++p) pr[p] += dppf<0x4E>(pr[p]);
+      }
+      // bit 0 (partner sub ^ 1)
+      if constexpr (SQP >= 2) pr[0] += dppf<0xB1>(pr[1]);
+      else pr[0] += dppf<0xB1>(pr[0]);
+      const int j = c0 + g + 8 * t;
+      const bool valid = myq < nq && j < kend && j <= pos0 + myq;
+      sc[t] = valid ? pr[0] * qscale : -INFINITY;
+      cm = fmaxf(cm, sc[t]);
+    }
+    cm = groups_max(cm);
+    const float mn = fmaxf(m_run, cm);
+    const float ms = (mn == -INFINITY) ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - ms);   // 0 at start
+    m_run = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float p = __builtin_amdgcn_exp2f(sc[t] - ms);    // 0 if masked
+      ps += p;
+      if (uniq) s_buf[(g + 8 * t) * SQP + myq] = p;
+    }
+    l_loc = l_loc * alpha + ps;
+    if (uniq && g == 0) s_alpha[myq] = alpha;
+    __syncthreads();
+    float al[SQP];
+#pragma unroll
+    for (int i = 0; i < SQP; ++i) al[i] = s_alpha[i];
+#pragma unroll
+    for (int i = 0; i < SQP; ++i)
+#pragma unroll
+      for (int x = 0; x < 4; ++x) acc[i][x] *= al[i];
+#pragma unroll
+    for (int t = 0; t < TPV; ++t) {
+      // rows past the chunk (KPI not dividing it) read a masked row's zeros
+      const int jj = min(r + KPI * t, kChunk - 1);
+      const float m = (r + KPI * t < kChunk) ? 1.f : 0.f;
+      float pk[SQP];
+      const float *pp = s_buf + jj * SQP;
+      if constexpr (SQP >= 4) {
+#pragma unroll
+        for (int i = 0; i < SQP; i += 4) {
+          const float4 w = *reinterpret_cast<const float4 *>(pp + i);
+          pk[i] = w.x * m; pk[i + 1] = w.y * m; pk[i + 2] = w.z * m;
+          pk[i + 3] = w.w * m;
         }
+      } else {
+#pragma unroll
+        for (int i = 0; i < SQP; ++i) pk[i] = pp[i] * m;
+      }
+#pragma unroll
+      for (int i = 0; i < SQP; ++i) {
+        acc[i][0] += pk[i] * vv[t].x; acc[i][1] += pk[i] * vv[t].y;
+        acc[i][2] += pk[i] * vv[t].z; acc[i][3] += pk[i] * vv[t].w;
       }
     }
-  };
-  // online softmax over one block of 4 keys starting at j0
-  auto consume = [&](int j0, const Blk &bk) {
-#pragma unroll
-    for (int i = 0; i < SQ; ++i) {
-      float qv[8];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) qv[x] = x < dl ? s_q[i][sub * dl + x] : 0.f;
-      float sc[kKeysPerGroup];
-      float mb = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < kKeysPerGroup; ++e) {
-        float dot = 0.f;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) dot += qv[x] * bk.k[e][x];
-        dot = group8_sum(dot);
-        const int j = j0 + e;
-        const bool valid = i < nq && j < kend && j <= pos0 + i;   // causal
-        sc[e] = valid ? dot / scale : -INFINITY;
-        mb = fmaxf(mb, sc[e]);
-      }
-      if (mb == -INFINITY) continue;
-      const float mn = fmaxf(m[i], mb);
-      const float a = (m[i] == -INFINITY) ? 0.f : expf(m[i] - mn);
-      l[i] *= a;
-#pragma unroll
-      for (int x = 0; x < 8; ++x) acc[i][x] *= a;
-      m[i] = mn;
-#pragma unroll
-      for (int e = 0; e < kKeysPerGroup; ++e) {
-        const float p = expf(sc[e] - mn);        // 0 for masked keys
-        l[i] += p;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) acc[i][x] += p * bk.v[e][x];
-      }
-    }
-  };
-  // group g takes blocks g, g+32, ... of the split; the next block's loads
-  // are in flight while the current one is scored
-  constexpr int kStride = kGroups * kKeysPerGroup;
-  Blk ba, bb;
-  int j0 = ks + g * kKeysPerGroup;
-  if (j0 < kend) load(j0, ba);
-  while (j0 < kend) {
-    if (j0 + kStride < kend) load(j0 + kStride, bb);
-    consume(j0, ba);
-    j0 += kStride;
-    if (j0 >= kend) break;
-    if (j0 + kStride < kend) load(j0 + kStride, ba);
-    consume(j0, bb);
-    j0 += kStride;
+    __syncthreads();
   }
+  const float l = groups_sum(l_loc);
+  if (pv_lane) {
 #pragma unroll
-  for (int i = 0; i < SQ; ++i) {
-    if (sub == 0) { s_m[g][i] = m[i]; s_l[g][i] = l[i]; }
-#pragma unroll
-    for (int x = 0; x < 8; ++x)
-      if (x < dl) s_acc[g][i][sub * dl + x] = acc[i][x];
+    for (int i = 0; i < SQP; ++i)
+      *reinterpret_cast<float4 *>(s_buf + (r * SQP + i) * D + dq * 4) =
+          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
   }
   __syncthreads();
-  // merge the 32 groups: per query the common max, per (group, query) the
-  // rescale factor, then per (query, dim) the weighted sums
-  if (threadIdx.x < nq) {
-    float mn = -INFINITY;
-    for (int gg = 0; gg < kGroups; ++gg) mn = fmaxf(mn, s_m[gg][threadIdx.x]);
-    s_M[threadIdx.x] = mn;
+  const int64_t row0 = (int64_t)b * S + q0;
+  if (uniq && g == 0 && myq < nq) {
+    float *pp = part + (((row0 + myq) * H + h) * nsplit + sp) * (D + 2);
+    pp[0] = m_run;
+    pp[1] = l;
   }
-  __syncthreads();
-  for (int t = threadIdx.x; t < kGroups * nq; t += blockDim.x) {
-    const int gg = t / nq, i = t % nq;
-    const float mg = s_m[gg][i];
-    s_f[gg][i] = (mg == -INFINITY) ? 0.f : expf(mg - s_M[i]);
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < nq * D; t += blockDim.x) {
+  for (int t = lane; t < nq * D; t += kWave) {
     const int i = t / D, dd = t % D;
-    float ls = 0.f, as = 0.f;
-    for (int gg = 0; gg < kGroups; ++gg) {
-      const float f = s_f[gg][i];
-      ls += s_l[gg][i] * f;
-      as += s_acc[gg][i][dd] * f;
-    }
-    const int64_t row = (int64_t)b * S + q0 + i;
-    const int64_t pi = (row * H + h) * nsplit + sp;
-    float *pp = part + pi * (D + 2);
-    if (dd == 0) { pp[0] = s_M[i]; pp[1] = ls; }
-    pp[2 + dd] = as;
+    float s = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < KPI; ++rr) s += s_buf[(rr * SQP + i) * D + dd];
+    part[(((row0 + i) * H + h) * nsplit + sp) * (D + 2) + 2 + dd] = s;
   }
 }
 
 // Merges the splits of every head of one row (b, s), writes the context row
 // [H*D] and, when requested, its int8 digits for the output projection
-// (same rule as act_quant_kernel).
-__global__ __launch_bounds__(256) void attn_combine_kernel(
+// (same rule as act_quant_kernel).  The per-split weights
+// 2^(m_s - M) / L are formed once per head in LDS, then every output element
+// is a weighted sum over the splits.
+constexpr int kCombineThreads = 1024;
+constexpr int kMaxHeadSplits = 2048;         // H * nsplit bound
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(
     const float *__restrict__ part, int S, int H, int D, int nsplit,
     const int32_t *__restrict__ active, float *__restrict__ out,
     int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
   __shared__ float srow[4096];
-  __shared__ float sred[4];
+  __shared__ float s_m[kMaxHeadSplits], s_l[kMaxHeadSplits];
+  __shared__ float sred[kCombineThreads / kWave];
   const int64_t row = blockIdx.x;
   if (active && !active[row / S]) return;
-  const int E = H * D;
+  const int E = H * D, HS = H * nsplit;
+  const float *prow = part + row * HS * (D + 2);
+  for (int t = threadIdx.x; t < HS; t += blockDim.x) {
+    s_m[t] = prow[(int64_t)t * (D + 2)];
+    s_l[t] = prow[(int64_t)t * (D + 2) + 1];
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < H; h += blockDim.x) {
+    float mn = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) mn = fmaxf(mn, s_m[h * nsplit + sp]);
+    float ls = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float ms = s_m[h * nsplit + sp];
+      const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mn);
+      s_m[h * nsplit + sp] = f;
+      ls += s_l[h * nsplit + sp] * f;
+    }
+    const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) s_m[h * nsplit + sp] *= inv;
+  }
+  __syncthreads();
   float mx = 0.f;
   for (int t = threadIdx.x; t < E; t += blockDim.x) {
     const int h = t / D, dd = t % D;
-    const float *pp = part + (row * H + h) * nsplit * (D + 2);
-    float mn = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) mn = fmaxf(mn, pp[sp * (D + 2)]);
-    float ls = 0.f, as = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float ms = pp[sp * (D + 2)];
-      const float f = (ms == -INFINITY) ? 0.f : expf(ms - mn);
-      ls += pp[sp * (D + 2) + 1] * f;
-      as += pp[sp * (D + 2) + 2 + dd] * f;
-    }
-    const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-    const float v = as * inv;
+    const float *pp = prow + (int64_t)h * nsplit * (D + 2) + 2 + dd;
+    const float *w = s_m + h * nsplit;
+    float v = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) v += w[sp] * pp[(int64_t)sp * (D + 2)];
     out[row * E + t] = v;
     if (limbs) { srow[t] = v; mx = fmaxf(mx, fabsf(v)); }
   }
@@ -305,7 +377,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
   if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+  mx = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCombineThreads / kWave; ++w) mx = fmaxf(mx, sred[w]);
   const int e = digit_exponent(mx);
   if (threadIdx.x == 0) rexp[row] = e;
   typedef int v4i __attribute__((ext_vector_type(4)));
@@ -454,17 +528,20 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
   NNHIP_CHECK(hipGetLastError());
 }
 
-// Splits of the key range: enough (sequence, head, query block, split)
-// workgroups to fill the GPU about 3 times over, each split a multiple of
-// 128 keys.
+int g_attn_waves = 4096;
+
+// Splits of the key range: about g_attn_waves waves over the whole launch
+// (4 per SIMD by default), each split a whole number of 32-key chunks.
 static int attention_splits(int B, int S, int H, int max_keys, int *kps) {
   const int nqb = (S + kMaxQ - 1) / kMaxQ;
   const int units = std::max(1, B * H * nqb);
-  const int max_split = std::max(1, (std::max(max_keys, 1) + kKeysPerSplit - 1) / kKeysPerSplit);
-  int ns = std::min(max_split, std::max(1, (768 + units - 1) / units));
-  int k = (std::max(max_keys, 1) + ns - 1) / ns;
-  k = (k + kKeysPerSplit - 1) / kKeysPerSplit * kKeysPerSplit;
-  ns = (std::max(max_keys, 1) + k - 1) / k;
+  const int keys = std::max(max_keys, 1);
+  const int max_split = (keys + kChunk - 1) / kChunk;
+  int ns = std::min(max_split, std::max(1, (g_attn_waves + units - 1) / units));
+  ns = std::max(1, std::min(ns, kMaxHeadSplits / std::max(H, 1)));
+  int k = (keys + ns - 1) / ns;
+  k = (k + kChunk - 1) / kChunk * kChunk;
+  ns = (keys + k - 1) / k;
   if (kps) *kps = k;
   return ns;
 }
@@ -493,24 +570,31 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
                 kErrArg, "attention: partial buffer too small");
   const int nqb = (S + kMaxQ - 1) / kMaxQ;
   const int sq = S < kMaxQ ? S : kMaxQ;
+  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
   dim3 grid(nsplit, H, B * nqb);
-#define NNHIP_ATTN(SQV)                                                      \
-  hipLaunchKernelGGL((attn_kernel<SQV>), grid, dim3(256), 0, st, q, kc, vc, S, \
-                     H, Hkv, D, cap, seq_stride, base, off, active, nsplit,    \
-                     nqb, kps, part)
-  switch (sq) {
-    case 1: NNHIP_ATTN(1); break;
-    case 2: NNHIP_ATTN(2); break;
-    case 3: NNHIP_ATTN(3); break;
-    case 4: NNHIP_ATTN(4); break;
-    case 5: NNHIP_ATTN(5); break;
-    case 6: NNHIP_ATTN(6); break;
-    case 7: NNHIP_ATTN(7); break;
-    default: NNHIP_ATTN(8); break;
+#define NNHIP_ATTN(SQP, DL)                                                   \
+  hipLaunchKernelGGL((attn_kernel<SQP, DL>), grid, dim3(kWave), 0, st, q, kc, \
+                     vc, S, H, Hkv, cap, seq_stride, base, off, active,       \
+                     nsplit, nqb, kps, qscale, part)
+#define NNHIP_ATTN_D(SQP)                                                     \
+  switch (D / 8) {                                                            \
+    case 1: NNHIP_ATTN(SQP, 1); break;                                        \
+    case 2: NNHIP_ATTN(SQP, 2); break;                                        \
+    case 3: NNHIP_ATTN(SQP, 3); break;                                        \
+    case 4: NNHIP_ATTN(SQP, 4); break;                                        \
+    case 5: NNHIP_ATTN(SQP, 5); break;                                        \
+    case 6: NNHIP_ATTN(SQP, 6); break;                                        \
+    case 7: NNHIP_ATTN(SQP, 7); break;                                        \
+    default: NNHIP_ATTN(SQP, 8); break;                                       \
   }
+  if (sq == 1) NNHIP_ATTN_D(1)
+  else if (sq == 2) NNHIP_ATTN_D(2)
+  else if (sq <= 4) NNHIP_ATTN_D(4)
+  else NNHIP_ATTN_D(8)
+#undef NNHIP_ATTN_D
 #undef NNHIP_ATTN
   NNHIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S), dim3(256), 0, st, part,
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S), dim3(kCombineThreads), 0, st, part,
                      S, H, D, nsplit, active, out, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
 }

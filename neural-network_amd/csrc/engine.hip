@@ -406,7 +406,7 @@ namespace {
 struct SpecBuffers {
   DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok,
       out, n_active, vids, prompts;
-  DevBuf<float> qprob, dlog, tlog;
+  DevBuf<float> qprob, dlog, tlog, tstat;
   DevBuf<int64_t> stats;
 };
 
@@ -451,6 +451,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
   bf.dlog.alloc((size_t)B * V);
   bf.tlog.alloc((size_t)B * (k + 1) * V);
+  bf.tstat.alloc((size_t)B * (k + 1) * 4);
   bf.stats.alloc((size_t)B * 6);
   NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
   NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 4, st));
@@ -476,6 +477,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     SpecState &s = gs[g];
     s.cur = bf.cur.p + b0; s.cand = bf.cand.p + (size_t)b0 * k;
     s.qprob = bf.qprob.p ? bf.qprob.p + (size_t)b0 * k * V : nullptr;
+    s.tstat = bf.tstat.p + (size_t)b0 * (k + 1) * 4;
     s.tlen = bf.tlen.p + b0; s.dlen = bf.dlen.p + b0; s.gen = bf.gen.p + b0;
     s.cyc = bf.cyc.p + b0; s.active = bf.active.p + b0;
     s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;

@@ -173,6 +173,7 @@ __device__ inline int digit_exponent(float mx) {
 
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
+extern int g_attn_waves; // attention: waves one launch aims for
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
@@ -227,6 +228,7 @@ struct SpecState {
   int32_t *cur;        // [B] last committed token (generated.back())
   int32_t *cand;       // [B][k] draft candidates of this cycle
   float *qprob;        // [B][k][V] draft probabilities (sampled mode)
+  float *tstat;        // [B][k+1][4] verify-row statistics (accept step)
   int32_t *tlen;       // [B] target cache length
   int32_t *dlen;       // [B] draft cache length
   int32_t *gen;        // [B] tokens generated so far

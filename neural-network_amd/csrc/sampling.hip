@@ -74,20 +74,9 @@ __device__ __forceinline__ float block_sum(float v, Shared &sh) {
   return r;
 }
 
-__device__ __forceinline__ double block_sum_d(double v, Shared &sh) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh.d[threadIdx.x >> 6] = v;
-  __syncthreads();
-  double r = 0.0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) r += sh.d[w];
-  return r;
-}
-
-// exclusive prefix sum over threads in index order
-__device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh) {
+// exclusive prefix sum over threads in index order; *total = the block sum
+__device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh,
+                                                    double *total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   double incl = v;
 #pragma unroll
@@ -98,8 +87,14 @@ __device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh) {
   __syncthreads();
   if (lane == 63) sh.d[w] = incl;
   __syncthreads();
-  double pre = 0.0;
-  for (int i = 0; i < w; ++i) pre += sh.d[i];
+  double pre = 0.0, tot = 0.0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    const double x = sh.d[i];
+    pre += i < w ? x : 0.0;
+    tot += x;
+  }
+  *total = tot;
   return pre + incl - v;
 }
 
@@ -135,79 +130,107 @@ __device__ int block_argmax(const float *__restrict__ row, int V, Shared &sh) {
   return r == 0x7fffffff ? 0 : r;
 }
 
-struct RowStats { float mx, sum, fs; };
-
 // get_probs (layer.cpp:1426-1489) for T > 0 without top-k / top-p:
-// s = l / T, e = exp(s - max), p1 = e / sum (float sum), p = p1 / final_sum.
-// Writes p into sh.prow and returns the three row constants.
-__device__ RowStats row_probs(const float *__restrict__ row, int V, float T,
-                              Shared &sh) {
-  float mx = -INFINITY;
-  for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float s = row[v] / T;
-    sh.prow[la(v)] = s;
-    mx = fmaxf(mx, s);
-  }
-  mx = block_max(mx, sh);
-  float s = 0.f;
-  for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float e = expf(sh.prow[la(v)] - mx);
-    sh.prow[la(v)] = e;
-    s += e;
-  }
-  const float sum = block_sum(s, sh);
-  float f = 0.f;
-  for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float p1 = sh.prow[la(v)] / sum;
-    sh.prow[la(v)] = p1;
-    f += p1;
-  }
-  const float fs = block_sum(f, sh);
-  for (int v = threadIdx.x; v < V; v += kThreads)
-    sh.prow[la(v)] = sh.prow[la(v)] / fs;
-  __syncthreads();
-  return RowStats{mx, sum, fs};
-}
+// s = l / T, e = exp(s - max), p1 = e / sum, p = p1 / sum(p1).  The two
+// normalisations multiply by the correctly rounded reciprocals 1/sum and
+// 1/sum(p1), so p may differ from the divided value in the last place.
+// RowStats holds what recomputes p at one index (prob_at).
+struct RowStats { float mx, rsum, rfs; };
 
-// Same statistics without materialising the row.
-__device__ RowStats row_stats(const float *__restrict__ row, int V, float T,
-                              Shared &sh) {
-  float mx = -INFINITY;
-  for (int v = threadIdx.x; v < V; v += kThreads) mx = fmaxf(mx, row[v] / T);
-  mx = block_max(mx, sh);
-  float s = 0.f;
-  for (int v = threadIdx.x; v < V; v += kThreads) s += expf(row[v] / T - mx);
-  const float sum = block_sum(s, sh);
-  float f = 0.f;
-  for (int v = threadIdx.x; v < V; v += kThreads)
-    f += expf(row[v] / T - mx) / sum;
-  const float fs = block_sum(f, sh);
-  return RowStats{mx, sum, fs};
+constexpr int kPer = kMaxV / kThreads;   // row entries per thread
+
+__device__ __forceinline__ float scaled(float l, float T) {
+  return T == 1.0f ? l : l / T;
 }
 
 __device__ __forceinline__ float prob_at(const float *row, int v, float T,
                                          RowStats st) {
-  return (expf(row[v] / T - st.mx) / st.sum) / st.fs;
+  return (expf(scaled(row[v], T) - st.mx) * st.rsum) * st.rfs;
+}
+
+// The row is held in registers (entry v = tid + 1024 i); p goes to sh.prow
+// when `to_lds`, and to gout when given.
+__device__ RowStats row_pass(const float *__restrict__ row, int V, float T,
+                             Shared &sh, bool to_lds,
+                             float *__restrict__ gout) {
+  float x[kPer];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int v = threadIdx.x + i * kThreads;
+    x[i] = v < V ? scaled(row[v], T) : -INFINITY;
+    mx = fmaxf(mx, x[i]);
+  }
+  mx = block_max(mx, sh);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int v = threadIdx.x + i * kThreads;
+    x[i] = v < V ? expf(x[i] - mx) : 0.f;
+    s += x[i];
+  }
+  const float rs = 1.0f / block_sum(s, sh);
+  float f = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    x[i] = x[i] * rs;
+    f += x[i];
+  }
+  const float rf = 1.0f / block_sum(f, sh);
+  if (to_lds || gout) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int v = threadIdx.x + i * kThreads;
+      if (v < V) {
+        const float p = x[i] * rf;
+        if (to_lds) sh.prow[la(v)] = p;
+        if (gout) gout[v] = p;
+      }
+    }
+    __syncthreads();
+  }
+  return RowStats{mx, rs, rf};
+}
+
+__device__ __forceinline__ RowStats row_probs(const float *__restrict__ row,
+                                              int V, float T, Shared &sh,
+                                              float *__restrict__ gout = nullptr) {
+  return row_pass(row, V, T, sh, true, gout);
+}
+
+__device__ __forceinline__ RowStats row_stats(const float *__restrict__ row,
+                                              int V, float T, Shared &sh) {
+  return row_pass(row, V, T, sh, false, nullptr);
+}
+
+// sh.prow = p recomputed from a row's statistics
+__device__ void fill_probs(const float *__restrict__ row, int V, float T,
+                           RowStats st, Shared &sh) {
+  for (int v = threadIdx.x; v < V; v += kThreads)
+    sh.prow[la(v)] = prob_at(row, v, T, st);
+  __syncthreads();
 }
 
 // sample_token (layer.cpp:1493-1498): std::discrete_distribution over
-// sh.prow widened to double -- normalise by the double sum, running sum,
-// last entry 1.0, first v with cdf[v] >= u.
+// sh.prow widened to double (weights w = p / S, S = sum p, running sum, last
+// entry 1.0): the first v whose running sum of p reaches u * S.  Each thread
+// owns a contiguous chunk; a chunk is scanned only when the crossing can lie
+// in it or before it.
 __device__ int block_sample(int V, float u, Shared &sh) {
   const int C = (V + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * C;
   const int b1 = min(b0 + C, V);
   double loc = 0.0;
   for (int v = b0; v < b1; ++v) loc += (double)sh.prow[la(v)];
-  const double S = block_sum_d(loc, sh);
-  double part = 0.0;
-  for (int v = b0; v < b1; ++v) part += (double)sh.prow[la(v)] / S;
-  double c = block_excl_scan_d(part, sh);
+  double S;
+  double c = block_excl_scan_d(loc, sh, &S);
+  const double target = (double)u * S;
   int found = 0x7fffffff;
-  const double ud = (double)u;
-  for (int v = b0; v < b1 && v < V - 1; ++v) {
-    c += (double)sh.prow[la(v)] / S;
-    if (c >= ud) { found = v; break; }
+  if (c + loc >= target - 1e-12 * S) {
+    for (int v = b0; v < b1 && v < V - 1; ++v) {
+      c += (double)sh.prow[la(v)];
+      if (c >= target) { found = v; break; }
+    }
   }
   const int r = block_min_i(found, sh);
   return r == 0x7fffffff ? V - 1 : r;
@@ -255,41 +278,59 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
   if (s.T <= 0.f) {
     tok = block_argmax(row, s.V, sh);
   } else {
-    row_probs(row, s.V, s.T, sh);
-    float *qd = s.qprob + ((int64_t)b * s.k + j) * s.V;
-    for (int v = threadIdx.x; v < s.V; v += kThreads) qd[v] = sh.prow[la(v)];
+    row_probs(row, s.V, s.T, sh, s.qprob + ((int64_t)b * s.k + j) * s.V);
     tok = block_sample(s.V, uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
   }
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
 }
 
-// Residual max(0, p - q) (layer.cpp:1611-1630) over sh.prow = p, q from
-// qrow (stored) or recomputed from draft logits; then sample it, or p when
-// the residual sums to zero (p is recomputed from tlog_row then).
+// Per verify row (b, j <= M): argmax (greedy) or the get_probs statistics
+// (sampled), for all rows of the cycle at once.  tstat[b][j] =
+// {max, 1/sum, 1/sum(p1), argmax as int bits}.
+__global__ __launch_bounds__(kThreads) void target_stats_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  __shared__ Shared sh;
+  const int j = blockIdx.x, b = blockIdx.y;
+  if (!s.active[b]) return;
+  const int M = min(s.k, s.max_new - s.gen[b]);
+  if (j > M) return;
+  const int64_t r = (int64_t)b * (s.k + 1) + j;
+  const float *row = tlogits + r * s.V;
+  float *ts = s.tstat + r * 4;
+  if (s.T <= 0.f) {
+    const int a = block_argmax(row, s.V, sh);
+    if (threadIdx.x == 0) ts[3] = __int_as_float(a);
+  } else {
+    const RowStats st = row_stats(row, s.V, s.T, sh);
+    if (threadIdx.x == 0) { ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs; }
+  }
+}
+
+// Residual max(0, p - q) (layer.cpp:1611-1630), p from the target row's
+// statistics, q from qrow (stored) or from the draft row's statistics; then
+// sample it, or p when the residual sums to zero.  The residual is sampled
+// unnormalised: the discrete distribution normalises it.
 __device__ int residual_sample(const float *__restrict__ qrow,
                                const float *__restrict__ dlog_row,
                                RowStats qst, const float *__restrict__ tlog_row,
-                               int V, float T, float u, Shared &sh) {
+                               RowStats tst, int V, float T, float u,
+                               Shared &sh) {
   float loc = 0.f;
   for (int v = threadIdx.x; v < V; v += kThreads) {
+    const float p = prob_at(tlog_row, v, T, tst);
     const float q = qrow ? qrow[v] : prob_at(dlog_row, v, T, qst);
-    const float r = fmaxf(0.0f, sh.prow[la(v)] - q);
+    const float r = fmaxf(0.0f, p - q);
     sh.prow[la(v)] = r;
     loc += r;
   }
   const float sr = block_sum(loc, sh);
-  if (sr <= 0.0f) {
-    row_probs(tlog_row, V, T, sh);
-  } else {
-    for (int v = threadIdx.x; v < V; v += kThreads)
-      sh.prow[la(v)] = sh.prow[la(v)] / sr;
-    __syncthreads();
-  }
+  if (sr <= 0.0f) fill_probs(tlog_row, V, T, tst, sh);
   return block_sample(V, u, sh);
 }
 
-// Accept / reject, resample or bonus, rollback (layer.cpp:1581-1655).
-// tlogits: [B][k+1][V], row i = verify position i.
+// Accept / reject, resample or bonus, rollback (layer.cpp:1581-1655), from
+// the verify rows' statistics (target_stats_kernel).  tlogits: [B][k+1][V],
+// row i = verify position i.
 __global__ __launch_bounds__(kThreads) void accept_kernel(
     SpecState s, const float *__restrict__ tlogits) {
   __shared__ Shared sh;
@@ -305,15 +346,21 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   int nout = s.P + gen0;
   int rej = -1;
   int64_t ties = 0;
+  auto stats_of = [&](int j) {
+    const float *ts = s.tstat + ((int64_t)b * (k + 1) + j) * 4;
+    return RowStats{ts[0], ts[1], ts[2]};
+  };
+  auto argmax_of = [&](int j) {
+    return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * 4 + 3]);
+  };
   for (int j = 0; j < M; ++j) {
     const float *row = tlogits + ((int64_t)b * (k + 1) + j) * V;
     const int c = s.cand[b * k + j];
     bool acc;
     if (greedy) {
-      acc = c == block_argmax(row, V, sh);
+      acc = c == argmax_of(j);
     } else {
-      row_probs(row, V, s.T, sh);
-      const float pc = sh.prow[la(c)];
+      const float pc = prob_at(row, c, s.T, stats_of(j));
       const float qc = s.qprob[((int64_t)b * k + j) * V + c];
       const float r = uniform(s.seed, seq, cyc, k + j);
       acc = __fmul_rn(r, qc) < pc;
@@ -329,15 +376,21 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   if (rej >= 0) {
     const float *row = tlogits + ((int64_t)b * (k + 1) + rej) * V;
     if (greedy) {
-      tok = block_argmax(row, V, sh);
+      tok = argmax_of(rej);
     } else {
       tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, nullptr,
-                            RowStats{0.f, 1.f, 1.f}, row, V, s.T, u, sh);
+                            RowStats{0.f, 1.f, 1.f}, row, stats_of(rej), V,
+                            s.T, u, sh);
     }
     catch_tok = tok;
   } else if (gen < s.max_new) {
     const float *row = tlogits + ((int64_t)b * (k + 1) + M) * V;
-    tok = draw_row(row, V, s.T, u, sh);
+    if (greedy) {
+      tok = argmax_of(M);
+    } else {
+      fill_probs(row, V, s.T, stats_of(M), sh);
+      tok = block_sample(V, u, sh);
+    }
     catch_tok = s.cand[b * k + M - 1];
   }
   if (threadIdx.x == 0) {
@@ -397,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void accept_bench_kernel(
   __shared__ Shared sh;
   const int b = blockIdx.x;
   int rej = -1;
-  RowStats qst{0.f, 1.f, 1.f};
+  RowStats qst{0.f, 1.f, 1.f}, tst{0.f, 1.f, 1.f};
   for (int j = 0; j < k; ++j) {
     const float *tr = tlog + ((int64_t)b * k + j) * V;
     const float *dr = dlog + ((int64_t)b * k + j) * V;
@@ -407,8 +460,8 @@ __global__ __launch_bounds__(kThreads) void accept_bench_kernel(
       acc = c == block_argmax(tr, V, sh);
     } else {
       qst = row_stats(dr, V, T, sh);
-      row_probs(tr, V, T, sh);
-      const float pc = sh.prow[la(c)];
+      tst = row_stats(tr, V, T, sh);
+      const float pc = prob_at(tr, c, T, tst);
       const float qc = prob_at(dr, c, T, qst);
       acc = __fmul_rn(u_acc[b * k + j], qc) < pc;
     }
@@ -421,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void accept_bench_kernel(
       tok = block_argmax(tr, V, sh);
     else
       tok = residual_sample(nullptr, dlog + ((int64_t)b * k + rej) * V, qst,
-                            tr, V, T, u_res[b], sh);
+                            tr, tst, V, T, u_res[b], sh);
   }
   if (threadIdx.x == 0) {
     n_acc[b] = rej < 0 ? k : rej;
@@ -441,10 +494,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(
   if (T <= 0.f) {
     t = block_argmax(row, V, sh);
   } else {
-    row_probs(row, V, T, sh);
-    if (probs)
-      for (int v = threadIdx.x; v < V; v += kThreads)
-        probs[(int64_t)b * V + v] = sh.prow[la(v)];
+    row_probs(row, V, T, sh, probs ? probs + (int64_t)b * V : nullptr);
     t = block_sample(V, u[b], sh);
   }
   if (threadIdx.x == 0) tok[b] = t;
@@ -469,6 +519,10 @@ void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
 }
 
 void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
+  NNHIP_REQUIRE(s.tstat != nullptr, kErrArg, "accept: no row statistics");
+  hipLaunchKernelGGL(target_stats_kernel, dim3(s.k + 1, s.B), dim3(kThreads),
+                     0, st, s, tlogits);
+  NNHIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
                      tlogits);
   NNHIP_CHECK(hipGetLastError());
