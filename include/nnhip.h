@@ -175,10 +175,23 @@ int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
                       int8_t *codes, float *scales);
 /* QuantizedDense::forward (quantization.cpp:127-147): y [rows][N] =
  * x [rows][K] . (codes * scales)^T + bias.  path: 0 auto, 1 fp32 GEMV,
- * 2 int8-digit MFMA GEMM (K % 128 == 0, N % 64 == 0). */
+ * 2 int8-digit MFMA GEMM (K % 128 == 0, N % 64 == 0), 3 MFMA GEMM with the
+ * digits formed in LDS from x, 4 the same GEMM fed with digit planes
+ * (3 and 4: K in {128, 256, 512, 1024}, N % 32 == 0). */
 int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
                        const int8_t *codes, const float *scales,
                        const float *bias, int N, float *y, int path);
+/* LayerNorm (layer.cpp:242-261) of h [rows][K] followed by
+ * QuantizedDense::forward (quantization.cpp:127-147), the pair
+ * TransformerDecoderLayer::forward runs at norm1 -> ffn and norm2 -> the next
+ * layer (layer.cpp:1098-1113): y = LN(h) . W^T + b,
+ * and LN(h) into ln_out when it is not NULL.  K in {128, 256, 512, 1024},
+ * N % 32 == 0. */
+int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
+                                 int K, const float *gamma, const float *beta,
+                                 float *ln_out, const int8_t *codes,
+                                 const float *scales, const float *bias, int N,
+                                 float *y);
 /* Dense::forward (layer.cpp:162-171) with w [N][K] fp32 (transposed). */
 int nnhip_linear_f32(nnhip_ctx *ctx, const float *x, int rows, int K,
                      const float *w, const float *bias, int N, float *y);
@@ -233,7 +246,9 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
 int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
                             float temperature, int iters, int nbuf, float *ms,
                             int32_t *n_accept);
-/* path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included). */
+/* path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included),
+ * 3 = LDS GEMM digitising fp32 rows, 4 = LDS GEMM over digit planes (their
+ * digit split included), 5 = LDS GEMM with LayerNorm in its prologue. */
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms);
 

@@ -383,7 +383,22 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
     bool mfma = path == 2 || (path == 0 && rows >= 16 && mfma_ok);
     NNHIP_REQUIRE(!(path == 2 && !mfma_ok), nnhip::kErrArg,
                   "MFMA path needs K % 128 == 0 and N % 64 == 0");
-    if (mfma) {
+    NNHIP_REQUIRE(path >= 0 && path <= 4, nnhip::kErrArg, "unknown path");
+    if (path == 3 || path == 4) {
+      NNHIP_REQUIRE(nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
+                    "LDS GEMM needs K in {128, 256, 512, 1024} and N % 32 == 0");
+      LimbScratch ls;
+      ls.ensure(rows, K);
+      nnhip::DevBuf<int8_t> sw((size_t)N * K);
+      nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
+      if (path == 4)
+        nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
+      nnhip::launch_gemm_lds(st, path == 4 ? nnhip::kAFromDigits : nnhip::kAFromRows,
+                             ls.limbs.p, ls.mpad, ls.rexp.p, x, K, nullptr,
+                             nullptr, nullptr, 0, rows, K, N, sw.p, scales,
+                             bias, nullptr, 0, y, N, nnhip::kEpiBias);
+      NNHIP_CHECK(hipStreamSynchronize(st));
+    } else if (mfma) {
       LimbScratch ls;
       ls.ensure(rows, K);
       nnhip::DevBuf<int8_t> sw((size_t)N * K);
@@ -397,6 +412,26 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
       nnhip::launch_gemv(st, x, K, rows, K, N, codes, nullptr, scales, bias,
                          nullptr, 0, y, N, nnhip::kEpiBias);
     }
+  });
+}
+
+int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
+                                 int K, const float *gamma, const float *beta,
+                                 float *ln_out, const int8_t *codes,
+                                 const float *scales, const float *bias, int N,
+                                 float *y) {
+  return guard([&] {
+    REQ(ctx && h && gamma && beta && codes && scales && bias && y && rows > 0,
+        "nnhip_layernorm_linear_w8a32: bad argument");
+    NNHIP_REQUIRE(nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
+                  "fused LayerNorm GEMM needs K in {128, 256, 512, 1024} and N % 32 == 0");
+    hipStream_t st = ctx->c.stream;
+    nnhip::DevBuf<int8_t> sw((size_t)N * K);
+    nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
+    nnhip::launch_gemm_lds(st, nnhip::kAFromLayerNorm, nullptr, 0, nullptr, h,
+                           K, gamma, beta, ln_out, K, rows, K, N, sw.p, scales,
+                           bias, nullptr, 0, y, N, nnhip::kEpiBias);
+    NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }
 

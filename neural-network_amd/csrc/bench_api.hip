@@ -110,7 +110,9 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
 }
 
 // W8A32 Linear: rows x K activations N(0, 1) times an int8 [N][K] weight.
-// path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included).
+// path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included),
+// 3 = LDS GEMM from fp32 rows, 4 = LDS GEMM over digit planes (digit split
+// included), 5 = LDS GEMM with LayerNorm (gamma 1, beta 0) in its prologue.
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms) {
   return guard([&] {
@@ -126,7 +128,7 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
       W[i].alloc((size_t)N * K); S[i].alloc(N);
       nnhip::launch_init_normal(st, wf.p, 1, N * K, 0, 1, 20 + i, 0, 0.02f, 0);
       nnhip::launch_quantize_w8(st, wf.p, N, K, W[i].p, S[i].p);
-      if (path == 2) {
+      if (path >= 2) {
         WS[i].alloc((size_t)N * K);
         nnhip::launch_swizzle_rows(st, W[i].p, N, K, WS[i].p, false);
       }
@@ -134,9 +136,22 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     const int mpad = (rows + 63) / 64 * 64;
     nnhip::DevBuf<int8_t> limbs((size_t)3 * mpad * K);
     nnhip::DevBuf<int> rexp(mpad);
+    nnhip::DevBuf<float> g1(K), b0(K);
+    nnhip::launch_fill(st, g1.p, K, 1.f);
+    nnhip::launch_fill(st, b0.p, K, 0.f);
+    NNHIP_REQUIRE(path <= 2 || nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
+                  "nnhip_bench_linear: shape not supported by the LDS GEMM");
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      if (path == 2) {
+      if (path >= 3) {
+        if (path == 4)
+          nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
+        const int mode = path == 3 ? nnhip::kAFromRows
+                         : path == 4 ? nnhip::kAFromDigits : nnhip::kAFromLayerNorm;
+        nnhip::launch_gemm_lds(st, mode, limbs.p, mpad, rexp.p, x.p, K, g1.p,
+                               b0.p, nullptr, 0, rows, K, N, WS[j].p, S[j].p,
+                               b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
+      } else if (path == 2) {
         nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
         nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, WS[j].p,
                                 S[j].p, b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);

@@ -11,6 +11,8 @@ namespace nnhip {
 namespace {
 
 constexpr int kLimbMinRows = 16;
+constexpr int64_t kFusedNormMaxBlocks = 768;
+constexpr int kLdsQkvMinRows = 64;
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
@@ -302,6 +304,65 @@ bool Model::use_limbs(const Linear &ln, int rows) const {
          ln.N % 64 == 0;
 }
 
+// Where the LDS-resident GEMM is used (measured per call site on the
+// batch-32 decode shapes): the lm head (its many column blocks amortise the
+// digit tile), and the q/k/v projection of tall inputs (>= 64 rows), where
+// folding the preceding LayerNorm into the prologue saves a launch.  The
+// O, gate/up and down projections and short q/k/v inputs run faster as
+// separate LayerNorm / digit kernels plus the digit-plane GEMM.
+bool Model::use_lds(const Linear &ln, int rows) const {
+  if (!(ln.quant && ln.qs.p && rows >= kLimbMinRows &&
+        gemm_lds_supports(rows, ln.K, ln.N)))
+    return false;
+  if (&ln == &lm) return true;
+  for (const LayerW &ly : layers)
+    if (&ln == &ly.qkv) return rows >= kLdsQkvMinRows;
+  return false;
+}
+
+void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
+                      const PendingNorm *pn, int rows, bool limbs_ready,
+                      const float *resid, int64_t ldr, float *y, int64_t ldy,
+                      int epi, const RopeArgs *ra) {
+  hipStream_t st = ctx->lane(g);
+  Workspace &ws = this->ws(g);
+  if (use_lds(ln, rows)) {
+    // Each column block of the fused GEMM normalises and digitises its rows
+    // again; past a few hundred blocks one LayerNorm launch writing digit
+    // planes costs less.
+    if (pn && pn->ldh == ln.K &&
+        gemm_lds_workgroups(rows, ln.K, ln.N) > kFusedNormMaxBlocks) {
+      launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b,
+                       pn->out ? pn->out : ws.x.p, ws.limbs.p, ws.mpad,
+                       ws.rexp.p);
+      launch_gemm_lds(st, kAFromDigits, ws.limbs.p, ws.mpad, ws.rexp.p,
+                      nullptr, 0, nullptr, nullptr, nullptr, 0, rows, ln.K,
+                      ln.N, ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi,
+                      ra);
+      return;
+    }
+    const int mode = pn ? kAFromLayerNorm
+                        : (limbs_ready ? kAFromDigits : kAFromRows);
+    launch_gemm_lds(st, mode, ws.limbs.p, ws.mpad, ws.rexp.p,
+                    pn ? pn->h : x, pn ? pn->ldh : ldx, pn ? pn->g : nullptr,
+                    pn ? pn->b : nullptr, pn ? pn->out : nullptr,
+                    pn ? pn->ldo : 0, rows, ln.K, ln.N, ln.qs.p, ln.s.p,
+                    ln.b.p, resid, ldr, y, ldy, epi, ra);
+    return;
+  }
+  if (pn) {
+    // the normalisation as its own kernel, then the linear over its output
+    NNHIP_REQUIRE(pn->out && pn->ldh == ln.K && pn->ldo == ln.K, kErrArg,
+                  "linear_in: unfused LayerNorm needs contiguous rows");
+    const bool lr = use_limbs(ln, rows);
+    launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b, pn->out,
+                     lr ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+    linear(g, ln, pn->out, pn->ldo, rows, lr, resid, ldr, y, ldy, epi, ra);
+    return;
+  }
+  linear(g, ln, x, ldx, rows, limbs_ready, resid, ldr, y, ldy, epi, ra);
+}
+
 void Model::linear(int g, const Linear &ln, const float *x, int64_t ldx,
                    int rows, bool limbs_ready, const float *resid, int64_t ldr,
                    float *y, int64_t ldy, int epi, const RopeArgs *ra) {
@@ -338,7 +399,11 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   Workspace &ws = this->ws(g);
   const int32_t *bp = base ? base : ws.zeros.p;
   launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p);
-  bool limbs_ready = false;
+  // Post-norm blocks (layer.cpp:1098-1113): each LayerNorm is applied by the
+  // linear that consumes it (norm1 -> ffn gate/up, norm2 -> next q/k/v or
+  // the lm head), which also writes the normalised rows for the residual.
+  PendingNorm norm2;            // norm2 of the previous layer, if any
+  bool have_norm2 = false;
   for (int l = 0; l < L; ++l) {
     LayerW &ly = layers[l];
     float *kc = kv->k.p + (int64_t)l * kv->layer_stride() + b_off * kv->seq_stride();
@@ -348,29 +413,44 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
     ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
     ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
     ra.qrot = ws.qrot.p; ra.kc = kc; ra.vc = vc; ra.seq_stride = kv->seq_stride();
-    linear(g, ly.qkv, ws.x.p, d, R, limbs_ready, nullptr, 0, nullptr, 3 * d,
-           kEpiRope, &ra);
-    const bool lo = use_limbs(ly.o, R);
+    linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R, false,
+              nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
+    const bool lo = use_lds(ly.o, R) || use_limbs(ly.o, R);
     launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
                      kv->seq_stride(), bp, off, active, max_keys, ws.part.p,
                      ws.part_elems, ws.ctx.p, lo ? ws.limbs.p : nullptr,
                      ws.mpad, ws.rexp.p);
-    linear(g, ly.o, ws.ctx.p, d, R, lo, ws.x.p, d, ws.h.p, d, kEpiResid);
-    const bool l1 = use_limbs(ly.gu, R);
-    launch_layernorm(st, ws.h.p, R, d, ly.g1.p, ly.b1.p, ws.x1.p,
-                     l1 ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
-    linear(g, ly.gu, ws.x1.p, d, R, l1, nullptr, 0, ws.ff.p, F, kEpiSwiGLU);
-    linear(g, ly.down, ws.ff.p, F, R, false, ws.x1.p, d, ws.h.p, d, kEpiResid);
-    limbs_ready = l + 1 < L && use_limbs(layers[l + 1].qkv, R);
-    launch_layernorm(st, ws.h.p, R, d, ly.g2.p, ly.b2.p, ws.x.p,
-                     limbs_ready ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+    linear_in(g, ly.o, ws.ctx.p, d, nullptr, R, lo, ws.x.p, d, ws.h.p, d,
+              kEpiResid);
+    PendingNorm norm1;
+    norm1.h = ws.h.p; norm1.ldh = d; norm1.g = ly.g1.p; norm1.b = ly.b1.p;
+    norm1.out = ws.x1.p; norm1.ldo = d;
+    linear_in(g, ly.gu, nullptr, 0, &norm1, R, false, nullptr, 0, ws.ff.p, F,
+              kEpiSwiGLU);
+    linear_in(g, ly.down, ws.ff.p, F, nullptr, R, false, ws.x1.p, d, ws.h.p,
+              d, kEpiResid);
+    norm2.h = ws.h.p; norm2.ldh = d; norm2.g = ly.g2.p; norm2.b = ly.b2.p;
+    norm2.out = ws.x.p; norm2.ldo = d;
+    have_norm2 = true;
   }
   if (logits) {
-    if (last_only)
-      linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
-             nullptr, 0, logits, V, kEpiBias);
-    else
-      linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
+    // norm2 of the last layer feeds the lm head only
+    const int rows = last_only ? B : R;
+    if (use_lds(lm, rows)) {
+      PendingNorm pn = norm2;
+      pn.out = nullptr;
+      if (last_only) { pn.h = ws.h.p + (int64_t)(S - 1) * d; pn.ldh = (int64_t)S * d; }
+      linear_in(g, lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, V,
+                kEpiBias);
+    } else {
+      launch_layernorm(st, ws.h.p, R, d, norm2.g, norm2.b, ws.x.p, nullptr,
+                       ws.mpad, ws.rexp.p);
+      if (last_only)
+        linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
+               nullptr, 0, logits, V, kEpiBias);
+      else
+        linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
+    }
   }
   if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
 }
@@ -395,8 +475,12 @@ void KVCache::sync_len_to_device() {
 // ---------------------------------------------------------------------------
 // Speculative decoding for B independent sequences, entirely on the device
 // after the prompt upload: per cycle k draft forwards + k draft samplings,
-// one verify forward of k+1 tokens, one accept kernel and one draft catch-up
-// forward.  The per-sequence state (lengths, counters, candidates) stays in
+// one verify forward of k+1 tokens and the accept step.  The draft's
+// catch-up token (layer.cpp:1639-1653) is not given a forward of its own:
+// it is the first of two rows of the next cycle's first draft forward
+// (positions dlen-1 and dlen), which writes the same cache entries; the
+// draft prefill stops one token short so that the first cycle has the last
+// prompt token in that place.  The per-sequence state (lengths, counters, candidates) stays in
 // device memory, so the cycle is a fixed kernel sequence that is captured
 // once into a HIP graph and replayed; the host only polls the count of
 // active sequences one cycle behind.
@@ -404,7 +488,7 @@ void KVCache::sync_len_to_device() {
 namespace {
 
 struct SpecBuffers {
-  DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok,
+  DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok, pair,
       out, n_active, vids, prompts;
   DevBuf<float> qprob, dlog, tlog, tstat;
   DevBuf<int64_t> stats;
@@ -445,7 +529,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   SpecBuffers bf;
   bf.cur.alloc(B); bf.cand.alloc((size_t)B * k); bf.tlen.alloc(B);
   bf.dlen.alloc(B); bf.gen.alloc(B); bf.cyc.alloc(B); bf.active.alloc(B);
-  bf.catchup.alloc(B); bf.catch_tok.alloc(B);
+  bf.catchup.alloc(B); bf.catch_tok.alloc(B); bf.pair.alloc((size_t)2 * B);
   bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
   bf.vids.alloc((size_t)B * (k + 1)); bf.prompts.alloc((size_t)B * P);
   if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
@@ -481,6 +565,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     s.tlen = bf.tlen.p + b0; s.dlen = bf.dlen.p + b0; s.gen = bf.gen.p + b0;
     s.cyc = bf.cyc.p + b0; s.active = bf.active.p + b0;
     s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;
+    s.pair = bf.pair.p + (size_t)2 * b0;
     s.out = bf.out.p + (size_t)b0 * out_stride; s.n_active = bf.n_active.p;
     s.stats = bf.stats.p + (size_t)b0 * 6;
     s.B = Bg; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
@@ -489,6 +574,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     t.reserve(g, Bg * P, Bg * (k + 1), t_need);
     t.reserve(g, Bg * (k + 1), Bg * (k + 1), t_need);
     dm.reserve(g, Bg * P, Bg, d_need);
+    dm.reserve(g, 2 * Bg, Bg, d_need);
   }
   std::vector<hipEvent_t> evj(G);
   hipEvent_t evf;
@@ -519,7 +605,9 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     float *dl = bf.dlog.p + (size_t)b0 * V;
     t.forward(g, &tc, b0, pr, P, Bg, P, nullptr, 0, nullptr, P, dl, true);
     launch_first_token(lanes[g], gs[g], dl, V);
-    dm.forward(g, &dc, b0, pr, P, Bg, P, nullptr, 0, nullptr, P, nullptr, true);
+    if (P > 1)
+      dm.forward(g, &dc, b0, pr, P, Bg, P - 1, nullptr, 0, nullptr, P - 1,
+                 nullptr, true);
   }
   join();
   NNHIP_CHECK(hipEventRecord(e1, st));
@@ -535,17 +623,18 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
       float *tl = bf.tlog.p + (size_t)b0 * (k + 1) * V;
       int32_t *vids = bf.vids.p + (size_t)b0 * (k + 1);
       for (int j = 0; j < k; ++j) {
-        const int32_t *ids = j == 0 ? cur : cand + (j - 1);
-        dm.forward(g, &dc, b0, ids, j == 0 ? 1 : k, Bg, 1, dlen, j, act,
-                   d_need, dl, false);
+        if (j == 0)   // {catch-up token, cur} at dlen - 1, dlen
+          dm.forward(g, &dc, b0, bf.pair.p + (size_t)2 * b0, 2, Bg, 2, dlen,
+                     -1, act, d_need, dl, true);
+        else
+          dm.forward(g, &dc, b0, cand + (j - 1), k, Bg, 1, dlen, j, act,
+                     d_need, dl, false);
         launch_draft_sample(ls, gs[g], j, dl, V);
       }
       launch_build_verify_ids(ls, cur, cand, Bg, k, vids);
       t.forward(g, &tc, b0, vids, k + 1, Bg, k + 1, bf.tlen.p + b0, 0, act,
                 t_need, tl, false);
       launch_accept(ls, gs[g], tl);
-      dm.forward(g, &dc, b0, bf.catch_tok.p + b0, 1, Bg, 1, dlen, -1,
-                 bf.catchup.p + b0, d_need, nullptr, false);
     }
     join();
   };

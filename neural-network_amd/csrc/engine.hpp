@@ -92,7 +92,21 @@ struct Model {
   void linear(int g, const Linear &ln, const float *x, int64_t ldx, int rows,
               bool limbs_ready, const float *resid, int64_t ldr, float *y,
               int64_t ldy, int epi, const RopeArgs *ra = nullptr);
+  // A LayerNorm of h (rows of stride ldh) that the next linear applies to
+  // its input; the normalised rows go to out (stride ldo) when out is set.
+  struct PendingNorm {
+    const float *h = nullptr, *g = nullptr, *b = nullptr;
+    int64_t ldh = 0;
+    float *out = nullptr;
+    int64_t ldo = 0;
+  };
+  // linear over x, or over LN(h) when pn is given (x is then ignored)
+  void linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
+                 const PendingNorm *pn, int rows, bool limbs_ready,
+                 const float *resid, int64_t ldr, float *y, int64_t ldy,
+                 int epi, const RopeArgs *ra = nullptr);
   bool use_limbs(const Linear &ln, int rows) const;
+  bool use_lds(const Linear &ln, int rows) const;
 };
 
 // Ragged KV cache for B sequences: per layer [B][H][cap][D], one length per

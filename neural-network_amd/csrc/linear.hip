@@ -329,6 +329,242 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// int8 MFMA GEMM with the activation digits resident in LDS (K <= 1024).
+// One workgroup of 16 waves owns a 32-row x 32*CT-column tile: wave
+// (column tile ct, K slice ks) multiplies its 32 columns over K/KS of the K
+// range (KS = min(4, K/128), CT = 16/KS); the slices' int64 totals are
+// summed in LDS with 64-bit integer atomics (exact, order-free) and the
+// epilogue runs over the summed tile.  Every
+// global load is issued at the start -- the weight slice into registers,
+// the per-column scale and bias and the LayerNorm parameters into LDS, the
+// residual into registers -- so a workgroup waits for memory about once.
+// The 32 x K digit tile (3 planes, MFMA operand layout) is built by the
+// prologue:
+//   kAFromDigits     copied from digit planes written by another kernel,
+//   kAFromRows       digitised from fp32 rows (x, ldx),
+//   kAFromLayerNorm  LayerNorm (layer.cpp:242-261) of fp32 rows, written
+//                    to ln_out by the first column block, then digitised.
+// ---------------------------------------------------------------------------
+constexpr int kLdsThreads = 1024;
+
+template <int MODE, int KPT>
+__global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
+    const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
+    const float *__restrict__ x, int64_t ldx, const float *__restrict__ lng,
+    const float *__restrict__ lnb, float *__restrict__ ln_out, int64_t ldo,
+    int M, int N, const int8_t *__restrict__ wq,
+    const float *__restrict__ scale, const float *__restrict__ bias,
+    const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
+    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
+  constexpr int K = KPT * 32;
+  constexpr int nch = K / 128;
+  constexpr int KS = nch < 4 ? nch : 4;       // K slices
+  constexpr int CT = 16 / KS;                 // 32-column tiles per workgroup
+  constexpr int CPW = nch / KS;               // 128-wide chunks per wave
+  constexpr int NC = 32 * CT;                 // columns per workgroup
+  constexpr int kPlane = kGemmMT * K;         // bytes per digit plane
+  constexpr int kRedLd = 33;                  // padded row of the sum tile
+  constexpr int kABytes = kLimbs * kPlane;
+  constexpr bool kLN = MODE == kAFromLayerNorm;
+  __shared__ __attribute__((aligned(16))) int8_t sa[kABytes];
+  __shared__ long long red[CT][kGemmMT][kRedLd];
+  __shared__ float s_sc[NC], s_bi[NC];
+  __shared__ __attribute__((aligned(16))) float s_g[kLN ? K : 4], s_b[kLN ? K : 4];
+  __shared__ int s_e[kGemmMT];
+  const int T = ntm * ntn;
+  const int per = (T + 7) / 8;
+  const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (wi >= T) return;
+  const int tn = wi / ntm, tm = wi % ntm;
+  const int m0 = tm * kGemmMT, n0 = tn * NC;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ct = w % CT, ks = w / CT;
+  const int nw = n0 + 32 * ct;                // this wave's column tile
+
+  // ---- loads: weight slice, per-column and LayerNorm vectors, residual ----
+  v4i bf[CPW][4];
+  {
+    const int nt = min(nw, N - 32);           // past N: the last tile, unused
+    const int8_t *pb = wq + (int64_t)(nt >> 5) * nch * 4096 + lane * 16;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        bf[c][s] = *reinterpret_cast<const v4i *>(pb + (ks * CPW + c) * 4096 + s * 1024);
+  }
+  float vsc = 0.f, vbi = 0.f;
+  if (tid < NC && n0 + tid < N && epi != kEpiTotals) {
+    vsc = scale[n0 + tid];
+    vbi = bias[n0 + tid];
+  }
+  float vg = 0.f, vb = 0.f;
+  if (kLN && tid < K) { vg = lng[tid]; vb = lnb[tid]; }
+  // epilogue items: thread -> (row, column pair)
+  constexpr int ITEMS = kGemmMT * NC / 2 / kLdsThreads;
+  float e_rs[ITEMS][2];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int idx = tid + it * kLdsThreads;
+    const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+    const int m = m0 + row, n = n0 + c0;
+    const bool ok = epi == kEpiResid && m < M && n < N;
+    e_rs[it][0] = ok ? resid[(int64_t)m * ldr + n] : 0.f;
+    e_rs[it][1] = ok ? resid[(int64_t)m * ldr + n + 1] : 0.f;
+  }
+
+  if constexpr (KS > 1)
+    for (int i = tid; i < CT * kGemmMT * kRedLd; i += kLdsThreads)
+      (&red[0][0][0])[i] = 0;
+
+  // ---- prologue: the 32 x K digit tile in LDS ----
+  if constexpr (MODE == kAFromDigits) {
+    const int8_t *src = limbs + (int64_t)tm * nch * 4096;
+    const int64_t plane = (int64_t)mpad * K;
+    for (int i = tid; i < kLimbs * kPlane / 16; i += kLdsThreads) {
+      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
+      *reinterpret_cast<v4i *>(sa + l * kPlane + o) =
+          *reinterpret_cast<const v4i *>(src + l * plane + o);
+    }
+    if (tid < kGemmMT) s_e[tid] = m0 + tid < M ? rexp[m0 + tid] : 0;
+    if (tid < NC) { s_sc[tid] = vsc; s_bi[tid] = vbi; }
+  } else {
+#pragma clang fp contract(off)
+    // thread -> (row r, part p): entries 4p + 128i, i < K/128, as float4
+    constexpr int PP = K / 128;
+    const int r = tid >> 5, p = tid & 31;
+    const int m = m0 + r;
+    const bool live = m < M;
+    float4 v[PP];
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      v[i] = live ? *reinterpret_cast<const float4 *>(x + (int64_t)m * ldx + 4 * p + 128 * i)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < NC) { s_sc[tid] = vsc; s_bi[tid] = vbi; }
+    if (kLN && tid < K) { s_g[tid] = vg; s_b[tid] = vb; }
+    // sums / maxima over the 32 lanes of a row (aligned half-waves)
+    auto row_sum = [](float a) {
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) a += __shfl_xor(a, o, kWave);
+      return a;
+    };
+    auto row_max = [](float a) {
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
+      return a;
+    };
+    if constexpr (kLN) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+      const float Nf = (float)K;
+      const float mean = row_sum(s) / Nf;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) {
+        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean,
+                    d = v[i].w - mean;
+        sq += (a * a + b * b) + (c * c + d * d);
+      }
+      const float sd = sqrtf(row_sum(sq) / Nf + 1e-5f);
+      __syncthreads();                        // s_g, s_b written
+      const bool wr = ln_out && tn == 0 && live;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) {
+        const int k = 4 * p + 128 * i;
+        const float4 gg = *reinterpret_cast<const float4 *>(s_g + k);
+        const float4 bb = *reinterpret_cast<const float4 *>(s_b + k);
+        v[i].x = (v[i].x - mean) / sd * gg.x + bb.x;
+        v[i].y = (v[i].y - mean) / sd * gg.y + bb.y;
+        v[i].z = (v[i].z - mean) / sd * gg.z + bb.z;
+        v[i].w = (v[i].w - mean) / sd * gg.w + bb.w;
+        if (wr) *reinterpret_cast<float4 *>(ln_out + (int64_t)m * ldo + k) = v[i];
+      }
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                           fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = row_max(mx);
+    const int e = digit_exponent(mx);
+    if (p == 0) s_e[r] = live ? e : 0;
+#pragma unroll
+    for (int i = 0; i < PP; ++i) {
+      const int k = 4 * p + 128 * i;
+      const float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      int3 d = digits4(f, e);
+      if (!live) d = make_int3(0, 0, 0);
+      const int o = (int)mfma_operand_offset(r, k, K);
+      *reinterpret_cast<int *>(sa + o) = d.x;
+      *reinterpret_cast<int *>(sa + kPlane + o) = d.y;
+      *reinterpret_cast<int *>(sa + 2 * kPlane + o) = d.z;
+    }
+  }
+  __syncthreads();
+
+  // ---- the wave's K slice; its totals are stored (one slice) or added
+  // (int64 atomics) into the summed tile ----
+  if (nw < N) {
+    v16i acc[kLimbs];
+#pragma unroll
+    for (int l = 0; l < kLimbs; ++l) acc[l] = v16i{};
+    const int8_t *pa = sa + lane * 16;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int off = (ks * CPW + c) * 4096 + s * 1024;
+#pragma unroll
+        for (int l = 0; l < kLimbs; ++l) {
+          const v4i a = *reinterpret_cast<const v4i *>(pa + l * kPlane + off);
+          acc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bf[c][s], acc[l], 0, 0, 0);
+        }
+      }
+    // lane holds column (lane & 31) of rows (j >> 2) * 8 + (lane >> 5) * 4 +
+    // (j & 3), j < 16
+    long long *rp = &red[ct][(lane >> 5) * 4][lane & 31];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const long long tot = (long long)acc[0][j] * 65536LL +
+                            (long long)acc[1][j] * 256LL + (long long)acc[2][j];
+      long long *q = rp + ((j >> 2) * 8 + (j & 3)) * kRedLd;
+      if constexpr (KS == 1) *q = tot;
+      else atomicAdd(reinterpret_cast<unsigned long long *>(q), (unsigned long long)tot);
+    }
+  }
+  __syncthreads();
+
+  // ---- epilogue over the summed tile ----
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int idx = tid + it * kLdsThreads;
+    const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+    const int m = m0 + row, n = n0 + c0;
+    if (m >= M || n >= N) continue;
+    const long long t0 = red[c0 >> 5][row][c0 & 31];
+    const long long t1 = red[c0 >> 5][row][(c0 & 31) + 1];
+    if (epi == kEpiTotals) {
+      long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
+      yt[0] = t0; yt[1] = t1;
+      continue;
+    }
+    const int e = s_e[row];
+    float v0 = ldexpf((float)t0, -e), v1 = ldexpf((float)t1, -e);
+    v0 = __fadd_rn(__fmul_rn(v0, s_sc[c0]), s_bi[c0]);
+    v1 = __fadd_rn(__fmul_rn(v1, s_sc[c0 + 1]), s_bi[c0 + 1]);
+    if (epi == kEpiSwiGLU) {
+      y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
+    } else if (epi == kEpiRope) {
+      rope_store_pair(ra, m, n, v0, v1);
+    } else {
+      if (epi == kEpiResid) { v0 = e_rs[it][0] + v0; v1 = e_rs[it][1] + v1; }
+      y[(int64_t)m * ldy + n] = v0;
+      y[(int64_t)m * ldy + n + 1] = v1;
+    }
+  }
+}
+
 // QuantizedDense ctor, INT8 (quantization.cpp:36-66), one output channel per
 // workgroup: s = max|w|/127 (1 if 0), code = clamp(round(w/s), +-127).
 __global__ __launch_bounds__(256) void quantize_w8_kernel(
@@ -535,6 +771,52 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
                        ldr, y, ldy, epi, ntm, ntn, rz);
   }
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
+                     const int *rexp, const float *x, int64_t ldx,
+                     const float *lng, const float *lnb, float *ln_out,
+                     int64_t ldo, int rows, int K, int N, const int8_t *wq,
+                     const float *scale, const float *bias,
+                     const float *resid, int64_t ldr, float *y, int64_t ldy,
+                     int epi, const RopeArgs *ra) {
+  NNHIP_REQUIRE(gemm_lds_supports(rows, K, N), kErrArg,
+                "gemm_lds: needs K in {128, 256, 512, 1024}, N % 32 == 0");
+  NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg,
+                "gemm_lds: RoPE epilogue needs its arguments");
+  if (mode == kAFromDigits)
+    NNHIP_REQUIRE(limbs && rexp && rows <= mpad && mpad % 32 == 0, kErrArg,
+                  "gemm_lds: digit planes missing");
+  else
+    NNHIP_REQUIRE(x && ldx >= K && ldx % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(x) & 15) == 0,
+                  kErrArg, "gemm_lds: rows must be 16-byte aligned, ldx >= K");
+  if (mode == kAFromLayerNorm)
+    NNHIP_REQUIRE(lng && lnb && (!ln_out || (ldo >= K && ldo % 4 == 0)),
+                  kErrArg, "gemm_lds: LayerNorm parameters missing");
+  const RopeArgs rz = ra ? *ra : RopeArgs{};
+  const int ntm = (rows + kGemmMT - 1) / kGemmMT;
+  const int ntn = (int)(gemm_lds_workgroups(rows, K, N) / ntm);
+  const int per = (ntm * ntn + 7) / 8;
+  dim3 grid(8 * per);
+#define NNHIP_GL(MD, KP)                                                      \
+  hipLaunchKernelGGL((gemm_lds_kernel<MD, KP>), grid, dim3(kLdsThreads), 0,   \
+                     st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,    \
+                     rows, N, wq, scale, bias, resid, ldr, y, ldy, epi, ntm,  \
+                     ntn, rz)
+#define NNHIP_GL_K(MD)                                                        \
+  switch (K) {                                                                \
+    case 128: NNHIP_GL(MD, 4); break;                                         \
+    case 256: NNHIP_GL(MD, 8); break;                                         \
+    case 512: NNHIP_GL(MD, 16); break;                                        \
+    default: NNHIP_GL(MD, 32); break;                                         \
+  }
+  if (mode == kAFromDigits) { NNHIP_GL_K(kAFromDigits) }
+  else if (mode == kAFromRows) { NNHIP_GL_K(kAFromRows) }
+  else { NNHIP_GL_K(kAFromLayerNorm) }
+#undef NNHIP_GL_K
+#undef NNHIP_GL
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -174,6 +174,25 @@ __device__ inline int digit_exponent(float mx) {
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
 extern int g_attn_waves; // attention: waves one launch aims for
+// workgroups of one LDS-GEMM launch (32-row tiles x column blocks of
+// 32 * 16 / min(4, K/128) columns)
+inline int64_t gemm_lds_workgroups(int rows, int K, int N) {
+  const int nch = K / 128, nc = 32 * 16 / (nch < 4 ? nch : 4);
+  return (int64_t)((rows + 31) / 32) * ((N + nc - 1) / nc);
+}
+// Source of the activation digits of the LDS-resident GEMM.
+enum AFrom { kAFromDigits = 0, kAFromRows = 1, kAFromLayerNorm = 2 };
+inline bool gemm_lds_supports(int rows, int K, int N) {
+  return rows > 0 && (K == 128 || K == 256 || K == 512 || K == 1024) &&
+         N >= 32 && N % 32 == 0;
+}
+void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
+                     const int *rexp, const float *x, int64_t ldx,
+                     const float *lng, const float *lnb, float *ln_out,
+                     int64_t ldo, int rows, int K, int N, const int8_t *wq,
+                     const float *scale, const float *bias,
+                     const float *resid, int64_t ldr, float *y, int64_t ldy,
+                     int epi, const RopeArgs *ra = nullptr);
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
@@ -236,6 +255,8 @@ struct SpecState {
   int32_t *active;     // [B] 1 while gen < max_new
   int32_t *catchup;    // [B] 1 when the draft needs a catch-up forward
   int32_t *catch_tok;  // [B] token of that catch-up forward
+  int32_t *pair;       // [B][2] {catch_tok, cur}: ids of the next cycle's
+                       // first draft forward
   int32_t *out;        // [B][out_stride] prompt + generated ids
   int32_t *n_active;   // [1]
   int64_t *stats;      // [B][6] cycles, drafted, accepted, ties, resampled,

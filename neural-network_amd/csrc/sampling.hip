@@ -253,13 +253,19 @@ __global__ __launch_bounds__(kThreads) void first_token_kernel(
   const float u = uniform(s.seed, s.seq0 + b, 0, 2 * s.k);
   const int tok = draw_row(logits + b * ldl, s.V, s.T, u, sh);
   if (threadIdx.x == 0) {
-    s.out[(int64_t)b * s.out_stride + s.P] = tok;
+    int32_t *out = s.out + (int64_t)b * s.out_stride;
+    out[s.P] = tok;
     s.cur[b] = tok;
     s.gen[b] = 1;
     s.cyc[b] = 1;
     s.tlen[b] = s.P;
+    // the draft prefill stops one token short: the last prompt token is the
+    // pending catch-up token of the first cycle, dlen the length after it
     s.dlen[b] = s.P;
-    s.catchup[b] = 0;
+    s.catchup[b] = 1;
+    s.catch_tok[b] = out[s.P - 1];
+    s.pair[2 * b] = out[s.P - 1];
+    s.pair[2 * b + 1] = tok;
     const int act = s.max_new > 1 ? 1 : 0;
     s.active[b] = act;
     if (act) atomicAdd(s.n_active, 1);
@@ -414,6 +420,8 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     if (tok >= 0) s.dlen[b] = dstart + keep + (rej >= 0 ? 2 : 1);
     s.catchup[b] = tok >= 0 ? 1 : 0;
     s.catch_tok[b] = catch_tok;
+    s.pair[2 * b] = catch_tok;
+    s.pair[2 * b + 1] = tok;
     s.gen[b] = gen;
     s.cyc[b] = (int)cyc + 1;
     if (gen >= s.max_new) {

@@ -156,6 +156,72 @@ def test_mfma_linear_vs_oracle(ctx, rows, K, N):
     assert_as_accurate(got, want, exact, what="mfma w8a32")
 
 
+LDS_SHAPES = [(16, 128, 64), (32, 512, 1536), (192, 1024, 3072),
+              (5, 256, 96), (40, 1024, 32000), (64, 512, 4096),
+              (33, 128, 160)]
+
+
+def linear_path(ctx, x, codes, scales, b, path):
+    rows, K = x.shape
+    N = codes.shape[1]
+    dx, dc = ctx.array(x), ctx.array(np.ascontiguousarray(codes.T))
+    ds, db = ctx.array(scales), ctx.array(b)
+    dy = ctx.array(shape=(rows, N))
+    call("nnhip_linear_w8a32", ctx.h, dx.p, rows, K, dc.p, ds.p, db.p, N,
+         dy.p, path)
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("rows,K,N", LDS_SHAPES)
+def test_lds_gemm_matches_digit_gemm(ctx, rows, K, N):
+    """The LDS-resident GEMM (digits formed in its prologue, path 3, or read
+    from digit planes, path 4) computes the same exact integers and the same
+    epilogue as the digit-plane GEMM: bit-identical outputs, and within the
+    oracle's accuracy."""
+    rng = np.random.default_rng(rows * 7 + K + N)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    x[0] *= 1e-3
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    codes, scales = quantize_oracle(w)
+    g3 = linear_path(ctx, x, codes, scales, b, 3)
+    g4 = linear_path(ctx, x, codes, scales, b, 4)
+    np.testing.assert_array_equal(g3, g4)
+    if N % 64 == 0:
+        np.testing.assert_array_equal(g3, linear_path(ctx, x, codes, scales, b, 2))
+    want = dense_oracle(x, codes, scales, bias=b)
+    assert_rows_close(g3, want, 1e-4, "lds gemm")
+    exact = x.astype(np.float64) @ (codes.astype(np.float64) *
+                                    scales.astype(np.float64)) + b
+    assert_as_accurate(g3, want, exact, what="lds gemm")
+
+
+@pytest.mark.parametrize("rows,K,N", [(32, 512, 1536), (192, 1024, 8192),
+                                      (20, 128, 256), (7, 256, 64)])
+def test_layernorm_linear_vs_oracle(ctx, rows, K, N):
+    """LayerNorm fused into the GEMM prologue: LN(h) against the oracle's
+    layernorm, y against the oracle's dense over the oracle's LN(h)."""
+    rng = np.random.default_rng(rows + K + 3 * N)
+    h = (rng.standard_normal((rows, K)) * 2 + 0.3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    bt = (0.1 * rng.standard_normal(K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    codes, scales = quantize_oracle(w)
+    ln = np.zeros_like(h)
+    O.lib().or_layernorm(O.fptr(h), rows, K, O.fptr(g), O.fptr(bt), 1e-5,
+                         O.fptr(ln))
+    want = dense_oracle(ln, codes, scales, bias=b)
+    dh, dg, dbt = ctx.array(h), ctx.array(g), ctx.array(bt)
+    dc, ds, db = (ctx.array(np.ascontiguousarray(codes.T)), ctx.array(scales),
+                  ctx.array(b))
+    dln, dy = ctx.array(shape=(rows, K)), ctx.array(shape=(rows, N))
+    call("nnhip_layernorm_linear_w8a32", ctx.h, dh.p, rows, K, dg.p, dbt.p,
+         dln.p, dc.p, ds.p, db.p, N, dy.p)
+    assert_rows_close(dln.numpy(), ln, 1e-5, "fused layernorm")
+    assert_rows_close(dy.numpy(), want, 1e-4, "layernorm linear")
+
+
 def test_rope_kv_append(ctx):
     rng = np.random.default_rng(11)
     B, S, H, D, cap = 3, 5, 4, 64, 700
