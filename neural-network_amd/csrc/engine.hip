@@ -398,7 +398,11 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   reserve(g, R, logits ? (last_only ? B : R) : 0, max_keys);
   Workspace &ws = this->ws(g);
   const int32_t *bp = base ? base : ws.zeros.p;
-  launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p);
+  // the first q/k/v GEMM reads the embedding rows' digits when it is the
+  // digit-plane GEMM; the LDS GEMM digitises the rows itself
+  const bool emb_digits = !use_lds(layers[0].qkv, R) && use_limbs(layers[0].qkv, R);
+  launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
+                       emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
   // Post-norm blocks (layer.cpp:1098-1113): each LayerNorm is applied by the
   // linear that consumes it (norm1 -> ffn gate/up, norm2 -> next q/k/v or
   // the lm head), which also writes the normalised rows for the residual.
@@ -413,8 +417,8 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
     ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
     ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
     ra.qrot = ws.qrot.p; ra.kc = kc; ra.vc = vc; ra.seq_stride = kv->seq_stride();
-    linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R, false,
-              nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
+    linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
+              l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
     const bool lo = use_lds(ly.o, R) || use_limbs(ly.o, R);
     launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
                      kv->seq_stride(), bp, off, active, max_keys, ws.part.p,

@@ -223,7 +223,8 @@ void launch_embed(hipStream_t st, const float *emb, int vocab, int d,
                   const int32_t *ids, int rows, float *x);
 void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
                           const int32_t *ids, int B, int S, int stride_b,
-                          float *x);
+                          float *x, int8_t *limbs = nullptr, int mpad = 0,
+                          int *rexp = nullptr);
 void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
                              const int32_t *cand, int B, int k, int32_t *ids);
 void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
