@@ -135,7 +135,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split-K attention, one wave per (key split, head, sequence, query block).
+// Split-K attention: a wave per (key split, head, sequence, query block).
+// Either each wave is its own workgroup and writes its split's partial state
+// for attn_combine_kernel (W = 1), or the W waves of one workgroup are the
+// splits of one (head, sequence, query block) and merge in LDS, writing the
+// context rows (W > 1, short contexts).
 // Arithmetic as layer.cpp:859-948: score = q.k / sqrt(D), keys j > q_pos
 // masked, softmax, out = (sum p v) / (sum p).  The exponentials are taken in
 // base 2: the dot product is scaled by log2(e)/sqrt(D) and p = 2^(s - max),
@@ -155,14 +159,25 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 //  * PV: lane (r, dq) owns dims 4dq..4dq+3 of keys c0 + r + kpi*t, with
 //    kpi = 256 / D key rows per wave instruction; the SQP probabilities of a
 //    key are one broadcast LDS read.
-// The split's (max, sum, acc) per query goes to `part` for the combine.
+// The split's (max, sum, acc) per query goes to `part` for the combine, or to
+// LDS for the in-workgroup merge.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 32;
+constexpr int kMergedWaves = 8;    // key splits of a merged workgroup
+constexpr int kMergedChunks = 4;   // at most this many chunks per split
 
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
              0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Orders a wave's LDS accesses across its lanes (a wave's LDS operations
+// complete in program order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // max / sum over the 8 lanes l, l^8, ..., l^56 (same `sub`, all groups)
@@ -200,25 +215,31 @@ __device__ __forceinline__ void load_lane_dims(const float *p, int sub,
   }
 }
 
-template <int SQP, int DL>
-__global__ __launch_bounds__(kWave) void attn_kernel(
+template <int SQP, int DL, int W>
+__global__ __launch_bounds__(kWave * W) void attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc,
     const float *__restrict__ vc, int S, int H, int Hkv, int cap,
     int64_t seq_stride, const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
-    float qscale, float *__restrict__ part) {
+    float qscale, float *__restrict__ part, float *__restrict__ out) {
   constexpr int D = DL * 8;
   constexpr int NQ4 = D / 4, KPI = kWave / NQ4;   // PV: key rows per wave op
   constexpr int TPV = (kChunk + KPI - 1) / KPI;   // PV keys per lane
-  // chunk probabilities [kChunk][SQP], later the PV partials [KPI][SQP][D]
-  __shared__ float4 s_buf4[(KPI * SQP * D > kChunk * SQP ? KPI * SQP * D
-                                                         : kChunk * SQP) / 4];
-  __shared__ float s_alpha[SQP];
-  float *s_buf = reinterpret_cast<float *>(s_buf4);
-  const int sp = blockIdx.x, h = blockIdx.y;
+  // per wave: chunk probabilities [kChunk][SQP], later the PV partials
+  // [KPI][SQP][D]; with W > 1 also the wave's (max, sum) per query
+  constexpr int kBuf = (KPI * SQP * D > kChunk * SQP ? KPI * SQP * D
+                                                      : kChunk * SQP) / 4;
+  __shared__ float4 s_buf4[W][kBuf];
+  __shared__ float s_alpha[W][SQP];
+  __shared__ float s_ml[W][SQP][2];
+  const int wv = threadIdx.x >> 6;
+  float *s_buf = reinterpret_cast<float *>(s_buf4[wv]);
+  // W == 1: one key split per workgroup (blockIdx.x); W > 1: the splits are
+  // the workgroup's waves and are merged here
+  const int sp = W == 1 ? (int)blockIdx.x : wv, h = blockIdx.y;
   const int b = blockIdx.z / nqb, qb = blockIdx.z % nqb;
   if (active && !active[b]) return;
-  const int lane = threadIdx.x, g = lane >> 3, sub = lane & 7;
+  const int lane = threadIdx.x & 63, g = lane >> 3, sub = lane & 7;
   const int g8 = sub ^ (((sub >> 2) & 1) * 3);
   const int myq = g8 & (SQP - 1);
   const bool uniq = g8 < SQP;                 // one lane per (group, query)
@@ -312,11 +333,11 @@ __global__ __launch_bounds__(kWave) void attn_kernel(
       if (uniq) s_buf[(g + 8 * t) * SQP + myq] = p;
     }
     l_loc = l_loc * alpha + ps;
-    if (uniq && g == 0) s_alpha[myq] = alpha;
-    __syncthreads();
+    if (uniq && g == 0) s_alpha[wv][myq] = alpha;
+    wave_lds_sync();
     float al[SQP];
 #pragma unroll
-    for (int i = 0; i < SQP; ++i) al[i] = s_alpha[i];
+    for (int i = 0; i < SQP; ++i) al[i] = s_alpha[wv][i];
 #pragma unroll
     for (int i = 0; i < SQP; ++i)
 #pragma unroll
@@ -345,7 +366,7 @@ __global__ __launch_bounds__(kWave) void attn_kernel(
         acc[i][2] += pk[i] * vv[t].z; acc[i][3] += pk[i] * vv[t].w;
       }
     }
-    __syncthreads();
+    wave_lds_sync();
   }
   const float l = groups_sum(l_loc);
   if (pv_lane) {
@@ -354,8 +375,39 @@ __global__ __launch_bounds__(kWave) void attn_kernel(
       *reinterpret_cast<float4 *>(s_buf + (r * SQP + i) * D + dq * 4) =
           make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
   }
-  __syncthreads();
+  wave_lds_sync();
   const int64_t row0 = (int64_t)b * S + q0;
+  if constexpr (W > 1) {
+    // the wave's reduced acc into the front of its buffer, (max, sum) per
+    // query beside it, then the W splits merged as attn_combine_kernel does
+    for (int t = lane; t < nq * D; t += kWave) {
+      const int i = t / D, dd = t % D;
+      float s = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < KPI; ++rr) s += s_buf[(rr * SQP + i) * D + dd];
+      s_buf[i * D + dd] = s;
+    }
+    if (uniq && g == 0) { s_ml[wv][myq][0] = m_run; s_ml[wv][myq][1] = l; }
+    __syncthreads();
+    const int E = H * D;
+    for (int t = threadIdx.x; t < nq * D; t += kWave * W) {
+      const int i = t / D, dd = t % D;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < W; ++u) mx = fmaxf(mx, s_ml[u][i][0]);
+      float ls = 0.f, as = 0.f;
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
+        const float mu = s_ml[u][i][0];
+        const float f = mu == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mu - mx);
+        ls += s_ml[u][i][1] * f;
+        as += reinterpret_cast<const float *>(s_buf4[u])[i * D + dd] * f;
+      }
+      const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+      out[(row0 + i) * E + h * D + dd] = as * inv;
+    }
+    return;
+  }
   if (uniq && g == 0 && myq < nq) {
     float *pp = part + (((row0 + myq) * H + h) * nsplit + sp) * (D + 2);
     pp[0] = m_run;
@@ -554,7 +606,12 @@ int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys) {
   return (int64_t)B * S * H * nsplit * (D + 2);
 }
 
-void launch_attention(hipStream_t st, const float *q, const float *kc,
+bool attention_merged(int D, int max_keys) {
+  return (D == 32 || D == 64) &&
+         max_keys <= kMergedWaves * kMergedChunks * kChunk;
+}
+
+bool launch_attention(hipStream_t st, const float *q, const float *kc,
                       const float *vc, int B, int S, int H, int Hkv, int D,
                       int cap, int64_t seq_stride, const int32_t *base,
                       int off, const int32_t *active, int max_keys,
@@ -567,18 +624,40 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
   NNHIP_REQUIRE(!limbs || ((H * D) % 128 == 0 && B * S <= mpad), kErrArg,
                 "attention: digit output needs H*D % 128 == 0");
   if (max_keys < 1) max_keys = 1;
+  const int nqb = (S + kMaxQ - 1) / kMaxQ;
+  const int sq = S < kMaxQ ? S : kMaxQ;
+  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+  if (attention_merged(D, max_keys)) {
+    // one workgroup per (head, sequence, query block); its waves are the key
+    // splits, merged in LDS, and the context rows are written directly
+    int kps = (max_keys + kMergedWaves - 1) / kMergedWaves;
+    kps = (kps + kChunk - 1) / kChunk * kChunk;
+    dim3 grid(1, H, B * nqb);
+#define NNHIP_ATTN(SQP, DL)                                                   \
+  hipLaunchKernelGGL((attn_kernel<SQP, DL, kMergedWaves>), grid,              \
+                     dim3(kWave * kMergedWaves), 0, st, q, kc, vc, S, H, Hkv, \
+                     cap, seq_stride, base, off, active, kMergedWaves, nqb,   \
+                     kps, qscale, nullptr, out)
+#define NNHIP_ATTN_D(SQP)                                                     \
+  if (D == 32) NNHIP_ATTN(SQP, 4); else NNHIP_ATTN(SQP, 8);
+    if (sq == 1) { NNHIP_ATTN_D(1) }
+    else if (sq == 2) { NNHIP_ATTN_D(2) }
+    else if (sq <= 4) { NNHIP_ATTN_D(4) }
+    else { NNHIP_ATTN_D(8) }
+#undef NNHIP_ATTN_D
+#undef NNHIP_ATTN
+    NNHIP_CHECK(hipGetLastError());
+    return false;
+  }
   int kps = 0;
   const int nsplit = attention_splits(B, S, H, max_keys, &kps);
   NNHIP_REQUIRE(part_elems >= attention_partial_elems(B, S, H, D, max_keys),
                 kErrArg, "attention: partial buffer too small");
-  const int nqb = (S + kMaxQ - 1) / kMaxQ;
-  const int sq = S < kMaxQ ? S : kMaxQ;
-  const float qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
   dim3 grid(nsplit, H, B * nqb);
 #define NNHIP_ATTN(SQP, DL)                                                   \
-  hipLaunchKernelGGL((attn_kernel<SQP, DL>), grid, dim3(kWave), 0, st, q, kc, \
-                     vc, S, H, Hkv, cap, seq_stride, base, off, active,       \
-                     nsplit, nqb, kps, qscale, part)
+  hipLaunchKernelGGL((attn_kernel<SQP, DL, 1>), grid, dim3(kWave), 0, st, q,  \
+                     kc, vc, S, H, Hkv, cap, seq_stride, base, off, active,   \
+                     nsplit, nqb, kps, qscale, part, nullptr)
 #define NNHIP_ATTN_D(SQP)                                                     \
   switch (D / 8) {                                                            \
     case 1: NNHIP_ATTN(SQP, 1); break;                                        \
@@ -597,9 +676,10 @@ void launch_attention(hipStream_t st, const float *q, const float *kc,
 #undef NNHIP_ATTN_D
 #undef NNHIP_ATTN
   NNHIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S), dim3(kCombineThreads), 0, st, part,
-                     S, H, D, nsplit, active, out, limbs, mpad, rexp);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(B * S), dim3(kCombineThreads), 0,
+                     st, part, S, H, D, nsplit, active, out, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
+  return limbs != nullptr;
 }
 
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,

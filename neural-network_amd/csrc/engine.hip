@@ -419,13 +419,23 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
     ra.qrot = ws.qrot.p; ra.kc = kc; ra.vc = vc; ra.seq_stride = kv->seq_stride();
     linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
               l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
-    const bool lo = use_lds(ly.o, R) || use_limbs(ly.o, R);
+    // short contexts: the attention workgroups merge their key splits and
+    // write ctx; the output projection then digitises ctx itself.  Long
+    // ones: split attention + combine, which also writes ctx's digits.
+    const bool merged = attention_merged(D, max_keys);
+    const bool lo = !merged && (use_lds(ly.o, R) || use_limbs(ly.o, R));
     launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
                      kv->seq_stride(), bp, off, active, max_keys, ws.part.p,
                      ws.part_elems, ws.ctx.p, lo ? ws.limbs.p : nullptr,
                      ws.mpad, ws.rexp.p);
-    linear_in(g, ly.o, ws.ctx.p, d, nullptr, R, lo, ws.x.p, d, ws.h.p, d,
-              kEpiResid);
+    if (merged && ly.o.quant && ly.o.qs.p && R >= kLimbMinRows &&
+        gemm_lds_supports(R, d, d))
+      launch_gemm_lds(st, kAFromRows, nullptr, 0, nullptr, ws.ctx.p, d,
+                      nullptr, nullptr, nullptr, 0, R, d, d, ly.o.qs.p,
+                      ly.o.s.p, ly.o.b.p, ws.x.p, d, ws.h.p, d, kEpiResid);
+    else
+      linear_in(g, ly.o, ws.ctx.p, d, nullptr, R, lo, ws.x.p, d, ws.h.p, d,
+                kEpiResid);
     PendingNorm norm1;
     norm1.h = ws.h.p; norm1.ldh = d; norm1.g = ly.g1.p; norm1.b = ly.b1.p;
     norm1.out = ws.x1.p; norm1.ldo = d;

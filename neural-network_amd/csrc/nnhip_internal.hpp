@@ -231,7 +231,11 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
                     int D, const int32_t *base, int off, const int32_t *active,
                     const float *cosb, const float *sinb, float *qrot,
                     float *kc, float *vc, int cap, int64_t seq_stride);
-void launch_attention(hipStream_t st, const float *q, const float *kc,
+// true when launch_attention writes the context rows without the combine
+// kernel (and so without digit planes)
+bool attention_merged(int D, int max_keys);
+// returns whether the digit planes were written
+bool launch_attention(hipStream_t st, const float *q, const float *kc,
                       const float *vc, int B, int S, int H, int Hkv, int D,
                       int cap, int64_t seq_stride, const int32_t *base,
                       int off, const int32_t *active, int max_keys,
