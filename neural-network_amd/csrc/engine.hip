@@ -12,7 +12,7 @@ namespace {
 
 constexpr int kLimbMinRows = 16;
 constexpr int64_t kFusedNormMaxBlocks = 768;
-constexpr int kLdsQkvMinRows = 64;
+constexpr int kLdsMinRows = 64;
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
@@ -304,20 +304,18 @@ bool Model::use_limbs(const Linear &ln, int rows) const {
          ln.N % 64 == 0;
 }
 
-// Where the LDS-resident GEMM is used (measured per call site on the
-// batch-32 decode shapes): the lm head (its many column blocks amortise the
-// digit tile), and the q/k/v projection of tall inputs (>= 64 rows), where
-// folding the preceding LayerNorm into the prologue saves a launch.  The
-// O, gate/up and down projections and short q/k/v inputs run faster as
-// separate LayerNorm / digit kernels plus the digit-plane GEMM.
+// Where the LDS-resident GEMM is used (measured on the batch-32 decode
+// shapes): the lm head, and every projection with K <= 1024 on tall inputs
+// (>= 64 rows: the verify batch), where one digit tile per 32 rows serves
+// 128 columns.  Short inputs (the draft's 32 rows) run faster on the
+// digit-plane GEMM.  A pending LayerNorm is folded into the GEMM prologue
+// only for the lm head of a short batch; elsewhere the prologue's repeated
+// per-column-block normalisation costs more than a LayerNorm launch.
 bool Model::use_lds(const Linear &ln, int rows) const {
   if (!(ln.quant && ln.qs.p && rows >= kLimbMinRows &&
         gemm_lds_supports(rows, ln.K, ln.N)))
     return false;
-  if (&ln == &lm) return true;
-  for (const LayerW &ly : layers)
-    if (&ln == &ly.qkv) return rows >= kLdsQkvMinRows;
-  return false;
+  return &ln == &lm || rows >= kLdsMinRows;
 }
 
 void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
@@ -327,11 +325,12 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
   hipStream_t st = ctx->lane(g);
   Workspace &ws = this->ws(g);
   if (use_lds(ln, rows)) {
-    // Each column block of the fused GEMM normalises and digitises its rows
-    // again; past a few hundred blocks one LayerNorm launch writing digit
-    // planes costs less.
-    if (pn && pn->ldh == ln.K &&
-        gemm_lds_workgroups(rows, ln.K, ln.N) > kFusedNormMaxBlocks) {
+    // Each column block of a fused GEMM normalises and digitises its rows
+    // again: only the short-batch lm head folds the norm in; elsewhere one
+    // LayerNorm launch writes digit planes for the GEMM to copy.
+    const bool fold = &ln == &lm && rows < kLdsMinRows &&
+                      gemm_lds_workgroups(rows, ln.K, ln.N) <= kFusedNormMaxBlocks;
+    if (pn && !fold && pn->ldh == ln.K) {
       launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b,
                        pn->out ? pn->out : ws.x.p, ws.limbs.p, ws.mpad,
                        ws.rexp.p);
@@ -398,9 +397,9 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   reserve(g, R, logits ? (last_only ? B : R) : 0, max_keys);
   Workspace &ws = this->ws(g);
   const int32_t *bp = base ? base : ws.zeros.p;
-  // the first q/k/v GEMM reads the embedding rows' digits when it is the
-  // digit-plane GEMM; the LDS GEMM digitises the rows itself
-  const bool emb_digits = !use_lds(layers[0].qkv, R) && use_limbs(layers[0].qkv, R);
+  // the embedding kernel also writes the rows' digits for the first q/k/v
+  // GEMM when that is an MFMA GEMM
+  const bool emb_digits = use_lds(layers[0].qkv, R) || use_limbs(layers[0].qkv, R);
   launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
                        emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
   // Post-norm blocks (layer.cpp:1098-1113): each LayerNorm is applied by the
