@@ -534,6 +534,93 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
   store_row_digits<256>(srow, d, mx, row, limbs, mpad, rexp, sred);
 }
 
+// LayerNorm as layernorm_kernel, one wave per row for d % 16 == 0: lane l
+// holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, the
+// row sums and the max are wave reductions, and the digits of y (for the
+// next MFMA GEMM) are written from the same registers.
+template <int PPL>
+__global__ __launch_bounds__(256) void layernorm_rows_kernel(
+    const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
+    const float *__restrict__ bt, float *__restrict__ y,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+#pragma clang fp contract(off)
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float *xr = hin + (int64_t)row * d;
+  const int np = d / 16;
+  float v[PPL][16];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int pc = lane + 64 * j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = pc < np ? *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) s += v[j][q];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+  const float N = (float)d;
+  const float mean = s / N;
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    if (lane + 64 * j >= np) break;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) { const float df = v[j][q] - mean; sq += df * df; }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+  const float sd = sqrtf(sq / N + 1e-5f);
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int pc = lane + 64 * j;
+    if (pc >= np) break;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
+      const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
+      float *w = v[j] + 4 * q;
+      w[0] = (w[0] - mean) / sd * gg.x + bb.x;
+      w[1] = (w[1] - mean) / sd * gg.y + bb.y;
+      w[2] = (w[2] - mean) / sd * gg.z + bb.z;
+      w[3] = (w[3] - mean) / sd * gg.w + bb.w;
+      *reinterpret_cast<float4 *>(y + (int64_t)row * d + 16 * pc + 4 * q) =
+          make_float4(w[0], w[1], w[2], w[3]);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])),
+                           fmaxf(fabsf(w[2]), fabsf(w[3]))));
+    }
+  }
+  if (!limbs) return;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  const int e = digit_exponent(mx);
+  if (lane == 0) rexp[row] = e;
+  const int64_t plane = (int64_t)mpad * d;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int pc = lane + 64 * j;
+    if (pc >= np) break;
+    v4i hi, mid, lo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int3 t = digits4(v[j] + 4 * q, e);
+      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
+    }
+    const int64_t off = mfma_operand_offset(row, 16 * pc, d);
+    *reinterpret_cast<v4i *>(limbs + off) = hi;
+    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
+    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
+  }
+}
+
 __global__ void add_scalar_kernel(int32_t *p, int n, int v) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] += v;
@@ -688,8 +775,22 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
   NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
   NNHIP_REQUIRE(!limbs || (d % 128 == 0 && rows <= mpad), kErrArg,
                 "layernorm: digit output needs d % 128 == 0");
-  hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,
-                     b, y, limbs, mpad, rexp);
+  if (d % 16 == 0) {
+    const int np = d / 16;
+    const dim3 grid((rows + 3) / 4);
+    if (np <= 64)
+      hipLaunchKernelGGL(layernorm_rows_kernel<1>, grid, dim3(256), 0, st, h, d,
+                         rows, g, b, y, limbs, mpad, rexp);
+    else if (np <= 128)
+      hipLaunchKernelGGL(layernorm_rows_kernel<2>, grid, dim3(256), 0, st, h, d,
+                         rows, g, b, y, limbs, mpad, rexp);
+    else
+      hipLaunchKernelGGL(layernorm_rows_kernel<4>, grid, dim3(256), 0, st, h, d,
+                         rows, g, b, y, limbs, mpad, rexp);
+  } else {
+    hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,
+                       b, y, limbs, mpad, rexp);
+  }
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -148,43 +148,50 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Activation digits for the MFMA GEMM.  Row m: e = 22 - exponent(max|x|), so
-// |x * 2^e| < 2^22; X = rint(x * 2^e) (exact scaling, ties to even) is split
-// into balanced base-256 digits hi, mid, lo in [-128, 127], written as three
-// planes in the MFMA operand layout (mfma_operand_offset).
-// ---------------------------------------------------------------------------
+// Digits of activation rows for the MFMA GEMM: X = rint(x * 2^e) with
+// e = 22 - exponent(max|x|) per row, split into balanced base-256 digits
+// (hi, mid, lo), written in the MFMA operand layout.  One wave per row; lane
+// l holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, so
+// the row is read once and the max needs no workgroup barrier.
+template <int PPL>
 __global__ __launch_bounds__(256) void act_quant_kernel(
-    const float *__restrict__ x, int64_t ldx, int K, int8_t *__restrict__ limbs,
-    int mpad, int *__restrict__ rexp) {
-  __shared__ float smax[4];
-  const int m = blockIdx.x;
+    const float *__restrict__ x, int64_t ldx, int K, int rows,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (m >= rows) return;
   const float *xr = x + m * ldx;
+  const int np = K / 16;
+  float v[PPL][16];
   float mx = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(xr[k]));
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
-  const int e = digit_exponent(mx);
-  if (threadIdx.x == 0) rexp[m] = e;
-  const int64_t plane = (int64_t)mpad * K;
-  for (int p = threadIdx.x; p < K / 16; p += blockDim.x) {
-    const int k = p * 16;
-    float v[16];
+  for (int j = 0; j < PPL; ++j) {
+    const int pc = lane + 64 * j;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 f = *reinterpret_cast<const float4 *>(xr + k + 4 * q);
-      v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+      const float4 f = pc < np ? *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
     }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  const int e = digit_exponent(mx);
+  if (lane == 0) rexp[m] = e;
+  const int64_t plane = (int64_t)mpad * K;
+#pragma unroll
+  for (int j = 0; j < PPL; ++j) {
+    const int pc = lane + 64 * j;
+    if (pc >= np) break;
     v4i hi, mid, lo;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int3 t = digits4(v + 4 * q, e);
+      const int3 t = digits4(v[j] + 4 * q, e);
       hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
     }
-    const int64_t off = mfma_operand_offset(m, k, K);
+    const int64_t off = mfma_operand_offset(m, 16 * pc, K);
     *reinterpret_cast<v4i *>(limbs + off) = hi;
     *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
     *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
@@ -740,8 +747,18 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   if (rows <= 0) return;
   NNHIP_REQUIRE(K % 128 == 0 && ldx % 4 == 0 && rows <= mpad, kErrArg,
                 "act_quant: K % 128 and ldx % 4 must be 0");
-  hipLaunchKernelGGL(act_quant_kernel, dim3(rows), dim3(256), 0, st, x, ldx, K,
-                     limbs, mpad, rexp);
+  NNHIP_REQUIRE(K <= 4096, kErrArg, "act_quant: K must be <= 4096");
+  const int np = K / 16;
+  const dim3 grid((rows + 3) / 4);
+  if (np <= 64)
+    hipLaunchKernelGGL(act_quant_kernel<1>, grid, dim3(256), 0, st, x, ldx, K,
+                       rows, limbs, mpad, rexp);
+  else if (np <= 128)
+    hipLaunchKernelGGL(act_quant_kernel<2>, grid, dim3(256), 0, st, x, ldx, K,
+                       rows, limbs, mpad, rexp);
+  else
+    hipLaunchKernelGGL(act_quant_kernel<4>, grid, dim3(256), 0, st, x, ldx, K,
+                       rows, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
 }
 
