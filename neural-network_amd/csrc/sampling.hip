@@ -110,21 +110,36 @@ __device__ __forceinline__ int block_min_i(int v, Shared &sh) {
   return r;
 }
 
+// The thread's row entries v = tid + kThreads * i, i < kPer, all requested
+// before the first is used (indices past V re-read entry V-1 and are
+// replaced by `fill`).
+constexpr int kPer = kMaxV / kThreads;   // row entries per thread
+
+__device__ __forceinline__ void load_row(const float *__restrict__ row, int V,
+                                         float fill, float (&x)[kPer]) {
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    x[i] = row[min((int)threadIdx.x + i * kThreads, V - 1)];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    if ((int)threadIdx.x + i * kThreads >= V) x[i] = fill;
+}
+
 // First index of the maximum (layer.cpp:1413-1421, std::max_element).
-__device__ int block_argmax(const float *__restrict__ row, int V, Shared &sh) {
+__device__ __forceinline__ int block_argmax(const float *__restrict__ row,
+                                            int V, Shared &sh) {
+  float x[kPer];
+  load_row(row, V, -INFINITY, x);
   float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float x = row[v];
-    if (bi == 0x7fffffff || x > bv) { bv = x; bi = v; }
-  }
-  const float mx = block_max(bi == 0x7fffffff ? -INFINITY : bv, sh);
-  // lowest index holding the maximum (each thread scanned ascending v)
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) bv = fmaxf(bv, x[i]);
+  const float mx = block_max(bv, sh);
+  // lowest index holding the maximum (entries ascend with i)
   int cand = 0x7fffffff;
-  if (bi != 0x7fffffff && bv == mx) cand = bi;
-  if (cand != 0x7fffffff) {
-    for (int v = threadIdx.x; v < bi; v += kThreads)
-      if (row[v] == mx) { cand = v; break; }
+#pragma unroll
+  for (int i = kPer - 1; i >= 0; --i) {
+    const int v = (int)threadIdx.x + i * kThreads;
+    if (v < V && x[i] == mx) cand = v;
   }
   const int r = block_min_i(cand, sh);
   return r == 0x7fffffff ? 0 : r;
@@ -137,8 +152,6 @@ __device__ int block_argmax(const float *__restrict__ row, int V, Shared &sh) {
 // RowStats holds what recomputes p at one index (prob_at).
 struct RowStats { float mx, rsum, rfs; };
 
-constexpr int kPer = kMaxV / kThreads;   // row entries per thread
-
 __device__ __forceinline__ float scaled(float l, float T) {
   return T == 1.0f ? l : l / T;
 }
@@ -148,19 +161,20 @@ __device__ __forceinline__ float prob_at(const float *row, int v, float T,
   return (expf(scaled(row[v], T) - st.mx) * st.rsum) * st.rfs;
 }
 
-// The row is held in registers (entry v = tid + 1024 i); p goes to sh.prow
+// The row is held in registers (entry v = tid + kThreads i); p goes to sh.prow
 // when `to_lds`, and to gout when given.
-__device__ RowStats row_pass(const float *__restrict__ row, int V, float T,
+__device__ __forceinline__ RowStats row_pass(const float *__restrict__ row, int V, float T,
                              Shared &sh, bool to_lds,
                              float *__restrict__ gout) {
   float x[kPer];
+  load_row(row, V, -INFINITY, x);
+  if (T != 1.0f) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) x[i] = x[i] / T;
+  }
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int v = threadIdx.x + i * kThreads;
-    x[i] = v < V ? scaled(row[v], T) : -INFINITY;
-    mx = fmaxf(mx, x[i]);
-  }
+  for (int i = 0; i < kPer; ++i) mx = fmaxf(mx, x[i]);
   mx = block_max(mx, sh);
   float s = 0.f;
 #pragma unroll
@@ -204,10 +218,16 @@ __device__ __forceinline__ RowStats row_stats(const float *__restrict__ row,
 }
 
 // sh.prow = p recomputed from a row's statistics
-__device__ void fill_probs(const float *__restrict__ row, int V, float T,
-                           RowStats st, Shared &sh) {
-  for (int v = threadIdx.x; v < V; v += kThreads)
-    sh.prow[la(v)] = prob_at(row, v, T, st);
+__device__ __forceinline__ void fill_probs(const float *__restrict__ row,
+                                           int V, float T, RowStats st,
+                                           Shared &sh) {
+  float x[kPer];
+  load_row(row, V, 0.f, x);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int v = (int)threadIdx.x + i * kThreads;
+    if (v < V) sh.prow[la(v)] = (expf(scaled(x[i], T) - st.mx) * st.rsum) * st.rfs;
+  }
   __syncthreads();
 }
 
@@ -216,27 +236,34 @@ __device__ void fill_probs(const float *__restrict__ row, int V, float T,
 // entry 1.0): the first v whose running sum of p reaches u * S.  Each thread
 // owns a contiguous chunk; a chunk is scanned only when the crossing can lie
 // in it or before it.
-__device__ int block_sample(int V, float u, Shared &sh) {
+__device__ __forceinline__ int block_sample(int V, float u, Shared &sh) {
+  // the thread's chunk [b0, b0 + C) (C <= kPer), read from LDS once
   const int C = (V + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * C;
-  const int b1 = min(b0 + C, V);
+  float pv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    pv[i] = (i < C && b0 + i < V) ? sh.prow[la(min(b0 + i, V - 1))] : 0.f;
   double loc = 0.0;
-  for (int v = b0; v < b1; ++v) loc += (double)sh.prow[la(v)];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) loc += (double)pv[i];
   double S;
   double c = block_excl_scan_d(loc, sh, &S);
   const double target = (double)u * S;
   int found = 0x7fffffff;
   if (c + loc >= target - 1e-12 * S) {
-    for (int v = b0; v < b1 && v < V - 1; ++v) {
-      c += (double)sh.prow[la(v)];
-      if (c >= target) { found = v; break; }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int v = b0 + i;
+      c += (double)pv[i];
+      if (found == 0x7fffffff && i < C && v < V - 1 && c >= target) found = v;
     }
   }
   const int r = block_min_i(found, sh);
   return r == 0x7fffffff ? V - 1 : r;
 }
 
-__device__ int draw_row(const float *row, int V, float T, float u,
+__device__ __forceinline__ int draw_row(const float *row, int V, float T, float u,
                         Shared &sh) {
   if (T <= 0.f) return block_argmax(row, V, sh);
   row_probs(row, V, T, sh);
@@ -316,18 +343,35 @@ __global__ __launch_bounds__(kThreads) void target_stats_kernel(
 // statistics, q from qrow (stored) or from the draft row's statistics; then
 // sample it, or p when the residual sums to zero.  The residual is sampled
 // unnormalised: the discrete distribution normalises it.
-__device__ int residual_sample(const float *__restrict__ qrow,
-                               const float *__restrict__ dlog_row,
-                               RowStats qst, const float *__restrict__ tlog_row,
-                               RowStats tst, int V, float T, float u,
-                               Shared &sh) {
+__device__ __forceinline__ int residual_sample(
+    const float *__restrict__ qrow, const float *__restrict__ dlog_row,
+    RowStats qst, const float *__restrict__ tlog_row, RowStats tst, int V,
+    float T, float u, Shared &sh) {
+  // two halves of the thread's entries, each with its loads in flight
+  const float *qsrc = qrow ? qrow : dlog_row;
+  constexpr int kHalf = kPer / 2;
   float loc = 0.f;
-  for (int v = threadIdx.x; v < V; v += kThreads) {
-    const float p = prob_at(tlog_row, v, T, tst);
-    const float q = qrow ? qrow[v] : prob_at(dlog_row, v, T, qst);
-    const float r = fmaxf(0.0f, p - q);
-    sh.prow[la(v)] = r;
-    loc += r;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    float xt[kHalf], xq[kHalf];
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i) {
+      const int v = min((int)threadIdx.x + (hf * kHalf + i) * kThreads, V - 1);
+      xt[i] = tlog_row[v];
+      xq[i] = qsrc[v];
+    }
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i) {
+      const int v = (int)threadIdx.x + (hf * kHalf + i) * kThreads;
+      if (v < V) {
+        const float p = (expf(scaled(xt[i], T) - tst.mx) * tst.rsum) * tst.rfs;
+        const float q = qrow ? xq[i]
+                             : (expf(scaled(xq[i], T) - qst.mx) * qst.rsum) * qst.rfs;
+        const float r = fmaxf(0.0f, p - q);
+        sh.prow[la(v)] = r;
+        loc += r;
+      }
+    }
   }
   const float sr = block_sum(loc, sh);
   if (sr <= 0.0f) fill_probs(tlog_row, V, T, tst, sh);
@@ -359,20 +403,43 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   auto argmax_of = [&](int j) {
     return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * 4 + 3]);
   };
-  for (int j = 0; j < M; ++j) {
-    const float *row = tlogits + ((int64_t)b * (k + 1) + j) * V;
-    const int c = s.cand[b * k + j];
-    bool acc;
-    if (greedy) {
-      acc = c == argmax_of(j);
-    } else {
-      const float pc = prob_at(row, c, s.T, stats_of(j));
-      const float qc = s.qprob[((int64_t)b * k + j) * V + c];
-      const float r = uniform(s.seed, seq, cyc, k + j);
-      acc = __fmul_rn(r, qc) < pc;
-      if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
+  // the candidates' target logits and draft probabilities, the first kPre
+  // positions requested at once (their loop is unrolled so that the
+  // prefetched values stay in registers)
+  constexpr int kPre = 8;
+  float lc[kPre], qcp[kPre];
+  if (!greedy) {
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      if (j < M) {
+        const int c = s.cand[b * k + j];
+        lc[j] = tlogits[((int64_t)b * (k + 1) + j) * V + c];
+        qcp[j] = s.qprob[((int64_t)b * k + j) * V + c];
+      }
     }
-    if (!acc) { rej = j; break; }
+  }
+  // accept test of position j given its candidate's p and q
+  auto test = [&](int j, int c, float lj, float qc) {
+    if (greedy) return c == argmax_of(j);
+    const RowStats st = stats_of(j);
+    const float pc = (expf(scaled(lj, s.T) - st.mx) * st.rsum) * st.rfs;
+    const float r = uniform(s.seed, seq, cyc, k + j);
+    if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
+    return __fmul_rn(r, qc) < pc;
+  };
+#pragma unroll
+  for (int j = 0; j < kPre; ++j) {
+    if (j >= M || rej >= 0) break;
+    const int c = s.cand[b * k + j];
+    if (!test(j, c, lc[j], qcp[j])) { rej = j; break; }
+    if (threadIdx.x == 0) out[nout] = c;
+    ++nout;
+  }
+  for (int j = kPre; j < M && rej < 0; ++j) {
+    const int c = s.cand[b * k + j];
+    const float lj = greedy ? 0.f : tlogits[((int64_t)b * (k + 1) + j) * V + c];
+    const float qc = greedy ? 0.f : s.qprob[((int64_t)b * k + j) * V + c];
+    if (!test(j, c, lj, qc)) { rej = j; break; }
     if (threadIdx.x == 0) out[nout] = c;
     ++nout;
   }
