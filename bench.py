@@ -129,18 +129,58 @@ def run_cfg2(ctx):
                 accepted=stats[0].accepted)
 
 
+ATTN_SHAPE = dict(B=B, S=K_LOOK + 1, H=16, D=64, n_cached=P + NEW // 2)
+TRAFFIC_NOTE = os.path.join(ROOT, "profiles", "attention_verify_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the verify attention kernel, as measured by
+    the rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/."""
+    try:
+        with open(TRAFFIC_NOTE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def roofline_attention(ctx):
     """Verify-step attention at the cfg4 mid-run shape: 32 sequences x 16
-    heads, 6 queries, 320 cached keys (+6 new)."""
-    n_cached = P + NEW // 2
-    S = K_LOOK + 1
-    ms = nnhip.bench_attention(ctx, B, S, 16, 64, n_cached, iters=200, nbuf=4)
-    byt = attention_bytes(B, S, 16, 64, n_cached + S)
+    heads, 6 queries, 320 cached keys (+6 new); one launch of the merged
+    split kernel.  Algorithmic bytes: K and V of every visible key once, the
+    queries read and the context rows written."""
+    sh = ATTN_SHAPE
+    ms = nnhip.bench_attention(ctx, sh["B"], sh["S"], sh["H"], sh["D"],
+                               sh["n_cached"], iters=200, nbuf=4)
+    byt = attention_bytes(sh["B"], sh["S"], sh["H"], sh["D"],
+                          sh["n_cached"] + sh["S"])
     ach = byt / (ms / 1e3) / 1e9
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
-                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="attn_kernel<6> (+combine)", bytes_per_launch=byt,
-                us_per_launch=round(ms * 1e3, 2))
+                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
+                traffic=measured_traffic(),
+                kernel="attn_kernel<8, 8, 8> (verify, splits merged in LDS)",
+                bytes_per_launch=byt, us_per_launch=round(ms * 1e3, 2))
+
+
+def traffic_probe():
+    """For rocprofv3 --pmc runs: a plain device copy of 256 MiB (the
+    calibration of FETCH_SIZE / WRITE_SIZE) followed by 20 launches of the
+    verify attention kernel at the roofline shape."""
+    import torch
+    a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    b_ = torch.empty_like(a)
+    for _ in range(3):
+        b_.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copied {a.numel() * 4} bytes x 3")
+    ctx = nnhip.Context(0)
+    sh = ATTN_SHAPE
+    ms = nnhip.bench_attention(ctx, sh["B"], sh["S"], sh["H"], sh["D"],
+                               sh["n_cached"], iters=20, nbuf=4)
+    log(f"attention: {ms * 1e3:.2f} us per launch, algorithmic bytes "
+        f"{attention_bytes(sh['B'], sh['S'], sh['H'], sh['D'], sh['n_cached'] + sh['S'])}")
 
 
 def cpu_baseline(models, sample_new=12):
@@ -174,7 +214,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
-    ap.add_argument("--groups", type=int, default=2,
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the copy calibration and the attention "
+                         "kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--groups", type=int, default=1,
                     help="sequence groups driven on separate HIP streams")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch each kernel of a cycle separately instead "
@@ -185,6 +228,9 @@ def main():
               "single MI355X (sharding is described in DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+    if a.traffic_probe:
+        traffic_probe()
+        return
     ctx = nnhip.Context(0)
     if a.no_graphs:
         ctx.set_option("graphs", 0)
