@@ -236,6 +236,25 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   const int r = lane & 31, h = lane >> 5;
   for (int i = threadIdx.x; i < kLimbs * kGemmMT * NT; i += 256)
     (&red[0][0][0])[i] = 0;
+  // the epilogue's operands (thread -> (row, column pair) items), requested
+  // now so that they arrive with the MFMA operands
+  // (256 is a multiple of NT/2, so a thread's items share one column pair)
+  constexpr int IT = kGemmMT * NT / 2 / 256;
+  static_assert(256 % (NT / 2) == 0, "items must share their columns");
+  const int e_n = n0 + 2 * ((int)threadIdx.x % (NT / 2));
+  const bool e_cols = epi != kEpiTotals;
+  const float e_sc0 = e_cols ? scale[e_n] : 0.f, e_sc1 = e_cols ? scale[e_n + 1] : 0.f;
+  const float e_bi0 = e_cols ? bias[e_n] : 0.f, e_bi1 = e_cols ? bias[e_n + 1] : 0.f;
+  int e_ex[IT];
+  float e_rs[IT][2];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int m = m0 + ((int)threadIdx.x + it * 256) / (NT / 2);
+    const bool ok = m < M && epi != kEpiTotals;
+    e_ex[it] = ok ? rexp[m] : 0;
+    e_rs[it][0] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n] : 0.f;
+    e_rs[it][1] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n + 1] : 0.f;
+  }
   __syncthreads();
 
   v16i acc[NSUB][kLimbs];
@@ -297,7 +316,9 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   }
   __syncthreads();
   // epilogue: thread -> (row, column pair)
-  for (int idx = threadIdx.x; idx < kGemmMT * NT / 2; idx += 256) {
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int idx = threadIdx.x + it * 256;
     const int row = idx / (NT / 2), cp = idx % (NT / 2);
     const int m = m0 + row;
     if (m >= M) continue;
@@ -314,22 +335,15 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
       yt[0] = tot[0]; yt[1] = tot[1];
       continue;
     }
-    const int e = rexp[m];
     float v[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      v[q] = ldexpf((float)tot[q], -e);
-      v[q] = __fadd_rn(__fmul_rn(v[q], scale[n + q]), bias[n + q]);
-    }
+    v[0] = __fadd_rn(__fmul_rn(ldexpf((float)tot[0], -e_ex[it]), e_sc0), e_bi0);
+    v[1] = __fadd_rn(__fmul_rn(ldexpf((float)tot[1], -e_ex[it]), e_sc1), e_bi1);
     if (epi == kEpiSwiGLU) {
       y[(int64_t)m * ldy + n / 2] = silu_mul(v[0], v[1]);
     } else if (epi == kEpiRope) {
       rope_store_pair(ra, m, n, v[0], v[1]);
     } else {
-      if (epi == kEpiResid) {
-        v[0] = resid[(int64_t)m * ldr + n] + v[0];
-        v[1] = resid[(int64_t)m * ldr + n + 1] + v[1];
-      }
+      if (epi == kEpiResid) { v[0] = e_rs[it][0] + v[0]; v[1] = e_rs[it][1] + v[1]; }
       y[(int64_t)m * ldy + n] = v[0];
       y[(int64_t)m * ldy + n + 1] = v[1];
     }
