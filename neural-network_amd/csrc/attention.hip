@@ -249,8 +249,12 @@ __global__ __launch_bounds__(kWave * W) void attn_kernel(
   const int hk = h / (H / Hkv);
   const int pos0 = base[b] + off + q0;
   const int kend_all = min(pos0 + nq, cap);
-  const int ks = sp * kps;
-  const int kend = min(ks + kps, kend_all);
+  // W > 1: the workgroup's visible keys are shared out over its W waves in
+  // whole chunks (kps from the host only bounds the capacity)
+  const int kspan = W == 1 ? kps
+      : (((kend_all + kChunk - 1) / kChunk + W - 1) / W) * kChunk;
+  const int ks = sp * kspan;
+  const int kend = min(ks + kspan, kend_all);
   const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
   const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
   const int r = min(lane / NQ4, KPI - 1), dq = lane % NQ4;
