@@ -222,6 +222,9 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch each kernel of a cycle separately instead "
                          "of replaying one HIP graph per cycle")
+    ap.add_argument("--option", action="append", default=[],
+                    metavar="KEY=VALUE",
+                    help="nnhip_set_option before the run (repeatable)")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU only: every box in this setup has a "
@@ -235,6 +238,9 @@ def main():
     if a.no_graphs:
         ctx.set_option("graphs", 0)
     ctx.set_option("groups", a.groups)
+    for kv in a.option:
+        key, val = kv.split("=")
+        ctx.set_option(key, int(val))
     r = run_cfg4(ctx, a.steps, a.warmup)
     roof = roofline_attention(ctx)
     b1 = None if a.no_batch1 else run_cfg2(ctx)

@@ -61,6 +61,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * 0 = always 32x32 tiles (default; process-wide).
  * "attn_waves": number of (key split) waves an attention launch aims for;
  * the key range of each sequence is split accordingly (default 4096;
+ * process-wide).
+ * "gemm_fk": 1 = the LDS-resident GEMM runs as full-K waves (8 waves, each
+ * 32 columns over all of K) instead of 16 K-split waves (default 0;
  * process-wide). */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);

@@ -70,6 +70,7 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
     if (std::strcmp(key, "graphs") == 0) ctx->c.use_graphs = value != 0;
     else if (std::strcmp(key, "groups") == 0) ctx->c.groups = value;
     else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
+    else if (std::strcmp(key, "gemm_fk") == 0) nnhip::g_gemm_fk = value != 0;
     else if (std::strcmp(key, "attn_waves") == 0) {
       REQ(value >= 64 && value <= (1 << 20), "attn_waves must be in [64, 2^20]");
       nnhip::g_attn_waves = value;

@@ -78,10 +78,31 @@ __global__ __launch_bounds__(256) void embed_kernel(
   const float *src = emb + (int64_t)id * d;
   float *dst = x + (int64_t)t * d;
   float mx = 0.f;
-  for (int i = threadIdx.x; i < d; i += blockDim.x) {
-    const float v = src[i];
-    dst[i] = v;
-    if (limbs) { srow[i] = v; mx = fmaxf(mx, fabsf(v)); }
+  if (d <= 4096 && ((d & 3) | (((uintptr_t)emb | (uintptr_t)x) & 15)) == 0) {
+    // float4 pieces, at most 4 per thread (d <= 4096), all requested before
+    // any is stored
+    const int np = d >> 2;
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = reinterpret_cast<const float4 *>(src)[min((int)threadIdx.x + 256 * j, np - 1)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int p = threadIdx.x + 256 * j;
+      if (p >= np) break;
+      reinterpret_cast<float4 *>(dst)[p] = v[j];
+      if (limbs) {
+        reinterpret_cast<float4 *>(srow)[p] = v[j];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                             fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+      const float v = src[i];
+      dst[i] = v;
+      if (limbs) { srow[i] = v; mx = fmaxf(mx, fabsf(v)); }
+    }
   }
   if (limbs) store_row_digits<256>(srow, d, mx, t, limbs, mpad, rexp, sred);
 }

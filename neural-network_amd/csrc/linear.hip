@@ -19,6 +19,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 namespace nnhip {
 
 namespace {
@@ -352,20 +354,26 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
 
 // ---------------------------------------------------------------------------
 // int8 MFMA GEMM with the activation digits resident in LDS (K <= 1024).
-// One workgroup of 16 waves owns a 32-row x 32*CT-column tile: wave
+// One workgroup of 16 waves owns a 32*CT-column block and walks `rpt`
+// consecutive 32-row tiles with its weight slice held in registers, so the
+// weights are read once per workgroup however many rows there are: wave
 // (column tile ct, K slice ks) multiplies its 32 columns over K/KS of the K
 // range (KS = min(4, K/128), CT = 16/KS); the slices' int64 totals are
 // summed in LDS with 64-bit integer atomics (exact, order-free) and the
-// epilogue runs over the summed tile.  Every
-// global load is issued at the start -- the weight slice into registers,
-// the per-column scale and bias and the LayerNorm parameters into LDS, the
-// residual into registers -- so a workgroup waits for memory about once.
+// epilogue runs over the summed tile.
+// Loads are issued in the order they are needed -- the per-column vectors
+// and the residual, the first row tile's activations, then the weight slice
+// -- so the prologue works on the activations while the weights stream in,
+// and the first tile's MFMAs on a chunk wait only for that chunk.  The next
+// row tile's digits are copied into LDS as soon as every wave is done with
+// the current tile's, so they arrive during its epilogue.
 // The 32 x K digit tile (3 planes, MFMA operand layout) is built by the
 // prologue:
 //   kAFromDigits     copied from digit planes written by another kernel,
 //   kAFromRows       digitised from fp32 rows (x, ldx),
 //   kAFromLayerNorm  LayerNorm (layer.cpp:242-261) of fp32 rows, written
 //                    to ln_out by the first column block, then digitised.
+// Only kAFromDigits walks more than one row tile (rpt > 1).
 // ---------------------------------------------------------------------------
 constexpr int kLdsThreads = 1024;
 
@@ -377,7 +385,7 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
     int M, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
+    int64_t ldy, int epi, int ntm, int ntn, int rpt, RopeArgs ra) {
   constexpr int K = KPT * 32;
   constexpr int nch = K / 128;
   constexpr int KS = nch < 4 ? nch : 4;       // K slices
@@ -388,32 +396,26 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
   constexpr int kRedLd = 33;                  // padded row of the sum tile
   constexpr int kABytes = kLimbs * kPlane;
   constexpr bool kLN = MODE == kAFromLayerNorm;
+  constexpr bool kDig = MODE == kAFromDigits;
   __shared__ __attribute__((aligned(16))) int8_t sa[kABytes];
   __shared__ long long red[CT][kGemmMT][kRedLd];
   __shared__ float s_sc[NC], s_bi[NC];
   __shared__ __attribute__((aligned(16))) float s_g[kLN ? K : 4], s_b[kLN ? K : 4];
-  __shared__ int s_e[kGemmMT];
-  const int T = ntm * ntn;
+  __shared__ int s_e[2][kGemmMT];
+  const int rt = kDig ? rpt : 1;              // row tiles per workgroup
+  const int ngr = (ntm + rt - 1) / rt;        // row-tile groups
+  const int T = ngr * ntn;
   const int per = (T + 7) / 8;
   const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
   if (wi >= T) return;
-  const int tn = wi / ntm, tm = wi % ntm;
-  const int m0 = tm * kGemmMT, n0 = tn * NC;
+  const int tn = wi / ngr, tg = wi % ngr;
+  const int tmb = tg * rt, tme = min(ntm, tmb + rt);
+  const int n0 = tn * NC;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ct = w % CT, ks = w / CT;
   const int nw = n0 + 32 * ct;                // this wave's column tile
 
-  // ---- loads: weight slice, per-column and LayerNorm vectors, residual ----
-  v4i bf[CPW][4];
-  {
-    const int nt = min(nw, N - 32);           // past N: the last tile, unused
-    const int8_t *pb = wq + (int64_t)(nt >> 5) * nch * 4096 + lane * 16;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        bf[c][s] = *reinterpret_cast<const v4i *>(pb + (ks * CPW + c) * 4096 + s * 1024);
-  }
+  // ---- small operands: per-column and LayerNorm vectors, residual ----
   float vsc = 0.f, vbi = 0.f;
   if (tid < NC && n0 + tid < N && epi != kEpiTotals) {
     vsc = scale[n0 + tid];
@@ -424,44 +426,83 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
   // epilogue items: thread -> (row, column pair)
   constexpr int ITEMS = kGemmMT * NC / 2 / kLdsThreads;
   float e_rs[ITEMS][2];
+  auto load_resid = [&](int tm) {
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int idx = tid + it * kLdsThreads;
-    const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
-    const int m = m0 + row, n = n0 + c0;
-    const bool ok = epi == kEpiResid && m < M && n < N;
-    e_rs[it][0] = ok ? resid[(int64_t)m * ldr + n] : 0.f;
-    e_rs[it][1] = ok ? resid[(int64_t)m * ldr + n + 1] : 0.f;
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = tid + it * kLdsThreads;
+      const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+      const int m = tm * kGemmMT + row, n = n0 + c0;
+      const bool ok = epi == kEpiResid && m < M && n < N;
+      e_rs[it][0] = ok ? resid[(int64_t)m * ldr + n] : 0.f;
+      e_rs[it][1] = ok ? resid[(int64_t)m * ldr + n + 1] : 0.f;
+    }
+  };
+  load_resid(tmb);
+
+  // ---- the first row tile's activations ----
+  // digits: 16-byte pieces of the 32 x K tile, consecutive pieces on
+  // consecutive lanes (a wave's 64 pieces are one 1 KB run of a plane);
+  // rows: thread (row rr, part pp) takes entries 4pp + 128i, i < K/128
+  constexpr int kPieces = kABytes / 16;
+  constexpr int kPer = kDig ? (kPieces + kLdsThreads - 1) / kLdsThreads : 1;
+  constexpr int PP = kDig ? 1 : K / 128;
+  const int64_t plane = (int64_t)mpad * K;
+  auto row_exps = [&](int tm) {
+    return tid < kGemmMT && tm * kGemmMT + tid < M ? rexp[tm * kGemmMT + tid] : 0;
+  };
+  v4i apc[kPer];
+  float4 v[PP];
+  int a_e = 0;
+  const int rr = tid >> 5, pp = tid & 31;
+  const bool live = tmb * kGemmMT + rr < M;
+  if constexpr (kDig) {
+    a_e = row_exps(tmb);
+    const int8_t *src = limbs + (int64_t)tmb * nch * 4096;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = min(tid + j * kLdsThreads, kPieces - 1);
+      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
+      apc[j] = *reinterpret_cast<const v4i *>(src + l * plane + o);
+    }
+  } else {
+    const int m = tmb * kGemmMT + rr;
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      v[i] = live ? *reinterpret_cast<const float4 *>(x + (int64_t)m * ldx + 4 * pp + 128 * i)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  // ---- the weight slice ----
+  v4i bf[CPW][4];
+  {
+    const int nt = min(nw, N - 32);           // past N: the last tile, unused
+    const int8_t *pb = wq + (int64_t)(nt >> 5) * nch * 4096 + lane * 16;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        bf[c][s] = *reinterpret_cast<const v4i *>(pb + (ks * CPW + c) * 4096 + s * 1024);
   }
 
   if constexpr (KS > 1)
     for (int i = tid; i < CT * kGemmMT * kRedLd; i += kLdsThreads)
       (&red[0][0][0])[i] = 0;
+  if (tid < NC) { s_sc[tid] = vsc; s_bi[tid] = vbi; }
 
-  // ---- prologue: the 32 x K digit tile in LDS ----
-  if constexpr (MODE == kAFromDigits) {
-    const int8_t *src = limbs + (int64_t)tm * nch * 4096;
-    const int64_t plane = (int64_t)mpad * K;
-    for (int i = tid; i < kLimbs * kPlane / 16; i += kLdsThreads) {
-      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
-      *reinterpret_cast<v4i *>(sa + l * kPlane + o) =
-          *reinterpret_cast<const v4i *>(src + l * plane + o);
+  // ---- prologue: the first 32 x K digit tile in LDS ----
+  if constexpr (kDig) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kLdsThreads;
+      if (kPieces % kLdsThreads == 0 || i < kPieces) {
+        const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
+        *reinterpret_cast<v4i *>(sa + l * kPlane + o) = apc[j];
+      }
     }
-    if (tid < kGemmMT) s_e[tid] = m0 + tid < M ? rexp[m0 + tid] : 0;
-    if (tid < NC) { s_sc[tid] = vsc; s_bi[tid] = vbi; }
+    if (tid < kGemmMT) s_e[0][tid] = a_e;
   } else {
 #pragma clang fp contract(off)
-    // thread -> (row r, part p): entries 4p + 128i, i < K/128, as float4
-    constexpr int PP = K / 128;
-    const int r = tid >> 5, p = tid & 31;
-    const int m = m0 + r;
-    const bool live = m < M;
-    float4 v[PP];
-#pragma unroll
-    for (int i = 0; i < PP; ++i)
-      v[i] = live ? *reinterpret_cast<const float4 *>(x + (int64_t)m * ldx + 4 * p + 128 * i)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < NC) { s_sc[tid] = vsc; s_bi[tid] = vbi; }
+    const int m = tmb * kGemmMT + rr;
     if (kLN && tid < K) { s_g[tid] = vg; s_b[tid] = vb; }
     // sums / maxima over the 32 lanes of a row (aligned half-waves)
     auto row_sum = [](float a) {
@@ -492,7 +533,7 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
       const bool wr = ln_out && tn == 0 && live;
 #pragma unroll
       for (int i = 0; i < PP; ++i) {
-        const int k = 4 * p + 128 * i;
+        const int k = 4 * pp + 128 * i;
         const float4 gg = *reinterpret_cast<const float4 *>(s_g + k);
         const float4 bb = *reinterpret_cast<const float4 *>(s_b + k);
         v[i].x = (v[i].x - mean) / sd * gg.x + bb.x;
@@ -509,14 +550,14 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
                            fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     mx = row_max(mx);
     const int e = digit_exponent(mx);
-    if (p == 0) s_e[r] = live ? e : 0;
+    if (pp == 0) s_e[0][rr] = live ? e : 0;
 #pragma unroll
     for (int i = 0; i < PP; ++i) {
-      const int k = 4 * p + 128 * i;
+      const int k = 4 * pp + 128 * i;
       const float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
       int3 d = digits4(f, e);
       if (!live) d = make_int3(0, 0, 0);
-      const int o = (int)mfma_operand_offset(r, k, K);
+      const int o = (int)mfma_operand_offset(rr, k, K);
       *reinterpret_cast<int *>(sa + o) = d.x;
       *reinterpret_cast<int *>(sa + kPlane + o) = d.y;
       *reinterpret_cast<int *>(sa + 2 * kPlane + o) = d.z;
@@ -524,65 +565,403 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
   }
   __syncthreads();
 
-  // ---- the wave's K slice; its totals are stored (one slice) or added
-  // (int64 atomics) into the summed tile ----
-  if (nw < N) {
-    v16i acc[kLimbs];
+  // one row tile: MFMAs over the wave's K slice, the slices summed into the
+  // tile of totals, then the epilogue; when another tile follows, its digits
+  // go straight into the tile buffer meanwhile (global_load_lds puts lane
+  // i's 16 bytes at the wave's LDS address + 16 i)
+  auto row_tile = [&](int tm) {
+    const int buf = (tm - tmb) & 1;
+    const bool more = tm + 1 < tme;
+    if (nw < N) {
+      v16i acc[kLimbs];
 #pragma unroll
-    for (int l = 0; l < kLimbs; ++l) acc[l] = v16i{};
-    const int8_t *pa = sa + lane * 16;
+      for (int l = 0; l < kLimbs; ++l) acc[l] = v16i{};
+      const int8_t *pa = sa + lane * 16;
 #pragma unroll
-    for (int c = 0; c < CPW; ++c)
+      for (int c = 0; c < CPW; ++c)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int off = (ks * CPW + c) * 4096 + s * 1024;
+        for (int s = 0; s < 4; ++s) {
+          const int off = (ks * CPW + c) * 4096 + s * 1024;
 #pragma unroll
-        for (int l = 0; l < kLimbs; ++l) {
-          const v4i a = *reinterpret_cast<const v4i *>(pa + l * kPlane + off);
-          acc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bf[c][s], acc[l], 0, 0, 0);
+          for (int l = 0; l < kLimbs; ++l) {
+            const v4i a = *reinterpret_cast<const v4i *>(pa + l * kPlane + off);
+            acc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bf[c][s], acc[l], 0, 0, 0);
+          }
+        }
+      // lane holds column (lane & 31) of rows (j >> 2) * 8 + (lane >> 5) * 4 +
+      // (j & 3), j < 16
+      long long *rp = &red[ct][(lane >> 5) * 4][lane & 31];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const long long tot = (long long)acc[0][j] * 65536LL +
+                              (long long)acc[1][j] * 256LL + (long long)acc[2][j];
+        long long *q = rp + ((j >> 2) * 8 + (j & 3)) * kRedLd;
+        if constexpr (KS == 1) *q = tot;
+        else atomicAdd(reinterpret_cast<unsigned long long *>(q), (unsigned long long)tot);
+      }
+    }
+    __syncthreads();
+
+    // ---- epilogue over the summed tile: its LDS operands are read first
+    // (the totals cleared behind them when another tile follows), then the
+    // next tile's digit copy is started, then the outputs are formed ----
+    const int m0 = tm * kGemmMT;
+    long long et[ITEMS][2];
+    float esc[ITEMS][2], ebi[ITEMS][2];
+    int eex[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = tid + it * kLdsThreads;
+      const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+      long long *rq = &red[c0 >> 5][row][c0 & 31];
+      et[it][0] = rq[0]; et[it][1] = rq[1];
+      if (KS > 1 && more) { rq[0] = 0; rq[1] = 0; }
+      eex[it] = s_e[buf][row];
+      esc[it][0] = s_sc[c0]; esc[it][1] = s_sc[c0 + 1];
+      ebi[it][0] = s_bi[c0]; ebi[it][1] = s_bi[c0 + 1];
+    }
+    if (kDig && more) {
+      a_e = row_exps(tm + 1);
+      const int8_t *src = limbs + (int64_t)(tm + 1) * nch * 4096;
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i0 = w * kWave + j * kLdsThreads;
+        if (kPieces % kLdsThreads == 0 || i0 < kPieces) {
+          const int l = i0 / (kPlane / 16), o = (i0 % (kPlane / 16)) * 16;
+          __builtin_amdgcn_global_load_lds(
+              (__attribute__((address_space(1))) void *)(src + l * plane + o + lane * 16),
+              (__attribute__((address_space(3))) void *)(sa + l * kPlane + o), 16, 0, 0);
         }
       }
-    // lane holds column (lane & 31) of rows (j >> 2) * 8 + (lane >> 5) * 4 +
-    // (j & 3), j < 16
-    long long *rp = &red[ct][(lane >> 5) * 4][lane & 31];
+    }
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int idx = tid + it * kLdsThreads;
+      const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+      const int m = m0 + row, n = n0 + c0;
+      if (m >= M || n >= N) continue;
+      if (epi == kEpiTotals) {
+        long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
+        yt[0] = et[it][0]; yt[1] = et[it][1];
+        continue;
+      }
+      float v0 = ldexpf((float)et[it][0], -eex[it]), v1 = ldexpf((float)et[it][1], -eex[it]);
+      v0 = __fadd_rn(__fmul_rn(v0, esc[it][0]), ebi[it][0]);
+      v1 = __fadd_rn(__fmul_rn(v1, esc[it][1]), ebi[it][1]);
+      if (epi == kEpiSwiGLU) {
+        y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
+      } else if (epi == kEpiRope) {
+        rope_store_pair(ra, m, n, v0, v1);
+      } else {
+        if (epi == kEpiResid) { v0 = e_rs[it][0] + v0; v1 = e_rs[it][1] + v1; }
+        y[(int64_t)m * ldy + n] = v0;
+        y[(int64_t)m * ldy + n + 1] = v1;
+      }
+    }
+    if (kDig && more) {
+      if (tid < kGemmMT) s_e[buf ^ 1][tid] = a_e;
+      load_resid(tm + 1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // digits in LDS
+      __syncthreads();
+    }
+  };
+  // the first tile apart from the loop, so that its MFMAs wait for the
+  // weight chunks one at a time
+  row_tile(tmb);
+  for (int tm = tmb + 1; tm < tme; ++tm) row_tile(tm);
+}
+
+// ---------------------------------------------------------------------------
+// int8 MFMA GEMM with full-K waves.  One workgroup of 8 waves (two per SIMD,
+// so a wave may hold up to 256 registers) owns a 256-column block: wave w
+// multiplies columns n0 + 32w .. n0 + 32w + 31 over the whole of K with its
+// weights resident in registers (K/8 of them).  No partial sums cross waves,
+// so there is no reduction tile: the epilogue runs on the MFMA accumulators
+// (lane holds column lane & 31 of rows (j >> 2) * 8 + (lane >> 5) * 4 +
+// (j & 3), j < 16; gate/up and RoPE pairs are adjacent lanes).  The 32 x K
+// digit tile sits in LDS, shared by the 8 waves, and is built by the same
+// prologues as gemm_lds_kernel (digit planes / fp32 rows / LayerNorm of fp32
+// rows).  All loads are issued at the start, the activations first and the
+// weights behind them, so the MFMAs of a chunk wait only for that chunk.
+// Same integers and the same rounding steps as gemm_lds_kernel and
+// gemm_limb_kernel: the three GEMMs give bit-identical outputs.
+// ---------------------------------------------------------------------------
+constexpr int kFkWaves = 8;
+constexpr int kFkThreads = kFkWaves * kWave;
+
+template <int MODE, int KPT, bool RES>
+__global__ __launch_bounds__(kFkThreads) void gemm_fk_kernel(
+    const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
+    const float *__restrict__ x, int64_t ldx, const float *__restrict__ lng,
+    const float *__restrict__ lnb, float *__restrict__ ln_out, int64_t ldo,
+    int M, int N, const int8_t *__restrict__ wq,
+    const float *__restrict__ scale, const float *__restrict__ bias,
+    const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
+    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
+  constexpr int K = KPT * 32;
+  constexpr int nch = K / 128;
+  constexpr int NC = 32 * kFkWaves;           // columns per workgroup
+  constexpr int kPlane = kGemmMT * K;         // bytes per digit plane
+  constexpr int kABytes = kLimbs * kPlane;
+  constexpr bool kLN = MODE == kAFromLayerNorm;
+  constexpr bool kDig = MODE == kAFromDigits;
+  __shared__ __attribute__((aligned(16))) int8_t sa[kABytes];
+  __shared__ __attribute__((aligned(16))) float s_g[kLN ? K : 4], s_b[kLN ? K : 4];
+  __shared__ int s_e[kGemmMT];
+  const int T = ntm * ntn;
+  const int per = (T + 7) / 8;
+  const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (wi >= T) return;
+  const int tn = wi / ntm, tm = wi % ntm;
+  const int m0 = tm * kGemmMT, n0 = tn * NC;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nw = n0 + 32 * w;                 // this wave's column tile
+  const bool wcols = nw < N;                  // N % 32 == 0: all or none
+  const int hh = lane >> 5;
+  const int n = nw + (lane & 31);             // this lane's column
+
+  // ---- small operands: per-column vectors, the residual (RES) and the
+  // row exponent of row lane & 31 (digit planes) ----
+  float csc = 0.f, cbi = 0.f;
+  if (wcols && epi != kEpiTotals) { csc = scale[n]; cbi = bias[n]; }
+  // (with fp32 rows the residual is requested after the prologue, whose
+  // rows already hold many registers)
+  float ers[RES ? 16 : 1];
+  auto load_resid = [&]() {
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
+        ers[j] = m < M && wcols ? resid[(int64_t)m * ldr + n] : 0.f;
+      }
+    }
+  };
+  if constexpr (kDig) load_resid();
+  int e_lane = 0;
+  if (kDig && m0 + (lane & 31) < M) e_lane = rexp[m0 + (lane & 31)];
+
+  // ---- the first row tile's activations ----
+  // digits: 16-byte pieces of the 32 x K tile, consecutive pieces on
+  // consecutive lanes (a wave's 64 pieces are one 1 KB run of a plane);
+  // rows: thread (row rr, part pp) takes entries 4pp + 64i, i < K/64
+  constexpr int kPieces = kABytes / 16;
+  static_assert(kPieces % kWave == 0, "whole pieces per wave");
+  constexpr int kPer = kDig ? (kPieces + kFkThreads - 1) / kFkThreads : 1;
+  constexpr int PP = kDig ? 1 : K / 64;
+  const int64_t plane = (int64_t)mpad * K;
+  float4 v[PP];
+  v4i apc[kPer];
+  const int rr = tid >> 4, pp = tid & 15;
+  const bool live = m0 + rr < M;
+  if constexpr (kDig) {
+    const int8_t *src = limbs + (int64_t)tm * nch * 4096;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = min(tid + j * kFkThreads, kPieces - 1);
+      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
+      apc[j] = *reinterpret_cast<const v4i *>(src + l * plane + o);
+    }
+  } else {
+    const int m = m0 + rr;
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      v[i] = live ? *reinterpret_cast<const float4 *>(x + (int64_t)m * ldx + 4 * pp + 64 * i)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // LayerNorm parameters: entries tid and tid + 512
+  float vg[2] = {0.f, 0.f}, vb[2] = {0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    if (kLN && tid + h * kFkThreads < K) {
+      vg[h] = lng[tid + h * kFkThreads];
+      vb[h] = lnb[tid + h * kFkThreads];
+    }
+
+  // ---- the wave's weights over all of K ----
+  v4i bf[nch][4];
+  {
+    const int nt = min(nw, N - 32);           // past N: the last tile, unused
+    const int8_t *pb = wq + (int64_t)(nt >> 5) * nch * 4096 + lane * 16;
+#pragma unroll
+    for (int c = 0; c < nch; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        bf[c][s] = *reinterpret_cast<const v4i *>(pb + c * 4096 + s * 1024);
+  }
+  // RoPE: the sequence state of row lane & 31 (its position is formed in
+  // the epilogue)
+  RopeRow rrow{0, 0, 0};
+  const bool rrow_ok = epi == kEpiRope && m0 + (lane & 31) < M;
+  if (rrow_ok) rrow = rope_row_read(ra, m0 + (lane & 31));
+  __builtin_amdgcn_sched_barrier(0);          // every load issued before the prologue
+
+  // ---- prologue: the first 32 x K digit tile in LDS ----
+  if constexpr (kDig) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kFkThreads;
+      if (kPieces % kFkThreads == 0 || i < kPieces) {
+        const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
+        *reinterpret_cast<v4i *>(sa + l * kPlane + o) = apc[j];
+      }
+    }
+  } else {
+#pragma clang fp contract(off)
+    const int m = m0 + rr;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (kLN && tid + h * kFkThreads < K) {
+        s_g[tid + h * kFkThreads] = vg[h];
+        s_b[tid + h * kFkThreads] = vb[h];
+      }
+    // sums / maxima over the 16 lanes of a row
+    auto row_sum = [](float a) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) a += __shfl_xor(a, o, kWave);
+      return a;
+    };
+    auto row_max = [](float a) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
+      return a;
+    };
+    if constexpr (kLN) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+      const float Nf = (float)K;
+      const float mean = row_sum(s) / Nf;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) {
+        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean,
+                    d = v[i].w - mean;
+        sq += (a * a + b * b) + (c * c + d * d);
+      }
+      const float sd = sqrtf(row_sum(sq) / Nf + 1e-5f);
+      __syncthreads();                        // s_g, s_b written
+      const bool wr = ln_out && tn == 0 && live;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) {
+        const int k = 4 * pp + 64 * i;
+        const float4 gg = *reinterpret_cast<const float4 *>(s_g + k);
+        const float4 bb = *reinterpret_cast<const float4 *>(s_b + k);
+        v[i].x = (v[i].x - mean) / sd * gg.x + bb.x;
+        v[i].y = (v[i].y - mean) / sd * gg.y + bb.y;
+        v[i].z = (v[i].z - mean) / sd * gg.z + bb.z;
+        v[i].w = (v[i].w - mean) / sd * gg.w + bb.w;
+        if (wr) *reinterpret_cast<float4 *>(ln_out + (int64_t)m * ldo + k) = v[i];
+      }
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                           fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    mx = row_max(mx);
+    const int e = digit_exponent(mx);
+    if (pp == 0) s_e[rr] = live ? e : 0;
+#pragma unroll
+    for (int i = 0; i < PP; ++i) {
+      const int k = 4 * pp + 64 * i;
+      const float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      int3 d = digits4(f, e);
+      if (!live) d = make_int3(0, 0, 0);
+      const int o = (int)mfma_operand_offset(rr, k, K);
+      *reinterpret_cast<int *>(sa + o) = d.x;
+      *reinterpret_cast<int *>(sa + kPlane + o) = d.y;
+      *reinterpret_cast<int *>(sa + 2 * kPlane + o) = d.z;
+    }
+  }
+  __syncthreads();
+  if constexpr (!kDig) {
+    e_lane = s_e[lane & 31];
+    load_resid();
+  }
+
+  // ---- the wave's MFMAs over all of K ----
+  v16i acc[kLimbs];
+#pragma unroll
+  for (int l = 0; l < kLimbs; ++l) acc[l] = v16i{};
+  if (wcols) {
+    // the A operands of one step ahead are read while a step's MFMAs run;
+    // the scheduling barriers keep the reads from being hoisted further
+    // (the resident weights leave few registers)
+    const int8_t *pa = sa + lane * 16;
+    v4i a0[kLimbs], a1[kLimbs];
+#pragma unroll
+    for (int l = 0; l < kLimbs; ++l) a0[l] = *reinterpret_cast<const v4i *>(pa + l * kPlane);
+#pragma unroll
+    for (int st = 0; st < nch * 4; ++st) {
+      v4i (&cur)[kLimbs] = (st & 1) ? a1 : a0;
+      v4i (&nxt)[kLimbs] = (st & 1) ? a0 : a1;
+      if (st + 1 < nch * 4) {
+        const int off = ((st + 1) >> 2) * 4096 + ((st + 1) & 3) * 1024;
+#pragma unroll
+        for (int l = 0; l < kLimbs; ++l)
+          nxt[l] = *reinterpret_cast<const v4i *>(pa + l * kPlane + off);
+      }
+#pragma unroll
+      for (int l = 0; l < kLimbs; ++l)
+        acc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[l], bf[st >> 2][st & 3], acc[l], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue on the accumulators ----
+  if (epi == kEpiRope) {
+    // every value and every cos / sin is read before the first store;
+    // column pairs (2i, 2i + 1) sit on lanes (2i, 2i + 1)
+    float v0[16], v1[16], cs[16], sn[16];
+    int pos[16];
+    const bool vpart = n / (ra.H * ra.D) == 2;
+    // (the empty asm keeps the row state untouched until here, so that
+    // nothing waits for its reads before the MFMAs)
+    asm volatile("" : "+v"(rrow.base), "+v"(rrow.act));
+    const int pos_lane = rrow_ok ? rope_row_pos(ra, rrow) : -1;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const long long tot = (long long)acc[0][j] * 65536LL +
                             (long long)acc[1][j] * 256LL + (long long)acc[2][j];
-      long long *q = rp + ((j >> 2) * 8 + (j & 3)) * kRedLd;
-      if constexpr (KS == 1) *q = tot;
-      else atomicAdd(reinterpret_cast<unsigned long long *>(q), (unsigned long long)tot);
+      const int row = (j >> 2) * 8 + hh * 4 + (j & 3);
+      const int e = __shfl(e_lane, row, kWave);
+      v0[j] = __fadd_rn(__fmul_rn(ldexpf((float)tot, -e), csc), cbi);
+      v1[j] = __shfl_xor(v0[j], 1, kWave);
+      pos[j] = __shfl(pos_lane, row, kWave);
     }
-  }
-  __syncthreads();
-
-  // ---- epilogue over the summed tile ----
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int idx = tid + it * kLdsThreads;
-    const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
-    const int m = m0 + row, n = n0 + c0;
-    if (m >= M || n >= N) continue;
-    const long long t0 = red[c0 >> 5][row][c0 & 31];
-    const long long t1 = red[c0 >> 5][row][(c0 & 31) + 1];
-    if (epi == kEpiTotals) {
-      long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
-      yt[0] = t0; yt[1] = t1;
+    for (int j = 0; j < 16; ++j) {
+      const float2 c = vpart ? make_float2(0.f, 0.f) : rope_cos_sin(ra, max(pos[j], 0), n);
+      cs[j] = c.x; sn[j] = c.y;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
+      if ((n & 1) || m >= M || !wcols || pos[j] < 0) continue;
+      rope_store_pair_at(ra, m, pos[j], n, v0[j], v1[j], cs[j], sn[j]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
+    const long long tot = (long long)acc[0][j] * 65536LL +
+                          (long long)acc[1][j] * 256LL + (long long)acc[2][j];
+    const int e = __shfl(e_lane, (j >> 2) * 8 + hh * 4 + (j & 3), kWave);
+    float v0 = ldexpf((float)tot, -e);
+    v0 = __fadd_rn(__fmul_rn(v0, csc), cbi);
+    if (epi == kEpiSwiGLU) {
+      // gate / up pairs (2i, 2i + 1) sit on lanes (2i, 2i + 1)
+      const float v1 = __shfl_xor(v0, 1, kWave);
+      if ((n & 1) || m >= M || !wcols) continue;
+      y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
       continue;
     }
-    const int e = s_e[row];
-    float v0 = ldexpf((float)t0, -e), v1 = ldexpf((float)t1, -e);
-    v0 = __fadd_rn(__fmul_rn(v0, s_sc[c0]), s_bi[c0]);
-    v1 = __fadd_rn(__fmul_rn(v1, s_sc[c0 + 1]), s_bi[c0 + 1]);
-    if (epi == kEpiSwiGLU) {
-      y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
-    } else if (epi == kEpiRope) {
-      rope_store_pair(ra, m, n, v0, v1);
-    } else {
-      if (epi == kEpiResid) { v0 = e_rs[it][0] + v0; v1 = e_rs[it][1] + v1; }
-      y[(int64_t)m * ldy + n] = v0;
-      y[(int64_t)m * ldy + n + 1] = v1;
-    }
+    if (m >= M || !wcols) continue;
+    if (epi == kEpiTotals)
+      reinterpret_cast<long long *>(y)[(int64_t)m * ldy + n] = tot;
+    else
+      y[(int64_t)m * ldy + n] = RES ? ers[RES ? j : 0] + v0 : v0;
   }
 }
 
@@ -732,6 +1111,7 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
 // 1: allow 32x64 GEMM tiles for large grids; 0: always 32x32 (default,
 // measured faster on every decode shape).
 int g_gemm_wide = 0;
+int g_gemm_fk = 0;
 
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
@@ -805,6 +1185,44 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   NNHIP_CHECK(hipGetLastError());
 }
 
+// full-K-wave GEMM (gemm_fk_kernel) over the same operands as the LDS GEMM
+static void launch_gemm_fk(hipStream_t st, int mode, const int8_t *limbs,
+                           int mpad, const int *rexp, const float *x,
+                           int64_t ldx, const float *lng, const float *lnb,
+                           float *ln_out, int64_t ldo, int rows, int K, int N,
+                           const int8_t *wq, const float *scale,
+                           const float *bias, const float *resid, int64_t ldr,
+                           float *y, int64_t ldy, int epi, const RopeArgs &rz,
+                           int ntm) {
+  const int ntn = (N + 32 * kFkWaves - 1) / (32 * kFkWaves);
+  const int per = (ntm * ntn + 7) / 8;
+  dim3 grid(8 * per);
+#define NNHIP_FK(MD, KP)                                                      \
+  if (epi == kEpiResid)                                                       \
+    hipLaunchKernelGGL((gemm_fk_kernel<MD, KP, true>), grid, dim3(kFkThreads),\
+                       0, st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out,    \
+                       ldo, rows, N, wq, scale, bias, resid, ldr, y, ldy,     \
+                       epi, ntm, ntn, rz);                                    \
+  else                                                                        \
+    hipLaunchKernelGGL((gemm_fk_kernel<MD, KP, false>), grid,                 \
+                       dim3(kFkThreads), 0, st, limbs, mpad, rexp, x, ldx,    \
+                       lng, lnb, ln_out, ldo, rows, N, wq, scale, bias,       \
+                       resid, ldr, y, ldy, epi, ntm, ntn, rz)
+#define NNHIP_FK_K(MD)                                                        \
+  switch (K) {                                                                \
+    case 128: NNHIP_FK(MD, 4); break;                                         \
+    case 256: NNHIP_FK(MD, 8); break;                                         \
+    case 512: NNHIP_FK(MD, 16); break;                                        \
+    default: NNHIP_FK(MD, 32); break;                                         \
+  }
+  if (mode == kAFromDigits) { NNHIP_FK_K(kAFromDigits) }
+  else if (mode == kAFromRows) { NNHIP_FK_K(kAFromRows) }
+  else { NNHIP_FK_K(kAFromLayerNorm) }
+#undef NNHIP_FK_K
+#undef NNHIP_FK
+  NNHIP_CHECK(hipGetLastError());
+}
+
 void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                      const int *rexp, const float *x, int64_t ldx,
                      const float *lng, const float *lnb, float *ln_out,
@@ -828,14 +1246,25 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                   kErrArg, "gemm_lds: LayerNorm parameters missing");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
+  if (g_gemm_fk && !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
+    launch_gemm_fk(st, mode, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,
+                   rows, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, rz, ntm);
+    return;
+  }
   const int ntn = (int)(gemm_lds_workgroups(rows, K, N) / ntm);
-  const int per = (ntm * ntn + 7) / 8;
+  // digit planes: a workgroup walks as many row tiles as it takes for all
+  // workgroups to be resident at once (one per CU), so that the weights are
+  // read once and no second wave of workgroups waits behind the first
+  int rpt = 1;
+  if (mode == kAFromDigits && ntm * ntn > kGemmSlots)
+    rpt = ntn >= kGemmSlots ? ntm : (ntm + kGemmSlots / ntn - 1) / (kGemmSlots / ntn);
+  const int per = ((ntm + rpt - 1) / rpt * ntn + 7) / 8;
   dim3 grid(8 * per);
 #define NNHIP_GL(MD, KP)                                                      \
   hipLaunchKernelGGL((gemm_lds_kernel<MD, KP>), grid, dim3(kLdsThreads), 0,   \
                      st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,    \
                      rows, N, wq, scale, bias, resid, ldr, y, ldy, epi, ntm,  \
-                     ntn, rz)
+                     ntn, rpt, rz)
 #define NNHIP_GL_K(MD)                                                        \
   switch (K) {                                                                \
     case 128: NNHIP_GL(MD, 4); break;                                         \

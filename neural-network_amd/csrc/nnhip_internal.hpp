@@ -95,14 +95,36 @@ struct RopeArgs {
   int64_t seq_stride = 0;
 };
 
+// Cache position of row m of a RoPE epilogue: base[b] + off + s for row
+// m = b*S + s, or -1 when the row is not written (inactive sequence,
+// position outside the cache).
+// The two reads (base[b], active[b]) and the arithmetic are separate steps
+// so that a kernel can issue the reads early and form the position late.
+struct RopeRow { int base, act, s; };
+__device__ inline RopeRow rope_row_read(const RopeArgs &ra, int64_t m) {
+  const int b = (int)(m / ra.S);
+  // without an active mask base[b] is read twice, unconditionally, so that
+  // nothing waits for the reads here
+  const int32_t *ap = ra.active ? ra.active : ra.base;
+  return RopeRow{ra.base[b], ap[b], (int)(m % ra.S)};
+}
+__device__ inline int rope_row_pos(const RopeArgs &ra, const RopeRow &r) {
+  const int pos = r.base + ra.off + r.s;
+  const bool act = !ra.active || r.act != 0;
+  return !act || pos < 0 || pos >= ra.cap ? -1 : pos;
+}
+__device__ inline int rope_row_pos(const RopeArgs &ra, int64_t m) {
+  return rope_row_pos(ra, rope_row_read(ra, m));
+}
+
 // Tensor::rope (tensor.cpp:1141-1173) on one pair (x_2j, x_2j+1) of output
-// column n (even) of row m, then the KV append of layer.cpp:758-807.
-__device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
-                                       float xe, float xo) {
-  const int b = (int)(m / ra.S), s = (int)(m % ra.S);
-  if (ra.active && !ra.active[b]) return;
-  const int pos = ra.base[b] + ra.off + s;
-  if (pos < 0 || pos >= ra.cap) return;
+// column n (even) of row m at cache position pos (>= 0), with the pair's
+// cos / sin already read (unused for the v part), then the KV append of
+// layer.cpp:758-807.
+__device__ inline void rope_store_pair_at(const RopeArgs &ra, int64_t m,
+                                          int pos, int n, float xe, float xo,
+                                          float c, float sn) {
+  const int b = (int)(m / ra.S);
   const int E = ra.H * ra.D;
   const int part = n / E, nn = n % E;
   const int h = nn / ra.D, j = (nn % ra.D) >> 1;
@@ -111,15 +133,29 @@ __device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
     vd[0] = xe; vd[1] = xo;
     return;
   }
-  const int half = ra.D >> 1;
-  const float c = ra.cosb[(int64_t)pos * half + j];
-  const float sn = ra.sinb[(int64_t)pos * half + j];
   const float r0 = __fsub_rn(__fmul_rn(xe, c), __fmul_rn(xo, sn));
   const float r1 = __fadd_rn(__fmul_rn(xe, sn), __fmul_rn(xo, c));
   float *dst = part == 0
                    ? ra.qrot + m * E + nn
                    : ra.kc + b * ra.seq_stride + ((int64_t)h * ra.cap + pos) * ra.D + 2 * j;
   dst[0] = r0; dst[1] = r1;
+}
+
+// cos / sin of column n's pair at position pos (>= 0)
+__device__ inline float2 rope_cos_sin(const RopeArgs &ra, int pos, int n) {
+  const int nn = n % (ra.H * ra.D), j = (nn % ra.D) >> 1, half = ra.D >> 1;
+  return make_float2(ra.cosb[(int64_t)pos * half + j], ra.sinb[(int64_t)pos * half + j]);
+}
+
+// rope_store_pair_at for row m, reading the row's position and the pair's
+// cos / sin itself.
+__device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
+                                       float xe, float xo) {
+  const int pos = rope_row_pos(ra, m);
+  if (pos < 0) return;
+  const bool vpart = n / (ra.H * ra.D) == 2;
+  const float2 cs = vpart ? make_float2(0.f, 0.f) : rope_cos_sin(ra, pos, n);
+  rope_store_pair_at(ra, m, pos, n, xe, xo, cs.x, cs.y);
 }
 
 // Activation limbs for the int8 MFMA GEMM: x[m][k] ~= X[m][k] * 2^-e[m] with
@@ -173,6 +209,9 @@ __device__ inline int digit_exponent(float mx) {
 
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
+extern int g_gemm_fk;        // LDS GEMM: 1 = full-K-wave kernel
+// workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
+constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
 // workgroups of one LDS-GEMM launch (32-row tiles x column blocks of
 // 32 * 16 / min(4, K/128) columns)

@@ -80,6 +80,28 @@ def test_forward_vs_oracle(ctx, quant, S):
     gm.free()
 
 
+# one layer at the batch-32 config's width (d 1024, 16 heads, MLP 4096)
+WIDE = dict(vocab=512, d=1024, H=16, F=4096, L=1)
+
+
+@pytest.mark.parametrize("fk", [0, 1])
+def test_forward_wide_vs_oracle(ctx, fk):
+    """80 rows through a d = 1024 layer: q/k/v with RoPE, the output
+    projection with its residual, gate/up with SwiGLU on the LDS-resident
+    GEMMs (16-wave K-split kernel, or full-K waves with fk = 1)."""
+    om, gm, _ = build(ctx, WIDE, 8, True, std=0.03)
+    rng = np.random.default_rng(9)
+    ids = rng.integers(0, 512, (2, 40)).astype(np.int32)
+    try:
+        ctx.set_option("gemm_fk", fk)
+        got = gm.forward(ids)
+    finally:
+        ctx.set_option("gemm_fk", 0)
+    for b in range(2):
+        assert_rows_close(got[b], om.forward(ids[b]), 1e-4, f"forward b={b}")
+    gm.free()
+
+
 @pytest.mark.parametrize("quant", [False, True])
 def test_forward_cache_truncate_vs_oracle(ctx, quant):
     om, gm, _ = build(ctx, TOY_T, 4, quant, std=0.05)
@@ -188,13 +210,19 @@ def test_batch_matches_oracle_per_sequence(ctx, T, groups):
     gt.free(); gd.free()
 
 
-def test_batch_mfma_rows_match_oracle(ctx):
-    """B = 20 rows of drafting use the MFMA digit GEMM (rows >= 16)."""
+@pytest.mark.parametrize("fk", [0, 1])
+def test_batch_mfma_rows_match_oracle(ctx, fk):
+    """B = 20 rows of drafting use the MFMA digit GEMM (rows >= 16); the
+    100-row verify and the 320-row prefill use the LDS-resident GEMMs."""
     ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 40, True, std=0.2)
     B = 20
     rng = np.random.default_rng(41)
     prompts = rng.integers(0, 256, (B, 16)).astype(np.int32)
-    got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
+    try:
+        ctx.set_option("gemm_fk", fk)
+        got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
+    finally:
+        ctx.set_option("gemm_fk", 0)
     for b in (0, 7, 19):
         want, _ = O.generate_speculative(ot, od, prompts[b], 24, 4, 0.0, 5,
                                          seq=b)
