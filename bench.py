@@ -146,7 +146,7 @@ def measured_traffic():
     return None
 
 
-def roofline_attention(ctx):
+def roofline_attention(ctx, w4=True):
     """Verify-step attention at the cfg4 mid-run shape: 32 sequences x 16
     heads, 6 queries, 320 cached keys (+6 new); one launch of the merged
     split kernel.  Algorithmic bytes: K and V of every visible key once, the
@@ -160,7 +160,10 @@ def roofline_attention(ctx):
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
                 traffic=measured_traffic(),
-                kernel="attn_kernel<8, 8, 8> (verify, splits merged in LDS)",
+                kernel=("attn_kernel<8, 8, 4> (verify, 4 key splits merged "
+                        "in LDS, 2 workgroups per CU)" if w4 else
+                        "attn_kernel<8, 8, 8> (verify, 8 key splits merged "
+                        "in LDS)"),
                 bytes_per_launch=byt, us_per_launch=round(ms * 1e3, 2))
 
 
@@ -242,7 +245,7 @@ def main():
         key, val = kv.split("=")
         ctx.set_option(key, int(val))
     r = run_cfg4(ctx, a.steps, a.warmup)
-    roof = roofline_attention(ctx)
+    roof = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
     b1 = None if a.no_batch1 else run_cfg2(ctx)
     cpu = None if a.no_cpu_baseline else cpu_baseline(r["models"])
     ms_step = r["wall_s"] / a.steps * 1e3

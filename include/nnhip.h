@@ -64,6 +64,13 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * process-wide).
  * "gemm_fk": 1 = the LDS-resident GEMM runs as full-K waves (8 waves, each
  * 32 columns over all of K) instead of 16 K-split waves (default 0;
+ * process-wide).
+ * "attn_w4": 1 = attention rows of 4+ queries run in workgroups of 4 key
+ * splits (two per CU) instead of 8 (default 1; process-wide).
+ * "lds_min_rows": the LDS-resident GEMM serves projections from this many
+ * rows on (default 64; process-wide).
+ * "fold_norm": 1 = a pending LayerNorm is folded into every LDS-resident
+ * GEMM's prologue, 0 = only into a short batch's lm head (default 0;
  * process-wide). */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);

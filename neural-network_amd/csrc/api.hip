@@ -71,6 +71,12 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
     else if (std::strcmp(key, "groups") == 0) ctx->c.groups = value;
     else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
     else if (std::strcmp(key, "gemm_fk") == 0) nnhip::g_gemm_fk = value != 0;
+    else if (std::strcmp(key, "lds_min_rows") == 0) {
+      REQ(value >= 16, "lds_min_rows must be >= 16");
+      nnhip::g_lds_min_rows = value;
+    }
+    else if (std::strcmp(key, "fold_norm") == 0) nnhip::g_fold_norm = value != 0;
+    else if (std::strcmp(key, "attn_w4") == 0) nnhip::g_attn_w4 = value != 0;
     else if (std::strcmp(key, "attn_waves") == 0) {
       REQ(value >= 64 && value <= (1 << 20), "attn_waves must be in [64, 2^20]");
       nnhip::g_attn_waves = value;

@@ -185,6 +185,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 32;
 constexpr int kMergedWaves = 8;    // key splits of a merged workgroup
+constexpr int kMergedWaves4 = 4;   // ... for 4+ queries (option attn_w4)
 constexpr int kMergedChunks = 4;   // at most this many chunks per split
 
 template <int CTRL>
@@ -237,7 +238,7 @@ __device__ __forceinline__ void load_lane_dims(const float *p, int sub,
 }
 
 template <int SQP, int DL, int W>
-__global__ __launch_bounds__(kWave * W) void attn_kernel(
+__global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
     const float *__restrict__ q, const float *__restrict__ kc,
     const float *__restrict__ vc, int S, int H, int Hkv, int cap,
     int64_t seq_stride, const int32_t *__restrict__ base, int off,
@@ -295,15 +296,21 @@ __global__ __launch_bounds__(kWave * W) void attn_kernel(
     for (int x = 0; x < 4; ++x) acc[i][x] = 0.f;
   float m_run = -INFINITY, l_loc = 0.f;
 
-  for (int c0 = ks; c0 < kend; c0 += kChunk) {
-    // every K and V row of the chunk is requested up front; rows past the
-    // split end re-read the last valid row and are masked
-    float kr[4][8];
-    float4 vv[TPV];
+  // A chunk's K and V rows are all requested before any arithmetic; rows
+  // past the split end re-read the last valid row and are masked.  The
+  // next chunk's K rows are requested before the current chunk is worked on
+  // (two register buffers, used in turn); its V rows, needed only after the
+  // scores, at the start of its own turn.
+  struct Chunk { float kr[4][8]; };
+  auto load_chunk = [&](int c0, Chunk &ck) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       load_lane_dims<DL>(kb + (int64_t)min(c0 + g + 8 * t, kend - 1) * D, sub,
-                         kr[t]);
+                         ck.kr[t]);
+  };
+  auto work_chunk = [&](int c0, const Chunk &ck) {
+    const auto &kr = ck.kr;
+    float4 vv[TPV];
 #pragma unroll
     for (int t = 0; t < TPV; ++t)
       vv[t] = *reinterpret_cast<const float4 *>(
@@ -392,6 +399,15 @@ __global__ __launch_bounds__(kWave * W) void attn_kernel(
       }
     }
     wave_lds_sync();
+  };
+  Chunk ca, cb;
+  if (ks < kend) load_chunk(ks, ca);
+  for (int c0 = ks; c0 < kend; c0 += 2 * kChunk) {
+    if (c0 + kChunk < kend) load_chunk(c0 + kChunk, cb);
+    work_chunk(c0, ca);
+    if (c0 + kChunk >= kend) break;
+    if (c0 + 2 * kChunk < kend) load_chunk(c0 + 2 * kChunk, ca);
+    work_chunk(c0 + kChunk, cb);
   }
   const float l = groups_sum(l_loc);
   if (pv_lane) {
@@ -696,6 +712,7 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
 }
 
 int g_attn_waves = 4096;
+int g_attn_w4 = 1;
 
 // Splits of the key range: about g_attn_waves waves over the whole launch
 // (4 per SIMD by default), each split a whole number of 32-key chunks.
@@ -745,17 +762,19 @@ bool launch_attention(hipStream_t st, const float *q, const float *kc,
     int kps = (max_keys + kMergedWaves - 1) / kMergedWaves;
     kps = (kps + kChunk - 1) / kChunk * kChunk;
     dim3 grid(1, H, B * nqb);
-#define NNHIP_ATTN(SQP, DL)                                                   \
-  hipLaunchKernelGGL((attn_kernel<SQP, DL, kMergedWaves>), grid,              \
-                     dim3(kWave * kMergedWaves), 0, st, q, kc, vc, S, H, Hkv, \
-                     cap, seq_stride, base, off, active, kMergedWaves, nqb,   \
-                     kps, qscale, nullptr, out)
-#define NNHIP_ATTN_D(SQP)                                                     \
-  if (D == 32) NNHIP_ATTN(SQP, 4); else NNHIP_ATTN(SQP, 8);
-    if (sq == 1) { NNHIP_ATTN_D(1) }
-    else if (sq == 2) { NNHIP_ATTN_D(2) }
-    else if (sq <= 4) { NNHIP_ATTN_D(4) }
-    else { NNHIP_ATTN_D(8) }
+#define NNHIP_ATTN(SQP, DL, W)                                                \
+  hipLaunchKernelGGL((attn_kernel<SQP, DL, W>), grid, dim3(kWave * W), 0, st, \
+                     q, kc, vc, S, H, Hkv, cap, seq_stride, base, off, active, \
+                     W, nqb, kps, qscale, nullptr, out)
+#define NNHIP_ATTN_D(SQP, W)                                                  \
+  if (D == 32) NNHIP_ATTN(SQP, 4, W); else NNHIP_ATTN(SQP, 8, W);
+    // many-query rows hold many registers (one workgroup of 8 waves per CU):
+    // with 4 waves two workgroups share a CU and a launch runs in one round
+    const bool w4 = g_attn_w4 && max_keys <= kMergedWaves4 * kMergedChunks * kChunk;
+    if (sq == 1) { NNHIP_ATTN_D(1, kMergedWaves) }
+    else if (sq == 2) { NNHIP_ATTN_D(2, kMergedWaves) }
+    else if (sq <= 4) { if (w4) { NNHIP_ATTN_D(4, kMergedWaves4) } else { NNHIP_ATTN_D(4, kMergedWaves) } }
+    else { if (w4) { NNHIP_ATTN_D(8, kMergedWaves4) } else { NNHIP_ATTN_D(8, kMergedWaves) } }
 #undef NNHIP_ATTN_D
 #undef NNHIP_ATTN
     NNHIP_CHECK(hipGetLastError());

@@ -8,11 +8,13 @@
 
 namespace nnhip {
 
+int g_lds_min_rows = 64;
+int g_fold_norm = 0;
+
 namespace {
 
 constexpr int kLimbMinRows = 16;
 constexpr int64_t kFusedNormMaxBlocks = 768;
-constexpr int kLdsMinRows = 64;
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
@@ -315,7 +317,7 @@ bool Model::use_lds(const Linear &ln, int rows) const {
   if (!(ln.quant && ln.qs.p && rows >= kLimbMinRows &&
         gemm_lds_supports(rows, ln.K, ln.N)))
     return false;
-  return &ln == &lm || rows >= kLdsMinRows;
+  return &ln == &lm || rows >= g_lds_min_rows;
 }
 
 void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
@@ -328,7 +330,7 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
     // Each column block of a fused GEMM normalises and digitises its rows
     // again: only the short-batch lm head folds the norm in; elsewhere one
     // LayerNorm launch writes digit planes for the GEMM to copy.
-    const bool fold = &ln == &lm && rows < kLdsMinRows &&
+    const bool fold = (g_fold_norm || (&ln == &lm && rows < g_lds_min_rows)) &&
                       gemm_lds_workgroups(rows, ln.K, ln.N) <= kFusedNormMaxBlocks;
     if (pn && !fold && pn->ldh == ln.K) {
       launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b,

@@ -210,9 +210,13 @@ __device__ inline int digit_exponent(float mx) {
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
 extern int g_gemm_fk;        // LDS GEMM: 1 = full-K-wave kernel
+// engine.hip
+extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
+extern int g_fold_norm;     // 1 = a pending LayerNorm folds into every LDS GEMM
 // workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
 constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
+extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
 // workgroups of one LDS-GEMM launch (32-row tiles x column blocks of
 // 32 * 16 / min(4, K/128) columns)
 inline int64_t gemm_lds_workgroups(int rows, int K, int N) {

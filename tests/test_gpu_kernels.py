@@ -283,8 +283,11 @@ ATTN_CASES = [(3, 1, 4, 64, [0, 37, 300]), (2, 6, 4, 64, [5, 380]),
               (16, 8, 8, 64, [2048] * 16)]
 
 
+@pytest.mark.parametrize("w4", [0, 1])
 @pytest.mark.parametrize("B,S,H,D,pos0", ATTN_CASES)
-def test_attention_kq(ctx, B, S, H, D, pos0):
+def test_attention_kq(ctx, B, S, H, D, pos0, w4):
+    """k-query causal attention against the oracle; w4 = 1 runs the 4-wave
+    merged workgroups for rows of 4+ queries."""
     rng = np.random.default_rng(B * 100 + S + D)
     pos0 = np.array(pos0, np.int32)
     cap = int(pos0.max()) + S
@@ -293,8 +296,12 @@ def test_attention_kq(ctx, B, S, H, D, pos0):
     v = rng.standard_normal((B, H, cap, D)).astype(np.float32)
     dq, dk, dv = ctx.array(q), ctx.array(k), ctx.array(v)
     dp, do = ctx.array(pos0), ctx.array(shape=(B * S, H * D))
-    call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
-         D, do.p)
+    try:
+        ctx.set_option("attn_w4", w4)
+        call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
+             D, do.p)
+    finally:
+        ctx.set_option("attn_w4", 0)
     got = do.numpy()
     for b in range(B):
         St = int(pos0[b]) + S
