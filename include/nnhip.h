@@ -258,7 +258,9 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
                             int32_t *n_accept);
 /* path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included),
  * 3 = LDS GEMM digitising fp32 rows, 4 = LDS GEMM over digit planes (their
- * digit split included), 5 = LDS GEMM with LayerNorm in its prologue. */
+ * digit split included), 5 = LDS GEMM with LayerNorm in its prologue,
+ * 6 = LDS GEMM over digit planes made once, with the lm head's tile
+ * softmax statistics (K of 512 or 1024). */
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms);
 

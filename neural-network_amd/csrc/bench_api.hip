@@ -112,7 +112,8 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
 // W8A32 Linear: rows x K activations N(0, 1) times an int8 [N][K] weight.
 // path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included),
 // 3 = LDS GEMM from fp32 rows, 4 = LDS GEMM over digit planes (digit split
-// included), 5 = LDS GEMM with LayerNorm (gamma 1, beta 0) in its prologue.
+// included), 5 = LDS GEMM with LayerNorm (gamma 1, beta 0) in its prologue,
+// 6 = LDS GEMM over digit planes made once, with tile statistics.
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms) {
   return guard([&] {
@@ -141,16 +142,29 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     nnhip::launch_fill(st, b0.p, K, 0.f);
     NNHIP_REQUIRE(path <= 2 || nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
                   "nnhip_bench_linear: shape not supported by the LDS GEMM");
+    // path 6: digit planes prepared once, then the GEMM alone with the lm
+    // head's tile statistics (T = 1)
+    const int tw = nnhip::gemm_lds_tile_width(K);
+    NNHIP_REQUIRE(path != 6 || tw > 0, nnhip::kErrArg,
+                  "nnhip_bench_linear: tile statistics need K of 512 or 1024");
+    const int ntile = tw > 0 ? (N + tw - 1) / tw : 0;
+    nnhip::DevBuf<float2> tstat(path == 6 ? (size_t)rows * ntile : 0);
+    nnhip::TileStatsArgs tsa;
+    tsa.out = tstat.p; tsa.ld = ntile; tsa.T = 1.f;
+    if (path == 6)
+      nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
       if (path >= 3) {
         if (path == 4)
           nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
         const int mode = path == 3 ? nnhip::kAFromRows
-                         : path == 4 ? nnhip::kAFromDigits : nnhip::kAFromLayerNorm;
+                         : path == 4 || path == 6 ? nnhip::kAFromDigits
+                                                  : nnhip::kAFromLayerNorm;
         nnhip::launch_gemm_lds(st, mode, limbs.p, mpad, rexp.p, x.p, K, g1.p,
                                b0.p, nullptr, 0, rows, K, N, WS[j].p, S[j].p,
-                               b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
+                               b.p, nullptr, 0, y.p, N, nnhip::kEpiBias,
+                               nullptr, path == 6 ? &tsa : nullptr);
       } else if (path == 2) {
         nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
         nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, WS[j].p,

@@ -320,10 +320,14 @@ bool Model::use_lds(const Linear &ln, int rows) const {
   return &ln == &lm || rows >= g_lds_min_rows;
 }
 
+bool Model::lm_tiles(int rows) const {
+  return use_lds(lm, rows) && gemm_lds_tile_width(lm.K) > 0;
+}
+
 void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                       const PendingNorm *pn, int rows, bool limbs_ready,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi, const RopeArgs *ra) {
+                      int epi, const RopeArgs *ra, const TileStatsArgs *ts) {
   hipStream_t st = ctx->lane(g);
   Workspace &ws = this->ws(g);
   if (use_lds(ln, rows)) {
@@ -339,7 +343,7 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
       launch_gemm_lds(st, kAFromDigits, ws.limbs.p, ws.mpad, ws.rexp.p,
                       nullptr, 0, nullptr, nullptr, nullptr, 0, rows, ln.K,
                       ln.N, ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi,
-                      ra);
+                      ra, ts);
       return;
     }
     const int mode = pn ? kAFromLayerNorm
@@ -348,9 +352,11 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                     pn ? pn->h : x, pn ? pn->ldh : ldx, pn ? pn->g : nullptr,
                     pn ? pn->b : nullptr, pn ? pn->out : nullptr,
                     pn ? pn->ldo : 0, rows, ln.K, ln.N, ln.qs.p, ln.s.p,
-                    ln.b.p, resid, ldr, y, ldy, epi, ra);
+                    ln.b.p, resid, ldr, y, ldy, epi, ra, ts);
     return;
   }
+  NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
+                "linear_in: tile statistics need the LDS-resident GEMM");
   if (pn) {
     // the normalisation as its own kernel, then the linear over its output
     NNHIP_REQUIRE(pn->out && pn->ldh == ln.K && pn->ldo == ln.K, kErrArg,
@@ -384,7 +390,8 @@ void Model::linear(int g, const Linear &ln, const float *x, int64_t ldx,
 void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
                     int ids_stride, int B, int S, const int32_t *base, int off,
                     const int32_t *active, int max_keys, float *logits,
-                    bool last_only) {
+                    bool last_only, int64_t ldl, const TileStatsArgs *ts) {
+  if (ldl == 0) ldl = V;
   hipStream_t st = ctx->lane(g);
   const int R = B * S;
   std::unique_ptr<KVCache> tmp;
@@ -455,16 +462,18 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       PendingNorm pn = norm2;
       pn.out = nullptr;
       if (last_only) { pn.h = ws.h.p + (int64_t)(S - 1) * d; pn.ldh = (int64_t)S * d; }
-      linear_in(g, lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, V,
-                kEpiBias);
+      linear_in(g, lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, ldl,
+                kEpiBias, nullptr, ts);
     } else {
+      NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
+                    "forward: tile statistics need the LDS-resident lm head");
       launch_layernorm(st, ws.h.p, R, d, norm2.g, norm2.b, ws.x.p, nullptr,
                        ws.mpad, ws.rexp.p);
       if (last_only)
         linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
-               nullptr, 0, logits, V, kEpiBias);
+               nullptr, 0, logits, ldl, kEpiBias);
       else
-        linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, V, kEpiBias);
+        linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, ldl, kEpiBias);
     }
   }
   if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
@@ -506,6 +515,7 @@ struct SpecBuffers {
   DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok, pair,
       out, n_active, vids, prompts;
   DevBuf<float> qprob, dlog, tlog, tstat;
+  DevBuf<float2> dtiles;
   DevBuf<int64_t> stats;
 };
 
@@ -547,10 +557,24 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.catchup.alloc(B); bf.catch_tok.alloc(B); bf.pair.alloc((size_t)2 * B);
   bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
   bf.vids.alloc((size_t)B * (k + 1)); bf.prompts.alloc((size_t)B * P);
+  // Drafting samples from the draft lm head's tile statistics when that lm
+  // head forms them for every group's row count; otherwise from full passes
+  // over the logits.  (The verify rows keep full passes: tile statistics in
+  // the target lm head, six row tiles per workgroup, cost about what
+  // target_stats_kernel does.)
+  int G = ctx->groups > 0 ? ctx->groups : 1;
+  G = std::max(1, std::min(G, B));
+  std::vector<int> gb0(G + 1);
+  for (int g = 0; g <= G; ++g) gb0[g] = (int)((int64_t)B * g / G);
+  const int tw = gemm_lds_tile_width(dm.lm.K);
+  const int nt = tw > 0 ? (V + tw - 1) / tw : 0;
+  bool tiles = tw > 0 && nt <= 1024;
+  for (int g = 0; g < G && tiles; ++g) tiles = dm.lm_tiles(gb0[g + 1] - gb0[g]);
+  if (tiles) bf.dtiles.alloc((size_t)B * k * nt);
   if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
+  bf.tstat.alloc((size_t)B * (k + 1) * 4);
   bf.dlog.alloc((size_t)B * V);
   bf.tlog.alloc((size_t)B * (k + 1) * V);
-  bf.tstat.alloc((size_t)B * (k + 1) * 4);
   bf.stats.alloc((size_t)B * 6);
   NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
   NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 4, st));
@@ -562,12 +586,9 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                                (size_t)P * 4, (size_t)P * 4, B,
                                hipMemcpyHostToDevice, st));
 
-  // Sequences are independent: split the batch into G groups, each driven on
-  // its own lane (stream) so that the groups' kernels overlap on the GPU.
-  int G = ctx->groups > 0 ? ctx->groups : 1;
-  G = std::max(1, std::min(G, B));
-  std::vector<int> gb0(G + 1);
-  for (int g = 0; g <= G; ++g) gb0[g] = (int)((int64_t)B * g / G);
+  // Sequences are independent: the batch is split into G groups (above),
+  // each driven on its own lane (stream) so that the groups' kernels overlap
+  // on the GPU.
   std::vector<SpecState> gs(G);
   std::vector<hipStream_t> lanes(G);
   for (int g = 0; g < G; ++g) {
@@ -577,6 +598,10 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     s.cur = bf.cur.p + b0; s.cand = bf.cand.p + (size_t)b0 * k;
     s.qprob = bf.qprob.p ? bf.qprob.p + (size_t)b0 * k * V : nullptr;
     s.tstat = bf.tstat.p + (size_t)b0 * (k + 1) * 4;
+    if (tiles) {
+      s.dtiles = bf.dtiles.p + (size_t)b0 * k * nt;
+      s.nt = nt; s.tw = tw;
+    }
     s.tlen = bf.tlen.p + b0; s.dlen = bf.dlen.p + b0; s.gen = bf.gen.p + b0;
     s.cyc = bf.cyc.p + b0; s.active = bf.active.p + b0;
     s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;
@@ -638,13 +663,20 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
       float *tl = bf.tlog.p + (size_t)b0 * (k + 1) * V;
       int32_t *vids = bf.vids.p + (size_t)b0 * (k + 1);
       for (int j = 0; j < k; ++j) {
+        TileStatsArgs dts;
+        if (tiles) {
+          dts.out = bf.dtiles.p + ((size_t)b0 * k + j) * nt;
+          dts.ld = (int64_t)k * nt;
+          dts.T = T;
+        }
         if (j == 0)   // {catch-up token, cur} at dlen - 1, dlen
           dm.forward(g, &dc, b0, bf.pair.p + (size_t)2 * b0, 2, Bg, 2, dlen,
-                     -1, act, d_need, dl, true);
+                     -1, act, d_need, dl, true, 0, &dts);
         else
           dm.forward(g, &dc, b0, cand + (j - 1), k, Bg, 1, dlen, j, act,
-                     d_need, dl, false);
-        launch_draft_sample(ls, gs[g], j, dl, V);
+                     d_need, dl, false, 0, &dts);
+        if (tiles) launch_draft_sample_tiles(ls, gs[g], j, dl, V);
+        else launch_draft_sample(ls, gs[g], j, dl, V);
       }
       launch_build_verify_ids(ls, cur, cand, Bg, k, vids);
       t.forward(g, &tc, b0, vids, k + 1, Bg, k + 1, bf.tlen.p + b0, 0, act,

@@ -83,11 +83,15 @@ struct Model {
   // Token of row (b, s): ids[b*ids_stride + s].  Positions start at
   // base[b] + off (device array; nullptr = 0).  Sequences with
   // active[b] == 0 neither write nor read the cache.  logits: nullptr (not
-  // needed), or [B*S][V] (all rows) or [B][V] (last_only).
+  // needed), or [B*S][V] (all rows) or [B][V] (last_only), rows ldl apart
+  // (0 = V).  ts: the lm head's tile statistics as well (lm_tiles(rows)).
   void forward(int g, KVCache *cache, int b_off, const int32_t *ids,
                int ids_stride, int B, int S, const int32_t *base, int off,
                const int32_t *active, int max_keys, float *logits,
-               bool last_only);
+               bool last_only, int64_t ldl = 0,
+               const TileStatsArgs *ts = nullptr);
+  // whether the lm head on `rows` rows can form tile statistics
+  bool lm_tiles(int rows) const;
 
   void linear(int g, const Linear &ln, const float *x, int64_t ldx, int rows,
               bool limbs_ready, const float *resid, int64_t ldr, float *y,
@@ -104,7 +108,8 @@ struct Model {
   void linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                  const PendingNorm *pn, int rows, bool limbs_ready,
                  const float *resid, int64_t ldr, float *y, int64_t ldy,
-                 int epi, const RopeArgs *ra = nullptr);
+                 int epi, const RopeArgs *ra = nullptr,
+                 const TileStatsArgs *ts = nullptr);
   bool use_limbs(const Linear &ln, int rows) const;
   bool use_lds(const Linear &ln, int rows) const;
 };

@@ -385,7 +385,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
     int M, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn, int rpt, RopeArgs ra) {
+    int64_t ldy, int epi, int ntm, int ntn, int rpt, RopeArgs ra,
+    TileStatsArgs tsa) {
   constexpr int K = KPT * 32;
   constexpr int nch = K / 128;
   constexpr int KS = nch < 4 ? nch : 4;       // K slices
@@ -656,6 +657,33 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
         if (epi == kEpiResid) { v0 = e_rs[it][0] + v0; v1 = e_rs[it][1] + v1; }
         y[(int64_t)m * ldy + n] = v0;
         y[(int64_t)m * ldy + n + 1] = v1;
+      }
+    }
+    // softmax statistics of this column block (NC == 128: item `it` of a
+    // wave is one row's whole block, two columns a lane)
+    if (NC == 2 * kWave && tsa.out && epi == kEpiBias) {
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+        const int idx = tid + it * kLdsThreads;
+        const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
+        const int m = m0 + row, n = n0 + c0;
+        if (m >= M) continue;                  // whole wave
+        float l0 = ldexpf((float)et[it][0], -eex[it]), l1 = ldexpf((float)et[it][1], -eex[it]);
+        l0 = __fadd_rn(__fmul_rn(l0, esc[it][0]), ebi[it][0]);
+        l1 = __fadd_rn(__fmul_rn(l1, esc[it][1]), ebi[it][1]);
+        if (tsa.T > 0.f) {
+          float s0 = n < N ? (tsa.T == 1.f ? l0 : l0 / tsa.T) : -INFINITY;
+          float s1 = n + 1 < N ? (tsa.T == 1.f ? l1 : l1 / tsa.T) : -INFINITY;
+          const float mx = wave_max_all(fmaxf(s0, s1));
+          const float e = wave_sum_all((n < N ? expf(s0 - mx) : 0.f) +
+                                       (n + 1 < N ? expf(s1 - mx) : 0.f));
+          if (lane == 0) tsa.out[(int64_t)m * tsa.ld + tn] = make_float2(mx, e);
+        } else {
+          const float a0 = n < N ? l0 : -INFINITY, a1 = n + 1 < N ? l1 : -INFINITY;
+          const float mx = wave_max_all(fmaxf(a0, a1));
+          const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
+          if (lane == 0) tsa.out[(int64_t)m * tsa.ld + tn] = make_float2(mx, __int_as_float(ix));
+        }
       }
     }
     if (kDig && more) {
@@ -1223,13 +1251,18 @@ static void launch_gemm_fk(hipStream_t st, int mode, const int8_t *limbs,
   NNHIP_CHECK(hipGetLastError());
 }
 
+int gemm_lds_tile_width(int K) {
+  // 16 waves of 32 columns over K/KS each: 128-column blocks when KS = 4
+  return K == 512 || K == 1024 ? 2 * kWave : 0;
+}
+
 void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                      const int *rexp, const float *x, int64_t ldx,
                      const float *lng, const float *lnb, float *ln_out,
                      int64_t ldo, int rows, int K, int N, const int8_t *wq,
                      const float *scale, const float *bias,
                      const float *resid, int64_t ldr, float *y, int64_t ldy,
-                     int epi, const RopeArgs *ra) {
+                     int epi, const RopeArgs *ra, const TileStatsArgs *ts) {
   NNHIP_REQUIRE(gemm_lds_supports(rows, K, N), kErrArg,
                 "gemm_lds: needs K in {128, 256, 512, 1024}, N % 32 == 0");
   NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg,
@@ -1246,7 +1279,10 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                   kErrArg, "gemm_lds: LayerNorm parameters missing");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
-  if (g_gemm_fk && !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
+  NNHIP_REQUIRE(!ts || !ts->out || (gemm_lds_tile_width(K) > 0 && epi == kEpiBias),
+                kErrArg, "gemm_lds: tile statistics need K of 512 or 1024 and a bias epilogue");
+  const TileStatsArgs tz = ts ? *ts : TileStatsArgs{};
+  if (g_gemm_fk && !tz.out && !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
     launch_gemm_fk(st, mode, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,
                    rows, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, rz, ntm);
     return;
@@ -1264,7 +1300,7 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
   hipLaunchKernelGGL((gemm_lds_kernel<MD, KP>), grid, dim3(kLdsThreads), 0,   \
                      st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,    \
                      rows, N, wq, scale, bias, resid, ldr, y, ldy, epi, ntm,  \
-                     ntn, rpt, rz)
+                     ntn, rpt, rz, tz)
 #define NNHIP_GL_K(MD)                                                        \
   switch (K) {                                                                \
     case 128: NNHIP_GL(MD, 4); break;                                         \

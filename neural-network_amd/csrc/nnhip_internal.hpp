@@ -229,13 +229,64 @@ inline bool gemm_lds_supports(int rows, int K, int N) {
   return rows > 0 && (K == 128 || K == 256 || K == 512 || K == 1024) &&
          N >= 32 && N % 32 == 0;
 }
+// Reductions over a whole wave that every lane receives: DPP row rotations
+// by 1, 2, 4, 8 within each row of 16 lanes, then the four rows' values read
+// from lanes 0, 16, 32, 48 (no LDS permutes).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = fmaxf(v, dpp_f<0x121>(v));
+  v = fmaxf(v, dpp_f<0x122>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  v = fmaxf(v, dpp_f<0x128>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v += dpp_f<0x121>(v);
+  v += dpp_f<0x122>(v);
+  v += dpp_f<0x124>(v);
+  v += dpp_f<0x128>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+__device__ __forceinline__ int wave_min_all(int v) {
+  v = min(v, dpp_i<0x121>(v));
+  v = min(v, dpp_i<0x122>(v));
+  v = min(v, dpp_i<0x124>(v));
+  v = min(v, dpp_i<0x128>(v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Softmax statistics of the lm head's logits per (row, column tile), written
+// by the LDS GEMM's epilogue: for T > 0 tile t of row m gets
+// out[m * ld + t] = (max_i s_i, sum_i exp(s_i - max)) with s = l / T (l when
+// T == 1); for T <= 0 (max_i l_i, first index of the max as int bits).
+// Tiles are the GEMM's column blocks, gemm_lds_tile_width(K) wide.
+struct TileStatsArgs {
+  float2 *out = nullptr;
+  int64_t ld = 0;
+  float T = 1.f;
+};
+// Column width of a tile of statistics, or 0 when the LDS GEMM cannot form
+// them for this K (its column block must be one wave's 128 columns).
+int gemm_lds_tile_width(int K);
 void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                      const int *rexp, const float *x, int64_t ldx,
                      const float *lng, const float *lnb, float *ln_out,
                      int64_t ldo, int rows, int K, int N, const int8_t *wq,
                      const float *scale, const float *bias,
                      const float *resid, int64_t ldr, float *y, int64_t ldy,
-                     int epi, const RopeArgs *ra = nullptr);
+                     int epi, const RopeArgs *ra = nullptr,
+                     const TileStatsArgs *ts = nullptr);
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
@@ -309,6 +360,9 @@ struct SpecState {
   int32_t *n_active;   // [1]
   int64_t *stats;      // [B][6] cycles, drafted, accepted, ties, resampled,
                        //        bonus
+  const float2 *dtiles;  // [B][k][nt] draft lm-head tile statistics
+                         // (TileStatsArgs) of the cycle's steps, or null
+  int nt, tw;            // tiles per row, tile width
   int B, out_stride, P, max_new, k, V;
   float T;
   uint64_t seed;
@@ -319,6 +373,9 @@ void launch_first_token(hipStream_t st, const SpecState &s,
 void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
                          const float *logits, int64_t ldl);
 void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits);
+// drafting step j from the draft lm head's tile statistics (s.dtiles)
+void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
+                               const float *logits, int64_t ldl);
 void launch_ar_sample(hipStream_t st, const SpecState &s, int step,
                       const float *logits, int64_t ldl);
 void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,

@@ -43,14 +43,30 @@ __device__ __forceinline__ float uniform(uint64_t seed, uint32_t seq,
   return (float)(c0 >> 8) * (1.0f / 16777216.0f);
 }
 
+// Row statistics of get_probs (T > 0), see row_pass
+struct RowStats { float mx, rsum, rfs; };
+
+// workgroup reduction slots; `rows` holds per-row statistics formed by
+// single waves (accept step, up to one row per wave)
 struct Shared {
   float f[kWaves];
   double d[kWaves];
   int i[kWaves];
+  RowStats rows[kWaves];
+  int argm[kWaves];
+  double xd;
   float prow[kRowWords];
 };
+// the same without the probability row, for kernels that need no full row
+struct SmallShared {
+  float f[kWaves];
+  double d[kWaves];
+  int i[kWaves];
+  double xd;
+};
 
-__device__ __forceinline__ float block_max(float v, Shared &sh) {
+template <class SH>
+__device__ __forceinline__ float block_max(float v, SH &sh) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   __syncthreads();
@@ -62,7 +78,8 @@ __device__ __forceinline__ float block_max(float v, Shared &sh) {
   return r;
 }
 
-__device__ __forceinline__ float block_sum(float v, Shared &sh) {
+template <class SH>
+__device__ __forceinline__ float block_sum(float v, SH &sh) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   __syncthreads();
@@ -75,7 +92,8 @@ __device__ __forceinline__ float block_sum(float v, Shared &sh) {
 }
 
 // exclusive prefix sum over threads in index order; *total = the block sum
-__device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh,
+template <class SH>
+__device__ __forceinline__ double block_excl_scan_d(double v, SH &sh,
                                                     double *total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   double incl = v;
@@ -98,7 +116,8 @@ __device__ __forceinline__ double block_excl_scan_d(double v, Shared &sh,
   return pre + incl - v;
 }
 
-__device__ __forceinline__ int block_min_i(int v, Shared &sh) {
+template <class SH>
+__device__ __forceinline__ int block_min_i(int v, SH &sh) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
   __syncthreads();
@@ -150,8 +169,6 @@ __device__ __forceinline__ int block_argmax(const float *__restrict__ row,
 // normalisations multiply by the correctly rounded reciprocals 1/sum and
 // 1/sum(p1), so p may differ from the divided value in the last place.
 // RowStats holds what recomputes p at one index (prob_at).
-struct RowStats { float mx, rsum, rfs; };
-
 __device__ __forceinline__ float scaled(float l, float T) {
   return T == 1.0f ? l : l / T;
 }
@@ -268,6 +285,148 @@ __device__ __forceinline__ int draw_row(const float *row, int V, float T, float 
   if (T <= 0.f) return block_argmax(row, V, sh);
   row_probs(row, V, T, sh);
   return block_sample(V, u, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Sampling from the lm head's tile statistics (TileStatsArgs: per 128-column
+// tile of a row, (max s, sum exp(s - max)) for T > 0, (max l, first index of
+// the max) for T <= 0).  The row's get_probs statistics are recombined from
+// the tiles -- max over the tiles, sum_t e_t exp(m_t - max) -- instead of a
+// pass over every logit, and the inverse CDF runs over the tiles' masses
+// before it scans the one tile where the running sum reaches u * S, with the
+// probabilities of that tile recomputed exactly as prob_at does.  The sums
+// are formed in another order than a full pass, so p and S differ from the
+// full pass in the last bits; a draw differs only if u * S falls within
+// that difference of a CDF step (a tie).
+// ---------------------------------------------------------------------------
+constexpr int kTileMax = 16;   // tiles per lane of one wave: rows <= 1024 tiles
+
+// RowStats (T > 0) of a row from its nt tile statistics, by one wave
+__device__ __forceinline__ RowStats wave_tiles_stats(const float2 *__restrict__ tl,
+                                                     int nt) {
+  const int lane = threadIdx.x & 63;
+  float2 v[kTileMax];
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i) v[i] = tl[min(lane + 64 * i, nt - 1)];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i)
+    if (lane + 64 * i < nt) mx = fmaxf(mx, v[i].x);
+  mx = wave_max_all(mx);
+  float e = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i)
+    if (lane + 64 * i < nt && v[i].x > -INFINITY) e += v[i].y * expf(v[i].x - mx);
+  e = wave_sum_all(e);
+  const float rs = 1.0f / e;
+  return RowStats{mx, rs, 1.0f / (e * rs)};
+}
+
+// first index of a row's maximum from its tile statistics (T <= 0), one wave
+__device__ __forceinline__ int wave_tiles_argmax(const float2 *__restrict__ tl,
+                                                 int nt) {
+  const int lane = threadIdx.x & 63;
+  float2 v[kTileMax];
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i) v[i] = tl[min(lane + 64 * i, nt - 1)];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i)
+    if (lane + 64 * i < nt) mx = fmaxf(mx, v[i].x);
+  mx = wave_max_all(mx);
+  int ix = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < kTileMax; ++i)
+    if (lane + 64 * i < nt && v[i].x == mx) ix = min(ix, __float_as_int(v[i].y));
+  ix = wave_min_all(ix);
+  return ix == 0x7fffffff ? 0 : ix;
+}
+
+// sample_token over p = prob_at(row, ., T, st) from the row's tile
+// statistics: the tile where the running sum of the tile masses reaches
+// u * S, then the first entry of it (entries in order, exact p) whose running
+// sum reaches u * S; the next tile if rounding left the crossing short.
+template <class SH>
+__device__ __forceinline__ int tiles_sample(const float *__restrict__ row,
+                                            const float2 *__restrict__ tl,
+                                            int nt, int tw, int V, float T,
+                                            RowStats st, float u, SH &sh) {
+  const int t = threadIdx.x;
+  double P = 0.0;
+  if (t < nt) {
+    const float2 v = tl[t];
+    if (v.x > -INFINITY)
+      P = (double)(v.y * expf(v.x - st.mx)) * (double)st.rsum * (double)st.rfs;
+  }
+  double S;
+  const double c = block_excl_scan_d(P, sh, &S);
+  const double target = (double)u * S;
+  int ts = block_min_i(t < nt && P > 0.0 && c + P >= target ? t : 0x7fffffff, sh);
+  if (ts == 0x7fffffff) return V - 1;
+  // running sum before tile ts, broadcast
+  if (t == ts) sh.xd = c;
+  __syncthreads();
+  double before = sh.xd;
+  for (; ts < nt; ++ts) {
+    const int v = ts * tw + t;
+    const bool in = t < tw && v < V;
+    const double p = in ? (double)((expf(scaled(row[v], T) - st.mx) * st.rsum) * st.rfs) : 0.0;
+    double tot;
+    const double ex = block_excl_scan_d(p, sh, &tot);
+    const int found = block_min_i(in && v < V - 1 && before + ex + p >= target ? v : 0x7fffffff, sh);
+    if (found != 0x7fffffff) return found;
+    before += tot;
+  }
+  return V - 1;
+}
+
+// One drafting step j (layer.cpp:1541-1558) from the draft lm head's tile
+// statistics: q_j's statistics recombined from the tiles, q_j written in one
+// pass over the row by kQParts workgroups per sequence (the accept step's
+// candidate and residual read it; the pass is VALU-bound on expf, so it is
+// spread over CUs), and the candidate drawn by tiles_sample in the first of
+// them.  Greedy: the argmax of the tiles.
+constexpr int kQParts = 8;
+constexpr int kQPer = (kMaxV / kQParts + kThreads - 1) / kThreads;
+
+__global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
+    SpecState s, int j, const float *__restrict__ logits, int64_t ldl) {
+  __shared__ SmallShared sh;
+  __shared__ RowStats rst;
+  const int b = blockIdx.x, part = blockIdx.y;
+  if (!s.active[b]) return;
+  const float2 *tl = s.dtiles + ((int64_t)b * s.k + j) * s.nt;
+  if (s.T <= 0.f) {
+    if (part == 0 && threadIdx.x < 64) {
+      const int a = wave_tiles_argmax(tl, s.nt);
+      if (threadIdx.x == 0) s.cand[b * s.k + j] = a;
+    }
+    return;
+  }
+  const float *row = logits + b * ldl;
+  // this part's entries requested while the statistics are formed
+  const int chunk = (s.V + kQParts - 1) / kQParts;
+  const int v0 = part * chunk, v1 = min(s.V, v0 + chunk);
+  float x[kQPer];
+#pragma unroll
+  for (int i = 0; i < kQPer; ++i)
+    x[i] = row[min(v0 + (int)threadIdx.x + i * kThreads, s.V - 1)];
+  if (threadIdx.x < 64) {
+    const RowStats st = wave_tiles_stats(tl, s.nt);
+    if (threadIdx.x == 0) rst = st;
+  }
+  __syncthreads();
+  const RowStats st = rst;
+  float *q = s.qprob + ((int64_t)b * s.k + j) * s.V;
+#pragma unroll
+  for (int i = 0; i < kQPer; ++i) {
+    const int v = v0 + (int)threadIdx.x + i * kThreads;
+    if (v < v1) q[v] = (expf(scaled(x[i], s.T) - st.mx) * st.rsum) * st.rfs;
+  }
+  if (part != 0) return;
+  const int tok = tiles_sample(row, tl, s.nt, s.tw, s.V, s.T, st,
+                               uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+  if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
 }
 
 // ---------------------------------------------------------------------------
@@ -600,6 +759,16 @@ void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
   NNHIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
                      tlogits);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
+                               const float *logits, int64_t ldl) {
+  NNHIP_REQUIRE(s.dtiles && (s.T <= 0.f || s.qprob) && s.nt <= kThreads &&
+                    s.tw <= kThreads && s.V <= kMaxV,
+                kErrArg, "draft sample: tile statistics missing or too many tiles");
+  hipLaunchKernelGGL(draft_sample_tiles_kernel, dim3(s.B, kQParts),
+                     dim3(kThreads), 0, st, s, j, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -230,6 +230,32 @@ def test_batch_mfma_rows_match_oracle(ctx, fk):
     gt.free(); gd.free()
 
 
+# d = 512 draft at batch 16: the draft lm head runs on the LDS-resident GEMM
+# with 128-column blocks, so drafting samples from its tile statistics
+TILE_T = dict(vocab=2000, d=512, H=8, F=1024, L=1)
+TILE_D = dict(vocab=2000, d=512, H=8, F=512, L=1)
+
+
+@pytest.mark.parametrize("T", [0.0, 1.0, 0.7])
+def test_batch_tile_sampling_matches_oracle(ctx, T):
+    """Drafting from the draft lm head's tile statistics: greedy streams
+    exact, sampled streams equal to the oracle's up to a recorded tie; the
+    last tile is ragged (vocabulary 2000 = 15 x 128 + 80)."""
+    ot, gt, od, gd = spec_pair(ctx, TILE_T, TILE_D, 70, True, std=0.1)
+    B = 16
+    rng = np.random.default_rng(71)
+    prompts = rng.integers(0, 2000, (B, 12)).astype(np.int32)
+    got, stats, _ = gt.generate_speculative_batch(gd, prompts, 20, 3, T, 9)
+    for b in (0, 5, 15):
+        want, ost = O.generate_speculative(ot, od, prompts[b], 20, 3, T, 9,
+                                           seq=b)
+        if not np.array_equal(got[b], want):
+            assert T > 0 and (ost.ties > 0 or stats[b].ties > 0), b
+        else:
+            assert stats[b].accepted == ost.accepted
+    gt.free(); gd.free()
+
+
 def test_cfg2_int8_greedy_full_size(ctx):
     """int8 greedy at full size: target 6L/512/8h/2048/V4096, draft
     2L/256/4h/1024, prompt 128, k=4, 256 new tokens; exact token stream."""
