@@ -576,9 +576,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
 }
 
 // LayerNorm as layernorm_kernel, one wave per row for d % 16 == 0: lane l
-// holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, the
-// row sums and the max are wave reductions, and the digits of y (for the
-// next MFMA GEMM) are written from the same registers.
+// holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, with
+// their gamma and beta requested together with the row; the row sums and the
+// max are DPP wave reductions, and the digits of y (for the next MFMA GEMM)
+// are written from the same registers.
 template <int PPL>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
@@ -591,33 +592,39 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
   if (row >= rows) return;
   const float *xr = hin + (int64_t)row * d;
   const int np = d / 16;
-  float v[PPL][16];
-  float s = 0.f;
+  // pieces past the row re-read the last piece and are masked
+  float v[PPL][16], gv[PPL][16], bv[PPL][16];
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
-    const int pc = lane + 64 * j;
+    const int pc = min(lane + 64 * j, np - 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 f = pc < np ? *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 f = *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q);
+      const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
+      const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
       v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
+      gv[j][4 * q] = gg.x; gv[j][4 * q + 1] = gg.y; gv[j][4 * q + 2] = gg.z; gv[j][4 * q + 3] = gg.w;
+      bv[j][4 * q] = bb.x; bv[j][4 * q + 1] = bb.y; bv[j][4 * q + 2] = bb.z; bv[j][4 * q + 3] = bb.w;
     }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) s += v[j][q];
   }
+  float s = 0.f;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+  for (int j = 0; j < PPL; ++j)
+    if (lane + 64 * j < np) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) s += v[j][q];
+    }
+  s = wave_sum_all(s);
   const float N = (float)d;
   const float mean = s / N;
   float sq = 0.f;
 #pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    if (lane + 64 * j >= np) break;
+  for (int j = 0; j < PPL; ++j)
+    if (lane + 64 * j < np) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) { const float df = v[j][q] - mean; sq += df * df; }
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+      for (int q = 0; q < 16; ++q) { const float df = v[j][q] - mean; sq += df * df; }
+    }
+  sq = wave_sum_all(sq);
   const float sd = sqrtf(sq / N + 1e-5f);
   float mx = 0.f;
 #pragma unroll
@@ -626,13 +633,12 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     if (pc >= np) break;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
-      const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
       float *w = v[j] + 4 * q;
-      w[0] = (w[0] - mean) / sd * gg.x + bb.x;
-      w[1] = (w[1] - mean) / sd * gg.y + bb.y;
-      w[2] = (w[2] - mean) / sd * gg.z + bb.z;
-      w[3] = (w[3] - mean) / sd * gg.w + bb.w;
+      const float *gg = gv[j] + 4 * q, *bb = bv[j] + 4 * q;
+      w[0] = (w[0] - mean) / sd * gg[0] + bb[0];
+      w[1] = (w[1] - mean) / sd * gg[1] + bb[1];
+      w[2] = (w[2] - mean) / sd * gg[2] + bb[2];
+      w[3] = (w[3] - mean) / sd * gg[3] + bb[3];
       *reinterpret_cast<float4 *>(y + (int64_t)row * d + 16 * pc + 4 * q) =
           make_float4(w[0], w[1], w[2], w[3]);
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])),
@@ -640,8 +646,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     }
   }
   if (!limbs) return;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  mx = wave_max_all(mx);
   const int e = digit_exponent(mx);
   if (lane == 0) rexp[row] = e;
   const int64_t plane = (int64_t)mpad * d;

@@ -164,22 +164,25 @@ __global__ __launch_bounds__(256) void act_quant_kernel(
   if (m >= rows) return;
   const float *xr = x + m * ldx;
   const int np = K / 16;
+  // pieces past the row re-read the last piece and are masked
   float v[PPL][16];
-  float mx = 0.f;
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
-    const int pc = lane + 64 * j;
+    const int pc = min(lane + 64 * j, np - 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 f = pc < np ? *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 f = *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q);
       v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
     }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
   }
+  float mx = 0.f;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  for (int j = 0; j < PPL; ++j)
+    if (lane + 64 * j < np) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
+    }
+  mx = wave_max_all(mx);
   const int e = digit_exponent(mx);
   if (lane == 0) rexp[m] = e;
   const int64_t plane = (int64_t)mpad * K;
