@@ -10,10 +10,11 @@ from a seeded generator (synthetic; no checkpoints).
 
 value = committed tokens per second of the decode loop (accepted drafts plus
 one resample or bonus per cycle, prefill excluded), timed by HIP events on
-the library's stream around the cycle loop.  Also reported: the batch-1
-int8 greedy configuration (6L/512 target, 2L/256 draft, k=4, 256 new), the
-roofline of the dominant kernel, and the oracle timed on the host as the CPU
-baseline.
+the library's stream around the cycle loop, with fp32 KV caches.  Also
+reported: the same workload with int8 KV caches (kv_int8, the reference's
+quantized_cache option), the batch-1 int8 greedy configuration (6L/512
+target, 2L/256 draft, k=4, 256 new), the roofline of the dominant kernel,
+and the oracle timed on the host as the CPU baseline.
 """
 import argparse
 import json
@@ -57,40 +58,50 @@ def weight_bytes(cfg):
     return dense + 8 * outs
 
 
-def kv_bytes(cfg, n_keys):
-    """fp32 K and V read by one forward over n_keys cached positions."""
+def kv_bytes(cfg, n_keys, q8=False):
+    """K and V read by one forward over n_keys cached positions: fp32 rows,
+    or int8 codes plus one fp32 scale per (head, position) row."""
+    if q8:
+        H = cfg["H"]
+        return cfg["L"] * 2 * n_keys * (cfg["d"] + 4 * H)
     return cfg["L"] * 2 * n_keys * cfg["d"] * 4
 
 
-def cycle_bytes(ctx_len, k, Bn):
+def cycle_bytes(ctx_len, k, Bn, q8=False):
     """Algorithmic HBM bytes of one cycle at mean context ctx_len: verify
     (weights once, k+1 rows of KV per sequence), k draft forwards and the
     catch-up, and the logits written and read by sampling."""
-    v = weight_bytes(TARGET) + Bn * kv_bytes(TARGET, ctx_len + k + 1)
-    dr = (k + 1) * (weight_bytes(DRAFT) + Bn * kv_bytes(DRAFT, ctx_len + k))
+    v = weight_bytes(TARGET) + Bn * kv_bytes(TARGET, ctx_len + k + 1, q8)
+    dr = (k + 1) * (weight_bytes(DRAFT) + Bn * kv_bytes(DRAFT, ctx_len + k, q8))
     lg = Bn * (2 * k + 1) * TARGET["vocab"] * 4 * 2
     return v + dr + lg
 
 
-def attention_bytes(Bn, S, H, D, n_keys):
-    return 2 * Bn * H * n_keys * D * 4 + 2 * Bn * S * H * D * 4
+def attention_bytes(Bn, S, H, D, n_keys, q8=False):
+    kv = 2 * Bn * H * n_keys * (D + 4 if q8 else D * 4)
+    return kv + 2 * Bn * S * H * D * 4
 
 
-def run_cfg4(ctx, steps, warmup):
-    log("building cfg4 models (init + int8 quantisation on device)")
-    t = make_model(ctx, TARGET, 1234)
-    d = make_model(ctx, DRAFT, 5678)
-    rng = np.random.default_rng(2024)
-    prompts = rng.integers(0, TARGET["vocab"], (B, P)).astype(np.int32)
+def run_cfg4(ctx, steps, warmup, models=None, q8=False):
+    if models is None:
+        log("building cfg4 models (init + int8 quantisation on device)")
+        t = make_model(ctx, TARGET, 1234)
+        d = make_model(ctx, DRAFT, 5678)
+        rng = np.random.default_rng(2024)
+        prompts = rng.integers(0, TARGET["vocab"], (B, P)).astype(np.int32)
+    else:
+        t, d, prompts = models
     for i in range(warmup):
-        log(f"warmup {i}")
-        t.generate_speculative_batch(d, prompts, NEW, K_LOOK, TEMP, 42)
+        log(f"warmup {i}" + (" (int8 KV cache)" if q8 else ""))
+        t.generate_speculative_batch(d, prompts, NEW, K_LOOK, TEMP, 42,
+                                     quantized_cache=q8)
     ctx.sync()
     dec_ms, wall, toks, stats_all = 0.0, 0.0, 0, []
     for i in range(steps):
         t0 = time.perf_counter()
         out, stats, tm = t.generate_speculative_batch(d, prompts, NEW, K_LOOK,
-                                                      TEMP, 42)
+                                                      TEMP, 42,
+                                                      quantized_cache=q8)
         ctx.sync()
         wall += time.perf_counter() - t0
         dec_ms += tm.decode_ms
@@ -108,7 +119,7 @@ def run_cfg4(ctx, steps, warmup):
                tokens_per_cycle_per_seq=(NEW - 1) / max(cycles, 1))
     # algorithmic-byte roofline of the whole decode loop
     ctx_mid = P + NEW // 2
-    bytes_total = cycles * cycle_bytes(ctx_mid, K_LOOK, B)
+    bytes_total = cycles * cycle_bytes(ctx_mid, K_LOOK, B, q8)
     res["loop_bytes"] = bytes_total
     res["loop_GBs"] = bytes_total / (dec_ms / steps / 1e3) / 1e9
     res["models"] = (t, d, prompts)
@@ -146,17 +157,24 @@ def measured_traffic():
     return None
 
 
-def roofline_attention(ctx, w4=True):
+def roofline_attention(ctx, w4=True, q8=False):
     """Verify-step attention at the cfg4 mid-run shape: 32 sequences x 16
     heads, 6 queries, 320 cached keys (+6 new); one launch of the merged
-    split kernel.  Algorithmic bytes: K and V of every visible key once, the
-    queries read and the context rows written."""
+    split kernel.  Algorithmic bytes: K and V of every visible key once
+    (fp32 rows, or int8 codes and a scale per row), the queries read and
+    the context rows written."""
     sh = ATTN_SHAPE
     ms = nnhip.bench_attention(ctx, sh["B"], sh["S"], sh["H"], sh["D"],
-                               sh["n_cached"], iters=200, nbuf=4)
+                               sh["n_cached"], iters=200, nbuf=4,
+                               quantized=q8)
     byt = attention_bytes(sh["B"], sh["S"], sh["H"], sh["D"],
-                          sh["n_cached"] + sh["S"])
+                          sh["n_cached"] + sh["S"], q8)
     ach = byt / (ms / 1e3) / 1e9
+    if q8:
+        return dict(achieved=round(ach, 1), frac=round(ach / HBM_PEAK_GBS, 4),
+                    unit="GB/s", bytes_per_launch=byt,
+                    us_per_launch=round(ms * 1e3, 2),
+                    kernel="attn_kernel<8, 8, 4, int8 rows>")
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
                 traffic=measured_traffic(),
@@ -217,6 +235,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--no-kv-int8", action="store_true",
+                    help="skip the secondary run with int8 KV caches "
+                         "(generate_speculative(..., quantized_cache=true))")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the copy calibration and the attention "
                          "kernel (for rocprofv3 --pmc)")
@@ -246,6 +267,17 @@ def main():
         ctx.set_option(key, int(val))
     r = run_cfg4(ctx, a.steps, a.warmup)
     roof = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
+    kv8 = None
+    if not a.no_kv_int8:
+        r8 = run_cfg4(ctx, 1, 1, models=r["models"], q8=True)
+        kv8 = {"value": round(r8["value"], 1), "unit": "tokens/s",
+               "decode_ms": round(r8["decode_ms"], 2),
+               "cycles": r8["cycles"],
+               "acceptance": round(r8["accepted"] / max(r8["drafted"], 1), 4),
+               "loop_roofline": {
+                   "achieved_GBs": round(r8["loop_GBs"], 1),
+                   "frac": round(r8["loop_GBs"] / HBM_PEAK_GBS, 4)},
+               "attention": roofline_attention(ctx, q8=True)}
     b1 = None if a.no_batch1 else run_cfg2(ctx)
     cpu = None if a.no_cpu_baseline else cpu_baseline(r["models"])
     ms_step = r["wall_s"] / a.steps * 1e3
@@ -276,6 +308,7 @@ def main():
         "loop_roofline": {"achieved_GBs": round(r["loop_GBs"], 1),
                           "frac": round(r["loop_GBs"] / HBM_PEAK_GBS, 4)},
         "roofline": roof,
+        "kv_int8": kv8,
         "batch1": b1,
         "cpu_baseline": cpu,
     }

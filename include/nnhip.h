@@ -128,10 +128,18 @@ int nnhip_decoder_forward(nnhip_model *m, nnhip_kvcache *cache,
 
 /* ---- KV cache --------------------------------------------------------------
  * KVCache (layer.hpp:212-230) for `batch` sequences with one length each,
- * capacity max_seq_len.  quantized != 0 (int8 cache) returns
- * NNHIP_EUNSUPPORTED. */
+ * capacity max_seq_len.  quantized != 0 is KVCache(true): every appended
+ * k / v row of one head is stored as int8 codes with one fp32 scale
+ * (quantize_kv, layer.cpp:635-657) and attention reads code * scale
+ * (layer.cpp:878-890, 925-938); head dim even and <= 64. */
 int nnhip_kvcache_create(nnhip_model *m, int batch, int quantized,
                          nnhip_kvcache **out);
+/* KVCache::quantized_k / quantized_v / k_scales / v_scales (layer.hpp:
+ * 216-220) of one layer and sequence of an int8 cache, its first
+ * length(b) positions: codes [H][len][D] and scales [H][len] (host). */
+int nnhip_kvcache_read_q8(const nnhip_kvcache *c, int layer, int b,
+                          int8_t *kcodes, float *kscales, int8_t *vcodes,
+                          float *vscales);
 int nnhip_kvcache_free(nnhip_kvcache *c);
 int nnhip_kvcache_length(const nnhip_kvcache *c, int b, int *len);
 /* KVCache::truncate(len) (layer.cpp:67-149) for sequence b: an O(1) length
@@ -145,8 +153,10 @@ int nnhip_kvcache_truncate(nnhip_kvcache *c, int b, int len);
  * (host) receives the prompt and the generated ids.  Uniforms come from the
  * Philox stream u[seq][cycle][slot] (slot j < k: draft sample j, k + j:
  * accept test j, 2k: resample or bonus; cycle 0 slot 2k: first token)
- * instead of std::mt19937.  temperature <= 0 is greedy.  top_k in (0, V) or
- * top_p in (0, 1) and quantized_cache != 0 return NNHIP_EUNSUPPORTED. */
+ * instead of std::mt19937.  temperature <= 0 is greedy.  quantized_cache
+ * != 0 gives both models int8 KV caches (KVCache(true), layer.cpp:
+ * 1396-1398).  top_k in (0, V) or top_p in (0, 1) return
+ * NNHIP_EUNSUPPORTED. */
 int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
                                const int32_t *prompt, int P, int max_new,
                                int lookahead, float temperature, int top_k,
@@ -163,7 +173,8 @@ int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
                                      int max_new, int lookahead,
                                      float temperature, int top_k, float top_p,
                                      uint64_t seed, uint32_t seq0,
-                                     int32_t *out, nnhip_spec_stats *stats,
+                                     int quantized_cache, int32_t *out,
+                                     nnhip_spec_stats *stats,
                                      nnhip_spec_timing *timing);
 /* TransformerDecoder::generate_advanced(prompt, max_new_tokens, temperature,
  * top_k, top_p, seed, use_kv_cache) (layer.hpp:310-316, layer.cpp:
@@ -225,6 +236,22 @@ int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
 int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
                        const float *vcache, int cap, const int32_t *pos0,
                        int B, int S, int H, int Hkv, int D, float *out);
+/* nnhip_rope_kv_append into an int8 cache: RoPE on q and k, then each new
+ * k and v row of one head quantised as quantize_kv does (layer.cpp:635-657:
+ * scale = max|x| / 127, 1 when 0; code = clamp(round(x * (1 / scale)),
+ * -127, 127)) into kcodes / vcodes [B][H][cap][D] and kscales / vscales
+ * [B][H][cap].  D even and <= 64. */
+int nnhip_rope_kv_append_q8(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                            int H, int D, const int32_t *pos, float *q_out,
+                            int8_t *kcodes, float *kscales, int8_t *vcodes,
+                            float *vscales, int cap);
+/* nnhip_attention_kq over an int8 cache (layer.cpp:842-952, quantized
+ * branches): element j of a cached row enters as (float)code * scale.
+ * kcodes / vcodes [B][Hkv][cap][D], kscales / vscales [B][Hkv][cap]. */
+int nnhip_attention_kq_q8(nnhip_ctx *ctx, const float *q, const int8_t *kcodes,
+                          const float *kscales, const int8_t *vcodes,
+                          const float *vscales, int cap, const int32_t *pos0,
+                          int B, int S, int H, int Hkv, int D, float *out);
 /* LayerNorm::forward (layer.cpp:242-261), eps 1e-5, over rows of d. */
 int nnhip_layernorm(nnhip_ctx *ctx, const float *x, int rows, int d,
                     const float *gamma, const float *beta, float *y);
@@ -250,8 +277,11 @@ int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
  * mean per launch.  No counterpart in the reference (it has no benchmarks);
  * they time the verify-step attention and acceptance-sampling steps and the
  * W8A32 Linear of the decode path in isolation. */
+/* Verify attention over n_cached + S keys; quantized != 0 reads an int8
+ * cache (codes and per-row scales). */
 int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
-                          int n_cached, int iters, int nbuf, float *ms);
+                          int n_cached, int iters, int nbuf, int quantized,
+                          float *ms);
 /* n_accept (host [B] or NULL): accepted counts on input set 0. */
 int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
                             float temperature, int iters, int nbuf, float *ms,

@@ -256,11 +256,37 @@ int nnhip_kvcache_create(nnhip_model *m, int batch, int quantized,
                          nnhip_kvcache **out) {
   return guard([&] {
     REQ(m && out, "nnhip_kvcache_create: NULL argument");
-    NNHIP_REQUIRE(!quantized, nnhip::kErrUnsupported,
-                  "the int8 KV cache is not implemented on the device");
     std::unique_ptr<nnhip_kvcache> c(new nnhip_kvcache);
-    c->c.reset(new nnhip::KVCache(m->m.get(), batch, m->m->max_seq));
+    c->c.reset(new nnhip::KVCache(m->m.get(), batch, m->m->max_seq, quantized != 0));
     *out = c.release();
+  });
+}
+
+int nnhip_kvcache_read_q8(const nnhip_kvcache *c, int layer, int b,
+                          int8_t *kq, float *ks, int8_t *vq, float *vs) {
+  return guard([&] {
+    REQ(c && kq && ks && vq && vs, "nnhip_kvcache_read_q8: NULL argument");
+    const nnhip::KVCache &kv = *c->c;
+    REQ(kv.q8, "nnhip_kvcache_read_q8: the cache is not quantised");
+    REQ(layer >= 0 && layer < kv.m->L && b >= 0 && b < kv.B,
+        "nnhip_kvcache_read_q8: bad layer or sequence");
+    hipStream_t st = kv.m->ctx->stream;
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    const int H = kv.m->H, D = kv.m->D, n = kv.host_len[b];
+    const nnhip::KvSrc src = kv.src(layer, b);
+    for (int h = 0; h < H; ++h) {
+      const int64_t row0 = (int64_t)h * kv.cap;
+      NNHIP_CHECK(hipMemcpy(kq + (int64_t)h * n * D,
+                            (const int8_t *)src.k + row0 * D, (size_t)n * D,
+                            hipMemcpyDeviceToHost));
+      NNHIP_CHECK(hipMemcpy(vq + (int64_t)h * n * D,
+                            (const int8_t *)src.v + row0 * D, (size_t)n * D,
+                            hipMemcpyDeviceToHost));
+      NNHIP_CHECK(hipMemcpy(ks + (int64_t)h * n, src.ks + row0,
+                            (size_t)n * sizeof(float), hipMemcpyDeviceToHost));
+      NNHIP_CHECK(hipMemcpy(vs + (int64_t)h * n, src.vs + row0,
+                            (size_t)n * sizeof(float), hipMemcpyDeviceToHost));
+    }
   });
 }
 
@@ -298,12 +324,11 @@ int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
                                nnhip_spec_stats *stats) {
   return guard([&] {
     REQ(target && draft && prompt && out, "nnhip_generate_speculative: NULL argument");
-    NNHIP_REQUIRE(!quantized_cache, nnhip::kErrUnsupported,
-                  "the int8 KV cache is not implemented on the device");
     nnhip::SpecStats st{};
     nnhip::generate_speculative_batch(*target->m, *draft->m, 1, prompt, P,
                                       max_new, lookahead, temperature, top_k,
-                                      top_p, seed, 0, out, &st, nullptr);
+                                      top_p, seed, 0, quantized_cache != 0,
+                                      out, &st, nullptr);
     if (stats) std::memcpy(stats, &st, sizeof(st));
   });
 }
@@ -313,7 +338,8 @@ int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
                                      int max_new, int lookahead,
                                      float temperature, int top_k, float top_p,
                                      uint64_t seed, uint32_t seq0,
-                                     int32_t *out, nnhip_spec_stats *stats,
+                                     int quantized_cache, int32_t *out,
+                                     nnhip_spec_stats *stats,
                                      nnhip_spec_timing *timing) {
   return guard([&] {
     REQ(target && draft && prompts && out, "nnhip_generate_speculative_batch: NULL argument");
@@ -321,7 +347,7 @@ int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
     static_assert(sizeof(nnhip::SpecTiming) == sizeof(nnhip_spec_timing), "timing layout");
     nnhip::generate_speculative_batch(
         *target->m, *draft->m, B, prompts, P, max_new, lookahead, temperature,
-        top_k, top_p, seed, seq0, out,
+        top_k, top_p, seed, seq0, quantized_cache != 0, out,
         reinterpret_cast<nnhip::SpecStats *>(stats),
         reinterpret_cast<nnhip::SpecTiming *>(timing));
   });
@@ -480,6 +506,22 @@ int nnhip_linear_limb_totals(nnhip_ctx *ctx, const float *x, int rows, int K,
   });
 }
 
+// RoPE factors for positions [0, cap) by the reference's float formula
+// (tensor.cpp:1141-1173): theta = pow(10000, -2j/D), omega = pos * theta.
+static void rope_tables(int cap, int D, std::vector<float> &hc,
+                        std::vector<float> &hs) {
+  const int half = D / 2;
+  hc.assign((size_t)cap * half, 0.f);
+  hs.assign((size_t)cap * half, 0.f);
+  for (int p = 0; p < cap; ++p)
+    for (int j = 0; j < half; ++j) {
+      const float theta = std::pow(10000.0f, -2.0f * (float)j / (float)D);
+      const float omega = (float)p * theta;
+      hc[(size_t)p * half + j] = std::cos(omega);
+      hs[(size_t)p * half + j] = std::sin(omega);
+    }
+}
+
 int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
                          int H, int D, const int32_t *pos, float *q_out,
                          float *kcache, float *vcache, int cap) {
@@ -488,16 +530,8 @@ int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
             H > 0 && D > 0 && D % 2 == 0 && cap > 0,
         "nnhip_rope_kv_append: bad argument");
     hipStream_t st = ctx->c.stream;
-    // RoPE factors for positions [0, cap) by the reference's float formula
-    const int half = D / 2;
-    std::vector<float> hc((size_t)cap * half), hs((size_t)cap * half);
-    for (int p = 0; p < cap; ++p)
-      for (int j = 0; j < half; ++j) {
-        const float theta = std::pow(10000.0f, -2.0f * (float)j / (float)D);
-        const float omega = (float)p * theta;
-        hc[(size_t)p * half + j] = std::cos(omega);
-        hs[(size_t)p * half + j] = std::sin(omega);
-      }
+    std::vector<float> hc, hs;
+    rope_tables(cap, D, hc, hs);
     auto dc = upload(st, hc.data(), hc.size());
     auto ds = upload(st, hs.data(), hs.size());
     nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
@@ -517,9 +551,53 @@ int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
     const int max_keys = cap;
     const int64_t pe = nnhip::attention_partial_elems(B, S, H, D, max_keys);
     nnhip::DevBuf<float> part(pe > 0 ? pe : 1);
-    nnhip::launch_attention(st, q, kcache, vcache, B, S, H, Hkv, D, cap,
-                            (int64_t)Hkv * cap * D, pos0, 0, nullptr, max_keys,
-                            part.p, pe, out);
+    nnhip::KvSrc kv;
+    kv.k = kcache; kv.v = vcache; kv.seq_stride = (int64_t)Hkv * cap * D;
+    nnhip::launch_attention(st, q, kv, B, S, H, Hkv, D, cap, pos0, 0, nullptr,
+                            max_keys, part.p, pe, out);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+int nnhip_rope_kv_append_q8(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                            int H, int D, const int32_t *pos, float *q_out,
+                            int8_t *kcodes, float *kscales, int8_t *vcodes,
+                            float *vscales, int cap) {
+  return guard([&] {
+    REQ(ctx && qkv && pos && q_out && kcodes && kscales && vcodes && vscales &&
+            B > 0 && S > 0 && H > 0 && D > 0 && D % 2 == 0 && D <= 64 && cap > 0,
+        "nnhip_rope_kv_append_q8: bad argument");
+    hipStream_t st = ctx->c.stream;
+    std::vector<float> hc, hs;
+    rope_tables(cap, D, hc, hs);
+    auto dc = upload(st, hc.data(), hc.size());
+    auto ds = upload(st, hs.data(), hs.size());
+    nnhip::launch_rope_kv_q8(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
+                             q_out, kcodes, kscales, vcodes, vscales, cap,
+                             (int64_t)H * cap * D, (int64_t)H * cap);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
+int nnhip_attention_kq_q8(nnhip_ctx *ctx, const float *q, const int8_t *kcodes,
+                          const float *kscales, const int8_t *vcodes,
+                          const float *vscales, int cap, const int32_t *pos0,
+                          int B, int S, int H, int Hkv, int D, float *out) {
+  return guard([&] {
+    REQ(ctx && q && kcodes && kscales && vcodes && vscales && pos0 && out &&
+            B > 0 && S > 0 && H > 0 && Hkv > 0 && cap > 0,
+        "nnhip_attention_kq_q8: bad argument");
+    hipStream_t st = ctx->c.stream;
+    const int max_keys = cap;
+    const int64_t pe = nnhip::attention_partial_elems(B, S, H, D, max_keys);
+    nnhip::DevBuf<float> part(pe > 0 ? pe : 1);
+    nnhip::KvSrc kv;
+    kv.q8 = true;
+    kv.k = kcodes; kv.v = vcodes; kv.ks = kscales; kv.vs = vscales;
+    kv.seq_stride = (int64_t)Hkv * cap * D;
+    kv.sc_stride = (int64_t)Hkv * cap;
+    nnhip::launch_attention(st, q, kv, B, S, H, Hkv, D, cap, pos0, 0, nullptr,
+                            max_keys, part.p, pe, out);
     NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }

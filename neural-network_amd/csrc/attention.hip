@@ -14,6 +14,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <algorithm>
 #include <cmath>
 
@@ -155,6 +157,67 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
   }
 }
 
+// RoPE on q and k as rope_kv_kernel, then the append into an int8 cache:
+// quantize_kv of layer.cpp:635-657 on each new k row (after RoPE) and v row
+// of one head: scale = max|x| / 127 (1 when 0), code = clamp(round(x *
+// (1 / scale)), +-127), round half away from zero.  One wave per (row,
+// head): lane j < D/2 rotates pair j of q and k, lane 32 + j holds pair j
+// of v; each half-wave reduces its row's max.
+__global__ __launch_bounds__(256) void rope_kv_q8_kernel(
+    const float *__restrict__ qkv, int R, int S, int H, int D,
+    const int32_t *__restrict__ base, int off,
+    const int32_t *__restrict__ active, const float *__restrict__ cosb,
+    const float *__restrict__ sinb, float *__restrict__ qrot,
+    int8_t *__restrict__ kq, float *__restrict__ ks, int8_t *__restrict__ vq,
+    float *__restrict__ vs, int cap, int64_t seq_stride, int64_t sc_stride) {
+#pragma clang fp contract(off)
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= R * H) return;
+  const int t = wid / H, h = wid % H;
+  const int b = t / S, s = t % S;
+  if (active && !active[b]) return;
+  const int pos = base[b] + off + s;
+  if (pos < 0 || pos >= cap) return;
+  const int lane = threadIdx.x & 63, half = D / 2, E = H * D;
+  const bool vlane = lane >= 32;
+  const int j = lane & 31;
+  const bool own = j < half;
+  const int jj = own ? j : half - 1;
+  const float *row = qkv + (int64_t)t * 3 * E + h * D + 2 * jj;
+  float xe, xo;
+  if (!vlane) {
+    const float c = cosb[(int64_t)pos * half + jj];
+    const float sn = sinb[(int64_t)pos * half + jj];
+    const float qe = row[0], qo = row[1];
+    if (own) {
+      float *qd = qrot + (int64_t)t * E + h * D + 2 * jj;
+      qd[0] = qe * c - qo * sn;
+      qd[1] = qe * sn + qo * c;
+    }
+    const float ke = row[E], ko = row[E + 1];
+    xe = ke * c - ko * sn;
+    xo = ke * sn + ko * c;
+  } else {
+    xe = row[2 * E];
+    xo = row[2 * E + 1];
+  }
+  float mx = own ? fmaxf(fabsf(xe), fabsf(xo)) : 0.f;
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  float scale = mx / 127.0f;
+  if (scale == 0.0f) scale = 1.0f;
+  const float inv = 1.0f / scale;
+  const float ce = fmaxf(-127.0f, fminf(127.0f, roundf(xe * inv)));
+  const float co = fmaxf(-127.0f, fminf(127.0f, roundf(xo * inv)));
+  const int64_t rix = b * sc_stride + (int64_t)h * cap + pos;
+  int8_t *dst = (vlane ? vq : kq) + b * seq_stride + ((int64_t)h * cap + pos) * D + 2 * jj;
+  if (own) {
+    dst[0] = (int8_t)ce;
+    dst[1] = (int8_t)co;
+  }
+  if (j == 0) (vlane ? vs : ks)[rix] = scale;
+}
+
 // ---------------------------------------------------------------------------
 // Split-K attention: a wave per (key split, head, sequence, query block).
 // Either each wave is its own workgroup and writes its split's partial state
@@ -237,11 +300,37 @@ __device__ __forceinline__ void load_lane_dims(const float *p, int sub,
   }
 }
 
-template <int SQP, int DL, int W>
+// The same dims of an int8 row as int8 codes packed four to a word (byte i
+// of the lane's run in bits 8(i&3) of word i>>2).
+template <int DL>
+__device__ __forceinline__ void load_lane_codes(const int8_t *p, int sub,
+                                                uint32_t (&w)[2]) {
+  if constexpr (DL == 8) {
+    w[0] = *reinterpret_cast<const uint32_t *>(p + 4 * sub);
+    w[1] = *reinterpret_cast<const uint32_t *>(p + 32 + 4 * sub);
+  } else if constexpr (DL == 4) {
+    w[0] = *reinterpret_cast<const uint32_t *>(p + 4 * sub);
+    w[1] = 0u;
+  } else {
+    w[0] = 0u; w[1] = 0u;
+#pragma unroll
+    for (int i = 0; i < DL; ++i)
+      w[i >> 2] |= (uint32_t)(uint8_t)p[DL * sub + i] << (8 * (i & 3));
+  }
+}
+
+__device__ __forceinline__ float code_at(uint32_t w, int i) {
+  return (float)(int8_t)(w >> (8 * i));
+}
+
+// A chunk's K rows in flight: fp32 dims, or codes and the rows' scales.
+template <bool Q8> struct KChunk { float kr[4][8]; };
+template <> struct KChunk<true> { uint32_t kc[4][2]; float ks[4]; };
+
+template <int SQP, int DL, int W, bool Q8>
 __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
-    const float *__restrict__ q, const float *__restrict__ kc,
-    const float *__restrict__ vc, int S, int H, int Hkv, int cap,
-    int64_t seq_stride, const int32_t *__restrict__ base, int off,
+    const float *__restrict__ q, KvSrc kv, int S, int H, int Hkv, int cap,
+    const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
     float qscale, float *__restrict__ part, float *__restrict__ out) {
   constexpr int D = DL * 8;
@@ -277,8 +366,12 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
       : (((kend_all + kChunk - 1) / kChunk + W - 1) / W) * kChunk;
   const int ks = sp * kspan;
   const int kend = min(ks + kspan, kend_all);
-  const float *kb = kc + b * seq_stride + (int64_t)hk * cap * D;
-  const float *vb = vc + b * seq_stride + (int64_t)hk * cap * D;
+  using KT = typename std::conditional<Q8, int8_t, float>::type;
+  const KT *kb = static_cast<const KT *>(kv.k) + b * kv.seq_stride + (int64_t)hk * cap * D;
+  const KT *vb = static_cast<const KT *>(kv.v) + b * kv.seq_stride + (int64_t)hk * cap * D;
+  // int8 rows: the scales of this (sequence, kv head)
+  const float *ksb = Q8 ? kv.ks + b * kv.sc_stride + (int64_t)hk * cap : nullptr;
+  const float *vsb = Q8 ? kv.vs + b * kv.sc_stride + (int64_t)hk * cap : nullptr;
   const int r = min(lane / NQ4, KPI - 1), dq = lane % NQ4;
   const bool pv_lane = lane < KPI * NQ4;
 
@@ -300,21 +393,52 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
   // past the split end re-read the last valid row and are masked.  The
   // next chunk's K rows are requested before the current chunk is worked on
   // (two register buffers, used in turn); its V rows, needed only after the
-  // scores, at the start of its own turn.
-  struct Chunk { float kr[4][8]; };
+  // scores, at the start of its own turn.  An int8 row enters as
+  // (float)code * scale per element, the product layer.cpp:886-887 and
+  // :932-934 form.
+  using Chunk = KChunk<Q8>;
   auto load_chunk = [&](int c0, Chunk &ck) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      load_lane_dims<DL>(kb + (int64_t)min(c0 + g + 8 * t, kend - 1) * D, sub,
-                         ck.kr[t]);
+    for (int t = 0; t < 4; ++t) {
+      const int j = min(c0 + g + 8 * t, kend - 1);
+      if constexpr (Q8) {
+        load_lane_codes<DL>(kb + (int64_t)j * D, sub, ck.kc[t]);
+        ck.ks[t] = ksb[j];
+      } else {
+        load_lane_dims<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+      }
+    }
   };
   auto work_chunk = [&](int c0, const Chunk &ck) {
-    const auto &kr = ck.kr;
     float4 vv[TPV];
+    float kr[4][8];
+    if constexpr (Q8) {
+      uint32_t vw[TPV];
+      float vsc[TPV];
 #pragma unroll
-    for (int t = 0; t < TPV; ++t)
-      vv[t] = *reinterpret_cast<const float4 *>(
-          vb + (int64_t)min(c0 + r + KPI * t, kend - 1) * D + dq * 4);
+      for (int t = 0; t < TPV; ++t) {
+        const int row = min(c0 + r + KPI * t, kend - 1);
+        vw[t] = *reinterpret_cast<const uint32_t *>(vb + (int64_t)row * D + dq * 4);
+        vsc[t] = vsb[row];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) kr[t][x] = code_at(ck.kc[t][x >> 2], x & 3) * ck.ks[t];
+#pragma unroll
+      for (int t = 0; t < TPV; ++t)
+        vv[t] = make_float4(code_at(vw[t], 0) * vsc[t], code_at(vw[t], 1) * vsc[t],
+                            code_at(vw[t], 2) * vsc[t], code_at(vw[t], 3) * vsc[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) kr[t][x] = ck.kr[t][x];
+#pragma unroll
+      for (int t = 0; t < TPV; ++t)
+        vv[t] = *reinterpret_cast<const float4 *>(
+            vb + (int64_t)min(c0 + r + KPI * t, kend - 1) * D + dq * 4);
+    }
     // scores of this lane's query for keys c0 + g + 8t
     float sc[4], cm = -INFINITY;
 #pragma unroll
@@ -716,6 +840,21 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
   NNHIP_CHECK(hipGetLastError());
 }
 
+void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
+                       int D, const int32_t *base, int off,
+                       const int32_t *active, const float *cosb,
+                       const float *sinb, float *qrot, int8_t *kq, float *ks,
+                       int8_t *vq, float *vs, int cap, int64_t seq_stride,
+                       int64_t sc_stride) {
+  NNHIP_REQUIRE(D % 2 == 0 && D <= 64, kErrArg,
+                "rope_kv_q8: head dim must be even and <= 64");
+  const int R = B * S;
+  hipLaunchKernelGGL(rope_kv_q8_kernel, dim3((R * H + 3) / 4), dim3(256), 0,
+                     st, qkv, R, S, H, D, base, off, active, cosb, sinb, qrot,
+                     kq, ks, vq, vs, cap, seq_stride, sc_stride);
+  NNHIP_CHECK(hipGetLastError());
+}
+
 int g_attn_waves = 4096;
 int g_attn_w4 = 1;
 
@@ -745,14 +884,15 @@ bool attention_merged(int D, int max_keys) {
          max_keys <= kMergedWaves * kMergedChunks * kChunk;
 }
 
-bool launch_attention(hipStream_t st, const float *q, const float *kc,
-                      const float *vc, int B, int S, int H, int Hkv, int D,
-                      int cap, int64_t seq_stride, const int32_t *base,
-                      int off, const int32_t *active, int max_keys,
-                      float *part, int64_t part_elems, float *out,
-                      int8_t *limbs, int mpad, int *rexp) {
+bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
+                      int S, int H, int Hkv, int D, int cap,
+                      const int32_t *base, int off, const int32_t *active,
+                      int max_keys, float *part, int64_t part_elems,
+                      float *out, int8_t *limbs, int mpad, int *rexp) {
   NNHIP_REQUIRE(D % 8 == 0 && D <= kMaxD, kErrArg,
                 "attention: head dim must be a multiple of 8 and <= 64");
+  NNHIP_REQUIRE(!kv.q8 || (kv.ks && kv.vs), kErrArg,
+                "attention: int8 rows need their scales");
   NNHIP_REQUIRE(Hkv > 0 && H % Hkv == 0, kErrArg, "attention: bad kv heads");
   NNHIP_REQUIRE(H * D <= 4096, kErrArg, "attention: H*D must be <= 4096");
   NNHIP_REQUIRE(!limbs || ((H * D) % 128 == 0 && B * S <= mpad), kErrArg,
@@ -768,11 +908,16 @@ bool launch_attention(hipStream_t st, const float *q, const float *kc,
     kps = (kps + kChunk - 1) / kChunk * kChunk;
     dim3 grid(1, H, B * nqb);
 #define NNHIP_ATTN(SQP, DL, W)                                                \
-  hipLaunchKernelGGL((attn_kernel<SQP, DL, W>), grid, dim3(kWave * W), 0, st, \
-                     q, kc, vc, S, H, Hkv, cap, seq_stride, base, off, active, \
-                     W, nqb, kps, qscale, nullptr, out)
+  if (kv.q8)                                                                  \
+    hipLaunchKernelGGL((attn_kernel<SQP, DL, W, true>), grid, dim3(kWave * W),  \
+                       0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
+                       kps, qscale, nullptr, out);                              \
+  else                                                                        \
+    hipLaunchKernelGGL((attn_kernel<SQP, DL, W, false>), grid, dim3(kWave * W), \
+                       0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
+                       kps, qscale, nullptr, out)
 #define NNHIP_ATTN_D(SQP, W)                                                  \
-  if (D == 32) NNHIP_ATTN(SQP, 4, W); else NNHIP_ATTN(SQP, 8, W);
+  if (D == 32) { NNHIP_ATTN(SQP, 4, W); } else { NNHIP_ATTN(SQP, 8, W); }
     // many-query rows hold many registers (one workgroup of 8 waves per CU):
     // with 4 waves two workgroups share a CU and a launch runs in one round
     const bool w4 = g_attn_w4 && max_keys <= kMergedWaves4 * kMergedChunks * kChunk;
@@ -791,19 +936,24 @@ bool launch_attention(hipStream_t st, const float *q, const float *kc,
                 kErrArg, "attention: partial buffer too small");
   dim3 grid(nsplit, H, B * nqb);
 #define NNHIP_ATTN(SQP, DL)                                                   \
-  hipLaunchKernelGGL((attn_kernel<SQP, DL, 1>), grid, dim3(kWave), 0, st, q,  \
-                     kc, vc, S, H, Hkv, cap, seq_stride, base, off, active,   \
-                     nsplit, nqb, kps, qscale, part, nullptr)
+  if (kv.q8)                                                                  \
+    hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, true>), grid, dim3(kWave), 0,  \
+                       st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
+                       nqb, kps, qscale, part, nullptr);                      \
+  else                                                                        \
+    hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, false>), grid, dim3(kWave), 0, \
+                       st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
+                       nqb, kps, qscale, part, nullptr)
 #define NNHIP_ATTN_D(SQP)                                                     \
   switch (D / 8) {                                                            \
-    case 1: NNHIP_ATTN(SQP, 1); break;                                        \
-    case 2: NNHIP_ATTN(SQP, 2); break;                                        \
-    case 3: NNHIP_ATTN(SQP, 3); break;                                        \
-    case 4: NNHIP_ATTN(SQP, 4); break;                                        \
-    case 5: NNHIP_ATTN(SQP, 5); break;                                        \
-    case 6: NNHIP_ATTN(SQP, 6); break;                                        \
-    case 7: NNHIP_ATTN(SQP, 7); break;                                        \
-    default: NNHIP_ATTN(SQP, 8); break;                                       \
+    case 1: { NNHIP_ATTN(SQP, 1); } break;                                    \
+    case 2: { NNHIP_ATTN(SQP, 2); } break;                                    \
+    case 3: { NNHIP_ATTN(SQP, 3); } break;                                    \
+    case 4: { NNHIP_ATTN(SQP, 4); } break;                                    \
+    case 5: { NNHIP_ATTN(SQP, 5); } break;                                    \
+    case 6: { NNHIP_ATTN(SQP, 6); } break;                                    \
+    case 7: { NNHIP_ATTN(SQP, 7); } break;                                    \
+    default: { NNHIP_ATTN(SQP, 8); } break;                                   \
   }
   if (sq == 1) NNHIP_ATTN_D(1)
   else if (sq == 2) NNHIP_ATTN_D(2)

@@ -29,9 +29,12 @@ extern "C" {
 
 // Verify-step attention: B sequences x H heads, S new queries per sequence
 // attending causally among themselves and fully to n_cached cached
-// positions (keys n_cached + S), K/V entries N(0, 1).
+// positions (keys n_cached + S), K/V entries N(0, 1); quantized != 0 reads
+// an int8 cache instead (constant codes and scales: the timing does not
+// depend on the values).
 int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
-                          int n_cached, int iters, int nbuf, float *ms) {
+                          int n_cached, int iters, int nbuf, int quantized,
+                          float *ms) {
   return guard([&] {
     NNHIP_REQUIRE(ctx && ms && B > 0 && S > 0 && H > 0 && D > 0 &&
                       n_cached >= 0 && iters > 0 && nbuf > 0,
@@ -39,13 +42,24 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
     hipStream_t st = ctx->c.stream;
     const int cap = n_cached + S;
     const int64_t kv = (int64_t)B * H * cap * D;
+    const int64_t ns = (int64_t)B * H * cap;
     std::vector<nnhip::DevBuf<float>> K(nbuf), Vv(nbuf), Q(nbuf), O(nbuf);
+    std::vector<nnhip::DevBuf<int8_t>> Kq(nbuf), Vq(nbuf);
+    std::vector<nnhip::DevBuf<float>> Ks(nbuf), Vs(nbuf);
     for (int i = 0; i < nbuf; ++i) {
-      K[i].alloc(kv); Vv[i].alloc(kv);
       Q[i].alloc((size_t)B * S * H * D); O[i].alloc((size_t)B * S * H * D);
-      nnhip::launch_init_normal(st, K[i].p, 1, (int)kv, 0, 1, 1000 + i, 0, 1.f, 0);
-      nnhip::launch_init_normal(st, Vv[i].p, 1, (int)kv, 0, 1, 2000 + i, 0, 1.f, 0);
       nnhip::launch_init_normal(st, Q[i].p, 1, B * S * H * D, 0, 1, 3000 + i, 0, 1.f, 0);
+      if (quantized) {
+        Kq[i].alloc(kv); Vq[i].alloc(kv); Ks[i].alloc(ns); Vs[i].alloc(ns);
+        NNHIP_CHECK(hipMemsetAsync(Kq[i].p, 0x25, (size_t)kv, st));
+        NNHIP_CHECK(hipMemsetAsync(Vq[i].p, 0x1b, (size_t)kv, st));
+        nnhip::launch_fill(st, Ks[i].p, ns, 0.02f);
+        nnhip::launch_fill(st, Vs[i].p, ns, 0.02f);
+      } else {
+        K[i].alloc(kv); Vv[i].alloc(kv);
+        nnhip::launch_init_normal(st, K[i].p, 1, (int)kv, 0, 1, 1000 + i, 0, 1.f, 0);
+        nnhip::launch_init_normal(st, Vv[i].p, 1, (int)kv, 0, 1, 2000 + i, 0, 1.f, 0);
+      }
     }
     std::vector<int32_t> hpos(B, n_cached);
     nnhip::DevBuf<int32_t> pos(B);
@@ -54,9 +68,17 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
     nnhip::DevBuf<float> part(pe > 0 ? pe : 1);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      nnhip::launch_attention(st, Q[j].p, K[j].p, Vv[j].p, B, S, H, H, D, cap,
-                              (int64_t)H * cap * D, pos.p, 0, nullptr, cap,
-                              part.p, pe, O[j].p);
+      nnhip::KvSrc src;
+      src.seq_stride = (int64_t)H * cap * D;
+      if (quantized) {
+        src.q8 = true;
+        src.k = Kq[j].p; src.v = Vq[j].p; src.ks = Ks[j].p; src.vs = Vs[j].p;
+        src.sc_stride = (int64_t)H * cap;
+      } else {
+        src.k = K[j].p; src.v = Vv[j].p;
+      }
+      nnhip::launch_attention(st, Q[j].p, src, B, S, H, H, D, cap, pos.p, 0,
+                              nullptr, cap, part.p, pe, O[j].p);
     });
   });
 }

@@ -418,24 +418,33 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   bool have_norm2 = false;
   for (int l = 0; l < L; ++l) {
     LayerW &ly = layers[l];
-    float *kc = kv->k.p + (int64_t)l * kv->layer_stride() + b_off * kv->seq_stride();
-    float *vc = kv->v.p + (int64_t)l * kv->layer_stride() + b_off * kv->seq_stride();
-    // q, k, v projection with RoPE and the KV append in its epilogue
-    RopeArgs ra;
-    ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
-    ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
-    ra.qrot = ws.qrot.p; ra.kc = kc; ra.vc = vc; ra.seq_stride = kv->seq_stride();
-    linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
-              l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
+    const KvSrc kvs = kv->src(l, b_off);
+    if (kv->q8) {
+      // q, k, v rows, then RoPE and the quantised append
+      linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
+                l == 0 && emb_digits, nullptr, 0, ws.qkv.p, 3 * d, kEpiBias);
+      launch_rope_kv_q8(st, ws.qkv.p, B, S, H, D, bp, off, active, cosb.p,
+                        sinb.p, ws.qrot.p, (int8_t *)kvs.k, (float *)kvs.ks,
+                        (int8_t *)kvs.v, (float *)kvs.vs, kv->cap,
+                        kvs.seq_stride, kvs.sc_stride);
+    } else {
+      // q, k, v projection with RoPE and the KV append in its epilogue
+      RopeArgs ra;
+      ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
+      ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
+      ra.qrot = ws.qrot.p; ra.kc = (float *)kvs.k; ra.vc = (float *)kvs.v;
+      ra.seq_stride = kvs.seq_stride;
+      linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
+                l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
+    }
     // short contexts: the attention workgroups merge their key splits and
     // write ctx; the output projection then digitises ctx itself.  Long
     // ones: split attention + combine, which also writes ctx's digits.
     const bool merged = attention_merged(D, max_keys);
     const bool lo = !merged && (use_lds(ly.o, R) || use_limbs(ly.o, R));
-    launch_attention(st, ws.qrot.p, kc, vc, B, S, H, H, D, kv->cap,
-                     kv->seq_stride(), bp, off, active, max_keys, ws.part.p,
-                     ws.part_elems, ws.ctx.p, lo ? ws.limbs.p : nullptr,
-                     ws.mpad, ws.rexp.p);
+    launch_attention(st, ws.qrot.p, kvs, B, S, H, H, D, kv->cap, bp, off,
+                     active, max_keys, ws.part.p, ws.part_elems, ws.ctx.p,
+                     lo ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
     if (merged && ly.o.quant && ly.o.qs.p && R >= kLimbMinRows &&
         gemm_lds_supports(R, d, d))
       launch_gemm_lds(st, kAFromRows, nullptr, 0, nullptr, ws.ctx.p, d,
@@ -479,15 +488,41 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
 }
 
-KVCache::KVCache(Model *model, int batch, int capacity)
-    : m(model), B(batch), cap(capacity) {
+KVCache::KVCache(Model *model, int batch, int capacity, bool quantized)
+    : m(model), B(batch), cap(capacity), q8(quantized) {
   NNHIP_REQUIRE(batch > 0 && capacity > 0, kErrArg, "kvcache: bad size");
+  NNHIP_REQUIRE(!q8 || (m->D % 2 == 0 && m->D <= 64), kErrUnsupported,
+                "kvcache: the int8 cache needs an even head dim <= 64");
   const size_t n = (size_t)m->L * B * m->H * cap * m->D;
-  k.alloc(n);
-  v.alloc(n);
+  if (q8) {
+    const size_t ns = (size_t)m->L * B * m->H * cap;
+    kq.alloc(n);
+    vq.alloc(n);
+    ks.alloc(ns);
+    vs.alloc(ns);
+  } else {
+    k.alloc(n);
+    v.alloc(n);
+  }
   len.alloc(B);
   host_len.assign(B, 0);
   sync_len_to_device();
+}
+
+KvSrc KVCache::src(int l, int b_off) const {
+  KvSrc s;
+  s.q8 = q8;
+  s.seq_stride = seq_stride();
+  s.sc_stride = sc_seq_stride();
+  const int64_t o = (int64_t)l * layer_stride() + b_off * seq_stride();
+  if (q8) {
+    const int64_t so = (int64_t)l * sc_layer_stride() + b_off * sc_seq_stride();
+    s.k = kq.p + o; s.v = vq.p + o;
+    s.ks = ks.p + so; s.vs = vs.p + so;
+  } else {
+    s.k = k.p + o; s.v = v.p + o;
+  }
+  return s;
 }
 
 void KVCache::sync_len_to_device() {
@@ -531,7 +566,8 @@ void check_sampling_options(int V, int top_k, float top_p) {
 void generate_speculative_batch(Model &t, Model &dm, int B,
                                 const int32_t *prompts, int P, int max_new,
                                 int k, float T, int top_k, float top_p,
-                                uint64_t seed, uint32_t seq0, int32_t *out,
+                                uint64_t seed, uint32_t seq0,
+                                bool quantized_cache, int32_t *out,
                                 SpecStats *stats, SpecTiming *timing) {
   NNHIP_REQUIRE(t.ctx == dm.ctx, kErrArg, "target and draft need one context");
   NNHIP_REQUIRE(t.V == dm.V, kErrArg, "target and draft vocabularies differ");
@@ -550,7 +586,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   const int V = t.V;
   const int out_stride = P + std::max(max_new, 1);
 
-  KVCache tc(&t, B, t_need), dc(&dm, B, d_need);
+  // KVCache(quantized_cache) for both models (layer.cpp:1396-1398)
+  KVCache tc(&t, B, t_need, quantized_cache), dc(&dm, B, d_need, quantized_cache);
   SpecBuffers bf;
   bf.cur.alloc(B); bf.cand.alloc((size_t)B * k); bf.tlen.alloc(B);
   bf.dlen.alloc(B); bf.gen.alloc(B); bf.cyc.alloc(B); bf.active.alloc(B);

@@ -115,16 +115,25 @@ struct Model {
 };
 
 // Ragged KV cache for B sequences: per layer [B][H][cap][D], one length per
-// sequence (KVCache, layer.hpp:212-230, with per-sequence lengths).
+// sequence (KVCache, layer.hpp:212-230, with per-sequence lengths).  A
+// quantised cache (KVCache(true)) holds int8 codes in the same layout and one
+// fp32 scale per (sequence, head, position) for k and for v.
 struct KVCache {
   Model *m = nullptr;
   int B = 0, cap = 0;
-  DevBuf<float> k, v;
+  bool q8 = false;
+  DevBuf<float> k, v;          // fp32 cache
+  DevBuf<int8_t> kq, vq;       // int8 cache: codes
+  DevBuf<float> ks, vs;        //             scales [L][B][H][cap]
   DevBuf<int32_t> len;
   std::vector<int32_t> host_len;
-  KVCache(Model *model, int batch, int capacity);
+  KVCache(Model *model, int batch, int capacity, bool quantized = false);
   int64_t seq_stride() const { return (int64_t)m->H * cap * m->D; }
   int64_t layer_stride() const { return (int64_t)B * seq_stride(); }
+  int64_t sc_seq_stride() const { return (int64_t)m->H * cap; }
+  int64_t sc_layer_stride() const { return (int64_t)B * sc_seq_stride(); }
+  // the rows layer l's attention reads for sequences [b_off, B)
+  KvSrc src(int l, int b_off) const;
   void sync_len_to_device();
 };
 
@@ -141,7 +150,8 @@ struct SpecTiming {
 void generate_speculative_batch(Model &target, Model &draft, int B,
                                 const int32_t *prompts, int P, int max_new,
                                 int k, float T, int top_k, float top_p,
-                                uint64_t seed, uint32_t seq0, int32_t *out,
+                                uint64_t seed, uint32_t seq0,
+                                bool quantized_cache, int32_t *out,
                                 SpecStats *stats, SpecTiming *timing);
 
 // generate_advanced (layer.cpp:1240-1380) for B independent sequences.

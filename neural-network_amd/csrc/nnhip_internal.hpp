@@ -325,16 +325,35 @@ void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
                     int D, const int32_t *base, int off, const int32_t *active,
                     const float *cosb, const float *sinb, float *qrot,
                     float *kc, float *vc, int cap, int64_t seq_stride);
+// RoPE on q and k, then the append into an int8 cache: each new k / v row
+// (one head, one position) is quantised as quantize_kv does
+// (layer.cpp:635-657); codes [B][H][cap][D] (seq_stride codes per
+// sequence), scales [B][H][cap] (sc_stride per sequence).
+void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
+                       int D, const int32_t *base, int off,
+                       const int32_t *active, const float *cosb,
+                       const float *sinb, float *qrot, int8_t *kq, float *ks,
+                       int8_t *vq, float *vs, int cap, int64_t seq_stride,
+                       int64_t sc_stride);
+// K / V rows an attention launch reads: fp32 rows, or int8 codes with one
+// fp32 scale per (head, position) row (KVCache(quantized=true),
+// layer.hpp:212-230).  Rows [B][Hkv][cap][D], seq_stride elements apart
+// per sequence; scales [B][Hkv][cap], sc_stride apart.
+struct KvSrc {
+  const void *k = nullptr, *v = nullptr;
+  const float *ks = nullptr, *vs = nullptr;
+  int64_t seq_stride = 0, sc_stride = 0;
+  bool q8 = false;
+};
 // true when launch_attention writes the context rows without the combine
 // kernel (and so without digit planes)
 bool attention_merged(int D, int max_keys);
 // returns whether the digit planes were written
-bool launch_attention(hipStream_t st, const float *q, const float *kc,
-                      const float *vc, int B, int S, int H, int Hkv, int D,
-                      int cap, int64_t seq_stride, const int32_t *base,
-                      int off, const int32_t *active, int max_keys,
-                      float *part, int64_t part_elems, float *out,
-                      int8_t *limbs = nullptr, int mpad = 0,
+bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
+                      int S, int H, int Hkv, int D, int cap,
+                      const int32_t *base, int off, const int32_t *active,
+                      int max_keys, float *part, int64_t part_elems,
+                      float *out, int8_t *limbs = nullptr, int mpad = 0,
                       int *rexp = nullptr);
 int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys);
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,

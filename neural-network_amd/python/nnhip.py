@@ -58,13 +58,15 @@ SIGNATURES = {
     "nnhip_decoder_get_quantized": [_vp, _i, _i, _vp, _vp],
     "nnhip_decoder_forward": [_vp, _vp, _vp, _i, _i, _vp],
     "nnhip_kvcache_create": [_vp, _i, _i, _pp],
+    "nnhip_kvcache_read_q8": [_vp, _i, _i, _vp, _vp, _vp, _vp],
     "nnhip_kvcache_free": [_vp],
     "nnhip_kvcache_length": [_vp, _i, C.POINTER(C.c_int)],
     "nnhip_kvcache_truncate": [_vp, _i, _i],
     "nnhip_generate_speculative": [_vp, _vp, _vp, _i, _i, _i, _f, _i, _f,
                                    _u64, _i, _vp, _vp],
     "nnhip_generate_speculative_batch": [_vp, _vp, _i, _vp, _i, _i, _i, _f,
-                                         _i, _f, _u64, _u32, _vp, _vp, _vp],
+                                         _i, _f, _u64, _u32, _i, _vp, _vp,
+                                         _vp],
     "nnhip_generate_advanced": [_vp, _vp, _i, _i, _f, _i, _f, _u64, _i, _vp],
     "nnhip_generate_advanced_batch": [_vp, _i, _vp, _i, _i, _f, _i, _f, _u64,
                                       _u32, _i, _vp],
@@ -78,11 +80,15 @@ SIGNATURES = {
                              _i],
     "nnhip_attention_kq": [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i,
                            _vp],
+    "nnhip_rope_kv_append_q8": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _i],
+    "nnhip_attention_kq_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i,
+                              _i, _i, _i, _vp],
     "nnhip_layernorm": [_vp, _vp, _i, _i, _vp, _vp, _vp],
     "nnhip_sample_rows": [_vp, _vp, _i, _i, _f, _vp, _vp, _vp],
     "nnhip_spec_accept": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp,
                           _vp],
-    "nnhip_bench_attention": [_vp, _i, _i, _i, _i, _i, _i, _i,
+    "nnhip_bench_attention": [_vp, _i, _i, _i, _i, _i, _i, _i, _i,
                               C.POINTER(C.c_float)],
     "nnhip_bench_spec_accept": [_vp, _i, _i, _i, _f, _i, _i,
                                 C.POINTER(C.c_float), _vp],
@@ -196,10 +202,11 @@ class DeviceArray:
             pass
 
 
-def bench_attention(ctx, B, S, H, D, n_cached, iters=100, nbuf=3):
+def bench_attention(ctx, B, S, H, D, n_cached, iters=100, nbuf=3,
+                    quantized=False):
     ms = C.c_float()
     call("nnhip_bench_attention", ctx.h, B, S, H, D, n_cached, iters, nbuf,
-         C.byref(ms))
+         int(quantized), C.byref(ms))
     return ms.value
 
 
@@ -292,7 +299,8 @@ class Decoder:
         return out[:len(prompt) + max_new], st
 
     def generate_speculative_batch(self, draft, prompts, max_new, lookahead,
-                                   T, seed, seq0=0, top_k=0, top_p=1.0):
+                                   T, seed, seq0=0, top_k=0, top_p=1.0,
+                                   quantized_cache=False):
         prompts = np.ascontiguousarray(prompts, np.int32)
         B, P = prompts.shape
         out = np.zeros((B, P + max(max_new, 1)), np.int32)
@@ -300,7 +308,7 @@ class Decoder:
         tm = SpecTiming()
         call("nnhip_generate_speculative_batch", self.h, draft.h, B,
              ptr(prompts), P, max_new, lookahead, T, top_k, top_p, seed,
-             seq0, ptr(out), stats, C.byref(tm))
+             seq0, int(quantized_cache), ptr(out), stats, C.byref(tm))
         return out[:, :P + max_new], list(stats), tm
 
     def generate_advanced(self, prompt, max_new, T, seed=42,
@@ -341,3 +349,15 @@ class KVCache:
 
     def truncate(self, n, b=0):
         call("nnhip_kvcache_truncate", self.h, b, n)
+
+    def read_q8(self, layer, b=0, heads=None, head_dim=None):
+        """Codes and scales of one layer and sequence of an int8 cache:
+        (kq [H][len][D], ks [H][len], vq, vs)."""
+        n = self.length(b)
+        kq = np.zeros((heads, n, head_dim), np.int8)
+        vq = np.zeros_like(kq)
+        ks = np.zeros((heads, n), np.float32)
+        vs = np.zeros_like(ks)
+        call("nnhip_kvcache_read_q8", self.h, layer, b, ptr(kq), ptr(ks),
+             ptr(vq), ptr(vs))
+        return kq, ks, vq, vs

@@ -71,7 +71,15 @@ struct or_model {
 
 struct or_cache {
   int L, H, D, cap, len;
-  float *k, *v;             /* [L][H][cap][D] */
+  int quantized;            /* KVCache(quantized) (layer.hpp:223) */
+  float *k, *v;             /* fp32 cache: [L][H][cap][D] */
+  int8_t *kq, *vq;          /* int8 cache: codes [L][H][cap][D] */
+  float *ks, *vs;           /*             scales [L][H][cap] */
+  /* checker state of an int8 cache (no counterpart in the reference):
+   * the rows as they were before quantisation, and `frozen`, under which an
+   * append leaves the codes already stored at the new positions in place */
+  float *kraw, *vraw;       /* [L][H][cap][D] */
+  int frozen;
 };
 
 static void dense_init(or_dense_t *dn, int64_t in, int64_t out) {
@@ -350,21 +358,153 @@ void or_attention(const float *q, const float *k, const float *v, int64_t H,
   free(row);
 }
 
+/* quantize_kv of MultiHeadAttention::forward (layer.cpp:635-657) over rows
+ * of D values: scale = max|x| / 127 (1 when 0), code = clamp(round(x *
+ * (1 / scale)), -127, 127), round half away from zero. */
+void or_quantize_kv(const float *src, int64_t rows, int64_t D, int8_t *codes,
+                    float *scales) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *x = src + r * D;
+    float mx = 0.0f;
+    for (int64_t d = 0; d < D; ++d) {
+      float a = fabsf(x[d]);
+      if (a > mx) mx = a;
+    }
+    float scale = mx / 127.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    scales[r] = scale;
+    float inv = 1.0f / scale;
+    for (int64_t d = 0; d < D; ++d) {
+      float qv = roundf(x[d] * inv);
+      qv = fmaxf(-127.0f, fminf(127.0f, qv));
+      codes[r * D + d] = (int8_t)qv;
+    }
+  }
+}
+
+/* Fused attention over an int8 cache (layer.cpp:842-952, quantized
+ * branches :878-890 and :925-938): every cached element enters as
+ * (float)code * scale of its row, in the same products and order as the
+ * fp32 path.  kq / vq [H_kv][S_total][D], ks / vs [H_kv][S_total]. */
+void or_attention_q8(const float *q, const int8_t *kq, const float *ks,
+                     const int8_t *vq, const float *vs, int64_t H,
+                     int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
+                     int causal, float *out) {
+  int64_t S_past = S_total - S;
+  int64_t group = H / H_kv;
+  float scale = sqrtf((float)D);
+  float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
+  for (int64_t h = 0; h < H; ++h) {
+    int64_t hk = h / group;
+    for (int64_t i = 0; i < S; ++i) {
+      float mx = -INFINITY;
+      const float *qi = q + (h * S + i) * D;
+      for (int64_t j = 0; j < S_total; ++j) {
+        if (causal && j > S_past + i) { row[j] = -1e9f; continue; }
+        const int8_t *kj = kq + (hk * S_total + j) * D;
+        float ksc = ks[hk * S_total + j];
+        float dot = 0.0f;
+        for (int64_t dd = 0; dd < D; ++dd) dot += qi[dd] * ((float)kj[dd] * ksc);
+        float sc = dot / scale;
+        row[j] = sc;
+        if (sc > mx) mx = sc;
+      }
+      float sum = 0.0f;
+      for (int64_t j = 0; j < S_total; ++j) {
+        if (causal && j > S_past + i) { row[j] = 0.0f; continue; }
+        float e = expf(row[j] - mx);
+        row[j] = e;
+        sum += e;
+      }
+      if (sum > 0.0f) {
+        float inv = 1.0f / sum;
+        for (int64_t j = 0; j < S_total; ++j) row[j] *= inv;
+      }
+      float *o = out + (i * H + h) * D;
+      for (int64_t dd = 0; dd < D; ++dd) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < S_total; ++j) {
+          if (row[j] == 0.0f) continue;
+          acc += row[j] * ((float)vq[(hk * S_total + j) * D + dd] *
+                           vs[hk * S_total + j]);
+        }
+        o[dd] = acc;
+      }
+    }
+  }
+  free(row);
+}
+
 /* ------------------------------------------------------------------ */
 /* Cache and forward                                                   */
 /* ------------------------------------------------------------------ */
-or_cache *or_cache_create(const or_model *m) {
+or_cache *or_cache_create_q(const or_model *m, int quantized) {
   or_cache *c = (or_cache *)calloc(1, sizeof(or_cache));
   c->L = m->L; c->H = m->H; c->D = m->d / m->H; c->cap = m->max_seq;
+  c->quantized = quantized != 0;
   size_t n = (size_t)c->L * c->H * c->cap * c->D;
-  c->k = (float *)calloc(n, sizeof(float));
-  c->v = (float *)calloc(n, sizeof(float));
+  if (c->quantized) {
+    size_t ns = (size_t)c->L * c->H * c->cap;
+    c->kq = (int8_t *)calloc(n, 1);
+    c->vq = (int8_t *)calloc(n, 1);
+    c->ks = (float *)calloc(ns, sizeof(float));
+    c->vs = (float *)calloc(ns, sizeof(float));
+    c->kraw = (float *)calloc(n, sizeof(float));
+    c->vraw = (float *)calloc(n, sizeof(float));
+  } else {
+    c->k = (float *)calloc(n, sizeof(float));
+    c->v = (float *)calloc(n, sizeof(float));
+  }
   c->len = 0;
   return c;
 }
+or_cache *or_cache_create(const or_model *m) { return or_cache_create_q(m, 0); }
 void or_cache_free(or_cache *c) {
   if (!c) return;
-  free(c->k); free(c->v); free(c);
+  free(c->k); free(c->v); free(c->kq); free(c->vq); free(c->ks); free(c->vs);
+  free(c->kraw); free(c->vraw);
+  free(c);
+}
+int or_cache_read_raw(const or_cache *c, int layer, float *kraw, float *vraw) {
+  if (!c->quantized || layer < 0 || layer >= c->L) return -1;
+  for (int h = 0; h < c->H; ++h) {
+    size_t src = (((size_t)layer * c->H + h) * c->cap) * c->D;
+    size_t dst = (size_t)h * c->len * c->D;
+    memcpy(kraw + dst, c->kraw + src, sizeof(float) * (size_t)c->len * c->D);
+    memcpy(vraw + dst, c->vraw + src, sizeof(float) * (size_t)c->len * c->D);
+  }
+  return 0;
+}
+int or_cache_write_q8(or_cache *c, int layer, int len, const int8_t *kq,
+                      const float *ks, const int8_t *vq, const float *vs) {
+  if (!c->quantized || layer < 0 || layer >= c->L || len < 0 || len > c->cap)
+    return -1;
+  for (int h = 0; h < c->H; ++h) {
+    size_t dst = ((size_t)layer * c->H + h) * c->cap;
+    size_t src = (size_t)h * len;
+    memcpy(c->kq + dst * c->D, kq + src * c->D, (size_t)len * c->D);
+    memcpy(c->vq + dst * c->D, vq + src * c->D, (size_t)len * c->D);
+    memcpy(c->ks + dst, ks + src, sizeof(float) * (size_t)len);
+    memcpy(c->vs + dst, vs + src, sizeof(float) * (size_t)len);
+  }
+  return 0;
+}
+void or_cache_set_len(or_cache *c, int len) {
+  if (len >= 0 && len <= c->cap) c->len = len;
+}
+void or_cache_freeze(or_cache *c, int frozen) { c->frozen = frozen != 0; }
+int or_cache_read_q8(const or_cache *c, int layer, int8_t *kq, float *ks,
+                     int8_t *vq, float *vs) {
+  if (!c->quantized || layer < 0 || layer >= c->L) return -1;
+  for (int h = 0; h < c->H; ++h) {
+    size_t src = ((size_t)layer * c->H + h) * c->cap;
+    size_t dst = (size_t)h * c->len;
+    memcpy(kq + dst * c->D, c->kq + src * c->D, (size_t)c->len * c->D);
+    memcpy(vq + dst * c->D, c->vq + src * c->D, (size_t)c->len * c->D);
+    memcpy(ks + dst, c->ks + src, sizeof(float) * (size_t)c->len);
+    memcpy(vs + dst, c->vs + src, sizeof(float) * (size_t)c->len);
+  }
+  return 0;
 }
 int or_cache_len(const or_cache *c) { return c->len; }
 /* KVCache::truncate (layer.cpp:67-149): keep the first len positions. */
@@ -420,7 +560,42 @@ int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
         }
     or_rope(qh, H, S, D, S_past);
     or_rope(kh, H, S, D, S_past);
-    if (cache) {
+    if (cache && cache->quantized) {
+      /* int8 append (layer.cpp:683-757): the new rotated k and v rows are
+       * quantised per (head, position), then attention reads the codes */
+      size_t lay = (size_t)l * H * cache->cap;
+      int8_t *cq = (int8_t *)malloc(sd);
+      float *cs = (float *)malloc(sizeof(float) * (size_t)H * S);
+      for (int pass = 0; pass < 2; ++pass) {
+        const float *src = pass ? vh : kh;
+        or_quantize_kv(src, (int64_t)H * S, D, cq, cs);
+        int8_t *dq = pass ? cache->vq : cache->kq;
+        float *ds = pass ? cache->vs : cache->ks;
+        float *dr = pass ? cache->vraw : cache->kraw;
+        for (int h = 0; h < H; ++h)
+          for (int s = 0; s < S; ++s) {
+            size_t dst = lay + (size_t)h * cache->cap + S_past + s;
+            memcpy(dr + dst * D, src + ((size_t)h * S + s) * D, sizeof(float) * D);
+            if (cache->frozen) continue;
+            memcpy(dq + dst * D, cq + ((size_t)h * S + s) * D, (size_t)D);
+            ds[dst] = cs[(size_t)h * S + s];
+          }
+      }
+      free(cq); free(cs);
+      int8_t *Kq = (int8_t *)malloc((size_t)H * S_total * D);
+      int8_t *Vq = (int8_t *)malloc((size_t)H * S_total * D);
+      float *Ks = (float *)malloc(sizeof(float) * (size_t)H * S_total);
+      float *Vs = (float *)malloc(sizeof(float) * (size_t)H * S_total);
+      for (int h = 0; h < H; ++h) {
+        size_t src = lay + (size_t)h * cache->cap;
+        memcpy(Kq + (size_t)h * S_total * D, cache->kq + src * D, (size_t)S_total * D);
+        memcpy(Vq + (size_t)h * S_total * D, cache->vq + src * D, (size_t)S_total * D);
+        memcpy(Ks + (size_t)h * S_total, cache->ks + src, sizeof(float) * (size_t)S_total);
+        memcpy(Vs + (size_t)h * S_total, cache->vs + src, sizeof(float) * (size_t)S_total);
+      }
+      or_attention_q8(qh, Kq, Ks, Vq, Vs, H, H, S, S_total, D, 1, ctx);
+      free(Kq); free(Vq); free(Ks); free(Vs); free(kh); free(vh);
+    } else if (cache) {
       /* KV append (layer.cpp:758-807) */
       size_t lay = (size_t)l * H * cache->cap * D;
       for (int h = 0; h < H; ++h)
@@ -616,13 +791,16 @@ static double now_ms(void) {
 int or_generate_speculative(const or_model *t, const or_model *dm,
                             const int32_t *prompt, int P, int max_new, int k,
                             float T, int top_k, float top_p, uint64_t seed,
-                            uint32_t seq, int32_t *out, or_spec_stats *st) {
+                            int quantized_cache, uint32_t seq, int32_t *out,
+                            or_spec_stats *st) {
   int V = t->vocab;
   int greedy = T <= 0.0f;
   if (dm->vocab != V || P <= 0 || k <= 0 || k > 63) return -2;
   or_spec_stats local;
   memset(&local, 0, sizeof(local));
-  or_cache *tc = or_cache_create(t), *dc = or_cache_create(dm);
+  /* KVCache(quantized_cache) for both models (layer.cpp:1396-1398) */
+  or_cache *tc = or_cache_create_q(t, quantized_cache);
+  or_cache *dc = or_cache_create_q(dm, quantized_cache);
   float *tl = (float *)malloc(sizeof(float) * (size_t)(P > k + 1 ? P : k + 1) * V);
   float *dl = (float *)malloc(sizeof(float) * (size_t)P * V);
   float *q = (float *)malloc(sizeof(float) * (size_t)k * V);

@@ -68,7 +68,24 @@ int or_model_get_quantized(const or_model *m, int layer, int which,
                            int8_t *codes, float *scales);
 
 or_cache *or_cache_create(const or_model *m);
+/* KVCache(quantized): quantized != 0 keeps int8 codes and per-(head,
+ * position) scales instead of fp32 rows. */
+or_cache *or_cache_create_q(const or_model *m, int quantized);
 void or_cache_free(or_cache *c);
+/* Codes [H][len][D] and scales [H][len] of one layer of an int8 cache. */
+int or_cache_read_q8(const or_cache *c, int layer, int8_t *kq, float *ks,
+                     int8_t *vq, float *vs);
+/* Checker hooks of an int8 cache (no counterpart in the reference):
+ * the fp32 rows [H][len][D] that were quantised; codes / scales written
+ * into positions [0, len) of one layer; the length set directly; and
+ * freeze: while set, a forward leaves the codes already stored at its new
+ * positions in place (so that a forward can be recomputed on codes taken
+ * from elsewhere). */
+int or_cache_read_raw(const or_cache *c, int layer, float *kraw, float *vraw);
+int or_cache_write_q8(or_cache *c, int layer, int len, const int8_t *kq,
+                      const float *ks, const int8_t *vq, const float *vs);
+void or_cache_set_len(or_cache *c, int len);
+void or_cache_freeze(or_cache *c, int frozen);
 int or_cache_len(const or_cache *c);
 void or_cache_truncate(or_cache *c, int len);
 
@@ -91,6 +108,15 @@ void or_layernorm(const float *x, int64_t rows, int64_t n, const float *gamma,
 void or_attention(const float *q, const float *k, const float *v, int64_t H,
                   int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
                   int causal, float *out);
+/* quantize_kv (layer.cpp:635-657): codes [rows][D], scales [rows]. */
+void or_quantize_kv(const float *src, int64_t rows, int64_t D, int8_t *codes,
+                    float *scales);
+/* or_attention over an int8 cache: kq / vq [H_kv][S_total][D] codes,
+ * ks / vs [H_kv][S_total] scales. */
+void or_attention_q8(const float *q, const int8_t *kq, const float *ks,
+                     const int8_t *vq, const float *vs, int64_t H,
+                     int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
+                     int causal, float *out);
 
 /* get_probs and sample_token of generate_speculative. */
 void or_get_probs(const float *logits, int V, float temperature, int top_k,
@@ -106,8 +132,9 @@ int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
 int or_generate_speculative(const or_model *target, const or_model *draft,
                             const int32_t *prompt, int P, int max_new,
                             int lookahead, float temperature, int top_k,
-                            float top_p, uint64_t seed, uint32_t seq_index,
-                            int32_t *out, or_spec_stats *stats);
+                            float top_p, uint64_t seed, int quantized_cache,
+                            uint32_t seq_index, int32_t *out,
+                            or_spec_stats *stats);
 /* generate_advanced for one sequence; out receives P + max_new ids. */
 int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
                          int max_new, float temperature, int top_k,

@@ -50,6 +50,19 @@ def lib():
                                              C.POINTER(C.c_int8), fp]
         L.or_cache_create.argtypes = [vp]
         L.or_cache_create.restype = vp
+        L.or_cache_create_q.argtypes = [vp, i32]
+        L.or_cache_create_q.restype = vp
+        L.or_cache_read_q8.argtypes = [vp, i32, C.POINTER(C.c_int8), fp,
+                                       C.POINTER(C.c_int8), fp]
+        L.or_cache_read_raw.argtypes = [vp, i32, fp, fp]
+        L.or_cache_write_q8.argtypes = [vp, i32, i32, C.POINTER(C.c_int8), fp,
+                                        C.POINTER(C.c_int8), fp]
+        L.or_cache_set_len.argtypes = [vp, i32]
+        L.or_cache_freeze.argtypes = [vp, i32]
+        L.or_quantize_kv.argtypes = [fp, i64, i64, C.POINTER(C.c_int8), fp]
+        L.or_attention_q8.argtypes = [fp, C.POINTER(C.c_int8), fp,
+                                      C.POINTER(C.c_int8), fp, i64, i64, i64,
+                                      i64, i64, i32, fp]
         L.or_cache_free.argtypes = [vp]
         L.or_cache_len.argtypes = [vp]
         L.or_cache_truncate.argtypes = [vp, i32]
@@ -68,7 +81,7 @@ def lib():
                                      C.POINTER(C.c_int),
                                      C.POINTER(C.c_int64)]
         L.or_generate_speculative.argtypes = [vp, vp, ip, i32, i32, i32, f32,
-                                              i32, f32, u64, u32, ip,
+                                              i32, f32, u64, i32, u32, ip,
                                               C.POINTER(SpecStats)]
         L.or_generate_advanced.argtypes = [vp, ip, i32, i32, f32, i32, f32,
                                            u64, u32, i32, ip]
@@ -179,8 +192,47 @@ class Model:
 
 
 class Cache:
-    def __init__(self, model):
-        self.h = lib().or_cache_create(model.h)
+    def __init__(self, model, quantized=False):
+        self.h = lib().or_cache_create_q(model.h, 1 if quantized else 0)
+        self.H = model.H
+        self.D = model.d // model.H
+
+    def read_q8(self, layer):
+        """Codes and scales of one layer of an int8 cache:
+        (kq [H][len][D], ks [H][len], vq, vs)."""
+        n = len(self)
+        kq = np.zeros((self.H, n, self.D), np.int8)
+        vq = np.zeros_like(kq)
+        ks = np.zeros((self.H, n), np.float32)
+        vs = np.zeros_like(ks)
+        rc = lib().or_cache_read_q8(self.h, layer, i8ptr(kq), fptr(ks),
+                                    i8ptr(vq), fptr(vs))
+        if rc != 0:
+            raise RuntimeError("or_cache_read_q8 failed")
+        return kq, ks, vq, vs
+
+    def read_raw(self, layer):
+        """The fp32 k / v rows [H][len][D] an int8 cache quantised."""
+        n = len(self)
+        kr = np.zeros((self.H, n, self.D), np.float32)
+        vr = np.zeros_like(kr)
+        if lib().or_cache_read_raw(self.h, layer, fptr(kr), fptr(vr)) != 0:
+            raise RuntimeError("or_cache_read_raw failed")
+        return kr, vr
+
+    def write_q8(self, layer, kq, ks, vq, vs):
+        """Codes [H][n][D] / scales [H][n] into positions [0, n)."""
+        kq, vq = (np.ascontiguousarray(a, np.int8) for a in (kq, vq))
+        ks, vs = (np.ascontiguousarray(a, np.float32) for a in (ks, vs))
+        if lib().or_cache_write_q8(self.h, layer, kq.shape[1], i8ptr(kq),
+                                   fptr(ks), i8ptr(vq), fptr(vs)) != 0:
+            raise RuntimeError("or_cache_write_q8 failed")
+
+    def set_len(self, n):
+        lib().or_cache_set_len(self.h, n)
+
+    def freeze(self, frozen=True):
+        lib().or_cache_freeze(self.h, 1 if frozen else 0)
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -221,14 +273,15 @@ def accept_step(p, q, cand, greedy, has_bonus, u_accept, u_final):
 
 
 def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,
-                         top_k=0, top_p=1.0):
+                         top_k=0, top_p=1.0, quantized_cache=False):
     prompt = np.ascontiguousarray(prompt, np.int32)
     out = np.zeros(len(prompt) + max_new, np.int32)
     st = SpecStats()
     rc = lib().or_generate_speculative(target.h, draft.h, iptr(prompt),
                                        len(prompt), max_new, k, T, top_k,
-                                       top_p, seed, seq, iptr(out),
-                                       C.byref(st))
+                                       top_p, seed,
+                                       1 if quantized_cache else 0, seq,
+                                       iptr(out), C.byref(st))
     if rc != 0:
         raise RuntimeError(f"or_generate_speculative failed: {rc}")
     return out, st
@@ -243,4 +296,32 @@ def generate_advanced(model, prompt, max_new, T, seed, seq=0, use_cache=True,
                                     1 if use_cache else 0, iptr(out))
     if rc != 0:
         raise RuntimeError(f"or_generate_advanced failed: {rc}")
+    return out
+
+
+def quantize_kv(x):
+    """quantize_kv of MultiHeadAttention::forward over the rows of x [..., D]:
+    (codes int8 [..., D], scales fp32 [...])."""
+    x = np.ascontiguousarray(x, np.float32)
+    D = x.shape[-1]
+    rows = x.size // D
+    codes = np.zeros(x.shape, np.int8)
+    scales = np.zeros(x.shape[:-1], np.float32)
+    lib().or_quantize_kv(fptr(x), rows, D, i8ptr(codes), fptr(scales))
+    return codes, scales
+
+
+def attention_q8(q, kq, ks, vq, vs, causal=True):
+    """Fused attention of one sequence over an int8 cache: q [H][S][D],
+    kq / vq [Hkv][St][D], ks / vs [Hkv][St]; returns [S][H][D]."""
+    q = np.ascontiguousarray(q, np.float32)
+    kq = np.ascontiguousarray(kq, np.int8)
+    vq = np.ascontiguousarray(vq, np.int8)
+    ks = np.ascontiguousarray(ks, np.float32)
+    vs = np.ascontiguousarray(vs, np.float32)
+    H, S, D = q.shape
+    Hkv, St = kq.shape[0], kq.shape[1]
+    out = np.zeros((S, H, D), np.float32)
+    lib().or_attention_q8(fptr(q), i8ptr(kq), fptr(ks), i8ptr(vq), fptr(vs),
+                          H, Hkv, S, St, D, 1 if causal else 0, fptr(out))
     return out

@@ -142,8 +142,133 @@ def test_capacity_and_unsupported_errors(ctx):
         gt.generate_speculative(gd, np.arange(3), 4, 2, 1.0, top_k=5)
     assert e.value.code == nnhip.EUNSUPPORTED
     with pytest.raises(nnhip.NNHipError) as e:
-        nnhip.KVCache(gt, 1, quantized=True)
-    assert e.value.code == nnhip.EUNSUPPORTED
+        gt.generate_speculative(gd, np.arange(30), 20, 4, 0.0,
+                                quantized_cache=True)
+    assert e.value.code == nnhip.ECAPACITY
+    gt.free(); gd.free()
+
+
+def check_on_device_codes(om, gc, cfg, b, n_before, ids, got, what):
+    """One forward of `ids` (sequence b, positions n_before..) over an int8
+    cache, checked against the oracle given the same cache:
+    (a) the oracle's forward over a cache holding the device's codes and
+        scales for every position (the new ones included) gives the device's
+        logits within 1e-4 (row-relative);
+    (b) the device's codes at the new positions are the oracle's quantize_kv
+        of the fp32 k / v rows that forward computed, except by one where the
+        oracle's x * (1 / scale) lies within 2e-3 of a rounding boundary (the
+        rows differ from the device's in their last bits, and the quantiser is
+        exact on either side: see test_rope_kv_append_q8); scales within
+        1e-5.
+    Chained over forwards, (a) and (b) pin the whole int8-cache path; the
+    oracle's own int8 run is not compared code by code, because one code
+    rounded the other way at a boundary moves every later row of the
+    layers above it."""
+    H, D, L = cfg["H"], cfg["d"] // cfg["H"], cfg["L"]
+    dev = [gc.read_q8(layer, b, H, D) for layer in range(L)]
+    oc = O.Cache(om, quantized=True)
+    for layer in range(L):
+        oc.write_q8(layer, *dev[layer])
+    oc.set_len(n_before)
+    oc.freeze()
+    want = om.forward(ids, oc)
+    assert_rows_close(got, want, 1e-4, what)
+    new = slice(n_before, n_before + len(ids))
+    for layer in range(L):
+        kr, vr = oc.read_raw(layer)
+        dk, dks, dv, dvs = dev[layer]
+        for raw, dq, ds in ((kr, dk, dks), (vr, dv, dvs)):
+            oq, os_ = O.quantize_kv(raw[:, new])
+            np.testing.assert_allclose(ds[:, new], os_, rtol=1e-5)
+            d = dq[:, new].astype(np.int32) - oq.astype(np.int32)
+            assert np.abs(d).max() <= 1, (what, layer)
+            off = d != 0
+            if off.any():
+                t = np.abs(raw[:, new] * (np.float32(1.0) / os_)[..., None])
+                frac = t - np.floor(t)
+                assert (np.abs(frac[off] - 0.5) < 2e-3).all(), (what, layer)
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_forward_int8_cache_vs_oracle(ctx, quant):
+    """KVCache(quantized=true) through prefill, single steps, a multi-token
+    step and a truncation, each forward checked by check_on_device_codes."""
+    om, gm, _ = build(ctx, TOY_T, 14, quant, std=0.05)
+    rng = np.random.default_rng(15)
+    seq = rng.integers(0, 256, 40).astype(np.int32)
+    gc = nnhip.KVCache(gm, 1, quantized=True)
+    n = 0
+    for lo, hi in [(0, 20), (20, 21), (21, 27), ("truncate", 23), (27, 35)]:
+        if lo == "truncate":
+            gc.truncate(hi)
+            n = hi
+            continue
+        g = gm.forward(seq[None, lo:hi], gc)[0]
+        check_on_device_codes(om, gc, TOY_T, 0, n, seq[lo:hi], g,
+                              f"int8 cache [{lo},{hi})")
+        n += hi - lo
+    assert gc.length() == 31
+    gc.free()
+    gm.free()
+
+
+@pytest.mark.parametrize("S", [1, 2, 4, 6])
+def test_forward_int8_cache_ragged_batch(ctx, S):
+    """The verify / draft shapes on an int8 cache: 5 sequences at different
+    lengths (prefill, then per-sequence truncation) take S rows each; each
+    sequence's forwards checked by check_on_device_codes."""
+    om, gm, _ = build(ctx, TOY_T, 18, True, std=0.2)
+    B = 5
+    rng = np.random.default_rng(19 + S)
+    seqs = rng.integers(0, 256, (B, 40)).astype(np.int32)
+    gc = nnhip.KVCache(gm, B, quantized=True)
+    pre = gm.forward(seqs[:, :24], gc)
+    for b in range(B):
+        check_on_device_codes(om, gc, TOY_T, b, 0, seqs[b, :24], pre[b],
+                              f"prefill seq {b}")
+    keeps = [24 - 3 * b for b in range(B)]
+    for b in range(B):
+        gc.truncate(keeps[b], b)
+    ids = np.stack([seqs[b, keeps[b]:keeps[b] + S] for b in range(B)])
+    got = gm.forward(ids, gc)
+    for b in range(B):
+        check_on_device_codes(om, gc, TOY_T, b, keeps[b], ids[b], got[b],
+                              f"ragged int8 seq {b}")
+    gc.free()
+    gm.free()
+
+
+@pytest.mark.parametrize("T", [0.0, 1.0])
+def test_int8_cache_spec_matches_oracle(ctx, T):
+    """generate_speculative(..., quantized_cache=true): batch-1 and a batch
+    of 5 in lockstep against the oracle with int8 caches; greedy streams
+    exact, sampled ones up to a recorded tie.  Weights N(0, 0.05): a code
+    that rounds the other way at a boundary (see assert_q8_cache_matches)
+    moves the logits by ~1e-6 here, far below the streams' argmax margins,
+    whereas with large weights (N(0, 0.3)) one such code can move a logit by
+    1e-2 and legitimately change a greedy stream."""
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 16, True, std=0.05)
+    rng = np.random.default_rng(17)
+    prompt = rng.integers(0, 256, 32).astype(np.int32)
+    got, st = gt.generate_speculative(gd, prompt, 48, 4, T, seed=3,
+                                      quantized_cache=True)
+    want, ost = O.generate_speculative(ot, od, prompt, 48, 4, T, 3,
+                                       quantized_cache=True)
+    if not np.array_equal(got, want):
+        assert T > 0 and (ost.ties > 0 or st.ties > 0)
+    else:
+        assert (st.cycles, st.accepted) == (ost.cycles, ost.accepted)
+    B = 5
+    prompts = rng.integers(0, 256, (B, 20)).astype(np.int32)
+    gotb, stats, _ = gt.generate_speculative_batch(gd, prompts, 30, 3, T, 8,
+                                                   quantized_cache=True)
+    for b in range(B):
+        want, ost = O.generate_speculative(ot, od, prompts[b], 30, 3, T, 8,
+                                           seq=b, quantized_cache=True)
+        if not np.array_equal(gotb[b], want):
+            assert T > 0 and (ost.ties > 0 or stats[b].ties > 0), b
+        else:
+            assert stats[b].accepted == ost.accepted
     gt.free(); gd.free()
 
 

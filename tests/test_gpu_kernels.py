@@ -301,7 +301,7 @@ def test_attention_kq(ctx, B, S, H, D, pos0, w4):
         call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
              D, do.p)
     finally:
-        ctx.set_option("attn_w4", 0)
+        ctx.set_option("attn_w4", 1)
     got = do.numpy()
     for b in range(B):
         St = int(pos0[b]) + S
@@ -314,6 +314,86 @@ def test_attention_kq(ctx, B, S, H, D, pos0, w4):
                              D, 1, O.fptr(out))
         assert_rows_close(got[b * S:(b + 1) * S].reshape(S, H * D),
                           out.reshape(S, H * D), 1e-4, f"attention seq {b}")
+
+
+@pytest.mark.parametrize("D", [64, 32, 8])
+def test_rope_kv_append_q8(ctx, D):
+    """RoPE + int8 append: q bit-exact with or_rope, codes and scales
+    bit-exact with or_quantize_kv of the oracle's rotated k and of v."""
+    rng = np.random.default_rng(12 + D)
+    B, S, H, cap = 3, 5, 4, 700
+    pos = np.array([0, 17, 640], np.int32)
+    qkv = rng.standard_normal((B * S, 3 * H * D)).astype(np.float32)
+    qkv[2, H * D:2 * H * D] = 0.0          # an all-zero k row: scale 1
+    qkv[4, 2 * H * D:2 * H * D + D] = 0.5  # exact halves: round away from 0
+    dq, dpos = ctx.array(qkv), ctx.array(pos)
+    qo = ctx.array(shape=(B * S, H * D))
+    kq = ctx.array(np.zeros((B, H, cap, D), np.int8))
+    vq = ctx.array(np.zeros((B, H, cap, D), np.int8))
+    ks = ctx.array(np.zeros((B, H, cap), np.float32))
+    vs = ctx.array(np.zeros((B, H, cap), np.float32))
+    call("nnhip_rope_kv_append_q8", ctx.h, dq.p, B, S, H, D, dpos.p, qo.p,
+         kq.p, ks.p, vq.p, vs.p, cap)
+    qg, kqg, ksg, vqg, vsg = (qo.numpy(), kq.numpy(), ks.numpy(), vq.numpy(),
+                              vs.numpy())
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        sl = slice(int(pos[b]), int(pos[b]) + S)
+        heads = []
+        for part in range(3):
+            x = np.ascontiguousarray(
+                rows[:, part * H * D:(part + 1) * H * D].reshape(S, H, D)
+                .transpose(1, 0, 2))
+            if part < 2:
+                O.lib().or_rope(O.fptr(x), H, S, D, int(pos[b]))
+            heads.append(x)
+        np.testing.assert_array_equal(
+            qg[b * S:(b + 1) * S].reshape(S, H, D).transpose(1, 0, 2), heads[0])
+        kc, ksc = O.quantize_kv(heads[1])
+        vc, vsc = O.quantize_kv(heads[2])
+        np.testing.assert_array_equal(kqg[b, :, sl], kc)
+        np.testing.assert_array_equal(ksg[b, :, sl], ksc)
+        np.testing.assert_array_equal(vqg[b, :, sl], vc)
+        np.testing.assert_array_equal(vsg[b, :, sl], vsc)
+    # positions outside [pos, pos + S) are untouched
+    assert not kqg[0, :, S:].any() and not ksg[1, :, :17].any()
+
+
+ATTN_Q8_CASES = [(3, 1, 4, 64, [0, 37, 300]), (2, 6, 4, 64, [5, 380]),
+                 (2, 8, 2, 32, [0, 900]), (2, 13, 2, 64, [0, 20]),
+                 (2, 3, 2, 16, [7, 1200]), (16, 8, 8, 64, [2048] * 16)]
+
+
+@pytest.mark.parametrize("w4", [0, 1])
+@pytest.mark.parametrize("B,S,H,D,pos0", ATTN_Q8_CASES)
+def test_attention_kq_q8(ctx, B, S, H, D, pos0, w4):
+    """Attention over an int8 cache against or_attention_q8 (merged
+    workgroups, 4-wave merged workgroups and the split + combine path)."""
+    rng = np.random.default_rng(B * 100 + S + D + 7)
+    pos0 = np.array(pos0, np.int32)
+    cap = int(pos0.max()) + S
+    q = rng.standard_normal((B * S, H * D)).astype(np.float32)
+    kq = rng.integers(-127, 128, (B, H, cap, D)).astype(np.int8)
+    vq = rng.integers(-127, 128, (B, H, cap, D)).astype(np.int8)
+    ks = (rng.random((B, H, cap)) * 0.03 + 0.001).astype(np.float32)
+    vs = (rng.random((B, H, cap)) * 0.03 + 0.001).astype(np.float32)
+    dq, dkq, dvq = ctx.array(q), ctx.array(kq), ctx.array(vq)
+    dks, dvs = ctx.array(ks), ctx.array(vs)
+    dp, do = ctx.array(pos0), ctx.array(shape=(B * S, H * D))
+    try:
+        ctx.set_option("attn_w4", w4)
+        call("nnhip_attention_kq_q8", ctx.h, dq.p, dkq.p, dks.p, dvq.p, dvs.p,
+             cap, dp.p, B, S, H, H, D, do.p)
+    finally:
+        ctx.set_option("attn_w4", 1)
+    got = do.numpy()
+    for b in range(B):
+        St = int(pos0[b]) + S
+        qb = q[b * S:(b + 1) * S].reshape(S, H, D).transpose(1, 0, 2)
+        out = O.attention_q8(qb, kq[b, :, :St], ks[b, :, :St], vq[b, :, :St],
+                             vs[b, :, :St])
+        assert_rows_close(got[b * S:(b + 1) * S].reshape(S, H * D),
+                          out.reshape(S, H * D), 1e-4, f"int8 attention seq {b}")
 
 
 @pytest.mark.parametrize("rows,d", [(7, 64), (5, 1024), (3, 4096), (2, 100)])

@@ -360,3 +360,141 @@ def test_speculative_sampling_preserves_target_distribution():
     q = O.get_probs(d.forward(prompt + [3])[-1], 1.0)
     p = O.get_probs(t.forward(prompt + [3])[-1], 1.0)
     assert np.abs(p - q).sum() > 0.2
+
+
+# --------------------------------------------------------------------------
+# int8 KV cache (KVCache(quantized=true), layer.cpp:635-757, 878-938)
+# --------------------------------------------------------------------------
+def test_quantize_kv_known_answers():
+    """quantize_kv on rows whose answers are fixed by hand: max 127 gives
+    scale 1 exactly, so the codes are round-half-away-from-zero of the
+    values themselves (2.5 -> 3, -2.5 -> -3, 1.5 -> 2, -0.5 -> -1, where
+    round-half-even would give 2, -2, 2, 0); an all-zero row gets scale 1
+    and zero codes; a row led by a negative maximum maps it to -127."""
+    rows = np.array([[127.0, -63.5, 2.5, -2.5, 0.49, 0.0, 1.5, -0.5],
+                     [0.0] * 8,
+                     [-3.0, 1.0, 0.0, 0.0, 0.0, 0.0, 0.0, 1.5]], np.float32)
+    codes, scales = O.quantize_kv(rows)
+    np.testing.assert_array_equal(codes[0], [127, -64, 3, -3, 0, 0, 2, -1])
+    np.testing.assert_array_equal(codes[1], np.zeros(8))
+    s = np.float32(3.0) / np.float32(127.0)
+    inv = np.float32(1.0) / s
+    assert scales[0] == 1.0 and scales[1] == 1.0 and scales[2] == s
+    assert codes[2, 0] == -127
+    assert codes[2, 1] == int(np.round(np.float32(1.0) * inv))     # 42
+    assert codes[2, 7] == 64                                        # 63.5 -> 64
+
+
+def test_quantize_kv_error_bound():
+    """|code * scale - x| <= scale / 2 (plus one rounding of x / scale) for
+    every element; the largest |x| of a row maps to +-127."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((300, 64)) * rng.random((300, 1)) * 5).astype(np.float32)
+    codes, scales = O.quantize_kv(x)
+    deq = codes.astype(np.float64) * scales[:, None]
+    err = np.abs(deq - x.astype(np.float64))
+    assert (err <= scales[:, None] * (0.5 + 1e-5)).all()
+    top = np.abs(x).argmax(1)
+    np.testing.assert_array_equal(np.abs(codes[np.arange(300), top]), 127)
+    assert np.abs(codes).max() <= 127
+
+
+def test_attention_q8_equals_dequantised_fp32_path():
+    """The quantized fused path equals the fp32 fused path run on the
+    dequantised cache (layer.cpp:826-831 dequantize_k / _v then the same
+    per-element products): bit-exact, since both form (float)code * scale
+    and then the same fp32 operations in the same order."""
+    rng = np.random.default_rng(4)
+    H, Hkv, S, St, D = 4, 2, 3, 21, 16
+    q = rng.standard_normal((H, S, D)).astype(np.float32)
+    kq = rng.integers(-127, 128, (Hkv, St, D)).astype(np.int8)
+    vq = rng.integers(-127, 128, (Hkv, St, D)).astype(np.int8)
+    ks = (rng.random((Hkv, St)) * 0.05 + 1e-3).astype(np.float32)
+    vs = (rng.random((Hkv, St)) * 0.05 + 1e-3).astype(np.float32)
+    got = O.attention_q8(q, kq, ks, vq, vs)
+    k = (kq.astype(np.float32) * ks[:, :, None]).astype(np.float32)
+    v = (vq.astype(np.float32) * vs[:, :, None]).astype(np.float32)
+    want = np.zeros((S, H, D), np.float32)
+    O.lib().or_attention(O.fptr(q), O.fptr(np.ascontiguousarray(k)),
+                         O.fptr(np.ascontiguousarray(v)), H, Hkv, S, St, D, 1,
+                         O.fptr(want))
+    np.testing.assert_array_equal(got, want)
+    # and both agree with the float64 softmax attention over the same rows
+    kk = np.repeat(k, H // Hkv, 0)
+    vv = np.repeat(v, H // Hkv, 0)
+    np.testing.assert_allclose(got, attn_f64(q, kk, vv, True), rtol=1e-5,
+                               atol=1e-5)
+
+
+def test_int8_cache_close_to_fp32_cache():
+    """gqa_test.cpp:213-265 (KVQuantizationVerification): the int8-cache
+    outputs stay within 0.08 of the fp32-cache ones, step by step; here on
+    whole-model logits with the cache's codes checked against a fresh
+    quantisation of the fp32 cache's rows."""
+    t, _ = tiny_models(quantize=True)
+    cf, cq = O.Cache(t), O.Cache(t, quantized=True)
+    for ids in ([5, 1, 2], [7], [3, 0]):
+        a = t.forward(ids, cf)
+        b = t.forward(ids, cq)
+        assert np.abs(a - b).max() <= 0.08
+        assert not np.array_equal(a, b) or len(ids) == 0
+    kq, ks, vq, vs = cq.read_q8(1)
+    assert kq.shape == (2, 6, 8) and ks.shape == (2, 6)
+    assert (np.abs(kq).max(2) == 127).all() and (np.abs(vq).max(2) == 127).all()
+
+
+def test_spec_quantized_reference_case():
+    """transformer_test.cpp:348-371 (SpeculativeDecodingQuantized): vocab 6,
+    embed 8, 2 heads, MLP 16, target 2 layers, draft 1, max_seq 32, prompt
+    {2, 4, 1}, 5 new, k = 2, greedy, quantized cache: 8 ids, all < 6."""
+    tp = O.make_params(6, 8, 2, 16, 2, 5, std=0.3)
+    dp = O.make_params(6, 8, 2, 16, 1, 6, std=0.3)
+    t = O.Model(6, 8, 2, 16, 2, 32, tp)
+    d = O.Model(6, 8, 2, 16, 1, 32, dp)
+    out, st = O.generate_speculative(t, d, [2, 4, 1], 5, 2, 0.0, 42,
+                                     quantized_cache=True)
+    assert len(out) == 8 and ((out >= 0) & (out < 6)).all()
+    assert list(out[:3]) == [2, 4, 1]
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_greedy_spec_int8_cache_equals_ar_int8_cache(k):
+    """Greedy speculative decoding with int8 caches equals greedy
+    autoregressive decoding through an int8 cache: every cached row is
+    quantised from the same token prefix however the cycles batch and
+    roll back the positions (transformer_test.cpp:307-346 with
+    KVCache(true))."""
+    t, d = tiny_models(quantize=True)
+    for prompt in ([1, 2, 3], [7, 0, 5, 5, 2]):
+        c = O.Cache(t, quantized=True)
+        seq = list(prompt)
+        lg = t.forward(np.array(seq, np.int32), c)
+        for _ in range(12):
+            seq.append(int(np.argmax(lg[-1])))
+            lg = t.forward(np.array(seq[-1:], np.int32), c)
+        sp, st = O.generate_speculative(t, d, prompt, 12, k, 0.0, 42,
+                                        quantized_cache=True)
+        np.testing.assert_array_equal(sp, seq)
+        assert st.accepted + st.resampled + st.bonus + 1 == 12
+
+
+def test_frozen_cache_recomputes_forward():
+    """The checker hook: a forward over a cache that was given another
+    cache's codes (new positions included) and frozen reproduces that
+    cache's own forward bit for bit."""
+    t, _ = tiny_models(quantize=True)
+    a = O.Cache(t, quantized=True)
+    t.forward([5, 1, 2, 6], a)
+    want = t.forward([7, 3], a)
+    b = O.Cache(t, quantized=True)
+    for layer in range(2):
+        b.write_q8(layer, *a.read_q8(layer))
+    b.set_len(4)
+    b.freeze()
+    np.testing.assert_array_equal(t.forward([7, 3], b), want)
+    kr, vr = a.read_raw(0)
+    kq, ks, vq, vs = a.read_q8(0)
+    for raw, codes, scales in ((kr, kq, ks), (vr, vq, vs)):
+        c, sc = O.quantize_kv(raw)
+        np.testing.assert_array_equal(c, codes)
+        np.testing.assert_array_equal(sc, scales)
