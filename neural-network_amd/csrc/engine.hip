@@ -419,7 +419,14 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   for (int l = 0; l < L; ++l) {
     LayerW &ly = layers[l];
     const KvSrc kvs = kv->src(l, b_off);
-    if (kv->q8) {
+    // the int8 append runs in the LDS GEMM's epilogue (each head's pairs on
+    // one group of lanes), or the digit-plane GEMM's for heads of <= 32;
+    // otherwise (GEMV rows, 64-wide heads on 32-column tiles) it is a
+    // kernel of its own
+    const bool q8_epi = kv->q8 && rope_q8_head_dim_ok(D) &&
+                        (use_lds(ly.qkv, R) ||
+                         (use_limbs(ly.qkv, R) && gemm_limb_q8_ok(D)));
+    if (kv->q8 && !q8_epi) {
       // q, k, v rows, then RoPE and the quantised append
       linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
                 l == 0 && emb_digits, nullptr, 0, ws.qkv.p, 3 * d, kEpiBias);
@@ -432,8 +439,15 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       RopeArgs ra;
       ra.S = S; ra.H = H; ra.D = D; ra.off = off; ra.cap = kv->cap;
       ra.base = bp; ra.active = active; ra.cosb = cosb.p; ra.sinb = sinb.p;
-      ra.qrot = ws.qrot.p; ra.kc = (float *)kvs.k; ra.vc = (float *)kvs.v;
+      ra.qrot = ws.qrot.p;
       ra.seq_stride = kvs.seq_stride;
+      if (kv->q8) {
+        ra.kq = (int8_t *)kvs.k; ra.vq = (int8_t *)kvs.v;
+        ra.ks = (float *)kvs.ks; ra.vs = (float *)kvs.vs;
+        ra.sc_stride = kvs.sc_stride;
+      } else {
+        ra.kc = (float *)kvs.k; ra.vc = (float *)kvs.v;
+      }
       linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
                 l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
     }

@@ -346,7 +346,8 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     if (epi == kEpiSwiGLU) {
       y[(int64_t)m * ldy + n / 2] = silu_mul(v[0], v[1]);
     } else if (epi == kEpiRope) {
-      rope_store_pair(ra, m, n, v[0], v[1]);
+      if (ra.kq) rope_store_pair_q8(ra, m, n, v[0], v[1]);
+      else rope_store_pair(ra, m, n, v[0], v[1]);
     } else {
       if (epi == kEpiResid) { v[0] = e_rs[it][0] + v[0]; v[1] = e_rs[it][1] + v[1]; }
       y[(int64_t)m * ldy + n] = v[0];
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLdsThreads = 1024;
 
-template <int MODE, int KPT>
+template <int MODE, int KPT, bool Q8KV = false>
 __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
     const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
     const float *__restrict__ x, int64_t ldx, const float *__restrict__ lng,
@@ -655,7 +656,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
       if (epi == kEpiSwiGLU) {
         y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
       } else if (epi == kEpiRope) {
-        rope_store_pair(ra, m, n, v0, v1);
+        if constexpr (Q8KV) rope_store_pair_q8(ra, m, n, v0, v1);
+        else rope_store_pair(ra, m, n, v0, v1);
       } else {
         if (epi == kEpiResid) { v0 = e_rs[it][0] + v0; v1 = e_rs[it][1] + v1; }
         y[(int64_t)m * ldy + n] = v0;
@@ -1151,6 +1153,8 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
   NNHIP_REQUIRE(K % 4 == 0 && K <= 4096, kErrArg, "gemv: K must be a multiple of 4 and <= 4096");
   NNHIP_REQUIRE(epi != kEpiSwiGLU || N % 2 == 0, kErrArg, "gemv: SwiGLU needs even N");
   NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg, "gemv: RoPE epilogue needs its arguments");
+  NNHIP_REQUIRE(!(ra && ra->kq), kErrArg,
+                "gemv: no int8 KV append in this epilogue (use rope_kv_q8)");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
   for (int r0 = 0; r0 < rows; r0 += 4) {
     int rr = rows - r0 < 4 ? rows - r0 : 4;
@@ -1187,6 +1191,10 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   NNHIP_CHECK(hipGetLastError());
 }
 
+// The int8 KV append in gemm_limb_kernel's epilogue needs each head's pairs
+// within one tile row's 16 (32x32 tiles) column pairs.
+bool gemm_limb_q8_ok(int D) { return rope_q8_head_dim_ok(D) && D <= 32; }
+
 void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
@@ -1198,6 +1206,9 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                 "gemm_limb: RoPE epilogue needs its arguments");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
   NNHIP_REQUIRE(mpad % 64 == 0 && rows <= mpad, kErrArg, "gemm_limb: bad mpad");
+  const bool q8 = epi == kEpiRope && rz.kq;
+  NNHIP_REQUIRE(!q8 || gemm_limb_q8_ok(rz.D), kErrArg,
+                "gemm_limb: int8 KV append needs a power-of-two head dim <= 32");
   // 32x64 tiles when they alone give enough workgroups to fill the chip,
   // otherwise 32x32 tiles (twice the workgroups, two resident per CU)
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
@@ -1281,11 +1292,16 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
     NNHIP_REQUIRE(lng && lnb && (!ln_out || (ldo >= K && ldo % 4 == 0)),
                   kErrArg, "gemm_lds: LayerNorm parameters missing");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
+  const bool q8 = epi == kEpiRope && rz.kq;
+  NNHIP_REQUIRE(!q8 || rope_q8_head_dim_ok(rz.D), kErrArg,
+                "gemm_lds: int8 KV append needs a power-of-two head dim <= 64");
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
   NNHIP_REQUIRE(!ts || !ts->out || (gemm_lds_tile_width(K) > 0 && epi == kEpiBias),
                 kErrArg, "gemm_lds: tile statistics need K of 512 or 1024 and a bias epilogue");
   const TileStatsArgs tz = ts ? *ts : TileStatsArgs{};
-  if (g_gemm_fk && !tz.out && !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
+  // (the full-K-wave GEMM's epilogue holds 32 columns a wave: no int8 append)
+  if (g_gemm_fk && !tz.out && !q8 &&
+      !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
     launch_gemm_fk(st, mode, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,
                    rows, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, rz, ntm);
     return;
@@ -1300,16 +1316,22 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
   const int per = ((ntm + rpt - 1) / rpt * ntn + 7) / 8;
   dim3 grid(8 * per);
 #define NNHIP_GL(MD, KP)                                                      \
-  hipLaunchKernelGGL((gemm_lds_kernel<MD, KP>), grid, dim3(kLdsThreads), 0,   \
-                     st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,    \
-                     rows, N, wq, scale, bias, resid, ldr, y, ldy, epi, ntm,  \
-                     ntn, rpt, rz, tz)
+  if (q8)                                                                     \
+    hipLaunchKernelGGL((gemm_lds_kernel<MD, KP, true>), grid,                 \
+                       dim3(kLdsThreads), 0, st, limbs, mpad, rexp, x, ldx,   \
+                       lng, lnb, ln_out, ldo, rows, N, wq, scale, bias, resid, \
+                       ldr, y, ldy, epi, ntm, ntn, rpt, rz, tz);              \
+  else                                                                        \
+    hipLaunchKernelGGL((gemm_lds_kernel<MD, KP, false>), grid,                \
+                       dim3(kLdsThreads), 0, st, limbs, mpad, rexp, x, ldx,   \
+                       lng, lnb, ln_out, ldo, rows, N, wq, scale, bias, resid, \
+                       ldr, y, ldy, epi, ntm, ntn, rpt, rz, tz)
 #define NNHIP_GL_K(MD)                                                        \
   switch (K) {                                                                \
-    case 128: NNHIP_GL(MD, 4); break;                                         \
-    case 256: NNHIP_GL(MD, 8); break;                                         \
-    case 512: NNHIP_GL(MD, 16); break;                                        \
-    default: NNHIP_GL(MD, 32); break;                                         \
+    case 128: { NNHIP_GL(MD, 4); } break;                                     \
+    case 256: { NNHIP_GL(MD, 8); } break;                                     \
+    case 512: { NNHIP_GL(MD, 16); } break;                                    \
+    default: { NNHIP_GL(MD, 32); } break;                                     \
   }
   if (mode == kAFromDigits) { NNHIP_GL_K(kAFromDigits) }
   else if (mode == kAFromRows) { NNHIP_GL_K(kAFromRows) }

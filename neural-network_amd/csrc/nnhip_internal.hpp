@@ -87,12 +87,18 @@ enum Epi : int {
 // base[b] + off + s; columns [0, E) are q (rotated into qrot [rows][E]),
 // [E, 2E) are k (rotated into the cache), [2E, 3E) are v (into the cache),
 // E = H*D; cache rows [b][h][pos][D] with seq_stride floats per sequence.
+// With an int8 cache (KVCache(true)) kq / vq / ks / vs are set instead of
+// kc / vc: codes [b][h][pos][D] (seq_stride per sequence) and one scale per
+// row [b][h][pos] (sc_stride per sequence); see rope_store_pair_q8.
 struct RopeArgs {
   int S = 1, H = 1, D = 2, off = 0, cap = 0;
   const int32_t *base = nullptr, *active = nullptr;
   const float *cosb = nullptr, *sinb = nullptr;
   float *qrot = nullptr, *kc = nullptr, *vc = nullptr;
   int64_t seq_stride = 0;
+  int8_t *kq = nullptr, *vq = nullptr;
+  float *ks = nullptr, *vs = nullptr;
+  int64_t sc_stride = 0;
 };
 
 // Cache position of row m of a RoPE epilogue: base[b] + off + s for row
@@ -156,6 +162,52 @@ __device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
   const bool vpart = n / (ra.H * ra.D) == 2;
   const float2 cs = vpart ? make_float2(0.f, 0.f) : rope_cos_sin(ra, pos, n);
   rope_store_pair_at(ra, m, pos, n, xe, xo, cs.x, cs.y);
+}
+
+// The KV append into an int8 cache from an epilogue whose lanes hold the
+// D/2 pairs of one (row, head) on D/2 consecutive lanes, aligned (D a power
+// of two <= 64); every lane of such a group calls this together.  q pairs
+// are rotated and stored as rope_store_pair does; k pairs (after RoPE) and
+// v pairs are quantised as quantize_kv does (layer.cpp:635-657): scale =
+// max|x| over the row / 127 (1 when 0), code = clamp(round(x * (1 /
+// scale)), +-127), the same operations as rope_kv_q8_kernel.
+__device__ inline void rope_store_pair_q8(const RopeArgs &ra, int64_t m, int n,
+                                          float xe, float xo) {
+  const int pos = rope_row_pos(ra, m);
+  const int E = ra.H * ra.D;
+  const int part = n / E, nn = n % E;
+  const int h = nn / ra.D, j = (nn % ra.D) >> 1;
+  float a = xe, b = xo;
+  if (part != 2) {
+    const float2 cs = pos >= 0 ? rope_cos_sin(ra, pos, n) : make_float2(0.f, 0.f);
+    a = __fsub_rn(__fmul_rn(xe, cs.x), __fmul_rn(xo, cs.y));
+    b = __fadd_rn(__fmul_rn(xe, cs.y), __fmul_rn(xo, cs.x));
+  }
+  if (part == 0) {
+    if (pos >= 0) { float *q = ra.qrot + m * E + nn; q[0] = a; q[1] = b; }
+    return;
+  }
+  float mx = fmaxf(fabsf(a), fabsf(b));
+  for (int o = 1; o < ra.D / 2; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (pos < 0) return;
+  float scale = mx / 127.0f;
+  if (scale == 0.0f) scale = 1.0f;
+  const float inv = 1.0f / scale;
+  const float ca = fmaxf(-127.0f, fminf(127.0f, roundf(__fmul_rn(a, inv))));
+  const float cb = fmaxf(-127.0f, fminf(127.0f, roundf(__fmul_rn(b, inv))));
+  const int bq = (int)(m / ra.S);
+  int8_t *dst = (part == 1 ? ra.kq : ra.vq) + bq * ra.seq_stride +
+                ((int64_t)h * ra.cap + pos) * ra.D + 2 * j;
+  dst[0] = (int8_t)ca;
+  dst[1] = (int8_t)cb;
+  if (j == 0)
+    (part == 1 ? ra.ks : ra.vs)[bq * ra.sc_stride + (int64_t)h * ra.cap + pos] = scale;
+}
+
+// whether an epilogue can append to an int8 cache in place: each head's
+// pairs on an aligned group of D/2 lanes, within a wave
+__host__ __device__ inline bool rope_q8_head_dim_ok(int D) {
+  return D >= 2 && D <= 64 && (D & (D - 1)) == 0;
 }
 
 // Activation limbs for the int8 MFMA GEMM: x[m][k] ~= X[m][k] * 2^-e[m] with
@@ -293,6 +345,7 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int64_t ldy, int epi, const RopeArgs *ra = nullptr);
 void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
                       int K, int8_t *limbs, int mpad, int *rexp);
+bool gemm_limb_q8_ok(int D);
 void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
