@@ -153,10 +153,10 @@ int nnhip_kvcache_truncate(nnhip_kvcache *c, int b, int len);
  * (host) receives the prompt and the generated ids.  Uniforms come from the
  * Philox stream u[seq][cycle][slot] (slot j < k: draft sample j, k + j:
  * accept test j, 2k: resample or bonus; cycle 0 slot 2k: first token)
- * instead of std::mt19937.  temperature <= 0 is greedy.  quantized_cache
+ * instead of std::mt19937.  temperature <= 0 is greedy.  top_k / top_p
+ * filter every get_probs as nnhip_sample_rows describes.  quantized_cache
  * != 0 gives both models int8 KV caches (KVCache(true), layer.cpp:
- * 1396-1398).  top_k in (0, V) or top_p in (0, 1) return
- * NNHIP_EUNSUPPORTED. */
+ * 1396-1398).  A vocabulary above 32768 returns NNHIP_EUNSUPPORTED. */
 int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
                                const int32_t *prompt, int P, int max_new,
                                int lookahead, float temperature, int top_k,
@@ -256,10 +256,14 @@ int nnhip_attention_kq_q8(nnhip_ctx *ctx, const float *q, const int8_t *kcodes,
 int nnhip_layernorm(nnhip_ctx *ctx, const float *x, int rows, int d,
                     const float *gamma, const float *beta, float *y);
 /* get_probs + sample_token (layer.cpp:1410-1498) per row: logits [B][V],
- * u [B]; tok [B]; probs [B][V] or NULL (not written when temperature <= 0). */
+ * u [B]; tok [B]; probs [B][V] or NULL (not written when temperature <= 0).
+ * top_k in (0, V) keeps the top_k largest probabilities, top_p in (0, 1)
+ * the shortest prefix (descending, ties by lower index) whose sum reaches
+ * top_p; both renormalise what is kept (layer.cpp:1447-1489).  Other values
+ * leave the row unfiltered. */
 int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
-                      float temperature, const float *u, int32_t *tok,
-                      float *probs);
+                      float temperature, int top_k, float top_p,
+                      const float *u, int32_t *tok, float *probs);
 /* Accept loop + residual resample of generate_speculative (layer.cpp:
  * 1581-1630) for B sequences of k drafted positions: target and draft
  * logits [B][k][V], draft ids [B][k], accept uniforms [B][k], resample

@@ -612,12 +612,12 @@ int nnhip_layernorm(nnhip_ctx *ctx, const float *x, int rows, int d,
 }
 
 int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
-                      float temperature, const float *u, int32_t *tok,
-                      float *probs) {
+                      float temperature, int top_k, float top_p,
+                      const float *u, int32_t *tok, float *probs) {
   return guard([&] {
     REQ(ctx && logits && u && tok && B > 0 && V > 0, "nnhip_sample_rows: bad argument");
     nnhip::launch_sample_rows(ctx->c.stream, logits, B, V, temperature, u, tok,
-                              probs);
+                              probs, top_k, top_p);
   });
 }
 

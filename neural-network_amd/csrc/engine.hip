@@ -569,10 +569,9 @@ struct SpecBuffers {
 };
 
 void check_sampling_options(int V, int top_k, float top_p) {
-  NNHIP_REQUIRE(top_k <= 0 || top_k >= V, kErrUnsupported,
-                "top_k filtering is not implemented on the device path");
-  NNHIP_REQUIRE(top_p <= 0.0f || top_p >= 1.0f, kErrUnsupported,
-                "top_p filtering is not implemented on the device path");
+  NNHIP_REQUIRE(V > 0 && V <= 32768, kErrUnsupported,
+                "sampling: vocabulary above 32768");
+  (void)top_k; (void)top_p;
 }
 
 }  // namespace
@@ -619,11 +618,12 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   for (int g = 0; g <= G; ++g) gb0[g] = (int)((int64_t)B * g / G);
   const int tw = gemm_lds_tile_width(dm.lm.K);
   const int nt = tw > 0 ? (V + tw - 1) / tw : 0;
-  bool tiles = tw > 0 && nt <= 1024;
+  // (tile statistics carry no top-k / top-p: filtered rows take full passes)
+  bool tiles = tw > 0 && nt <= 1024 && (T <= 0.f || !sampling_filtered(V, top_k, top_p));
   for (int g = 0; g < G && tiles; ++g) tiles = dm.lm_tiles(gb0[g + 1] - gb0[g]);
   if (tiles) bf.dtiles.alloc((size_t)B * k * nt);
   if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
-  bf.tstat.alloc((size_t)B * (k + 1) * 4);
+  bf.tstat.alloc((size_t)B * (k + 1) * kTstat);
   bf.dlog.alloc((size_t)B * V);
   bf.tlog.alloc((size_t)B * (k + 1) * V);
   bf.stats.alloc((size_t)B * 6);
@@ -648,7 +648,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     SpecState &s = gs[g];
     s.cur = bf.cur.p + b0; s.cand = bf.cand.p + (size_t)b0 * k;
     s.qprob = bf.qprob.p ? bf.qprob.p + (size_t)b0 * k * V : nullptr;
-    s.tstat = bf.tstat.p + (size_t)b0 * (k + 1) * 4;
+    s.tstat = bf.tstat.p + (size_t)b0 * (k + 1) * kTstat;
     if (tiles) {
       s.dtiles = bf.dtiles.p + (size_t)b0 * k * nt;
       s.nt = nt; s.tw = tw;
@@ -661,6 +661,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     s.stats = bf.stats.p + (size_t)b0 * 6;
     s.B = Bg; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
     s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0 + b0;
+    s.top_k = top_k; s.top_p = top_p;
     // workspace for every shape the loop uses, before any graph capture
     t.reserve(g, Bg * P, Bg * (k + 1), t_need);
     t.reserve(g, Bg * (k + 1), Bg * (k + 1), t_need);
@@ -843,7 +844,7 @@ void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
   SpecState s{};
   s.cur = cur.p; s.out = dout.p; s.B = B; s.out_stride = total; s.P = P;
   s.max_new = max_new; s.k = 0; s.V = m.V; s.T = T; s.seed = seed;
-  s.seq0 = seq0;
+  s.seq0 = seq0; s.top_k = top_k; s.top_p = top_p;
   std::unique_ptr<KVCache> cache;
   if (use_cache) cache.reset(new KVCache(&m, B, std::max(total, 1)));
   for (int step = 0; step < max_new; ++step) {

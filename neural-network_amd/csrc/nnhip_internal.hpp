@@ -414,11 +414,17 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       int8_t *limbs, int mpad, int *rexp);
 
 // sampling.hip
+// floats per verify row of SpecState::tstat
+constexpr int kTstat = 6;
+// whether get_probs filters with these options (layer.cpp:1452-1472)
+inline bool sampling_filtered(int V, int top_k, float top_p) {
+  return (top_k > 0 && top_k < V) || (top_p > 0.0f && top_p < 1.0f);
+}
 struct SpecState {
   int32_t *cur;        // [B] last committed token (generated.back())
   int32_t *cand;       // [B][k] draft candidates of this cycle
   float *qprob;        // [B][k][V] draft probabilities (sampled mode)
-  float *tstat;        // [B][k+1][4] verify-row statistics (accept step)
+  float *tstat;        // [B][k+1][kTstat] verify-row statistics (accept)
   int32_t *tlen;       // [B] target cache length
   int32_t *dlen;       // [B] draft cache length
   int32_t *gen;        // [B] tokens generated so far
@@ -437,6 +443,8 @@ struct SpecState {
   int nt, tw;            // tiles per row, tile width
   int B, out_stride, P, max_new, k, V;
   float T;
+  int top_k;             // get_probs filters (layer.cpp:1447-1489): top_k in
+  float top_p;           // (0, V) and top_p in (0, 1) are active
   uint64_t seed;
   uint32_t seq0;       // global index of sequence 0 (Philox key part)
 };
@@ -451,7 +459,8 @@ void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
 void launch_ar_sample(hipStream_t st, const SpecState &s, int step,
                       const float *logits, int64_t ldl);
 void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
-                        float T, const float *u, int32_t *tok, float *probs);
+                        float T, const float *u, int32_t *tok, float *probs,
+                        int top_k = 0, float top_p = 1.f);
 void launch_add_scalar(hipStream_t st, int32_t *p, int n, int v);
 void launch_accept_bench(hipStream_t st, const float *tlog, const float *dlog,
                          const int32_t *dtok, const float *u_acc,

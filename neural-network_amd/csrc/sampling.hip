@@ -43,11 +43,26 @@ __device__ __forceinline__ float uniform(uint64_t seed, uint32_t seq,
   return (float)(c0 >> 8) * (1.0f / 16777216.0f);
 }
 
-// Row statistics of get_probs (T > 0), see row_pass
-struct RowStats { float mx, rsum, rfs; };
+// Row statistics of get_probs (T > 0), see row_pass; tau / tix: the top-k /
+// top-p rule (block_filter), which keeps entry v iff bits(p1_v) > tau or
+// (bits(p1_v) == tau and v <= tix) -- everything by default.
+struct RowStats {
+  float mx, rsum, rfs;
+  uint32_t tau;
+  int tix;
+};
+__device__ __forceinline__ RowStats mk_stats(float mx, float rsum, float rfs) {
+  return RowStats{mx, rsum, rfs, 0u, 0x7fffffff};
+}
+
+__device__ __forceinline__ bool kept(float p1, int v, const RowStats &st) {
+  const uint32_t u = __float_as_uint(p1);
+  return u > st.tau || (u == st.tau && v <= st.tix);
+}
 
 // workgroup reduction slots; `rows` holds per-row statistics formed by
 // single waves (accept step, up to one row per wave)
+constexpr int kDigits = 16;   // digit values of one level of block_filter
 struct Shared {
   float f[kWaves];
   double d[kWaves];
@@ -55,6 +70,8 @@ struct Shared {
   RowStats rows[kWaves];
   int argm[kWaves];
   double xd;
+  int hn[kWaves][kDigits];
+  double hs[kWaves][kDigits];
   float prow[kRowWords];
 };
 // the same without the probability row, for kernels that need no full row
@@ -173,16 +190,164 @@ __device__ __forceinline__ float scaled(float l, float T) {
   return T == 1.0f ? l : l / T;
 }
 
+// p at index v of a row with logit l, from the row's statistics
+__device__ __forceinline__ float prob_of(float l, int v, float T,
+                                         const RowStats &st) {
+  const float p1 = expf(scaled(l, T) - st.mx) * st.rsum;
+  return kept(p1, v, st) ? p1 * st.rfs : 0.f;
+}
+
 __device__ __forceinline__ float prob_at(const float *row, int v, float T,
                                          RowStats st) {
-  return (expf(scaled(row[v], T) - st.mx) * st.rsum) * st.rfs;
+  return prob_of(row[v], v, T, st);
+}
+
+// ---------------------------------------------------------------------------
+// top-k / top-p of get_probs (layer.cpp:1447-1489).  The reference sorts p1
+// (the probabilities after the first normalisation) descending, zeroes the
+// ranks from top_k on, then zeroes every rank after the one at which the
+// running sum first reaches top_p, and renormalises by what is left: the
+// kept set is the first R = min(top_k, r + 1) ranks, r the top-p crossing.
+// Ties in the order go to the lower index (std::sort leaves them
+// unspecified; the oracle does the same).  No sort here: a most-significant-
+// digit search over the bit patterns of p1 (non-negative floats order as
+// their bits), 4 bits a level; per level, counts and double sums of the
+// candidates per digit value are reduced over the workgroup and the digit
+// where the running count from the top reaches top_k or the running sum
+// reaches top_p is taken.  After 8 levels the boundary value tau is exact;
+// of the entries equal to tau, those in index order up to what the rule
+// allows are kept (tix: the last kept index; all of them when no cut falls
+// inside the group).  The running sum is double here and a float sum in
+// sorted order in the reference, so the crossing rank can differ where that
+// float sum lies within its rounding error of top_p (a tie).
+// x: p1 of entries v = tid + kThreads i (entries v >= V ignored).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void block_filter(const float (&x)[kPer], int V,
+                                          int top_k, float top_p, Shared &sh,
+                                          RowStats &st) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const bool use_k = top_k > 0 && top_k < V;
+  const bool use_p = top_p > 0.f && top_p < 1.f;
+  const int kcap = use_k ? top_k : V;
+  uint32_t prefix = 0u;
+  int above_n = 0, gcnt = 0;
+  double above_s = 0.0;
+  bool p_cut = false;
+  for (int level = 0; level < 8; ++level) {
+    const int shift = 28 - 4 * level;
+    // a thread's counts and (float) sums per digit, eight digits at a time,
+    // then summed over the wave (double) into the wave's LDS slots
+    __syncthreads();
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      int cnt[kDigits / 2];
+      float smf[kDigits / 2];
+#pragma unroll
+      for (int d = 0; d < kDigits / 2; ++d) { cnt[d] = 0; smf[d] = 0.f; }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int v = tid + i * kThreads;
+        const uint32_t u = __float_as_uint(x[i]);
+        const bool cand = v < V && (level == 0 || (u >> (shift + 4)) == prefix);
+        const int dg = cand ? (int)((u >> shift) & 15u) - half * (kDigits / 2) : -1;
+#pragma unroll
+        for (int d = 0; d < kDigits / 2; ++d) {
+          cnt[d] += dg == d ? 1 : 0;
+          smf[d] += dg == d ? x[i] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < kDigits / 2; ++d) {
+        const int n = wave_sum_i(cnt[d]);
+        const double a = wave_sum_d((double)smf[d]);
+        if (lane == 0) {
+          sh.hn[w][half * (kDigits / 2) + d] = n;
+          sh.hs[w][half * (kDigits / 2) + d] = a;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < kDigits) {
+      int n = 0;
+      double a = 0.0;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) { n += sh.hn[ww][tid]; a += sh.hs[ww][tid]; }
+      sh.hn[0][tid] = n;
+      sh.hs[0][tid] = a;
+    }
+    __syncthreads();
+    // the digit holding the boundary, scanned from the top
+    int run_n = above_n, sel = 0;
+    double run_s = above_s;
+    bool pc = false;
+    for (int d = kDigits - 1; d >= 0; --d) {
+      const int n = sh.hn[0][d];
+      if (n == 0) continue;
+      const double a = sh.hs[0][d];
+      pc = use_p && run_s + a >= (double)top_p;
+      if (run_n + n >= kcap || pc) { sel = d; gcnt = n; break; }
+      run_n += n;
+      run_s += a;
+    }
+    above_n = run_n;
+    above_s = run_s;
+    p_cut = pc;
+    prefix = (prefix << 4) | (uint32_t)sel;
+  }
+  // entries equal to tau: how many the rule keeps
+  const float tf = __uint_as_float(prefix);
+  int m = kcap - above_n;
+  if (p_cut && tf > 0.f) {
+    const double need = ((double)top_p - above_s) / (double)tf;
+    const int mp = max(1, (int)ceil(need));
+    m = min(m, mp);
+  }
+  int tix = 0x7fffffff;
+  if (m < gcnt) {
+    // the m-th index (in index order) of the group: bisection on the index
+    int lo = 0, hi = V - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int v = tid + i * kThreads;
+        c += (v <= mid && v < V && __float_as_uint(x[i]) == prefix) ? 1 : 0;
+      }
+      c = wave_sum_i(c);
+      __syncthreads();
+      if (lane == 0) sh.i[w] = c;
+      __syncthreads();
+      int tot = 0;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) tot += sh.i[ww];
+      if (tot >= m) hi = mid; else lo = mid + 1;
+    }
+    tix = lo;
+  }
+  st.tau = prefix;
+  st.tix = tix;
+  __syncthreads();
 }
 
 // The row is held in registers (entry v = tid + kThreads i); p goes to sh.prow
 // when `to_lds`, and to gout when given.
+template <bool FILT>
 __device__ __forceinline__ RowStats row_pass(const float *__restrict__ row, int V, float T,
                              Shared &sh, bool to_lds,
-                             float *__restrict__ gout) {
+                             float *__restrict__ gout, int top_k = 0,
+                             float top_p = 1.f) {
   float x[kPer];
   load_row(row, V, -INFINITY, x);
   if (T != 1.0f) {
@@ -201,37 +366,46 @@ __device__ __forceinline__ RowStats row_pass(const float *__restrict__ row, int 
     s += x[i];
   }
   const float rs = 1.0f / block_sum(s, sh);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) x[i] = x[i] * rs;
+  RowStats st = mk_stats(mx, rs, 1.f);
+  if constexpr (FILT) block_filter(x, V, top_k, top_p, sh, st);
   float f = 0.f;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    x[i] = x[i] * rs;
+    if (FILT && !kept(x[i], (int)threadIdx.x + i * kThreads, st)) x[i] = 0.f;
     f += x[i];
   }
-  const float rf = 1.0f / block_sum(f, sh);
+  st.rfs = 1.0f / block_sum(f, sh);
   if (to_lds || gout) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int v = threadIdx.x + i * kThreads;
       if (v < V) {
-        const float p = x[i] * rf;
+        const float p = x[i] * st.rfs;
         if (to_lds) sh.prow[la(v)] = p;
         if (gout) gout[v] = p;
       }
     }
     __syncthreads();
   }
-  return RowStats{mx, rs, rf};
+  return st;
 }
 
+// FILT: the row is filtered by top_k / top_p (block_filter)
+template <bool FILT = false>
 __device__ __forceinline__ RowStats row_probs(const float *__restrict__ row,
                                               int V, float T, Shared &sh,
-                                              float *__restrict__ gout = nullptr) {
-  return row_pass(row, V, T, sh, true, gout);
+                                              float *__restrict__ gout = nullptr,
+                                              int top_k = 0, float top_p = 1.f) {
+  return row_pass<FILT>(row, V, T, sh, true, gout, top_k, top_p);
 }
 
+template <bool FILT = false>
 __device__ __forceinline__ RowStats row_stats(const float *__restrict__ row,
-                                              int V, float T, Shared &sh) {
-  return row_pass(row, V, T, sh, false, nullptr);
+                                              int V, float T, Shared &sh,
+                                              int top_k = 0, float top_p = 1.f) {
+  return row_pass<FILT>(row, V, T, sh, false, nullptr, top_k, top_p);
 }
 
 // sh.prow = p recomputed from a row's statistics
@@ -243,7 +417,7 @@ __device__ __forceinline__ void fill_probs(const float *__restrict__ row,
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int v = (int)threadIdx.x + i * kThreads;
-    if (v < V) sh.prow[la(v)] = (expf(scaled(x[i], T) - st.mx) * st.rsum) * st.rfs;
+    if (v < V) sh.prow[la(v)] = prob_of(x[i], v, T, st);
   }
   __syncthreads();
 }
@@ -280,10 +454,11 @@ __device__ __forceinline__ int block_sample(int V, float u, Shared &sh) {
   return r == 0x7fffffff ? V - 1 : r;
 }
 
+template <bool FILT>
 __device__ __forceinline__ int draw_row(const float *row, int V, float T, float u,
-                        Shared &sh) {
+                        Shared &sh, int top_k = 0, float top_p = 1.f) {
   if (T <= 0.f) return block_argmax(row, V, sh);
-  row_probs(row, V, T, sh);
+  row_probs<FILT>(row, V, T, sh, nullptr, top_k, top_p);
   return block_sample(V, u, sh);
 }
 
@@ -319,7 +494,7 @@ __device__ __forceinline__ RowStats wave_tiles_stats(const float2 *__restrict__ 
     if (lane + 64 * i < nt && v[i].x > -INFINITY) e += v[i].y * expf(v[i].x - mx);
   e = wave_sum_all(e);
   const float rs = 1.0f / e;
-  return RowStats{mx, rs, 1.0f / (e * rs)};
+  return mk_stats(mx, rs, 1.0f / (e * rs));
 }
 
 // first index of a row's maximum from its tile statistics (T <= 0), one wave
@@ -432,12 +607,13 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
 // ---------------------------------------------------------------------------
 // First token after the prefill (layer.cpp:1500-1510): cycle 0, slot 2k.
 // ---------------------------------------------------------------------------
+template <bool FILT>
 __global__ __launch_bounds__(kThreads) void first_token_kernel(
     SpecState s, const float *__restrict__ logits, int64_t ldl) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
   const float u = uniform(s.seed, s.seq0 + b, 0, 2 * s.k);
-  const int tok = draw_row(logits + b * ldl, s.V, s.T, u, sh);
+  const int tok = draw_row<FILT>(logits + b * ldl, s.V, s.T, u, sh, s.top_k, s.top_p);
   if (threadIdx.x == 0) {
     int32_t *out = s.out + (int64_t)b * s.out_stride;
     out[s.P] = tok;
@@ -460,6 +636,7 @@ __global__ __launch_bounds__(kThreads) void first_token_kernel(
 
 // One drafting step j (layer.cpp:1541-1558): q_j = get_probs(draft logits),
 // candidate = sample_token(q_j) with u[seq][cycle][j].
+template <bool FILT>
 __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
     SpecState s, int j, const float *__restrict__ logits, int64_t ldl) {
   __shared__ Shared sh;
@@ -470,7 +647,8 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
   if (s.T <= 0.f) {
     tok = block_argmax(row, s.V, sh);
   } else {
-    row_probs(row, s.V, s.T, sh, s.qprob + ((int64_t)b * s.k + j) * s.V);
+    row_probs<FILT>(row, s.V, s.T, sh, s.qprob + ((int64_t)b * s.k + j) * s.V,
+                    s.top_k, s.top_p);
     tok = block_sample(s.V, uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
   }
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
@@ -478,7 +656,9 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
 
 // Per verify row (b, j <= M): argmax (greedy) or the get_probs statistics
 // (sampled), for all rows of the cycle at once.  tstat[b][j] =
-// {max, 1/sum, 1/sum(p1), argmax as int bits}.
+// {max, 1/sum, 1/sum(kept p1), argmax, tau, tix} (the last three as int
+// bits).
+template <bool FILT>
 __global__ __launch_bounds__(kThreads) void target_stats_kernel(
     SpecState s, const float *__restrict__ tlogits) {
   __shared__ Shared sh;
@@ -488,13 +668,16 @@ __global__ __launch_bounds__(kThreads) void target_stats_kernel(
   if (j > M) return;
   const int64_t r = (int64_t)b * (s.k + 1) + j;
   const float *row = tlogits + r * s.V;
-  float *ts = s.tstat + r * 4;
+  float *ts = s.tstat + r * kTstat;
   if (s.T <= 0.f) {
     const int a = block_argmax(row, s.V, sh);
     if (threadIdx.x == 0) ts[3] = __int_as_float(a);
   } else {
-    const RowStats st = row_stats(row, s.V, s.T, sh);
-    if (threadIdx.x == 0) { ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs; }
+    const RowStats st = row_stats<FILT>(row, s.V, s.T, sh, s.top_k, s.top_p);
+    if (threadIdx.x == 0) {
+      ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs;
+      ts[4] = __uint_as_float(st.tau); ts[5] = __int_as_float(st.tix);
+    }
   }
 }
 
@@ -523,9 +706,8 @@ __device__ __forceinline__ int residual_sample(
     for (int i = 0; i < kHalf; ++i) {
       const int v = (int)threadIdx.x + (hf * kHalf + i) * kThreads;
       if (v < V) {
-        const float p = (expf(scaled(xt[i], T) - tst.mx) * tst.rsum) * tst.rfs;
-        const float q = qrow ? xq[i]
-                             : (expf(scaled(xq[i], T) - qst.mx) * qst.rsum) * qst.rfs;
+        const float p = prob_of(xt[i], v, T, tst);
+        const float q = qrow ? xq[i] : prob_of(xq[i], v, T, qst);
         const float r = fmaxf(0.0f, p - q);
         sh.prow[la(v)] = r;
         loc += r;
@@ -556,11 +738,14 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   int rej = -1;
   int64_t ties = 0;
   auto stats_of = [&](int j) {
-    const float *ts = s.tstat + ((int64_t)b * (k + 1) + j) * 4;
-    return RowStats{ts[0], ts[1], ts[2]};
+    const float *ts = s.tstat + ((int64_t)b * (k + 1) + j) * kTstat;
+    RowStats st = mk_stats(ts[0], ts[1], ts[2]);
+    st.tau = __float_as_uint(ts[4]);
+    st.tix = __float_as_int(ts[5]);
+    return st;
   };
   auto argmax_of = [&](int j) {
-    return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * 4 + 3]);
+    return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * kTstat + 3]);
   };
   // the candidates' target logits and draft probabilities, the first kPre
   // positions requested at once (their loop is unrolled so that the
@@ -581,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   auto test = [&](int j, int c, float lj, float qc) {
     if (greedy) return c == argmax_of(j);
     const RowStats st = stats_of(j);
-    const float pc = (expf(scaled(lj, s.T) - st.mx) * st.rsum) * st.rfs;
+    const float pc = prob_of(lj, c, s.T, st);
     const float r = uniform(s.seed, seq, cyc, k + j);
     if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
     return __fmul_rn(r, qc) < pc;
@@ -611,7 +796,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
       tok = argmax_of(rej);
     } else {
       tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, nullptr,
-                            RowStats{0.f, 1.f, 1.f}, row, stats_of(rej), V,
+                            mk_stats(0.f, 1.f, 1.f), row, stats_of(rej), V,
                             s.T, u, sh);
     }
     catch_tok = tok;
@@ -659,12 +844,13 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
 }
 
 // generate_advanced sampling step (layer.cpp:1294-1373): u[seq][step][0].
+template <bool FILT>
 __global__ __launch_bounds__(kThreads) void ar_sample_kernel(
     SpecState s, int step, const float *__restrict__ logits, int64_t ldl) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
   const float u = uniform(s.seed, s.seq0 + b, (uint32_t)step, 0);
-  const int tok = draw_row(logits + b * ldl, s.V, s.T, u, sh);
+  const int tok = draw_row<FILT>(logits + b * ldl, s.V, s.T, u, sh, s.top_k, s.top_p);
   if (threadIdx.x == 0) {
     s.out[(int64_t)b * s.out_stride + s.P + step] = tok;
     s.cur[b] = tok;
@@ -684,7 +870,7 @@ __global__ __launch_bounds__(kThreads) void accept_bench_kernel(
   __shared__ Shared sh;
   const int b = blockIdx.x;
   int rej = -1;
-  RowStats qst{0.f, 1.f, 1.f}, tst{0.f, 1.f, 1.f};
+  RowStats qst = mk_stats(0.f, 1.f, 1.f), tst = mk_stats(0.f, 1.f, 1.f);
   for (int j = 0; j < k; ++j) {
     const float *tr = tlog + ((int64_t)b * k + j) * V;
     const float *dr = dlog + ((int64_t)b * k + j) * V;
@@ -717,8 +903,9 @@ __global__ __launch_bounds__(kThreads) void accept_bench_kernel(
 }
 
 // get_probs + sample_token on independent rows with explicit uniforms.
+template <bool FILT>
 __global__ __launch_bounds__(kThreads) void sample_rows_kernel(
-    const float *__restrict__ logits, int V, float T,
+    const float *__restrict__ logits, int V, float T, int top_k, float top_p,
     const float *__restrict__ u, int32_t *__restrict__ tok,
     float *__restrict__ probs) {
   __shared__ Shared sh;
@@ -728,10 +915,16 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(
   if (T <= 0.f) {
     t = block_argmax(row, V, sh);
   } else {
-    row_probs(row, V, T, sh, probs ? probs + (int64_t)b * V : nullptr);
+    row_probs<FILT>(row, V, T, sh, probs ? probs + (int64_t)b * V : nullptr,
+                    top_k, top_p);
     t = block_sample(V, u[b], sh);
   }
   if (threadIdx.x == 0) tok[b] = t;
+}
+
+// whether a loop's sampling passes filter by top_k / top_p
+bool filtered(const SpecState &s) {
+  return s.T > 0.f && sampling_filtered(s.V, s.top_k, s.top_p);
 }
 
 }  // namespace
@@ -740,22 +933,34 @@ void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl) {
   NNHIP_REQUIRE(s.V <= kMaxV, kErrUnsupported,
                 "sampling: vocabulary above 32768");
-  hipLaunchKernelGGL(first_token_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
-                     logits, ldl);
+  if (filtered(s))
+    hipLaunchKernelGGL(first_token_kernel<true>, dim3(s.B), dim3(kThreads), 0,
+                       st, s, logits, ldl);
+  else
+    hipLaunchKernelGGL(first_token_kernel<false>, dim3(s.B), dim3(kThreads), 0,
+                       st, s, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
 }
 
 void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
                          const float *logits, int64_t ldl) {
-  hipLaunchKernelGGL(draft_sample_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
-                     j, logits, ldl);
+  if (filtered(s))
+    hipLaunchKernelGGL(draft_sample_kernel<true>, dim3(s.B), dim3(kThreads), 0,
+                       st, s, j, logits, ldl);
+  else
+    hipLaunchKernelGGL(draft_sample_kernel<false>, dim3(s.B), dim3(kThreads), 0,
+                       st, s, j, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
 }
 
 void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
   NNHIP_REQUIRE(s.tstat != nullptr, kErrArg, "accept: no row statistics");
-  hipLaunchKernelGGL(target_stats_kernel, dim3(s.k + 1, s.B), dim3(kThreads),
-                     0, st, s, tlogits);
+  if (filtered(s))
+    hipLaunchKernelGGL(target_stats_kernel<true>, dim3(s.k + 1, s.B),
+                       dim3(kThreads), 0, st, s, tlogits);
+  else
+    hipLaunchKernelGGL(target_stats_kernel<false>, dim3(s.k + 1, s.B),
+                       dim3(kThreads), 0, st, s, tlogits);
   NNHIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
                      tlogits);
@@ -767,6 +972,8 @@ void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
   NNHIP_REQUIRE(s.dtiles && (s.T <= 0.f || s.qprob) && s.nt <= kThreads &&
                     s.tw <= kThreads && s.V <= kMaxV,
                 kErrArg, "draft sample: tile statistics missing or too many tiles");
+  NNHIP_REQUIRE(s.T <= 0.f || !sampling_filtered(s.V, s.top_k, s.top_p), kErrArg,
+                "draft sample: tile statistics cannot apply top-k / top-p");
   hipLaunchKernelGGL(draft_sample_tiles_kernel, dim3(s.B, kQParts),
                      dim3(kThreads), 0, st, s, j, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
@@ -776,17 +983,26 @@ void launch_ar_sample(hipStream_t st, const SpecState &s, int step,
                       const float *logits, int64_t ldl) {
   NNHIP_REQUIRE(s.V <= kMaxV, kErrUnsupported,
                 "sampling: vocabulary above 32768");
-  hipLaunchKernelGGL(ar_sample_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
-                     step, logits, ldl);
+  if (filtered(s))
+    hipLaunchKernelGGL(ar_sample_kernel<true>, dim3(s.B), dim3(kThreads), 0, st,
+                       s, step, logits, ldl);
+  else
+    hipLaunchKernelGGL(ar_sample_kernel<false>, dim3(s.B), dim3(kThreads), 0,
+                       st, s, step, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
 }
 
 void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
-                        float T, const float *u, int32_t *tok, float *probs) {
+                        float T, const float *u, int32_t *tok, float *probs,
+                        int top_k, float top_p) {
   NNHIP_REQUIRE(V <= kMaxV, kErrUnsupported,
                 "sampling: vocabulary above 32768");
-  hipLaunchKernelGGL(sample_rows_kernel, dim3(B), dim3(kThreads), 0, st,
-                     logits, V, T, u, tok, probs);
+  if (T > 0.f && sampling_filtered(V, top_k, top_p))
+    hipLaunchKernelGGL(sample_rows_kernel<true>, dim3(B), dim3(kThreads), 0, st,
+                       logits, V, T, top_k, top_p, u, tok, probs);
+  else
+    hipLaunchKernelGGL(sample_rows_kernel<false>, dim3(B), dim3(kThreads), 0,
+                       st, logits, V, T, top_k, top_p, u, tok, probs);
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -85,7 +85,7 @@ SIGNATURES = {
     "nnhip_attention_kq_q8": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i,
                               _i, _i, _i, _vp],
     "nnhip_layernorm": [_vp, _vp, _i, _i, _vp, _vp, _vp],
-    "nnhip_sample_rows": [_vp, _vp, _i, _i, _f, _vp, _vp, _vp],
+    "nnhip_sample_rows": [_vp, _vp, _i, _i, _f, _i, _f, _vp, _vp, _vp],
     "nnhip_spec_accept": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp,
                           _vp],
     "nnhip_bench_attention": [_vp, _i, _i, _i, _i, _i, _i, _i, _i,
@@ -320,12 +320,13 @@ class Decoder:
         return out
 
     def generate_advanced_batch(self, prompts, max_new, T, seed, seq0=0,
-                                use_kv_cache=True):
+                                use_kv_cache=True, top_k=0, top_p=1.0):
         prompts = np.ascontiguousarray(prompts, np.int32)
         B, P = prompts.shape
         out = np.zeros((B, P + max_new), np.int32)
         call("nnhip_generate_advanced_batch", self.h, B, ptr(prompts), P,
-             max_new, T, 0, 1.0, seed, seq0, int(use_kv_cache), ptr(out))
+             max_new, T, top_k, top_p, seed, seq0, int(use_kv_cache),
+             ptr(out))
         return out
 
 

@@ -426,7 +426,7 @@ def test_sample_rows(ctx, V, T):
     dl, du = ctx.array(lg), ctx.array(u)
     dt = ctx.array(shape=(B,), dtype=np.int32)
     dp = ctx.array(shape=(B, V))
-    call("nnhip_sample_rows", ctx.h, dl.p, B, V, T, du.p, dt.p, dp.p)
+    call("nnhip_sample_rows", ctx.h, dl.p, B, V, T, 0, 1.0, du.p, dt.p, dp.p)
     tok = dt.numpy()
     mism = 0
     for b in range(B):
@@ -438,6 +438,87 @@ def test_sample_rows(ctx, V, T):
         want = O.sample(p, u[b])
         if tok[b] != want:
             assert cdf_tie(p, u[b]), (b, tok[b], want)
+            mism += 1
+    assert mism <= 1
+
+
+def exact_kept(p1, top_k, top_p):
+    """The kept set of get_probs' top-k / top-p with the running sum taken
+    exactly (float64), descending p1, ties by lower index; returns it and
+    the exact running sum at each entry's rank."""
+    V = p1.size
+    order = np.lexsort((np.arange(V), -p1.astype(np.float64)))
+    cs = np.cumsum(p1.astype(np.float64)[order])
+    R = top_k if 0 < top_k < V else V
+    if 0 < top_p < 1:
+        r = int(np.searchsorted(cs, top_p))       # first rank with cs >= top_p
+        R = min(R, r + 1)
+    kept = np.zeros(V, bool)
+    kept[order[:R]] = True
+    rank = np.empty_like(order)
+    rank[order] = np.arange(V)
+    return kept, cs[rank]
+
+
+TOPKP_CASES = [(256, 1.0, 4, 1.0), (32000, 1.0, 0, 0.9), (32000, 0.7, 50, 0.9),
+               (4096, 1.0, 4096, 0.5), (1000, 2.5, 0, 0.3), (32000, 1.0, 1, 1.0),
+               (5000, 1.0, 7, 0.0)]
+
+
+@pytest.mark.parametrize("V,T,top_k,top_p", TOPKP_CASES)
+def test_sample_rows_top_k_top_p(ctx, V, T, top_k, top_p):
+    """get_probs with top-k / top-p (layer.cpp:1447-1489).  The device keeps
+    exactly the set the rule gives with an exact running sum (exact_kept;
+    an entry may differ only where that sum is within 1e-6 of top_p, i.e.
+    where p1 itself differs from the oracle's in its last bits).  The
+    oracle, like the reference, sums in float in sorted order, which drifts
+    (most over long runs of equal probabilities: rows 0-2 hold duplicated
+    logits, so cuts fall inside groups of equal values, kept in index
+    order); where its kept set differs from the device's, every differing
+    entry lies between the exact and the float crossing.  Otherwise
+    probabilities within 1e-4 (row-relative) and the same draws except at a
+    CDF tie."""
+    B = 16
+    rng = np.random.default_rng(V + top_k)
+    lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    lg[0, :] = np.round(lg[0, :])                 # many exact ties
+    lg[1, :V // 2] = lg[1, 0]                     # one large tie group
+    lg[2, ::3] = 1.5                              # a tie group at the top
+    u = np.array([O.uniform(98, b, 4, 1) for b in range(B)], np.float32)
+    dl, du = ctx.array(lg), ctx.array(u)
+    dt = ctx.array(shape=(B,), dtype=np.int32)
+    dp = ctx.array(shape=(B, V))
+    call("nnhip_sample_rows", ctx.h, dl.p, B, V, T, top_k, top_p, du.p, dt.p,
+         dp.p)
+    tok, got = dt.numpy(), dp.numpy()
+    mism = 0
+    for b in range(B):
+        # p1 exactly normalised (the oracle's own float sums can drift by
+        # 1e-4 on rows of many equal logits, as the reference's do)
+        z = lg[b].astype(np.float64) / T
+        p1 = np.exp(z - z.max())
+        p1 /= p1.sum()
+        want = O.get_probs(lg[b], T, top_k, top_p)
+        kd, ko = got[b] > 0, want > 0
+        ke, cs = exact_kept(p1, top_k, top_p)
+        off = kd != ke
+        assert not off.any() or np.all(np.abs(cs[off] - top_p) < 1e-6), b
+        if not np.array_equal(kd, ko):
+            # the oracle's float running sum crossed top_p elsewhere
+            lo, hi = sorted((ko.sum(), kd.sum()))
+            order = np.lexsort((np.arange(V), -p1.astype(np.float64)))
+            assert set(np.nonzero(kd != ko)[0]) <= set(order[lo:hi]), b
+            common = kd & ko
+            ga = got[b] * common / (got[b] * common).sum()
+            wa = want * common / (want * common).sum()
+            assert row_rel_err(ga[None], wa[None]) <= 1e-4
+            continue
+        assert row_rel_err(got[b][None], want[None]) <= 1e-4, b
+        if 0 < top_k < V and not (0 < top_p < 1):
+            assert kd.sum() == top_k
+        w = O.sample(want, u[b])
+        if tok[b] != w:
+            assert cdf_tie(want, u[b]), (b, tok[b], w)
             mism += 1
     assert mism <= 1
 
