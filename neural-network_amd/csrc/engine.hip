@@ -9,6 +9,7 @@
 namespace nnhip {
 
 int g_lds_min_rows = 64;
+int g_fold_small = 0;
 int g_fold_norm = 0;
 
 namespace {
@@ -330,6 +331,16 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                       int epi, const RopeArgs *ra, const TileStatsArgs *ts) {
   hipStream_t st = ctx->lane(g);
   Workspace &ws = this->ws(g);
+  // option fold_small: a pending LayerNorm on a short batch (the draft's
+  // rows) folded into the LDS GEMM's prologue instead of a launch of its own
+  if (pn && g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
+      ln.quant && ln.qs.p && gemm_lds_supports(rows, ln.K, ln.N) &&
+      (!ts || !ts->out || gemm_lds_tile_width(ln.K) > 0)) {
+    launch_gemm_lds(st, kAFromLayerNorm, ws.limbs.p, ws.mpad, ws.rexp.p, pn->h,
+                    pn->ldh, pn->g, pn->b, pn->out, pn->ldo, rows, ln.K, ln.N,
+                    ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi, ra, ts);
+    return;
+  }
   if (use_lds(ln, rows)) {
     // Each column block of a fused GEMM normalises and digitises its rows
     // again: only the short-batch lm head folds the norm in; elsewhere one

@@ -265,6 +265,8 @@ extern int g_gemm_fk;        // LDS GEMM: 1 = full-K-wave kernel
 // engine.hip
 extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
 extern int g_fold_norm;     // 1 = a pending LayerNorm folds into every LDS GEMM
+extern int g_fold_small;    // 1 = ... and, on rows below g_lds_min_rows, into
+                            //     an LDS GEMM instead of a LayerNorm launch
 // workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
 constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
