@@ -27,6 +27,7 @@ extern "C" {
 #define NNHIP_ECAPACITY (-2)     /* sequence would exceed max_seq_len        */
 #define NNHIP_EHIP (-3)          /* HIP runtime failure                      */
 #define NNHIP_EUNSUPPORTED (-4)  /* option the device path does not provide  */
+#define NNHIP_EIO (-5)           /* a file could not be opened or written    */
 
 typedef struct nnhip_ctx nnhip_ctx;
 typedef struct nnhip_model nnhip_model;
@@ -119,6 +120,17 @@ int nnhip_decoder_quantize(nnhip_model *m, int bits);
  * [in][out] int8 (host), scales [out] (host). */
 int nnhip_decoder_get_quantized(const nnhip_model *m, int layer, int which,
                                 int8_t *codes, float *scales);
+/* Layer::save_weights / load_weights (layer.cpp:463-470) over parameters():
+ * the NETW v1 file of serialization::save_parameters / load_parameters
+ * (serialization.cpp:8-111): "NETW", uint16 version 1, uint32 count, per
+ * tensor uint32 rank, uint64 extents, uint64 element count, fp32 data, in
+ * the reference's shapes (embedding [V][d], Dense weight [in][out], bias
+ * [1][out], LayerNorm gamma / beta [d]).  load rejects a file whose count,
+ * ranks or extents differ from the model's with the reference's messages
+ * (NNHIP_EARG) and re-quantises a quantised model's Dense layers from the
+ * loaded fp32 weights; a file that cannot be opened is NNHIP_EIO. */
+int nnhip_decoder_save_weights(const nnhip_model *m, const char *path);
+int nnhip_decoder_load_weights(nnhip_model *m, const char *path);
 /* TransformerDecoder::forward(x, caches) (layer.cpp:1161-1193) for B
  * sequences of S ids each: ids [B][S] (host), logits [B][S][V] (host).
  * cache may be NULL (no cache: attention over the S ids only).  With a

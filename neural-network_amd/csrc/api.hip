@@ -211,6 +211,20 @@ int nnhip_decoder_quantize(nnhip_model *m, int bits) {
   });
 }
 
+int nnhip_decoder_save_weights(const nnhip_model *m, const char *path) {
+  return guard([&] {
+    REQ(m && path, "nnhip_decoder_save_weights: NULL argument");
+    nnhip::save_weights(*m->m, path);
+  });
+}
+
+int nnhip_decoder_load_weights(nnhip_model *m, const char *path) {
+  return guard([&] {
+    REQ(m && path, "nnhip_decoder_load_weights: NULL argument");
+    nnhip::load_weights(*m->m, path);
+  });
+}
+
 int nnhip_decoder_get_quantized(const nnhip_model *m, int layer, int which,
                                 int8_t *codes, float *scales) {
   return guard([&] {

@@ -7,6 +7,7 @@
 #include "nnhip_internal.hpp"
 
 #include <memory>
+#include <string>
 
 namespace nnhip {
 
@@ -145,6 +146,11 @@ struct SpecTiming {
   double prefill_ms, decode_ms;
   int64_t cycles_launched;
 };
+
+// Layer::save_weights / load_weights (layer.cpp:463-470): NETW v1 files of
+// the decoder's parameters() (netw.hip).
+void save_weights(const Model &m, const std::string &path);
+void load_weights(Model &m, const std::string &path);
 
 // generate_speculative (layer.cpp:1382-1661) for B independent sequences.
 void generate_speculative_batch(Model &target, Model &draft, int B,

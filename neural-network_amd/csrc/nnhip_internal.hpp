@@ -39,7 +39,8 @@ enum : int {
   kErrArg = -1,        // bad argument / shape
   kErrCapacity = -2,   // sequence would exceed max_seq_len
   kErrHip = -3,        // HIP runtime failure
-  kErrUnsupported = -4 // option the device path does not implement
+  kErrUnsupported = -4, // option the device path does not implement
+  kErrIO = -5          // a file could not be opened or written
 };
 
 // ---------------------------------------------------------------------------

@@ -11,7 +11,7 @@ import numpy as np
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG, "libnnhip.so")
 
-OK, EARG, ECAPACITY, EHIP, EUNSUPPORTED = 0, -1, -2, -3, -4
+OK, EARG, ECAPACITY, EHIP, EUNSUPPORTED, EIO = 0, -1, -2, -3, -4, -5
 
 
 class NNHipError(RuntimeError):
@@ -56,6 +56,8 @@ SIGNATURES = {
     "nnhip_decoder_init_normal": [_vp, _u64, _f],
     "nnhip_decoder_quantize": [_vp, _i],
     "nnhip_decoder_get_quantized": [_vp, _i, _i, _vp, _vp],
+    "nnhip_decoder_save_weights": [_vp, C.c_char_p],
+    "nnhip_decoder_load_weights": [_vp, C.c_char_p],
     "nnhip_decoder_forward": [_vp, _vp, _vp, _i, _i, _vp],
     "nnhip_kvcache_create": [_vp, _i, _i, _pp],
     "nnhip_kvcache_read_q8": [_vp, _i, _i, _vp, _vp, _vp, _vp],
@@ -278,6 +280,12 @@ class Decoder:
         call("nnhip_decoder_get_quantized", self.h, layer, which, ptr(codes),
              ptr(scales))
         return codes, scales
+
+    def save_weights(self, path):
+        call("nnhip_decoder_save_weights", self.h, os.fsencode(path))
+
+    def load_weights(self, path):
+        call("nnhip_decoder_load_weights", self.h, os.fsencode(path))
 
     def forward(self, ids, cache=None):
         ids = np.ascontiguousarray(np.atleast_2d(ids), np.int32)

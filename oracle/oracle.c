@@ -12,6 +12,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <time.h>
 #include <stdlib.h>
 #include <string.h>
@@ -433,6 +434,88 @@ void or_attention_q8(const float *q, const int8_t *kq, const float *ks,
     }
   }
   free(row);
+}
+
+/* ------------------------------------------------------------------ */
+/* NETW weight files                                                   */
+/* ------------------------------------------------------------------ */
+/* The reference's rank of parameters()[idx]: LayerNorm gamma / beta are
+ * Shape{embed_dim} (layer.cpp:204-209, 1063-1064); the embedding, Dense
+ * weights and biases ([1][out], layer.cpp:153-157) are 2-D. */
+static int param_rank(const or_model *m, int idx) {
+  int last = 1 + 18 * m->L;
+  return (idx >= 1 && idx < last && (idx - 1) % 18 >= 14) ? 1 : 2;
+}
+
+/* serialization::save_parameters (serialization.cpp:8-47): "NETW", uint16
+ * version 1, uint32 count, per tensor uint32 rank, uint64 extents, uint64
+ * element count, fp32 data.  Returns 0, or -1 when the file cannot be
+ * written. */
+int or_model_save_weights(const or_model *m, const char *path) {
+  FILE *f = fopen(path, "wb");
+  if (!f) return -1;
+  uint16_t version = 1;
+  uint32_t count = (uint32_t)or_model_num_params(m);
+  fwrite("NETW", 1, 4, f);
+  fwrite(&version, sizeof(version), 1, f);
+  fwrite(&count, sizeof(count), 1, f);
+  for (int i = 0; i < (int)count; ++i) {
+    int64_t r = 0, c = 0;
+    const float *p = param_ptr(m, i, &r, &c);
+    uint32_t rank = (uint32_t)param_rank(m, i);
+    uint64_t ext[2] = {(uint64_t)r, (uint64_t)c};
+    uint64_t n = (uint64_t)(r * c);
+    fwrite(&rank, sizeof(rank), 1, f);
+    if (rank == 1) fwrite(&ext[1], sizeof(uint64_t), 1, f);
+    else fwrite(ext, sizeof(uint64_t), 2, f);
+    fwrite(&n, sizeof(n), 1, f);
+    fwrite(p, sizeof(float), (size_t)n, f);
+  }
+  return fclose(f) == 0 ? 0 : -1;
+}
+
+/* serialization::load_parameters (serialization.cpp:49-109).  Returns 0;
+ * -1 when the file cannot be opened; -2 bad signature; -3 version; -4
+ * tensor count; -5 rank; -6 extent; -7 element count; -8 short read.
+ * A quantised model's Dense layers are quantised again from the loaded
+ * weights (what quantize_model after load_weights does). */
+int or_model_load_weights(or_model *m, const char *path) {
+  FILE *f = fopen(path, "rb");
+  if (!f) return -1;
+  int rc = 0;
+  char magic[4];
+  uint16_t version = 0;
+  uint32_t count = 0;
+  float *buf = NULL;
+  if (fread(magic, 1, 4, f) != 4 || memcmp(magic, "NETW", 4) != 0) { rc = -2; goto out; }
+  if (fread(&version, sizeof(version), 1, f) != 1) { rc = -8; goto out; }
+  if (version != 1) { rc = -3; goto out; }
+  if (fread(&count, sizeof(count), 1, f) != 1) { rc = -8; goto out; }
+  if (count != (uint32_t)or_model_num_params(m)) { rc = -4; goto out; }
+  for (int i = 0; i < (int)count; ++i) {
+    int64_t r = 0, c = 0;
+    float *p = param_ptr(m, i, &r, &c);
+    uint32_t rank = 0;
+    if (fread(&rank, sizeof(rank), 1, f) != 1) { rc = -8; goto out; }
+    if (rank != (uint32_t)param_rank(m, i)) { rc = -5; goto out; }
+    uint64_t want[2] = {(uint64_t)r, (uint64_t)c};
+    for (uint32_t d = 0; d < rank; ++d) {
+      uint64_t e = 0;
+      if (fread(&e, sizeof(e), 1, f) != 1) { rc = -8; goto out; }
+      if (e != want[2 - rank + d]) { rc = -6; goto out; }
+    }
+    uint64_t n = 0;
+    if (fread(&n, sizeof(n), 1, f) != 1) { rc = -8; goto out; }
+    if (n != (uint64_t)(r * c)) { rc = -7; goto out; }
+    buf = (float *)realloc(buf, sizeof(float) * (size_t)n);
+    if (fread(buf, sizeof(float), (size_t)n, f) != (size_t)n) { rc = -8; goto out; }
+    memcpy(p, buf, sizeof(float) * (size_t)n);
+  }
+  if (m->lm.codes) or_model_quantize(m);
+out:
+  free(buf);
+  fclose(f);
+  return rc;
 }
 
 /* ------------------------------------------------------------------ */

@@ -59,6 +59,12 @@ int or_model_num_params(const or_model *m);
 int or_model_param_shape(const or_model *m, int idx, int64_t *rows,
                          int64_t *cols);
 int or_model_set_param(or_model *m, int idx, const float *data);
+/* Layer::save_weights / load_weights (layer.cpp:463-470) over parameters():
+ * the NETW v1 file of serialization.cpp:8-109.  save: 0 or -1 (file).
+ * load: 0; -1 open; -2 signature; -3 version; -4 tensor count; -5 rank;
+ * -6 extent; -7 element count; -8 short read. */
+int or_model_save_weights(const or_model *m, const char *path);
+int or_model_load_weights(or_model *m, const char *path);
 /* Quantise every Dense (q,k,v,o,gate,up,down,lm_head) to symmetric int8
  * per output channel; the embedding stays fp32. */
 int or_model_quantize(or_model *m);

@@ -59,6 +59,8 @@ def lib():
                                         C.POINTER(C.c_int8), fp]
         L.or_cache_set_len.argtypes = [vp, i32]
         L.or_cache_freeze.argtypes = [vp, i32]
+        L.or_model_save_weights.argtypes = [vp, C.c_char_p]
+        L.or_model_load_weights.argtypes = [vp, C.c_char_p]
         L.or_quantize_kv.argtypes = [fp, i64, i64, C.POINTER(C.c_int8), fp]
         L.or_attention_q8.argtypes = [fp, C.POINTER(C.c_int8), fp,
                                       C.POINTER(C.c_int8), fp, i64, i64, i64,
@@ -178,6 +180,14 @@ class Model:
         assert lib().or_model_get_quantized(self.h, layer, which,
                                             i8ptr(codes), fptr(scales)) == 0
         return codes, scales
+
+    def save_weights(self, path):
+        if lib().or_model_save_weights(self.h, os.fsencode(path)) != 0:
+            raise RuntimeError(f"or_model_save_weights failed: {path}")
+
+    def load_weights(self, path):
+        """0 on success, else the oracle's error code (see oracle.h)."""
+        return lib().or_model_load_weights(self.h, os.fsencode(path))
 
     def forward(self, ids, cache=None):
         ids = np.ascontiguousarray(ids, np.int32)

@@ -123,6 +123,54 @@ def test_forward_cache_truncate_vs_oracle(ctx, quant):
     gm.free()
 
 
+def test_netw_weights_files(ctx, tmp_path):
+    """Layer::save_weights / load_weights (layer.cpp:463-470) through the
+    device decoder: its NETW file is byte-identical to the oracle's
+    (serialization.cpp:8-47) for the same parameters; a device decoder
+    loaded from the oracle's file holds the same parameters and gives the
+    oracle's logits (1e-4), quantised too (the Dense layers re-quantised from
+    the loaded weights); bad files are rejected with the reference's
+    messages."""
+    cfg = TOY_T
+    args = (cfg["vocab"], cfg["d"], cfg["H"], cfg["F"], cfg["L"])
+    params = O.make_params(*args, 31, std=0.05, bias_std=0.02)
+    om = O.Model(*args, 256, params)
+    gm = nnhip.Decoder(ctx, *args, 256)
+    gm.set_params(params)
+    pd, po = tmp_path / "dev.netw", tmp_path / "oracle.netw"
+    gm.save_weights(pd)
+    om.save_weights(po)
+    assert pd.read_bytes() == po.read_bytes()
+    ids = np.array([[5, 17, 200, 3, 99, 42]], np.int32)
+    for quant in (False, True):
+        g2 = nnhip.Decoder(ctx, *args, 256)
+        g2.init_normal(9, 0.02)
+        if quant:
+            g2.quantize()
+        g2.load_weights(po)
+        for i in (0, 1, 2, 9, 15, len(params) - 1):
+            np.testing.assert_array_equal(g2.get_param(i).ravel(),
+                                          params[i].ravel())
+        want = O.Model(*args, 256, params, quant).forward(ids[0])
+        assert_rows_close(g2.forward(ids)[0], want, 1e-4, f"loaded q={quant}")
+        g2.free()
+    wide = nnhip.Decoder(ctx, cfg["vocab"], 2 * cfg["d"], cfg["H"], cfg["F"],
+                         cfg["L"], 256)
+    with pytest.raises(nnhip.NNHipError) as e:
+        wide.load_weights(po)
+    assert e.value.code == nnhip.EARG and "shape mismatch" in str(e.value)
+    bad = tmp_path / "bad.netw"
+    bad.write_bytes(b"NETX" + po.read_bytes()[4:])
+    with pytest.raises(nnhip.NNHipError) as e:
+        gm.load_weights(bad)
+    assert "Invalid file format signature" in str(e.value)
+    with pytest.raises(nnhip.NNHipError) as e:
+        gm.load_weights(tmp_path / "missing.netw")
+    assert e.value.code == nnhip.EIO
+    wide.free()
+    gm.free()
+
+
 def test_causal_independence(ctx):
     """transformer_test.cpp:153-176 on the device."""
     _, gm, _ = build(ctx, TOY_T, 6, True)

@@ -498,3 +498,97 @@ def test_frozen_cache_recomputes_forward():
         c, sc = O.quantize_kv(raw)
         np.testing.assert_array_equal(c, codes)
         np.testing.assert_array_equal(sc, scales)
+
+
+# --------------------------------------------------------------------------
+# NETW weight files (serialization.cpp:8-109; serialization_test.cpp)
+# --------------------------------------------------------------------------
+def reference_shapes(vocab, d, F, L):
+    """parameters() shapes as the reference constructs them: Embedding
+    [V][d] (layer.cpp:267-268); Dense weight [in][out] and bias [1][out]
+    (layer.cpp:153-157); LayerNorm gamma / beta [d] (layer.cpp:1063-1064)."""
+    dense = lambda i, o: [(i, o), (1, o)]
+    shapes = [(vocab, d)]
+    for _ in range(L):
+        for _ in range(4):
+            shapes += dense(d, d)                     # q, k, v, o
+        shapes += dense(d, F) + dense(d, F) + dense(F, d)   # gate, up, down
+        shapes += [(d,), (d,), (d,), (d,)]
+    return shapes + dense(d, vocab)
+
+
+def parse_netw(blob):
+    import struct
+    assert blob[:4] == b"NETW"
+    version, count = struct.unpack_from("<HI", blob, 4)
+    off, out = 10, []
+    for _ in range(count):
+        (rank,) = struct.unpack_from("<I", blob, off); off += 4
+        dims = struct.unpack_from("<%dQ" % rank, blob, off); off += 8 * rank
+        (n,) = struct.unpack_from("<Q", blob, off); off += 8
+        data = np.frombuffer(blob, np.float32, n, off); off += 4 * n
+        out.append((dims, data))
+    assert off == len(blob)
+    return version, out
+
+
+def test_netw_layout(tmp_path):
+    """The file bytes follow save_parameters field by field: magic, uint16
+    version 1, uint32 count, then rank / extents / count / fp32 data per
+    tensor in parameters() order with the reference's shapes."""
+    V, d, H, F, L = 5, 4, 2, 8, 2
+    params = O.make_params(V, d, H, F, L, 3, std=0.5, bias_std=0.1)
+    m = O.Model(V, d, H, F, L, 16, params)
+    path = tmp_path / "w.netw"
+    m.save_weights(path)
+    version, tensors = parse_netw(path.read_bytes())
+    assert version == 1
+    shapes = reference_shapes(V, d, F, L)
+    assert len(tensors) == len(shapes) == len(params)
+    for (dims, data), shape, p in zip(tensors, shapes, params):
+        assert dims == shape
+        np.testing.assert_array_equal(data, p.ravel())
+
+
+def test_netw_round_trip(tmp_path):
+    """serialization_test.cpp SaveAndLoadConsistency: a model loaded from
+    another's file has its parameters and gives its outputs (bit-equal);
+    a quantised model re-quantises from the loaded weights."""
+    V, d, H, F, L = 12, 8, 2, 16, 2
+    pa = O.make_params(V, d, H, F, L, 4, std=0.3)
+    pb = O.make_params(V, d, H, F, L, 5, std=0.3)
+    a = O.Model(V, d, H, F, L, 32, pa)
+    path = tmp_path / "a.netw"
+    a.save_weights(path)
+    ids = [3, 1, 4, 1, 5]
+    for quant in (False, True):
+        b = O.Model(V, d, H, F, L, 32, pb, quantize=quant)
+        assert b.load_weights(path) == 0
+        want = O.Model(V, d, H, F, L, 32, pa, quantize=quant).forward(ids)
+        np.testing.assert_array_equal(b.forward(ids), want)
+
+
+def test_netw_errors(tmp_path):
+    """serialization_test.cpp ShapeMismatchAssertion and the other checks of
+    load_parameters: wrong extent, tensor count, rank, signature, version,
+    a missing file and a truncated one are all rejected."""
+    import struct
+    V, d, H, F = 6, 4, 2, 8
+    a = O.Model(V, d, H, F, 1, 16, O.make_params(V, d, H, F, 1, 1))
+    path = tmp_path / "a.netw"
+    a.save_weights(path)
+    blob = path.read_bytes()
+    wide = O.Model(V, 8, H, F, 1, 16, O.make_params(V, 8, H, F, 1, 1))
+    assert wide.load_weights(path) == -6                  # extent
+    deep = O.Model(V, d, H, F, 2, 16, O.make_params(V, d, H, F, 2, 1))
+    assert deep.load_weights(path) == -4                  # tensor count
+    fresh = O.Model(V, d, H, F, 1, 16, O.make_params(V, d, H, F, 1, 2))
+    for name, data, code in (
+            ("magic", b"NETX" + blob[4:], -2),
+            ("version", blob[:4] + struct.pack("<H", 2) + blob[6:], -3),
+            ("rank", blob[:10] + struct.pack("<I", 3) + blob[14:], -5),
+            ("short", blob[:-3], -8)):
+        p = tmp_path / name
+        p.write_bytes(data)
+        assert fresh.load_weights(p) == code, name
+    assert fresh.load_weights(tmp_path / "missing") == -1
