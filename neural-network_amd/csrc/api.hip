@@ -77,6 +77,7 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
     }
     else if (std::strcmp(key, "fold_norm") == 0) nnhip::g_fold_norm = value != 0;
     else if (std::strcmp(key, "fold_small") == 0) nnhip::g_fold_small = value != 0;
+    else if (std::strcmp(key, "down_split") == 0) nnhip::g_down_split = value != 0;
     else if (std::strcmp(key, "attn_w4") == 0) nnhip::g_attn_w4 = value != 0;
     else if (std::strcmp(key, "attn_waves") == 0) {
       REQ(value >= 64 && value <= (1 << 20), "attn_waves must be in [64, 2^20]");

@@ -704,11 +704,14 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
 // their gamma and beta requested together with the row; the row sums and the
 // max are DPP wave reductions, and the digits of y (for the next MFMA GEMM)
 // are written from the same registers.
-template <int PPL>
+// EPI: the row is first formed from a limb GEMM's int64 totals by the
+// deferred kEpiResid epilogue (LinEpiArgs), whose totals are then zeroed.
+template <int PPL, bool EPI>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
     const float *__restrict__ bt, float *__restrict__ y,
-    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp,
+    LinEpiArgs ea) {
 #pragma clang fp contract(off)
   typedef int v4i __attribute__((ext_vector_type(4)));
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -718,6 +721,43 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
   const int np = d / 16;
   // pieces past the row re-read the last piece and are masked
   float v[PPL][16], gv[PPL][16], bv[PPL][16];
+  if constexpr (EPI) {
+    const int te = ea.texp[row];
+    long long *tr = ea.tot + (int64_t)row * d;
+    const float *rr = ea.resid + (int64_t)row * ea.ldr;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      const int pc = min(lane + 64 * j, np - 1);
+      long long t[16];
+      float sc[16], bi[16], rs[16];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const longlong2 tt = *reinterpret_cast<const longlong2 *>(tr + 16 * pc + 2 * q);
+        t[2 * q] = tt.x; t[2 * q + 1] = tt.y;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 a = *reinterpret_cast<const float4 *>(ea.scale + 16 * pc + 4 * q);
+        const float4 c = *reinterpret_cast<const float4 *>(ea.bias + 16 * pc + 4 * q);
+        const float4 r = *reinterpret_cast<const float4 *>(rr + 16 * pc + 4 * q);
+        const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
+        const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
+        sc[4 * q] = a.x; sc[4 * q + 1] = a.y; sc[4 * q + 2] = a.z; sc[4 * q + 3] = a.w;
+        bi[4 * q] = c.x; bi[4 * q + 1] = c.y; bi[4 * q + 2] = c.z; bi[4 * q + 3] = c.w;
+        rs[4 * q] = r.x; rs[4 * q + 1] = r.y; rs[4 * q + 2] = r.z; rs[4 * q + 3] = r.w;
+        gv[j][4 * q] = gg.x; gv[j][4 * q + 1] = gg.y; gv[j][4 * q + 2] = gg.z; gv[j][4 * q + 3] = gg.w;
+        bv[j][4 * q] = bb.x; bv[j][4 * q + 1] = bb.y; bv[j][4 * q + 2] = bb.z; bv[j][4 * q + 3] = bb.w;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        v[j][q] = rs[q] + __fadd_rn(__fmul_rn(ldexpf((float)t[q], -te), sc[q]), bi[q]);
+      if (lane + 64 * j < np) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          *reinterpret_cast<longlong2 *>(tr + 16 * pc + 2 * q) = make_longlong2(0, 0);
+      }
+    }
+  } else {
 #pragma unroll
   for (int j = 0; j < PPL; ++j) {
     const int pc = min(lane + 64 * j, np - 1);
@@ -730,6 +770,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
       gv[j][4 * q] = gg.x; gv[j][4 * q + 1] = gg.y; gv[j][4 * q + 2] = gg.z; gv[j][4 * q + 3] = gg.w;
       bv[j][4 * q] = bb.x; bv[j][4 * q + 1] = bb.y; bv[j][4 * q + 2] = bb.z; bv[j][4 * q + 3] = bb.w;
     }
+  }
   }
   float s = 0.f;
 #pragma unroll
@@ -970,22 +1011,30 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
 
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,
-                      int8_t *limbs, int mpad, int *rexp) {
+                      int8_t *limbs, int mpad, int *rexp,
+                      const LinEpiArgs *ea) {
   NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
   NNHIP_REQUIRE(!limbs || (d % 128 == 0 && rows <= mpad), kErrArg,
                 "layernorm: digit output needs d % 128 == 0");
+  const bool epi = ea && ea->tot;
+  NNHIP_REQUIRE(!epi || (d % 16 == 0 && ea->texp && ea->scale && ea->bias &&
+                         ea->resid && ea->ldr % 4 == 0),
+                kErrArg, "layernorm: GEMM epilogue arguments missing");
+  const LinEpiArgs ez = epi ? *ea : LinEpiArgs{};
   if (d % 16 == 0) {
     const int np = d / 16;
     const dim3 grid((rows + 3) / 4);
-    if (np <= 64)
-      hipLaunchKernelGGL(layernorm_rows_kernel<1>, grid, dim3(256), 0, st, h, d,
-                         rows, g, b, y, limbs, mpad, rexp);
-    else if (np <= 128)
-      hipLaunchKernelGGL(layernorm_rows_kernel<2>, grid, dim3(256), 0, st, h, d,
-                         rows, g, b, y, limbs, mpad, rexp);
-    else
-      hipLaunchKernelGGL(layernorm_rows_kernel<4>, grid, dim3(256), 0, st, h, d,
-                         rows, g, b, y, limbs, mpad, rexp);
+#define NNHIP_LN(P)                                                           \
+  if (epi)                                                                    \
+    hipLaunchKernelGGL((layernorm_rows_kernel<P, true>), grid, dim3(256), 0,  \
+                       st, h, d, rows, g, b, y, limbs, mpad, rexp, ez);       \
+  else                                                                        \
+    hipLaunchKernelGGL((layernorm_rows_kernel<P, false>), grid, dim3(256), 0, \
+                       st, h, d, rows, g, b, y, limbs, mpad, rexp, ez)
+    if (np <= 64) { NNHIP_LN(1); }
+    else if (np <= 128) { NNHIP_LN(2); }
+    else { NNHIP_LN(4); }
+#undef NNHIP_LN
   } else {
     hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,
                        b, y, limbs, mpad, rexp);

@@ -10,6 +10,7 @@ namespace nnhip {
 
 int g_lds_min_rows = 64;
 int g_fold_small = 0;
+int g_down_split = 0;
 int g_fold_norm = 0;
 
 namespace {
@@ -283,6 +284,8 @@ void Model::reserve(int g, int rows, int lrows, int max_keys) {
     ws.ctx.alloc((size_t)r * d); ws.h.alloc((size_t)r * d);
     ws.x1.alloc((size_t)r * d);
     ws.qkv.alloc((size_t)r * 3 * d);
+    ws.tot.alloc((size_t)r * d);
+    NNHIP_CHECK(hipMemsetAsync(ws.tot.p, 0, ws.tot.bytes(), ctx->lane(g)));
     ws.ff.alloc((size_t)r * F);
     ws.mpad = round_up(r, 64);
     ws.limbs.alloc((size_t)kLimbs * ws.mpad * std::max(d, F));
@@ -321,6 +324,16 @@ bool Model::use_lds(const Linear &ln, int rows) const {
   return &ln == &lm || rows >= g_lds_min_rows;
 }
 
+// whether linear_in folds a pending LayerNorm into the LDS GEMM's prologue
+bool Model::norm_folds(const Linear &ln, int rows) const {
+  if (g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
+      ln.quant && ln.qs.p && gemm_lds_supports(rows, ln.K, ln.N))
+    return true;
+  return use_lds(ln, rows) &&
+         (g_fold_norm || (&ln == &lm && rows < g_lds_min_rows)) &&
+         gemm_lds_workgroups(rows, ln.K, ln.N) <= kFusedNormMaxBlocks;
+}
+
 bool Model::lm_tiles(int rows) const {
   return use_lds(lm, rows) && gemm_lds_tile_width(lm.K) > 0;
 }
@@ -333,7 +346,7 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
   Workspace &ws = this->ws(g);
   // option fold_small: a pending LayerNorm on a short batch (the draft's
   // rows) folded into the LDS GEMM's prologue instead of a launch of its own
-  if (pn && g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
+  if (pn && !pn->ea.tot && g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
       ln.quant && ln.qs.p && gemm_lds_supports(rows, ln.K, ln.N) &&
       (!ts || !ts->out || gemm_lds_tile_width(ln.K) > 0)) {
     launch_gemm_lds(st, kAFromLayerNorm, ws.limbs.p, ws.mpad, ws.rexp.p, pn->h,
@@ -345,12 +358,11 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
     // Each column block of a fused GEMM normalises and digitises its rows
     // again: only the short-batch lm head folds the norm in; elsewhere one
     // LayerNorm launch writes digit planes for the GEMM to copy.
-    const bool fold = (g_fold_norm || (&ln == &lm && rows < g_lds_min_rows)) &&
-                      gemm_lds_workgroups(rows, ln.K, ln.N) <= kFusedNormMaxBlocks;
+    const bool fold = !(pn && pn->ea.tot) && norm_folds(ln, rows);
     if (pn && !fold && pn->ldh == ln.K) {
       launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b,
                        pn->out ? pn->out : ws.x.p, ws.limbs.p, ws.mpad,
-                       ws.rexp.p);
+                       ws.rexp.p, &pn->ea);
       launch_gemm_lds(st, kAFromDigits, ws.limbs.p, ws.mpad, ws.rexp.p,
                       nullptr, 0, nullptr, nullptr, nullptr, 0, rows, ln.K,
                       ln.N, ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi,
@@ -374,7 +386,7 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                   "linear_in: unfused LayerNorm needs contiguous rows");
     const bool lr = use_limbs(ln, rows);
     launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b, pn->out,
-                     lr ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+                     lr ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p, &pn->ea);
     linear(g, ln, pn->out, pn->ldo, rows, lr, resid, ldr, y, ldy, epi, ra);
     return;
   }
@@ -483,8 +495,35 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
     norm1.out = ws.x1.p; norm1.ldo = d;
     linear_in(g, ly.gu, nullptr, 0, &norm1, R, false, nullptr, 0, ws.ff.p, F,
               kEpiSwiGLU);
-    linear_in(g, ly.down, ws.ff.p, F, nullptr, R, false, ws.x1.p, d, ws.h.p,
-              d, kEpiResid);
+    // Option down_split: the down projection on the digit-plane GEMM splits
+    // its K range over workgroups that add exact int64 totals, and the
+    // LayerNorm that follows applies the epilogue (scale, bias, residual) --
+    // unless that norm is folded into the lm head's prologue or never
+    // applied.  Measured on the batch-32 decode: the draft's GEMM gains what
+    // its LayerNorm loses (int64 reads and the zeroing), the verify's GEMM
+    // is slower (cross-XCD atomics), so it is off by default.
+    const bool last = l == L - 1;
+    const int lm_rows = last_only ? B : R;
+    const bool split = g_down_split && use_limbs(ly.down, R) &&
+                       !g_fold_norm && !g_fold_small &&
+                       (!last || (logits && !norm_folds(lm, lm_rows)));
+    norm2.ea = LinEpiArgs{};
+    if (split) {
+      const int nch = ly.down.K / 128;
+      const int tiles = ((R + 31) / 32) * (ly.down.N / 32);
+      const int ks = std::max(1, std::min(nch / 4, kGemmSlots * 2 / tiles));
+      launch_act_quant(st, ws.ff.p, F, R, ly.down.K, ws.limbs.p, ws.mpad, ws.rexp.p);
+      launch_gemm_limb(st, ws.limbs.p, ws.mpad, ws.rexp.p, R, ly.down.K,
+                       ly.down.N, ly.down.qs.p, ly.down.s.p, ly.down.b.p,
+                       nullptr, 0, reinterpret_cast<float *>(ws.tot.p), d,
+                       kEpiAddTotals, nullptr, ks);
+      norm2.ea.tot = ws.tot.p; norm2.ea.texp = ws.rexp.p;
+      norm2.ea.scale = ly.down.s.p; norm2.ea.bias = ly.down.b.p;
+      norm2.ea.resid = ws.x1.p; norm2.ea.ldr = d;
+    } else {
+      linear_in(g, ly.down, ws.ff.p, F, nullptr, R, false, ws.x1.p, d, ws.h.p,
+                d, kEpiResid);
+    }
     norm2.h = ws.h.p; norm2.ldh = d; norm2.g = ly.g2.p; norm2.b = ly.b2.p;
     norm2.out = ws.x.p; norm2.ldo = d;
     have_norm2 = true;
@@ -502,7 +541,7 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                     "forward: tile statistics need the LDS-resident lm head");
       launch_layernorm(st, ws.h.p, R, d, norm2.g, norm2.b, ws.x.p, nullptr,
-                       ws.mpad, ws.rexp.p);
+                       ws.mpad, ws.rexp.p, &norm2.ea);
       if (last_only)
         linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
                nullptr, 0, logits, ldl, kEpiBias);

@@ -45,6 +45,7 @@ struct LayerW {
 struct Workspace {
   int rows = 0, lrows = 0;
   DevBuf<float> x, qkv, qrot, ctx, h, x1, ff, logits, part;
+  DevBuf<long long> tot;   // [rows][d] split-K totals, kept zeroed
   DevBuf<int8_t> limbs;
   DevBuf<int> rexp;
   DevBuf<int32_t> ids, zeros;
@@ -99,11 +100,15 @@ struct Model {
               int64_t ldy, int epi, const RopeArgs *ra = nullptr);
   // A LayerNorm of h (rows of stride ldh) that the next linear applies to
   // its input; the normalised rows go to out (stride ldo) when out is set.
+  // ea.tot set: h is not written; its rows are formed from a split-K limb
+  // GEMM's totals by the LayerNorm kernel (LinEpiArgs), which cannot be
+  // folded into a GEMM prologue.
   struct PendingNorm {
     const float *h = nullptr, *g = nullptr, *b = nullptr;
     int64_t ldh = 0;
     float *out = nullptr;
     int64_t ldo = 0;
+    LinEpiArgs ea;
   };
   // linear over x, or over LN(h) when pn is given (x is then ignored)
   void linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
@@ -112,6 +117,7 @@ struct Model {
                  int epi, const RopeArgs *ra = nullptr,
                  const TileStatsArgs *ts = nullptr);
   bool use_limbs(const Linear &ln, int rows) const;
+  bool norm_folds(const Linear &ln, int rows) const;
   bool use_lds(const Linear &ln, int rows) const;
 };
 

@@ -227,14 +227,15 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     int M, int K, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
+    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra, int ksplit) {
   constexpr int NT = 32 * NSUB;
   __shared__ int red[kLimbs][kGemmMT][NT];
-  const int T = ntm * ntn;
+  const int T = ntm * ntn * ksplit;
   const int per = (T + 7) / 8;
   const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
   if (wi >= T) return;
-  const int tn = wi / ntm, tm = wi % ntm;
+  const int kq = wi / (ntm * ntn), wt = wi % (ntm * ntn);
+  const int tn = wt / ntm, tm = wt % ntm;
   const int m0 = tm * kGemmMT, n0 = tn * NT;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -247,7 +248,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   constexpr int IT = kGemmMT * NT / 2 / 256;
   static_assert(256 % (NT / 2) == 0, "items must share their columns");
   const int e_n = n0 + 2 * ((int)threadIdx.x % (NT / 2));
-  const bool e_cols = epi != kEpiTotals;
+  const bool e_cols = epi != kEpiTotals && epi != kEpiAddTotals;
   const float e_sc0 = e_cols ? scale[e_n] : 0.f, e_sc1 = e_cols ? scale[e_n + 1] : 0.f;
   const float e_bi0 = e_cols ? bias[e_n] : 0.f, e_bi1 = e_cols ? bias[e_n + 1] : 0.f;
   int e_ex[IT];
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int m = m0 + ((int)threadIdx.x + it * 256) / (NT / 2);
-    const bool ok = m < M && epi != kEpiTotals;
+    const bool ok = m < M && e_cols;
     e_ex[it] = ok ? rexp[m] : 0;
     e_rs[it][0] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n] : 0.f;
     e_rs[it][1] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n + 1] : 0.f;
@@ -268,6 +269,8 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
 #pragma unroll
     for (int l = 0; l < kLimbs; ++l) acc[t][l] = v16i{};
   const int nch = K / 128;
+  // this workgroup's chunks [cb, ce) of the K range
+  const int cb = kq * nch / ksplit, ce = (kq + 1) * nch / ksplit;
   // tile bases in the operand layout: 32 rows x 128 k = 4 KB per chunk
   const int8_t *pb = wq + (int64_t)(n0 >> 5) * nch * 4096 + lane * 16;
   const int8_t *pa = limbs + (int64_t)(m0 >> 5) * nch * 4096 + lane * 16;
@@ -297,18 +300,18 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   // ping-pong over the wave's chunks w, w+4, w+8, ...: the loads of the next
   // chunk are in flight while the current chunk's MFMAs run
   Frag fa, fb;
-  int c = w;
-  if (c < nch) load(c, fa);
-  while (c < nch) {
-    if (c + 4 < nch) load(c + 4, fb);
+  int c = cb + w;
+  if (c < ce) load(c, fa);
+  while (c < ce) {
+    if (c + 4 < ce) load(c + 4, fb);
     mma(fa);
     c += 4;
-    if (c >= nch) break;
-    if (c + 4 < nch) load(c + 4, fa);
+    if (c >= ce) break;
+    if (c + 4 < ce) load(c + 4, fa);
     mma(fb);
     c += 4;
   }
-  if (w < nch) {
+  if (cb + w < ce) {
 #pragma unroll
     for (int t = 0; t < NSUB; ++t)
 #pragma unroll
@@ -338,6 +341,13 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     if (epi == kEpiTotals) {
       long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
       yt[0] = tot[0]; yt[1] = tot[1];
+      continue;
+    }
+    if (epi == kEpiAddTotals) {
+      unsigned long long *yt =
+          reinterpret_cast<unsigned long long *>(y) + (int64_t)m * ldy + n;
+      atomicAdd(yt, (unsigned long long)tot[0]);
+      atomicAdd(yt + 1, (unsigned long long)tot[1]);
       continue;
     }
     float v[2];
@@ -1199,9 +1209,12 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi, const RopeArgs *ra) {
+                      int epi, const RopeArgs *ra, int ksplit) {
   NNHIP_REQUIRE(K % 128 == 0 && N % 64 == 0, kErrArg,
                 "gemm_limb: K % 128 and N % 64 must be 0");
+  NNHIP_REQUIRE(ksplit >= 1 && ksplit <= K / 128 &&
+                    (ksplit == 1 || epi == kEpiAddTotals),
+                kErrArg, "gemm_limb: a K split needs the atomic totals epilogue");
   NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg,
                 "gemm_limb: RoPE epilogue needs its arguments");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
@@ -1214,15 +1227,15 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
   const bool wide = ntm * (N / 64) >= 512 && g_gemm_wide != 0;
   if (wide) {
-    const int ntn = N / 64, per = (ntm * ntn + 7) / 8;
+    const int ntn = N / 64, per = (ntm * ntn * ksplit + 7) / 8;
     hipLaunchKernelGGL(gemm_limb_kernel<2>, dim3(8 * per), dim3(256), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
-                       ldr, y, ldy, epi, ntm, ntn, rz);
+                       ldr, y, ldy, epi, ntm, ntn, rz, ksplit);
   } else {
-    const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
+    const int ntn = N / 32, per = (ntm * ntn * ksplit + 7) / 8;
     hipLaunchKernelGGL(gemm_limb_kernel<1>, dim3(8 * per), dim3(256), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
-                       ldr, y, ldy, epi, ntm, ntn, rz);
+                       ldr, y, ldy, epi, ntm, ntn, rz, ksplit);
   }
   NNHIP_CHECK(hipGetLastError());
 }

@@ -84,19 +84,23 @@ def test_forward_vs_oracle(ctx, quant, S):
 WIDE = dict(vocab=512, d=1024, H=16, F=4096, L=1)
 
 
-@pytest.mark.parametrize("fk", [0, 1])
-def test_forward_wide_vs_oracle(ctx, fk):
+@pytest.mark.parametrize("fk,split", [(0, 0), (1, 0), (0, 1)])
+def test_forward_wide_vs_oracle(ctx, fk, split):
     """80 rows through a d = 1024 layer: q/k/v with RoPE, the output
     projection with its residual, gate/up with SwiGLU on the LDS-resident
-    GEMMs (16-wave K-split kernel, or full-K waves with fk = 1)."""
+    GEMMs (16-wave K-split kernel, or full-K waves with fk = 1); split = 1
+    runs the down projection as a K split with int64 atomic totals whose
+    epilogue the LayerNorm before the lm head applies."""
     om, gm, _ = build(ctx, WIDE, 8, True, std=0.03)
     rng = np.random.default_rng(9)
     ids = rng.integers(0, 512, (2, 40)).astype(np.int32)
     try:
         ctx.set_option("gemm_fk", fk)
+        ctx.set_option("down_split", split)
         got = gm.forward(ids)
     finally:
         ctx.set_option("gemm_fk", 0)
+        ctx.set_option("down_split", 0)
     for b in range(2):
         assert_rows_close(got[b], om.forward(ids[b]), 1e-4, f"forward b={b}")
     gm.free()
@@ -419,19 +423,23 @@ def test_batch_matches_oracle_per_sequence(ctx, T, groups):
     gt.free(); gd.free()
 
 
-@pytest.mark.parametrize("fk", [0, 1])
-def test_batch_mfma_rows_match_oracle(ctx, fk):
+@pytest.mark.parametrize("fk,split", [(0, 0), (1, 0), (0, 1)])
+def test_batch_mfma_rows_match_oracle(ctx, fk, split):
     """B = 20 rows of drafting use the MFMA digit GEMM (rows >= 16); the
-    100-row verify and the 320-row prefill use the LDS-resident GEMMs."""
+    100-row verify and the 320-row prefill use the LDS-resident GEMMs.
+    fk = 1: full-K-wave GEMMs; split = 1: the down projection split over
+    workgroups with int64 atomic totals, its epilogue in the LayerNorm."""
     ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 40, True, std=0.2)
     B = 20
     rng = np.random.default_rng(41)
     prompts = rng.integers(0, 256, (B, 16)).astype(np.int32)
     try:
         ctx.set_option("gemm_fk", fk)
+        ctx.set_option("down_split", split)
         got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
     finally:
         ctx.set_option("gemm_fk", 0)
+        ctx.set_option("down_split", 0)
     for b in (0, 7, 19):
         want, _ = O.generate_speculative(ot, od, prompts[b], 24, 4, 0.0, 5,
                                          seq=b)
