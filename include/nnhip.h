@@ -58,8 +58,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
 /* "graphs": 1 = replay each speculative cycle as one HIP graph (default).
  * "groups": split a batch into this many groups of sequences, each driven
  * on its own HIP stream so that their kernels overlap (0 = 1 group).
- * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids,
- * 0 = always 32x32 tiles (default; process-wide).
+ * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids
+ * (default: the prompt prefill's 8192-row down projection), 0 = always
+ * 32x32 tiles (process-wide).
  * "attn_waves": number of (key split) waves an attention launch aims for;
  * the key range of each sequence is split accordingly (default 4096;
  * process-wide).
@@ -72,7 +73,13 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * rows on (default 64; process-wide).
  * "fold_norm": 1 = a pending LayerNorm is folded into every LDS-resident
  * GEMM's prologue, 0 = only into a short batch's lm head (default 0;
- * process-wide). */
+ * process-wide).
+ * "fold_small": 1 = a short batch's pending LayerNorm is folded into an
+ * LDS-resident GEMM instead of running as its own kernel (default 0).
+ * "down_split": 1 = the down projection on the digit-plane GEMM splits K
+ * over workgroups that add exact int64 totals, the next LayerNorm applying
+ * its epilogue (default 0).  No option changes results beyond fp32
+ * rounding order. */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);
 int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out);

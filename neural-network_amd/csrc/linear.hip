@@ -1153,7 +1153,7 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
 
 // 1: allow 32x64 GEMM tiles for large grids; 0: always 32x32 (default,
 // measured faster on every decode shape).
-int g_gemm_wide = 0;
+int g_gemm_wide = 1;
 int g_gemm_fk = 0;
 
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,

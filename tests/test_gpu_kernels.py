@@ -105,8 +105,10 @@ def digits_reference(x):
     return e, hi, mid, lo
 
 
+# (2048, 512, 1024): 1024 tiles of 32 x 64, the wide-tile grid (gemm_wide)
 MFMA_SHAPES = [(16, 128, 64), (32, 512, 1536), (192, 1024, 3072),
-               (70, 4096, 1024), (8, 256, 256), (64, 2048, 512)]
+               (70, 4096, 1024), (8, 256, 256), (64, 2048, 512),
+               (2048, 512, 1024)]
 
 
 @pytest.mark.parametrize("rows,K,N", MFMA_SHAPES)
@@ -158,7 +160,7 @@ def test_mfma_linear_vs_oracle(ctx, rows, K, N):
 
 LDS_SHAPES = [(16, 128, 64), (32, 512, 1536), (192, 1024, 3072),
               (5, 256, 96), (40, 1024, 32000), (64, 512, 4096),
-              (33, 128, 160)]
+              (33, 128, 160), (2048, 512, 1024)]
 
 
 def linear_path(ctx, x, codes, scales, b, path):
