@@ -304,7 +304,8 @@ class Decoder:
         call("nnhip_generate_speculative", self.h, draft.h, ptr(prompt),
              len(prompt), max_new, lookahead, T, top_k, top_p, seed,
              int(quantized_cache), ptr(out), C.byref(st))
-        return out[:len(prompt) + max_new], st
+        # the reference always appends the first token (layer.cpp:1508-1510)
+        return out, st
 
     def generate_speculative_batch(self, draft, prompts, max_new, lookahead,
                                    T, seed, seq0=0, top_k=0, top_p=1.0,
@@ -317,7 +318,7 @@ class Decoder:
         call("nnhip_generate_speculative_batch", self.h, draft.h, B,
              ptr(prompts), P, max_new, lookahead, T, top_k, top_p, seed,
              seq0, int(quantized_cache), ptr(out), stats, C.byref(tm))
-        return out[:, :P + max_new], list(stats), tm
+        return out, list(stats), tm
 
     def generate_advanced(self, prompt, max_new, T, seed=42,
                           use_kv_cache=True, top_k=0, top_p=1.0):

@@ -285,7 +285,8 @@ def accept_step(p, q, cand, greedy, has_bonus, u_accept, u_final):
 def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,
                          top_k=0, top_p=1.0, quantized_cache=False):
     prompt = np.ascontiguousarray(prompt, np.int32)
-    out = np.zeros(len(prompt) + max_new, np.int32)
+    # the first token is always appended (layer.cpp:1508-1510)
+    out = np.zeros(len(prompt) + max(max_new, 1), np.int32)
     st = SpecStats()
     rc = lib().or_generate_speculative(target.h, draft.h, iptr(prompt),
                                        len(prompt), max_new, k, T, top_k,

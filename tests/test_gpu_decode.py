@@ -361,6 +361,32 @@ def test_toy_sampled_matches_oracle(ctx):
     gt.free(); gd.free()
 
 
+@pytest.mark.parametrize("T", [0.0, 1.0])
+def test_spec_edge_lengths_match_oracle(ctx, T):
+    """Lengths at the edges of the loop (layer.cpp:1508-1518): max_new 0 and
+    1 (the first token only: the reference always appends it), 2 and 3 with
+    k = 4 > max_new - 1 (M = min(k, remaining)), a one-token prompt, in a
+    batch of 3 and alone; streams equal to the oracle's (sampled: up to a
+    recorded tie)."""
+    ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 24, True, std=0.3)
+    rng = np.random.default_rng(25)
+    for P in (1, 5):
+        prompts = rng.integers(0, 256, (3, P)).astype(np.int32)
+        for max_new in (0, 1, 2, 3):
+            got, stats, _ = gt.generate_speculative_batch(gd, prompts, max_new,
+                                                          4, T, 11)
+            assert got.shape == (3, P + max(max_new, 1))
+            for b in range(3):
+                want, ost = O.generate_speculative(ot, od, prompts[b], max_new,
+                                                   4, T, 11, seq=b)
+                if not np.array_equal(got[b], want):
+                    assert T > 0 and (ost.ties > 0 or stats[b].ties > 0)
+            one, _ = gt.generate_speculative(gd, prompts[0], max_new, 4, T,
+                                             seed=11)
+            np.testing.assert_array_equal(one, got[0])
+    gt.free(); gd.free()
+
+
 @pytest.mark.parametrize("top_k,top_p", [(4, 0.9), (0, 0.8), (6, 1.0)])
 def test_spec_top_k_top_p_matches_oracle(ctx, top_k, top_p):
     """transformer_test.cpp:340-345 runs generate_speculative with top_k 4,
