@@ -69,6 +69,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * process-wide).
  * "attn_w4": 1 = attention rows of 4+ queries run in workgroups of 4 key
  * splits (two per CU) instead of 8 (default 1; process-wide).
+ * "kv_stream": fp32 KV rows read with non-temporal loads: 0 never, 1 when
+ * one attention launch reads more rows than the L2 caches hold (default),
+ * 2 always (process-wide).
  * "lds_min_rows": the LDS-resident GEMM serves projections from this many
  * rows on (default 64; process-wide).
  * "fold_norm": 1 = a pending LayerNorm is folded into every LDS-resident

@@ -247,6 +247,7 @@ __global__ __launch_bounds__(256) void rope_kv_q8_kernel(
 // LDS for the in-workgroup merge.
 // ---------------------------------------------------------------------------
 constexpr int kChunk = 32;
+constexpr double kL2StreamBytes = 32.0 * 1024 * 1024;   // 8 XCDs x 4 MB of L2
 constexpr int kMergedWaves = 8;    // key splits of a merged workgroup
 constexpr int kMergedWaves4 = 4;   // ... for 4+ queries (option attn_w4)
 constexpr int kMergedChunks = 4;   // at most this many chunks per split
@@ -275,6 +276,34 @@ __device__ __forceinline__ float groups_sum(float v) {
   v += dppf<0x128>(v);
   v += __shfl_xor(v, 16, kWave);
   return v + __shfl_xor(v, 32, kWave);
+}
+
+// KV-cache rows of a launch whose rows exceed the L2 (the verify step's)
+// are streamed: non-temporal loads, so that they do not evict the weights
+// and activations held in L2 between launches.  Smaller caches (the
+// draft's, re-read by each draft step) are loaded normally and stay in L2.
+typedef float nnhip_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream4(const float *p) {
+  const nnhip_f4 v = __builtin_nontemporal_load(reinterpret_cast<const nnhip_f4 *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+template <int DL>
+__device__ __forceinline__ void load_lane_dims_stream(const float *p, int sub,
+                                                      float (&x)[8]) {
+  if constexpr (DL == 8) {
+    const float4 a = ld_stream4(p + 4 * sub);
+    const float4 c = ld_stream4(p + 32 + 4 * sub);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+  } else if constexpr (DL == 4) {
+    const float4 a = ld_stream4(p + 4 * sub);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+#pragma unroll
+    for (int i = 4; i < 8; ++i) x[i] = 0.f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = i < DL ? __builtin_nontemporal_load(p + DL * sub + i) : 0.f;
+  }
 }
 
 // Dims of a lane in the score phase (DL = D/8 of them): for DL = 8 the two
@@ -332,7 +361,7 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
     const float *__restrict__ q, KvSrc kv, int S, int H, int Hkv, int cap,
     const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
-    float qscale, float *__restrict__ part, float *__restrict__ out) {
+    float qscale, float *__restrict__ part, float *__restrict__ out, int nt) {
   constexpr int D = DL * 8;
   constexpr int NQ4 = D / 4, KPI = kWave / NQ4;   // PV: key rows per wave op
   constexpr int TPV = (kChunk + KPI - 1) / KPI;   // PV keys per lane
@@ -405,7 +434,8 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
         load_lane_codes<DL>(kb + (int64_t)j * D, sub, ck.kc[t]);
         ck.ks[t] = ksb[j];
       } else {
-        load_lane_dims<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+        if (nt) load_lane_dims_stream<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+        else load_lane_dims<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
       }
     }
   };
@@ -435,9 +465,10 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
 #pragma unroll
         for (int x = 0; x < 8; ++x) kr[t][x] = ck.kr[t][x];
 #pragma unroll
-      for (int t = 0; t < TPV; ++t)
-        vv[t] = *reinterpret_cast<const float4 *>(
-            vb + (int64_t)min(c0 + r + KPI * t, kend - 1) * D + dq * 4);
+      for (int t = 0; t < TPV; ++t) {
+        const float *pv = vb + (int64_t)min(c0 + r + KPI * t, kend - 1) * D + dq * 4;
+        vv[t] = nt ? ld_stream4(pv) : *reinterpret_cast<const float4 *>(pv);
+      }
     }
     // scores of this lane's query for keys c0 + g + 8t
     float sc[4], cm = -INFINITY;
@@ -897,6 +928,7 @@ void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
 }
 
 int g_attn_waves = 4096;
+int g_kv_stream = 1;
 int g_attn_w4 = 1;
 
 // Splits of the key range: about g_attn_waves waves over the whole launch
@@ -942,6 +974,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   const int nqb = (S + kMaxQ - 1) / kMaxQ;
   const int sq = S < kMaxQ ? S : kMaxQ;
   const float qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+  // stream the fp32 rows when the launch reads more than the L2s hold
+  const double kv_bytes = 2.0 * B * Hkv * (double)std::min(max_keys, cap) * D *
+                          (kv.q8 ? 1.0 : 4.0);
+  const int nt = !kv.q8 && (g_kv_stream == 2 ||
+                            (g_kv_stream == 1 && kv_bytes > kL2StreamBytes));
   if (attention_merged(D, max_keys)) {
     // one workgroup per (head, sequence, query block); its waves are the key
     // splits, merged in LDS, and the context rows are written directly
@@ -952,11 +989,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   if (kv.q8)                                                                  \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, W, true>), grid, dim3(kWave * W),  \
                        0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
-                       kps, qscale, nullptr, out);                              \
+                       kps, qscale, nullptr, out, nt);                          \
   else                                                                        \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, W, false>), grid, dim3(kWave * W), \
                        0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
-                       kps, qscale, nullptr, out)
+                       kps, qscale, nullptr, out, nt)
 #define NNHIP_ATTN_D(SQP, W)                                                  \
   if (D == 32) { NNHIP_ATTN(SQP, 4, W); } else { NNHIP_ATTN(SQP, 8, W); }
     // many-query rows hold many registers (one workgroup of 8 waves per CU):
@@ -980,11 +1017,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   if (kv.q8)                                                                  \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, true>), grid, dim3(kWave), 0,  \
                        st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
-                       nqb, kps, qscale, part, nullptr);                      \
+                       nqb, kps, qscale, part, nullptr, nt);                  \
   else                                                                        \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, false>), grid, dim3(kWave), 0, \
                        st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
-                       nqb, kps, qscale, part, nullptr)
+                       nqb, kps, qscale, part, nullptr, nt)
 #define NNHIP_ATTN_D(SQP)                                                     \
   switch (D / 8) {                                                            \
     case 1: { NNHIP_ATTN(SQP, 1); } break;                                    \
