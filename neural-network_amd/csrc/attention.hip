@@ -11,6 +11,7 @@
 // length and truncation (KVCache::truncate, layer.cpp:67-149) is a length
 // update.  Each sequence carries its own length, so a batch is ragged.
 #include "nnhip_internal.hpp"
+#include "rows.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -730,137 +731,53 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
   store_row_digits<256>(srow, d, mx, row, limbs, mpad, rexp, sred);
 }
 
-// LayerNorm as layernorm_kernel, one wave per row for d % 16 == 0: lane l
-// holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, with
-// their gamma and beta requested together with the row; the row sums and the
-// max are DPP wave reductions, and the digits of y (for the next MFMA GEMM)
-// are written from the same registers.
+// LayerNorm as layernorm_kernel, one wave per row for d % 16 == 0: the row
+// is held in quads (rows.hpp: lane l has entries 256 i + 4 l .. + 3, i < NQ)
+// with its gamma and beta, all requested at once; the row sums and the max
+// are DPP wave reductions, and the digits of y (for the next MFMA GEMM) are
+// written from the same registers.
 // EPI: the row is first formed from a limb GEMM's int64 totals by the
 // deferred kEpiResid epilogue (LinEpiArgs), whose totals are then zeroed.
-template <int PPL, bool EPI>
+template <int NQ, bool EPI>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
     const float *__restrict__ bt, float *__restrict__ y,
     int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp,
     LinEpiArgs ea) {
 #pragma clang fp contract(off)
-  typedef int v4i __attribute__((ext_vector_type(4)));
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
-  const float *xr = hin + (int64_t)row * d;
-  const int np = d / 16;
-  // pieces past the row re-read the last piece and are masked
-  float v[PPL][16], gv[PPL][16], bv[PPL][16];
+  // the row, gamma and beta in quads (rows.hpp), all requested at once
+  float v[NQ][4], gv[NQ][4], bv[NQ][4];
+  load_quads<NQ>(g, d, lane, gv);
+  load_quads<NQ>(bt, d, lane, bv);
   if constexpr (EPI) {
     const int te = ea.texp[row];
     long long *tr = ea.tot + (int64_t)row * d;
     const float *rr = ea.resid + (int64_t)row * ea.ldr;
+    float sc[NQ][4], bi[NQ][4], rs[NQ][4];
+    load_quads<NQ>(ea.scale, d, lane, sc);
+    load_quads<NQ>(ea.bias, d, lane, bi);
+    load_quads<NQ>(rr, d, lane, rs);
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-      const int pc = min(lane + 64 * j, np - 1);
-      long long t[16];
-      float sc[16], bi[16], rs[16];
+    for (int i = 0; i < NQ; ++i) {
+      const int k = quad_at(i, lane, d);
+      const longlong2 t0 = *reinterpret_cast<const longlong2 *>(tr + k);
+      const longlong2 t1 = *reinterpret_cast<const longlong2 *>(tr + k + 2);
+      const long long t[4] = {t0.x, t0.y, t1.x, t1.y};
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const longlong2 tt = *reinterpret_cast<const longlong2 *>(tr + 16 * pc + 2 * q);
-        t[2 * q] = tt.x; t[2 * q + 1] = tt.y;
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 a = *reinterpret_cast<const float4 *>(ea.scale + 16 * pc + 4 * q);
-        const float4 c = *reinterpret_cast<const float4 *>(ea.bias + 16 * pc + 4 * q);
-        const float4 r = *reinterpret_cast<const float4 *>(rr + 16 * pc + 4 * q);
-        const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
-        const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
-        sc[4 * q] = a.x; sc[4 * q + 1] = a.y; sc[4 * q + 2] = a.z; sc[4 * q + 3] = a.w;
-        bi[4 * q] = c.x; bi[4 * q + 1] = c.y; bi[4 * q + 2] = c.z; bi[4 * q + 3] = c.w;
-        rs[4 * q] = r.x; rs[4 * q + 1] = r.y; rs[4 * q + 2] = r.z; rs[4 * q + 3] = r.w;
-        gv[j][4 * q] = gg.x; gv[j][4 * q + 1] = gg.y; gv[j][4 * q + 2] = gg.z; gv[j][4 * q + 3] = gg.w;
-        bv[j][4 * q] = bb.x; bv[j][4 * q + 1] = bb.y; bv[j][4 * q + 2] = bb.z; bv[j][4 * q + 3] = bb.w;
-      }
-#pragma unroll
-      for (int q = 0; q < 16; ++q)
-        v[j][q] = rs[q] + __fadd_rn(__fmul_rn(ldexpf((float)t[q], -te), sc[q]), bi[q]);
-      if (lane + 64 * j < np) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          *reinterpret_cast<longlong2 *>(tr + 16 * pc + 2 * q) = make_longlong2(0, 0);
+      for (int j = 0; j < 4; ++j)
+        v[i][j] = rs[i][j] + __fadd_rn(__fmul_rn(ldexpf((float)t[j], -te), sc[i][j]), bi[i][j]);
+      if (quad_ok(i, lane, d)) {
+        *reinterpret_cast<longlong2 *>(tr + k) = make_longlong2(0, 0);
+        *reinterpret_cast<longlong2 *>(tr + k + 2) = make_longlong2(0, 0);
       }
     }
   } else {
-#pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int pc = min(lane + 64 * j, np - 1);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 f = *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q);
-      const float4 gg = *reinterpret_cast<const float4 *>(g + 16 * pc + 4 * q);
-      const float4 bb = *reinterpret_cast<const float4 *>(bt + 16 * pc + 4 * q);
-      v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
-      gv[j][4 * q] = gg.x; gv[j][4 * q + 1] = gg.y; gv[j][4 * q + 2] = gg.z; gv[j][4 * q + 3] = gg.w;
-      bv[j][4 * q] = bb.x; bv[j][4 * q + 1] = bb.y; bv[j][4 * q + 2] = bb.z; bv[j][4 * q + 3] = bb.w;
-    }
+    load_quads<NQ>(hin + (int64_t)row * d, d, lane, v);
   }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j)
-    if (lane + 64 * j < np) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) s += v[j][q];
-    }
-  s = wave_sum_all(s);
-  const float N = (float)d;
-  const float mean = s / N;
-  float sq = 0.f;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j)
-    if (lane + 64 * j < np) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) { const float df = v[j][q] - mean; sq += df * df; }
-    }
-  sq = wave_sum_all(sq);
-  const float sd = sqrtf(sq / N + 1e-5f);
-  float mx = 0.f;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int pc = lane + 64 * j;
-    if (pc >= np) break;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float *w = v[j] + 4 * q;
-      const float *gg = gv[j] + 4 * q, *bb = bv[j] + 4 * q;
-      w[0] = (w[0] - mean) / sd * gg[0] + bb[0];
-      w[1] = (w[1] - mean) / sd * gg[1] + bb[1];
-      w[2] = (w[2] - mean) / sd * gg[2] + bb[2];
-      w[3] = (w[3] - mean) / sd * gg[3] + bb[3];
-      *reinterpret_cast<float4 *>(y + (int64_t)row * d + 16 * pc + 4 * q) =
-          make_float4(w[0], w[1], w[2], w[3]);
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])),
-                           fmaxf(fabsf(w[2]), fabsf(w[3]))));
-    }
-  }
-  if (!limbs) return;
-  mx = wave_max_all(mx);
-  const int e = digit_exponent(mx);
-  if (lane == 0) rexp[row] = e;
-  const int64_t plane = (int64_t)mpad * d;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int pc = lane + 64 * j;
-    if (pc >= np) break;
-    v4i hi, mid, lo;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int3 t = digits4(v[j] + 4 * q, e);
-      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
-    }
-    const int64_t off = mfma_operand_offset(row, 16 * pc, d);
-    *reinterpret_cast<v4i *>(limbs + off) = hi;
-    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
-    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
-  }
+  ln_row_finish<NQ>(v, gv, bv, d, row, y, limbs, mpad, rexp, lane);
 }
 
 __global__ void add_scalar_kernel(int32_t *p, int n, int v) {
@@ -1058,8 +975,7 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                          ea->resid && ea->ldr % 4 == 0),
                 kErrArg, "layernorm: GEMM epilogue arguments missing");
   const LinEpiArgs ez = epi ? *ea : LinEpiArgs{};
-  if (d % 16 == 0) {
-    const int np = d / 16;
+  if (d % 16 == 0 && d <= 4096) {
     const dim3 grid((rows + 3) / 4);
 #define NNHIP_LN(P)                                                           \
   if (epi)                                                                    \
@@ -1068,9 +984,9 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
   else                                                                        \
     hipLaunchKernelGGL((layernorm_rows_kernel<P, false>), grid, dim3(256), 0, \
                        st, h, d, rows, g, b, y, limbs, mpad, rexp, ez)
-    if (np <= 64) { NNHIP_LN(1); }
-    else if (np <= 128) { NNHIP_LN(2); }
-    else { NNHIP_LN(4); }
+    if (d <= 1024) { NNHIP_LN(4); }
+    else if (d <= 2048) { NNHIP_LN(8); }
+    else { NNHIP_LN(16); }
 #undef NNHIP_LN
   } else {
     hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, st, h, d, g,

@@ -16,6 +16,7 @@
 //    fp32.  Result: an fp32 product whose only error is the 2^-23 (relative
 //    to the row maximum) digit truncation of x and one final rounding.
 #include "nnhip_internal.hpp"
+#include "rows.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -152,55 +153,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 
 // Digits of activation rows for the MFMA GEMM: X = rint(x * 2^e) with
 // e = 22 - exponent(max|x|) per row, split into balanced base-256 digits
-// (hi, mid, lo), written in the MFMA operand layout.  One wave per row; lane
-// l holds the 16-element pieces l, l + 64, ... (PPL of them) in registers, so
-// the row is read once and the max needs no workgroup barrier.
-template <int PPL>
+// (hi, mid, lo), written in the MFMA operand layout.  One wave per row held
+// in quads (rows.hpp: lane l has entries 256 i + 4 l .. + 3, i < NQ) in
+// registers, so the row is read once, every load is a contiguous 1 KB per
+// wave, and the max needs no workgroup barrier.
+template <int NQ>
 __global__ __launch_bounds__(256) void act_quant_kernel(
     const float *__restrict__ x, int64_t ldx, int K, int rows,
     int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (m >= rows) return;
-  const float *xr = x + m * ldx;
-  const int np = K / 16;
-  // pieces past the row re-read the last piece and are masked
-  float v[PPL][16];
-#pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int pc = min(lane + 64 * j, np - 1);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 f = *reinterpret_cast<const float4 *>(xr + 16 * pc + 4 * q);
-      v[j][4 * q] = f.x; v[j][4 * q + 1] = f.y; v[j][4 * q + 2] = f.z; v[j][4 * q + 3] = f.w;
-    }
-  }
-  float mx = 0.f;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j)
-    if (lane + 64 * j < np) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) mx = fmaxf(mx, fabsf(v[j][q]));
-    }
-  mx = wave_max_all(mx);
-  const int e = digit_exponent(mx);
-  if (lane == 0) rexp[m] = e;
-  const int64_t plane = (int64_t)mpad * K;
-#pragma unroll
-  for (int j = 0; j < PPL; ++j) {
-    const int pc = lane + 64 * j;
-    if (pc >= np) break;
-    v4i hi, mid, lo;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int3 t = digits4(v[j] + 4 * q, e);
-      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
-    }
-    const int64_t off = mfma_operand_offset(m, 16 * pc, K);
-    *reinterpret_cast<v4i *>(limbs + off) = hi;
-    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
-    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
-  }
+  float v[NQ][4];
+  load_quads<NQ>(x + m * ldx, K, lane, v);
+  aq_row_finish<NQ>(v, K, m, limbs, mpad, rexp, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1187,16 +1153,15 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   NNHIP_REQUIRE(K % 128 == 0 && ldx % 4 == 0 && rows <= mpad, kErrArg,
                 "act_quant: K % 128 and ldx % 4 must be 0");
   NNHIP_REQUIRE(K <= 4096, kErrArg, "act_quant: K must be <= 4096");
-  const int np = K / 16;
   const dim3 grid((rows + 3) / 4);
-  if (np <= 64)
-    hipLaunchKernelGGL(act_quant_kernel<1>, grid, dim3(256), 0, st, x, ldx, K,
+  if (K <= 1024)
+    hipLaunchKernelGGL(act_quant_kernel<4>, grid, dim3(256), 0, st, x, ldx, K,
                        rows, limbs, mpad, rexp);
-  else if (np <= 128)
-    hipLaunchKernelGGL(act_quant_kernel<2>, grid, dim3(256), 0, st, x, ldx, K,
+  else if (K <= 2048)
+    hipLaunchKernelGGL(act_quant_kernel<8>, grid, dim3(256), 0, st, x, ldx, K,
                        rows, limbs, mpad, rexp);
   else
-    hipLaunchKernelGGL(act_quant_kernel<4>, grid, dim3(256), 0, st, x, ldx, K,
+    hipLaunchKernelGGL(act_quant_kernel<16>, grid, dim3(256), 0, st, x, ldx, K,
                        rows, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
 }

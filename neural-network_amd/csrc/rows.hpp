@@ -1,0 +1,121 @@
+// Row-wise LayerNorm and activation-digit arithmetic of the LayerNorm and
+// act_quant kernels: one wave per row, the row held in "quads".
+#pragma once
+
+#include "nnhip_internal.hpp"
+
+namespace nnhip {
+
+// A row held by a wave in "quads": lane l has the 4 consecutive entries
+// 256 i + 4 l .. + 3 for i < NQ (a quad is valid while 256 i + 4 l < d), so
+// every wave-wide load or store of a quad index i is one contiguous 1 KB.
+__device__ __forceinline__ bool quad_ok(int i, int lane, int d) {
+  return 256 * i + 4 * lane < d;
+}
+// start of quad i of a lane (the last quad of the row for invalid ones, so
+// that loads stay unconditional)
+__device__ __forceinline__ int quad_at(int i, int lane, int d) {
+  return min(256 * i + 4 * lane, d - 4);
+}
+
+// LayerNorm of one row (layer.cpp:242-261) held by a wave in quads with
+// their gamma / beta: mean = sum / N, var = sum((x - mean)^2) / N,
+// (x - mean) / sqrt(var + 1e-5) * gamma + beta; the sums are DPP wave
+// reductions.  y gets the normalised row; with limbs its digits for the next
+// MFMA GEMM (row exponent from the row's max, as aq_row_finish).
+template <int NQ>
+__device__ __forceinline__ void ln_row_finish(
+    float (&v)[NQ][4], const float (&gv)[NQ][4], const float (&bv)[NQ][4],
+    int d, int row, float *__restrict__ y, int8_t *__restrict__ limbs,
+    int mpad, int *__restrict__ rexp, int lane) {
+#pragma clang fp contract(off)
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+    if (quad_ok(i, lane, d)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += v[i][j];
+    }
+  s = wave_sum_all(s);
+  const float N = (float)d;
+  const float mean = s / N;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+    if (quad_ok(i, lane, d)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { const float df = v[i][j] - mean; sq += df * df; }
+    }
+  sq = wave_sum_all(sq);
+  const float sd = sqrtf(sq / N + 1e-5f);
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    if (!quad_ok(i, lane, d)) break;
+    float *w = v[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (w[j] - mean) / sd * gv[i][j] + bv[i][j];
+    *reinterpret_cast<float4 *>(y + (int64_t)row * d + 256 * i + 4 * lane) =
+        make_float4(w[0], w[1], w[2], w[3]);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(w[0]), fabsf(w[1])),
+                         fmaxf(fabsf(w[2]), fabsf(w[3]))));
+  }
+  if (!limbs) return;
+  mx = wave_max_all(mx);
+  const int e = digit_exponent(mx);
+  if (lane == 0) rexp[row] = e;
+  const int64_t plane = (int64_t)mpad * d;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    if (!quad_ok(i, lane, d)) break;
+    const int3 t = digits4(v[i], e);
+    // the quad's 4 bytes are adjacent in the operand layout
+    const int64_t off = mfma_operand_offset(row, 256 * i + 4 * lane, d);
+    *reinterpret_cast<int *>(limbs + off) = t.x;
+    *reinterpret_cast<int *>(limbs + plane + off) = t.y;
+    *reinterpret_cast<int *>(limbs + 2 * plane + off) = t.z;
+  }
+}
+
+// Digits of one row of K entries held by a wave in quads: X = rint(x * 2^e)
+// with e = 22 - exponent(max|x|), split into balanced base-256 digits
+// (hi, mid, lo) in the MFMA operand layout, and the row exponent.
+template <int NQ>
+__device__ __forceinline__ void aq_row_finish(const float (&v)[NQ][4], int K,
+                                              int m, int8_t *__restrict__ limbs,
+                                              int mpad, int *__restrict__ rexp,
+                                              int lane) {
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i)
+    if (quad_ok(i, lane, K)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[i][j]));
+    }
+  mx = wave_max_all(mx);
+  const int e = digit_exponent(mx);
+  if (lane == 0) rexp[m] = e;
+  const int64_t plane = (int64_t)mpad * K;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    if (!quad_ok(i, lane, K)) break;
+    const int3 t = digits4(v[i], e);
+    const int64_t off = mfma_operand_offset(m, 256 * i + 4 * lane, K);
+    *reinterpret_cast<int *>(limbs + off) = t.x;
+    *reinterpret_cast<int *>(limbs + plane + off) = t.y;
+    *reinterpret_cast<int *>(limbs + 2 * plane + off) = t.z;
+  }
+}
+
+// quads of a row with ordinary loads
+template <int NQ>
+__device__ __forceinline__ void load_quads(const float *__restrict__ xr, int d,
+                                           int lane, float (&v)[NQ][4]) {
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const float4 f = *reinterpret_cast<const float4 *>(xr + quad_at(i, lane, d));
+    v[i][0] = f.x; v[i][1] = f.y; v[i][2] = f.z; v[i][3] = f.w;
+  }
+}
+
+}  // namespace nnhip
