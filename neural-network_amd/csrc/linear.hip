@@ -1132,17 +1132,26 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
   NNHIP_REQUIRE(!(ra && ra->kq), kErrArg,
                 "gemv: no int8 KV append in this epilogue (use rope_kv_q8)");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
-  for (int r0 = 0; r0 < rows; r0 += 4) {
-    int rr = rows - r0 < 4 ? rows - r0 : 4;
+  // up to 8 rows per pass, so that a verify step's k+1 rows (k <= 7) read
+  // the weights once
+  for (int r0 = 0; r0 < rows; r0 += 8) {
+    int rr = rows - r0 < 8 ? rows - r0 : 8;
     const float *xp = x + r0 * ldx;
     const float *rp = resid ? resid + r0 * ldr : nullptr;
     float *yp = y ? y + r0 * ldy : nullptr;
+#define NNHIP_GEMV(R) \
+    gemv_dispatch<R>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz)
     switch (rr) {
-      case 1: gemv_dispatch<1>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
-      case 2: gemv_dispatch<2>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
-      case 3: gemv_dispatch<3>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
-      default: gemv_dispatch<4>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz); break;
+      case 1: NNHIP_GEMV(1); break;
+      case 2: NNHIP_GEMV(2); break;
+      case 3: NNHIP_GEMV(3); break;
+      case 4: NNHIP_GEMV(4); break;
+      case 5: NNHIP_GEMV(5); break;
+      case 6: NNHIP_GEMV(6); break;
+      case 7: NNHIP_GEMV(7); break;
+      default: NNHIP_GEMV(8); break;
     }
+#undef NNHIP_GEMV
   }
   NNHIP_CHECK(hipGetLastError());
 }
