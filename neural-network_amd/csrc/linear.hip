@@ -46,13 +46,50 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV: y[r][n] = epi( sum_k x[r][k] * w[n][k] ), r < R (<= 4).
+// GEMV: y[r][n] = epi( sum_k x[r][k] * w[n][k] ), r < R (<= 8).
 // A workgroup of 4 waves covers NC columns for each of CG = 4/nks column
 // sets; wave (c, s) reduces K-slice s of column set c.  Each lane owns
-// 4-element groups of K at stride 256, keeps its slice of x for all R rows in
-// registers, and loops over the columns 4 at a time.
+// 4-element groups of K at stride 256 and keeps its slice of x for all R rows
+// in registers; the int8 weights of all NC columns are requested together
+// with x.  The NC x R partial sums of a lane are then reduced over the wave
+// by a butterfly reduce-scatter (each exchange step halves the values a lane
+// carries), which leaves one (column, row) total per lane.
 // ---------------------------------------------------------------------------
 constexpr int kGemvNC = 8;  // columns per column set
+
+// Butterfly reduce-scatter of NP (a power of two <= 64) values per lane over
+// the 64 lanes of a wave: afterwards v[0] of lane l is the wave's total of
+// slot gemv_slot<NP>(l).
+template <int NP>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[NP]) {
+  const int lane = threadIdx.x & 63;
+  int cnt = NP;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    if (cnt > 1) {
+      const int half = cnt / 2;
+      const bool up = (lane & o) != 0;
+#pragma unroll
+      for (int i = 0; i < NP / 2; ++i) {
+        if (i >= half) break;
+        const float send = up ? v[i] : v[i + half];
+        const float keep = up ? v[i + half] : v[i];
+        v[i] = keep + __shfl_xor(send, o, 64);
+      }
+      cnt = half;
+    } else {
+      v[0] += __shfl_xor(v[0], o, 64);
+    }
+  }
+}
+template <int NP>
+__device__ __forceinline__ int gemv_slot(int lane) {
+  int slot = 0, cnt = NP;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+    if (cnt > 1) { cnt /= 2; if (lane & o) slot += cnt; }
+  return slot;
+}
 
 template <int R, bool Q8>
 __global__ __launch_bounds__(256) void gemv_kernel(
@@ -62,6 +99,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
     int64_t ldy, int epi, int nks, int64_t row0, RopeArgs ra) {
   constexpr int kMaxIt = 4;  // slice <= 1024 elements
+  constexpr int P = kGemvNC * R;
+  constexpr int NP = P <= 8 ? 8 : P <= 16 ? 16 : P <= 32 ? 32 : 64;
   __shared__ float red[4][kGemvNC][R];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -84,45 +123,54 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       xr[r][it][0] = v.x; xr[r][it][1] = v.y;
       xr[r][it][2] = v.z; xr[r][it][3] = v.w;
     }
+  // int8 weights of all the wave's columns (zero past N or the slice)
+  int wpk[Q8 ? kGemvNC : 1][kMaxIt];
+  if constexpr (Q8) {
+#pragma unroll
+    for (int c = 0; c < kGemvNC; ++c)
+#pragma unroll
+      for (int it = 0; it < kMaxIt; ++it) {
+        const int k = k0 + it * 256 + lane * 4;
+        const int64_t n = ncol0 + c;
+        const bool ok = it < iters && k < k0 + slen && k < K && n < N;
+        wpk[c][it] = ok ? *reinterpret_cast<const int *>(wq + n * K + k) : 0;
+      }
+  }
 
-  for (int c0 = 0; c0 < kGemvNC; c0 += 4) {
-    float acc[4][R];
+  float acc[NP];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+  for (int i = 0; i < NP; ++i) acc[i] = 0.f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[c][r] = 0.f;
+  for (int it = 0; it < kMaxIt; ++it) {
+    int k = k0 + it * 256 + lane * 4;
+    if (!(it < iters && k < k0 + slen && k < K)) continue;
 #pragma unroll
-    for (int it = 0; it < kMaxIt; ++it) {
-      int k = k0 + it * 256 + lane * 4;
-      if (!(it < iters && k < k0 + slen && k < K)) continue;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        int64_t n = ncol0 + c0 + c;
+    for (int c = 0; c < kGemvNC; ++c) {
+      float wv[4];
+      if constexpr (Q8) {
+        const int pk = wpk[c][it];
+        wv[0] = (float)(int8_t)(pk & 0xff);
+        wv[1] = (float)(int8_t)((pk >> 8) & 0xff);
+        wv[2] = (float)(int8_t)((pk >> 16) & 0xff);
+        wv[3] = (float)(int8_t)((pk >> 24) & 0xff);
+      } else {
+        const int64_t n = ncol0 + c;
         if (n >= N) continue;
-        float wv[4];
-        if (Q8) {
-          int pk = *reinterpret_cast<const int *>(wq + n * K + k);
-          wv[0] = (float)(int8_t)(pk & 0xff);
-          wv[1] = (float)(int8_t)((pk >> 8) & 0xff);
-          wv[2] = (float)(int8_t)((pk >> 16) & 0xff);
-          wv[3] = (float)(int8_t)((pk >> 24) & 0xff);
-        } else {
-          float4 f = *reinterpret_cast<const float4 *>(wf + n * K + k);
-          wv[0] = f.x; wv[1] = f.y; wv[2] = f.z; wv[3] = f.w;
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[c][r] += xr[r][it][e] * wv[e];
+        float4 f = *reinterpret_cast<const float4 *>(wf + n * K + k);
+        wv[0] = f.x; wv[1] = f.y; wv[2] = f.z; wv[3] = f.w;
       }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[c * R + r] += xr[r][it][e] * wv[e];
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float t = wave_sum(acc[c][r]);
-        if (lane == 0) red[w][c0 + c][r] = t;
-      }
+  }
+  wave_reduce_scatter<NP>(acc);
+  {
+    const int slot = gemv_slot<NP>(lane);
+    // lanes sharing a slot (NP < 64) hold the same total: the first writes
+    if (slot < P && (lane & (64 / NP - 1)) == 0)
+      red[w][slot / R][slot % R] = acc[0];
   }
   __syncthreads();
   // combine the nks slices and apply the epilogue
