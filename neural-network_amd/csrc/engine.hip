@@ -380,6 +380,16 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
   }
   NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                 "linear_in: tile statistics need the LDS-resident GEMM");
+  if (pn && !pn->ea.tot && !use_limbs(ln, rows) && ln.K <= 1024 &&
+      ln.K % 4 == 0 && pn->ldh % 4 == 0 && (!pn->out || pn->ldo % 4 == 0)) {
+    // short rows on the GEMV: the LayerNorm is its prologue
+    GemvLn lf;
+    lf.g = pn->g; lf.b = pn->b; lf.out = pn->out; lf.ldo = pn->ldo;
+    launch_gemv(st, pn->h, pn->ldh, rows, ln.K, ln.N, ln.quant ? ln.q.p : nullptr,
+                ln.quant ? nullptr : ln.w.p, ln.s.p, ln.b.p, resid, ldr, y, ldy,
+                epi, ra, &lf);
+    return;
+  }
   if (pn) {
     // the normalisation as its own kernel, then the linear over its output
     NNHIP_REQUIRE(pn->out && pn->ldh == ln.K && pn->ldo == ln.K, kErrArg,
@@ -537,6 +547,18 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       if (last_only) { pn.h = ws.h.p + (int64_t)(S - 1) * d; pn.ldh = (int64_t)S * d; }
       linear_in(g, lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, ldl,
                 kEpiBias, nullptr, ts);
+    } else if (!norm2.ea.tot && !use_limbs(lm, rows) && d <= 1024 &&
+               d % 4 == 0) {
+      // short rows on the GEMV: the last norm2 is its prologue
+      NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
+                    "forward: tile statistics need the LDS-resident lm head");
+      GemvLn lf;
+      lf.g = norm2.g; lf.b = norm2.b;
+      const float *hx = last_only ? ws.h.p + (int64_t)(S - 1) * d : ws.h.p;
+      const int64_t ldh = last_only ? (int64_t)S * d : d;
+      launch_gemv(st, hx, ldh, rows, d, V, lm.quant ? lm.q.p : nullptr,
+                  lm.quant ? nullptr : lm.w.p, lm.s.p, lm.b.p, nullptr, 0,
+                  logits, ldl, kEpiBias, nullptr, &lf);
     } else {
       NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                     "forward: tile statistics need the LDS-resident lm head");

@@ -91,13 +91,17 @@ __device__ __forceinline__ int gemv_slot(int lane) {
   return slot;
 }
 
+// lf.g set: the rows x are first normalised, LayerNorm (layer.cpp:242-261)
+// with the arithmetic of layernorm_rows_kernel (row sums in quads, DPP wave
+// reductions), so the normalised entries are the ones that kernel writes;
+// workgroup 0 also writes them to lf.out when set.
 template <int R, bool Q8>
 __global__ __launch_bounds__(256) void gemv_kernel(
     const float *__restrict__ x, int64_t ldx, int K, int N,
     const int8_t *__restrict__ wq, const float *__restrict__ wf,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int nks, int64_t row0, RopeArgs ra) {
+    int64_t ldy, int epi, int nks, int64_t row0, RopeArgs ra, GemvLn lf) {
   constexpr int kMaxIt = 4;  // slice <= 1024 elements
   constexpr int P = kGemvNC * R;
   constexpr int NP = P <= 8 ? 8 : P <= 16 ? 16 : P <= 32 ? 32 : 64;
@@ -137,6 +141,53 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       }
   }
 
+  if (lf.g) {
+#pragma clang fp contract(off)
+    // each row's mean and deviation over all K, then the wave's slice
+    // normalised in place
+    float mean[R], sd[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float q[4][4];
+      load_quads<4>(x + r * ldx, K, lane, q);
+      float sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (quad_ok(i, lane, K)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sm += q[i][j];
+        }
+      sm = wave_sum_all(sm);
+      const float Nf = (float)K;
+      mean[r] = sm / Nf;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (quad_ok(i, lane, K)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) { const float df = q[i][j] - mean[r]; sq += df * df; }
+        }
+      sq = wave_sum_all(sq);
+      sd[r] = sqrtf(sq / Nf + 1e-5f);
+    }
+#pragma unroll
+    for (int it = 0; it < kMaxIt; ++it) {
+      const int k = k0 + it * 256 + lane * 4;
+      if (!(it < iters && k < k0 + slen && k < K)) continue;
+      const float4 gg = *reinterpret_cast<const float4 *>(lf.g + k);
+      const float4 bb = *reinterpret_cast<const float4 *>(lf.b + k);
+      const float ga[4] = {gg.x, gg.y, gg.z, gg.w}, ba[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xr[r][it][e] = (xr[r][it][e] - mean[r]) / sd[r] * ga[e] + ba[e];
+        if (lf.out && blockIdx.x == 0 && cset == 0)
+          *reinterpret_cast<float4 *>(lf.out + r * lf.ldo + k) =
+              make_float4(xr[r][it][0], xr[r][it][1], xr[r][it][2], xr[r][it][3]);
+      }
+    }
+  }
   float acc[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) acc[i] = 0.f;
@@ -1149,18 +1200,18 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
                    const int8_t *wq, const float *wf, const float *scale,
                    const float *bias, const float *resid, int64_t ldr,
                    float *y, int64_t ldy, int epi, int64_t row0,
-                   const RopeArgs &ra) {
+                   const RopeArgs &ra, const GemvLn &lf) {
   int nks = K >= 1024 ? 4 : (K >= 512 ? 2 : 1);
   int cols = (4 / nks) * kGemvNC;
   dim3 grid((N + cols - 1) / cols);
   if (wq)
     hipLaunchKernelGGL((gemv_kernel<R, true>), grid, dim3(256), 0, st, x, ldx,
                        K, N, wq, wf, scale, bias, resid, ldr, y, ldy, epi,
-                       nks, row0, ra);
+                       nks, row0, ra, lf);
   else
     hipLaunchKernelGGL((gemv_kernel<R, false>), grid, dim3(256), 0, st, x,
                        ldx, K, N, wq, wf, scale, bias, resid, ldr, y, ldy,
-                       epi, nks, row0, ra);
+                       epi, nks, row0, ra, lf);
 }
 
 }  // namespace
@@ -1173,8 +1224,12 @@ int g_gemm_fk = 0;
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
-                 int64_t ldy, int epi, const RopeArgs *ra) {
+                 int64_t ldy, int epi, const RopeArgs *ra, const GemvLn *ln) {
   NNHIP_REQUIRE(K % 4 == 0 && K <= 4096, kErrArg, "gemv: K must be a multiple of 4 and <= 4096");
+  const GemvLn lz = ln ? *ln : GemvLn{};
+  NNHIP_REQUIRE(!lz.g || (lz.b && K <= 1024 && ldx % 4 == 0 &&
+                          (!lz.out || lz.ldo % 4 == 0)),
+                kErrArg, "gemv: a folded LayerNorm needs K <= 1024 and aligned rows");
   NNHIP_REQUIRE(epi != kEpiSwiGLU || N % 2 == 0, kErrArg, "gemv: SwiGLU needs even N");
   NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg, "gemv: RoPE epilogue needs its arguments");
   NNHIP_REQUIRE(!(ra && ra->kq), kErrArg,
@@ -1187,8 +1242,10 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
     const float *xp = x + r0 * ldx;
     const float *rp = resid ? resid + r0 * ldr : nullptr;
     float *yp = y ? y + r0 * ldy : nullptr;
+    GemvLn lp = lz;
+    if (lp.out) lp.out += r0 * lp.ldo;
 #define NNHIP_GEMV(R) \
-    gemv_dispatch<R>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz)
+    gemv_dispatch<R>(st, xp, ldx, K, N, wq, wf, scale, bias, rp, ldr, yp, ldy, epi, r0, rz, lp)
     switch (rr) {
       case 1: NNHIP_GEMV(1); break;
       case 2: NNHIP_GEMV(2); break;

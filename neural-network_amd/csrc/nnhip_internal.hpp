@@ -363,10 +363,19 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
                      const float *resid, int64_t ldr, float *y, int64_t ldy,
                      int epi, const RopeArgs *ra = nullptr,
                      const TileStatsArgs *ts = nullptr);
+// A LayerNorm folded into the GEMV's input rows (launch_gemv): gamma g,
+// beta b over the K entries of each row; the normalised rows go to out
+// (stride ldo) when out is set.
+struct GemvLn {
+  const float *g = nullptr, *b = nullptr;
+  float *out = nullptr;
+  int64_t ldo = 0;
+};
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
                  const float *bias, const float *resid, int64_t ldr, float *y,
-                 int64_t ldy, int epi, const RopeArgs *ra = nullptr);
+                 int64_t ldy, int epi, const RopeArgs *ra = nullptr,
+                 const GemvLn *ln = nullptr);
 void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
                       int K, int8_t *limbs, int mpad, int *rexp);
 bool gemm_limb_q8_ok(int D);
