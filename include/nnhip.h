@@ -67,8 +67,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * "gemm_fk": 1 = the LDS-resident GEMM runs as full-K waves (8 waves, each
  * 32 columns over all of K) instead of 16 K-split waves (default 0;
  * process-wide).
- * "attn_w4": 1 = attention rows of 4+ queries run in workgroups of 4 key
- * splits (two per CU) instead of 8 (default 1; process-wide).
+ * "attn_w4": attention rows of 4+ queries run in workgroups of 4 key
+ * splits (two per CU) instead of 8: 1 = when a launch has 128 or more
+ * workgroups (default), 2 = always, 0 = never (process-wide).
  * "kv_stream": fp32 KV rows read with non-temporal loads: 0 never, 1 when
  * one attention launch reads more rows than the L2 caches hold (default),
  * 2 always (process-wide).

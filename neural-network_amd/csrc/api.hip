@@ -78,7 +78,10 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
     else if (std::strcmp(key, "fold_norm") == 0) nnhip::g_fold_norm = value != 0;
     else if (std::strcmp(key, "fold_small") == 0) nnhip::g_fold_small = value != 0;
     else if (std::strcmp(key, "down_split") == 0) nnhip::g_down_split = value != 0;
-    else if (std::strcmp(key, "attn_w4") == 0) nnhip::g_attn_w4 = value != 0;
+    else if (std::strcmp(key, "attn_w4") == 0) {
+      REQ(value >= 0 && value <= 2, "attn_w4 must be 0, 1 or 2");
+      nnhip::g_attn_w4 = value;
+    }
     else if (std::strcmp(key, "kv_stream") == 0) {
       REQ(value >= 0 && value <= 2, "kv_stream must be 0, 1 or 2");
       nnhip::g_kv_stream = value;

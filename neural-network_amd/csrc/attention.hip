@@ -914,8 +914,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
 #define NNHIP_ATTN_D(SQP, W)                                                  \
   if (D == 32) { NNHIP_ATTN(SQP, 4, W); } else { NNHIP_ATTN(SQP, 8, W); }
     // many-query rows hold many registers (one workgroup of 8 waves per CU):
-    // with 4 waves two workgroups share a CU and a launch runs in one round
-    const bool w4 = g_attn_w4 && max_keys <= kMergedWaves4 * kMergedChunks * kChunk;
+    // with 4 waves two workgroups share a CU and a launch runs in one round;
+    // a launch of few workgroups (one sequence) keeps 8 waves each, which
+    // shortens every wave's walk (batch-1 verify: 183.1 -> 181.7 ms)
+    const bool w4 = g_attn_w4 && max_keys <= kMergedWaves4 * kMergedChunks * kChunk &&
+                    (g_attn_w4 == 2 || B * H * nqb >= 128);
     if (sq == 1) { NNHIP_ATTN_D(1, kMergedWaves) }
     else if (sq == 2) { NNHIP_ATTN_D(2, kMergedWaves) }
     else if (sq <= 4) { if (w4) { NNHIP_ATTN_D(4, kMergedWaves4) } else { NNHIP_ATTN_D(4, kMergedWaves) } }

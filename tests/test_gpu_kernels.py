@@ -299,7 +299,7 @@ def test_attention_kq(ctx, B, S, H, D, pos0, w4):
     dq, dk, dv = ctx.array(q), ctx.array(k), ctx.array(v)
     dp, do = ctx.array(pos0), ctx.array(shape=(B * S, H * D))
     try:
-        ctx.set_option("attn_w4", w4)
+        ctx.set_option("attn_w4", 2 * w4)
         call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
              D, do.p)
     finally:
@@ -383,7 +383,7 @@ def test_attention_kq_q8(ctx, B, S, H, D, pos0, w4):
     dks, dvs = ctx.array(ks), ctx.array(vs)
     dp, do = ctx.array(pos0), ctx.array(shape=(B * S, H * D))
     try:
-        ctx.set_option("attn_w4", w4)
+        ctx.set_option("attn_w4", 2 * w4)
         call("nnhip_attention_kq_q8", ctx.h, dq.p, dkq.p, dks.p, dvq.p, dvs.p,
              cap, dp.p, B, S, H, H, D, do.p)
     finally:
