@@ -59,28 +59,32 @@ constexpr int kGemvNC = 8;  // columns per column set
 
 // Butterfly reduce-scatter of NP (a power of two <= 64) values per lane over
 // the 64 lanes of a wave: afterwards v[0] of lane l is the wave's total of
-// slot gemv_slot<NP>(l).
-template <int NP>
-__device__ __forceinline__ void wave_reduce_scatter(float (&v)[NP]) {
-  const int lane = threadIdx.x & 63;
-  int cnt = NP;
+// slot gemv_slot<NP>(l).  Step O (32, 16, ..., 1) halves the CNT values a
+// lane carries while CNT > 1 (the lane with bit O set keeps the upper half),
+// then adds the partner's single value; every index is a constant, so v
+// stays in registers.
+template <int NP, int CNT, int O>
+__device__ __forceinline__ void rs_step(float (&v)[NP], int lane) {
+  if constexpr (O >= 1) {
+    if constexpr (CNT > 1) {
+      constexpr int H = CNT / 2;
+      const bool up = (lane & O) != 0;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    if (cnt > 1) {
-      const int half = cnt / 2;
-      const bool up = (lane & o) != 0;
-#pragma unroll
-      for (int i = 0; i < NP / 2; ++i) {
-        if (i >= half) break;
-        const float send = up ? v[i] : v[i + half];
-        const float keep = up ? v[i + half] : v[i];
-        v[i] = keep + __shfl_xor(send, o, 64);
+      for (int i = 0; i < H; ++i) {
+        const float send = up ? v[i] : v[i + H];
+        const float keep = up ? v[i + H] : v[i];
+        v[i] = keep + __shfl_xor(send, O, 64);
       }
-      cnt = half;
+      rs_step<NP, H, O / 2>(v, lane);
     } else {
-      v[0] += __shfl_xor(v[0], o, 64);
+      v[0] += __shfl_xor(v[0], O, 64);
+      rs_step<NP, 1, O / 2>(v, lane);
     }
   }
+}
+template <int NP>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[NP]) {
+  rs_step<NP, NP, 32>(v, (int)threadIdx.x & 63);
 }
 template <int NP>
 __device__ __forceinline__ int gemv_slot(int lane) {
