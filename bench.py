@@ -238,6 +238,9 @@ def main():
     ap.add_argument("--no-kv-int8", action="store_true",
                     help="skip the secondary run with int8 KV caches "
                          "(generate_speculative(..., quantized_cache=true))")
+    ap.add_argument("--batch1-only", action="store_true",
+                    help="only run the batch-1 int8 greedy configuration "
+                         "and print its figures (for profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the copy calibration and the attention "
                          "kernel (for rocprofv3 --pmc)")
@@ -265,6 +268,9 @@ def main():
     for kv in a.option:
         key, val = kv.split("=")
         ctx.set_option(key, int(val))
+    if a.batch1_only:
+        print(json.dumps({"batch1": run_cfg2(ctx)}), flush=True)
+        return
     r = run_cfg4(ctx, a.steps, a.warmup)
     roof = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
     kv8 = None
