@@ -230,7 +230,9 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
  * TransformerDecoderLayer::forward runs at norm1 -> ffn and norm2 -> the next
  * layer (layer.cpp:1098-1113): y = LN(h) . W^T + b,
  * and LN(h) into ln_out when it is not NULL.  K in {128, 256, 512, 1024},
- * N % 32 == 0. */
+ * N % 32 == 0.  Rows below 16 run on the GEMV with the LayerNorm as its
+ * prologue (the decode path of short batches), others on the LDS-resident
+ * MFMA GEMM with the LayerNorm in its prologue. */
 int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
                                  int K, const float *gamma, const float *beta,
                                  float *ln_out, const int8_t *codes,

@@ -482,6 +482,14 @@ int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
     NNHIP_REQUIRE(nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
                   "fused LayerNorm GEMM needs K in {128, 256, 512, 1024} and N % 32 == 0");
     hipStream_t st = ctx->c.stream;
+    if (rows < 16) {
+      nnhip::GemvLn lf;
+      lf.g = gamma; lf.b = beta; lf.out = ln_out; lf.ldo = K;
+      nnhip::launch_gemv(st, h, K, rows, K, N, codes, nullptr, scales, bias,
+                         nullptr, 0, y, N, nnhip::kEpiBias, nullptr, &lf);
+      NNHIP_CHECK(hipStreamSynchronize(st));
+      return;
+    }
     nnhip::DevBuf<int8_t> sw((size_t)N * K);
     nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
     nnhip::launch_gemm_lds(st, nnhip::kAFromLayerNorm, nullptr, 0, nullptr, h,

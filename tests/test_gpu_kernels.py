@@ -221,11 +221,13 @@ def test_full_k_gemm_matches_lds_gemm(ctx, rows, K, N):
 
 @pytest.mark.parametrize("fk", [0, 1])
 @pytest.mark.parametrize("rows,K,N", [(32, 512, 1536), (192, 1024, 8192),
-                                      (20, 128, 256), (7, 256, 64)])
+                                      (20, 128, 256), (7, 256, 64),
+                                      (1, 512, 2048), (5, 1024, 512)])
 def test_layernorm_linear_vs_oracle(ctx, rows, K, N, fk):
     """LayerNorm fused into the GEMM prologue (16-wave K-split GEMM, or
-    full-K waves with fk = 1): LN(h) against the oracle's layernorm, y
-    against the oracle's dense over the oracle's LN(h)."""
+    full-K waves with fk = 1; rows below 16: the GEMV's prologue): LN(h)
+    against the oracle's layernorm, y against the oracle's dense over the
+    oracle's LN(h)."""
     rng = np.random.default_rng(rows + K + 3 * N)
     h = (rng.standard_normal((rows, K)) * 2 + 0.3).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
