@@ -254,8 +254,9 @@ def main():
                     help="nnhip_set_option before the run (repeatable)")
     a = ap.parse_args()
     if a.gpus != 1:
-        print("bench.py measures one GPU only: every box in this setup has a "
-              "single MI355X (sharding is described in DESIGN.md)",
+        print("bench.py measures one GPU only: the workload's sequences "
+              "shard over GPUs with no exchange step (each GPU runs its own "
+              "copy of this measurement on its share of the batch)",
               file=sys.stderr)
         sys.exit(2)
     if a.traffic_probe:
