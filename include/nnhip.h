@@ -290,15 +290,98 @@ int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
                       float temperature, int top_k, float top_p,
                       const float *u, int32_t *tok, float *probs);
 /* Accept loop + residual resample of generate_speculative (layer.cpp:
- * 1581-1630) for B sequences of k drafted positions: target and draft
- * logits [B][k][V], draft ids [B][k], accept uniforms [B][k], resample
- * uniforms [B].  n_accept [B]; next_tok [B] = resampled id, or -1 when all
- * k are accepted (no target row k for a bonus sample). */
+ * 1581-1630) for B sequences of k drafted positions, run by the kernels the
+ * device loop itself uses: the draft rows' get_probs as the drafting steps
+ * form them (layer.cpp:1554), then the verify rows' statistics and the
+ * accept / residual kernel.  Target and draft logits [B][k][V], draft ids
+ * [B][k], accept uniforms [B][k] (in place of the Philox slots k + j),
+ * resample uniforms [B] (slot 2k).  n_accept [B]; next_tok [B] = resampled
+ * id, or -1 when all k are accepted (no target row k for a bonus sample).
+ * Allocates its scratch and returns with the results written. */
 int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
                       const float *dlogits, const int32_t *dtok,
                       const float *u_accept, const float *u_resample, int B,
                       int k, int V, float temperature, int32_t *n_accept,
                       int32_t *next_tok);
+
+/* ---- ExecutionBackend ops (dev buffers, stream-ordered) -------------------
+ * The strided fp32 ops of the reference's backend interface
+ * (include/backend/backend.hpp:35-220) with CpuBackend's semantics
+ * (src/backend/cpu_backend.cpp), so that a HipBackend can run Tensor code
+ * unchanged.  An operand is a view: a dev buffer, an element offset, a
+ * shape and strides in elements (the reference passes DeviceBuffer, offset,
+ * Shape, Strides).  Inputs are right-aligned against the output's shape and
+ * their size-1 dimensions broadcast (get_input_offset, cpu_backend.cpp:
+ * 69-88).  Errors carry the reference's messages where it has one
+ * (cpu_backend.cpp:332-342). */
+#define NNHIP_MAX_RANK 8
+typedef struct {
+  void *data;                      /* dev buffer                          */
+  int64_t offset;                  /* elements                            */
+  int32_t rank;                    /* 0 .. NNHIP_MAX_RANK                 */
+  int64_t shape[NNHIP_MAX_RANK];
+  int64_t strides[NNHIP_MAX_RANK]; /* elements                            */
+} nnhip_view;
+/* binary ops: out = a (op) b */
+#define NNHIP_OP_ADD 0
+#define NNHIP_OP_SUB 1
+#define NNHIP_OP_MUL 2
+#define NNHIP_OP_DIV 3
+/* backward element-wise ops: grad_in = f(a, grad_out), a the forward input
+ * (relu, log) or output (sigmoid, tanh, sqrt), as the *_backward virtuals
+ * compute them (cpu_backend.cpp:473-481, 492-502, 513-521, 659-669,
+ * 680-690) */
+#define NNHIP_OP_RELU_BACKWARD 4
+#define NNHIP_OP_SIGMOID_BACKWARD 5
+#define NNHIP_OP_TANH_BACKWARD 6
+#define NNHIP_OP_SQRT_BACKWARD 7
+#define NNHIP_OP_LOG_BACKWARD 8
+/* unary ops: out = f(in); log is log(x + 1e-8) as in cpu_backend.cpp:675 */
+#define NNHIP_OP_RELU 16
+#define NNHIP_OP_SIGMOID 17
+#define NNHIP_OP_TANH 18
+#define NNHIP_OP_SQRT 19
+#define NNHIP_OP_LOG 20
+/* ExecutionBackend::add / sub / mul / div (backend.hpp:35-61) and the
+ * element-wise *_backward virtuals (:78-183): out = a (op) b. */
+int nnhip_binary_f32(nnhip_ctx *ctx, int op, const nnhip_view *a,
+                     const nnhip_view *b, const nnhip_view *out);
+/* ExecutionBackend::relu / sigmoid / tanh / sqrt / log (backend.hpp:73-166). */
+int nnhip_unary_f32(nnhip_ctx *ctx, int op, const nnhip_view *in,
+                    const nnhip_view *out);
+/* ExecutionBackend::matmul (backend.hpp:63-68, cpu_backend.cpp:326-387):
+ * 2-D a [M][K] . b [K][N] -> out [M][N], any strides; each output adds its
+ * products in ascending k. */
+int nnhip_matmul_f32(nnhip_ctx *ctx, const nnhip_view *a, const nnhip_view *b,
+                     const nnhip_view *out);
+/* ExecutionBackend::sum (backend.hpp:70-74, cpu_backend.cpp:389-459): sums
+ * over `axes`; out has the input's rank (summed dims of extent 1) or that
+ * rank minus naxes.  Each output adds its inputs in ascending input index,
+ * the reference's order. */
+int nnhip_sum_f32(nnhip_ctx *ctx, const nnhip_view *in, const nnhip_view *out,
+                  const int64_t *axes, int naxes);
+/* ExecutionBackend::softmax (backend.hpp:117-121, cpu_backend.cpp:523-583):
+ * exp(x - max) / sum along `axis`. */
+int nnhip_softmax_f32(nnhip_ctx *ctx, const nnhip_view *in,
+                      const nnhip_view *out, int axis);
+/* ExecutionBackend::softmax_backward (backend.hpp:123-130, cpu_backend.cpp:
+ * 586-638): dx = y * (dy - sum(dy * y)) along `axis`. */
+int nnhip_softmax_backward_f32(nnhip_ctx *ctx, const nnhip_view *y,
+                               const nnhip_view *dy, const nnhip_view *dx,
+                               int axis);
+/* ExecutionBackend::embedding (backend.hpp:199-206, cpu_backend.cpp:
+ * 998-1033): weight [V][D], indices [N][T] holding fp32 ids, out [N][T][D];
+ * an id outside [0, V) takes row 0. */
+int nnhip_embedding_f32(nnhip_ctx *ctx, const nnhip_view *weight,
+                        const nnhip_view *indices, const nnhip_view *out);
+/* ExecutionBackend::slice_backward (backend.hpp:215-219, cpu_backend.cpp:
+ * 1082-1120): grad_parent[..., index along axis, ...] += grad_slice. */
+int nnhip_slice_backward_f32(nnhip_ctx *ctx, const nnhip_view *grad_slice,
+                             const nnhip_view *grad_parent, int axis,
+                             int64_t index);
+/* ExecutionBackend::fill (backend.hpp:33, cpu_backend.cpp:49-67): count
+ * fp32 values of dev set to value. */
+int nnhip_fill_f32(nnhip_ctx *ctx, void *dev, size_t count, float value);
 
 /* ---- microbenchmarks -------------------------------------------------------
  * Time one kernel on the context's stream with HIP events (one untimed

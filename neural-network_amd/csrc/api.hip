@@ -661,9 +661,20 @@ int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
     REQ(ctx && tlogits && dlogits && dtok && u_accept && u_resample &&
             n_accept && next_tok && B > 0 && k > 0 && V > 0,
         "nnhip_spec_accept: bad argument");
-    nnhip::launch_accept_bench(ctx->c.stream, tlogits, dlogits, dtok, u_accept,
-                               u_resample, B, k, V, temperature, n_accept,
-                               next_tok);
+    hipStream_t st = ctx->c.stream;
+    nnhip::AcceptRows ar(B, k, V, temperature);
+    nnhip::DevBuf<float> q;
+    nnhip::DevBuf<int32_t> junk;
+    if (temperature > 0.f) {
+      // the drafting steps' get_probs of the draft rows (row_probs)
+      q.alloc((size_t)B * k * V);
+      junk.alloc((size_t)B * k);
+      nnhip::launch_sample_rows(st, dlogits, B * k, V, temperature, u_accept,
+                                junk.p, q.p);
+    }
+    ar.launch(st, tlogits, q.p, dtok, u_accept, u_resample, n_accept,
+              next_tok);
+    NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }
 

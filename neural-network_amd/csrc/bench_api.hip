@@ -83,10 +83,13 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
   });
 }
 
-// Acceptance step: B sequences x k positions x V, target and draft logits
-// N(0, 2), draft ids drawn from softmax(draft) with a separate stream, one
-// accept uniform per position and one resample uniform per sequence.
-// n_accept (host, [B]) receives the accepted counts of the timed inputs.
+// Acceptance step of the speculative loop (target_stats_kernel +
+// accept_kernel, after a reset of the per-sequence state): B sequences x k
+// positions x V, target and draft logits N(0, 2), the draft rows' get_probs
+// formed once beforehand (the drafting steps form them in the loop), draft
+// ids drawn from them with a separate stream, one accept uniform per
+// position and one resample uniform per sequence.  n_accept (host, [B])
+// receives the accepted counts of input set 0.
 int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
                             int iters, int nbuf, float *ms,
                             int32_t *n_accept) {
@@ -95,16 +98,11 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
                   nnhip::kErrArg, "nnhip_bench_spec_accept: bad argument");
     hipStream_t st = ctx->c.stream;
     const int64_t n = (int64_t)B * k * V;
-    std::vector<nnhip::DevBuf<float>> TL(nbuf), DL(nbuf);
-    nnhip::DevBuf<int32_t> dtok((size_t)B * k), nacc(B), next(B);
+    std::vector<nnhip::DevBuf<float>> TL(nbuf), Q(nbuf);
+    nnhip::DevBuf<float> dl(n);
+    nnhip::DevBuf<int32_t> dtok((size_t)B * k), nacc(B), next(B), junk((size_t)B * k);
     nnhip::DevBuf<float> ua((size_t)B * k), ur(B), us((size_t)B * k);
-    for (int i = 0; i < nbuf; ++i) {
-      TL[i].alloc(n); DL[i].alloc(n);
-      nnhip::launch_init_normal(st, TL[i].p, 1, (int)n, 0, 1, 4000 + i, 0, 2.f, 0);
-      nnhip::launch_init_normal(st, DL[i].p, 1, (int)n, 0, 1, 5000 + i, 0, 2.f, 0);
-    }
-    // uniforms in [0, 1): |N(0,1)| folded through the normal CDF would do,
-    // but a fresh Philox stream is simpler: host-generated, fixed seed
+    // uniforms in [0, 1) from a fixed host xorshift stream
     std::vector<float> hu((size_t)B * k * 2 + B);
     uint64_t x = 0x9E3779B97F4A7C15ull;
     for (auto &u : hu) {
@@ -114,17 +112,22 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
     NNHIP_CHECK(hipMemcpyAsync(ua.p, hu.data(), (size_t)B * k * 4, hipMemcpyHostToDevice, st));
     NNHIP_CHECK(hipMemcpyAsync(us.p, hu.data() + B * k, (size_t)B * k * 4, hipMemcpyHostToDevice, st));
     NNHIP_CHECK(hipMemcpyAsync(ur.p, hu.data() + 2 * B * k, (size_t)B * 4, hipMemcpyHostToDevice, st));
-    // draft ids: sample each draft row of buffer 0 (rows are [B*k][V])
-    nnhip::launch_sample_rows(st, DL[0].p, B * k, V, T > 0.f ? T : 1.f, us.p,
-                              dtok.p, nullptr);
+    const float Tq = T > 0.f ? T : 1.f;
+    for (int i = 0; i < nbuf; ++i) {
+      TL[i].alloc(n); Q[i].alloc(n);
+      nnhip::launch_init_normal(st, TL[i].p, 1, (int)n, 0, 1, 4000 + i, 0, 2.f, 0);
+      nnhip::launch_init_normal(st, dl.p, 1, (int)n, 0, 1, 5000 + i, 0, 2.f, 0);
+      // draft probabilities; set 0's draws are the draft ids
+      nnhip::launch_sample_rows(st, dl.p, B * k, V, Tq, us.p,
+                                i == 0 ? dtok.p : junk.p, Q[i].p);
+    }
+    nnhip::AcceptRows ar(B, k, V, T);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      nnhip::launch_accept_bench(st, TL[j].p, DL[j].p, dtok.p, ua.p, ur.p, B,
-                                 k, V, T, nacc.p, next.p);
+      ar.launch(st, TL[j].p, Q[j].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
     });
     if (n_accept) {
-      nnhip::launch_accept_bench(st, TL[0].p, DL[0].p, dtok.p, ua.p, ur.p, B,
-                                 k, V, T, nacc.p, next.p);
+      ar.launch(st, TL[0].p, Q[0].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
       NNHIP_CHECK(hipMemcpyAsync(n_accept, nacc.p, (size_t)B * 4, hipMemcpyDeviceToHost, st));
       NNHIP_CHECK(hipStreamSynchronize(st));
     }

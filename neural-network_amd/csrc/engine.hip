@@ -97,8 +97,16 @@ Model::Model(Ctx *c, int vocab, int d_model, int heads, int d_ff,
   }
   lm.init(d, V);
   init_normal(0, 0.0f);  // zero weights, zero biases, gamma 1, beta 0
+  ensure_rope(max_seq);
+  NNHIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Model::ensure_rope(int n) {
+  if (n <= rope_len) return;
   std::vector<float> hc, hs;
-  rope_tables(max_seq, D, hc, hs);
+  rope_tables(n, D, hc, hs);
+  hipStream_t st = ctx->stream;
+  NNHIP_CHECK(hipStreamSynchronize(st));
   cosb.alloc(hc.size());
   sinb.alloc(hs.size());
   NNHIP_CHECK(hipMemcpyAsync(cosb.p, hc.data(), hc.size() * 4,
@@ -106,6 +114,7 @@ Model::Model(Ctx *c, int vocab, int d_model, int heads, int d_ff,
   NNHIP_CHECK(hipMemcpyAsync(sinb.p, hs.data(), hs.size() * 4,
                              hipMemcpyHostToDevice, st));
   NNHIP_CHECK(hipStreamSynchronize(st));
+  rope_len = n;
 }
 
 static ParamRef param_ref(Model &m, int idx) {
@@ -658,14 +667,25 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   NNHIP_REQUIRE(t.V == dm.V, kErrArg, "target and draft vocabularies differ");
   NNHIP_REQUIRE(B > 0 && P > 0 && k > 0 && max_new >= 0, kErrArg,
                 "generate_speculative: bad sizes");
+  NNHIP_REQUIRE(k <= kMaxLookahead, kErrUnsupported,
+                "generate_speculative: lookahead above 63");
   check_sampling_options(t.V, top_k, top_p);
-  // The target cache peaks at P + max_new + k; the draft cache also keeps a
-  // duplicate of every recovered token (layer.cpp:1639-1642 then :1542), up
-  // to one per generated token.
+  // The reference throws when a forward's S_past + S exceeds max_seq_len
+  // (layer.cpp:1171-1179); with an int8 cache it never checks (the length
+  // is read from caches[0].k, which is null).  The prefill is checked here;
+  // the cycles' lengths depend on acceptance and are checked after the run
+  // from the largest lengths the device recorded.
+  NNHIP_REQUIRE(quantized_cache || (P <= t.max_seq && P <= dm.max_seq),
+                kErrCapacity,
+                "Sequence length S plus past cached length exceeds max_seq_len");
+  // Cache capacities cover every row the device writes: the verify step
+  // always runs k + 1 rows, and the draft cache keeps a duplicate of every
+  // recovered token (layer.cpp:1639-1642 then :1542), up to one per
+  // generated token.
   const int t_need = P + max_new + k + 1;
   const int d_need = P + 2 * max_new + k + 2;
-  NNHIP_REQUIRE(t_need <= t.max_seq && d_need <= dm.max_seq, kErrCapacity,
-                "Sequence length S plus past cached length exceeds max_seq_len");
+  t.ensure_rope(t_need);
+  dm.ensure_rope(d_need);
   Ctx *ctx = t.ctx;
   hipStream_t st = ctx->stream;
   const int V = t.V;
@@ -698,7 +718,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.tstat.alloc((size_t)B * (k + 1) * kTstat);
   bf.dlog.alloc((size_t)B * V);
   bf.tlog.alloc((size_t)B * (k + 1) * V);
-  bf.stats.alloc((size_t)B * 6);
+  bf.stats.alloc((size_t)B * kSpecStats);
   NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
   NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 4, st));
   NNHIP_CHECK(hipMemsetAsync(bf.cand.p, 0, bf.cand.bytes(), st));
@@ -730,7 +750,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;
     s.pair = bf.pair.p + (size_t)2 * b0;
     s.out = bf.out.p + (size_t)b0 * out_stride; s.n_active = bf.n_active.p;
-    s.stats = bf.stats.p + (size_t)b0 * 6;
+    s.stats = bf.stats.p + (size_t)b0 * kSpecStats;
     s.B = Bg; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
     s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0 + b0;
     s.top_k = top_k; s.top_p = top_p;
@@ -825,7 +845,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
         try {
           cycle();
         } catch (...) {
-          hipGraph_t g2;
+          hipGraph_t g2 = nullptr;
           (void)hipStreamEndCapture(st, &g2);
           if (g2) (void)hipGraphDestroy(g2);
           throw;
@@ -878,13 +898,20 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     timing->decode_ms = ms_dec;
     timing->cycles_launched = launched;
   }
+  std::vector<int64_t> hs((size_t)B * kSpecStats);
+  NNHIP_CHECK(hipMemcpy(hs.data(), bf.stats.p, hs.size() * 8,
+                        hipMemcpyDeviceToHost));
+  if (!quantized_cache) {
+    for (int b = 0; b < B; ++b) {
+      const int64_t *x = &hs[(size_t)b * kSpecStats];
+      NNHIP_REQUIRE(x[6] <= t.max_seq && x[7] <= dm.max_seq, kErrCapacity,
+                    "Sequence length S plus past cached length exceeds max_seq_len");
+    }
+  }
   NNHIP_CHECK(hipMemcpy(out, bf.out.p, bf.out.bytes(), hipMemcpyDeviceToHost));
   if (stats) {
-    std::vector<int64_t> hs((size_t)B * 6);
-    NNHIP_CHECK(hipMemcpy(hs.data(), bf.stats.p, hs.size() * 8,
-                          hipMemcpyDeviceToHost));
     for (int b = 0; b < B; ++b) {
-      const int64_t *x = &hs[(size_t)b * 6];
+      const int64_t *x = &hs[(size_t)b * kSpecStats];
       stats[b] = SpecStats{x[0], x[1], x[2], x[3], x[4], x[5]};
     }
   }

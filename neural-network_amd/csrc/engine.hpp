@@ -62,7 +62,12 @@ struct Model {
   DevBuf<float> emb;  // [V][d]
   std::vector<LayerW> layers;
   Linear lm;
-  DevBuf<float> cosb, sinb;  // [max_seq][D/2]
+  DevBuf<float> cosb, sinb;  // [rope_len][D/2], rope_len >= max_seq
+  int rope_len = 0;
+  // RoPE tables for positions [0, n): the speculative loop writes rows past
+  // max_seq_len (its verify step always runs k + 1 rows, and an int8 cache
+  // has no length check in the reference)
+  void ensure_rope(int n);
   std::vector<Workspace> wss;  // one per lane
 
   Model(Ctx *c, int vocab, int d_model, int heads, int d_ff, int n_layers,

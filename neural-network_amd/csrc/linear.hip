@@ -31,12 +31,6 @@ constexpr int kWave = 64;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
 __device__ __forceinline__ float silu_mul(float g, float u) {
   // SwiGLU::forward (layer.cpp:1704-1710): (g * sigmoid(g)) * u, with
   // sigmoid = 1 / (1 + exp(-g)) (cpu_backend.cpp:483-489).

@@ -450,9 +450,51 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       int8_t *limbs, int mpad, int *rexp,
                       const LinEpiArgs *ea = nullptr);
 
+// tensor_ops.hip: strided fp32 operands of the ExecutionBackend ops
+// (include/backend/backend.hpp:35-206): element offset, shape and strides
+// in elements, up to kMaxRank dimensions.
+constexpr int kMaxRank = 8;
+struct TensorView {
+  void *data = nullptr;
+  int64_t offset = 0;
+  int rank = 0;
+  int64_t shape[kMaxRank] = {};
+  int64_t strides[kMaxRank] = {};
+};
+enum TensorOp : int {
+  // binary: out = f(a, b)
+  kOpAdd = 0, kOpSub = 1, kOpMul = 2, kOpDiv = 3,
+  // binary backward: grad_in = f(forward input or output, grad_out)
+  kOpReluBack = 4, kOpSigmoidBack = 5, kOpTanhBack = 6, kOpSqrtBack = 7,
+  kOpLogBack = 8,
+  // unary: out = f(in)
+  kOpRelu = 16, kOpSigmoid = 17, kOpTanh = 18, kOpSqrt = 19, kOpLog = 20
+};
+void launch_binary(hipStream_t st, int op, const TensorView &a,
+                   const TensorView &b, const TensorView &out);
+void launch_unary(hipStream_t st, int op, const TensorView &in,
+                  const TensorView &out);
+void launch_matmul(hipStream_t st, const TensorView &a, const TensorView &b,
+                   const TensorView &out);
+void launch_sum(hipStream_t st, const TensorView &in, const TensorView &out,
+                const int64_t *axes, int naxes);
+void launch_softmax(hipStream_t st, const TensorView &in, const TensorView &out,
+                    int axis);
+void launch_softmax_backward(hipStream_t st, const TensorView &y,
+                             const TensorView &dy, const TensorView &dx,
+                             int axis);
+void launch_embedding(hipStream_t st, const TensorView &w, const TensorView &ids,
+                      const TensorView &out);
+void launch_slice_backward(hipStream_t st, const TensorView &gs,
+                           const TensorView &gp, int axis, int64_t index);
+
 // sampling.hip
 // floats per verify row of SpecState::tstat
 constexpr int kTstat = 6;
+// int64 counters per sequence of SpecState::stats
+constexpr int kSpecStats = 8;
+// largest lookahead k of the speculative loop
+constexpr int kMaxLookahead = 63;
 // whether get_probs filters with these options (layer.cpp:1452-1472)
 inline bool sampling_filtered(int V, int top_k, float top_p) {
   return (top_k > 0 && top_k < V) || (top_p > 0.0f && top_p < 1.0f);
@@ -473,8 +515,10 @@ struct SpecState {
                        // first draft forward
   int32_t *out;        // [B][out_stride] prompt + generated ids
   int32_t *n_active;   // [1]
-  int64_t *stats;      // [B][6] cycles, drafted, accepted, ties, resampled,
-                       //        bonus
+  int64_t *stats;      // [B][kSpecStats] cycles, drafted, accepted, ties,
+                       // resampled, bonus, and the largest target / draft
+                       // cache lengths the reference's forwards reach
+                       // (S_past + S of layer.cpp:1171-1179)
   const float2 *dtiles;  // [B][k][nt] draft lm-head tile statistics
                          // (TileStatsArgs) of the cycle's steps, or null
   int nt, tw;            // tiles per row, tile width
@@ -484,6 +528,13 @@ struct SpecState {
   float top_p;           // (0, V) and top_p in (0, 1) are active
   uint64_t seed;
   uint32_t seq0;       // global index of sequence 0 (Philox key part)
+  int trows = 0;       // verify rows per sequence in tlogits (0: k + 1)
+  // explicit accept / final uniforms ([B][k] and [B]) instead of the
+  // Philox slots k + j and 2k (nnhip_spec_accept); null in the loop
+  const float *ua = nullptr, *ur = nullptr;
+  // when set, accept_kernel also writes each sequence's accepted count and
+  // its resampled / bonus token (-1 when none)
+  int32_t *n_acc_out = nullptr, *tok_out = nullptr;
 };
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl);
@@ -499,9 +550,22 @@ void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
                         float T, const float *u, int32_t *tok, float *probs,
                         int top_k = 0, float top_p = 1.f);
 void launch_add_scalar(hipStream_t st, int32_t *p, int n, int v);
-void launch_accept_bench(hipStream_t st, const float *tlog, const float *dlog,
-                         const int32_t *dtok, const float *u_acc,
-                         const float *u_res, int B, int k, int V, float T,
-                         int32_t *n_acc, int32_t *next_tok);
+// The speculative loop's accept step (target_stats_kernel + accept_kernel)
+// over given rows: B sequences that each drafted k candidates, target
+// logits [B][k][V] (no bonus row), draft probabilities [B][k][V] as the
+// drafting steps form them (get_probs), explicit uniforms ua [B][k] and
+// ur [B].  Writes n_acc [B] and tok [B] (resampled id, or -1 when all k
+// are accepted).  The sequence state is reset by each launch.
+struct AcceptRows {
+  DevBuf<int32_t> cur, tlen, dlen, gen, cyc, active, catchup, catch_tok, pair,
+      out, n_active;
+  DevBuf<float> tstat;
+  DevBuf<int64_t> stats;
+  SpecState s;
+  AcceptRows(int B, int k, int V, float T);
+  void launch(hipStream_t st, const float *tlogits, const float *qprob,
+              const int32_t *cand, const float *ua, const float *ur,
+              int32_t *n_acc, int32_t *tok);
+};
 
 }  // namespace nnhip

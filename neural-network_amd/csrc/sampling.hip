@@ -197,11 +197,6 @@ __device__ __forceinline__ float prob_of(float l, int v, float T,
   return kept(p1, v, st) ? p1 * st.rfs : 0.f;
 }
 
-__device__ __forceinline__ float prob_at(const float *row, int v, float T,
-                                         RowStats st) {
-  return prob_of(row[v], v, T, st);
-}
-
 // ---------------------------------------------------------------------------
 // top-k / top-p of get_probs (layer.cpp:1447-1489).  The reference sorts p1
 // (the probabilities after the first normalisation) descending, zeroes the
@@ -654,6 +649,10 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
 }
 
+__device__ __forceinline__ int verify_rows(const SpecState &s) {
+  return s.trows > 0 ? s.trows : s.k + 1;
+}
+
 // Per verify row (b, j <= M): argmax (greedy) or the get_probs statistics
 // (sampled), for all rows of the cycle at once.  tstat[b][j] =
 // {max, 1/sum, 1/sum(kept p1), argmax, tau, tix} (the last three as int
@@ -664,10 +663,12 @@ __global__ __launch_bounds__(kThreads) void target_stats_kernel(
   __shared__ Shared sh;
   const int j = blockIdx.x, b = blockIdx.y;
   if (!s.active[b]) return;
-  const int M = min(s.k, s.max_new - s.gen[b]);
-  if (j > M) return;
+  const int gen0 = s.gen[b];
+  const int M = min(s.k, s.max_new - gen0);
+  // row M serves only the bonus sample, which needs room for one more token
+  if (j > M || (j == M && gen0 + M >= s.max_new)) return;
   const int64_t r = (int64_t)b * (s.k + 1) + j;
-  const float *row = tlogits + r * s.V;
+  const float *row = tlogits + ((int64_t)b * verify_rows(s) + j) * s.V;
   float *ts = s.tstat + r * kTstat;
   if (s.T <= 0.f) {
     const int a = block_argmax(row, s.V, sh);
@@ -682,15 +683,13 @@ __global__ __launch_bounds__(kThreads) void target_stats_kernel(
 }
 
 // Residual max(0, p - q) (layer.cpp:1611-1630), p from the target row's
-// statistics, q from qrow (stored) or from the draft row's statistics; then
-// sample it, or p when the residual sums to zero.  The residual is sampled
-// unnormalised: the discrete distribution normalises it.
+// statistics, q from the stored draft probabilities; then sample it, or p
+// when the residual sums to zero.  The residual is sampled unnormalised:
+// the discrete distribution normalises it.
 __device__ __forceinline__ int residual_sample(
-    const float *__restrict__ qrow, const float *__restrict__ dlog_row,
-    RowStats qst, const float *__restrict__ tlog_row, RowStats tst, int V,
-    float T, float u, Shared &sh) {
+    const float *__restrict__ qrow, const float *__restrict__ tlog_row,
+    RowStats tst, int V, float T, float u, Shared &sh) {
   // two halves of the thread's entries, each with its loads in flight
-  const float *qsrc = qrow ? qrow : dlog_row;
   constexpr int kHalf = kPer / 2;
   float loc = 0.f;
 #pragma unroll
@@ -700,15 +699,14 @@ __device__ __forceinline__ int residual_sample(
     for (int i = 0; i < kHalf; ++i) {
       const int v = min((int)threadIdx.x + (hf * kHalf + i) * kThreads, V - 1);
       xt[i] = tlog_row[v];
-      xq[i] = qsrc[v];
+      xq[i] = qrow[v];
     }
 #pragma unroll
     for (int i = 0; i < kHalf; ++i) {
       const int v = (int)threadIdx.x + (hf * kHalf + i) * kThreads;
       if (v < V) {
         const float p = prob_of(xt[i], v, T, tst);
-        const float q = qrow ? xq[i] : prob_of(xq[i], v, T, qst);
-        const float r = fmaxf(0.0f, p - q);
+        const float r = fmaxf(0.0f, p - xq[i]);
         sh.prow[la(v)] = r;
         loc += r;
       }
@@ -733,6 +731,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   const int M = min(k, s.max_new - gen0);
   const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
   const int tstart = s.tlen[b], dstart = s.dlen[b];
+  const int tr = verify_rows(s);
   int32_t *out = s.out + (int64_t)b * s.out_stride;
   int nout = s.P + gen0;
   int rej = -1;
@@ -757,7 +756,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     for (int j = 0; j < kPre; ++j) {
       if (j < M) {
         const int c = s.cand[b * k + j];
-        lc[j] = tlogits[((int64_t)b * (k + 1) + j) * V + c];
+        lc[j] = tlogits[((int64_t)b * tr + j) * V + c];
         qcp[j] = s.qprob[((int64_t)b * k + j) * V + c];
       }
     }
@@ -767,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     if (greedy) return c == argmax_of(j);
     const RowStats st = stats_of(j);
     const float pc = prob_of(lj, c, s.T, st);
-    const float r = uniform(s.seed, seq, cyc, k + j);
+    const float r = s.ua ? s.ua[(int64_t)b * k + j] : uniform(s.seed, seq, cyc, k + j);
     if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
     return __fmul_rn(r, qc) < pc;
   };
@@ -781,7 +780,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   }
   for (int j = kPre; j < M && rej < 0; ++j) {
     const int c = s.cand[b * k + j];
-    const float lj = greedy ? 0.f : tlogits[((int64_t)b * (k + 1) + j) * V + c];
+    const float lj = greedy ? 0.f : tlogits[((int64_t)b * tr + j) * V + c];
     const float qc = greedy ? 0.f : s.qprob[((int64_t)b * k + j) * V + c];
     if (!test(j, c, lj, qc)) { rej = j; break; }
     if (threadIdx.x == 0) out[nout] = c;
@@ -789,19 +788,18 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   }
   int gen = gen0 + (rej < 0 ? M : rej);
   int tok = -1, catch_tok = -1;
-  const float u = uniform(s.seed, seq, cyc, 2 * k);
+  const float u = s.ur ? s.ur[b] : uniform(s.seed, seq, cyc, 2 * k);
   if (rej >= 0) {
-    const float *row = tlogits + ((int64_t)b * (k + 1) + rej) * V;
+    const float *row = tlogits + ((int64_t)b * tr + rej) * V;
     if (greedy) {
       tok = argmax_of(rej);
     } else {
-      tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, nullptr,
-                            mk_stats(0.f, 1.f, 1.f), row, stats_of(rej), V,
-                            s.T, u, sh);
+      tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, row,
+                            stats_of(rej), V, s.T, u, sh);
     }
     catch_tok = tok;
   } else if (gen < s.max_new) {
-    const float *row = tlogits + ((int64_t)b * (k + 1) + M) * V;
+    const float *row = tlogits + ((int64_t)b * tr + M) * V;
     if (greedy) {
       tok = argmax_of(M);
     } else {
@@ -811,11 +809,15 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     catch_tok = s.cand[b * k + M - 1];
   }
   if (threadIdx.x == 0) {
-    int64_t *st = s.stats + (int64_t)b * 6;
+    int64_t *st = s.stats + (int64_t)b * kSpecStats;
     st[0] += 1;
     st[1] += M;
     st[2] += (rej < 0 ? M : rej);
     st[3] += ties;
+    if (s.n_acc_out) {
+      s.n_acc_out[b] = rej < 0 ? M : rej;
+      s.tok_out[b] = tok;
+    }
     if (tok >= 0) {
       out[nout] = tok;
       ++gen;
@@ -829,6 +831,10 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     // full acceptance, then takes the catch-up token (layer.cpp:1639-1653);
     // dlen is the length after that catch-up, which writes at dlen - 1.
     if (tok >= 0) s.dlen[b] = dstart + keep + (rej >= 0 ? 2 : 1);
+    // lengths the reference's forwards reach this cycle: the verify forward
+    // of M + 1 ids, the M drafting steps, the catch-up
+    st[6] = max(st[6], (int64_t)(tstart + M + 1));
+    st[7] = max(st[7], (int64_t)max(dstart + M, tok >= 0 ? s.dlen[b] : 0));
     s.catchup[b] = tok >= 0 ? 1 : 0;
     s.catch_tok[b] = catch_tok;
     s.pair[2 * b] = catch_tok;
@@ -857,49 +863,15 @@ __global__ __launch_bounds__(kThreads) void ar_sample_kernel(
   }
 }
 
-// Acceptance microbenchmark: k target rows and k draft rows of logits per
-// sequence, draft ids, one accept uniform per position and one resample
-// uniform per sequence.  Rows are read only up to the first rejection.
-// next_tok = residual resample, or -1 when all k drafts are accepted (no
-// target row k is given for a bonus sample).
-__global__ __launch_bounds__(kThreads) void accept_bench_kernel(
-    const float *__restrict__ tlog, const float *__restrict__ dlog,
-    const int32_t *__restrict__ dtok, const float *__restrict__ u_acc,
-    const float *__restrict__ u_res, int k, int V, float T,
-    int32_t *__restrict__ n_acc, int32_t *__restrict__ next_tok) {
-  __shared__ Shared sh;
-  const int b = blockIdx.x;
-  int rej = -1;
-  RowStats qst = mk_stats(0.f, 1.f, 1.f), tst = mk_stats(0.f, 1.f, 1.f);
-  for (int j = 0; j < k; ++j) {
-    const float *tr = tlog + ((int64_t)b * k + j) * V;
-    const float *dr = dlog + ((int64_t)b * k + j) * V;
-    const int c = dtok[b * k + j];
-    bool acc;
-    if (T <= 0.f) {
-      acc = c == block_argmax(tr, V, sh);
-    } else {
-      qst = row_stats(dr, V, T, sh);
-      tst = row_stats(tr, V, T, sh);
-      const float pc = prob_at(tr, c, T, tst);
-      const float qc = prob_at(dr, c, T, qst);
-      acc = __fmul_rn(u_acc[b * k + j], qc) < pc;
-    }
-    if (!acc) { rej = j; break; }
-  }
-  int tok = -1;
-  if (rej >= 0) {
-    const float *tr = tlog + ((int64_t)b * k + rej) * V;
-    if (T <= 0.f)
-      tok = block_argmax(tr, V, sh);
-    else
-      tok = residual_sample(nullptr, dlog + ((int64_t)b * k + rej) * V, qst,
-                            tr, tst, V, T, u_res[b], sh);
-  }
-  if (threadIdx.x == 0) {
-    n_acc[b] = rej < 0 ? k : rej;
-    next_tok[b] = tok;
-  }
+// State of the accept step run on given rows (AcceptRows): every sequence
+// drafted k candidates (gen 0 of max_new = k, so no bonus row), at cycle 1.
+__global__ void accept_rows_reset_kernel(SpecState s) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b == 0) *s.n_active = s.B;
+  if (b >= s.B) return;
+  s.cur[b] = -1; s.tlen[b] = 0; s.dlen[b] = 0; s.gen[b] = 0; s.cyc[b] = 1;
+  s.active[b] = 1; s.catchup[b] = 0; s.catch_tok[b] = -1;
+  for (int i = 0; i < kSpecStats; ++i) s.stats[(int64_t)b * kSpecStats + i] = 0;
 }
 
 // get_probs + sample_token on independent rows with explicit uniforms.
@@ -1006,15 +978,34 @@ void launch_sample_rows(hipStream_t st, const float *logits, int B, int V,
   NNHIP_CHECK(hipGetLastError());
 }
 
-void launch_accept_bench(hipStream_t st, const float *tlog, const float *dlog,
-                         const int32_t *dtok, const float *u_acc,
-                         const float *u_res, int B, int k, int V, float T,
-                         int32_t *n_acc, int32_t *next_tok) {
-  NNHIP_REQUIRE(V <= kMaxV, kErrUnsupported,
-                "sampling: vocabulary above 32768");
-  hipLaunchKernelGGL(accept_bench_kernel, dim3(B), dim3(kThreads), 0, st, tlog,
-                     dlog, dtok, u_acc, u_res, k, V, T, n_acc, next_tok);
+AcceptRows::AcceptRows(int B, int k, int V, float T) {
+  NNHIP_REQUIRE(B > 0 && k > 0 && V > 0, kErrArg, "accept: bad sizes");
+  NNHIP_REQUIRE(V <= kMaxV, kErrUnsupported, "sampling: vocabulary above 32768");
+  cur.alloc(B); tlen.alloc(B); dlen.alloc(B); gen.alloc(B); cyc.alloc(B);
+  active.alloc(B); catchup.alloc(B); catch_tok.alloc(B);
+  pair.alloc((size_t)2 * B); out.alloc((size_t)B * (k + 1)); n_active.alloc(1);
+  tstat.alloc((size_t)B * (k + 1) * kTstat);
+  stats.alloc((size_t)B * kSpecStats);
+  s = SpecState{};
+  s.cur = cur.p; s.tstat = tstat.p; s.tlen = tlen.p; s.dlen = dlen.p;
+  s.gen = gen.p; s.cyc = cyc.p; s.active = active.p; s.catchup = catchup.p;
+  s.catch_tok = catch_tok.p; s.pair = pair.p; s.out = out.p;
+  s.n_active = n_active.p; s.stats = stats.p;
+  s.B = B; s.out_stride = k + 1; s.P = 0; s.max_new = k; s.k = k; s.V = V;
+  s.T = T; s.trows = k; s.top_k = 0; s.top_p = 1.f;
+}
+
+void AcceptRows::launch(hipStream_t st, const float *tlogits, const float *qprob,
+                        const int32_t *cand, const float *ua, const float *ur,
+                        int32_t *n_acc, int32_t *tok) {
+  SpecState a = s;
+  a.qprob = const_cast<float *>(qprob);
+  a.cand = const_cast<int32_t *>(cand);
+  a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
+  hipLaunchKernelGGL(accept_rows_reset_kernel, dim3((s.B + 255) / 256),
+                     dim3(256), 0, st, a);
   NNHIP_CHECK(hipGetLastError());
+  launch_accept(st, a, tlogits);
 }
 
 }  // namespace nnhip

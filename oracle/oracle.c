@@ -17,6 +17,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* threads of the Dense products and attention heads (or_set_threads) */
+static int g_threads = 1;
+void or_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+
 /* ------------------------------------------------------------------ */
 /* Philox4x32-10 (Random123 paper, Salmon et al. 2011).                */
 /* ------------------------------------------------------------------ */
@@ -239,27 +243,35 @@ int or_model_get_quantized(const or_model *m, int layer, int which,
 void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
               const float *w, const int8_t *codes, const float *scales,
               const float *bias, float *y) {
-  float *wrow = (float *)malloc(sizeof(float) * (size_t)out);
-  for (int64_t i = 0; i < rows * out; ++i) y[i] = 0.0f;
-  for (int64_t k = 0; k < in; ++k) {
-    const float *wr;
-    if (codes) {
-      const int8_t *cr = codes + k * out;
-      for (int64_t n = 0; n < out; ++n) wrow[n] = (float)cr[n] * scales[n];
-      wr = wrow;
-    } else {
-      wr = w + k * out;
-    }
-    for (int64_t r = 0; r < rows; ++r) {
-      float xk = x[r * in + k];
-      float *yr = y + r * out;
-      for (int64_t n = 0; n < out; ++n) yr[n] += xk * wr[n];
-    }
-  }
-  if (bias)
+  /* column blocks are independent tasks; within a block the loop order is
+   * the single-thread one, so every output keeps its summation order */
+  enum { NB = 512 };
+  const int64_t tasks = (out + NB - 1) / NB;
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && tasks > 1)
+  for (int64_t t = 0; t < tasks; ++t) {
+    const int64_t n0 = t * NB, n1 = out < n0 + NB ? out : n0 + NB;
+    float wrow[NB];
     for (int64_t r = 0; r < rows; ++r)
-      for (int64_t n = 0; n < out; ++n) y[r * out + n] = y[r * out + n] + bias[n];
-  free(wrow);
+      for (int64_t n = n0; n < n1; ++n) y[r * out + n] = 0.0f;
+    for (int64_t k = 0; k < in; ++k) {
+      const float *wr;
+      if (codes) {
+        const int8_t *cr = codes + k * out;
+        for (int64_t n = n0; n < n1; ++n) wrow[n - n0] = (float)cr[n] * scales[n];
+        wr = wrow - n0;
+      } else {
+        wr = w + k * out;
+      }
+      for (int64_t r = 0; r < rows; ++r) {
+        float xk = x[r * in + k];
+        float *yr = y + r * out;
+        for (int64_t n = n0; n < n1; ++n) yr[n] += xk * wr[n];
+      }
+    }
+    if (bias)
+      for (int64_t r = 0; r < rows; ++r)
+        for (int64_t n = n0; n < n1; ++n) y[r * out + n] = y[r * out + n] + bias[n];
+  }
 }
 
 static void dense_fwd(const or_dense_t *dn, const float *x, int64_t rows,
@@ -319,8 +331,11 @@ void or_attention(const float *q, const float *k, const float *v, int64_t H,
   int64_t S_past = S_total - S;
   int64_t group = H / H_kv;
   float scale = sqrtf((float)D);
-  float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
+  /* heads are independent tasks (the reference's ThreadPool splits B*H,
+   * layer.cpp:859-948) */
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && H > 1)
   for (int64_t h = 0; h < H; ++h) {
+    float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
     int64_t hk = h / group;
     for (int64_t i = 0; i < S; ++i) {
       float mx = -INFINITY;
@@ -355,8 +370,8 @@ void or_attention(const float *q, const float *k, const float *v, int64_t H,
         o[dd] = acc;
       }
     }
+    free(row);
   }
-  free(row);
 }
 
 /* quantize_kv of MultiHeadAttention::forward (layer.cpp:635-657) over rows
@@ -394,8 +409,11 @@ void or_attention_q8(const float *q, const int8_t *kq, const float *ks,
   int64_t S_past = S_total - S;
   int64_t group = H / H_kv;
   float scale = sqrtf((float)D);
-  float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
+  /* heads are independent tasks (the reference's ThreadPool splits B*H,
+   * layer.cpp:859-948) */
+#pragma omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1 && H > 1)
   for (int64_t h = 0; h < H; ++h) {
+    float *row = (float *)malloc(sizeof(float) * (size_t)S_total);
     int64_t hk = h / group;
     for (int64_t i = 0; i < S; ++i) {
       float mx = -INFINITY;
@@ -432,8 +450,8 @@ void or_attention_q8(const float *q, const int8_t *kq, const float *ks,
         o[dd] = acc;
       }
     }
+    free(row);
   }
-  free(row);
 }
 
 /* ------------------------------------------------------------------ */
@@ -542,6 +560,31 @@ or_cache *or_cache_create_q(const or_model *m, int quantized) {
   return c;
 }
 or_cache *or_cache_create(const or_model *m) { return or_cache_create_q(m, 0); }
+
+/* An int8 cache grows past max_seq_len, as the reference's does (its
+ * quantised vectors have no capacity; see or_forward). */
+static void *regrow(void *old, size_t esz, int L, int H, int cap, int ncap,
+                    int len, int D) {
+  char *nw = (char *)calloc((size_t)L * H * ncap * D, esz);
+  for (int l = 0; l < L; ++l)
+    for (int h = 0; h < H; ++h)
+      memcpy(nw + (((size_t)l * H + h) * ncap) * D * esz,
+             (char *)old + (((size_t)l * H + h) * cap) * D * esz,
+             (size_t)len * D * esz);
+  free(old);
+  return nw;
+}
+static void cache_reserve(or_cache *c, int need) {
+  if (need <= c->cap) return;
+  int ncap = need > 2 * c->cap ? need : 2 * c->cap;
+  c->kq = regrow(c->kq, 1, c->L, c->H, c->cap, ncap, c->len, c->D);
+  c->vq = regrow(c->vq, 1, c->L, c->H, c->cap, ncap, c->len, c->D);
+  c->ks = regrow(c->ks, sizeof(float), c->L, c->H, c->cap, ncap, c->len, 1);
+  c->vs = regrow(c->vs, sizeof(float), c->L, c->H, c->cap, ncap, c->len, 1);
+  c->kraw = regrow(c->kraw, sizeof(float), c->L, c->H, c->cap, ncap, c->len, c->D);
+  c->vraw = regrow(c->vraw, sizeof(float), c->L, c->H, c->cap, ncap, c->len, c->D);
+  c->cap = ncap;
+}
 void or_cache_free(or_cache *c) {
   if (!c) return;
   free(c->k); free(c->v); free(c->kq); free(c->vq); free(c->ks); free(c->vs);
@@ -602,7 +645,10 @@ int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
                float *logits) {
   int d = m->d, H = m->H, D = d / H, F = m->F;
   int S_past = cache ? cache->len : 0;
-  if (S_past + S > m->max_seq) return -1;
+  /* the reference reads S_past from caches[0].k (layer.cpp:1171-1179),
+   * which an int8 cache leaves null: then nothing is checked */
+  if (!(cache && cache->quantized) && S_past + S > m->max_seq) return -1;
+  if (cache && cache->quantized) cache_reserve(cache, S_past + S);
   int S_total = S_past + S;
   size_t sd = (size_t)S * d;
   float *x = (float *)malloc(sizeof(float) * sd);
@@ -797,16 +843,36 @@ void or_get_probs(const float *logits, int V, float T, int top_k, float top_p,
  * over the probabilities widened to double (libstdc++ random.tcc:
  * normalise by the double sum, partial_sum, last entry forced to 1.0,
  * lower_bound of the uniform): the first v with cdf[v] >= u. */
-int or_sample(const float *probs, int V, double u) {
-  if (V < 2) return 0;
+/* or_sample that also reports how far u lies from the drawn interval's
+ * edges [cdf[v-1], cdf[v]] (checker use: a draw whose margin is below the
+ * device's rounding may legitimately come out differently there). */
+static int sample_margin(const float *probs, int V, double u, double *margin) {
+  if (V < 2) { if (margin) *margin = 1.0; return 0; }
   double sum = 0.0;
   for (int v = 0; v < V; ++v) sum += (double)probs[v];
-  double c = 0.0;
+  double c = 0.0, prev = 0.0;
   for (int v = 0; v < V - 1; ++v) {
     c += (double)probs[v] / sum;
-    if (c >= u) return v;
+    if (c >= u) {
+      if (margin) *margin = fmin(c - u, u - prev);
+      return v;
+    }
+    prev = c;
   }
+  if (margin) *margin = u - prev;
   return V - 1;
+}
+
+int or_sample(const float *probs, int V, double u) {
+  return sample_margin(probs, V, u, NULL);
+}
+
+/* smallest decision margin of the current cycle (checker record) */
+static double g_margin = 1.0;
+double or_decision_margin(int reset) {
+  double m = g_margin;
+  if (reset) g_margin = 1.0;
+  return m;
 }
 
 /* Draws of the speculative loop: greedy mode (T <= 0) samples only one-hot
@@ -815,7 +881,10 @@ int or_sample(const float *probs, int V, double u) {
 static int draw(const float *probs, int V, int greedy, uint64_t seed,
                 uint32_t seq, uint32_t cycle, uint32_t slot) {
   if (greedy) return or_argmax(probs, V);
-  return or_sample(probs, V, (double)or_uniform(seed, seq, cycle, slot));
+  double m = 1.0;
+  int v = sample_margin(probs, V, (double)or_uniform(seed, seq, cycle, slot), &m);
+  if (m < g_margin) g_margin = m;
+  return v;
 }
 
 /* The accept loop and its ending (layer.cpp:1581-1630, 1643-1647) over
@@ -838,8 +907,9 @@ int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
     } else {
       float r = u_accept[j];
       acc = r * qj[c] < pj[c];
-      if (ties && fabs((double)r - (double)pj[c] / (double)qj[c]) < 1e-6)
-        (*ties)++;
+      double dist = fabs((double)r - (double)pj[c] / (double)qj[c]);
+      if (ties && dist < 1e-6) (*ties)++;
+      if (dist < g_margin) g_margin = dist;
     }
     if (acc) continue;
     if (greedy) { *tok = or_argmax(pj, V); return j; }
@@ -849,17 +919,24 @@ int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
       rec[v] = fmaxf(0.0f, pj[v] - qj[v]);
       sr += rec[v];
     }
-    if (sr <= 0.0f) *tok = or_sample(pj, V, (double)u_final);
+    double m = 1.0;
+    if (sr <= 0.0f) *tok = sample_margin(pj, V, (double)u_final, &m);
     else {
       for (int v = 0; v < V; ++v) rec[v] /= sr;
-      *tok = or_sample(rec, V, (double)u_final);
+      *tok = sample_margin(rec, V, (double)u_final, &m);
     }
+    if (m < g_margin) g_margin = m;
     free(rec);
     return j;
   }
   if (has_bonus) {
     const float *pm = p + (size_t)M * V;
-    *tok = greedy ? or_argmax(pm, V) : or_sample(pm, V, (double)u_final);
+    if (greedy) *tok = or_argmax(pm, V);
+    else {
+      double m = 1.0;
+      *tok = sample_margin(pm, V, (double)u_final, &m);
+      if (m < g_margin) g_margin = m;
+    }
   }
   return M;
 }
@@ -869,6 +946,9 @@ static double now_ms(void) {
   clock_gettime(CLOCK_MONOTONIC, &ts);
   return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
 }
+
+static or_spec_trace *g_trace = NULL;
+void or_set_spec_trace(or_spec_trace *trace) { g_trace = trace; }
 
 /* generate_speculative (layer.cpp:1382-1661) for one sequence. */
 int or_generate_speculative(const or_model *t, const or_model *dm,
@@ -899,7 +979,9 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
     rc = -1; goto done;
   }
   or_get_probs(tl + (size_t)(P - 1) * V, V, T, top_k, top_p, p);
+  g_margin = 1.0;
   out[n++] = draw(p, V, greedy, seed, seq, 0, 2 * k);
+  if (g_trace) g_trace->first_margin = g_margin;
   int ngen = 1;
   uint32_t cycle = 0;
   t1 = now_ms();
@@ -907,12 +989,24 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
     int M = k < max_new - ngen ? k : max_new - ngen;
     ++cycle;
     int tstart = tc->len, dstart = dc->len;
+    or_spec_trace *tr = g_trace;
+    int tc_i = -1;
+    g_margin = 1.0;
+    if (tr && tr->n < tr->max_cycles && tr->k == k && tr->V == V) {
+      tc_i = tr->n++;
+      tr->dstart[tc_i] = dstart;
+      tr->tstart[tc_i] = tstart;
+      tr->M[tc_i] = M;
+    }
     /* draft loop (layer.cpp:1541-1558) */
     for (int j = 0; j < M; ++j) {
       int32_t in = j == 0 ? out[n - 1] : cand[j - 1];
       if (or_forward(dm, dc, &in, 1, dl)) { rc = -1; goto done; }
+      if (tc_i >= 0)
+        memcpy(tr->dlogits + ((size_t)tc_i * k + j) * V, dl, sizeof(float) * V);
       or_get_probs(dl, V, T, top_k, top_p, q + (size_t)j * V);
       cand[j] = draw(q + (size_t)j * V, V, greedy, seed, seq, cycle, j);
+      if (tc_i >= 0) tr->cand[(size_t)tc_i * k + j] = cand[j];
     }
     /* verify (layer.cpp:1560-1579) */
     int32_t tin[64];
@@ -930,6 +1024,9 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
     int acc = or_accept_step(p, q, cand, M, V, greedy, ngen + M < max_new, ua,
                              uf, &tok, &ties);
     for (int j = 0; j < acc; ++j) out[n++] = cand[j];
+    if (tc_i >= 0) {
+      tr->acc[tc_i] = acc; tr->tok[tc_i] = tok; tr->margin[tc_i] = g_margin;
+    }
     ngen += acc;
     local.accepted += acc;
     local.ties += ties;

@@ -96,7 +96,10 @@ int or_cache_len(const or_cache *c);
 void or_cache_truncate(or_cache *c, int len);
 
 /* TransformerDecoder::forward for one sequence of S ids; logits [S][V].
- * cache may be NULL.  Returns 0, or -1 when S_past + S > max_seq_len. */
+ * cache may be NULL.  Returns 0, or -1 when S_past + S > max_seq_len with
+ * no cache or an fp32 one; an int8 cache is not checked and grows
+ * (layer.cpp:1171-1179 reads the length from caches[0].k, which an int8
+ * cache leaves null). */
 int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
                float *logits);
 
@@ -141,6 +144,38 @@ int or_generate_speculative(const or_model *target, const or_model *draft,
                             float top_p, uint64_t seed, int quantized_cache,
                             uint32_t seq_index, int32_t *out,
                             or_spec_stats *stats);
+/* Checker hook (not restated reference behaviour): when set, every cycle of
+ * or_generate_speculative is recorded here, so that a test can compare the
+ * draft logits of each drafting step with a no-cache forward of the token
+ * sequence the reference's draft cache holds at that step
+ * (layer.cpp:1541-1545, 1632-1653).  Arrays hold max_cycles cycles of
+ * lookahead k and vocabulary V; cycles beyond max_cycles are not recorded. */
+typedef struct {
+  int max_cycles, k, V;
+  int n;             /* cycles recorded */
+  float *dlogits;    /* [max_cycles][k][V] draft logits of drafting step j */
+  int32_t *cand;     /* [max_cycles][k] drafted candidates */
+  int32_t *M;        /* [max_cycles] drafted this cycle */
+  int32_t *acc;      /* [max_cycles] accepted drafts */
+  int32_t *tok;      /* [max_cycles] resampled / bonus token, -1 if none */
+  int32_t *dstart;   /* [max_cycles] draft cache length at cycle start */
+  int32_t *tstart;   /* [max_cycles] target cache length at cycle start */
+  double *margin;    /* [max_cycles] smallest distance of a random decision
+                      * from its boundary: |r - p/q| of the accept tests,
+                      * |u - cdf edge| of the draws */
+  double first_margin;  /* the same for the first token's draw */
+} or_spec_trace;
+void or_set_spec_trace(or_spec_trace *trace);  /* NULL: recording off */
+/* The smallest decision margin (as in or_spec_trace) of the random
+ * decisions made since the last reset, e.g. by one or_accept_step; reset
+ * != 0 starts a new record. */
+double or_decision_margin(int reset);
+
+/* Threads of the oracle's Dense products and attention heads (default 1).
+ * Each output element keeps its single-thread summation order, so results
+ * do not depend on the count. */
+void or_set_threads(int n);
+
 /* generate_advanced for one sequence; out receives P + max_new ids. */
 int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
                          int max_new, float temperature, int top_k,

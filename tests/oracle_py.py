@@ -17,6 +17,17 @@ LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 _lib = None
 
 
+class SpecTrace(C.Structure):
+    _fields_ = [("max_cycles", C.c_int), ("k", C.c_int), ("V", C.c_int),
+                ("n", C.c_int), ("dlogits", C.POINTER(C.c_float)),
+                ("cand", C.POINTER(C.c_int32)), ("M", C.POINTER(C.c_int32)),
+                ("acc", C.POINTER(C.c_int32)), ("tok", C.POINTER(C.c_int32)),
+                ("dstart", C.POINTER(C.c_int32)),
+                ("tstart", C.POINTER(C.c_int32)),
+                ("margin", C.POINTER(C.c_double)),
+                ("first_margin", C.c_double)]
+
+
 class SpecStats(C.Structure):
     _fields_ = [("cycles", C.c_int64), ("drafted", C.c_int64),
                 ("accepted", C.c_int64), ("ties", C.c_int64),
@@ -85,6 +96,10 @@ def lib():
         L.or_generate_speculative.argtypes = [vp, vp, ip, i32, i32, i32, f32,
                                               i32, f32, u64, i32, u32, ip,
                                               C.POINTER(SpecStats)]
+        L.or_set_spec_trace.argtypes = [C.POINTER(SpecTrace)]
+        L.or_set_threads.argtypes = [i32]
+        L.or_decision_margin.argtypes = [i32]
+        L.or_decision_margin.restype = C.c_double
         L.or_generate_advanced.argtypes = [vp, ip, i32, i32, f32, i32, f32,
                                            u64, u32, i32, ip]
         _lib = L
@@ -268,6 +283,12 @@ def sample(probs, u):
     return lib().or_sample(fptr(probs), probs.size, float(u))
 
 
+def decision_margin(reset=True):
+    """Smallest decision margin of the oracle's random decisions since the
+    last reset (or_decision_margin)."""
+    return lib().or_decision_margin(1 if reset else 0)
+
+
 def accept_step(p, q, cand, greedy, has_bonus, u_accept, u_final):
     """or_accept_step: p [M(+1)][V], q [M][V] probability rows."""
     p = np.ascontiguousarray(p, np.float32)
@@ -296,6 +317,52 @@ def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,
     if rc != 0:
         raise RuntimeError(f"or_generate_speculative failed: {rc}")
     return out, st
+
+
+def set_threads(n):
+    """Threads of the oracle's Dense products and attention heads."""
+    lib().or_set_threads(int(n))
+
+
+def generate_speculative_traced(target, draft, prompt, max_new, k, T, seed,
+                                seq=0, max_cycles=None, **kw):
+    """generate_speculative with the oracle's per-cycle record (or_spec_trace):
+    returns (out, stats, cycles, first_margin), cycles a list of dicts with
+    the draft logits [M][V] of each drafting step, the candidates, M,
+    accepted count, resampled / bonus token, the draft / target cache
+    lengths at the start of the cycle and the cycle's smallest decision
+    margin; first_margin that of the first token's draw."""
+    V = target.vocab
+    if max_cycles is None:
+        max_cycles = max(max_new, 1)
+    arrs = dict(dlogits=np.zeros((max_cycles, k, V), np.float32),
+                cand=np.zeros((max_cycles, k), np.int32),
+                M=np.zeros(max_cycles, np.int32),
+                acc=np.zeros(max_cycles, np.int32),
+                tok=np.zeros(max_cycles, np.int32),
+                dstart=np.zeros(max_cycles, np.int32),
+                tstart=np.zeros(max_cycles, np.int32),
+                margin=np.zeros(max_cycles, np.float64))
+    tr = SpecTrace(max_cycles, k, V, 0, fptr(arrs["dlogits"]),
+                   *(iptr(arrs[n]) for n in ("cand", "M", "acc", "tok",
+                                             "dstart", "tstart")),
+                   arrs["margin"].ctypes.data_as(C.POINTER(C.c_double)), 1.0)
+    lib().or_set_spec_trace(C.byref(tr))
+    try:
+        out, st = generate_speculative(target, draft, prompt, max_new, k, T,
+                                       seed, seq=seq, **kw)
+    finally:
+        lib().or_set_spec_trace(None)
+    cycles = []
+    for c in range(tr.n):
+        M = int(arrs["M"][c])
+        cycles.append(dict(dlogits=arrs["dlogits"][c, :M].copy(),
+                           cand=arrs["cand"][c, :M].copy(), M=M,
+                           acc=int(arrs["acc"][c]), tok=int(arrs["tok"][c]),
+                           dstart=int(arrs["dstart"][c]),
+                           tstart=int(arrs["tstart"][c]),
+                           margin=float(arrs["margin"][c])))
+    return out, st, cycles, tr.first_margin
 
 
 def generate_advanced(model, prompt, max_new, T, seed, seq=0, use_cache=True,
@@ -336,3 +403,34 @@ def attention_q8(q, kq, ks, vq, vs, causal=True):
     lib().or_attention_q8(fptr(q), i8ptr(kq), fptr(ks), i8ptr(vq), fptr(vs),
                           H, Hkv, S, St, D, 1 if causal else 0, fptr(out))
     return out
+
+
+def assert_same_stream(got, want, cycles, first_margin, P, tol=1e-5,
+                       what=""):
+    """A sampled device stream equals the oracle's, or first differs inside
+    a cycle (or the first token) whose random decisions the oracle made
+    within `tol` of their boundary (|r - p/q| or |u - cdf edge|): there the
+    fp32 rounding of the two implementations may legitimately decide
+    differently.  Everything before the divergence must be equal.  Returns
+    the first differing index, or None."""
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, what
+    diff = np.nonzero(got != want)[0]
+    if len(diff) == 0:
+        return None
+    i = int(diff[0])
+    assert i >= P, f"{what}: prompt differs at {i}"
+    if i == P:
+        assert first_margin < tol, (what, i, first_margin)
+        return i
+    pos = P + 1
+    for c in cycles:
+        n = c["acc"] + (1 if c["tok"] >= 0 else 0)
+        if pos <= i < pos + n:
+            assert c["margin"] < tol, (
+                f"{what}: streams differ at {i} in a cycle whose closest "
+                f"decision is {c['margin']:.3g} from its boundary")
+            return i
+        pos += n
+    raise AssertionError(f"{what}: divergence at {i} beyond the record")

@@ -308,6 +308,38 @@ def test_max_seq_len_throws():
         t.forward(list(range(8)) * 9)
 
 
+def test_int8_cache_skips_the_length_check():
+    """layer.cpp:1171-1179 reads S_past from caches[0].k, which an int8
+    cache leaves null: the check never fires and the cache grows past
+    max_seq_len, while an fp32 cache throws at the same length.
+    Past max_seq_len the int8-cache forward equals a no-cache forward of
+    the same ids on a model with room (attention over the dequantised
+    rows within 0.08, gqa_test.cpp:213-265's bound)."""
+    vocab = 8
+    tp = O.make_params(vocab, 16, 2, 32, 2, 11, std=0.3)
+    small = O.Model(vocab, 16, 2, 32, 2, 16, tp)
+    big = O.Model(vocab, 16, 2, 32, 2, 64, tp)
+    ids = [i * 5 % vocab for i in range(24)]
+    c8 = O.Cache(small, quantized=True)
+    parts = [small.forward(ids[:10], c8), small.forward(ids[10:20], c8),
+             small.forward(ids[20:], c8)]
+    assert len(c8) == 24
+    np.testing.assert_allclose(np.concatenate(parts), big.forward(ids),
+                               atol=0.08)
+    c32 = O.Cache(small)
+    small.forward(ids[:10], c32)
+    with pytest.raises(RuntimeError):
+        small.forward(ids[10:20], c32)
+    # the speculative loop: the int8 run completes, the fp32 one fails
+    d = O.Model(vocab, 16, 2, 32, 1, 16,
+                O.make_params(vocab, 16, 2, 32, 1, 12, std=0.3))
+    out, _ = O.generate_speculative(small, d, [1, 2, 3], 20, 3, 0.0, 42,
+                                    quantized_cache=True)
+    assert len(out) == 23
+    with pytest.raises(RuntimeError):
+        O.generate_speculative(small, d, [1, 2, 3], 20, 3, 0.0, 42)
+
+
 @pytest.mark.parametrize("quant", [False, True])
 @pytest.mark.parametrize("k", [1, 3, 4])
 def test_greedy_spec_equals_ar(quant, k):
@@ -319,6 +351,105 @@ def test_greedy_spec_equals_ar(quant, k):
         np.testing.assert_array_equal(sp, ar)
         assert len(sp) == len(prompt) + 12
         assert st.accepted + st.resampled + st.bonus + 1 == 12
+
+
+def _trace_draft_cache(prompt, first, cycles, draft, what):
+    """Hand trace of the reference's draft cache (layer.cpp:1541-1545,
+    1632-1653), written as the explicit token sequence it holds: the draft
+    prefill holds the prompt; drafting step j of a cycle appends
+    generated.back() (j = 0) or c_{j-1}; a rejection at r truncates it to
+    dstart + r + 1 and appends the recovered token, which the next cycle
+    appends again as generated.back(); full acceptance with a bonus appends
+    c_{M-1}.  Each drafting step's logits must be those of a no-cache
+    forward over that sequence (positions = indices).  Returns what kinds of
+    cycle ends were seen and how far the duplicate moved the logits."""
+    dseq = list(prompt)
+    gen = list(prompt) + [first]
+    kinds, dup_effect = set(), 0.0
+    prev_rej = None
+    for ci, cyc in enumerate(cycles):
+        assert cyc["dstart"] == len(dseq), (what, ci)
+        assert cyc["tstart"] == len(gen) - 1, (what, ci)
+        if prev_rej is not None:
+            # after a rejection at r: dstart' = dstart + r + 2, and the
+            # recovered token is fed again at the next position
+            dstart0, r, rec = prev_rej
+            assert cyc["dstart"] == dstart0 + r + 2, (what, ci)
+            assert dseq[-1] == rec and gen[-1] == rec
+        for j in range(cyc["M"]):
+            dseq.append(gen[-1] if j == 0 else int(cyc["cand"][j - 1]))
+            want = draft.forward(dseq)[-1]
+            np.testing.assert_allclose(cyc["dlogits"][j], want, rtol=1e-5,
+                                       atol=1e-6, err_msg=f"{what} {ci} {j}")
+            if j == 0 and prev_rej is not None:
+                # the sequence without the duplicate gives other logits
+                alt = draft.forward(dseq[:-2] + dseq[-1:])[-1]
+                dup_effect = max(dup_effect, float(np.abs(alt - want).max()))
+        acc, tok, M = cyc["acc"], cyc["tok"], cyc["M"]
+        gen += [int(c) for c in cyc["cand"][:acc]]
+        prev_rej = None
+        if acc < M:
+            dseq = dseq[:cyc["dstart"] + acc + 1] + [tok]
+            gen.append(tok)
+            kinds.add("reject@0" if acc == 0 else "reject@j")
+            prev_rej = (cyc["dstart"], acc, tok)
+        elif tok >= 0:
+            dseq.append(int(cyc["cand"][M - 1]))
+            gen.append(tok)
+            kinds.add("bonus")
+    return gen, kinds, dup_effect
+
+
+@pytest.mark.parametrize("T", [1.0, 0.0])
+def test_draft_cache_duplicate_rule_hand_traced(T):
+    """The oracle's draft-side state pinned by a hand trace of
+    the reference: after a rejection the draft cache holds the recovered
+    token twice and later draft positions drift by one
+    (layer.cpp:1541-1545, 1632-1642); after full acceptance it does not
+    (layer.cpp:1649-1653).  A draft close to the target (its weights the
+    target's plus noise) gives rejections at j = 0 and j > 0 and full
+    acceptances in one run."""
+    vocab, d_, H, F = 16, 16, 2, 32
+    tp = O.make_params(vocab, d_, H, F, 2, 31, std=0.3)
+    rng = np.random.default_rng(5)
+    dp = [p + (rng.standard_normal(p.shape).astype(np.float32) *
+               np.float32(0.05) if p.ndim == 2 and p.shape[0] > 1 else 0)
+          for p in tp]
+    dp = [np.ascontiguousarray(p, np.float32) for p in dp]
+    t = O.Model(vocab, d_, H, F, 2, 256, tp)
+    dm = O.Model(vocab, d_, H, F, 2, 256, dp)
+    prompt = [3, 1, 4, 1, 5]
+    kinds_all, effect = set(), 0.0
+    for seed in (42, 7, 99):
+        out, st, cycles, _ = O.generate_speculative_traced(t, dm, prompt, 40,
+                                                           3, T, seed)
+        gen, kinds, eff = _trace_draft_cache(prompt, int(out[len(prompt)]),
+                                             cycles, dm, f"seed {seed}")
+        np.testing.assert_array_equal(gen, out)
+        assert len(cycles) == st.cycles
+        kinds_all |= kinds
+        effect = max(effect, eff)
+    want = {"reject@0", "reject@j", "bonus"} if T > 0 else {"reject@0"}
+    assert want <= kinds_all, kinds_all
+    # a restatement without the duplicate would fail the check above
+    assert effect > 1e-3, effect
+
+
+def test_threads_do_not_change_results():
+    """or_set_threads splits only independent outputs: logits and a sampled
+    run are bit-identical for 1 and 4 threads."""
+    t, d = tiny_models(vocab=64)
+    try:
+        O.set_threads(1)
+        a = t.forward(list(range(20)))
+        sa, _ = O.generate_speculative(t, d, [1, 2, 3], 10, 3, 1.0, 42)
+        O.set_threads(4)
+        b = t.forward(list(range(20)))
+        sb, _ = O.generate_speculative(t, d, [1, 2, 3], 10, 3, 1.0, 42)
+    finally:
+        O.set_threads(1)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(sa, sb)
 
 
 def test_sampled_same_seed_same_output():
