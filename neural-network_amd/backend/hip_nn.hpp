@@ -1,0 +1,106 @@
+// Drop-in device counterparts of the reference's decoder objects, over
+// libnnhip.so's C ABI (include/nnhip.h).  Compiled against the reference's
+// headers; a program using them links the reference's own nn / core
+// sources, as any other user of TransformerDecoder does.
+//
+//   reference                                   here
+//   TransformerDecoder (layer.hpp:299-330)       HipDecoder (mirrors one by
+//                                                its parameters())
+//   TransformerDecoder::forward(x, caches)       HipDecoder::forward(ids,
+//     (layer.cpp:1161-1193)                      HipKVCache *)
+//   KVCache / KVCache::truncate (layer.hpp:      HipKVCache / truncate
+//     212-230, layer.cpp:67-149)
+//   quantize_model (quantization.hpp:43) over    HipDecoder::quantize
+//     every Dense of the decoder
+//   QuantizedDense::forward (quantization.cpp:   HipQuantizedDense::forward
+//     127-147)
+//   generate_advanced (layer.hpp:310-316)        HipDecoder::generate_advanced
+//   generate_speculative (layer.hpp:318-323)     HipDecoder::generate_speculative
+//
+// Sampled generation draws from a counter-based Philox stream keyed by the
+// seed instead of std::mt19937 (greedy output is the reference's).
+#pragma once
+
+#include "hip_backend.hpp"
+#include "nn/layer.hpp"
+#include "nn/quantization.hpp"
+
+#include <memory>
+#include <vector>
+
+namespace nnhip_backend {
+
+// TransformerDecoder's constructor arguments (layer.hpp:300-302), which the
+// decoder does not expose
+struct DecoderConfig {
+  size_t vocab_size, embed_dim, num_heads, dim_feedforward, num_layers,
+      max_seq_len;
+};
+
+class HipKVCache;
+
+class HipDecoder {
+ public:
+  // copies d.parameters() (layer.cpp:1140-1154, same order) to the device
+  HipDecoder(HipBackend &backend, TransformerDecoder &d,
+             const DecoderConfig &cfg);
+  ~HipDecoder();
+  HipDecoder(const HipDecoder &) = delete;
+  HipDecoder &operator=(const HipDecoder &) = delete;
+
+  // every Dense (q, k, v, o, gate, up, down, lm_head) to symmetric int8 per
+  // output channel with the QuantizedDense formula (quantization.cpp:36-66)
+  void quantize();
+  // logits [S][V] of one sequence of ids [S]; cache may be null
+  std::vector<float> forward(const std::vector<size_t> &ids,
+                             HipKVCache *cache);
+  std::vector<size_t> generate_advanced(const std::vector<size_t> &prompt,
+                                        size_t max_new_tokens,
+                                        float temperature = 1.0f,
+                                        size_t top_k = 0, float top_p = 1.0f,
+                                        unsigned int seed = 42,
+                                        bool use_kv_cache = true);
+  std::vector<size_t>
+  generate_speculative(HipDecoder *draft_model,
+                       const std::vector<size_t> &prompt, size_t max_new_tokens,
+                       size_t lookahead = 4, float temperature = 1.0f,
+                       size_t top_k = 0, float top_p = 1.0f,
+                       unsigned int seed = 42, bool quantized_cache = false);
+  [[nodiscard]] nnhip_model *handle() const noexcept { return m_; }
+  [[nodiscard]] const DecoderConfig &config() const noexcept { return cfg_; }
+
+ private:
+  nnhip_model *m_ = nullptr;
+  DecoderConfig cfg_;
+};
+
+// KVCache(quantized) for one sequence of a HipDecoder
+class HipKVCache {
+ public:
+  HipKVCache(HipDecoder &model, bool quantized = false);
+  ~HipKVCache();
+  HipKVCache(const HipKVCache &) = delete;
+  HipKVCache &operator=(const HipKVCache &) = delete;
+  void truncate(size_t len);
+  [[nodiscard]] size_t length() const;
+  [[nodiscard]] nnhip_kvcache *handle() const noexcept { return c_; }
+
+ private:
+  nnhip_kvcache *c_ = nullptr;
+};
+
+// QuantizedDense (INT8) with its codes and scales resident on the device;
+// forward runs on tensors whose storage belongs to `backend`.
+class HipQuantizedDense {
+ public:
+  HipQuantizedDense(HipBackend &backend, const QuantizedDense &layer);
+  // y [rows, out] = x [rows, in] . (codes * scales) + bias, x contiguous
+  std::shared_ptr<Tensor> forward(const std::shared_ptr<Tensor> &input);
+
+ private:
+  HipBackend &be_;
+  size_t in_ = 0, out_ = 0;
+  std::unique_ptr<DeviceBuffer> codes_, scales_, bias_;  // codes [out][in]
+};
+
+}  // namespace nnhip_backend

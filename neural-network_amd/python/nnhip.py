@@ -31,6 +31,39 @@ class SpecTiming(C.Structure):
                 ("cycles_launched", C.c_int64)]
 
 
+MAX_RANK = 8
+OP_ADD, OP_SUB, OP_MUL, OP_DIV = 0, 1, 2, 3
+(OP_RELU_BACKWARD, OP_SIGMOID_BACKWARD, OP_TANH_BACKWARD, OP_SQRT_BACKWARD,
+ OP_LOG_BACKWARD) = 4, 5, 6, 7, 8
+OP_RELU, OP_SIGMOID, OP_TANH, OP_SQRT, OP_LOG = 16, 17, 18, 19, 20
+
+
+class View(C.Structure):
+    """nnhip_view: a dev buffer, an element offset, shape and strides."""
+    _fields_ = [("data", C.c_void_p), ("offset", C.c_int64),
+                ("rank", C.c_int32), ("shape", C.c_int64 * MAX_RANK),
+                ("strides", C.c_int64 * MAX_RANK)]
+
+
+def view(arr, shape=None, strides=None, offset=0):
+    """A View of DeviceArray `arr`: its own shape and row-major strides, or
+    the given ones (elements)."""
+    shape = tuple(arr.shape if shape is None else shape)
+    if strides is None:
+        strides, acc = [], 1
+        for n in reversed(shape):
+            strides.insert(0, acc)
+            acc *= n
+    v = View()
+    v.data = arr.p
+    v.offset = offset
+    v.rank = len(shape)
+    for i, (n, st) in enumerate(zip(shape, strides)):
+        v.shape[i] = n
+        v.strides[i] = st
+    return v
+
+
 # name -> argument types (all functions return int status unless listed)
 _vp, _i, _i64, _u32, _u64, _f, _sz = (C.c_void_p, C.c_int, C.c_int64,
                                       C.c_uint32, C.c_uint64, C.c_float,
@@ -90,6 +123,21 @@ SIGNATURES = {
     "nnhip_sample_rows": [_vp, _vp, _i, _i, _f, _i, _f, _vp, _vp, _vp],
     "nnhip_spec_accept": [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp,
                           _vp],
+    "nnhip_binary_f32": [_vp, _i, C.POINTER(View), C.POINTER(View),
+                         C.POINTER(View)],
+    "nnhip_unary_f32": [_vp, _i, C.POINTER(View), C.POINTER(View)],
+    "nnhip_matmul_f32": [_vp, C.POINTER(View), C.POINTER(View),
+                         C.POINTER(View)],
+    "nnhip_sum_f32": [_vp, C.POINTER(View), C.POINTER(View),
+                      C.POINTER(C.c_int64), _i],
+    "nnhip_softmax_f32": [_vp, C.POINTER(View), C.POINTER(View), _i],
+    "nnhip_softmax_backward_f32": [_vp, C.POINTER(View), C.POINTER(View),
+                                   C.POINTER(View), _i],
+    "nnhip_embedding_f32": [_vp, C.POINTER(View), C.POINTER(View),
+                            C.POINTER(View)],
+    "nnhip_slice_backward_f32": [_vp, C.POINTER(View), C.POINTER(View), _i,
+                                 _i64],
+    "nnhip_fill_f32": [_vp, _vp, _sz, _f],
     "nnhip_bench_attention": [_vp, _i, _i, _i, _i, _i, _i, _i, _i,
                               C.POINTER(C.c_float)],
     "nnhip_bench_spec_accept": [_vp, _i, _i, _i, _f, _i, _i,

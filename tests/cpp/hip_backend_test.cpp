@@ -1,0 +1,296 @@
+// HipBackend (neural-network_amd/backend) driven through the reference's
+// ExecutionBackend interface exactly as its Tensor does: each op allocates
+// its output with backend->allocate, sets the dtype, takes row-major strides
+// from compute_strides and passes (storage, offset, shape, strides) of every
+// operand (src/core/tensor.cpp:392-428 matmul, :430-490 sum, :677-711
+// softmax, :915-967 embedding; add / sub / mul / div via the broadcast shape
+// of the operands).  Checked against the reference's own known answers
+// (tests/core/tensor_test.cpp, tests/nn/layer_test.cpp), the oracle
+// (or_dense, or_layernorm) and closed forms.  Needs a GPU; prints one line a
+// check and exits non-zero on the first failure.
+#include "backend/hip_backend.hpp"  // neural-network_amd/backend
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+extern "C" {
+// the oracle (tests' checker, oracle/oracle.h)
+void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
+              const float *w, const int8_t *codes, const float *scales,
+              const float *bias, float *y);
+void or_layernorm(const float *x, int64_t rows, int64_t n, const float *gamma,
+                  const float *beta, float eps, float *y);
+}
+
+using nnhip_backend::HipBackend;
+
+namespace {
+
+int g_checks = 0;
+
+void expect(bool ok, const std::string &what) {
+  ++g_checks;
+  if (!ok) {
+    std::printf("FAIL %s\n", what.c_str());
+    std::fflush(stdout);
+    std::exit(1);
+  }
+}
+
+// A tensor as the reference's Tensor holds one: shared storage, offset,
+// shape and strides.
+struct T {
+  std::shared_ptr<DeviceBuffer> buf;
+  Shape shape;
+  Strides strides;
+  size_t offset = 0;
+};
+
+T make(ExecutionBackend &be, const Shape &shape, const std::vector<float> &v) {
+  T t;
+  t.shape = shape;
+  t.strides = compute_strides(shape);
+  t.buf = be.allocate(count_elements(shape) * sizeof(float));
+  t.buf->set_dtype(DataType::FP32);
+  if (!v.empty()) be.copy_host_to_device(v.data(), *t.buf, v.size() * sizeof(float));
+  return t;
+}
+
+std::vector<float> host(ExecutionBackend &be, const T &t) {
+  // contiguous, offset 0 (outputs of the ops below)
+  std::vector<float> h(count_elements(t.shape));
+  be.copy_device_to_host(*t.buf, h.data(), h.size() * sizeof(float));
+  return h;
+}
+
+// the transpose view of Tensor::transpose (swapped shape and strides)
+T transposed(const T &t) {
+  T r = t;
+  std::swap(r.shape[0], r.shape[1]);
+  std::swap(r.strides[0], r.strides[1]);
+  return r;
+}
+
+Shape broadcast(const Shape &a, const Shape &b) {
+  const size_t n = std::max(a.size(), b.size());
+  Shape o(n);
+  for (size_t i = 0; i < n; ++i) {
+    const size_t da = i + a.size() >= n ? a[i + a.size() - n] : 1;
+    const size_t db = i + b.size() >= n ? b[i + b.size() - n] : 1;
+    o[i] = std::max(da, db);
+  }
+  return o;
+}
+
+enum Bin { kAdd, kSub, kMul, kDiv };
+T binary(ExecutionBackend &be, Bin op, const T &a, const T &b) {
+  T o = make(be, broadcast(a.shape, b.shape), {});
+  auto f = op == kAdd ? &ExecutionBackend::add
+           : op == kSub ? &ExecutionBackend::sub
+           : op == kMul ? &ExecutionBackend::mul
+                        : &ExecutionBackend::div;
+  (be.*f)(*a.buf, a.offset, a.shape, a.strides, *b.buf, b.offset, b.shape,
+          b.strides, *o.buf, 0, o.shape, o.strides);
+  return o;
+}
+
+T matmul(ExecutionBackend &be, const T &a, const T &b) {
+  T o = make(be, {a.shape[0], b.shape[1]}, {});
+  be.matmul(*a.buf, a.offset, a.shape, a.strides, *b.buf, b.offset, b.shape,
+            b.strides, *o.buf, 0, o.shape, o.strides);
+  return o;
+}
+
+T sum(ExecutionBackend &be, const T &a, const std::vector<size_t> &axes,
+      bool keep) {
+  Shape os;
+  for (size_t i = 0; i < a.shape.size(); ++i) {
+    bool summed = false;
+    for (size_t ax : axes) summed |= ax == i;
+    if (!summed) os.push_back(a.shape[i]);
+    else if (keep) os.push_back(1);
+  }
+  T o = make(be, os, {});
+  be.sum(*a.buf, a.offset, a.shape, a.strides, *o.buf, 0, o.shape, o.strides,
+         axes);
+  return o;
+}
+
+T softmax(ExecutionBackend &be, const T &a, size_t axis) {
+  T o = make(be, a.shape, {});
+  be.softmax(*a.buf, a.offset, a.shape, a.strides, *o.buf, 0, o.shape,
+             o.strides, axis);
+  return o;
+}
+
+T sqrt_(ExecutionBackend &be, const T &a) {
+  T o = make(be, a.shape, {});
+  be.sqrt(*a.buf, a.offset, a.shape, a.strides, *o.buf, 0, o.shape, o.strides);
+  return o;
+}
+
+std::vector<float> randn(size_t n, unsigned seed, float sd = 1.0f) {
+  std::mt19937 g(seed);
+  std::normal_distribution<float> d(0.0f, sd);
+  std::vector<float> v(n);
+  for (auto &x : v) x = d(g);
+  return v;
+}
+
+void test_tensor_known_answers(ExecutionBackend &be) {
+  // TensorTest.MatmulContiguous (tensor_test.cpp:82-94)
+  T a = make(be, {2, 3}, {1, 2, 3, 4, 5, 6});
+  T b = make(be, {3, 2}, {7, 8, 9, 10, 11, 12});
+  expect(host(be, matmul(be, a, b)) == std::vector<float>{58, 64, 139, 154},
+         "matmul known answer");
+  // TensorTest.BroadcastingAdd (tensor_test.cpp:53-67)
+  T c = make(be, {1, 3}, {10, 20, 30});
+  expect(host(be, binary(be, kAdd, a, c)) ==
+             std::vector<float>{11, 22, 33, 14, 25, 36},
+         "broadcasting add");
+  // TensorTest.ElementwiseSubAndMul (tensor_test.cpp:69-80)
+  T s = make(be, {2}, {10, 20}), t = make(be, {2}, {2, 5});
+  expect(host(be, binary(be, kSub, s, t)) == std::vector<float>{8, 15}, "sub");
+  expect(host(be, binary(be, kMul, s, t)) == std::vector<float>{20, 100}, "mul");
+  // TensorTest.SumReduction (tensor_test.cpp:97-118)
+  T all = sum(be, a, {0, 1}, false);
+  expect(all.shape.empty() && host(be, all) == std::vector<float>{21}, "sum all");
+  expect(host(be, sum(be, a, {0}, false)) == std::vector<float>{5, 7, 9},
+         "sum axis 0");
+  T row = sum(be, a, {1}, true);
+  expect(row.shape == Shape({2, 1}) && host(be, row) == std::vector<float>{6, 15},
+         "sum axis 1 keep dims");
+  // the reference's matmul error text (cpu_backend.cpp:339-342)
+  bool threw = false;
+  try {
+    matmul(be, a, a);
+  } catch (const std::runtime_error &e) {
+    threw = std::string(e.what()).find("Incompatible shapes") != std::string::npos;
+  }
+  expect(threw, "matmul shape error");
+  std::printf("ok tensor known answers\n");
+}
+
+void test_matmul_vs_oracle(ExecutionBackend &be) {
+  const size_t M = 67, K = 130, N = 45;
+  const auto av = randn(M * K, 1), bv = randn(K * N, 2);
+  T a = make(be, {M, K}, av), b = make(be, {K, N}, bv);
+  std::vector<float> want(M * N);
+  or_dense(av.data(), M, K, N, bv.data(), nullptr, nullptr, nullptr, want.data());
+  expect(host(be, matmul(be, a, b)) == want, "matmul == or_dense");
+  // a^T stored, viewed transposed (Tensor::transpose): same values
+  std::vector<float> at(K * M);
+  for (size_t r = 0; r < M; ++r)
+    for (size_t k = 0; k < K; ++k) at[k * M + r] = av[r * K + k];
+  T atd = make(be, {K, M}, at);
+  expect(host(be, matmul(be, transposed(atd), b)) == want,
+         "matmul of a transposed view == or_dense");
+  std::printf("ok matmul vs oracle (%zux%zux%zu)\n", M, K, N);
+}
+
+void test_layernorm_vs_oracle(ExecutionBackend &be) {
+  // LayerNorm::forward's op sequence (layer.cpp:242-261) on the backend:
+  // sum / div / sub / mul / sum / div / add / sqrt / div / mul / add
+  const size_t R = 9, D = 256;
+  const float eps = 1e-5f;
+  const auto xv = randn(R * D, 3, 2.0f);
+  auto gv = randn(D, 4), bv = randn(D, 5);
+  T x = make(be, {R, D}, xv), gamma = make(be, {D}, gv), beta = make(be, {D}, bv);
+  T n_t = make(be, {}, {static_cast<float>(D)}), eps_t = make(be, {}, {eps});
+  T mean = binary(be, kDiv, sum(be, x, {1}, true), n_t);
+  T diff = binary(be, kSub, x, mean);
+  T var = binary(be, kDiv, sum(be, binary(be, kMul, diff, diff), {1}, true), n_t);
+  T sd = sqrt_(be, binary(be, kAdd, var, eps_t));
+  T y = binary(be, kAdd, binary(be, kMul, binary(be, kDiv, diff, sd), gamma), beta);
+  std::vector<float> want(R * D);
+  or_layernorm(xv.data(), R, D, gv.data(), bv.data(), eps, want.data());
+  expect(host(be, y) == want, "LayerNorm through backend ops == or_layernorm");
+  // LayerNormTest (layer_test.cpp:56-80): [1, 2, 3] -> -1.2247, 0, 1.2247
+  T x3 = make(be, {1, 3}, {1, 2, 3});
+  T n3 = make(be, {}, {3.0f});
+  T m3 = binary(be, kDiv, sum(be, x3, {1}, true), n3);
+  T d3 = binary(be, kSub, x3, m3);
+  T v3 = binary(be, kDiv, sum(be, binary(be, kMul, d3, d3), {1}, true), n3);
+  T y3 = binary(be, kDiv, d3, sqrt_(be, binary(be, kAdd, v3, eps_t)));
+  const auto h3 = host(be, y3);
+  expect(std::fabs(h3[0] + 1.2247f) < 1e-3f && std::fabs(h3[1]) < 1e-6f &&
+             std::fabs(h3[2] - 1.2247f) < 1e-3f,
+         "LayerNorm known answer");
+  std::printf("ok layernorm vs oracle\n");
+}
+
+void test_softmax_and_embedding(ExecutionBackend &be) {
+  const size_t R = 5, V = 3000;
+  const auto lv = randn(R * V, 6, 3.0f);
+  T l = make(be, {R, V}, lv);
+  const auto p = host(be, softmax(be, l, 1));
+  double worst = 0.0;
+  for (size_t r = 0; r < R; ++r) {
+    double mx = -1e300, s = 0.0;
+    for (size_t v = 0; v < V; ++v) mx = std::max(mx, (double)lv[r * V + v]);
+    for (size_t v = 0; v < V; ++v) s += std::exp((double)lv[r * V + v] - mx);
+    for (size_t v = 0; v < V; ++v) {
+      const double w = std::exp((double)lv[r * V + v] - mx) / s;
+      worst = std::max(worst, std::fabs(p[r * V + v] - w) / w);
+    }
+  }
+  expect(worst <= 2e-6, "softmax within 2e-6 of float64");
+  // Tensor::embedding (tensor.cpp:915-967): ids stored as fp32, out of
+  // range -> row 0 (cpu_backend.cpp:1022-1025)
+  const size_t Vw = 40, Dw = 12;
+  const auto wv = randn(Vw * Dw, 7);
+  T w = make(be, {Vw, Dw}, wv);
+  const std::vector<float> ids = {3, 39, 40, 1e6f, -2, 7.9f};
+  T idx = make(be, {2, 3}, ids);
+  T out = make(be, {2, 3, Dw}, {});
+  be.embedding(*w.buf, 0, w.shape, w.strides, *idx.buf, 0, idx.shape,
+               idx.strides, *out.buf, 0, out.shape, out.strides);
+  const auto o = host(be, out);
+  const size_t rows[6] = {3, 39, 0, 0, 0, 7};
+  bool same = true;
+  for (size_t i = 0; i < 6; ++i)
+    for (size_t d = 0; d < Dw; ++d) same &= o[i * Dw + d] == wv[rows[i] * Dw + d];
+  expect(same, "embedding gather");
+  std::printf("ok softmax and embedding\n");
+}
+
+void test_fill_and_unsupported(ExecutionBackend &be) {
+  T a = make(be, {4, 4}, {});
+  be.fill(*a.buf, 1.5f);
+  bool ok = true;
+  for (float v : host(be, a)) ok &= v == 1.5f;
+  expect(ok, "fill");
+  bool threw = false;
+  try {
+    be.maxpool2d(*a.buf, 0, a.shape, a.strides, *a.buf, 0, a.shape, a.strides,
+                 2, 2, 2);
+  } catch (const std::runtime_error &) {
+    threw = true;
+  }
+  expect(threw, "maxpool2d reports it is unsupported");
+  std::printf("ok fill and unsupported ops\n");
+}
+
+}  // namespace
+
+int main() {
+  try {
+    HipBackend hip(0);
+    ExecutionBackend &be = hip;
+    test_tensor_known_answers(be);
+    test_matmul_vs_oracle(be);
+    test_layernorm_vs_oracle(be);
+    test_softmax_and_embedding(be);
+    test_fill_and_unsupported(be);
+  } catch (const std::exception &e) {
+    std::printf("FAIL exception: %s\n", e.what());
+    return 1;
+  }
+  std::printf("all %d checks passed\n", g_checks);
+  return 0;
+}
