@@ -23,6 +23,10 @@
 
 #include <hip/hip_runtime.h>
 
+// Every product and sum below is rounded on its own, as in the reference's
+// scalar loops (no multiply-add is fused).
+#pragma clang fp contract(off)
+
 namespace nnhip {
 
 namespace {
@@ -44,9 +48,9 @@ __device__ __forceinline__ float apply_binary(int op, float a, float b) {
     // backward ops: a is the forward input or output, b the upstream gradient
     // (cpu_backend.cpp:473-481, 492-502, 513-521, 659-669, 680-690)
     case kOpReluBack: return a > 0.0f ? b : 0.0f;
-    case kOpSigmoidBack: return __fmul_rn(__fmul_rn(b, a), 1.0f - a);
-    case kOpTanhBack: return __fmul_rn(b, 1.0f - __fmul_rn(a, a));
-    case kOpSqrtBack: return __fmul_rn(b, 0.5f / (a + 1e-8f));
+    case kOpSigmoidBack: return (b * a) * (1.0f - a);
+    case kOpTanhBack: return b * (1.0f - a * a);
+    case kOpSqrtBack: return b * (0.5f / (a + 1e-8f));
     default: return b / (a + 1e-8f);  // kOpLogBack
   }
 }
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(kBlock) void matmul_kernel(
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+          acc[i][j] = acc[i][j] + av[i] * bv[j];
     }
     __syncthreads();
   }
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void sum_kernel(
         off += (u % din.shape[d]) * din.stride[d];
         u /= din.shape[d];
       }
-      acc = __fadd_rn(acc, in[off]);
+      acc = acc + in[off];
     }
     o[operand_offset(i, dout, dout)] = acc;
   }

@@ -320,6 +320,57 @@ def test_attention_kq(ctx, B, S, H, D, pos0, w4):
                           out.reshape(S, H * D), 1e-4, f"attention seq {b}")
 
 
+# grouped-query attention (MultiHeadAttention's num_kv_heads, layer.cpp:
+# 862-864: query head h reads kv head h / (H / H_kv)): the shapes of
+# gqa_test.cpp:115-211 (4 heads on 2 kv heads, B = 2 x 3 queries, and one
+# query over a growing cache) at head dim 8 (the device's smallest), the
+# batch-32 verify shape on 4 kv heads, and multi-query attention (H_kv = 1)
+GQA_CASES = [(2, 3, 4, 2, 8, [0, 0]), (1, 1, 4, 2, 8, [1]),
+             (3, 6, 16, 4, 64, [100, 300, 7]), (2, 8, 8, 1, 64, [2048, 17])]
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("B,S,H,Hkv,D,pos0", GQA_CASES)
+def test_attention_gqa(ctx, B, S, H, Hkv, D, pos0, q8):
+    """Grouped-query attention over fp32 and int8 caches against the
+    oracle's or_attention / or_attention_q8 with H_kv < H."""
+    rng = np.random.default_rng(B * 1000 + H * 10 + Hkv + q8)
+    pos0 = np.array(pos0, np.int32)
+    cap = int(pos0.max()) + S
+    q = rng.standard_normal((B * S, H * D)).astype(np.float32)
+    dq, dp = ctx.array(q), ctx.array(pos0)
+    do = ctx.array(shape=(B * S, H * D))
+    if q8:
+        kq = rng.integers(-127, 128, (B, Hkv, cap, D)).astype(np.int8)
+        vq = rng.integers(-127, 128, (B, Hkv, cap, D)).astype(np.int8)
+        ks = (rng.random((B, Hkv, cap)) * 0.03 + 0.001).astype(np.float32)
+        vs = (rng.random((B, Hkv, cap)) * 0.03 + 0.001).astype(np.float32)
+        dk, dv, dks, dvs = ctx.array(kq), ctx.array(vq), ctx.array(ks), ctx.array(vs)
+        call("nnhip_attention_kq_q8", ctx.h, dq.p, dk.p, dks.p, dv.p, dvs.p,
+             cap, dp.p, B, S, H, Hkv, D, do.p)
+    else:
+        k = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+        v = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+        dk, dv = ctx.array(k), ctx.array(v)
+        call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H,
+             Hkv, D, do.p)
+    got = do.numpy()
+    for b in range(B):
+        St = int(pos0[b]) + S
+        qb = np.ascontiguousarray(q[b * S:(b + 1) * S].reshape(S, H, D)
+                                  .transpose(1, 0, 2))
+        if q8:
+            out = O.attention_q8(qb, kq[b, :, :St], ks[b, :, :St],
+                                 vq[b, :, :St], vs[b, :, :St])
+        else:
+            out = np.zeros((S, H, D), np.float32)
+            O.lib().or_attention(O.fptr(qb), O.fptr(np.ascontiguousarray(k[b, :, :St])),
+                                 O.fptr(np.ascontiguousarray(v[b, :, :St])), H,
+                                 Hkv, S, St, D, 1, O.fptr(out))
+        assert_rows_close(got[b * S:(b + 1) * S].reshape(S, H * D),
+                          out.reshape(S, H * D), 1e-4, f"gqa seq {b}")
+
+
 @pytest.mark.parametrize("D", [64, 32, 8])
 def test_rope_kv_append_q8(ctx, D):
     """RoPE + int8 append: q bit-exact with or_rope, codes and scales

@@ -223,6 +223,30 @@ def test_attention_vs_float64(S, St):
                                atol=1e-5)
 
 
+@pytest.mark.parametrize("H,Hkv", [(4, 2), (8, 1), (6, 3)])
+def test_attention_gqa_equals_repeated_kv_heads(H, Hkv):
+    """Grouped-query attention (layer.cpp:862-864, h_kv = h / (H / H_kv)):
+    equal, bit for bit, to full multi-head attention over the kv heads
+    repeated H / H_kv times each (head h reading copy h); the modular
+    mapping h % H_kv would fail this."""
+    rng = np.random.default_rng(H * 10 + Hkv)
+    S, St, D = 3, 11, 8
+    q = rng.standard_normal((H, S, D)).astype(np.float32)
+    k = rng.standard_normal((Hkv, St, D)).astype(np.float32)
+    v = rng.standard_normal((Hkv, St, D)).astype(np.float32)
+    out = np.zeros((S, H, D), np.float32)
+    O.lib().or_attention(O.fptr(q), O.fptr(k), O.fptr(v), H, Hkv, S, St, D, 1,
+                         O.fptr(out))
+    kr = np.ascontiguousarray(np.repeat(k, H // Hkv, axis=0))
+    vr = np.ascontiguousarray(np.repeat(v, H // Hkv, axis=0))
+    full = np.zeros((S, H, D), np.float32)
+    O.lib().or_attention(O.fptr(q), O.fptr(kr), O.fptr(vr), H, H, S, St, D, 1,
+                         O.fptr(full))
+    np.testing.assert_array_equal(out, full)
+    np.testing.assert_allclose(out, attn_f64(q, kr, vr, True), rtol=1e-5,
+                               atol=1e-5)
+
+
 # --------------------------------------------------------------------------
 # get_probs / sample_token
 # --------------------------------------------------------------------------
