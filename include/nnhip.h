@@ -238,6 +238,20 @@ int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
                                  float *ln_out, const int8_t *codes,
                                  const float *scales, const float *bias, int N,
                                  float *y);
+/* nnhip_linear_w8a32 without any allocation.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, paths and results; its scratch (the codes in the MFMA operand
+ * layout, digit planes, row exponents: N*K + 3*K*rows64 + 4*rows64 bytes,
+ * rows64 = rows rounded up to 64) lives in one fixed 32 MiB device array per
+ * GPU, held until the process ends; larger calls return NNHIP_EARG.  The
+ * GEMV path (path 1, or path 0 below 16 rows) uses no scratch.  Stream-
+ * ordered, no synchronisation.  Calls that overlap on one GPU (contexts on
+ * different streams) race on the shared array. */
+int nnhip_linear_w8a32_noalloc(nnhip_ctx *ctx, const float *x, int rows,
+                               int K, const int8_t *codes,
+                               const float *scales, const float *bias, int N,
+                               float *y, int path);
 /* Dense::forward (layer.cpp:162-171) with w [N][K] fp32 (transposed). */
 int nnhip_linear_f32(nnhip_ctx *ctx, const float *x, int rows, int K,
                      const float *w, const float *bias, int N, float *y);

@@ -43,6 +43,7 @@ int nnhip_init(int device, nnhip_ctx **out) {
     NNHIP_CHECK(hipGetDeviceCount(&n));
     REQ(device >= 0 && device < n, "nnhip_init: no such device");
     NNHIP_CHECK(hipSetDevice(device));
+    nnhip::noalloc_setup(device);
     std::unique_ptr<nnhip_ctx> c(new nnhip_ctx);
     c->c.device = device;
     NNHIP_CHECK(hipStreamCreateWithFlags(&c->c.stream, hipStreamNonBlocking));

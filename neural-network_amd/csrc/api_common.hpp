@@ -22,6 +22,9 @@ struct nnhip_kvcache {
 namespace nnhip {
 
 void set_last_error(const std::string &msg);
+// resolves this device's copy of the fixed scratch array of
+// nnhip_linear_w8a32_noalloc (noalloc.hip); device must be current
+void noalloc_setup(int device);
 
 template <typename F>
 int guard(F &&f) {

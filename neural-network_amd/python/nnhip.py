@@ -107,6 +107,8 @@ SIGNATURES = {
                                       _u32, _i, _vp],
     "nnhip_quantize_w8": [_vp, _vp, _i, _i, _vp, _vp],
     "nnhip_linear_w8a32": [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _i],
+    "nnhip_linear_w8a32_noalloc": [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp,
+                                   _i],
     "nnhip_layernorm_linear_w8a32": [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp,
                                      _vp, _vp, _i, _vp],
     "nnhip_linear_f32": [_vp, _vp, _i, _i, _vp, _vp, _i, _vp],
