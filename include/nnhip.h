@@ -124,7 +124,8 @@ int nnhip_decoder_init_normal(nnhip_model *m, uint64_t seed, float stdv);
 /* quantize_model + MultiHeadAttention::quantize + QuantizedDense ctor
  * (quantization.cpp:7-87, 156-171; layer.cpp:545-558) applied to every Dense
  * of the decoder (q, k, v, o, gate, up, down, lm_head); the embedding stays
- * fp32.  bits: 8 (INT8).  INT4 returns NNHIP_EUNSUPPORTED. */
+ * fp32.  bits: 8 (INT8) or 4 (INT4: scale max|w| / 7, codes in [-7, 7],
+ * held one per byte on the device, so the INT8 kernels serve both). */
 int nnhip_decoder_quantize(nnhip_model *m, int bits);
 /* QuantizedDense::packed_weights / scales (quantization.hpp:31-33) of one
  * Dense: which 0..6 = q,k,v,o,gate,up,down of `layer`, 7 = lm_head.  codes
@@ -216,6 +217,13 @@ int nnhip_generate_advanced_batch(nnhip_model *m, int B,
 /* QuantizedDense ctor, INT8 (quantization.cpp:36-66): w [in][out] fp32 ->
  * codes [out][in] int8 (transposed for coalesced GEMV loads), scales [out]. */
 int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
+                      int8_t *codes, float *scales);
+/* The INT4 QuantizedDense ctor (quantization.cpp:38-86): scales = max|w| /
+ * 7, codes clamp(round(w / scale), -7, 7), held one per byte in the same
+ * [out][in] layout (every W8A32 entry point takes them); packing two to a
+ * byte (packed_weights, low nibble = even [in][out] index) is a host
+ * storage format the device does not use. */
+int nnhip_quantize_w4(nnhip_ctx *ctx, const float *w, int in, int out,
                       int8_t *codes, float *scales);
 /* QuantizedDense::forward (quantization.cpp:127-147): y [rows][N] =
  * x [rows][K] . (codes * scales)^T + bias.  path: 0 auto, 1 fp32 GEMV,

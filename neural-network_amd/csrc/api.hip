@@ -214,9 +214,9 @@ int nnhip_decoder_init_normal(nnhip_model *m, uint64_t seed, float stdv) {
 int nnhip_decoder_quantize(nnhip_model *m, int bits) {
   return guard([&] {
     REQ(m, "nnhip_decoder_quantize: NULL model");
-    NNHIP_REQUIRE(bits == 8, nnhip::kErrUnsupported,
-                  "only INT8 weight quantization is implemented on the device");
-    m->m->quantize();
+    NNHIP_REQUIRE(bits == 8 || bits == 4, nnhip::kErrUnsupported,
+                  "weight quantization: INT8 (8) or INT4 (4) only");
+    m->m->quantize(bits);
   });
 }
 
@@ -403,16 +403,29 @@ int nnhip_generate_advanced_batch(nnhip_model *m, int B,
 }
 
 // ---- fused device ops --------------------------------------------------------
-int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
-                      int8_t *codes, float *scales) {
+namespace {
+int quantize_w(nnhip_ctx *ctx, const float *w, int in, int out, int8_t *codes,
+               float *scales, int bits) {
   return guard([&] {
-    REQ(ctx && w && codes && scales && in > 0 && out > 0, "nnhip_quantize_w8: bad argument");
+    REQ(ctx && w && codes && scales && in > 0 && out > 0,
+        "nnhip_quantize_w: bad argument");
     hipStream_t st = ctx->c.stream;
     nnhip::DevBuf<float> t((size_t)in * out);
     nnhip::launch_transpose_into(st, w, in, out, t.p, 0, 1);
-    nnhip::launch_quantize_w8(st, t.p, out, in, codes, scales);
+    nnhip::launch_quantize_w8(st, t.p, out, in, codes, scales, bits);
     NNHIP_CHECK(hipStreamSynchronize(st));
   });
+}
+}  // namespace
+
+int nnhip_quantize_w8(nnhip_ctx *ctx, const float *w, int in, int out,
+                      int8_t *codes, float *scales) {
+  return quantize_w(ctx, w, in, out, codes, scales, 8);
+}
+
+int nnhip_quantize_w4(nnhip_ctx *ctx, const float *w, int in, int out,
+                      int8_t *codes, float *scales) {
+  return quantize_w(ctx, w, in, out, codes, scales, 4);
 }
 
 namespace {

@@ -170,7 +170,7 @@ void Model::set_param(int idx, const float *host) {
                           r.row_stride);
   if (r.kind == ParamRef::kWeight && r.lin->quant) {
     launch_quantize_w8(st, r.lin->w.p, r.lin->N, r.lin->K, r.lin->q.p,
-                       r.lin->s.p);
+                       r.lin->s.p, bits);
     if (r.lin->qs.p)
       launch_swizzle_rows(st, r.lin->q.p, r.lin->N, r.lin->K, r.lin->qs.p,
                           false);
@@ -224,19 +224,24 @@ void Model::init_normal(uint64_t seed, float stdv) {
       }
     }
   }
-  if (quantized) quantize();
+  if (quantized) quantize(bits);
   NNHIP_CHECK(hipStreamSynchronize(st));
 }
 
 // quantize_model / MultiHeadAttention::quantize extended to the whole
 // decoder: every Dense (q, k, v, o, gate, up, down, lm_head) becomes a
-// symmetric per-output-channel int8 QuantizedDense (quantization.cpp:7-87);
-// the embedding stays fp32.
-void Model::quantize() {
+// symmetric per-output-channel QuantizedDense (quantization.cpp:7-87), INT8
+// or INT4; the embedding stays fp32.  INT4 codes are held one per byte, as
+// INT8 codes are: dequantize_weight gives both the same values (code *
+// scale), so every kernel serves both.
+void Model::quantize(int b) {
   hipStream_t st = ctx->stream;
+  NNHIP_REQUIRE(b == 8 || b == 4, kErrUnsupported,
+                "weight quantization: INT8 or INT4 only");
+  bits = b;
   auto q = [&](Linear &ln) {
     if (!ln.q.p) ln.q.alloc((size_t)ln.N * ln.K);
-    launch_quantize_w8(st, ln.w.p, ln.N, ln.K, ln.q.p, ln.s.p);
+    launch_quantize_w8(st, ln.w.p, ln.N, ln.K, ln.q.p, ln.s.p, bits);
     if (ln.K % 128 == 0 && ln.N % 64 == 0) {
       if (!ln.qs.p) ln.qs.alloc((size_t)ln.N * ln.K);
       launch_swizzle_rows(st, ln.q.p, ln.N, ln.K, ln.qs.p, false);

@@ -59,6 +59,7 @@ struct Model {
   Ctx *ctx = nullptr;
   int V = 0, d = 0, H = 0, D = 0, F = 0, L = 0, max_seq = 0;
   bool quantized = false;
+  int bits = 8;       // weight code width once quantized (8 or 4)
   DevBuf<float> emb;  // [V][d]
   std::vector<LayerW> layers;
   Linear lm;
@@ -77,7 +78,7 @@ struct Model {
   void set_param(int idx, const float *host);
   void get_param(int idx, float *host) const;
   void init_normal(uint64_t seed, float stdv);
-  void quantize();
+  void quantize(int bits = 8);
   void get_quantized(int layer, int which, int8_t *codes_kn,
                      float *scales) const;
 

@@ -1074,7 +1074,7 @@ __global__ __launch_bounds__(kFkThreads) void gemm_fk_kernel(
 // QuantizedDense ctor, INT8 (quantization.cpp:36-66), one output channel per
 // workgroup: s = max|w|/127 (1 if 0), code = clamp(round(w/s), +-127).
 __global__ __launch_bounds__(256) void quantize_w8_kernel(
-    const float *__restrict__ w, int K, int8_t *__restrict__ q,
+    const float *__restrict__ w, int K, float max_q, int8_t *__restrict__ q,
     float *__restrict__ scales) {
   __shared__ float smax[4];
   const int64_t n = blockIdx.x;
@@ -1086,12 +1086,12 @@ __global__ __launch_bounds__(256) void quantize_w8_kernel(
   if ((threadIdx.x & 63) == 0) smax[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
-  float s = mx / 127.0f;
+  float s = mx / max_q;
   if (s == 0.0f) s = 1.0f;
   if (threadIdx.x == 0) scales[n] = s;
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
     float qf = roundf(wr[k] / s);
-    qf = fmaxf(-127.0f, fminf(127.0f, qf));
+    qf = fmaxf(-max_q, fminf(max_q, qf));
     q[n * K + k] = (int8_t)qf;
   }
 }
@@ -1432,9 +1432,11 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
 }
 
 void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
-                        int8_t *q_nk, float *scales) {
+                        int8_t *q_nk, float *scales, int bits) {
+  NNHIP_REQUIRE(bits == 8 || bits == 4, kErrUnsupported,
+                "weight quantization: INT8 or INT4 only");
   hipLaunchKernelGGL(quantize_w8_kernel, dim3(N), dim3(256), 0, st, w_nk, K,
-                     q_nk, scales);
+                     bits == 8 ? 127.0f : 7.0f, q_nk, scales);
   NNHIP_CHECK(hipGetLastError());
 }
 

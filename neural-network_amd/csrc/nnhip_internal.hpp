@@ -387,8 +387,11 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
                       int epi, const RopeArgs *ra = nullptr, int ksplit = 1);
+// QuantizedDense ctor (quantization.cpp:36-86) on rows of w [N][K]: one
+// scale per row = max|w| / max_q (1 when 0), codes clamp(round(w / scale),
+// +-max_q) one per byte; max_q 127 (bits 8, INT8) or 7 (bits 4, INT4)
 void launch_quantize_w8(hipStream_t st, const float *w_nk, int N, int K,
-                        int8_t *q_nk, float *scales);
+                        int8_t *q_nk, float *scales, int bits = 8);
 // row-major int8 [R][K] <-> MFMA operand layout (R % 32, K % 128 == 0)
 void launch_swizzle_rows(hipStream_t st, const int8_t *src, int R, int K,
                          int8_t *dst, bool inverse);

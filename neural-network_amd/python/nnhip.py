@@ -106,6 +106,7 @@ SIGNATURES = {
     "nnhip_generate_advanced_batch": [_vp, _i, _vp, _i, _i, _f, _i, _f, _u64,
                                       _u32, _i, _vp],
     "nnhip_quantize_w8": [_vp, _vp, _i, _i, _vp, _vp],
+    "nnhip_quantize_w4": [_vp, _vp, _i, _i, _vp, _vp],
     "nnhip_linear_w8a32": [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _i],
     "nnhip_linear_w8a32_noalloc": [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _vp,
                                    _i],

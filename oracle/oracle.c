@@ -176,42 +176,74 @@ int or_model_set_param(or_model *m, int idx, const float *data) {
 /* QuantizedDense ctor, INT8 branch (quantization.cpp:36-66): per output
  * column c, s_c = max_r |W[r,c]| / 127 (1 if 0); code = clamp(round(W/s),
  * -127, 127) with round-half-away-from-zero. */
-void or_quantize_w8(const float *w, int64_t in, int64_t out, int8_t *codes,
-                    float *scales) {
+void or_quantize_w(const float *w, int64_t in, int64_t out, int bits,
+                   int8_t *codes, float *scales) {
+  const float max_q = bits == 4 ? 7.0f : 127.0f;
   for (int64_t c = 0; c < out; ++c) {
     float mx = 0.0f;
     for (int64_t r = 0; r < in; ++r) {
       float a = fabsf(w[r * out + c]);
       if (a > mx) mx = a;
     }
-    float s = mx / 127.0f;
+    float s = mx / max_q;
     scales[c] = (s == 0.0f) ? 1.0f : s;
   }
   for (int64_t r = 0; r < in; ++r)
     for (int64_t c = 0; c < out; ++c) {
       float qf = roundf(w[r * out + c] / scales[c]);
-      qf = fmaxf(-127.0f, fminf(127.0f, qf));
+      qf = fmaxf(-max_q, fminf(max_q, qf));
       codes[r * out + c] = (int8_t)qf;
     }
 }
 
-static void dense_quantize(or_dense_t *dn) {
+void or_quantize_w8(const float *w, int64_t in, int64_t out, int8_t *codes,
+                    float *scales) {
+  or_quantize_w(w, in, out, 8, codes, scales);
+}
+
+/* INT4 packing of QuantizedDense (quantization.cpp:68-86): two codes a
+ * byte, the even flat index in the low nibble. */
+void or_pack_int4(const int8_t *codes, int64_t n, uint8_t *packed) {
+  for (int64_t i = 0; i < (n + 1) / 2; ++i) packed[i] = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    uint8_t v = (uint8_t)codes[i] & 0x0F;
+    if (i % 2 == 0) packed[i / 2] = v;
+    else packed[i / 2] |= (uint8_t)(v << 4);
+  }
+}
+
+/* dequantize_weight's unpacking (quantization.cpp:106-122): a nibble with
+ * bit 3 set is negative (sign-extended). */
+void or_unpack_int4(const uint8_t *packed, int64_t n, int8_t *codes) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint8_t b = i % 2 == 0 ? (packed[i / 2] & 0x0F) : ((packed[i / 2] >> 4) & 0x0F);
+    codes[i] = (b & 0x08) ? (int8_t)(b | 0xF0) : (int8_t)b;
+  }
+}
+
+/* The codes are kept one per byte: dequantize_weight gives the INT4 codes
+ * the same values (code * scale) as INT8 codes, so the forward is shared. */
+static void dense_quantize(or_dense_t *dn, int bits) {
   free(dn->codes); free(dn->scales);
   dn->codes = (int8_t *)malloc((size_t)(dn->in * dn->out));
   dn->scales = (float *)malloc(sizeof(float) * (size_t)dn->out);
-  or_quantize_w8(dn->w, dn->in, dn->out, dn->codes, dn->scales);
+  or_quantize_w(dn->w, dn->in, dn->out, bits, dn->codes, dn->scales);
 }
 
-int or_model_quantize(or_model *m) {
+int or_model_quantize_bits(or_model *m, int bits) {
+  if (bits != 8 && bits != 4) return -1;
   for (int l = 0; l < m->L; ++l) {
     or_layer_t *ly = &m->layers[l];
-    dense_quantize(&ly->q); dense_quantize(&ly->k); dense_quantize(&ly->v);
-    dense_quantize(&ly->o); dense_quantize(&ly->gate);
-    dense_quantize(&ly->up); dense_quantize(&ly->down);
+    dense_quantize(&ly->q, bits); dense_quantize(&ly->k, bits);
+    dense_quantize(&ly->v, bits); dense_quantize(&ly->o, bits);
+    dense_quantize(&ly->gate, bits); dense_quantize(&ly->up, bits);
+    dense_quantize(&ly->down, bits);
   }
-  dense_quantize(&m->lm);
+  dense_quantize(&m->lm, bits);
   return 0;
 }
+
+int or_model_quantize(or_model *m) { return or_model_quantize_bits(m, 8); }
 
 int or_model_get_quantized(const or_model *m, int layer, int which,
                            int8_t *codes, float *scales) {

@@ -68,6 +68,9 @@ int or_model_load_weights(or_model *m, const char *path);
 /* Quantise every Dense (q,k,v,o,gate,up,down,lm_head) to symmetric int8
  * per output channel; the embedding stays fp32. */
 int or_model_quantize(or_model *m);
+/* The same with INT4 codes (bits 4: scale = max|w| / 7, codes clamped to
+ * +-7, quantization.cpp:38-86) or INT8 (bits 8); -1 for other widths. */
+int or_model_quantize_bits(or_model *m, int bits);
 /* Read back int8 codes ([in,out] reference layout) and scales of a Dense.
  * which: 0..6 = q,k,v,o,gate,up,down of layer `layer`; 7 = lm_head. */
 int or_model_get_quantized(const or_model *m, int layer, int which,
@@ -106,6 +109,14 @@ int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
 /* Unit restatements used by kernel-level parity tests. */
 void or_quantize_w8(const float *w, int64_t in, int64_t out, int8_t *codes,
                     float *scales);
+/* QuantizedDense ctor for INT8 (bits 8) or INT4 (bits 4), codes [in][out]
+ * one per byte. */
+void or_quantize_w(const float *w, int64_t in, int64_t out, int bits,
+                   int8_t *codes, float *scales);
+/* INT4 codes <-> QuantizedDense::packed_weights (low nibble = even flat
+ * index, sign-extended on unpacking). */
+void or_pack_int4(const int8_t *codes, int64_t n, uint8_t *packed);
+void or_unpack_int4(const uint8_t *packed, int64_t n, int8_t *codes);
 void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
               const float *w, const int8_t *codes, const float *scales,
               const float *bias, float *y);

@@ -57,6 +57,12 @@ def lib():
                                            C.POINTER(i64)]
         L.or_model_set_param.argtypes = [vp, i32, fp]
         L.or_model_quantize.argtypes = [vp]
+        L.or_model_quantize_bits.argtypes = [vp, i32]
+        L.or_quantize_w.argtypes = [fp, i64, i64, i32, C.POINTER(C.c_int8), fp]
+        L.or_pack_int4.argtypes = [C.POINTER(C.c_int8), i64,
+                                   C.POINTER(C.c_uint8)]
+        L.or_unpack_int4.argtypes = [C.POINTER(C.c_uint8), i64,
+                                     C.POINTER(C.c_int8)]
         L.or_model_get_quantized.argtypes = [vp, i32, i32,
                                              C.POINTER(C.c_int8), fp]
         L.or_cache_create.argtypes = [vp]
@@ -170,7 +176,8 @@ def make_params(vocab, d, H, F, L, seed, std=0.02, bias_std=0.0):
 class Model:
     """Oracle TransformerDecoder(vocab, d, heads, d_ff, layers, max_seq)."""
 
-    def __init__(self, vocab, d, H, F, L, max_seq, params, quantize=False):
+    def __init__(self, vocab, d, H, F, L, max_seq, params, quantize=False,
+                 bits=8):
         self.vocab, self.d, self.H, self.F, self.L = vocab, d, H, F, L
         self.max_seq = max_seq
         self.h = lib().or_model_create(vocab, d, H, F, L, max_seq)
@@ -182,7 +189,7 @@ class Model:
             assert r.value * c.value == p.size, (i, p.shape)
             assert lib().or_model_set_param(self.h, i, fptr(p)) == 0
         if quantize:
-            lib().or_model_quantize(self.h)
+            assert lib().or_model_quantize_bits(self.h, bits) == 0
 
     def __del__(self):
         if getattr(self, "h", None):
@@ -434,3 +441,29 @@ def assert_same_stream(got, want, cycles, first_margin, P, tol=1e-5,
             return i
         pos += n
     raise AssertionError(f"{what}: divergence at {i} beyond the record")
+
+
+def quantize_w(w, bits):
+    """QuantizedDense ctor on w [in][out]: (codes int8 [in][out], scales)."""
+    w = np.ascontiguousarray(w, np.float32)
+    codes = np.zeros(w.shape, np.int8)
+    scales = np.zeros(w.shape[1], np.float32)
+    lib().or_quantize_w(fptr(w), w.shape[0], w.shape[1], bits, i8ptr(codes),
+                        fptr(scales))
+    return codes, scales
+
+
+def pack_int4(codes):
+    c = np.ascontiguousarray(codes, np.int8).ravel()
+    out = np.zeros((c.size + 1) // 2, np.uint8)
+    lib().or_pack_int4(i8ptr(c), c.size,
+                       out.ctypes.data_as(C.POINTER(C.c_uint8)))
+    return out
+
+
+def unpack_int4(packed, n):
+    p = np.ascontiguousarray(packed, np.uint8)
+    out = np.zeros(n, np.int8)
+    lib().or_unpack_int4(p.ctypes.data_as(C.POINTER(C.c_uint8)), n,
+                         i8ptr(out))
+    return out

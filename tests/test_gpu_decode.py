@@ -24,16 +24,16 @@ CFG2_T = dict(vocab=4096, d=512, H=8, F=2048, L=6)
 CFG2_D = dict(vocab=4096, d=256, H=4, F=1024, L=2)
 
 
-def build(ctx, cfg, seed, quantize, max_seq=1024, std=0.02):
+def build(ctx, cfg, seed, quantize, max_seq=1024, std=0.02, bits=8):
     params = O.make_params(cfg["vocab"], cfg["d"], cfg["H"], cfg["F"],
                            cfg["L"], seed, std=std)
     om = O.Model(cfg["vocab"], cfg["d"], cfg["H"], cfg["F"], cfg["L"],
-                 max_seq, params, quantize)
+                 max_seq, params, quantize, bits=bits)
     gm = nnhip.Decoder(ctx, cfg["vocab"], cfg["d"], cfg["H"], cfg["F"],
                        cfg["L"], max_seq)
     gm.set_params(params)
     if quantize:
-        gm.quantize()
+        gm.quantize(bits)
     return om, gm, params
 
 
@@ -51,6 +51,41 @@ def test_params_roundtrip_and_quantized_codes(ctx):
         np.testing.assert_array_equal(gc, oc)
         np.testing.assert_array_equal(gs, os_)
     gm.free()
+
+
+def test_int4_decoder_matches_oracle(ctx):
+    """INT4 QuantizedDense (quantization.cpp:38-86) for every Dense of the
+    decoder: codes and scales bit-exact with the oracle's, forward logits
+    within 1e-4, greedy speculative stream equal; nnhip_quantize_w4 on a
+    single weight equals the oracle's quantize_w(w, 4)."""
+    om, gm, params = build(ctx, TOY_T, 61, True, std=0.05, bits=4)
+    d, F, V = TOY_T["d"], TOY_T["F"], TOY_T["vocab"]
+    for layer, which, n_in, n_out in ((0, 0, d, d), (1, 4, d, F),
+                                      (0, 6, F, d), (0, 7, d, V)):
+        gc, gs = gm.get_quantized(layer, which, n_in, n_out)
+        oc, os_ = om.quantized(layer, which, n_in, n_out)
+        np.testing.assert_array_equal(gc, oc)
+        np.testing.assert_array_equal(gs, os_)
+        assert np.abs(gc).max() <= 7
+    rng = np.random.default_rng(62)
+    ids = rng.integers(0, V, (2, 9)).astype(np.int32)
+    got = gm.forward(ids)
+    for b in range(2):
+        assert_rows_close(got[b], om.forward(ids[b]), 1e-4, f"int4 b={b}")
+    od, gd, _ = build(ctx, TOY_D, 63, True, std=0.05, bits=4)
+    prompt = rng.integers(0, V, 20).astype(np.int32)
+    spec, _ = gm.generate_speculative(gd, prompt, 24, 4, 0.0)
+    want, _ = O.generate_speculative(om, od, prompt, 24, 4, 0.0, 42)
+    np.testing.assert_array_equal(spec, want)
+    w = (rng.standard_normal((96, 64)) * 0.1).astype(np.float32)
+    dw = ctx.array(w)
+    dc = ctx.array(shape=(64, 96), dtype=np.int8)
+    ds = ctx.array(shape=(64,))
+    nnhip.call("nnhip_quantize_w4", ctx.h, dw.p, 96, 64, dc.p, ds.p)
+    oc, os_ = O.quantize_w(w, 4)
+    np.testing.assert_array_equal(dc.numpy().T, oc)
+    np.testing.assert_array_equal(ds.numpy(), os_)
+    gm.free(); gd.free()
 
 
 def test_init_normal_rules(ctx):

@@ -105,6 +105,60 @@ def test_quantized_dense_forward_reference():
     assert rel.max() < 0.05
 
 
+def test_quantize_int4_reference_kat_and_packing():
+    """QuantizationTest.Int4Packing (quantization_test.cpp:28-45): scale
+    7 / 7 = 1, dequantised -7, 3, 0, 5.  Packing (quantization.cpp:68-86):
+    two codes a byte, the even flat index in the low nibble, so -7 (0x9)
+    and 3 give 0x39, 0 and 5 give 0x50; unpacking sign-extends
+    (quantization.cpp:106-122) back to the codes."""
+    kat = golden("reference_kats.json")["quantize_int4"]
+    w = np.array(kat["weight"], np.float32).reshape(kat["shape"])
+    codes, scales = O.quantize_w(w, 4)
+    np.testing.assert_array_equal(scales, kat["scales"])
+    np.testing.assert_array_equal((codes * scales[None, :]).ravel(),
+                                  kat["dequant"])
+    packed = O.pack_int4(codes)
+    assert packed.tolist() == [0x39, 0x50]
+    np.testing.assert_array_equal(O.unpack_int4(packed, 4), codes.ravel())
+    # every code value survives a round trip; an odd count leaves the last
+    # high nibble zero
+    allc = np.arange(-7, 8, dtype=np.int8)
+    p2 = O.pack_int4(allc)
+    assert len(p2) == 8 and p2[-1] >> 4 == 0
+    np.testing.assert_array_equal(O.unpack_int4(p2, 15), allc)
+
+
+def test_quantize_int4_closed_form_and_forward():
+    """INT4 codes: scale = max|w| / 7 per output column (1 when 0), codes
+    round-half-away-from-zero clamped to +-7, the column maximum at +-7;
+    QuantizedDenseForward's INT4 case (quantization_test.cpp:76-86) within
+    70% of the fp32 forward."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((33, 12)) * 0.02).astype(np.float32)
+    w[:, 3] = 0.0
+    codes, scales = O.quantize_w(w, 4)
+    for c in range(w.shape[1]):
+        mx = np.float32(np.abs(w[:, c]).max())
+        s = np.float32(mx / np.float32(7.0))
+        assert scales[c] == (np.float32(1.0) if s == 0 else s)
+        q = np.trunc(w[:, c] / scales[c] + np.copysign(np.float32(0.5), w[:, c]))
+        np.testing.assert_array_equal(codes[:, c], np.clip(q, -7, 7))
+    assert np.abs(codes).max() == 7
+    kat = golden("reference_kats.json")["quantized_dense_forward"]
+    wk = np.array(kat["weight"], np.float32).reshape(4, 3)
+    b = np.array(kat["bias"], np.float32)
+    x = np.array(kat["x"], np.float32).reshape(2, 4)
+    c4, s4 = O.quantize_w(wk, 4)
+    y = np.zeros((2, 3), np.float32)
+    y4 = np.zeros((2, 3), np.float32)
+    O.lib().or_dense(O.fptr(x), 2, 4, 3, O.fptr(wk), None, None, O.fptr(b),
+                     O.fptr(y))
+    O.lib().or_dense(O.fptr(x), 2, 4, 3, None, O.i8ptr(c4), O.fptr(s4),
+                     O.fptr(b), O.fptr(y4))
+    rel = np.abs(y - y4) / np.maximum(1.0, np.abs(y))
+    assert rel.max() < kat["max_rel_err_int4"]
+
+
 def test_matmul_kat_reference():
     """tensor_test.cpp:82-94: [[1,2,3],[4,5,6]] . [[7,8],[9,10],[11,12]]."""
     kat = golden("reference_kats.json")["matmul"]
