@@ -276,8 +276,6 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the copy calibration and the attention "
                          "kernel (for rocprofv3 --pmc)")
-    ap.add_argument("--groups", type=int, default=1,
-                    help="sequence groups driven on separate HIP streams")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch each kernel of a cycle separately instead "
                          "of replaying one HIP graph per cycle")
@@ -297,7 +295,6 @@ def main():
     ctx = nnhip.Context(0)
     if a.no_graphs:
         ctx.set_option("graphs", 0)
-    ctx.set_option("groups", a.groups)
     for kv in a.option:
         key, val = kv.split("=")
         ctx.set_option(key, int(val))
@@ -333,7 +330,6 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 weights x fp32 activations (fp32 KV)",
         "data": "synthetic: seeded N(0,0.02) weights, uniform random prompts",
-        "groups": a.groups,
         "config": {"workload": "sampled speculative decode, 32 sequences, "
                                "target 12L/1024/16h/4096/V32000 int8, draft "
                                "4L/512/8h/2048 int8, prompt 256, k=5, T=1.0, "

@@ -56,16 +56,11 @@ const char *nnhip_last_error(void);
 int nnhip_init(int device, nnhip_ctx **out);
 int nnhip_destroy(nnhip_ctx *ctx);
 /* "graphs": 1 = replay each speculative cycle as one HIP graph (default).
- * "groups": split a batch into this many groups of sequences, each driven
- * on its own HIP stream so that their kernels overlap (0 = 1 group).
  * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids
  * (default: the prompt prefill's 8192-row down projection), 0 = always
  * 32x32 tiles (process-wide).
  * "attn_waves": number of (key split) waves an attention launch aims for;
  * the key range of each sequence is split accordingly (default 4096;
- * process-wide).
- * "gemm_fk": 1 = the LDS-resident GEMM runs as full-K waves (8 waves, each
- * 32 columns over all of K) instead of 16 K-split waves (default 0;
  * process-wide).
  * "attn_w4": attention rows of 4+ queries run in workgroups of 4 key
  * splits (two per CU) instead of 8: 1 = when a launch has 128 or more
@@ -75,15 +70,7 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * 2 always (process-wide).
  * "lds_min_rows": the LDS-resident GEMM serves projections from this many
  * rows on (default 64; process-wide).
- * "fold_norm": 1 = a pending LayerNorm is folded into every LDS-resident
- * GEMM's prologue, 0 = only into a short batch's lm head (default 0;
- * process-wide).
- * "fold_small": 1 = a short batch's pending LayerNorm is folded into an
- * LDS-resident GEMM instead of running as its own kernel (default 0).
- * "down_split": 1 = the down projection on the digit-plane GEMM splits K
- * over workgroups that add exact int64 totals, the next LayerNorm applying
- * its epilogue (default 0).  No option changes results beyond fp32
- * rounding order. */
+ * No option changes results beyond fp32 rounding order. */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);
 int nnhip_malloc(nnhip_ctx *ctx, size_t bytes, void **out);

@@ -69,16 +69,11 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
   return guard([&] {
     REQ(ctx && key, "nnhip_set_option: NULL argument");
     if (std::strcmp(key, "graphs") == 0) ctx->c.use_graphs = value != 0;
-    else if (std::strcmp(key, "groups") == 0) ctx->c.groups = value;
     else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
-    else if (std::strcmp(key, "gemm_fk") == 0) nnhip::g_gemm_fk = value != 0;
     else if (std::strcmp(key, "lds_min_rows") == 0) {
       REQ(value >= 16, "lds_min_rows must be >= 16");
       nnhip::g_lds_min_rows = value;
     }
-    else if (std::strcmp(key, "fold_norm") == 0) nnhip::g_fold_norm = value != 0;
-    else if (std::strcmp(key, "fold_small") == 0) nnhip::g_fold_small = value != 0;
-    else if (std::strcmp(key, "down_split") == 0) nnhip::g_down_split = value != 0;
     else if (std::strcmp(key, "attn_w4") == 0) {
       REQ(value >= 0 && value <= 2, "attn_w4 must be 0, 1 or 2");
       nnhip::g_attn_w4 = value;
@@ -263,7 +258,7 @@ int nnhip_decoder_forward(nnhip_model *mm, nnhip_kvcache *cache,
     nnhip::DevBuf<float> d_log((size_t)B * S * m.V);
     int max_keys = S;
     if (kv) for (int b = 0; b < B; ++b) max_keys = std::max(max_keys, kv->host_len[b] + S);
-    m.forward(0, kv, 0, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
+    m.forward(kv, 0, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
               max_keys, d_log.p, false);
     NNHIP_CHECK(hipMemcpyAsync(logits, d_log.p, d_log.bytes(), hipMemcpyDeviceToHost, st));
     if (kv) {

@@ -736,14 +736,11 @@ __global__ __launch_bounds__(256) void layernorm_kernel(
 // with its gamma and beta, all requested at once; the row sums and the max
 // are DPP wave reductions, and the digits of y (for the next MFMA GEMM) are
 // written from the same registers.
-// EPI: the row is first formed from a limb GEMM's int64 totals by the
-// deferred kEpiResid epilogue (LinEpiArgs), whose totals are then zeroed.
-template <int NQ, bool EPI>
+template <int NQ>
 __global__ __launch_bounds__(256) void layernorm_rows_kernel(
     const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
     const float *__restrict__ bt, float *__restrict__ y,
-    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp,
-    LinEpiArgs ea) {
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
 #pragma clang fp contract(off)
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -752,31 +749,7 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
   float v[NQ][4], gv[NQ][4], bv[NQ][4];
   load_quads<NQ>(g, d, lane, gv);
   load_quads<NQ>(bt, d, lane, bv);
-  if constexpr (EPI) {
-    const int te = ea.texp[row];
-    long long *tr = ea.tot + (int64_t)row * d;
-    const float *rr = ea.resid + (int64_t)row * ea.ldr;
-    float sc[NQ][4], bi[NQ][4], rs[NQ][4];
-    load_quads<NQ>(ea.scale, d, lane, sc);
-    load_quads<NQ>(ea.bias, d, lane, bi);
-    load_quads<NQ>(rr, d, lane, rs);
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int k = quad_at(i, lane, d);
-      const longlong2 t0 = *reinterpret_cast<const longlong2 *>(tr + k);
-      const longlong2 t1 = *reinterpret_cast<const longlong2 *>(tr + k + 2);
-      const long long t[4] = {t0.x, t0.y, t1.x, t1.y};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        v[i][j] = rs[i][j] + __fadd_rn(__fmul_rn(ldexpf((float)t[j], -te), sc[i][j]), bi[i][j]);
-      if (quad_ok(i, lane, d)) {
-        *reinterpret_cast<longlong2 *>(tr + k) = make_longlong2(0, 0);
-        *reinterpret_cast<longlong2 *>(tr + k + 2) = make_longlong2(0, 0);
-      }
-    }
-  } else {
-    load_quads<NQ>(hin + (int64_t)row * d, d, lane, v);
-  }
+  load_quads<NQ>(hin + (int64_t)row * d, d, lane, v);
   ln_row_finish<NQ>(v, gv, bv, d, row, y, limbs, mpad, rexp, lane);
 }
 
@@ -968,25 +941,15 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
 
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,
-                      int8_t *limbs, int mpad, int *rexp,
-                      const LinEpiArgs *ea) {
+                      int8_t *limbs, int mpad, int *rexp) {
   NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
   NNHIP_REQUIRE(!limbs || (d % 128 == 0 && rows <= mpad), kErrArg,
                 "layernorm: digit output needs d % 128 == 0");
-  const bool epi = ea && ea->tot;
-  NNHIP_REQUIRE(!epi || (d % 16 == 0 && ea->texp && ea->scale && ea->bias &&
-                         ea->resid && ea->ldr % 4 == 0),
-                kErrArg, "layernorm: GEMM epilogue arguments missing");
-  const LinEpiArgs ez = epi ? *ea : LinEpiArgs{};
   if (d % 16 == 0 && d <= 4096) {
     const dim3 grid((rows + 3) / 4);
 #define NNHIP_LN(P)                                                           \
-  if (epi)                                                                    \
-    hipLaunchKernelGGL((layernorm_rows_kernel<P, true>), grid, dim3(256), 0,  \
-                       st, h, d, rows, g, b, y, limbs, mpad, rexp, ez);       \
-  else                                                                        \
-    hipLaunchKernelGGL((layernorm_rows_kernel<P, false>), grid, dim3(256), 0, \
-                       st, h, d, rows, g, b, y, limbs, mpad, rexp, ez)
+  hipLaunchKernelGGL((layernorm_rows_kernel<P>), grid, dim3(256), 0, st, h, d, \
+                     rows, g, b, y, limbs, mpad, rexp)
     if (d <= 1024) { NNHIP_LN(4); }
     else if (d <= 2048) { NNHIP_LN(8); }
     else { NNHIP_LN(16); }

@@ -9,9 +9,6 @@
 namespace nnhip {
 
 int g_lds_min_rows = 64;
-int g_fold_small = 0;
-int g_down_split = 0;
-int g_fold_norm = 0;
 
 namespace {
 
@@ -49,20 +46,6 @@ struct ParamRef {
 };
 
 }  // namespace
-
-hipStream_t Ctx::lane(int g) {
-  if (g == 0) return stream;
-  while ((int)extra.size() < g) {
-    hipStream_t st;
-    NNHIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-    extra.push_back(st);
-  }
-  return extra[g - 1];
-}
-
-Ctx::~Ctx() {
-  for (hipStream_t st : extra) (void)hipStreamDestroy(st);
-}
 
 void Linear::init(int k, int n) {
   K = k; N = n;
@@ -284,13 +267,8 @@ void Model::get_quantized(int layer, int which, int8_t *codes_kn,
   }
 }
 
-Workspace &Model::ws(int g) {
-  if ((int)wss.size() <= g) wss.resize(g + 1);
-  return wss[g];
-}
-
-void Model::reserve(int g, int rows, int lrows, int max_keys) {
-  Workspace &ws = this->ws(g);
+void Model::reserve(int rows, int lrows, int max_keys) {
+  Workspace &ws = wsp;
   if (rows > ws.rows) {
     const int r = std::max(rows, 64);
     ws.rows = r;
@@ -299,14 +277,14 @@ void Model::reserve(int g, int rows, int lrows, int max_keys) {
     ws.x1.alloc((size_t)r * d);
     ws.qkv.alloc((size_t)r * 3 * d);
     ws.tot.alloc((size_t)r * d);
-    NNHIP_CHECK(hipMemsetAsync(ws.tot.p, 0, ws.tot.bytes(), ctx->lane(g)));
+    NNHIP_CHECK(hipMemsetAsync(ws.tot.p, 0, ws.tot.bytes(), ctx->stream));
     ws.ff.alloc((size_t)r * F);
     ws.mpad = round_up(r, 64);
     ws.limbs.alloc((size_t)kLimbs * ws.mpad * std::max(d, F));
     ws.rexp.alloc(ws.mpad);
     ws.ids.alloc(r);
     ws.zeros.alloc(r);
-    NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->lane(g)));
+    NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->stream));
   }
   if (lrows > ws.lrows) {
     ws.lrows = lrows;
@@ -340,11 +318,7 @@ bool Model::use_lds(const Linear &ln, int rows) const {
 
 // whether linear_in folds a pending LayerNorm into the LDS GEMM's prologue
 bool Model::norm_folds(const Linear &ln, int rows) const {
-  if (g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
-      ln.quant && ln.qs.p && gemm_lds_supports(rows, ln.K, ln.N))
-    return true;
-  return use_lds(ln, rows) &&
-         (g_fold_norm || (&ln == &lm && rows < g_lds_min_rows)) &&
+  return use_lds(ln, rows) && &ln == &lm && rows < g_lds_min_rows &&
          gemm_lds_workgroups(rows, ln.K, ln.N) <= kFusedNormMaxBlocks;
 }
 
@@ -352,31 +326,21 @@ bool Model::lm_tiles(int rows) const {
   return use_lds(lm, rows) && gemm_lds_tile_width(lm.K) > 0;
 }
 
-void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
+void Model::linear_in(const Linear &ln, const float *x, int64_t ldx,
                       const PendingNorm *pn, int rows, bool limbs_ready,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
                       int epi, const RopeArgs *ra, const TileStatsArgs *ts) {
-  hipStream_t st = ctx->lane(g);
-  Workspace &ws = this->ws(g);
-  // option fold_small: a pending LayerNorm on a short batch (the draft's
-  // rows) folded into the LDS GEMM's prologue instead of a launch of its own
-  if (pn && !pn->ea.tot && g_fold_small && rows < g_lds_min_rows && rows >= kLimbMinRows &&
-      ln.quant && ln.qs.p && gemm_lds_supports(rows, ln.K, ln.N) &&
-      (!ts || !ts->out || gemm_lds_tile_width(ln.K) > 0)) {
-    launch_gemm_lds(st, kAFromLayerNorm, ws.limbs.p, ws.mpad, ws.rexp.p, pn->h,
-                    pn->ldh, pn->g, pn->b, pn->out, pn->ldo, rows, ln.K, ln.N,
-                    ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi, ra, ts);
-    return;
-  }
+  hipStream_t st = ctx->stream;
+  Workspace &ws = wsp;
   if (use_lds(ln, rows)) {
     // Each column block of a fused GEMM normalises and digitises its rows
     // again: only the short-batch lm head folds the norm in; elsewhere one
     // LayerNorm launch writes digit planes for the GEMM to copy.
-    const bool fold = !(pn && pn->ea.tot) && norm_folds(ln, rows);
+    const bool fold = norm_folds(ln, rows);
     if (pn && !fold && pn->ldh == ln.K) {
       launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b,
                        pn->out ? pn->out : ws.x.p, ws.limbs.p, ws.mpad,
-                       ws.rexp.p, &pn->ea);
+                       ws.rexp.p);
       launch_gemm_lds(st, kAFromDigits, ws.limbs.p, ws.mpad, ws.rexp.p,
                       nullptr, 0, nullptr, nullptr, nullptr, 0, rows, ln.K,
                       ln.N, ln.qs.p, ln.s.p, ln.b.p, resid, ldr, y, ldy, epi,
@@ -394,7 +358,7 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
   }
   NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                 "linear_in: tile statistics need the LDS-resident GEMM");
-  if (pn && !pn->ea.tot && !use_limbs(ln, rows) && ln.K <= 1024 &&
+  if (pn && !use_limbs(ln, rows) && ln.K <= 1024 &&
       ln.K % 4 == 0 && pn->ldh % 4 == 0 && (!pn->out || pn->ldo % 4 == 0)) {
     // short rows on the GEMV: the LayerNorm is its prologue
     GemvLn lf;
@@ -410,18 +374,18 @@ void Model::linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
                   "linear_in: unfused LayerNorm needs contiguous rows");
     const bool lr = use_limbs(ln, rows);
     launch_layernorm(st, pn->h, rows, ln.K, pn->g, pn->b, pn->out,
-                     lr ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p, &pn->ea);
-    linear(g, ln, pn->out, pn->ldo, rows, lr, resid, ldr, y, ldy, epi, ra);
+                     lr ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+    linear(ln, pn->out, pn->ldo, rows, lr, resid, ldr, y, ldy, epi, ra);
     return;
   }
-  linear(g, ln, x, ldx, rows, limbs_ready, resid, ldr, y, ldy, epi, ra);
+  linear(ln, x, ldx, rows, limbs_ready, resid, ldr, y, ldy, epi, ra);
 }
 
-void Model::linear(int g, const Linear &ln, const float *x, int64_t ldx,
+void Model::linear(const Linear &ln, const float *x, int64_t ldx,
                    int rows, bool limbs_ready, const float *resid, int64_t ldr,
                    float *y, int64_t ldy, int epi, const RopeArgs *ra) {
-  hipStream_t st = ctx->lane(g);
-  Workspace &ws = this->ws(g);
+  hipStream_t st = ctx->stream;
+  Workspace &ws = wsp;
   if (use_limbs(ln, rows)) {
     if (!limbs_ready)
       launch_act_quant(st, x, ldx, rows, ln.K, ws.limbs.p, ws.mpad, ws.rexp.p);
@@ -434,12 +398,12 @@ void Model::linear(int g, const Linear &ln, const float *x, int64_t ldx,
   }
 }
 
-void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
+void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
                     int ids_stride, int B, int S, const int32_t *base, int off,
                     const int32_t *active, int max_keys, float *logits,
                     bool last_only, int64_t ldl, const TileStatsArgs *ts) {
   if (ldl == 0) ldl = V;
-  hipStream_t st = ctx->lane(g);
+  hipStream_t st = ctx->stream;
   const int R = B * S;
   std::unique_ptr<KVCache> tmp;
   KVCache *kv = cache;
@@ -450,8 +414,8 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
   }
   NNHIP_REQUIRE(b_off >= 0 && b_off + B <= kv->B, kErrArg,
                 "forward: sequence range outside the cache");
-  reserve(g, R, logits ? (last_only ? B : R) : 0, max_keys);
-  Workspace &ws = this->ws(g);
+  reserve(R, logits ? (last_only ? B : R) : 0, max_keys);
+  Workspace &ws = wsp;
   const int32_t *bp = base ? base : ws.zeros.p;
   // the embedding kernel also writes the rows' digits for the first q/k/v
   // GEMM when that is an MFMA GEMM
@@ -475,7 +439,7 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
                          (use_limbs(ly.qkv, R) && gemm_limb_q8_ok(D)));
     if (kv->q8 && !q8_epi) {
       // q, k, v rows, then RoPE and the quantised append
-      linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
+      linear_in(ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
                 l == 0 && emb_digits, nullptr, 0, ws.qkv.p, 3 * d, kEpiBias);
       launch_rope_kv_q8(st, ws.qkv.p, B, S, H, D, bp, off, active, cosb.p,
                         sinb.p, ws.qrot.p, (int8_t *)kvs.k, (float *)kvs.ks,
@@ -495,7 +459,7 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       } else {
         ra.kc = (float *)kvs.k; ra.vc = (float *)kvs.v;
       }
-      linear_in(g, ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
+      linear_in(ly.qkv, ws.x.p, d, have_norm2 ? &norm2 : nullptr, R,
                 l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
     }
     // short contexts: the attention workgroups merge their key splits and
@@ -512,42 +476,15 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
                       nullptr, nullptr, nullptr, 0, R, d, d, ly.o.qs.p,
                       ly.o.s.p, ly.o.b.p, ws.x.p, d, ws.h.p, d, kEpiResid);
     else
-      linear_in(g, ly.o, ws.ctx.p, d, nullptr, R, lo, ws.x.p, d, ws.h.p, d,
+      linear_in(ly.o, ws.ctx.p, d, nullptr, R, lo, ws.x.p, d, ws.h.p, d,
                 kEpiResid);
     PendingNorm norm1;
     norm1.h = ws.h.p; norm1.ldh = d; norm1.g = ly.g1.p; norm1.b = ly.b1.p;
     norm1.out = ws.x1.p; norm1.ldo = d;
-    linear_in(g, ly.gu, nullptr, 0, &norm1, R, false, nullptr, 0, ws.ff.p, F,
+    linear_in(ly.gu, nullptr, 0, &norm1, R, false, nullptr, 0, ws.ff.p, F,
               kEpiSwiGLU);
-    // Option down_split: the down projection on the digit-plane GEMM splits
-    // its K range over workgroups that add exact int64 totals, and the
-    // LayerNorm that follows applies the epilogue (scale, bias, residual) --
-    // unless that norm is folded into the lm head's prologue or never
-    // applied.  Measured on the batch-32 decode: the draft's GEMM gains what
-    // its LayerNorm loses (int64 reads and the zeroing), the verify's GEMM
-    // is slower (cross-XCD atomics), so it is off by default.
-    const bool last = l == L - 1;
-    const int lm_rows = last_only ? B : R;
-    const bool split = g_down_split && use_limbs(ly.down, R) &&
-                       !g_fold_norm && !g_fold_small &&
-                       (!last || (logits && !norm_folds(lm, lm_rows)));
-    norm2.ea = LinEpiArgs{};
-    if (split) {
-      const int nch = ly.down.K / 128;
-      const int tiles = ((R + 31) / 32) * (ly.down.N / 32);
-      const int ks = std::max(1, std::min(nch / 4, kGemmSlots * 2 / tiles));
-      launch_act_quant(st, ws.ff.p, F, R, ly.down.K, ws.limbs.p, ws.mpad, ws.rexp.p);
-      launch_gemm_limb(st, ws.limbs.p, ws.mpad, ws.rexp.p, R, ly.down.K,
-                       ly.down.N, ly.down.qs.p, ly.down.s.p, ly.down.b.p,
-                       nullptr, 0, reinterpret_cast<float *>(ws.tot.p), d,
-                       kEpiAddTotals, nullptr, ks);
-      norm2.ea.tot = ws.tot.p; norm2.ea.texp = ws.rexp.p;
-      norm2.ea.scale = ly.down.s.p; norm2.ea.bias = ly.down.b.p;
-      norm2.ea.resid = ws.x1.p; norm2.ea.ldr = d;
-    } else {
-      linear_in(g, ly.down, ws.ff.p, F, nullptr, R, false, ws.x1.p, d, ws.h.p,
-                d, kEpiResid);
-    }
+    linear_in(ly.down, ws.ff.p, F, nullptr, R, false, ws.x1.p, d, ws.h.p, d,
+              kEpiResid);
     norm2.h = ws.h.p; norm2.ldh = d; norm2.g = ly.g2.p; norm2.b = ly.b2.p;
     norm2.out = ws.x.p; norm2.ldo = d;
     have_norm2 = true;
@@ -559,9 +496,9 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       PendingNorm pn = norm2;
       pn.out = nullptr;
       if (last_only) { pn.h = ws.h.p + (int64_t)(S - 1) * d; pn.ldh = (int64_t)S * d; }
-      linear_in(g, lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, ldl,
+      linear_in(lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, ldl,
                 kEpiBias, nullptr, ts);
-    } else if (!norm2.ea.tot && !use_limbs(lm, rows) && d <= 1024 &&
+    } else if (!use_limbs(lm, rows) && d <= 1024 &&
                d % 4 == 0) {
       // short rows on the GEMV: the last norm2 is its prologue
       NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
@@ -577,12 +514,12 @@ void Model::forward(int g, KVCache *cache, int b_off, const int32_t *ids,
       NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                     "forward: tile statistics need the LDS-resident lm head");
       launch_layernorm(st, ws.h.p, R, d, norm2.g, norm2.b, ws.x.p, nullptr,
-                       ws.mpad, ws.rexp.p, &norm2.ea);
+                       ws.mpad, ws.rexp.p);
       if (last_only)
-        linear(g, lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
+        linear(lm, ws.x.p + (int64_t)(S - 1) * d, (int64_t)S * d, B, false,
                nullptr, 0, logits, ldl, kEpiBias);
       else
-        linear(g, lm, ws.x.p, d, R, false, nullptr, 0, logits, ldl, kEpiBias);
+        linear(lm, ws.x.p, d, R, false, nullptr, 0, logits, ldl, kEpiBias);
     }
   }
   if (tmp) NNHIP_CHECK(hipStreamSynchronize(st));
@@ -705,19 +642,16 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
   bf.vids.alloc((size_t)B * (k + 1)); bf.prompts.alloc((size_t)B * P);
   // Drafting samples from the draft lm head's tile statistics when that lm
-  // head forms them for every group's row count; otherwise from full passes
+  // head forms them for the batch's row count; otherwise from full passes
   // over the logits.  (The verify rows keep full passes: tile statistics in
   // the target lm head, six row tiles per workgroup, cost about what
   // target_stats_kernel does.)
-  int G = ctx->groups > 0 ? ctx->groups : 1;
-  G = std::max(1, std::min(G, B));
-  std::vector<int> gb0(G + 1);
-  for (int g = 0; g <= G; ++g) gb0[g] = (int)((int64_t)B * g / G);
   const int tw = gemm_lds_tile_width(dm.lm.K);
   const int nt = tw > 0 ? (V + tw - 1) / tw : 0;
   // (tile statistics carry no top-k / top-p: filtered rows take full passes)
-  bool tiles = tw > 0 && nt <= 1024 && (T <= 0.f || !sampling_filtered(V, top_k, top_p));
-  for (int g = 0; g < G && tiles; ++g) tiles = dm.lm_tiles(gb0[g + 1] - gb0[g]);
+  const bool tiles = tw > 0 && nt <= 1024 &&
+                     (T <= 0.f || !sampling_filtered(V, top_k, top_p)) &&
+                     dm.lm_tiles(B);
   if (tiles) bf.dtiles.alloc((size_t)B * k * nt);
   if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
   bf.tstat.alloc((size_t)B * (k + 1) * kTstat);
@@ -734,52 +668,22 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                                (size_t)P * 4, (size_t)P * 4, B,
                                hipMemcpyHostToDevice, st));
 
-  // Sequences are independent: the batch is split into G groups (above),
-  // each driven on its own lane (stream) so that the groups' kernels overlap
-  // on the GPU.
-  std::vector<SpecState> gs(G);
-  std::vector<hipStream_t> lanes(G);
-  for (int g = 0; g < G; ++g) {
-    const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
-    lanes[g] = ctx->lane(g);
-    SpecState &s = gs[g];
-    s.cur = bf.cur.p + b0; s.cand = bf.cand.p + (size_t)b0 * k;
-    s.qprob = bf.qprob.p ? bf.qprob.p + (size_t)b0 * k * V : nullptr;
-    s.tstat = bf.tstat.p + (size_t)b0 * (k + 1) * kTstat;
-    if (tiles) {
-      s.dtiles = bf.dtiles.p + (size_t)b0 * k * nt;
-      s.nt = nt; s.tw = tw;
-    }
-    s.tlen = bf.tlen.p + b0; s.dlen = bf.dlen.p + b0; s.gen = bf.gen.p + b0;
-    s.cyc = bf.cyc.p + b0; s.active = bf.active.p + b0;
-    s.catchup = bf.catchup.p + b0; s.catch_tok = bf.catch_tok.p + b0;
-    s.pair = bf.pair.p + (size_t)2 * b0;
-    s.out = bf.out.p + (size_t)b0 * out_stride; s.n_active = bf.n_active.p;
-    s.stats = bf.stats.p + (size_t)b0 * kSpecStats;
-    s.B = Bg; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
-    s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0 + b0;
-    s.top_k = top_k; s.top_p = top_p;
-    // workspace for every shape the loop uses, before any graph capture
-    t.reserve(g, Bg * P, Bg * (k + 1), t_need);
-    t.reserve(g, Bg * (k + 1), Bg * (k + 1), t_need);
-    dm.reserve(g, Bg * P, Bg, d_need);
-    dm.reserve(g, 2 * Bg, Bg, d_need);
-  }
-  std::vector<hipEvent_t> evj(G);
-  hipEvent_t evf;
-  NNHIP_CHECK(hipEventCreateWithFlags(&evf, hipEventDisableTiming));
-  for (auto &e : evj) NNHIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-  auto fork = [&]() {
-    if (G == 1) return;
-    NNHIP_CHECK(hipEventRecord(evf, st));
-    for (int g = 1; g < G; ++g) NNHIP_CHECK(hipStreamWaitEvent(lanes[g], evf, 0));
-  };
-  auto join = [&]() {
-    for (int g = 1; g < G; ++g) {
-      NNHIP_CHECK(hipEventRecord(evj[g], lanes[g]));
-      NNHIP_CHECK(hipStreamWaitEvent(st, evj[g], 0));
-    }
-  };
+  SpecState s{};
+  s.cur = bf.cur.p; s.cand = bf.cand.p; s.qprob = bf.qprob.p;
+  s.tstat = bf.tstat.p;
+  if (tiles) { s.dtiles = bf.dtiles.p; s.nt = nt; s.tw = tw; }
+  s.tlen = bf.tlen.p; s.dlen = bf.dlen.p; s.gen = bf.gen.p; s.cyc = bf.cyc.p;
+  s.active = bf.active.p; s.catchup = bf.catchup.p;
+  s.catch_tok = bf.catch_tok.p; s.pair = bf.pair.p; s.out = bf.out.p;
+  s.n_active = bf.n_active.p; s.stats = bf.stats.p;
+  s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
+  s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;
+  s.top_k = top_k; s.top_p = top_p;
+  // workspace for every shape the loop uses, before any graph capture
+  t.reserve(B * P, B * (k + 1), t_need);
+  t.reserve(B * (k + 1), B * (k + 1), t_need);
+  dm.reserve(B * P, B, d_need);
+  dm.reserve(2 * B, B, d_need);
 
   hipEvent_t e0, e1, e2;
   NNHIP_CHECK(hipEventCreate(&e0));
@@ -787,52 +691,35 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   NNHIP_CHECK(hipEventCreate(&e2));
   NNHIP_CHECK(hipEventRecord(e0, st));
   // prefill (layer.cpp:1400-1408); the draft's prefill logits are unused
-  fork();
-  for (int g = 0; g < G; ++g) {
-    const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
-    const int32_t *pr = bf.prompts.p + (size_t)b0 * P;
-    float *dl = bf.dlog.p + (size_t)b0 * V;
-    t.forward(g, &tc, b0, pr, P, Bg, P, nullptr, 0, nullptr, P, dl, true);
-    launch_first_token(lanes[g], gs[g], dl, V);
-    if (P > 1)
-      dm.forward(g, &dc, b0, pr, P, Bg, P - 1, nullptr, 0, nullptr, P - 1,
-                 nullptr, true);
-  }
-  join();
+  t.forward(&tc, 0, bf.prompts.p, P, B, P, nullptr, 0, nullptr, P, bf.dlog.p,
+            true);
+  launch_first_token(st, s, bf.dlog.p, V);
+  if (P > 1)
+    dm.forward(&dc, 0, bf.prompts.p, P, B, P - 1, nullptr, 0, nullptr, P - 1,
+               nullptr, true);
   NNHIP_CHECK(hipEventRecord(e1, st));
 
   auto cycle = [&]() {
-    fork();
-    for (int g = 0; g < G; ++g) {
-      const int b0 = gb0[g], Bg = gb0[g + 1] - b0;
-      hipStream_t ls = lanes[g];
-      int32_t *cur = bf.cur.p + b0, *cand = bf.cand.p + (size_t)b0 * k;
-      int32_t *dlen = bf.dlen.p + b0, *act = bf.active.p + b0;
-      float *dl = bf.dlog.p + (size_t)b0 * V;
-      float *tl = bf.tlog.p + (size_t)b0 * (k + 1) * V;
-      int32_t *vids = bf.vids.p + (size_t)b0 * (k + 1);
-      for (int j = 0; j < k; ++j) {
-        TileStatsArgs dts;
-        if (tiles) {
-          dts.out = bf.dtiles.p + ((size_t)b0 * k + j) * nt;
-          dts.ld = (int64_t)k * nt;
-          dts.T = T;
-        }
-        if (j == 0)   // {catch-up token, cur} at dlen - 1, dlen
-          dm.forward(g, &dc, b0, bf.pair.p + (size_t)2 * b0, 2, Bg, 2, dlen,
-                     -1, act, d_need, dl, true, 0, &dts);
-        else
-          dm.forward(g, &dc, b0, cand + (j - 1), k, Bg, 1, dlen, j, act,
-                     d_need, dl, false, 0, &dts);
-        if (tiles) launch_draft_sample_tiles(ls, gs[g], j, dl, V);
-        else launch_draft_sample(ls, gs[g], j, dl, V);
+    for (int j = 0; j < k; ++j) {
+      TileStatsArgs dts;
+      if (tiles) {
+        dts.out = bf.dtiles.p + (size_t)j * nt;
+        dts.ld = (int64_t)k * nt;
+        dts.T = T;
       }
-      launch_build_verify_ids(ls, cur, cand, Bg, k, vids);
-      t.forward(g, &tc, b0, vids, k + 1, Bg, k + 1, bf.tlen.p + b0, 0, act,
-                t_need, tl, false);
-      launch_accept(ls, gs[g], tl);
+      if (j == 0)   // {catch-up token, cur} at dlen - 1, dlen
+        dm.forward(&dc, 0, bf.pair.p, 2, B, 2, bf.dlen.p, -1, bf.active.p,
+                   d_need, bf.dlog.p, true, 0, &dts);
+      else
+        dm.forward(&dc, 0, bf.cand.p + (j - 1), k, B, 1, bf.dlen.p, j,
+                   bf.active.p, d_need, bf.dlog.p, false, 0, &dts);
+      if (tiles) launch_draft_sample_tiles(st, s, j, bf.dlog.p, V);
+      else launch_draft_sample(st, s, j, bf.dlog.p, V);
     }
-    join();
+    launch_build_verify_ids(st, bf.cur.p, bf.cand.p, B, k, bf.vids.p);
+    t.forward(&tc, 0, bf.vids.p, k + 1, B, k + 1, bf.tlen.p, 0, bf.active.p,
+              t_need, bf.tlog.p, false);
+    launch_accept(st, s, bf.tlog.p);
   };
 
   int32_t *h_nact = nullptr;
@@ -881,8 +768,6 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     (void)hipHostFree(h_nact);
     (void)hipEventDestroy(ev[0]); (void)hipEventDestroy(ev[1]);
     (void)hipEventDestroy(e0); (void)hipEventDestroy(e1); (void)hipEventDestroy(e2);
-    (void)hipEventDestroy(evf);
-    for (auto &e : evj) (void)hipEventDestroy(e);
     throw;
   }
   if (exec) NNHIP_CHECK(hipGraphExecDestroy(exec));
@@ -896,8 +781,6 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   NNHIP_CHECK(hipEventDestroy(e0));
   NNHIP_CHECK(hipEventDestroy(e1));
   NNHIP_CHECK(hipEventDestroy(e2));
-  NNHIP_CHECK(hipEventDestroy(evf));
-  for (auto &e : evj) NNHIP_CHECK(hipEventDestroy(e));
   if (timing) {
     timing->prefill_ms = ms_pre;
     timing->decode_ms = ms_dec;
@@ -954,14 +837,14 @@ void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
   for (int step = 0; step < max_new; ++step) {
     const int n = P + step;
     if (use_cache && step > 0) {
-      m.forward(0, cache.get(), 0, cur.p, 1, B, 1, len.p, 0, nullptr, n, lg.p,
+      m.forward(cache.get(), 0, cur.p, 1, B, 1, len.p, 0, nullptr, n, lg.p,
                 true);
       launch_add_scalar(st, len.p, B, 1);
     } else {
       // the reference keeps the last max_seq_len tokens (layer.cpp:1271-1277)
       int S = n, start = 0;
       if (S > m.max_seq) { start = S - m.max_seq; S = m.max_seq; }
-      m.forward(0, cache.get(), 0, dout.p + start, total, B, S,
+      m.forward(cache.get(), 0, dout.p + start, total, B, S,
                 use_cache ? len.p : nullptr, 0, nullptr, S, lg.p, true);
       if (use_cache) launch_add_scalar(st, len.p, B, S);
     }

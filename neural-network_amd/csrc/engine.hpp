@@ -11,17 +11,12 @@
 
 namespace nnhip {
 
-// A context owns one HIP stream (lane 0) and, on demand, further lanes on
-// which independent groups of sequences run concurrently.  All lanes keep the
-// default stream priority.
+// A context owns one HIP stream at the default priority; every launch of the
+// library is ordered on it.
 struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   bool use_graphs = true;
-  int groups = 0;                     // sequence groups per batch (0 = auto)
-  std::vector<hipStream_t> extra;     // lanes 1.. (created on first use)
-  hipStream_t lane(int g);
-  ~Ctx();
 };
 
 // One Dense on the device, weight transposed to [N][K].  Fused layouts:
@@ -69,7 +64,7 @@ struct Model {
   // max_seq_len (its verify step always runs k + 1 rows, and an int8 cache
   // has no length check in the reference)
   void ensure_rope(int n);
-  std::vector<Workspace> wss;  // one per lane
+  Workspace wsp;  // activations of the current forward
 
   Model(Ctx *c, int vocab, int d_model, int heads, int d_ff, int n_layers,
         int max_seq_len);
@@ -82,18 +77,17 @@ struct Model {
   void get_quantized(int layer, int which, int8_t *codes_kn,
                      float *scales) const;
 
-  Workspace &ws(int g);
-  // Ensures lane g's workspace for `rows` rows of which `lrows` need logits.
-  void reserve(int g, int rows, int lrows, int max_keys);
+  // Ensures the workspace for `rows` rows of which `lrows` need logits.
+  void reserve(int rows, int lrows, int max_keys);
 
-  // TransformerDecoder::forward for B sequences of S new tokens each, on
-  // lane g, using cache sequences [b_off, b_off + B).
+  // TransformerDecoder::forward for B sequences of S new tokens each, using
+  // cache sequences [b_off, b_off + B).
   // Token of row (b, s): ids[b*ids_stride + s].  Positions start at
   // base[b] + off (device array; nullptr = 0).  Sequences with
   // active[b] == 0 neither write nor read the cache.  logits: nullptr (not
   // needed), or [B*S][V] (all rows) or [B][V] (last_only), rows ldl apart
   // (0 = V).  ts: the lm head's tile statistics as well (lm_tiles(rows)).
-  void forward(int g, KVCache *cache, int b_off, const int32_t *ids,
+  void forward(KVCache *cache, int b_off, const int32_t *ids,
                int ids_stride, int B, int S, const int32_t *base, int off,
                const int32_t *active, int max_keys, float *logits,
                bool last_only, int64_t ldl = 0,
@@ -101,23 +95,19 @@ struct Model {
   // whether the lm head on `rows` rows can form tile statistics
   bool lm_tiles(int rows) const;
 
-  void linear(int g, const Linear &ln, const float *x, int64_t ldx, int rows,
+  void linear(const Linear &ln, const float *x, int64_t ldx, int rows,
               bool limbs_ready, const float *resid, int64_t ldr, float *y,
               int64_t ldy, int epi, const RopeArgs *ra = nullptr);
   // A LayerNorm of h (rows of stride ldh) that the next linear applies to
   // its input; the normalised rows go to out (stride ldo) when out is set.
-  // ea.tot set: h is not written; its rows are formed from a split-K limb
-  // GEMM's totals by the LayerNorm kernel (LinEpiArgs), which cannot be
-  // folded into a GEMM prologue.
   struct PendingNorm {
     const float *h = nullptr, *g = nullptr, *b = nullptr;
     int64_t ldh = 0;
     float *out = nullptr;
     int64_t ldo = 0;
-    LinEpiArgs ea;
   };
   // linear over x, or over LN(h) when pn is given (x is then ignored)
-  void linear_in(int g, const Linear &ln, const float *x, int64_t ldx,
+  void linear_in(const Linear &ln, const float *x, int64_t ldx,
                  const PendingNorm *pn, int rows, bool limbs_ready,
                  const float *resid, int64_t ldr, float *y, int64_t ldy,
                  int epi, const RopeArgs *ra = nullptr,

@@ -290,15 +290,14 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     int M, int K, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra, int ksplit) {
+    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
   constexpr int NT = 32 * NSUB;
   __shared__ int red[kLimbs][kGemmMT][NT];
-  const int T = ntm * ntn * ksplit;
+  const int T = ntm * ntn;
   const int per = (T + 7) / 8;
   const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
   if (wi >= T) return;
-  const int kq = wi / (ntm * ntn), wt = wi % (ntm * ntn);
-  const int tn = wt / ntm, tm = wt % ntm;
+  const int tn = wi / ntm, tm = wi % ntm;
   const int m0 = tm * kGemmMT, n0 = tn * NT;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -311,7 +310,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   constexpr int IT = kGemmMT * NT / 2 / 256;
   static_assert(256 % (NT / 2) == 0, "items must share their columns");
   const int e_n = n0 + 2 * ((int)threadIdx.x % (NT / 2));
-  const bool e_cols = epi != kEpiTotals && epi != kEpiAddTotals;
+  const bool e_cols = epi != kEpiTotals;
   const float e_sc0 = e_cols ? scale[e_n] : 0.f, e_sc1 = e_cols ? scale[e_n + 1] : 0.f;
   const float e_bi0 = e_cols ? bias[e_n] : 0.f, e_bi1 = e_cols ? bias[e_n + 1] : 0.f;
   int e_ex[IT];
@@ -332,8 +331,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
 #pragma unroll
     for (int l = 0; l < kLimbs; ++l) acc[t][l] = v16i{};
   const int nch = K / 128;
-  // this workgroup's chunks [cb, ce) of the K range
-  const int cb = kq * nch / ksplit, ce = (kq + 1) * nch / ksplit;
+  const int cb = 0, ce = nch;
   // tile bases in the operand layout: 32 rows x 128 k = 4 KB per chunk
   const int8_t *pb = wq + (int64_t)(n0 >> 5) * nch * 4096 + lane * 16;
   const int8_t *pa = limbs + (int64_t)(m0 >> 5) * nch * 4096 + lane * 16;
@@ -404,13 +402,6 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
     if (epi == kEpiTotals) {
       long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
       yt[0] = tot[0]; yt[1] = tot[1];
-      continue;
-    }
-    if (epi == kEpiAddTotals) {
-      unsigned long long *yt =
-          reinterpret_cast<unsigned long long *>(y) + (int64_t)m * ldy + n;
-      atomicAdd(yt, (unsigned long long)tot[0]);
-      atomicAdd(yt + 1, (unsigned long long)tot[1]);
       continue;
     }
     float v[2];
@@ -777,302 +768,6 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
   for (int tm = tmb + 1; tm < tme; ++tm) row_tile(tm);
 }
 
-// ---------------------------------------------------------------------------
-// int8 MFMA GEMM with full-K waves.  One workgroup of 8 waves (two per SIMD,
-// so a wave may hold up to 256 registers) owns a 256-column block: wave w
-// multiplies columns n0 + 32w .. n0 + 32w + 31 over the whole of K with its
-// weights resident in registers (K/8 of them).  No partial sums cross waves,
-// so there is no reduction tile: the epilogue runs on the MFMA accumulators
-// (lane holds column lane & 31 of rows (j >> 2) * 8 + (lane >> 5) * 4 +
-// (j & 3), j < 16; gate/up and RoPE pairs are adjacent lanes).  The 32 x K
-// digit tile sits in LDS, shared by the 8 waves, and is built by the same
-// prologues as gemm_lds_kernel (digit planes / fp32 rows / LayerNorm of fp32
-// rows).  All loads are issued at the start, the activations first and the
-// weights behind them, so the MFMAs of a chunk wait only for that chunk.
-// Same integers and the same rounding steps as gemm_lds_kernel and
-// gemm_limb_kernel: the three GEMMs give bit-identical outputs.
-// ---------------------------------------------------------------------------
-constexpr int kFkWaves = 8;
-constexpr int kFkThreads = kFkWaves * kWave;
-
-template <int MODE, int KPT, bool RES>
-__global__ __launch_bounds__(kFkThreads) void gemm_fk_kernel(
-    const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
-    const float *__restrict__ x, int64_t ldx, const float *__restrict__ lng,
-    const float *__restrict__ lnb, float *__restrict__ ln_out, int64_t ldo,
-    int M, int N, const int8_t *__restrict__ wq,
-    const float *__restrict__ scale, const float *__restrict__ bias,
-    const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
-    int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
-  constexpr int K = KPT * 32;
-  constexpr int nch = K / 128;
-  constexpr int NC = 32 * kFkWaves;           // columns per workgroup
-  constexpr int kPlane = kGemmMT * K;         // bytes per digit plane
-  constexpr int kABytes = kLimbs * kPlane;
-  constexpr bool kLN = MODE == kAFromLayerNorm;
-  constexpr bool kDig = MODE == kAFromDigits;
-  __shared__ __attribute__((aligned(16))) int8_t sa[kABytes];
-  __shared__ __attribute__((aligned(16))) float s_g[kLN ? K : 4], s_b[kLN ? K : 4];
-  __shared__ int s_e[kGemmMT];
-  const int T = ntm * ntn;
-  const int per = (T + 7) / 8;
-  const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (wi >= T) return;
-  const int tn = wi / ntm, tm = wi % ntm;
-  const int m0 = tm * kGemmMT, n0 = tn * NC;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nw = n0 + 32 * w;                 // this wave's column tile
-  const bool wcols = nw < N;                  // N % 32 == 0: all or none
-  const int hh = lane >> 5;
-  const int n = nw + (lane & 31);             // this lane's column
-
-  // ---- small operands: per-column vectors, the residual (RES) and the
-  // row exponent of row lane & 31 (digit planes) ----
-  float csc = 0.f, cbi = 0.f;
-  if (wcols && epi != kEpiTotals) { csc = scale[n]; cbi = bias[n]; }
-  // (with fp32 rows the residual is requested after the prologue, whose
-  // rows already hold many registers)
-  float ers[RES ? 16 : 1];
-  auto load_resid = [&]() {
-    if constexpr (RES) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
-        ers[j] = m < M && wcols ? resid[(int64_t)m * ldr + n] : 0.f;
-      }
-    }
-  };
-  if constexpr (kDig) load_resid();
-  int e_lane = 0;
-  if (kDig && m0 + (lane & 31) < M) e_lane = rexp[m0 + (lane & 31)];
-
-  // ---- the first row tile's activations ----
-  // digits: 16-byte pieces of the 32 x K tile, consecutive pieces on
-  // consecutive lanes (a wave's 64 pieces are one 1 KB run of a plane);
-  // rows: thread (row rr, part pp) takes entries 4pp + 64i, i < K/64
-  constexpr int kPieces = kABytes / 16;
-  static_assert(kPieces % kWave == 0, "whole pieces per wave");
-  constexpr int kPer = kDig ? (kPieces + kFkThreads - 1) / kFkThreads : 1;
-  constexpr int PP = kDig ? 1 : K / 64;
-  const int64_t plane = (int64_t)mpad * K;
-  float4 v[PP];
-  v4i apc[kPer];
-  const int rr = tid >> 4, pp = tid & 15;
-  const bool live = m0 + rr < M;
-  if constexpr (kDig) {
-    const int8_t *src = limbs + (int64_t)tm * nch * 4096;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = min(tid + j * kFkThreads, kPieces - 1);
-      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
-      apc[j] = *reinterpret_cast<const v4i *>(src + l * plane + o);
-    }
-  } else {
-    const int m = m0 + rr;
-#pragma unroll
-    for (int i = 0; i < PP; ++i)
-      v[i] = live ? *reinterpret_cast<const float4 *>(x + (int64_t)m * ldx + 4 * pp + 64 * i)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  // LayerNorm parameters: entries tid and tid + 512
-  float vg[2] = {0.f, 0.f}, vb[2] = {0.f, 0.f};
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-    if (kLN && tid + h * kFkThreads < K) {
-      vg[h] = lng[tid + h * kFkThreads];
-      vb[h] = lnb[tid + h * kFkThreads];
-    }
-
-  // ---- the wave's weights over all of K ----
-  v4i bf[nch][4];
-  {
-    const int nt = min(nw, N - 32);           // past N: the last tile, unused
-    const int8_t *pb = wq + (int64_t)(nt >> 5) * nch * 4096 + lane * 16;
-#pragma unroll
-    for (int c = 0; c < nch; ++c)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        bf[c][s] = *reinterpret_cast<const v4i *>(pb + c * 4096 + s * 1024);
-  }
-  // RoPE: the sequence state of row lane & 31 (its position is formed in
-  // the epilogue)
-  RopeRow rrow{0, 0, 0};
-  const bool rrow_ok = epi == kEpiRope && m0 + (lane & 31) < M;
-  if (rrow_ok) rrow = rope_row_read(ra, m0 + (lane & 31));
-  __builtin_amdgcn_sched_barrier(0);          // every load issued before the prologue
-
-  // ---- prologue: the first 32 x K digit tile in LDS ----
-  if constexpr (kDig) {
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = tid + j * kFkThreads;
-      if (kPieces % kFkThreads == 0 || i < kPieces) {
-        const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
-        *reinterpret_cast<v4i *>(sa + l * kPlane + o) = apc[j];
-      }
-    }
-  } else {
-#pragma clang fp contract(off)
-    const int m = m0 + rr;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (kLN && tid + h * kFkThreads < K) {
-        s_g[tid + h * kFkThreads] = vg[h];
-        s_b[tid + h * kFkThreads] = vb[h];
-      }
-    // sums / maxima over the 16 lanes of a row
-    auto row_sum = [](float a) {
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) a += __shfl_xor(a, o, kWave);
-      return a;
-    };
-    auto row_max = [](float a) {
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, kWave));
-      return a;
-    };
-    if constexpr (kLN) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < PP; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-      const float Nf = (float)K;
-      const float mean = row_sum(s) / Nf;
-      float sq = 0.f;
-#pragma unroll
-      for (int i = 0; i < PP; ++i) {
-        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean,
-                    d = v[i].w - mean;
-        sq += (a * a + b * b) + (c * c + d * d);
-      }
-      const float sd = sqrtf(row_sum(sq) / Nf + 1e-5f);
-      __syncthreads();                        // s_g, s_b written
-      const bool wr = ln_out && tn == 0 && live;
-#pragma unroll
-      for (int i = 0; i < PP; ++i) {
-        const int k = 4 * pp + 64 * i;
-        const float4 gg = *reinterpret_cast<const float4 *>(s_g + k);
-        const float4 bb = *reinterpret_cast<const float4 *>(s_b + k);
-        v[i].x = (v[i].x - mean) / sd * gg.x + bb.x;
-        v[i].y = (v[i].y - mean) / sd * gg.y + bb.y;
-        v[i].z = (v[i].z - mean) / sd * gg.z + bb.z;
-        v[i].w = (v[i].w - mean) / sd * gg.w + bb.w;
-        if (wr) *reinterpret_cast<float4 *>(ln_out + (int64_t)m * ldo + k) = v[i];
-      }
-    }
-    float mx = 0.f;
-#pragma unroll
-    for (int i = 0; i < PP; ++i)
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
-                           fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-    mx = row_max(mx);
-    const int e = digit_exponent(mx);
-    if (pp == 0) s_e[rr] = live ? e : 0;
-#pragma unroll
-    for (int i = 0; i < PP; ++i) {
-      const int k = 4 * pp + 64 * i;
-      const float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-      int3 d = digits4(f, e);
-      if (!live) d = make_int3(0, 0, 0);
-      const int o = (int)mfma_operand_offset(rr, k, K);
-      *reinterpret_cast<int *>(sa + o) = d.x;
-      *reinterpret_cast<int *>(sa + kPlane + o) = d.y;
-      *reinterpret_cast<int *>(sa + 2 * kPlane + o) = d.z;
-    }
-  }
-  __syncthreads();
-  if constexpr (!kDig) {
-    e_lane = s_e[lane & 31];
-    load_resid();
-  }
-
-  // ---- the wave's MFMAs over all of K ----
-  v16i acc[kLimbs];
-#pragma unroll
-  for (int l = 0; l < kLimbs; ++l) acc[l] = v16i{};
-  if (wcols) {
-    // the A operands of one step ahead are read while a step's MFMAs run;
-    // the scheduling barriers keep the reads from being hoisted further
-    // (the resident weights leave few registers)
-    const int8_t *pa = sa + lane * 16;
-    v4i a0[kLimbs], a1[kLimbs];
-#pragma unroll
-    for (int l = 0; l < kLimbs; ++l) a0[l] = *reinterpret_cast<const v4i *>(pa + l * kPlane);
-#pragma unroll
-    for (int st = 0; st < nch * 4; ++st) {
-      v4i (&cur)[kLimbs] = (st & 1) ? a1 : a0;
-      v4i (&nxt)[kLimbs] = (st & 1) ? a0 : a1;
-      if (st + 1 < nch * 4) {
-        const int off = ((st + 1) >> 2) * 4096 + ((st + 1) & 3) * 1024;
-#pragma unroll
-        for (int l = 0; l < kLimbs; ++l)
-          nxt[l] = *reinterpret_cast<const v4i *>(pa + l * kPlane + off);
-      }
-#pragma unroll
-      for (int l = 0; l < kLimbs; ++l)
-        acc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[l], bf[st >> 2][st & 3], acc[l], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  // ---- epilogue on the accumulators ----
-  if (epi == kEpiRope) {
-    // every value and every cos / sin is read before the first store;
-    // column pairs (2i, 2i + 1) sit on lanes (2i, 2i + 1)
-    float v0[16], v1[16], cs[16], sn[16];
-    int pos[16];
-    const bool vpart = n / (ra.H * ra.D) == 2;
-    // (the empty asm keeps the row state untouched until here, so that
-    // nothing waits for its reads before the MFMAs)
-    asm volatile("" : "+v"(rrow.base), "+v"(rrow.act));
-    const int pos_lane = rrow_ok ? rope_row_pos(ra, rrow) : -1;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const long long tot = (long long)acc[0][j] * 65536LL +
-                            (long long)acc[1][j] * 256LL + (long long)acc[2][j];
-      const int row = (j >> 2) * 8 + hh * 4 + (j & 3);
-      const int e = __shfl(e_lane, row, kWave);
-      v0[j] = __fadd_rn(__fmul_rn(ldexpf((float)tot, -e), csc), cbi);
-      v1[j] = __shfl_xor(v0[j], 1, kWave);
-      pos[j] = __shfl(pos_lane, row, kWave);
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float2 c = vpart ? make_float2(0.f, 0.f) : rope_cos_sin(ra, max(pos[j], 0), n);
-      cs[j] = c.x; sn[j] = c.y;
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
-      if ((n & 1) || m >= M || !wcols || pos[j] < 0) continue;
-      rope_store_pair_at(ra, m, pos[j], n, v0[j], v1[j], cs[j], sn[j]);
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int m = m0 + (j >> 2) * 8 + hh * 4 + (j & 3);
-    const long long tot = (long long)acc[0][j] * 65536LL +
-                          (long long)acc[1][j] * 256LL + (long long)acc[2][j];
-    const int e = __shfl(e_lane, (j >> 2) * 8 + hh * 4 + (j & 3), kWave);
-    float v0 = ldexpf((float)tot, -e);
-    v0 = __fadd_rn(__fmul_rn(v0, csc), cbi);
-    if (epi == kEpiSwiGLU) {
-      // gate / up pairs (2i, 2i + 1) sit on lanes (2i, 2i + 1)
-      const float v1 = __shfl_xor(v0, 1, kWave);
-      if ((n & 1) || m >= M || !wcols) continue;
-      y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
-      continue;
-    }
-    if (m >= M || !wcols) continue;
-    if (epi == kEpiTotals)
-      reinterpret_cast<long long *>(y)[(int64_t)m * ldy + n] = tot;
-    else
-      y[(int64_t)m * ldy + n] = RES ? ers[RES ? j : 0] + v0 : v0;
-  }
-}
-
-// QuantizedDense ctor, INT8 (quantization.cpp:36-66), one output channel per
-// workgroup: s = max|w|/127 (1 if 0), code = clamp(round(w/s), +-127).
 __global__ __launch_bounds__(256) void quantize_w8_kernel(
     const float *__restrict__ w, int K, float max_q, int8_t *__restrict__ q,
     float *__restrict__ scales) {
@@ -1217,7 +912,6 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
 // 1: allow 32x64 GEMM tiles for large grids; 0: always 32x32 (default,
 // measured faster on every decode shape).
 int g_gemm_wide = 1;
-int g_gemm_fk = 0;
 
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,
@@ -1286,12 +980,9 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi, const RopeArgs *ra, int ksplit) {
+                      int epi, const RopeArgs *ra) {
   NNHIP_REQUIRE(K % 128 == 0 && N % 64 == 0, kErrArg,
                 "gemm_limb: K % 128 and N % 64 must be 0");
-  NNHIP_REQUIRE(ksplit >= 1 && ksplit <= K / 128 &&
-                    (ksplit == 1 || epi == kEpiAddTotals),
-                kErrArg, "gemm_limb: a K split needs the atomic totals epilogue");
   NNHIP_REQUIRE(epi != kEpiRope || ra, kErrArg,
                 "gemm_limb: RoPE epilogue needs its arguments");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
@@ -1304,56 +995,19 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   const int ntm = (rows + kGemmMT - 1) / kGemmMT;
   const bool wide = ntm * (N / 64) >= 512 && g_gemm_wide != 0;
   if (wide) {
-    const int ntn = N / 64, per = (ntm * ntn * ksplit + 7) / 8;
+    const int ntn = N / 64, per = (ntm * ntn + 7) / 8;
     hipLaunchKernelGGL(gemm_limb_kernel<2>, dim3(8 * per), dim3(256), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
-                       ldr, y, ldy, epi, ntm, ntn, rz, ksplit);
+                       ldr, y, ldy, epi, ntm, ntn, rz);
   } else {
-    const int ntn = N / 32, per = (ntm * ntn * ksplit + 7) / 8;
+    const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
     hipLaunchKernelGGL(gemm_limb_kernel<1>, dim3(8 * per), dim3(256), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
-                       ldr, y, ldy, epi, ntm, ntn, rz, ksplit);
+                       ldr, y, ldy, epi, ntm, ntn, rz);
   }
   NNHIP_CHECK(hipGetLastError());
 }
 
-// full-K-wave GEMM (gemm_fk_kernel) over the same operands as the LDS GEMM
-static void launch_gemm_fk(hipStream_t st, int mode, const int8_t *limbs,
-                           int mpad, const int *rexp, const float *x,
-                           int64_t ldx, const float *lng, const float *lnb,
-                           float *ln_out, int64_t ldo, int rows, int K, int N,
-                           const int8_t *wq, const float *scale,
-                           const float *bias, const float *resid, int64_t ldr,
-                           float *y, int64_t ldy, int epi, const RopeArgs &rz,
-                           int ntm) {
-  const int ntn = (N + 32 * kFkWaves - 1) / (32 * kFkWaves);
-  const int per = (ntm * ntn + 7) / 8;
-  dim3 grid(8 * per);
-#define NNHIP_FK(MD, KP)                                                      \
-  if (epi == kEpiResid)                                                       \
-    hipLaunchKernelGGL((gemm_fk_kernel<MD, KP, true>), grid, dim3(kFkThreads),\
-                       0, st, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out,    \
-                       ldo, rows, N, wq, scale, bias, resid, ldr, y, ldy,     \
-                       epi, ntm, ntn, rz);                                    \
-  else                                                                        \
-    hipLaunchKernelGGL((gemm_fk_kernel<MD, KP, false>), grid,                 \
-                       dim3(kFkThreads), 0, st, limbs, mpad, rexp, x, ldx,    \
-                       lng, lnb, ln_out, ldo, rows, N, wq, scale, bias,       \
-                       resid, ldr, y, ldy, epi, ntm, ntn, rz)
-#define NNHIP_FK_K(MD)                                                        \
-  switch (K) {                                                                \
-    case 128: NNHIP_FK(MD, 4); break;                                         \
-    case 256: NNHIP_FK(MD, 8); break;                                         \
-    case 512: NNHIP_FK(MD, 16); break;                                        \
-    default: NNHIP_FK(MD, 32); break;                                         \
-  }
-  if (mode == kAFromDigits) { NNHIP_FK_K(kAFromDigits) }
-  else if (mode == kAFromRows) { NNHIP_FK_K(kAFromRows) }
-  else { NNHIP_FK_K(kAFromLayerNorm) }
-#undef NNHIP_FK_K
-#undef NNHIP_FK
-  NNHIP_CHECK(hipGetLastError());
-}
 
 int gemm_lds_tile_width(int K) {
   // 16 waves of 32 columns over K/KS each: 128-column blocks when KS = 4
@@ -1389,13 +1043,6 @@ void launch_gemm_lds(hipStream_t st, int mode, const int8_t *limbs, int mpad,
   NNHIP_REQUIRE(!ts || !ts->out || (gemm_lds_tile_width(K) > 0 && epi == kEpiBias),
                 kErrArg, "gemm_lds: tile statistics need K of 512 or 1024 and a bias epilogue");
   const TileStatsArgs tz = ts ? *ts : TileStatsArgs{};
-  // (the full-K-wave GEMM's epilogue holds 32 columns a wave: no int8 append)
-  if (g_gemm_fk && !tz.out && !q8 &&
-      !(mode != kAFromDigits && K == 1024 && epi == kEpiResid)) {
-    launch_gemm_fk(st, mode, limbs, mpad, rexp, x, ldx, lng, lnb, ln_out, ldo,
-                   rows, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, rz, ntm);
-    return;
-  }
   const int ntn = (int)(gemm_lds_workgroups(rows, K, N) / ntm);
   // digit planes: a workgroup walks as many row tiles as it takes for all
   // workgroups to be resident at once (one per CU), so that the weights are

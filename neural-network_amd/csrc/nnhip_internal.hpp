@@ -81,23 +81,7 @@ enum Epi : int {
   kEpiResid = 1,   // y = resid + (acc*s + b)
   kEpiSwiGLU = 2,  // columns (2n, 2n+1) = (gate n, up n): y[n] = silu(g)*u
   kEpiTotals = 3,  // limb GEMM only: write the exact int64 dot totals
-  kEpiRope = 4,    // QKV projection: RoPE on q and k, k and v into the cache
-  kEpiAddTotals = 5 // limb GEMM only: add the int64 dot totals of the
-                    // workgroup's K range into y (int64, zeroed beforehand)
-                    // with device atomics (exact, order-free), for a K split
-                    // over workgroups; LinEpiArgs applies the epilogue
-};
-
-// A GEMM epilogue deferred to the kernel that reads its output: row m of
-// y = resid + (tot * 2^-texp[m] * scale + bias) (the kEpiResid arithmetic
-// of the limb GEMM), from the int64 totals of kEpiAddTotals; the reader
-// zeroes tot for the next accumulation.
-struct LinEpiArgs {
-  long long *tot = nullptr;       // [rows][N]
-  const int *texp = nullptr;      // [rows] exponents of the GEMM's digits
-  const float *scale = nullptr, *bias = nullptr;  // [N]
-  const float *resid = nullptr;   // [rows][ldr]
-  int64_t ldr = 0;
+  kEpiRope = 4     // QKV projection: RoPE on q and k, k and v into the cache
 };
 
 // Arguments of the kEpiRope epilogue: row m = b*S + s sits at position
@@ -278,15 +262,8 @@ __device__ inline int digit_exponent(float mx) {
 
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
-extern int g_gemm_fk;        // LDS GEMM: 1 = full-K-wave kernel
 // engine.hip
 extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
-extern int g_fold_norm;     // 1 = a pending LayerNorm folds into every LDS GEMM
-extern int g_down_split;    // 1 = the down projection splits K over
-                            //     workgroups (int64 atomic totals) and the
-                            //     next LayerNorm applies its epilogue
-extern int g_fold_small;    // 1 = ... and, on rows below g_lds_min_rows, into
-                            //     an LDS GEMM instead of a LayerNorm launch
 // workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
 constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
@@ -380,13 +357,11 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
 void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
                       int K, int8_t *limbs, int mpad, int *rexp);
 bool gemm_limb_q8_ok(int D);
-// ksplit > 1 (kEpiAddTotals only): the K range split over that many
-// workgroups per tile
 void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int *rexp, int rows, int K, int N,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
-                      int epi, const RopeArgs *ra = nullptr, int ksplit = 1);
+                      int epi, const RopeArgs *ra = nullptr);
 // QuantizedDense ctor (quantization.cpp:36-86) on rows of w [N][K]: one
 // scale per row = max|w| / max_q (1 when 0), codes clamp(round(w / scale),
 // +-max_q) one per byte; max_q 127 (bits 8, INT8) or 7 (bits 4, INT4)
@@ -450,8 +425,7 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
 int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys);
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,
-                      int8_t *limbs, int mpad, int *rexp,
-                      const LinEpiArgs *ea = nullptr);
+                      int8_t *limbs, int mpad, int *rexp);
 
 // tensor_ops.hip: strided fp32 operands of the ExecutionBackend ops
 // (include/backend/backend.hpp:35-206): element offset, shape and strides

@@ -120,23 +120,14 @@ def test_forward_vs_oracle(ctx, quant, S):
 WIDE = dict(vocab=512, d=1024, H=16, F=4096, L=1)
 
 
-@pytest.mark.parametrize("fk,split", [(0, 0), (1, 0), (0, 1)])
-def test_forward_wide_vs_oracle(ctx, fk, split):
+def test_forward_wide_vs_oracle(ctx):
     """80 rows through a d = 1024 layer: q/k/v with RoPE, the output
     projection with its residual, gate/up with SwiGLU on the LDS-resident
-    GEMMs (16-wave K-split kernel, or full-K waves with fk = 1); split = 1
-    runs the down projection as a K split with int64 atomic totals whose
-    epilogue the LayerNorm before the lm head applies."""
+    GEMMs, the down projection (K = 4096) on the digit-plane GEMM."""
     om, gm, _ = build(ctx, WIDE, 8, True, std=0.03)
     rng = np.random.default_rng(9)
     ids = rng.integers(0, 512, (2, 40)).astype(np.int32)
-    try:
-        ctx.set_option("gemm_fk", fk)
-        ctx.set_option("down_split", split)
-        got = gm.forward(ids)
-    finally:
-        ctx.set_option("gemm_fk", 0)
-        ctx.set_option("down_split", 0)
+    got = gm.forward(ids)
     for b in range(2):
         assert_rows_close(got[b], om.forward(ids[b]), 1e-4, f"forward b={b}")
     gm.free()
@@ -484,12 +475,9 @@ def test_spec_top_k_top_p_matches_oracle(ctx, top_k, top_p):
     gt.free(); gd.free()
 
 
-@pytest.mark.parametrize("groups", [1, 3])
 @pytest.mark.parametrize("T", [0.0, 1.0])
-def test_batch_matches_oracle_per_sequence(ctx, T, groups):
-    """B independent sequences in lockstep = B oracle runs (seq index b),
-    also when the batch is split into groups on separate streams."""
-    ctx.set_option("groups", groups)
+def test_batch_matches_oracle_per_sequence(ctx, T):
+    """B independent sequences in lockstep = B oracle runs (seq index b)."""
     ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 30, True, std=0.2)
     B = 6
     rng = np.random.default_rng(31)
@@ -499,27 +487,17 @@ def test_batch_matches_oracle_per_sequence(ctx, T, groups):
     for b in range(B):
         check_stream(ot, od, got[b], prompts[b], 40, 3, T, 77, seq=b,
                      dev=stats[b], what=f"b={b}")
-    ctx.set_option("groups", 0)
     gt.free(); gd.free()
 
 
-@pytest.mark.parametrize("fk,split", [(0, 0), (1, 0), (0, 1)])
-def test_batch_mfma_rows_match_oracle(ctx, fk, split):
+def test_batch_mfma_rows_match_oracle(ctx):
     """B = 20 rows of drafting use the MFMA digit GEMM (rows >= 16); the
-    100-row verify and the 320-row prefill use the LDS-resident GEMMs.
-    fk = 1: full-K-wave GEMMs; split = 1: the down projection split over
-    workgroups with int64 atomic totals, its epilogue in the LayerNorm."""
+    100-row verify and the 320-row prefill use the LDS-resident GEMMs."""
     ot, gt, od, gd = spec_pair(ctx, TOY_T, TOY_D, 40, True, std=0.2)
     B = 20
     rng = np.random.default_rng(41)
     prompts = rng.integers(0, 256, (B, 16)).astype(np.int32)
-    try:
-        ctx.set_option("gemm_fk", fk)
-        ctx.set_option("down_split", split)
-        got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
-    finally:
-        ctx.set_option("gemm_fk", 0)
-        ctx.set_option("down_split", 0)
+    got, stats, _ = gt.generate_speculative_batch(gd, prompts, 24, 4, 0.0, 5)
     for b in (0, 7, 19):
         want, _ = O.generate_speculative(ot, od, prompts[b], 24, 4, 0.0, 5,
                                          seq=b)

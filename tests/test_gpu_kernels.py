@@ -198,36 +198,13 @@ def test_lds_gemm_matches_digit_gemm(ctx, rows, K, N):
     assert_as_accurate(g3, want, exact, what="lds gemm")
 
 
-@pytest.mark.parametrize("rows,K,N", LDS_SHAPES + [(70, 1024, 8192)])
-def test_full_k_gemm_matches_lds_gemm(ctx, rows, K, N):
-    """The full-K-wave GEMM (no cross-wave sums, epilogue on the
-    accumulators) gives bit-identical outputs to the 16-wave K-split LDS
-    GEMM, from fp32 rows (path 3) and from digit planes (path 4)."""
-    rng = np.random.default_rng(rows * 3 + K + 7 * N)
-    x = rng.standard_normal((rows, K)).astype(np.float32)
-    x[-1] *= 1e-3
-    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
-    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
-    codes, scales = quantize_oracle(w)
-    ref3 = linear_path(ctx, x, codes, scales, b, 3)
-    ref4 = linear_path(ctx, x, codes, scales, b, 4)
-    try:
-        ctx.set_option("gemm_fk", 1)
-        np.testing.assert_array_equal(linear_path(ctx, x, codes, scales, b, 3), ref3)
-        np.testing.assert_array_equal(linear_path(ctx, x, codes, scales, b, 4), ref4)
-    finally:
-        ctx.set_option("gemm_fk", 0)
-
-
-@pytest.mark.parametrize("fk", [0, 1])
 @pytest.mark.parametrize("rows,K,N", [(32, 512, 1536), (192, 1024, 8192),
                                       (20, 128, 256), (7, 256, 64),
                                       (1, 512, 2048), (5, 1024, 512)])
-def test_layernorm_linear_vs_oracle(ctx, rows, K, N, fk):
-    """LayerNorm fused into the GEMM prologue (16-wave K-split GEMM, or
-    full-K waves with fk = 1; rows below 16: the GEMV's prologue): LN(h)
-    against the oracle's layernorm, y against the oracle's dense over the
-    oracle's LN(h)."""
+def test_layernorm_linear_vs_oracle(ctx, rows, K, N):
+    """LayerNorm fused into the GEMM prologue (rows below 16: the GEMV's
+    prologue): LN(h) against the oracle's layernorm, y against the oracle's
+    dense over the oracle's LN(h)."""
     rng = np.random.default_rng(rows + K + 3 * N)
     h = (rng.standard_normal((rows, K)) * 2 + 0.3).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
@@ -243,12 +220,8 @@ def test_layernorm_linear_vs_oracle(ctx, rows, K, N, fk):
     dc, ds, db = (ctx.array(np.ascontiguousarray(codes.T)), ctx.array(scales),
                   ctx.array(b))
     dln, dy = ctx.array(shape=(rows, K)), ctx.array(shape=(rows, N))
-    try:
-        ctx.set_option("gemm_fk", fk)
-        call("nnhip_layernorm_linear_w8a32", ctx.h, dh.p, rows, K, dg.p, dbt.p,
-             dln.p, dc.p, ds.p, db.p, N, dy.p)
-    finally:
-        ctx.set_option("gemm_fk", 0)
+    call("nnhip_layernorm_linear_w8a32", ctx.h, dh.p, rows, K, dg.p, dbt.p,
+         dln.p, dc.p, ds.p, db.p, N, dy.p)
     assert_rows_close(dln.numpy(), ln, 1e-5, "fused layernorm")
     assert_rows_close(dy.numpy(), want, 1e-4, "layernorm linear")
 
