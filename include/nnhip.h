@@ -216,7 +216,8 @@ int nnhip_quantize_w4(nnhip_ctx *ctx, const float *w, int in, int out,
  * x [rows][K] . (codes * scales)^T + bias.  path: 0 auto, 1 fp32 GEMV,
  * 2 int8-digit MFMA GEMM (K % 128 == 0, N % 64 == 0), 3 MFMA GEMM with the
  * digits formed in LDS from x, 4 the same GEMM fed with digit planes
- * (3 and 4: K in {128, 256, 512, 1024}, N % 32 == 0). */
+ * (3 and 4: K in {128, 256, 512, 1024}, N % 32 == 0).  The MFMA paths (2-4)
+ * agree bit for bit. */
 int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
                        const int8_t *codes, const float *scales,
                        const float *bias, int N, float *y, int path);
@@ -411,7 +412,8 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
  * 3 = LDS GEMM digitising fp32 rows, 4 = LDS GEMM over digit planes (their
  * digit split included), 5 = LDS GEMM with LayerNorm in its prologue,
  * 6 = LDS GEMM over digit planes made once, with the lm head's tile
- * softmax statistics (K of 512 or 1024). */
+ * softmax statistics (K of 512 or 1024); the GEMM alone over digit planes
+ * made once: 7 = LDS GEMM, 8 = digit-plane GEMM. */
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms);
 

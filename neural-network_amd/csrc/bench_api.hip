@@ -138,7 +138,9 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
 // path 1 = fp32 GEMV, 2 = int8-digit MFMA GEMM (digit split included),
 // 3 = LDS GEMM from fp32 rows, 4 = LDS GEMM over digit planes (digit split
 // included), 5 = LDS GEMM with LayerNorm (gamma 1, beta 0) in its prologue,
-// 6 = LDS GEMM over digit planes made once, with tile statistics.
+// 6 = LDS GEMM over digit planes made once, with tile statistics; over
+// digit planes made once, the GEMM alone: 7 = LDS GEMM, 8 = digit-plane
+// GEMM.
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms) {
   return guard([&] {
@@ -165,8 +167,11 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     nnhip::DevBuf<float> g1(K), b0(K);
     nnhip::launch_fill(st, g1.p, K, 1.f);
     nnhip::launch_fill(st, b0.p, K, 0.f);
-    NNHIP_REQUIRE(path <= 2 || nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
-                  "nnhip_bench_linear: shape not supported by the LDS GEMM");
+    NNHIP_REQUIRE(path >= 1 && path <= 8, nnhip::kErrArg, "nnhip_bench_linear: unknown path");
+    NNHIP_REQUIRE(path <= 2 || path >= 8 || nnhip::gemm_lds_supports(rows, K, N),
+                  nnhip::kErrArg, "nnhip_bench_linear: shape not supported by the LDS GEMM");
+    NNHIP_REQUIRE(path != 8 || (K % 128 == 0 && N % 64 == 0), nnhip::kErrArg,
+                  "nnhip_bench_linear: the digit-plane GEMM needs K % 128 == 0, N % 64 == 0");
     // path 6: digit planes prepared once, then the GEMM alone with the lm
     // head's tile statistics (T = 1)
     const int tw = nnhip::gemm_lds_tile_width(K);
@@ -176,15 +181,18 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     nnhip::DevBuf<float2> tstat(path == 6 ? (size_t)rows * ntile : 0);
     nnhip::TileStatsArgs tsa;
     tsa.out = tstat.p; tsa.ld = ntile; tsa.T = 1.f;
-    if (path == 6)
+    if (path >= 6)
       nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      if (path >= 3) {
+      if (path == 8) {
+        nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, WS[j].p,
+                                S[j].p, b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
+      } else if (path >= 3) {
         if (path == 4)
           nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
         const int mode = path == 3 ? nnhip::kAFromRows
-                         : path == 4 || path == 6 ? nnhip::kAFromDigits
+                         : path == 4 || path >= 6 ? nnhip::kAFromDigits
                                                   : nnhip::kAFromLayerNorm;
         nnhip::launch_gemm_lds(st, mode, limbs.p, mpad, rexp.p, x.p, K, g1.p,
                                b0.p, nullptr, 0, rows, K, N, WS[j].p, S[j].p,

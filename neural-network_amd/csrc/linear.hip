@@ -31,13 +31,6 @@ constexpr int kWave = 64;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  // SwiGLU::forward (layer.cpp:1704-1710): (g * sigmoid(g)) * u, with
-  // sigmoid = 1 / (1 + exp(-g)) (cpu_backend.cpp:483-489).
-  float sg = 1.0f / (1.0f + expf(-g));
-  float a = __fmul_rn(g, sg);
-  return __fmul_rn(a, u);
-}
 
 // ---------------------------------------------------------------------------
 // GEMV: y[r][n] = epi( sum_k x[r][k] * w[n][k] ), r < R (<= 8).
@@ -238,7 +231,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       float a1 = 0.f;
       for (int s = 0; s < nks; ++s) a1 += red[cs * nks + s][cc + 1][r];
       float u = (Q8 ? a1 * scale[n + 1] : a1) + bias[n + 1];
-      if (epi == kEpiSwiGLU) y[r * ldy + n / 2] = silu_mul(v, u);
+      if (epi == kEpiSwiGLU) y[r * ldy + n / 2] = swiglu_pair(v, u);
       else rope_store_pair(ra, row0 + r, (int)n, v, u);
     } else if (epi == kEpiResid) {
       y[r * ldy + n] = resid[r * ldr + n] + v;
@@ -405,10 +398,10 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
       continue;
     }
     float v[2];
-    v[0] = __fadd_rn(__fmul_rn(ldexpf((float)tot[0], -e_ex[it]), e_sc0), e_bi0);
-    v[1] = __fadd_rn(__fmul_rn(ldexpf((float)tot[1], -e_ex[it]), e_sc1), e_bi1);
+    v[0] = dequant_epilogue(tot[0], e_ex[it], e_sc0, e_bi0);
+    v[1] = dequant_epilogue(tot[1], e_ex[it], e_sc1, e_bi1);
     if (epi == kEpiSwiGLU) {
-      y[(int64_t)m * ldy + n / 2] = silu_mul(v[0], v[1]);
+      y[(int64_t)m * ldy + n / 2] = swiglu_pair(v[0], v[1]);
     } else if (epi == kEpiRope) {
       if (ra.kq) rope_store_pair_q8(ra, m, n, v[0], v[1]);
       else rope_store_pair(ra, m, n, v[0], v[1]);
@@ -714,11 +707,10 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
         yt[0] = et[it][0]; yt[1] = et[it][1];
         continue;
       }
-      float v0 = ldexpf((float)et[it][0], -eex[it]), v1 = ldexpf((float)et[it][1], -eex[it]);
-      v0 = __fadd_rn(__fmul_rn(v0, esc[it][0]), ebi[it][0]);
-      v1 = __fadd_rn(__fmul_rn(v1, esc[it][1]), ebi[it][1]);
+      float v0 = dequant_epilogue(et[it][0], eex[it], esc[it][0], ebi[it][0]);
+      float v1 = dequant_epilogue(et[it][1], eex[it], esc[it][1], ebi[it][1]);
       if (epi == kEpiSwiGLU) {
-        y[(int64_t)m * ldy + n / 2] = silu_mul(v0, v1);
+        y[(int64_t)m * ldy + n / 2] = swiglu_pair(v0, v1);
       } else if (epi == kEpiRope) {
         if constexpr (Q8KV) rope_store_pair_q8(ra, m, n, v0, v1);
         else rope_store_pair(ra, m, n, v0, v1);
@@ -737,9 +729,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
         const int row = idx / (NC / 2), c0 = 2 * (idx % (NC / 2));
         const int m = m0 + row, n = n0 + c0;
         if (m >= M) continue;                  // whole wave
-        float l0 = ldexpf((float)et[it][0], -eex[it]), l1 = ldexpf((float)et[it][1], -eex[it]);
-        l0 = __fadd_rn(__fmul_rn(l0, esc[it][0]), ebi[it][0]);
-        l1 = __fadd_rn(__fmul_rn(l1, esc[it][1]), ebi[it][1]);
+        const float l0 = dequant_epilogue(et[it][0], eex[it], esc[it][0], ebi[it][0]);
+        const float l1 = dequant_epilogue(et[it][1], eex[it], esc[it][1], ebi[it][1]);
         if (tsa.T > 0.f) {
           float s0 = n < N ? (tsa.T == 1.f ? l0 : l0 / tsa.T) : -INFINITY;
           float s1 = n + 1 < N ? (tsa.T == 1.f ? l1 : l1 / tsa.T) : -INFINITY;

@@ -216,6 +216,21 @@ __host__ __device__ inline bool rope_q8_head_dim_ok(int D) {
 static constexpr int kLimbs = 3;
 static constexpr int kLimbBits = 22;  // |X| < 2^22
 
+// The MFMA GEMMs' common epilogue steps, shared so that every kernel that
+// forms the same integer total writes the same float.
+// Dequantisation of an exact dot total of row digits (exponent e) and int8
+// codes: tot * 2^-e * scale + bias, product and sum in one rounding.
+__device__ inline float dequant_epilogue(long long tot, int e, float sc, float bi) {
+  return fmaf(ldexpf((float)tot, -e), sc, bi);
+}
+// SwiGLU::forward (layer.cpp:1704-1710) on one (gate, up) pair:
+// (g * sigmoid(g)) * u, sigmoid = 1 / (1 + exp(-g)) (cpu_backend.cpp:483-489).
+__device__ inline float swiglu_pair(float g, float u) {
+  const float sg = 1.0f / (1.0f + expf(-g));
+  const float a = __fmul_rn(g, sg);
+  return __fmul_rn(a, u);
+}
+
 // MFMA operand layout of an int8 [R][K] matrix (R % 32 == 0, K % 128 == 0):
 // element (m, k) lives at
 //   [m/32][k/128][(k%64)/16][lane = ((k%128)/64)*32 + m%32][k%16],
