@@ -67,14 +67,14 @@ def kv_bytes(cfg, n_keys, q8=False):
     return cfg["L"] * 2 * n_keys * cfg["d"] * 4
 
 
-def cycle_bytes(ctx_len, k, Bn, q8=False):
+def cycle_bytes(ctx_len, k, Bn, q8=False, target=TARGET, draft=DRAFT):
     """Algorithmic HBM bytes of one cycle at mean context ctx_len: verify
     (weights once, k+1 rows of KV per sequence), k draft forwards (the
     catch-up token rides in the first of them) and the logits written and
     read by sampling."""
-    v = weight_bytes(TARGET) + Bn * kv_bytes(TARGET, ctx_len + k + 1, q8)
-    dr = k * (weight_bytes(DRAFT) + Bn * kv_bytes(DRAFT, ctx_len + k, q8))
-    lg = Bn * (2 * k + 1) * TARGET["vocab"] * 4 * 2
+    v = weight_bytes(target) + Bn * kv_bytes(target, ctx_len + k + 1, q8)
+    dr = k * (weight_bytes(draft) + Bn * kv_bytes(draft, ctx_len + k, q8))
+    lg = Bn * (2 * k + 1) * target["vocab"] * 4 * 2
     return v + dr + lg
 
 
@@ -135,10 +135,25 @@ def run_cfg2(ctx):
     prompt = rng.integers(0, 4096, (1, 128)).astype(np.int32)
     t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
     out, stats, tm = t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
+    # the target's GEMV at the verify shape (k + 1 = 5 rows): gate/up and
+    # the lm head, int8 codes read once per launch
+    gemv = {}
+    for name, K_, N_ in (("gate/up", 512, 4096), ("lm head", 512, 4096)):
+        ms = nnhip.bench_linear(ctx, 5, K_, N_, 1, iters=200, nbuf=4)
+        byt = N_ * K_ + 8 * N_ + 5 * K_ * 4 + 5 * N_ * 4
+        gemv[name] = dict(us=round(ms * 1e3, 2),
+                          GBs=round(byt / (ms / 1e3) / 1e9, 1))
     t.free(); d.free()
+    cyc = stats[0].cycles
+    byt = cyc * cycle_bytes(128 + 128, 4, 1, target=CFG2_T, draft=CFG2_D)
+    gbs = byt / (tm.decode_ms / 1e3) / 1e9
     return dict(tokens_per_s=255 / (tm.decode_ms / 1e3),
-                decode_ms=tm.decode_ms, cycles=stats[0].cycles,
-                accepted=stats[0].accepted)
+                decode_ms=tm.decode_ms, cycles=cyc,
+                ms_per_cycle=round(tm.decode_ms / max(cyc, 1), 4),
+                accepted=stats[0].accepted,
+                loop_roofline=dict(achieved_GBs=round(gbs, 1),
+                                   frac=round(gbs / HBM_PEAK_GBS, 4)),
+                gemv_verify=gemv)
 
 
 ATTN_SHAPE = dict(B=B, S=K_LOOK + 1, H=16, D=64, n_cached=P + NEW // 2)
@@ -184,6 +199,139 @@ def roofline_attention(ctx, w4=True, q8=False):
                         "attn_kernel<8, 8, 8> (verify, 8 key splits merged "
                         "in LDS)"),
                 bytes_per_launch=byt, us_per_launch=round(ms * 1e3, 2))
+
+
+INT8_PEAK_TOPS = 5000.0
+
+
+def dense_shapes(cfg):
+    """(K, N) of every Dense one forward runs, in the device's fused layout:
+    q/k/v, output, gate/up (interleaved), down per layer, then the lm head."""
+    d, F = cfg["d"], cfg["F"]
+    return [(d, 3 * d), (d, d), (d, 2 * F), (F, d)] * cfg["L"] + \
+        [(d, cfg["vocab"])]
+
+
+def verify_step(ctx, t, q8=False):
+    """One target forward at the verify shape (32 sequences x k+1 = 6 rows,
+    320 cached positions), replayed as a HIP graph.  Algorithmic bytes:
+    every int8 weight with its scales and biases once, the KV rows read,
+    the logits written.  MFMA work: every projection as three int8 digit
+    planes of the activations against the codes (3 x 2 x rows x K x N int8
+    ops)."""
+    S, n_cached = K_LOOK + 1, P + NEW // 2
+    ms = nnhip.bench_forward(t, B, S, n_cached, quantized=q8, iters=50)
+    rows = B * S
+    byt = (weight_bytes(TARGET) + B * kv_bytes(TARGET, n_cached + S, q8) +
+           rows * TARGET["vocab"] * 4)
+    ops = sum(3 * 2 * rows * k_ * n_ for k_, n_ in dense_shapes(TARGET))
+    gbs = byt / (ms / 1e3) / 1e9
+    tops = ops / (ms / 1e3) / 1e12
+    return dict(us=round(ms * 1e3, 1), bytes=byt, achieved_GBs=round(gbs, 1),
+                frac_hbm=round(gbs / HBM_PEAK_GBS, 4),
+                mfma_TOPS_3digit=round(tops, 1),
+                frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4),
+                rows=rows, n_cached=n_cached,
+                kv="int8" if q8 else "fp32")
+
+
+# The cycle's GEMM launches (batch 32, k = 5): the 5 draft forwards on 32
+# rows (d 512; the first also carries the catch-up row, 64 rows) and the
+# verify forward on 192 rows (d 1024), with the kernel each runs in the
+# library (nnhip_bench_linear path: 3 = LDS GEMM digitising fp32 rows,
+# 6 = LDS GEMM over digit planes with the lm head's tile statistics,
+# 7 = LDS GEMM over digit planes, 8 = digit-plane GEMM) and launches per
+# cycle.
+CYCLE_GEMMS = [
+    # name, rows, K, N, path, kernel family, launches per cycle
+    ("draft qkv", 32, 512, 1536, 8, "gemm_limb_kernel", 16),
+    ("draft o", 32, 512, 512, 3, "gemm_lds_kernel", 16),
+    ("draft gate/up", 32, 512, 4096, 8, "gemm_limb_kernel", 16),
+    ("draft down", 32, 2048, 512, 8, "gemm_limb_kernel", 16),
+    ("draft lm head", 32, 512, 32000, 6, "gemm_lds_kernel", 4),
+    ("draft qkv (catch-up)", 64, 512, 1536, 7, "gemm_lds_kernel", 4),
+    ("draft o (catch-up)", 64, 512, 512, 3, "gemm_lds_kernel", 4),
+    ("draft gate/up (catch-up)", 64, 512, 4096, 7, "gemm_lds_kernel", 4),
+    ("draft down (catch-up)", 64, 2048, 512, 8, "gemm_limb_kernel", 4),
+    ("draft lm head (catch-up)", 32, 512, 32000, 6, "gemm_lds_kernel", 1),
+    ("verify qkv", 192, 1024, 3072, 7, "gemm_lds_kernel", 12),
+    ("verify o", 192, 1024, 1024, 3, "gemm_lds_kernel", 12),
+    ("verify gate/up", 192, 1024, 8192, 7, "gemm_lds_kernel", 12),
+    ("verify down", 192, 4096, 1024, 8, "gemm_limb_kernel", 12),
+    ("verify lm head", 192, 1024, 32000, 6, "gemm_lds_kernel", 1),
+]
+
+
+def gemm_bytes(rows, K, N, path):
+    """Algorithmic bytes of one GEMM launch: int8 codes, fp32 scale and bias
+    per column, the activations as read (three int8 digit planes and an
+    exponent per row, or fp32 rows for path 3), fp32 outputs written (tile
+    statistics instead of logits are not counted: the logits are written
+    too)."""
+    act = rows * K * 4 if path == 3 else rows * (3 * K + 4)
+    return N * K + 8 * N + act + rows * N * 4
+
+
+def gemm_table(ctx):
+    """Each GEMM shape of the cycle timed alone (HIP events around 100
+    launches over 4 weight sets), its bytes and int8 MFMA rate, then per
+    kernel family the launch-weighted totals per cycle."""
+    rows_out, fam = [], {}
+    for name, rows, K, N, path, kern, n in CYCLE_GEMMS:
+        ms = nnhip.bench_linear(ctx, rows, K, N, path, iters=100, nbuf=4)
+        us = ms * 1e3
+        byt = gemm_bytes(rows, K, N, path)
+        ops = 3 * 2 * rows * K * N
+        rows_out.append(dict(name=name, rows=rows, K=K, N=N, kernel=kern,
+                             launches=n, us=round(us, 2),
+                             GBs=round(byt / us / 1e3, 1),
+                             TOPS_3digit=round(ops / us / 1e6, 1)))
+        f = fam.setdefault(kern, dict(us=0.0, bytes=0, ops=0, launches=0))
+        f["us"] += n * us
+        f["bytes"] += n * byt
+        f["ops"] += n * ops
+        f["launches"] += n
+    families = {k: dict(us_per_cycle=round(v["us"], 1), launches=v["launches"],
+                        achieved_GBs=round(v["bytes"] / v["us"] / 1e3, 1),
+                        TOPS_3digit=round(v["ops"] / v["us"] / 1e6, 1))
+                for k, v in fam.items()}
+    return rows_out, families, fam
+
+
+def roofline_gemm(fam, kern):
+    """HBM roofline of one GEMM kernel family over the cycle's launches:
+    launch-weighted algorithmic bytes over launch-weighted time."""
+    f = fam[kern]
+    ach = f["bytes"] / f["us"] / 1e3
+    return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
+                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4), traffic=None,
+                kernel=kern, launches_per_cycle=f["launches"],
+                us_per_launch=round(f["us"] / f["launches"], 2),
+                bytes_per_launch=int(f["bytes"] / f["launches"]),
+                mfma_TOPS_3digit=round(f["ops"] / f["us"] / 1e6, 1),
+                mfma_frac=round(f["ops"] / f["us"] / 1e6 / INT8_PEAK_TOPS, 4))
+
+
+def cfg3_cfg5(ctx):
+    """The attention microbench (16 x 8 heads of 64, 2048 cached + 8 new
+    queries, fp32) and the acceptance microbench (256 sequences x 8
+    positions x vocab 32000, T = 1), 1000 and 200 timed launches."""
+    ms = nnhip.bench_attention(ctx, 16, 8, 8, 64, 2048, iters=1000, nbuf=4)
+    byt = attention_bytes(16, 8, 8, 64, 2048 + 8)
+    c3 = dict(us=round(ms * 1e3, 2), bytes=byt,
+              achieved_GBs=round(byt / (ms / 1e3) / 1e9, 1),
+              frac=round(byt / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+    ms5, nacc = nnhip.bench_spec_accept(ctx, 256, 8, 32000, 1.0, iters=200,
+                                        nbuf=3)
+    # algorithmic bytes: every target logit once (the softmax statistics
+    # of each position), then per sequence the target logits and draft
+    # probabilities of the one row the residual resample reads
+    b5 = 256 * 8 * 32000 * 4 + 256 * 2 * 32000 * 4
+    c5 = dict(us=round(ms5 * 1e3, 2), bytes=b5,
+              achieved_GBs=round(b5 / (ms5 / 1e3) / 1e9, 1),
+              frac=round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+              mean_accepted=round(float(np.mean(nacc)), 3))
+    return c3, c5
 
 
 def traffic_probe():
@@ -302,7 +450,13 @@ def main():
         print(json.dumps({"batch1": run_cfg2(ctx)}), flush=True)
         return
     r = run_cfg4(ctx, a.steps, a.warmup)
-    roof = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
+    attn = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
+    log("verify step, GEMM shapes, attention and acceptance microbenches")
+    ver = verify_step(ctx, r["models"][0])
+    gemms, families, fam = gemm_table(ctx)
+    dominant = max(fam, key=lambda k: fam[k]["us"])
+    roof = roofline_gemm(fam, dominant)
+    c3, c5 = cfg3_cfg5(ctx)
     kv8 = None
     if not a.no_kv_int8:
         r8 = run_cfg4(ctx, 1, 1, models=r["models"], q8=True)
@@ -313,7 +467,8 @@ def main():
                "loop_roofline": {
                    "achieved_GBs": round(r8["loop_GBs"], 1),
                    "frac": round(r8["loop_GBs"] / HBM_PEAK_GBS, 4)},
-               "attention": roofline_attention(ctx, q8=True)}
+               "attention": roofline_attention(ctx, q8=True),
+               "verify_step": verify_step(ctx, r["models"][0], q8=True)}
     b1 = None if a.no_batch1 else run_cfg2(ctx)
     cpu = None if a.no_cpu_baseline else cpu_baseline(r["models"])
     ms_step = r["wall_s"] / a.steps * 1e3
@@ -343,6 +498,12 @@ def main():
         "loop_roofline": {"achieved_GBs": round(r["loop_GBs"], 1),
                           "frac": round(r["loop_GBs"] / HBM_PEAK_GBS, 4)},
         "roofline": roof,
+        "attention_roofline": attn,
+        "verify_step": ver,
+        "gemm_families": families,
+        "gemm_shapes": gemms,
+        "cfg3_attention": c3,
+        "cfg5_accept": c5,
         "kv_int8": kv8,
         "batch1": b1,
         "cpu_baseline": cpu,

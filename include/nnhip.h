@@ -416,6 +416,13 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
  * made once: 7 = LDS GEMM, 8 = digit-plane GEMM. */
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms);
+/* One TransformerDecoder::forward (layer.cpp:1159-1216) of m over B
+ * sequences x S new tokens after n_cached cached positions (zeros), logits
+ * of every row written -- the speculative loop's verify step at S = k + 1
+ * -- replayed as a captured HIP graph; ms = milliseconds per forward.
+ * quantized != 0: int8 KV cache. */
+int nnhip_bench_forward(nnhip_model *m, int B, int S, int n_cached,
+                        int quantized, int iters, float *ms);
 
 #ifdef __cplusplus
 }

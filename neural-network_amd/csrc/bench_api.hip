@@ -210,4 +210,77 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
   });
 }
 
+// One forward of the model over B sequences x S new tokens after n_cached
+// cached positions (the verify step of the speculative loop: S = k + 1),
+// logits of every row written: TransformerDecoder::forward (layer.cpp:
+// 1159-1216) with its KV cache.  The cache holds zeros; the forward writes
+// positions [n_cached, n_cached + S) each time.  Captured once as a HIP
+// graph and replayed, as the loop replays its cycle.
+int nnhip_bench_forward(nnhip_model *mm, int B, int S, int n_cached,
+                        int quantized, int iters, float *ms) {
+  return guard([&] {
+    NNHIP_REQUIRE(mm && ms && B > 0 && S > 0 && n_cached >= 0 && iters > 0,
+                  nnhip::kErrArg, "nnhip_bench_forward: bad argument");
+    nnhip::Model &m = *mm->m;
+    NNHIP_REQUIRE(n_cached + S <= m.max_seq, nnhip::kErrCapacity,
+                  "nnhip_bench_forward: n_cached + S exceeds max_seq_len");
+    hipStream_t st = m.ctx->stream;
+    nnhip::KVCache kv(&m, B, m.max_seq, quantized != 0);
+    if (kv.q8) {
+      NNHIP_CHECK(hipMemsetAsync(kv.kq.p, 0, kv.kq.bytes(), st));
+      NNHIP_CHECK(hipMemsetAsync(kv.vq.p, 0, kv.vq.bytes(), st));
+      nnhip::launch_fill(st, kv.ks.p, (int64_t)kv.ks.n, 1.f);
+      nnhip::launch_fill(st, kv.vs.p, (int64_t)kv.vs.n, 1.f);
+    } else {
+      NNHIP_CHECK(hipMemsetAsync(kv.k.p, 0, kv.k.bytes(), st));
+      NNHIP_CHECK(hipMemsetAsync(kv.v.p, 0, kv.v.bytes(), st));
+    }
+    std::vector<int32_t> lens(B, n_cached);
+    NNHIP_CHECK(hipMemcpyAsync(kv.len.p, lens.data(), (size_t)B * 4,
+                               hipMemcpyHostToDevice, st));
+    nnhip::DevBuf<int32_t> ids((size_t)B * S);
+    NNHIP_CHECK(hipMemsetAsync(ids.p, 0, ids.bytes(), st));
+    nnhip::DevBuf<float> logits((size_t)B * S * m.V);
+    auto fwd = [&] {
+      m.forward(&kv, 0, ids.p, S, B, S, kv.len.p, 0, nullptr, n_cached + S,
+                logits.p, false);
+    };
+    fwd();  // sizes the workspace outside the capture
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    NNHIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    try {
+      fwd();
+    } catch (...) {
+      hipGraph_t g2 = nullptr;
+      (void)hipStreamEndCapture(st, &g2);
+      if (g2) (void)hipGraphDestroy(g2);
+      throw;
+    }
+    NNHIP_CHECK(hipStreamEndCapture(st, &graph));
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    NNHIP_CHECK(ie);
+    struct ExecGuard {
+      hipGraphExec_t e;
+      ~ExecGuard() { (void)hipGraphExecDestroy(e); }
+    } eg{exec};
+    struct Events {
+      hipEvent_t e[2] = {nullptr, nullptr};
+      ~Events() { for (hipEvent_t x : e) if (x) (void)hipEventDestroy(x); }
+    } ev;
+    NNHIP_CHECK(hipEventCreate(&ev.e[0]));
+    NNHIP_CHECK(hipEventCreate(&ev.e[1]));
+    NNHIP_CHECK(hipGraphLaunch(exec, st));  // warm-up replay
+    NNHIP_CHECK(hipEventRecord(ev.e[0], st));
+    for (int i = 0; i < iters; ++i) NNHIP_CHECK(hipGraphLaunch(exec, st));
+    NNHIP_CHECK(hipEventRecord(ev.e[1], st));
+    NNHIP_CHECK(hipEventSynchronize(ev.e[1]));
+    float t = 0.f;
+    NNHIP_CHECK(hipEventElapsedTime(&t, ev.e[0], ev.e[1]));
+    *ms = t / iters;
+  });
+}
+
 }  // extern "C"

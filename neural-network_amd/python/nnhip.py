@@ -146,6 +146,7 @@ SIGNATURES = {
     "nnhip_bench_spec_accept": [_vp, _i, _i, _i, _f, _i, _i,
                                 C.POINTER(C.c_float), _vp],
     "nnhip_bench_linear": [_vp, _i, _i, _i, _i, _i, _i, C.POINTER(C.c_float)],
+    "nnhip_bench_forward": [_vp, _i, _i, _i, _i, _i, C.POINTER(C.c_float)],
 }
 
 _lib = None
@@ -275,6 +276,15 @@ def bench_linear(ctx, rows, K, N, path, iters=100, nbuf=3):
     ms = C.c_float()
     call("nnhip_bench_linear", ctx.h, rows, K, N, path, iters, nbuf,
          C.byref(ms))
+    return ms.value
+
+
+def bench_forward(model, B, S, n_cached, quantized=False, iters=50):
+    """Milliseconds per graph-replayed forward of `model` (a Decoder) over
+    B x S new tokens after n_cached cached positions."""
+    ms = C.c_float()
+    call("nnhip_bench_forward", model.h, B, S, n_cached, int(quantized),
+         iters, C.byref(ms))
     return ms.value
 
 
