@@ -160,11 +160,15 @@ ATTN_SHAPE = dict(B=B, S=K_LOOK + 1, H=16, D=64, n_cached=P + NEW // 2)
 TRAFFIC_NOTE = os.path.join(ROOT, "profiles", "attention_verify_traffic.md")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the verify attention kernel, as measured by
-    the rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/."""
+GEMM_NOTE = os.path.join(ROOT, "profiles", "gemm_cycle_shapes.md")
+
+
+def measured_traffic(note=TRAFFIC_NOTE):
+    """HBM bytes per launch of a kernel as measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (the note's
+    traffic_bytes_per_launch line)."""
     try:
-        with open(TRAFFIC_NOTE) as f:
+        with open(note) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":")[1])
@@ -304,7 +308,9 @@ def roofline_gemm(fam, kern):
     f = fam[kern]
     ach = f["bytes"] / f["us"] / 1e3
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
-                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4), traffic=None,
+                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
+                traffic=(measured_traffic(GEMM_NOTE)
+                         if kern == "gemm_lds_kernel" else None),
                 kernel=kern, launches_per_cycle=f["launches"],
                 us_per_launch=round(f["us"] / f["launches"], 2),
                 bytes_per_launch=int(f["bytes"] / f["launches"]),
@@ -338,6 +344,18 @@ def traffic_probe():
     """For rocprofv3 --pmc runs: a plain device copy of 256 MiB (the
     calibration of FETCH_SIZE / WRITE_SIZE) followed by 20 launches of the
     verify attention kernel at the roofline shape."""
+    copy_calibration()
+    ctx = nnhip.Context(0)
+    sh = ATTN_SHAPE
+    ms = nnhip.bench_attention(ctx, sh["B"], sh["S"], sh["H"], sh["D"],
+                               sh["n_cached"], iters=20, nbuf=4)
+    log(f"attention: {ms * 1e3:.2f} us per launch, algorithmic bytes "
+        f"{attention_bytes(sh['B'], sh['S'], sh['H'], sh['D'], sh['n_cached'] + sh['S'])}")
+
+
+def copy_calibration():
+    """A plain device copy of 256 MiB, three times: the reference point for
+    scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
     import torch
     a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
     b_ = torch.empty_like(a)
@@ -345,12 +363,36 @@ def traffic_probe():
         b_.copy_(a)
     torch.cuda.synchronize()
     log(f"copied {a.numel() * 4} bytes x 3")
+
+
+def gemm_probe():
+    """For rocprofv3 --pmc runs: the copy calibration, then every GEMM shape
+    of the batch-32 cycle (20 launches each, the kernel alone over digit
+    planes made once, or digitising fp32 rows for the output projections)
+    and the prefill's gate/up projection (8192 rows = 32 prompts x 256)."""
+    copy_calibration()
     ctx = nnhip.Context(0)
-    sh = ATTN_SHAPE
-    ms = nnhip.bench_attention(ctx, sh["B"], sh["S"], sh["H"], sh["D"],
-                               sh["n_cached"], iters=20, nbuf=4)
-    log(f"attention: {ms * 1e3:.2f} us per launch, algorithmic bytes "
-        f"{attention_bytes(sh['B'], sh['S'], sh['H'], sh['D'], sh['n_cached'] + sh['S'])}")
+    for name, rows, K, N, path, kern, n in CYCLE_GEMMS:
+        ms = nnhip.bench_linear(ctx, rows, K, N, path, iters=20, nbuf=4)
+        log(f"{name}: {rows}x{K}x{N} path {path} {ms * 1e3:.2f} us")
+    ms = nnhip.bench_linear(ctx, B * P, 1024, 8192, 7, iters=20, nbuf=2)
+    log(f"prefill gate/up: {B * P}x1024x8192 path 7 {ms * 1e3:.2f} us")
+
+
+# batch-1 GEMV shapes of the target's verify step (k + 1 = 5 rows) and the
+# draft's single row: q/k/v, gate/up and the lm head
+GEMV_SHAPES = [(5, 512, 1536), (5, 512, 4096), (5, 512, 4096),
+               (1, 256, 768), (1, 256, 2048), (1, 256, 4096)]
+
+
+def gemv_probe():
+    """For rocprofv3 --pmc runs: the copy calibration, then the batch-1
+    GEMVs (fp32 rows x int8 codes), 20 launches each."""
+    copy_calibration()
+    ctx = nnhip.Context(0)
+    for rows, K, N in GEMV_SHAPES:
+        ms = nnhip.bench_linear(ctx, rows, K, N, 1, iters=20, nbuf=4)
+        log(f"gemv {rows}x{K}x{N}: {ms * 1e3:.2f} us")
 
 
 def cpu_model():
@@ -424,6 +466,15 @@ def main():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the copy calibration and the attention "
                          "kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only run the copy calibration and the cycle's GEMM "
+                         "shapes (for rocprofv3 --pmc)")
+    ap.add_argument("--gemv-probe", action="store_true",
+                    help="only run the copy calibration and the batch-1 "
+                         "GEMVs (for rocprofv3 --pmc)")
+    ap.add_argument("--loop-only", action="store_true",
+                    help="only the decode loop (no microbenchmarks): for "
+                         "kernel traces of the cycle")
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch each kernel of a cycle separately instead "
                          "of replaying one HIP graph per cycle")
@@ -440,6 +491,12 @@ def main():
     if a.traffic_probe:
         traffic_probe()
         return
+    if a.gemm_probe:
+        gemm_probe()
+        return
+    if a.gemv_probe:
+        gemv_probe()
+        return
     ctx = nnhip.Context(0)
     if a.no_graphs:
         ctx.set_option("graphs", 0)
@@ -450,6 +507,11 @@ def main():
         print(json.dumps({"batch1": run_cfg2(ctx)}), flush=True)
         return
     r = run_cfg4(ctx, a.steps, a.warmup)
+    if a.loop_only:
+        print(json.dumps({"value": round(r["value"], 1), "unit": "tokens/s",
+                          "decode_ms_per_step": round(r["decode_ms"] / a.steps, 2),
+                          "cycles": r["cycles"]}), flush=True)
+        return
     attn = roofline_attention(ctx, w4="attn_w4=0" not in a.option)
     log("verify step, GEMM shapes, attention and acceptance microbenches")
     ver = verify_step(ctx, r["models"][0])
