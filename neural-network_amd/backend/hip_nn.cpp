@@ -46,7 +46,10 @@ HipDecoder::HipDecoder(HipBackend &backend, TransformerDecoder &d,
 
 HipDecoder::~HipDecoder() { (void)nnhip_decoder_free(m_); }
 
-void HipDecoder::quantize() { check(nnhip_decoder_quantize(m_, 8)); }
+void HipDecoder::quantize(const QuantizationConfig &config) {
+  check(nnhip_decoder_quantize(
+      m_, config.type == QuantizationType::INT4 ? 4 : 8));
+}
 
 std::vector<float> HipDecoder::forward(const std::vector<size_t> &ids,
                                        HipKVCache *cache) {

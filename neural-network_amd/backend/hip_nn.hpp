@@ -48,9 +48,11 @@ class HipDecoder {
   HipDecoder(const HipDecoder &) = delete;
   HipDecoder &operator=(const HipDecoder &) = delete;
 
-  // every Dense (q, k, v, o, gate, up, down, lm_head) to symmetric int8 per
-  // output channel with the QuantizedDense formula (quantization.cpp:36-66)
-  void quantize();
+  // every Dense (q, k, v, o, gate, up, down, lm_head) to symmetric codes per
+  // output channel with the QuantizedDense formula (quantization.cpp:36-86):
+  // config.type INT8 (max|w| / 127) or INT4 (max|w| / 7), as quantize_model
+  // takes it (quantization.hpp:8-12, 43)
+  void quantize(const QuantizationConfig &config = QuantizationConfig{});
   // logits [S][V] of one sequence of ids [S]; cache may be null
   std::vector<float> forward(const std::vector<size_t> &ids,
                              HipKVCache *cache);
