@@ -44,6 +44,11 @@ class HipDecoder {
   // copies d.parameters() (layer.cpp:1140-1154, same order) to the device
   HipDecoder(HipBackend &backend, TransformerDecoder &d,
              const DecoderConfig &cfg);
+  // the same from host arrays in parameters() order (the shapes of
+  // nnhip_decoder_param_shape), for programs that hold the weights without
+  // a TransformerDecoder object (e.g. read from a file)
+  HipDecoder(HipBackend &backend, const DecoderConfig &cfg,
+             const std::vector<std::vector<float>> &params);
   ~HipDecoder();
   HipDecoder(const HipDecoder &) = delete;
   HipDecoder &operator=(const HipDecoder &) = delete;
@@ -91,8 +96,8 @@ class HipKVCache {
   nnhip_kvcache *c_ = nullptr;
 };
 
-// QuantizedDense (INT8) with its codes and scales resident on the device;
-// forward runs on tensors whose storage belongs to `backend`.
+// QuantizedDense (INT8 or INT4) with its codes and scales resident on the
+// device; forward runs on tensors whose storage belongs to `backend`.
 class HipQuantizedDense {
  public:
   HipQuantizedDense(HipBackend &backend, const QuantizedDense &layer);

@@ -6,9 +6,12 @@
 // softmax, :915-967 embedding; add / sub / mul / div via the broadcast shape
 // of the operands).  Checked against the reference's own known answers
 // (tests/core/tensor_test.cpp, tests/nn/layer_test.cpp), the oracle
-// (or_dense, or_layernorm) and closed forms.  Needs a GPU; prints one line a
-// check and exits non-zero on the first failure.
+// (or_dense, or_layernorm) and closed forms; then the decoder objects
+// HipDecoder / HipKVCache (backend/hip_nn.hpp) against the oracle's forward
+// and speculative decoding.  Needs a GPU; prints one line a check and exits
+// non-zero on the first failure.
 #include "backend/hip_backend.hpp"  // neural-network_amd/backend
+#include "backend/hip_nn.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -20,6 +23,28 @@
 
 extern "C" {
 // the oracle (tests' checker, oracle/oracle.h)
+typedef struct or_model or_model;
+typedef struct or_cache or_cache;
+typedef struct {
+  int64_t cycles, drafted, accepted, ties, resampled, bonus;
+  double prefill_ms, decode_ms;
+} or_spec_stats;
+or_model *or_model_create(int vocab, int d_model, int n_heads, int d_ff,
+                          int n_layers, int max_seq_len);
+void or_model_free(or_model *m);
+int or_model_num_params(const or_model *m);
+int or_model_param_shape(const or_model *m, int idx, int64_t *rows,
+                         int64_t *cols);
+int or_model_set_param(or_model *m, int idx, const float *data);
+int or_model_quantize_bits(or_model *m, int bits);
+int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
+               float *logits);
+int or_generate_speculative(const or_model *target, const or_model *draft,
+                            const int32_t *prompt, int P, int max_new,
+                            int lookahead, float temperature, int top_k,
+                            float top_p, uint64_t seed, int quantized_cache,
+                            uint32_t seq_index, int32_t *out,
+                            or_spec_stats *stats);
 void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
               const float *w, const int8_t *codes, const float *scales,
               const float *bias, float *y);
@@ -276,6 +301,105 @@ void test_fill_and_unsupported(ExecutionBackend &be) {
   std::printf("ok fill and unsupported ops\n");
 }
 
+// A decoder's parameters() as host arrays in the oracle's shapes, N(0, sd)
+// from a fixed seed, loaded into a fresh oracle model as well.
+struct OracleModel {
+  or_model *m = nullptr;
+  std::vector<std::vector<float>> params;
+  nnhip_backend::DecoderConfig cfg;
+  OracleModel(const nnhip_backend::DecoderConfig &c, unsigned seed, float sd)
+      : cfg(c) {
+    m = or_model_create((int)c.vocab_size, (int)c.embed_dim, (int)c.num_heads,
+                        (int)c.dim_feedforward, (int)c.num_layers,
+                        (int)c.max_seq_len);
+    const int n = or_model_num_params(m);
+    for (int i = 0; i < n; ++i) {
+      int64_t r = 0, cc = 0;
+      or_model_param_shape(m, i, &r, &cc);
+      params.push_back(randn((size_t)(r * cc), seed + 17u * (unsigned)i, sd));
+      or_model_set_param(m, i, params.back().data());
+    }
+  }
+  ~OracleModel() { or_model_free(m); }
+};
+
+double row_rel_err(const std::vector<float> &a, const std::vector<float> &b,
+                   size_t rows, size_t cols) {
+  double worst = 0.0;
+  for (size_t r = 0; r < rows; ++r) {
+    double num = 0.0, den = 0.0;
+    for (size_t c = 0; c < cols; ++c) {
+      num = std::max(num, (double)std::fabs(a[r * cols + c] - b[r * cols + c]));
+      den = std::max(den, (double)std::fabs(b[r * cols + c]));
+    }
+    worst = std::max(worst, num / std::max(den, 1e-30));
+  }
+  return worst;
+}
+
+std::vector<size_t> oracle_spec(const OracleModel &t, const OracleModel &d,
+                                 const std::vector<size_t> &prompt, int max_new,
+                                 int k) {
+  std::vector<int32_t> p(prompt.begin(), prompt.end());
+  std::vector<int32_t> out(p.size() + (size_t)std::max(max_new, 1));
+  or_spec_stats st;
+  or_generate_speculative(t.m, d.m, p.data(), (int)p.size(), max_new, k, 0.0f,
+                          0, 1.0f, 42, 0, 0, out.data(), &st);
+  return std::vector<size_t>(out.begin(), out.begin() + (long)(p.size() + max_new));
+}
+
+// HipDecoder / HipKVCache (the C++ drop-in decoder objects) against the
+// oracle: forward logits, the KV cache, and greedy speculative decoding in
+// fp32, INT8 and INT4 (the reference's SpeculativeDecodingParity with the
+// oracle as the CPU side).
+void test_decoder_adapter(HipBackend &hip) {
+  using nnhip_backend::HipDecoder;
+  using nnhip_backend::HipKVCache;
+  const nnhip_backend::DecoderConfig tc{96, 64, 2, 128, 2, 64};
+  const nnhip_backend::DecoderConfig dc{96, 32, 2, 64, 1, 64};
+  OracleModel ot(tc, 300, 0.1f), od(dc, 400, 0.1f);
+  HipDecoder t(hip, tc, ot.params), d(hip, dc, od.params);
+
+  std::vector<size_t> ids;
+  for (size_t i = 0; i < 10; ++i) ids.push_back((i * 37 + 5) % 96);
+  const std::vector<float> got = t.forward(ids, nullptr);
+  std::vector<int32_t> ids32(ids.begin(), ids.end());
+  std::vector<float> want(ids.size() * 96);
+  or_forward(ot.m, nullptr, ids32.data(), (int)ids32.size(), want.data());
+  const double e = row_rel_err(got, want, ids.size(), 96);
+  expect(e < 1e-4, "HipDecoder::forward vs or_forward (" + std::to_string(e) + ")");
+
+  // the cache: 7 tokens, then 3 more, equal to one forward of 10
+  HipKVCache cache(t);
+  const std::vector<size_t> a(ids.begin(), ids.begin() + 7), b(ids.begin() + 7, ids.end());
+  (void)t.forward(a, &cache);
+  const std::vector<float> tail = t.forward(b, &cache);
+  const std::vector<float> ref(want.begin() + 7 * 96, want.end());
+  expect(cache.length() == 10, "HipKVCache length after 7 + 3");
+  expect(row_rel_err(tail, ref, 3, 96) < 1e-4, "HipKVCache: cached forward == full forward");
+  cache.truncate(4);
+  expect(cache.length() == 4, "HipKVCache::truncate");
+
+  const std::vector<size_t> prompt(ids.begin(), ids.begin() + 8);
+  expect(t.generate_speculative(&d, prompt, 16, 3, 0.0f) == oracle_spec(ot, od, prompt, 16, 3),
+         "HipDecoder::generate_speculative fp32 greedy == oracle");
+  for (int bits : {8, 4}) {
+    OracleModel qt(tc, 300, 0.1f), qd(dc, 400, 0.1f);
+    or_model_quantize_bits(qt.m, bits);
+    or_model_quantize_bits(qd.m, bits);
+    HipDecoder ht(hip, tc, qt.params), hd(hip, dc, qd.params);
+    QuantizationConfig qc;
+    qc.type = bits == 4 ? QuantizationType::INT4 : QuantizationType::INT8;
+    ht.quantize(qc);
+    hd.quantize(qc);
+    expect(ht.generate_speculative(&hd, prompt, 16, 3, 0.0f) ==
+               oracle_spec(qt, qd, prompt, 16, 3),
+           "HipDecoder::generate_speculative INT" + std::to_string(bits) +
+               " greedy == oracle");
+  }
+  std::printf("ok HipDecoder / HipKVCache vs oracle\n");
+}
+
 }  // namespace
 
 int main() {
@@ -287,6 +411,7 @@ int main() {
     test_layernorm_vs_oracle(be);
     test_softmax_and_embedding(be);
     test_fill_and_unsupported(be);
+    test_decoder_adapter(hip);
   } catch (const std::exception &e) {
     std::printf("FAIL exception: %s\n", e.what());
     return 1;

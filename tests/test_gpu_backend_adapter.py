@@ -4,7 +4,10 @@ Runs tests/cpp/hip_backend_test, built by __graft_entry__.build() against the
 reference's headers (neural-network_amd/backend/Makefile): the Tensor-style
 op calls of src/core/tensor.cpp on HipBackend, checked against the
 reference's known answers (tensor_test.cpp, layer_test.cpp), the oracle's
-Dense product and LayerNorm (bit for bit) and closed forms.
+Dense product and LayerNorm (bit for bit) and closed forms; then the C++
+decoder objects HipDecoder / HipKVCache against the oracle (forward logits,
+the KV cache and truncate, greedy speculative decoding in fp32, INT8 and
+INT4).
 """
 import os
 import subprocess
