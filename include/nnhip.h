@@ -264,6 +264,14 @@ int nnhip_linear_limb_totals(nnhip_ctx *ctx, const float *x, int rows, int K,
 int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
                          int H, int D, const int32_t *pos, float *q_out,
                          float *kcache, float *vcache, int cap);
+/* nnhip_rope_kv_append with grouped-query heads (MultiHeadAttention's
+ * num_kv_heads, layer.cpp:471-489): qkv rows [q: H heads | k: Hkv heads |
+ * v: Hkv heads] of D, H a multiple of Hkv; kcache / vcache
+ * [B][Hkv][cap][D]. */
+int nnhip_rope_kv_append_gqa(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                             int H, int Hkv, int D, const int32_t *pos,
+                             float *q_out, float *kcache, float *vcache,
+                             int cap);
 /* Fused causal attention of MultiHeadAttention::forward (layer.cpp:842-952)
  * for S queries per sequence: q [B*S][H*D], kcache / vcache [B][Hkv][cap][D]
  * holding pos0[b] + S valid entries; query s sees keys j <= pos0[b] + s.

@@ -1,7 +1,8 @@
-// HipDecoder and HipKVCache (hip_nn.hpp) over libnnhip.so.  Nothing here
-// uses the reference's compiled code, only its headers' types, so programs
-// can run these objects without linking the reference's sources; the
-// constructor from a TransformerDecoder is in hip_nn.cpp.
+// HipDecoder, HipKVCache, HipMultiHeadAttention and HipMhaCache
+// (hip_nn.hpp) over libnnhip.so.  Nothing here uses the reference's compiled
+// code, only its headers' types, so programs can run these objects without
+// linking the reference's sources; the constructors from reference objects
+// and the Tensor overloads are in hip_nn.cpp.
 #include "hip_nn.hpp"
 
 #include <algorithm>
@@ -108,5 +109,165 @@ size_t HipKVCache::length() const {
   check(nnhip_kvcache_length(c_, 0, &n));
   return (size_t)n;
 }
+
+// ---- MultiHeadAttention ----------------------------------------------------
+
+namespace {
+
+std::unique_ptr<DeviceBuffer> upload_f32(HipBackend &be,
+                                         const std::vector<float> &v) {
+  std::unique_ptr<DeviceBuffer> d = be.allocate(v.size() * sizeof(float));
+  be.copy_host_to_device(v.data(), *d, v.size() * sizeof(float));
+  return d;
+}
+
+// w [in][out] -> rows [out][in] appended to dst
+void append_transposed(std::vector<float> &dst, const std::vector<float> &w,
+                       size_t in, size_t out) {
+  const size_t base = dst.size();
+  dst.resize(base + in * out);
+  for (size_t k = 0; k < in; ++k)
+    for (size_t n = 0; n < out; ++n) dst[base + n * in + k] = w[k * out + n];
+}
+
+float *fptr(DeviceBuffer &b) { return static_cast<float *>(b.data()); }
+int8_t *cptr(DeviceBuffer &b) { return static_cast<int8_t *>(b.data()); }
+
+}  // namespace
+
+HipMultiHeadAttention::HipMultiHeadAttention(
+    HipBackend &backend, const MhaConfig &cfg,
+    const std::vector<std::vector<float>> &params)
+    : be_(backend), cfg_(cfg) {
+  // the reference constructor's checks (layer.cpp:477-482)
+  if (cfg.num_heads == 0 || cfg.embed_dim % cfg.num_heads != 0)
+    throw std::runtime_error("embed_dim must be divisible by num_heads");
+  H_ = cfg.num_heads;
+  Hkv_ = cfg.num_kv_heads == 0 ? H_ : cfg.num_kv_heads;
+  if (H_ % Hkv_ != 0)
+    throw std::runtime_error("num_heads must be divisible by num_kv_heads");
+  D_ = cfg.embed_dim / H_;
+  if (D_ % 2 != 0)
+    throw std::runtime_error("HipMultiHeadAttention: RoPE needs an even head dim");
+  if (!cfg.causal)
+    throw std::runtime_error(
+        "HipMultiHeadAttention: non-causal attention is not on the device path");
+  const size_t E = cfg.embed_dim, Ekv = Hkv_ * D_;
+  const size_t sizes[8] = {E * E, E, E * Ekv, Ekv, E * Ekv, Ekv, E * E, E};
+  if (params.size() != 8)
+    throw std::runtime_error("HipMultiHeadAttention: parameter count mismatch");
+  for (int i = 0; i < 8; ++i)
+    if (params[i].size() != sizes[i])
+      throw std::runtime_error("HipMultiHeadAttention: parameter shape mismatch");
+  master_ = params;
+  std::vector<float> wqkv, bqkv;
+  append_transposed(wqkv, params[0], E, E);
+  append_transposed(wqkv, params[2], E, Ekv);
+  append_transposed(wqkv, params[4], E, Ekv);
+  for (int i : {1, 3, 5}) bqkv.insert(bqkv.end(), params[i].begin(), params[i].end());
+  std::vector<float> wo;
+  append_transposed(wo, params[6], E, E);
+  wqkv_ = upload_f32(be_, wqkv);
+  bqkv_ = upload_f32(be_, bqkv);
+  wo_ = upload_f32(be_, wo);
+  bo_ = upload_f32(be_, params[7]);
+}
+
+HipMultiHeadAttention::~HipMultiHeadAttention() = default;
+
+void HipMultiHeadAttention::quantize(const QuantizationConfig &config) {
+  const int bits = config.type == QuantizationType::INT4 ? 4 : 8;
+  const size_t E = cfg_.embed_dim, Ekv = Hkv_ * D_, Nqkv = E + 2 * Ekv;
+  cqkv_ = be_.allocate(Nqkv * E);
+  sqkv_ = be_.allocate(Nqkv * sizeof(float));
+  co_ = be_.allocate(E * E);
+  so_ = be_.allocate(E * sizeof(float));
+  // each projection from its fp32 [in][out] weights, into its rows of the
+  // fused codes and scales
+  auto quant = [&](const std::vector<float> &w, size_t out, int8_t *codes,
+                   float *scales) {
+    std::unique_ptr<DeviceBuffer> dw = upload_f32(be_, w);
+    check(bits == 4 ? nnhip_quantize_w4(be_.context(), fptr(*dw), (int)E,
+                                        (int)out, codes, scales)
+                    : nnhip_quantize_w8(be_.context(), fptr(*dw), (int)E,
+                                        (int)out, codes, scales));
+    be_.synchronize();
+  };
+  quant(master_[0], E, cptr(*cqkv_), fptr(*sqkv_));
+  quant(master_[2], Ekv, cptr(*cqkv_) + E * E, fptr(*sqkv_) + E);
+  quant(master_[4], Ekv, cptr(*cqkv_) + (E + Ekv) * E, fptr(*sqkv_) + E + Ekv);
+  quant(master_[6], E, cptr(*co_), fptr(*so_));
+  quantized_ = true;
+}
+
+void HipMultiHeadAttention::forward_device(const float *x, size_t B, size_t S,
+                                           float *y, HipMhaCache *cache) {
+  if (B == 0 || S == 0) return;
+  const size_t E = cfg_.embed_dim, Ekv = Hkv_ * D_, Nqkv = E + 2 * Ekv;
+  const size_t rows = B * S;
+  nnhip_ctx *ctx = be_.context();
+  // the past: the cache's length for every sequence, or none
+  std::unique_ptr<DeviceBuffer> tk, tv;
+  float *kc = nullptr, *vc = nullptr;
+  size_t cap = 0, past = 0;
+  if (cache) {
+    if (cache->B_ != B)
+      throw std::runtime_error("HipMultiHeadAttention: cache batch differs from B");
+    if (cache->len_ + S > cache->cap_)
+      throw std::runtime_error(
+          "HipMhaCache: cached length plus S exceeds its capacity");
+    kc = fptr(*cache->k_);
+    vc = fptr(*cache->v_);
+    cap = cache->cap_;
+    past = cache->len_;
+  } else {
+    tk = be_.allocate(B * Hkv_ * S * D_ * sizeof(float));
+    tv = be_.allocate(B * Hkv_ * S * D_ * sizeof(float));
+    kc = fptr(*tk);
+    vc = fptr(*tv);
+    cap = S;
+  }
+  std::unique_ptr<DeviceBuffer> qkv = be_.allocate(rows * Nqkv * sizeof(float));
+  std::unique_ptr<DeviceBuffer> qrot = be_.allocate(rows * E * sizeof(float));
+  std::unique_ptr<DeviceBuffer> ctxo = be_.allocate(rows * E * sizeof(float));
+  std::unique_ptr<DeviceBuffer> pos = be_.allocate(B * sizeof(int32_t));
+  const std::vector<int32_t> hpos(B, (int32_t)past);
+  check(nnhip_h2d(ctx, pos->data(), hpos.data(), B * sizeof(int32_t)));
+  const int32_t *dpos = static_cast<const int32_t *>(pos->data());
+  // q | k | v rows, RoPE at the cache length and the append, attention
+  if (quantized_)
+    check(nnhip_linear_w8a32(ctx, x, (int)rows, (int)E, cptr(*cqkv_),
+                             fptr(*sqkv_), fptr(*bqkv_), (int)Nqkv,
+                             fptr(*qkv), 0));
+  else
+    check(nnhip_linear_f32(ctx, x, (int)rows, (int)E, fptr(*wqkv_),
+                           fptr(*bqkv_), (int)Nqkv, fptr(*qkv)));
+  check(nnhip_rope_kv_append_gqa(ctx, fptr(*qkv), (int)B, (int)S, (int)H_,
+                                 (int)Hkv_, (int)D_, dpos, fptr(*qrot), kc, vc,
+                                 (int)cap));
+  check(nnhip_attention_kq(ctx, fptr(*qrot), kc, vc, (int)cap, dpos, (int)B,
+                           (int)S, (int)H_, (int)Hkv_, (int)D_, fptr(*ctxo)));
+  if (quantized_)
+    check(nnhip_linear_w8a32(ctx, fptr(*ctxo), (int)rows, (int)E, cptr(*co_),
+                             fptr(*so_), fptr(*bo_), (int)E, y, 0));
+  else
+    check(nnhip_linear_f32(ctx, fptr(*ctxo), (int)rows, (int)E, fptr(*wo_),
+                           fptr(*bo_), (int)E, y));
+  be_.synchronize();  // the scratch above is freed on return
+  if (cache) cache->len_ += S;
+}
+
+HipMhaCache::HipMhaCache(HipMultiHeadAttention &layer, size_t batch)
+    : B_(batch), cap_(layer.cfg_.max_seq_len) {
+  if (batch == 0 || cap_ == 0)
+    throw std::runtime_error("HipMhaCache: empty batch or capacity");
+  const size_t n = B_ * layer.Hkv_ * cap_ * layer.D_;
+  k_ = layer.be_.allocate(n * sizeof(float));
+  v_ = layer.be_.allocate(n * sizeof(float));
+  layer.be_.fill(*k_, 0.0f);
+  layer.be_.fill(*v_, 0.0f);
+}
+
+void HipMhaCache::truncate(size_t len) { len_ = std::min(len, len_); }
 
 }  // namespace nnhip_backend

@@ -21,6 +21,36 @@ HipDecoder::HipDecoder(HipBackend &backend, TransformerDecoder &d,
                        const DecoderConfig &cfg)
     : HipDecoder(backend, cfg, host_params(d)) {}
 
+static std::vector<std::vector<float>> host_params(MultiHeadAttention &m) {
+  std::vector<std::vector<float>> r;
+  for (const auto &p : m.parameters()) r.push_back(p->to_host());
+  return r;
+}
+
+HipMultiHeadAttention::HipMultiHeadAttention(HipBackend &backend,
+                                             MultiHeadAttention &layer,
+                                             const MhaConfig &cfg)
+    : HipMultiHeadAttention(backend, cfg, host_params(layer)) {}
+
+std::shared_ptr<Tensor> HipMultiHeadAttention::forward(
+    const std::shared_ptr<Tensor> &input, HipMhaCache *cache) {
+  const Shape &s = input->shape();
+  // the reference's check (layer.cpp:596-599)
+  if (s.size() != 3)
+    throw std::runtime_error("MultiHeadAttention input must be of shape (B, S, E)");
+  if (input->backend() != &be_ || s[2] != cfg_.embed_dim ||
+      !is_contiguous(s, input->strides()))
+    throw std::runtime_error(
+        "HipMultiHeadAttention: input must be a contiguous HipBackend tensor "
+        "whose last dimension is embed_dim");
+  std::shared_ptr<DeviceBuffer> y(be_.allocate(count_elements(s) * sizeof(float)));
+  const float *x =
+      static_cast<const float *>(input->storage()->data()) + input->offset();
+  forward_device(x, s[0], s[1], static_cast<float *>(y->data()), cache);
+  return std::make_shared<Tensor>(s, compute_strides(s), 0, y, &be_,
+                                  DataType::FP32);
+}
+
 HipQuantizedDense::HipQuantizedDense(HipBackend &backend,
                                      const QuantizedDense &layer)
     : be_(backend) {

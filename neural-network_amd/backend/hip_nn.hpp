@@ -14,6 +14,8 @@
 //     every Dense of the decoder
 //   QuantizedDense::forward (quantization.cpp:   HipQuantizedDense::forward
 //     127-147)
+//   MultiHeadAttention::forward(x, KVCache *)    HipMultiHeadAttention::forward
+//     (layer.cpp:593-994)                        (x, HipMhaCache *)
 //   generate_advanced (layer.hpp:310-316)        HipDecoder::generate_advanced
 //   generate_speculative (layer.hpp:318-323)     HipDecoder::generate_speculative
 //
@@ -94,6 +96,76 @@ class HipKVCache {
 
  private:
   nnhip_kvcache *c_ = nullptr;
+};
+
+// MultiHeadAttention's constructor arguments (layer.hpp:234-236)
+struct MhaConfig {
+  size_t embed_dim, num_heads;
+  size_t num_kv_heads = 0;   // 0: num_heads (layer.cpp:475)
+  bool causal = true;        // the device attention is causal (the decoder's)
+  size_t max_seq_len = 1024; // capacity of a HipMhaCache
+};
+
+class HipMhaCache;
+
+// MultiHeadAttention (layer.hpp:232-258, layer.cpp:471-994) on the device:
+// q / k / v projections as one fused Linear (fp32, or INT8 / INT4 codes
+// after quantize), RoPE at the cache's length and the KV append
+// (nnhip_rope_kv_append_gqa), the fused causal attention with grouped
+// query heads (nnhip_attention_kq), the output projection.
+class HipMultiHeadAttention {
+ public:
+  // parameters in MultiHeadAttention::parameters() order (layer.cpp:491-502):
+  // q, k, v, out projections, each weight [in][out] then bias [out]
+  HipMultiHeadAttention(HipBackend &backend, const MhaConfig &cfg,
+                        const std::vector<std::vector<float>> &params);
+  // the same from a reference layer (its parameters() copied to the host)
+  HipMultiHeadAttention(HipBackend &backend, MultiHeadAttention &layer,
+                        const MhaConfig &cfg);
+  ~HipMultiHeadAttention();
+  HipMultiHeadAttention(const HipMultiHeadAttention &) = delete;
+  HipMultiHeadAttention &operator=(const HipMultiHeadAttention &) = delete;
+
+  // MultiHeadAttention::quantize (layer.cpp:545-558): every projection to
+  // symmetric per-output-channel codes, INT8 or INT4
+  void quantize(const QuantizationConfig &config = QuantizationConfig{});
+  // forward(x, cache) on device rows: x [B*S][E] -> y [B*S][E] (E =
+  // embed_dim), B sequences of S new positions; cache may be null (no
+  // past), else holds B sequences and grows by S
+  void forward_device(const float *x, size_t B, size_t S, float *y,
+                      HipMhaCache *cache);
+  // forward(input [B, S, E], cache) on HipBackend tensors
+  std::shared_ptr<Tensor> forward(const std::shared_ptr<Tensor> &input,
+                                  HipMhaCache *cache = nullptr);
+  [[nodiscard]] const MhaConfig &config() const noexcept { return cfg_; }
+  [[nodiscard]] size_t head_dim() const noexcept { return D_; }
+  [[nodiscard]] size_t kv_heads() const noexcept { return Hkv_; }
+
+ private:
+  friend class HipMhaCache;
+  HipBackend &be_;
+  MhaConfig cfg_;
+  size_t H_ = 0, Hkv_ = 0, D_ = 0;
+  bool quantized_ = false;
+  // fused q | k | v: fp32 [Nqkv][E] or codes, scales, bias [Nqkv]; out: [E][E]
+  std::unique_ptr<DeviceBuffer> wqkv_, wo_, cqkv_, co_, sqkv_, so_, bqkv_, bo_;
+  std::vector<std::vector<float>> master_;  // parameters() as given
+};
+
+// KVCache for B sequences of one HipMultiHeadAttention: fp32 K / V
+// [B][Hkv][max_seq_len][D] on the device, one length for all sequences as
+// the reference's cache has (layer.hpp:212-230).
+class HipMhaCache {
+ public:
+  HipMhaCache(HipMultiHeadAttention &layer, size_t batch);
+  void truncate(size_t len);  // KVCache::truncate (layer.cpp:67-149)
+  [[nodiscard]] size_t length() const noexcept { return len_; }
+  [[nodiscard]] size_t batch() const noexcept { return B_; }
+
+ private:
+  friend class HipMultiHeadAttention;
+  size_t B_ = 0, cap_ = 0, len_ = 0;
+  std::unique_ptr<DeviceBuffer> k_, v_;
 };
 
 // QuantizedDense (INT8 or INT4) with its codes and scales resident on the

@@ -580,6 +580,26 @@ int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
   });
 }
 
+int nnhip_rope_kv_append_gqa(nnhip_ctx *ctx, const float *qkv, int B, int S,
+                             int H, int Hkv, int D, const int32_t *pos,
+                             float *q_out, float *kcache, float *vcache,
+                             int cap) {
+  return guard([&] {
+    REQ(ctx && qkv && pos && q_out && kcache && vcache && B > 0 && S > 0 &&
+            H > 0 && Hkv > 0 && H % Hkv == 0 && D > 0 && D % 2 == 0 && cap > 0,
+        "nnhip_rope_kv_append_gqa: bad argument");
+    hipStream_t st = ctx->c.stream;
+    std::vector<float> hc, hs;
+    rope_tables(cap, D, hc, hs);
+    auto dc = upload(st, hc.data(), hc.size());
+    auto ds = upload(st, hs.data(), hs.size());
+    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
+                          q_out, kcache, vcache, cap, (int64_t)Hkv * cap * D,
+                          Hkv);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+  });
+}
+
 int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
                        const float *vcache, int cap, const int32_t *pos0,
                        int B, int S, int H, int Hkv, int D, float *out) {

@@ -126,7 +126,7 @@ __global__ void build_verify_ids_kernel(const int32_t *__restrict__ cur,
 // append rotated k and v to the cache.  qkv row t = b*S + s holds
 // [q(H*D) | k(H*D) | v(H*D)].
 __global__ __launch_bounds__(256) void rope_kv_kernel(
-    const float *__restrict__ qkv, int S, int H, int D,
+    const float *__restrict__ qkv, int S, int H, int Hkv, int D,
     const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, const float *__restrict__ cosb,
     const float *__restrict__ sinb, float *__restrict__ qrot,
@@ -138,23 +138,30 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(
   if (active && !active[b]) return;
   const int pos = base[b] + off + s;
   if (pos < 0 || pos >= cap) return;
-  const int E = H * D, half = D / 2;
-  const float *row = qkv + (int64_t)t * 3 * E;
+  // row t: [q: H heads | k: Hkv heads | v: Hkv heads] of D
+  const int E = H * D, Ekv = Hkv * D, half = D / 2;
+  const float *row = qkv + (int64_t)t * (E + 2 * Ekv);
   for (int i = threadIdx.x; i < H * half; i += blockDim.x) {
     const int h = i / half, j = i % half;
     const float c = cosb[(int64_t)pos * half + j];
     const float sn = sinb[(int64_t)pos * half + j];
     const int e = h * D + 2 * j;
-    float xe = row[e], xo = row[e + 1];
+    const float xe = row[e], xo = row[e + 1];
     qrot[(int64_t)t * E + e] = xe * c - xo * sn;
     qrot[(int64_t)t * E + e + 1] = xe * sn + xo * c;
-    xe = row[E + e]; xo = row[E + e + 1];
+  }
+  for (int i = threadIdx.x; i < Hkv * half; i += blockDim.x) {
+    const int h = i / half, j = i % half;
+    const float c = cosb[(int64_t)pos * half + j];
+    const float sn = sinb[(int64_t)pos * half + j];
+    const int e = h * D + 2 * j;
+    const float xe = row[E + e], xo = row[E + e + 1];
     float *kd = kc + b * seq_stride + ((int64_t)h * cap + pos) * D + 2 * j;
     kd[0] = xe * c - xo * sn;
     kd[1] = xe * sn + xo * c;
     float *vd = vc + b * seq_stride + ((int64_t)h * cap + pos) * D + 2 * j;
-    vd[0] = row[2 * E + e];
-    vd[1] = row[2 * E + e + 1];
+    vd[0] = row[E + Ekv + e];
+    vd[1] = row[E + Ekv + e + 1];
   }
 }
 
@@ -795,9 +802,13 @@ void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
 void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
                     int D, const int32_t *base, int off, const int32_t *active,
                     const float *cosb, const float *sinb, float *qrot,
-                    float *kc, float *vc, int cap, int64_t seq_stride) {
+                    float *kc, float *vc, int cap, int64_t seq_stride,
+                    int Hkv) {
+  if (Hkv <= 0) Hkv = H;
+  NNHIP_REQUIRE(H % Hkv == 0 && D % 2 == 0, kErrArg,
+                "rope_kv: H must be a multiple of Hkv, D even");
   hipLaunchKernelGGL(rope_kv_kernel, dim3(B * S), dim3(256), 0, st, qkv, S, H,
-                     D, base, off, active, cosb, sinb, qrot, kc, vc, cap,
+                     Hkv, D, base, off, active, cosb, sinb, qrot, kc, vc, cap,
                      seq_stride);
   NNHIP_CHECK(hipGetLastError());
 }

@@ -403,10 +403,13 @@ void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
                           int *rexp = nullptr);
 void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
                              const int32_t *cand, int B, int k, int32_t *ids);
+// qkv rows [q: H heads | k: Hkv heads | v: Hkv heads] (Hkv 0: H); the
+// cache holds Hkv heads per sequence
 void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
                     int D, const int32_t *base, int off, const int32_t *active,
                     const float *cosb, const float *sinb, float *qrot,
-                    float *kc, float *vc, int cap, int64_t seq_stride);
+                    float *kc, float *vc, int cap, int64_t seq_stride,
+                    int Hkv = 0);
 // RoPE on q and k, then the append into an int8 cache: each new k / v row
 // (one head, one position) is quantised as quantize_kv does
 // (layer.cpp:635-657); codes [B][H][cap][D] (seq_stride codes per

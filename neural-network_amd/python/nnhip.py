@@ -116,6 +116,8 @@ SIGNATURES = {
     "nnhip_linear_limb_totals": [_vp, _vp, _i, _i, _vp, _i, _vp, _vp, _vp],
     "nnhip_rope_kv_append": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,
                              _i],
+    "nnhip_rope_kv_append_gqa": [_vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp,
+                                 _vp, _i],
     "nnhip_attention_kq": [_vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i,
                            _vp],
     "nnhip_rope_kv_append_q8": [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp,

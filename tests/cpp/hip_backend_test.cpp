@@ -8,7 +8,8 @@
 // (tests/core/tensor_test.cpp, tests/nn/layer_test.cpp), the oracle
 // (or_dense, or_layernorm) and closed forms; then the decoder objects
 // HipDecoder / HipKVCache (backend/hip_nn.hpp) against the oracle's forward
-// and speculative decoding.  Needs a GPU; prints one line a check and exits
+// and speculative decoding, and HipMultiHeadAttention / HipMhaCache against
+// MultiHeadAttention::forward restated with the oracle's pieces.  Needs a GPU; prints one line a check and exits
 // non-zero on the first failure.
 #include "backend/hip_backend.hpp"  // neural-network_amd/backend
 #include "backend/hip_nn.hpp"
@@ -39,6 +40,12 @@ int or_model_set_param(or_model *m, int idx, const float *data);
 int or_model_quantize_bits(or_model *m, int bits);
 int or_forward(const or_model *m, or_cache *cache, const int32_t *ids, int S,
                float *logits);
+void or_rope(float *x, int64_t heads, int64_t S, int64_t D, int64_t s_past);
+void or_attention(const float *q, const float *k, const float *v, int64_t H,
+                  int64_t H_kv, int64_t S, int64_t S_total, int64_t D,
+                  int causal, float *out);
+void or_quantize_w(const float *w, int64_t in, int64_t out, int bits,
+                   int8_t *codes, float *scales);
 int or_generate_speculative(const or_model *target, const or_model *draft,
                             const int32_t *prompt, int P, int max_new,
                             int lookahead, float temperature, int top_k,
@@ -400,6 +407,157 @@ void test_decoder_adapter(HipBackend &hip) {
   std::printf("ok HipDecoder / HipKVCache vs oracle\n");
 }
 
+// MultiHeadAttention::forward(x, cache) of one sequence restated with the
+// oracle's pieces (layer.cpp:593-994): q / k / v Dense, RoPE at the cache
+// length, append, fused causal attention with grouped heads, out Dense.
+struct OracleMha {
+  size_t E = 0, H = 0, Hkv = 0, D = 0;
+  std::vector<std::vector<float>> p;  // parameters() order
+  int bits = 0;                       // 0: fp32 weights
+  std::vector<std::vector<int8_t>> codes;
+  std::vector<std::vector<float>> scales;
+  std::vector<float> k, v;  // [Hkv][len][D]
+  size_t len = 0;
+  void quantize(int b) {
+    bits = b;
+    codes.clear(); scales.clear();
+    for (int i : {0, 2, 4, 6}) {
+      const size_t out = p[i].size() / E;
+      codes.emplace_back(p[i].size());
+      scales.emplace_back(out);
+      or_quantize_w(p[i].data(), (int64_t)E, (int64_t)out, b,
+                    codes.back().data(), scales.back().data());
+    }
+  }
+  std::vector<float> dense(const std::vector<float> &x, size_t rows, int which) {
+    const size_t out = p[2 * which].size() / E;
+    std::vector<float> y(rows * out);
+    if (bits)
+      or_dense(x.data(), (int64_t)rows, (int64_t)E, (int64_t)out, nullptr,
+               codes[which].data(), scales[which].data(), p[2 * which + 1].data(),
+               y.data());
+    else
+      or_dense(x.data(), (int64_t)rows, (int64_t)E, (int64_t)out,
+               p[2 * which].data(), nullptr, nullptr, p[2 * which + 1].data(),
+               y.data());
+    return y;
+  }
+  // rows [S][E] of one sequence -> [S][E]
+  std::vector<float> forward(const std::vector<float> &x, size_t S) {
+    const std::vector<float> q = dense(x, S, 0), kn = dense(x, S, 1), vn = dense(x, S, 2);
+    std::vector<float> qh(H * S * D), kh(Hkv * S * D), vh(Hkv * S * D);
+    for (size_t s = 0; s < S; ++s)
+      for (size_t h = 0; h < H; ++h)
+        for (size_t d = 0; d < D; ++d) qh[(h * S + s) * D + d] = q[s * H * D + h * D + d];
+    for (size_t s = 0; s < S; ++s)
+      for (size_t h = 0; h < Hkv; ++h)
+        for (size_t d = 0; d < D; ++d) {
+          kh[(h * S + s) * D + d] = kn[s * Hkv * D + h * D + d];
+          vh[(h * S + s) * D + d] = vn[s * Hkv * D + h * D + d];
+        }
+    or_rope(qh.data(), (int64_t)H, (int64_t)S, (int64_t)D, (int64_t)len);
+    or_rope(kh.data(), (int64_t)Hkv, (int64_t)S, (int64_t)D, (int64_t)len);
+    const size_t tot = len + S;
+    std::vector<float> nk(Hkv * tot * D), nv(Hkv * tot * D);
+    for (size_t h = 0; h < Hkv; ++h) {
+      for (size_t j = 0; j < len; ++j)
+        for (size_t d = 0; d < D; ++d) {
+          nk[(h * tot + j) * D + d] = k[(h * len + j) * D + d];
+          nv[(h * tot + j) * D + d] = v[(h * len + j) * D + d];
+        }
+      for (size_t s = 0; s < S; ++s)
+        for (size_t d = 0; d < D; ++d) {
+          nk[(h * tot + len + s) * D + d] = kh[(h * S + s) * D + d];
+          nv[(h * tot + len + s) * D + d] = vh[(h * S + s) * D + d];
+        }
+    }
+    k.swap(nk); v.swap(nv); len = tot;
+    std::vector<float> att(S * H * D);
+    or_attention(qh.data(), k.data(), v.data(), (int64_t)H, (int64_t)Hkv,
+                 (int64_t)S, (int64_t)len, (int64_t)D, 1, att.data());
+    return dense(att, S, 3);
+  }
+};
+
+// HipMultiHeadAttention / HipMhaCache against the oracle: grouped query
+// heads (H 4, H_kv 2), two sequences, a 5-token then a 3-token forward
+// through the cache, no-cache forward, truncate and recompute; fp32, INT8
+// and INT4 projections.
+void test_mha_adapter(HipBackend &hip) {
+  using nnhip_backend::HipMhaCache;
+  using nnhip_backend::HipMultiHeadAttention;
+  const size_t E = 64, H = 4, Hkv = 2, D = 16, B = 2;
+  nnhip_backend::MhaConfig cfg;
+  cfg.embed_dim = E; cfg.num_heads = H; cfg.num_kv_heads = Hkv; cfg.max_seq_len = 32;
+  const size_t Ekv = Hkv * D;
+  const size_t sizes[8] = {E * E, E, E * Ekv, Ekv, E * Ekv, Ekv, E * E, E};
+  std::vector<std::vector<float>> params;
+  for (int i = 0; i < 8; ++i) params.push_back(randn(sizes[i], 500 + (unsigned)i, 0.1f));
+  const std::vector<float> x1 = randn(B * 5 * E, 601), x2 = randn(B * 3 * E, 602);
+  auto dev = [&](const std::vector<float> &h) {
+    std::unique_ptr<DeviceBuffer> d = hip.allocate(std::max<size_t>(h.size(), 1) * sizeof(float));
+    if (!h.empty()) hip.copy_host_to_device(h.data(), *d, h.size() * sizeof(float));
+    return d;
+  };
+  auto get = [&](DeviceBuffer &d, size_t n) {
+    std::vector<float> h(n);
+    hip.copy_device_to_host(d, h.data(), n * sizeof(float));
+    return h;
+  };
+  for (int bits : {0, 8, 4}) {
+    HipMultiHeadAttention mha(hip, cfg, params);
+    if (bits) {
+      QuantizationConfig qc;
+      qc.type = bits == 4 ? QuantizationType::INT4 : QuantizationType::INT8;
+      mha.quantize(qc);
+    }
+    const std::string tag = bits ? "INT" + std::to_string(bits) : std::string("fp32");
+    HipMhaCache cache(mha, B);
+    auto dx1 = dev(x1), dx2 = dev(x2), dy1 = dev(std::vector<float>(B * 5 * E)),
+         dy2 = dev(std::vector<float>(B * 3 * E)), dy0 = dev(std::vector<float>(B * 5 * E));
+    mha.forward_device(static_cast<float *>(dx1->data()), B, 5,
+                       static_cast<float *>(dy1->data()), &cache);
+    mha.forward_device(static_cast<float *>(dx2->data()), B, 3,
+                       static_cast<float *>(dy2->data()), &cache);
+    mha.forward_device(static_cast<float *>(dx1->data()), B, 5,
+                       static_cast<float *>(dy0->data()), nullptr);
+    const std::vector<float> y1 = get(*dy1, B * 5 * E), y2 = get(*dy2, B * 3 * E),
+                             y0 = get(*dy0, B * 5 * E);
+    expect(cache.length() == 8, "HipMhaCache length after 5 + 3 (" + tag + ")");
+    for (size_t b = 0; b < B; ++b) {
+      OracleMha o;
+      o.E = E; o.H = H; o.Hkv = Hkv; o.D = D; o.p = params;
+      if (bits) o.quantize(bits);
+      const std::vector<float> a1(x1.begin() + (long)(b * 5 * E), x1.begin() + (long)((b + 1) * 5 * E));
+      const std::vector<float> a2(x2.begin() + (long)(b * 3 * E), x2.begin() + (long)((b + 1) * 3 * E));
+      const std::vector<float> w1 = o.forward(a1, 5), w2 = o.forward(a2, 3);
+      const std::vector<float> g1(y1.begin() + (long)(b * 5 * E), y1.begin() + (long)((b + 1) * 5 * E));
+      const std::vector<float> g2(y2.begin() + (long)(b * 3 * E), y2.begin() + (long)((b + 1) * 3 * E));
+      const std::vector<float> g0(y0.begin() + (long)(b * 5 * E), y0.begin() + (long)((b + 1) * 5 * E));
+      expect(row_rel_err(g1, w1, 5, E) < 1e-4, "MHA forward (5 new) vs oracle, " + tag);
+      expect(row_rel_err(g2, w2, 3, E) < 1e-4, "MHA forward through the cache (3 new) vs oracle, " + tag);
+      expect(row_rel_err(g0, w1, 5, E) < 1e-4, "MHA forward without a cache vs oracle, " + tag);
+    }
+    // truncate back to 5 and run the 3 tokens again: the same outputs
+    cache.truncate(5);
+    expect(cache.length() == 5, "HipMhaCache::truncate (" + tag + ")");
+    auto dy3 = dev(std::vector<float>(B * 3 * E));
+    mha.forward_device(static_cast<float *>(dx2->data()), B, 3,
+                       static_cast<float *>(dy3->data()), &cache);
+    expect(get(*dy3, B * 3 * E) == y2, "MHA recompute after truncate is bit-identical, " + tag);
+  }
+  bool threw = false;
+  try {
+    nnhip_backend::MhaConfig bad = cfg;
+    bad.num_kv_heads = 3;
+    HipMultiHeadAttention m(hip, bad, params);
+  } catch (const std::runtime_error &) {
+    threw = true;
+  }
+  expect(threw, "num_heads must be divisible by num_kv_heads");
+  std::printf("ok HipMultiHeadAttention / HipMhaCache vs oracle\n");
+}
+
 }  // namespace
 
 int main() {
@@ -412,6 +570,7 @@ int main() {
     test_softmax_and_embedding(be);
     test_fill_and_unsupported(be);
     test_decoder_adapter(hip);
+    test_mha_adapter(hip);
   } catch (const std::exception &e) {
     std::printf("FAIL exception: %s\n", e.what());
     return 1;

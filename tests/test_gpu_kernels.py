@@ -255,6 +255,46 @@ def test_rope_kv_append(ctx):
         np.testing.assert_array_equal(vg[b, :, pos[b]:pos[b] + S], v)
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(8, 2, 32), (4, 4, 64), (6, 3, 16)])
+def test_rope_kv_append_gqa(ctx, H, Hkv, D):
+    """RoPE on q (H heads) and k (Hkv heads), v copied, into a cache of Hkv
+    heads (MultiHeadAttention with num_kv_heads, layer.cpp:471-489, 593-807):
+    bit-exact against or_rope; Hkv == H equals nnhip_rope_kv_append."""
+    rng = np.random.default_rng(13 + H + Hkv)
+    B, S, cap = 2, 4, 300
+    pos = np.array([3, 250], np.int32)
+    E, Ekv = H * D, Hkv * D
+    qkv = rng.standard_normal((B * S, E + 2 * Ekv)).astype(np.float32)
+    dq, dpos = ctx.array(qkv), ctx.array(pos)
+    qo = ctx.array(shape=(B * S, E))
+    kc = ctx.array(np.zeros((B, Hkv, cap, D), np.float32))
+    vc = ctx.array(np.zeros((B, Hkv, cap, D), np.float32))
+    call("nnhip_rope_kv_append_gqa", ctx.h, dq.p, B, S, H, Hkv, D, dpos.p,
+         qo.p, kc.p, vc.p, cap)
+    qg, kg, vg = qo.numpy(), kc.numpy(), vc.numpy()
+    for b in range(B):
+        rows = qkv[b * S:(b + 1) * S]
+        q = np.ascontiguousarray(rows[:, :E].reshape(S, H, D).transpose(1, 0, 2))
+        O.lib().or_rope(O.fptr(q), H, S, D, int(pos[b]))
+        np.testing.assert_array_equal(
+            qg[b * S:(b + 1) * S].reshape(S, H, D).transpose(1, 0, 2), q)
+        k = np.ascontiguousarray(
+            rows[:, E:E + Ekv].reshape(S, Hkv, D).transpose(1, 0, 2))
+        O.lib().or_rope(O.fptr(k), Hkv, S, D, int(pos[b]))
+        np.testing.assert_array_equal(kg[b, :, pos[b]:pos[b] + S], k)
+        v = rows[:, E + Ekv:].reshape(S, Hkv, D).transpose(1, 0, 2)
+        np.testing.assert_array_equal(vg[b, :, pos[b]:pos[b] + S], v)
+    if H == Hkv:
+        q2 = ctx.array(shape=(B * S, E))
+        k2 = ctx.array(np.zeros((B, H, cap, D), np.float32))
+        v2 = ctx.array(np.zeros((B, H, cap, D), np.float32))
+        call("nnhip_rope_kv_append", ctx.h, dq.p, B, S, H, D, dpos.p, q2.p,
+             k2.p, v2.p, cap)
+        np.testing.assert_array_equal(q2.numpy(), qg)
+        np.testing.assert_array_equal(k2.numpy(), kg)
+        np.testing.assert_array_equal(v2.numpy(), vg)
+
+
 ATTN_CASES = [(3, 1, 4, 64, [0, 37, 300]), (2, 6, 4, 64, [5, 380]),
               (2, 8, 2, 32, [0, 900]), (2, 13, 2, 64, [0, 20]),
               (16, 8, 8, 64, [2048] * 16)]
