@@ -172,13 +172,35 @@ class HipMhaCache {
 // device; forward runs on tensors whose storage belongs to `backend`.
 class HipQuantizedDense {
  public:
+  // the codes and scales of a reference QuantizedDense
   HipQuantizedDense(HipBackend &backend, const QuantizedDense &layer);
+  // QuantizedDense(float_dense, config) (quantization.cpp:7-86): the Dense's
+  // weight quantised on the device (nnhip_quantize_w8 / _w4), the same codes
+  // and scales bit for bit
+  HipQuantizedDense(HipBackend &backend, std::shared_ptr<Dense> float_dense,
+                    const QuantizationConfig &config);
   // y [rows, out] = x [rows, in] . (codes * scales) + bias, x contiguous
   std::shared_ptr<Tensor> forward(const std::shared_ptr<Tensor> &input);
+  // the accessors of QuantizedDense (quantization.hpp:20-31)
+  [[nodiscard]] QuantizationType type() const noexcept { return type_; }
+  [[nodiscard]] const std::vector<uint8_t> &packed_weights() const noexcept {
+    return packed_;
+  }
+  [[nodiscard]] Shape weight_shape() const { return Shape{in_, out_}; }
+  std::shared_ptr<Tensor> scales() const;  // [out] on the HipBackend
+  std::shared_ptr<Tensor> bias() const;    // [1, out] on the HipBackend
+  // dequantize_weight (quantization.cpp:89-125): codes * scales, [in, out]
+  std::shared_ptr<Tensor> dequantize_weight() const;
 
  private:
+  void upload(const std::vector<int8_t> &codes_in_out,
+              const std::vector<float> &scales, const std::vector<float> &bias);
   HipBackend &be_;
+  QuantizationType type_ = QuantizationType::INT8;
   size_t in_ = 0, out_ = 0;
+  std::vector<uint8_t> packed_;                           // reference layout
+  std::vector<int8_t> host_codes_;                        // [in][out]
+  std::vector<float> host_scales_, host_bias_;
   std::unique_ptr<DeviceBuffer> codes_, scales_, bias_;  // codes [out][in]
 };
 
