@@ -93,6 +93,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
     int64_t ldy, int epi, int nks, int64_t row0, RopeArgs ra, GemvLn lf) {
+  // row group blockIdx.y: rows [R * blockIdx.y, R * blockIdx.y + R) of the
+  // launch
+  {
+    const int64_t g = (int64_t)blockIdx.y * R;
+    x += g * ldx;
+    if (resid) resid += g * ldr;
+    if (y) y += g * ldy;
+    if (lf.out) lf.out += g * lf.ldo;
+    row0 += g;
+  }
   constexpr int kMaxIt = 4;  // slice <= 1024 elements
   constexpr int P = kGemvNC * R;
   constexpr int NP = P <= 8 ? 8 : P <= 16 ? 16 : P <= 32 ? 32 : 64;
@@ -884,10 +894,10 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
                    const int8_t *wq, const float *wf, const float *scale,
                    const float *bias, const float *resid, int64_t ldr,
                    float *y, int64_t ldy, int epi, int64_t row0,
-                   const RopeArgs &ra, const GemvLn &lf) {
+                   const RopeArgs &ra, const GemvLn &lf, int groups = 1) {
   int nks = K >= 1024 ? 4 : (K >= 512 ? 2 : 1);
   int cols = (4 / nks) * kGemvNC;
-  dim3 grid((N + cols - 1) / cols);
+  dim3 grid((N + cols - 1) / cols, groups);
   if (wq)
     hipLaunchKernelGGL((gemv_kernel<R, true>), grid, dim3(256), 0, st, x, ldx,
                        K, N, wq, wf, scale, bias, resid, ldr, y, ldy, epi,
@@ -918,9 +928,14 @@ void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
   NNHIP_REQUIRE(!(ra && ra->kq), kErrArg,
                 "gemv: no int8 KV append in this epilogue (use rope_kv_q8)");
   const RopeArgs rz = ra ? *ra : RopeArgs{};
-  // up to 8 rows per pass, so that a verify step's k+1 rows (k <= 7) read
-  // the weights once
-  for (int r0 = 0; r0 < rows; r0 += 8) {
+  // 8 rows per workgroup, so that a verify step's k+1 rows (k <= 7) read
+  // the weights once: the whole groups of 8 rows in one launch (one row
+  // group per grid row), the remainder in a second
+  const int full = rows / 8;
+  if (full > 0)
+    gemv_dispatch<8>(st, x, ldx, K, N, wq, wf, scale, bias, resid, ldr, y,
+                     ldy, epi, 0, rz, lz, full);
+  for (int r0 = full * 8; r0 < rows; r0 += 8) {
     int rr = rows - r0 < 8 ? rows - r0 : 8;
     const float *xp = x + r0 * ldx;
     const float *rp = resid ? resid + r0 * ldr : nullptr;
