@@ -8,7 +8,8 @@
 
 namespace nnhip {
 
-int g_lds_min_rows = 64;
+int g_lds_min_rows = 128;
+int g_o_limb_rows = 256;
 
 namespace {
 
@@ -304,8 +305,8 @@ bool Model::use_limbs(const Linear &ln, int rows) const {
 
 // Where the LDS-resident GEMM is used (measured on the batch-32 decode
 // shapes): the lm head, and every projection with K <= 1024 on tall inputs
-// (>= 64 rows: the verify batch), where one digit tile per 32 rows serves
-// 128 columns.  Short inputs (the draft's 32 rows) run faster on the
+// (>= 128 rows: the verify batch), where one digit tile per 32 rows serves
+// 128 columns.  Short inputs (the draft's 32 and 64 rows) run faster on the
 // digit-plane GEMM.  A pending LayerNorm is folded into the GEMM prologue
 // only for the lm head of a short batch; elsewhere the prologue's repeated
 // per-column-block normalisation costs more than a LayerNorm launch.
@@ -463,15 +464,20 @@ void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
                 l == 0 && emb_digits, nullptr, 0, nullptr, 3 * d, kEpiRope, &ra);
     }
     // short contexts: the attention workgroups merge their key splits and
-    // write ctx; the output projection then digitises ctx itself.  Long
-    // ones: split attention + combine, which also writes ctx's digits.
+    // write ctx; up to g_o_limb_rows rows ctx is then digitised by act_quant
+    // for the digit-plane GEMM (two launches, measured faster than the LDS
+    // GEMM digitising ctx in its prologue), taller inputs (prefill) use the
+    // latter.  Long contexts: split attention + combine, which also writes
+    // ctx's digits.
     const bool merged = attention_merged(D, max_keys);
     const bool lo = !merged && (use_lds(ly.o, R) || use_limbs(ly.o, R));
     launch_attention(st, ws.qrot.p, kvs, B, S, H, H, D, kv->cap, bp, off,
                      active, max_keys, ws.part.p, ws.part_elems, ws.ctx.p,
                      lo ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
-    if (merged && ly.o.quant && ly.o.qs.p && R >= kLimbMinRows &&
-        gemm_lds_supports(R, d, d))
+    if (merged && R <= g_o_limb_rows && use_limbs(ly.o, R))
+      linear(ly.o, ws.ctx.p, d, R, false, ws.x.p, d, ws.h.p, d, kEpiResid);
+    else if (merged && ly.o.quant && ly.o.qs.p && R >= kLimbMinRows &&
+             gemm_lds_supports(R, d, d))
       launch_gemm_lds(st, kAFromRows, nullptr, 0, nullptr, ws.ctx.p, d,
                       nullptr, nullptr, nullptr, 0, R, d, d, ly.o.qs.p,
                       ly.o.s.p, ly.o.b.p, ws.x.p, d, ws.h.p, d, kEpiResid);

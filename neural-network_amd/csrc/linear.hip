@@ -253,20 +253,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 
 // Digits of activation rows for the MFMA GEMM: X = rint(x * 2^e) with
 // e = 22 - exponent(max|x|) per row, split into balanced base-256 digits
-// (hi, mid, lo), written in the MFMA operand layout.  One wave per row held
-// in quads (rows.hpp: lane l has entries 256 i + 4 l .. + 3, i < NQ) in
-// registers, so the row is read once, every load is a contiguous 1 KB per
-// wave, and the max needs no workgroup barrier.
-template <int NQ>
+// (hi, mid, lo), written in the MFMA operand layout.  WPR waves per row, each
+// holding a slice of K / WPR entries in quads (rows.hpp: lane l has entries
+// 256 i + 4 l .. + 3 of the slice, i < NQ) in registers, so the row is read
+// once and every load is a contiguous 1 KB per wave; the slices' maxima are
+// combined through LDS (max is exact, so the exponent does not depend on WPR).
+template <int NQ, int WPR>
 __global__ __launch_bounds__(256) void act_quant_kernel(
     const float *__restrict__ x, int64_t ldx, int K, int rows,
     int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (m >= rows) return;
+  __shared__ float s_mx[4];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m = blockIdx.x * (4 / WPR) + wv / WPR;
+  const int span = K / WPR, s0 = (wv % WPR) * span;
   float v[NQ][4];
-  load_quads<NQ>(x + m * ldx, K, lane, v);
-  aq_row_finish<NQ>(v, K, m, limbs, mpad, rexp, lane);
+  load_quads<NQ>(x + (int64_t)min(m, rows - 1) * ldx + s0, span, lane, v);
+  float mx = wave_max_all(quads_absmax<NQ>(v, span, lane));
+  if constexpr (WPR > 1) {
+    if (lane == 0) s_mx[wv] = mx;
+    __syncthreads();
+    const int w0 = wv - wv % WPR;
+#pragma unroll
+    for (int j = 0; j < WPR; ++j) mx = fmaxf(mx, s_mx[w0 + j]);
+  }
+  if (m >= rows) return;
+  const int e = digit_exponent(mx);
+  if (lane == 0 && s0 == 0) rexp[m] = e;
+  aq_store_digits<NQ>(v, s0, span, K, m, e, limbs, mpad, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -965,16 +978,16 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   NNHIP_REQUIRE(K % 128 == 0 && ldx % 4 == 0 && rows <= mpad, kErrArg,
                 "act_quant: K % 128 and ldx % 4 must be 0");
   NNHIP_REQUIRE(K <= 4096, kErrArg, "act_quant: K must be <= 4096");
-  const dim3 grid((rows + 3) / 4);
+  // one wave per 1024 entries of a row (at most 4 per row)
   if (K <= 1024)
-    hipLaunchKernelGGL(act_quant_kernel<4>, grid, dim3(256), 0, st, x, ldx, K,
-                       rows, limbs, mpad, rexp);
+    hipLaunchKernelGGL((act_quant_kernel<4, 1>), dim3((rows + 3) / 4), dim3(256),
+                       0, st, x, ldx, K, rows, limbs, mpad, rexp);
   else if (K <= 2048)
-    hipLaunchKernelGGL(act_quant_kernel<8>, grid, dim3(256), 0, st, x, ldx, K,
-                       rows, limbs, mpad, rexp);
+    hipLaunchKernelGGL((act_quant_kernel<4, 2>), dim3((rows + 1) / 2), dim3(256),
+                       0, st, x, ldx, K, rows, limbs, mpad, rexp);
   else
-    hipLaunchKernelGGL(act_quant_kernel<16>, grid, dim3(256), 0, st, x, ldx, K,
-                       rows, limbs, mpad, rexp);
+    hipLaunchKernelGGL((act_quant_kernel<4, 4>), dim3(rows), dim3(256), 0, st,
+                       x, ldx, K, rows, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
 }
 

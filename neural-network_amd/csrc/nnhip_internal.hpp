@@ -284,6 +284,8 @@ constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
+extern int g_o_limb_rows; // output projection after merged attention: digit
+                          // planes + digit-plane GEMM up to this many rows
 extern int g_kv_stream;  // attention: non-temporal fp32 KV loads (0 never,
                          // 1 when a launch reads more than the L2s hold, 2 always)
 // workgroups of one LDS-GEMM launch (32-row tiles x column blocks of

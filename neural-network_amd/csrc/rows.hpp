@@ -77,30 +77,36 @@ __device__ __forceinline__ void ln_row_finish(
   }
 }
 
-// Digits of one row of K entries held by a wave in quads: X = rint(x * 2^e)
-// with e = 22 - exponent(max|x|), split into balanced base-256 digits
-// (hi, mid, lo) in the MFMA operand layout, and the row exponent.
+// max |x| over the valid quads of a row slice of span entries held by a wave
+// (this lane's part)
 template <int NQ>
-__device__ __forceinline__ void aq_row_finish(const float (&v)[NQ][4], int K,
-                                              int m, int8_t *__restrict__ limbs,
-                                              int mpad, int *__restrict__ rexp,
+__device__ __forceinline__ float quads_absmax(const float (&v)[NQ][4], int span,
                                               int lane) {
   float mx = 0.f;
 #pragma unroll
   for (int i = 0; i < NQ; ++i)
-    if (quad_ok(i, lane, K)) {
+    if (quad_ok(i, lane, span)) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) mx = fmaxf(mx, fabsf(v[i][j]));
     }
-  mx = wave_max_all(mx);
-  const int e = digit_exponent(mx);
-  if (lane == 0) rexp[m] = e;
+  return mx;
+}
+
+// Digits of the quads of row m's entries [s0, s0 + span) (of K) held by a
+// wave, with the row exponent e = 22 - exponent(max|x|) over the whole row:
+// X = rint(x * 2^e) split into balanced base-256 digits (hi, mid, lo) in the
+// MFMA operand layout.
+template <int NQ>
+__device__ __forceinline__ void aq_store_digits(const float (&v)[NQ][4], int s0,
+                                                int span, int K, int m, int e,
+                                                int8_t *__restrict__ limbs,
+                                                int mpad, int lane) {
   const int64_t plane = (int64_t)mpad * K;
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
-    if (!quad_ok(i, lane, K)) break;
+    if (!quad_ok(i, lane, span)) break;
     const int3 t = digits4(v[i], e);
-    const int64_t off = mfma_operand_offset(m, 256 * i + 4 * lane, K);
+    const int64_t off = mfma_operand_offset(m, s0 + 256 * i + 4 * lane, K);
     *reinterpret_cast<int *>(limbs + off) = t.x;
     *reinterpret_cast<int *>(limbs + plane + off) = t.y;
     *reinterpret_cast<int *>(limbs + 2 * plane + off) = t.z;
