@@ -78,6 +78,14 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
       REQ(value >= 0 && value <= 2, "attn_w4 must be 0, 1 or 2");
       nnhip::g_attn_w4 = value;
     }
+    else if (std::strcmp(key, "gemv_down_rows") == 0) {
+      REQ(value >= 0, "gemv_down_rows must be >= 0");
+      nnhip::g_gemv_down_rows = value;
+    }
+    else if (std::strcmp(key, "limb_k8") == 0) {
+      REQ(value >= 128, "limb_k8 must be >= 128");
+      nnhip::g_limb_k8 = value;
+    }
     else if (std::strcmp(key, "o_limb_rows") == 0) {
       REQ(value >= 0, "o_limb_rows must be >= 0");
       nnhip::g_o_limb_rows = value;

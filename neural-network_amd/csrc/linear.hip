@@ -299,15 +299,17 @@ __global__ __launch_bounds__(256) void act_quant_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kGemmMT = 32;
 
-// NSUB 32-column sub-tiles per workgroup (tile 32 x 32*NSUB).
-template <int NSUB>
-__global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
+// NSUB 32-column sub-tiles per workgroup (tile 32 x 32*NSUB); NW waves
+// split K (chunks w, w + NW, ...).
+template <int NSUB, int NW = 4>
+__global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_limb_kernel(
     const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
     int M, int K, int N, const int8_t *__restrict__ wq,
     const float *__restrict__ scale, const float *__restrict__ bias,
     const float *__restrict__ resid, int64_t ldr, float *__restrict__ y,
     int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
   constexpr int NT = 32 * NSUB;
+  constexpr int kThr = 64 * NW;
   __shared__ int red[kLimbs][kGemmMT][NT];
   const int T = ntm * ntn;
   const int per = (T + 7) / 8;
@@ -318,13 +320,15 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r = lane & 31, h = lane >> 5;
-  for (int i = threadIdx.x; i < kLimbs * kGemmMT * NT; i += 256)
+  for (int i = threadIdx.x; i < kLimbs * kGemmMT * NT; i += kThr)
     (&red[0][0][0])[i] = 0;
   // the epilogue's operands (thread -> (row, column pair) items), requested
   // now so that they arrive with the MFMA operands
-  // (256 is a multiple of NT/2, so a thread's items share one column pair)
-  constexpr int IT = kGemmMT * NT / 2 / 256;
-  static_assert(256 % (NT / 2) == 0, "items must share their columns");
+  // (the thread count is a multiple of NT/2, so a thread's items share one
+  // column pair)
+  constexpr int IT = kGemmMT * NT / 2 / kThr;
+  static_assert(IT >= 1 && IT * kThr == kGemmMT * NT / 2, "one item set per thread");
+  static_assert(kThr % (NT / 2) == 0, "items must share their columns");
   const int e_n = n0 + 2 * ((int)threadIdx.x % (NT / 2));
   const bool e_cols = epi != kEpiTotals;
   const float e_sc0 = e_cols ? scale[e_n] : 0.f, e_sc1 = e_cols ? scale[e_n + 1] : 0.f;
@@ -333,7 +337,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   float e_rs[IT][2];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int m = m0 + ((int)threadIdx.x + it * 256) / (NT / 2);
+    const int m = m0 + ((int)threadIdx.x + it * kThr) / (NT / 2);
     const bool ok = m < M && e_cols;
     e_ex[it] = ok ? rexp[m] : 0;
     e_rs[it][0] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n] : 0.f;
@@ -374,19 +378,19 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
         for (int l = 0; l < kLimbs; ++l)
           acc[t][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[l][s], f.b[t][s], acc[t][l], 0, 0, 0);
   };
-  // ping-pong over the wave's chunks w, w+4, w+8, ...: the loads of the next
-  // chunk are in flight while the current chunk's MFMAs run
+  // ping-pong over the wave's chunks w, w+NW, w+2NW, ...: the loads of the
+  // next chunk are in flight while the current chunk's MFMAs run
   Frag fa, fb;
   int c = cb + w;
   if (c < ce) load(c, fa);
   while (c < ce) {
-    if (c + 4 < ce) load(c + 4, fb);
+    if (c + NW < ce) load(c + NW, fb);
     mma(fa);
-    c += 4;
+    c += NW;
     if (c >= ce) break;
-    if (c + 4 < ce) load(c + 4, fa);
+    if (c + NW < ce) load(c + NW, fa);
     mma(fb);
-    c += 4;
+    c += NW;
   }
   if (cb + w < ce) {
 #pragma unroll
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(256, NSUB == 1 ? 2 : 1) void gemm_limb_kernel(
   // epilogue: thread -> (row, column pair)
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int idx = threadIdx.x + it * 256;
+    const int idx = threadIdx.x + it * kThr;
     const int row = idx / (NT / 2), cp = idx % (NT / 2);
     const int m = m0 + row;
     if (m >= M) continue;
@@ -991,6 +995,8 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   NNHIP_CHECK(hipGetLastError());
 }
 
+int g_limb_k8 = 1024;
+
 // The int8 KV append in gemm_limb_kernel's epilogue needs each head's pairs
 // within one tile row's 16 (32x32 tiles) column pairs.
 bool gemm_limb_q8_ok(int D) { return rope_q8_head_dim_ok(D) && D <= 32; }
@@ -1016,6 +1022,12 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   if (wide) {
     const int ntn = N / 64, per = (ntm * ntn + 7) / 8;
     hipLaunchKernelGGL(gemm_limb_kernel<2>, dim3(8 * per), dim3(256), 0, st,
+                       limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
+                       ldr, y, ldy, epi, ntm, ntn, rz);
+  } else if (K >= g_limb_k8) {
+    // long K: 8 waves split it, half the chunks each
+    const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
+    hipLaunchKernelGGL((gemm_limb_kernel<1, 8>), dim3(8 * per), dim3(512), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
                        ldr, y, ldy, epi, ntm, ntn, rz);
   } else {

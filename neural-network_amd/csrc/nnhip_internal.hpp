@@ -277,6 +277,7 @@ __device__ inline int digit_exponent(float mx) {
 
 // linear.hip
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
+extern int g_limb_k8;    // digit-plane GEMM: 8 waves split K from this K on
 // engine.hip
 extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
 // workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
@@ -284,6 +285,7 @@ constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
+extern int g_gemv_down_rows; // down projection on the GEMV up to this many rows
 extern int g_o_limb_rows; // output projection after merged attention: digit
                           // planes + digit-plane GEMM up to this many rows
 extern int g_kv_stream;  // attention: non-temporal fp32 KV loads (0 never,
