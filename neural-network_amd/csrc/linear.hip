@@ -116,6 +116,32 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   const int iters = (slen + 255) / 256;
   const int64_t ncol0 = (int64_t)blockIdx.x * cg * kGemvNC + cset * kGemvNC;
 
+  // The epilogue's operands, requested first so that they arrive with the
+  // main loads: thread t < cg * 8 * R owns item (row e_r, column e_n) --
+  // an output, or the even column of a SwiGLU / RoPE pair.
+  const bool pair = epi == kEpiSwiGLU || epi == kEpiRope;
+  const int e_r = (int)threadIdx.x % R, e_cc = ((int)threadIdx.x / R) % kGemvNC;
+  const int e_cs = (int)threadIdx.x / (R * kGemvNC);
+  const int64_t e_n = (int64_t)blockIdx.x * cg * kGemvNC + e_cs * kGemvNC + e_cc;
+  const bool e_ok = (int)threadIdx.x < cg * kGemvNC * R && e_n < N &&
+                    (!pair || (e_n & 1) == 0);
+  float e_sc0 = 1.f, e_sc1 = 1.f, e_bi0 = 0.f, e_bi1 = 0.f, e_rs = 0.f;
+  int e_pos = -1;
+  float2 e_cos = make_float2(0.f, 0.f);
+  if (e_ok) {
+    if (Q8) e_sc0 = scale[e_n];
+    e_bi0 = bias[e_n];
+    if (pair) {
+      if (Q8) e_sc1 = scale[e_n + 1];
+      e_bi1 = bias[e_n + 1];
+    }
+    if (epi == kEpiResid) e_rs = resid[e_r * ldr + e_n];
+    if (epi == kEpiRope) {
+      e_pos = rope_row_pos(ra, row0 + e_r);
+      if (e_pos >= 0 && e_n / (ra.H * ra.D) != 2) e_cos = rope_cos_sin(ra, e_pos, (int)e_n);
+    }
+  }
+
   float xr[R][kMaxIt][4];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -225,26 +251,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       red[w][slot / R][slot % R] = acc[0];
   }
   __syncthreads();
-  // combine the nks slices and apply the epilogue
-  for (int t = threadIdx.x; t < cg * kGemvNC * R; t += blockDim.x) {
-    int r = t % R;
-    int cc = (t / R) % kGemvNC;
-    int cs = t / (R * kGemvNC);
-    int64_t n = (int64_t)blockIdx.x * cg * kGemvNC + cs * kGemvNC + cc;
-    if (n >= N) continue;
+  // combine the nks slices and apply the epilogue (one item per thread:
+  // cg * 8 * R <= 256)
+  if (e_ok) {
+    const int r = e_r, cc = e_cc, cs = e_cs;
+    const int64_t n = e_n;
     float a = 0.f;
     for (int s = 0; s < nks; ++s) a += red[cs * nks + s][cc][r];
-    float v = Q8 ? a * scale[n] : a;
-    v = v + bias[n];
-    if (epi == kEpiSwiGLU || epi == kEpiRope) {
-      if (n & 1) continue;
+    float v = Q8 ? a * e_sc0 : a;
+    v = v + e_bi0;
+    if (pair) {
       float a1 = 0.f;
       for (int s = 0; s < nks; ++s) a1 += red[cs * nks + s][cc + 1][r];
-      float u = (Q8 ? a1 * scale[n + 1] : a1) + bias[n + 1];
+      float u = (Q8 ? a1 * e_sc1 : a1) + e_bi1;
       if (epi == kEpiSwiGLU) y[r * ldy + n / 2] = swiglu_pair(v, u);
-      else rope_store_pair(ra, row0 + r, (int)n, v, u);
+      else if (e_pos >= 0) rope_store_pair_at(ra, row0 + r, e_pos, (int)n, v, u, e_cos.x, e_cos.y);
     } else if (epi == kEpiResid) {
-      y[r * ldy + n] = resid[r * ldr + n] + v;
+      y[r * ldy + n] = e_rs + v;
     } else {
       y[r * ldy + n] = v;
     }
