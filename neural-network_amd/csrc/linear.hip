@@ -562,19 +562,24 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
   auto row_exps = [&](int tm) {
     return tid < kGemmMT && tm * kGemmMT + tid < M ? rexp[tm * kGemmMT + tid] : 0;
   };
-  v4i apc[kPer];
   float4 v[PP];
   int a_e = 0;
   const int rr = tid >> 5, pp = tid & 31;
   const bool live = tmb * kGemmMT + rr < M;
   if constexpr (kDig) {
+    // straight into LDS (global_load_lds puts lane i's 16 bytes at the
+    // wave's LDS address + 16 i); waited for before the prologue's barrier
     a_e = row_exps(tmb);
     const int8_t *src = limbs + (int64_t)tmb * nch * 4096;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int i = min(tid + j * kLdsThreads, kPieces - 1);
-      const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
-      apc[j] = *reinterpret_cast<const v4i *>(src + l * plane + o);
+      const int i0 = w * kWave + j * kLdsThreads;
+      if (kPieces % kLdsThreads == 0 || i0 < kPieces) {
+        const int l = i0 / (kPlane / 16), o = (i0 % (kPlane / 16)) * 16;
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void *)(src + l * plane + o + lane * 16),
+            (__attribute__((address_space(3))) void *)(sa + l * kPlane + o), 16, 0, 0);
+      }
     }
   } else {
     const int m = tmb * kGemmMT + rr;
@@ -603,15 +608,8 @@ __global__ __launch_bounds__(kLdsThreads) void gemm_lds_kernel(
 
   // ---- prologue: the first 32 x K digit tile in LDS ----
   if constexpr (kDig) {
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = tid + j * kLdsThreads;
-      if (kPieces % kLdsThreads == 0 || i < kPieces) {
-        const int l = i / (kPlane / 16), o = (i % (kPlane / 16)) * 16;
-        *reinterpret_cast<v4i *>(sa + l * kPlane + o) = apc[j];
-      }
-    }
     if (tid < kGemmMT) s_e[0][tid] = a_e;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // digits in LDS
   } else {
 #pragma clang fp contract(off)
     const int m = tmb * kGemmMT + rr;
