@@ -760,6 +760,74 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(
   ln_row_finish<NQ>(v, gv, bv, d, row, y, limbs, mpad, rexp, lane);
 }
 
+// LayerNorm as layernorm_rows_kernel with a row spread over WPR waves
+// (256 entries each, one quad a lane): the sums and the max of the row are
+// combined through LDS in wave order.
+template <int WPR>
+__global__ __launch_bounds__(256) void layernorm_split_kernel(
+    const float *__restrict__ hin, int d, int rows, const float *__restrict__ g,
+    const float *__restrict__ bt, float *__restrict__ y,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
+#pragma clang fp contract(off)
+  __shared__ float s_sum[4], s_sq[4], s_mx[4];
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (4 / WPR) + wv / WPR;
+  const int s0 = (wv % WPR) * 256, w0 = wv - wv % WPR;
+  const bool live = row < rows;
+  const int64_t rr = live ? row : rows - 1;
+  const int k = s0 + 4 * lane;
+  const float4 hv = *reinterpret_cast<const float4 *>(hin + rr * d + k);
+  const float4 gq = *reinterpret_cast<const float4 *>(g + k);
+  const float4 bq = *reinterpret_cast<const float4 *>(bt + k);
+  float v[4] = {hv.x, hv.y, hv.z, hv.w};
+  const float gv[4] = {gq.x, gq.y, gq.z, gq.w}, bv[4] = {bq.x, bq.y, bq.z, bq.w};
+  float sm = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sm += v[j];
+  sm = wave_sum_all(sm);
+  if (lane == 0) s_sum[wv] = sm;
+  __syncthreads();
+  sm = 0.f;
+#pragma unroll
+  for (int j = 0; j < WPR; ++j) sm += s_sum[w0 + j];
+  const float N = (float)d;
+  const float mean = sm / N;
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { const float df = v[j] - mean; sq += df * df; }
+  sq = wave_sum_all(sq);
+  if (lane == 0) s_sq[wv] = sq;
+  __syncthreads();
+  sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < WPR; ++j) sq += s_sq[w0 + j];
+  const float sd = sqrtf(sq / N + 1e-5f);
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = (v[j] - mean) / sd * gv[j] + bv[j];
+    mx = fmaxf(mx, fabsf(v[j]));
+  }
+  if (live)
+    *reinterpret_cast<float4 *>(y + rr * d + k) = make_float4(v[0], v[1], v[2], v[3]);
+  if (!limbs) return;
+  mx = wave_max_all(mx);
+  if (lane == 0) s_mx[wv] = mx;
+  __syncthreads();
+  mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < WPR; ++j) mx = fmaxf(mx, s_mx[w0 + j]);
+  if (!live) return;
+  const int e = digit_exponent(mx);
+  if (lane == 0 && s0 == 0) rexp[row] = e;
+  const int64_t plane = (int64_t)mpad * d;
+  const int3 t = digits4(v, e);
+  const int64_t off = mfma_operand_offset(row, k, d);
+  *reinterpret_cast<int *>(limbs + off) = t.x;
+  *reinterpret_cast<int *>(limbs + plane + off) = t.y;
+  *reinterpret_cast<int *>(limbs + 2 * plane + off) = t.z;
+}
+
 __global__ void add_scalar_kernel(int32_t *p, int n, int v) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] += v;
@@ -831,6 +899,7 @@ void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
 int g_attn_waves = 4096;
 int g_kv_stream = 1;
 int g_attn_w4 = 1;
+int g_ln_split = 1;
 
 // Splits of the key range: about g_attn_waves waves over the whole launch
 // (4 per SIMD by default), each split a whole number of 32-key chunks.
@@ -956,7 +1025,17 @@ void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
   NNHIP_REQUIRE(d <= 4096, kErrArg, "layernorm: d must be <= 4096");
   NNHIP_REQUIRE(!limbs || (d % 128 == 0 && rows <= mpad), kErrArg,
                 "layernorm: digit output needs d % 128 == 0");
-  if (d % 16 == 0 && d <= 4096) {
+  if (g_ln_split && (d == 512 || d == 1024) &&
+      ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(y) |
+        reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(b)) & 15) == 0) {
+    // 256 entries a wave: 2 or 4 waves a row
+    if (d == 512)
+      hipLaunchKernelGGL((layernorm_split_kernel<2>), dim3((rows + 1) / 2), dim3(256), 0,
+                         st, h, d, rows, g, b, y, limbs, mpad, rexp);
+    else
+      hipLaunchKernelGGL((layernorm_split_kernel<4>), dim3(rows), dim3(256), 0, st, h,
+                         d, rows, g, b, y, limbs, mpad, rexp);
+  } else if (d % 16 == 0 && d <= 4096) {
     const dim3 grid((rows + 3) / 4);
 #define NNHIP_LN(P)                                                           \
   hipLaunchKernelGGL((layernorm_rows_kernel<P>), grid, dim3(256), 0, st, h, d, \

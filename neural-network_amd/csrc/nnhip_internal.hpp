@@ -283,6 +283,7 @@ extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
 // workgroups of the LDS GEMM resident at once (one per CU of an MI355X)
 constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
+extern int g_ln_split;   // LayerNorm rows of 512 / 1024 over 2 / 4 waves
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
 extern int g_gemv_down_rows; // down projection on the GEMV up to this many rows
