@@ -163,14 +163,16 @@ TRAFFIC_NOTE = os.path.join(ROOT, "profiles", "attention_verify_traffic.md")
 GEMM_NOTE = os.path.join(ROOT, "profiles", "gemm_cycle_shapes.md")
 
 
-def measured_traffic(note=TRAFFIC_NOTE):
+def measured_traffic(note=TRAFFIC_NOTE, kernel=None):
     """HBM bytes per launch of a kernel as measured by the rocprofv3
     FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (the note's
-    traffic_bytes_per_launch line)."""
+    traffic_bytes_per_launch line, or traffic_bytes_per_launch[kernel])."""
+    key = ("traffic_bytes_per_launch" if kernel is None
+           else f"traffic_bytes_per_launch[{kernel}]") + ":"
     try:
         with open(note) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key):
                     return int(line.split(":")[1])
     except OSError:
         pass
@@ -242,24 +244,25 @@ def verify_step(ctx, t, q8=False):
 # The cycle's GEMM launches (batch 32, k = 5): the 5 draft forwards on 32
 # rows (d 512; the first also carries the catch-up row, 64 rows) and the
 # verify forward on 192 rows (d 1024), with the kernel each runs in the
-# library (nnhip_bench_linear path: 3 = LDS GEMM digitising fp32 rows,
-# 6 = LDS GEMM over digit planes with the lm head's tile statistics,
-# 7 = LDS GEMM over digit planes, 8 = digit-plane GEMM) and launches per
-# cycle.
+# library (nnhip_bench_linear path: 1 = GEMV over fp32 rows, 6 = LDS GEMM
+# over digit planes with the lm head's tile statistics, 7 = LDS GEMM over
+# digit planes, 8 = digit-plane GEMM; the digit planes of the output and
+# down projections are made by act_quant_kernel, timed apart) and launches
+# per cycle.
 CYCLE_GEMMS = [
     # name, rows, K, N, path, kernel family, launches per cycle
     ("draft qkv", 32, 512, 1536, 8, "gemm_limb_kernel", 16),
-    ("draft o", 32, 512, 512, 3, "gemm_lds_kernel", 16),
+    ("draft o", 32, 512, 512, 8, "gemm_limb_kernel", 16),
     ("draft gate/up", 32, 512, 4096, 8, "gemm_limb_kernel", 16),
-    ("draft down", 32, 2048, 512, 8, "gemm_limb_kernel", 16),
+    ("draft down", 32, 2048, 512, 1, "gemv_kernel", 16),
     ("draft lm head", 32, 512, 32000, 6, "gemm_lds_kernel", 4),
-    ("draft qkv (catch-up)", 64, 512, 1536, 7, "gemm_lds_kernel", 4),
-    ("draft o (catch-up)", 64, 512, 512, 3, "gemm_lds_kernel", 4),
-    ("draft gate/up (catch-up)", 64, 512, 4096, 7, "gemm_lds_kernel", 4),
-    ("draft down (catch-up)", 64, 2048, 512, 8, "gemm_limb_kernel", 4),
+    ("draft qkv (catch-up)", 64, 512, 1536, 8, "gemm_limb_kernel", 4),
+    ("draft o (catch-up)", 64, 512, 512, 8, "gemm_limb_kernel", 4),
+    ("draft gate/up (catch-up)", 64, 512, 4096, 8, "gemm_limb_kernel", 4),
+    ("draft down (catch-up)", 64, 2048, 512, 1, "gemv_kernel", 4),
     ("draft lm head (catch-up)", 32, 512, 32000, 6, "gemm_lds_kernel", 1),
     ("verify qkv", 192, 1024, 3072, 7, "gemm_lds_kernel", 12),
-    ("verify o", 192, 1024, 1024, 3, "gemm_lds_kernel", 12),
+    ("verify o", 192, 1024, 1024, 8, "gemm_limb_kernel", 12),
     ("verify gate/up", 192, 1024, 8192, 7, "gemm_lds_kernel", 12),
     ("verify down", 192, 4096, 1024, 8, "gemm_limb_kernel", 12),
     ("verify lm head", 192, 1024, 32000, 6, "gemm_lds_kernel", 1),
@@ -269,10 +272,10 @@ CYCLE_GEMMS = [
 def gemm_bytes(rows, K, N, path):
     """Algorithmic bytes of one GEMM launch: int8 codes, fp32 scale and bias
     per column, the activations as read (three int8 digit planes and an
-    exponent per row, or fp32 rows for path 3), fp32 outputs written (tile
+    exponent per row, or fp32 rows for the GEMV), fp32 outputs written (tile
     statistics instead of logits are not counted: the logits are written
     too)."""
-    act = rows * K * 4 if path == 3 else rows * (3 * K + 4)
+    act = rows * K * 4 if path in (1, 3) else rows * (3 * K + 4)
     return N * K + 8 * N + act + rows * N * 4
 
 
@@ -309,8 +312,7 @@ def roofline_gemm(fam, kern):
     ach = f["bytes"] / f["us"] / 1e3
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
-                traffic=(measured_traffic(GEMM_NOTE)
-                         if kern == "gemm_lds_kernel" else None),
+                traffic=measured_traffic(GEMM_NOTE, kern),
                 kernel=kern, launches_per_cycle=f["launches"],
                 us_per_launch=round(f["us"] / f["launches"], 2),
                 bytes_per_launch=int(f["bytes"] / f["launches"]),

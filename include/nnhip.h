@@ -69,7 +69,16 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * one attention launch reads more rows than the L2 caches hold (default),
  * 2 always (process-wide).
  * "lds_min_rows": the LDS-resident GEMM serves projections from this many
- * rows on (default 64; process-wide).
+ * rows on (default 128; process-wide).
+ * "limb_k8": the digit-plane GEMM splits K over 8 waves from this K on
+ * (default 1024; process-wide).
+ * "o_limb_rows": after the merged attention, the output projection of up
+ * to this many rows runs as act_quant + digit-plane GEMM, taller inputs on
+ * the LDS GEMM digitising the context rows (default 256; process-wide).
+ * "gemv_down_rows": the down projection of up to this many rows runs on the
+ * GEMV over the fp32 SwiGLU rows (default 64; process-wide).
+ * "ln_split": 1 = LayerNorm rows of 512 / 1024 spread over 2 / 4 waves
+ * (default), 0 = one wave per row (process-wide).
  * No option changes results beyond fp32 rounding order. */
 int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value);
 int nnhip_sync(nnhip_ctx *ctx);
