@@ -54,9 +54,10 @@ def test_quantize_w8_bit_exact(ctx):
 GEMV_SHAPES = [(1, 64, 64), (1, 256, 768), (2, 512, 1536), (3, 1024, 1024),
                (4, 1024, 4096), (5, 2048, 512), (8, 4096, 1024),
                (1, 4096, 1024), (6, 128, 320),
-               # several 8-row groups in one launch, with and without a
-               # remainder launch (the draft's 32 / 64 rows)
-               (32, 512, 1536), (37, 2048, 512), (64, 512, 4096)]
+               # 32+ rows in 4-row groups (the draft's down projection at
+               # 32 / 64 rows), and 8-row groups with a remainder launch
+               (32, 512, 1536), (32, 2048, 512), (64, 2048, 512),
+               (37, 2048, 512), (64, 512, 4096)]
 
 
 @pytest.mark.parametrize("rows,K,N", GEMV_SHAPES)
