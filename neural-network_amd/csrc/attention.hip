@@ -28,55 +28,23 @@ constexpr int kWave = 64;
 constexpr int kMaxQ = 8;       // queries per workgroup
 constexpr int kMaxD = 64;      // head dim handled by the attention kernel
 
-// Digits of one row for the MFMA GEMM (same rule as act_quant_kernel): the
-// row (d floats, d % 128 == 0) is in LDS, mx is the thread's max |value|;
-// NT threads reduce it through sred, then the row exponent goes to rexp and
-// the three digit planes to limbs (MFMA operand layout, planes mpad x d).
-template <int NT>
-__device__ void store_row_digits(const float *srow, int d, float mx,
-                                 int64_t row, int8_t *__restrict__ limbs,
-                                 int mpad, int *__restrict__ rexp,
-                                 float *sred) {
-  typedef int v4i __attribute__((ext_vector_type(4)));
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  mx = 0.f;
-#pragma unroll
-  for (int w = 0; w < NT / kWave; ++w) mx = fmaxf(mx, sred[w]);
-  const int e = digit_exponent(mx);
-  if (threadIdx.x == 0) rexp[row] = e;
-  const int64_t plane = (int64_t)mpad * d;
-  for (int p = threadIdx.x; p < d / 16; p += NT) {
-    const int k = p * 16;
-    v4i hi, mid, lo;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int3 t = digits4(srow + k + 4 * q, e);
-      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
-    }
-    const int64_t off = mfma_operand_offset((int)row, k, d);
-    *reinterpret_cast<v4i *>(limbs + off) = hi;
-    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
-    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
-  }
-}
-
 // Embedding gather (cpu_backend.cpp:1020-1025): ids outside [0, vocab) read
-// row 0.  Row t = b*S + s takes ids[b*stride_b + s].  With limbs, the row's
-// digits for the first q/k/v GEMM are written too.
+// row 0.  Row t = b*S + s takes ids[b*stride_b + s], or with lead set
+// lead[b] for s = 0 and ids[b*stride_b + s - 1] after it (the verify rows
+// [generated.back(), c_0 .. c_{k-1}] of layer.cpp:1560-1566 read from the
+// last tokens and the candidates).  With limbs, the row's digits for the
+// first q/k/v GEMM are written too.
 __global__ __launch_bounds__(256) void embed_kernel(
     const float *__restrict__ emb, int vocab, int d,
     const int32_t *__restrict__ ids, int S, int stride_b,
-    float *__restrict__ x, int8_t *__restrict__ limbs, int mpad,
-    int *__restrict__ rexp) {
+    const int32_t *__restrict__ lead, float *__restrict__ x,
+    int8_t *__restrict__ limbs, int mpad, int *__restrict__ rexp) {
   __shared__ float srow[4096];
   __shared__ float sred[4];
   const int t = blockIdx.x;
   const int b = t / S, s = t % S;
-  int id = ids[(int64_t)b * stride_b + s];
+  int id = !lead ? ids[(int64_t)b * stride_b + s]
+                 : (s == 0 ? lead[b] : ids[(int64_t)b * stride_b + s - 1]);
   if (id < 0 || id >= vocab) id = 0;
   const float *src = emb + (int64_t)id * d;
   float *dst = x + (int64_t)t * d;
@@ -108,17 +76,6 @@ __global__ __launch_bounds__(256) void embed_kernel(
     }
   }
   if (limbs) store_row_digits<256>(srow, d, mx, t, limbs, mpad, rexp, sred);
-}
-
-// verify input of one cycle: [generated.back(), c_0 .. c_{k-1}] per sequence
-// (layer.cpp:1560-1566).
-__global__ void build_verify_ids_kernel(const int32_t *__restrict__ cur,
-                                        const int32_t *__restrict__ cand, int B,
-                                        int k, int32_t *__restrict__ ids) {
-  int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * (k + 1)) return;
-  int b = i / (k + 1), s = i % (k + 1);
-  ids[i] = s == 0 ? cur[b] : cand[b * k + s - 1];
 }
 
 // RoPE on q and k at position base[b] + off + s (tensor.cpp:1141-1173, with
@@ -845,25 +802,18 @@ void launch_embed(hipStream_t st, const float *emb, int vocab, int d,
                   const int32_t *ids, int rows, float *x) {
   // ids contiguous, one per row
   hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, st, emb, vocab, d,
-                     ids, 1, 1, x, nullptr, 0, nullptr);
+                     ids, 1, 1, nullptr, x, nullptr, 0, nullptr);
   NNHIP_CHECK(hipGetLastError());
 }
 
 void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
                           const int32_t *ids, int B, int S, int stride_b,
-                          float *x, int8_t *limbs, int mpad, int *rexp) {
+                          float *x, int8_t *limbs, int mpad, int *rexp,
+                          const int32_t *lead) {
   NNHIP_REQUIRE(d <= 4096 && (!limbs || (d % 128 == 0 && B * S <= mpad)),
                 kErrArg, "embed: digit output needs d % 128 == 0, d <= 4096");
   hipLaunchKernelGGL(embed_kernel, dim3(B * S), dim3(256), 0, st, emb, vocab,
-                     d, ids, S, stride_b, x, limbs, mpad, rexp);
-  NNHIP_CHECK(hipGetLastError());
-}
-
-void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
-                             const int32_t *cand, int B, int k, int32_t *ids) {
-  int n = B * (k + 1);
-  hipLaunchKernelGGL(build_verify_ids_kernel, dim3((n + 255) / 256), dim3(256),
-                     0, st, cur, cand, B, k, ids);
+                     d, ids, S, stride_b, lead, x, limbs, mpad, rexp);
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -400,10 +400,25 @@ void Model::linear(const Linear &ln, const float *x, int64_t ldx,
   }
 }
 
+bool Model::emb_digits(int rows) const {
+  return use_lds(layers[0].qkv, rows) || use_limbs(layers[0].qkv, rows);
+}
+
+NextRows Model::next_rows(int rows) const {
+  NNHIP_REQUIRE(wsp.rows >= rows && d <= 4096, kErrArg,
+                "next_rows: workspace not reserved, or d above 4096");
+  NextRows n;
+  n.emb = emb.p; n.vocab = V; n.d = d; n.x = wsp.x.p;
+  n.limbs = emb_digits(rows) ? wsp.limbs.p : nullptr;
+  n.mpad = wsp.mpad; n.rexp = wsp.rexp.p;
+  return n;
+}
+
 void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
                     int ids_stride, int B, int S, const int32_t *base, int off,
                     const int32_t *active, int max_keys, float *logits,
-                    bool last_only, int64_t ldl, const TileStatsArgs *ts) {
+                    bool last_only, int64_t ldl, const TileStatsArgs *ts,
+                    bool embedded, const int32_t *lead) {
   if (ldl == 0) ldl = V;
   hipStream_t st = ctx->stream;
   const int R = B * S;
@@ -421,9 +436,11 @@ void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
   const int32_t *bp = base ? base : ws.zeros.p;
   // the embedding kernel also writes the rows' digits for the first q/k/v
   // GEMM when that is an MFMA GEMM
-  const bool emb_digits = use_lds(layers[0].qkv, R) || use_limbs(layers[0].qkv, R);
-  launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
-                       emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
+  const bool emb_digits = this->emb_digits(R);
+  if (!embedded)
+    launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
+                         emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p,
+                         lead);
   // Post-norm blocks (layer.cpp:1098-1113): each LayerNorm is applied by the
   // linear that consumes it (norm1 -> ffn gate/up, norm2 -> next q/k/v or
   // the lm head), which also writes the normalised rows for the residual.
@@ -599,7 +616,7 @@ namespace {
 
 struct SpecBuffers {
   DevBuf<int32_t> cur, cand, tlen, dlen, gen, cyc, active, catchup, catch_tok, pair,
-      out, n_active, vids, prompts;
+      out, n_active, prompts;
   DevBuf<float> qprob, dlog, tlog, tstat;
   DevBuf<float2> dtiles;
   DevBuf<int64_t> stats;
@@ -654,7 +671,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.dlen.alloc(B); bf.gen.alloc(B); bf.cyc.alloc(B); bf.active.alloc(B);
   bf.catchup.alloc(B); bf.catch_tok.alloc(B); bf.pair.alloc((size_t)2 * B);
   bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
-  bf.vids.alloc((size_t)B * (k + 1)); bf.prompts.alloc((size_t)B * P);
+  bf.prompts.alloc((size_t)B * P);
   // Drafting samples from the draft lm head's tile statistics when that lm
   // head forms them for the batch's row count; otherwise from full passes
   // over the logits.  (The verify rows keep full passes: tile statistics in
@@ -713,6 +730,12 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                nullptr, true);
   NNHIP_CHECK(hipEventRecord(e1, st));
 
+  // Drafting steps j < k - 1 embed the next draft step's row themselves
+  // (s.nd), so those forwards gather nothing; the verify forward gathers
+  // [cur, c_0 .. c_{k-1}] straight from the last tokens and the candidates.
+  // (The last drafting step embedding the verify rows itself, k + 1 rows of
+  // one workgroup, measured no faster than the gather launch.)
+  s.nd = dm.next_rows(B);
   auto cycle = [&]() {
     for (int j = 0; j < k; ++j) {
       TileStatsArgs dts;
@@ -726,13 +749,12 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                    d_need, bf.dlog.p, true, 0, &dts);
       else
         dm.forward(&dc, 0, bf.cand.p + (j - 1), k, B, 1, bf.dlen.p, j,
-                   bf.active.p, d_need, bf.dlog.p, false, 0, &dts);
+                   bf.active.p, d_need, bf.dlog.p, false, 0, &dts, true);
       if (tiles) launch_draft_sample_tiles(st, s, j, bf.dlog.p, V);
       else launch_draft_sample(st, s, j, bf.dlog.p, V);
     }
-    launch_build_verify_ids(st, bf.cur.p, bf.cand.p, B, k, bf.vids.p);
-    t.forward(&tc, 0, bf.vids.p, k + 1, B, k + 1, bf.tlen.p, 0, bf.active.p,
-              t_need, bf.tlog.p, false);
+    t.forward(&tc, 0, bf.cand.p, k, B, k + 1, bf.tlen.p, 0, bf.active.p,
+              t_need, bf.tlog.p, false, 0, nullptr, false, bf.cur.p);
     launch_accept(st, s, bf.tlog.p);
   };
 

@@ -87,11 +87,21 @@ struct Model {
   // active[b] == 0 neither write nor read the cache.  logits: nullptr (not
   // needed), or [B*S][V] (all rows) or [B][V] (last_only), rows ldl apart
   // (0 = V).  ts: the lm head's tile statistics as well (lm_tiles(rows)).
+  // embedded: the rows (and their digits, when emb_digits(B * S)) are
+  // already in the workspace (next_rows), ids are not read.  lead: row
+  // (b, 0) takes lead[b] and row (b, s) ids[b*ids_stride + s - 1].
   void forward(KVCache *cache, int b_off, const int32_t *ids,
                int ids_stride, int B, int S, const int32_t *base, int off,
                const int32_t *active, int max_keys, float *logits,
                bool last_only, int64_t ldl = 0,
-               const TileStatsArgs *ts = nullptr);
+               const TileStatsArgs *ts = nullptr, bool embedded = false,
+               const int32_t *lead = nullptr);
+  // whether the embedding step also writes the rows' digits (the first
+  // q/k/v projection of `rows` rows is an MFMA GEMM)
+  bool emb_digits(int rows) const;
+  // where a kernel other than the embedding writes the input rows of a
+  // forward of `rows` rows (the workspace must be reserved for them)
+  NextRows next_rows(int rows) const;
   // whether the lm head on `rows` rows can form tile statistics
   bool lm_tiles(int rows) const;
 

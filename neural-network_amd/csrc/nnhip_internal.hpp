@@ -402,12 +402,12 @@ void launch_fill(hipStream_t st, float *p, int64_t n, float v);
 // attention.hip
 void launch_embed(hipStream_t st, const float *emb, int vocab, int d,
                   const int32_t *ids, int rows, float *x);
+// row (b, s) takes ids[b*stride_b + s]; with lead, lead[b] for s = 0 and
+// ids[b*stride_b + s - 1] after it
 void launch_embed_strided(hipStream_t st, const float *emb, int vocab, int d,
                           const int32_t *ids, int B, int S, int stride_b,
                           float *x, int8_t *limbs = nullptr, int mpad = 0,
-                          int *rexp = nullptr);
-void launch_build_verify_ids(hipStream_t st, const int32_t *cur,
-                             const int32_t *cand, int B, int k, int32_t *ids);
+                          int *rexp = nullptr, const int32_t *lead = nullptr);
 // qkv rows [q: H heads | k: Hkv heads | v: Hkv heads] (Hkv 0: H); the
 // cache holds Hkv heads per sequence
 void launch_rope_kv(hipStream_t st, const float *qkv, int B, int S, int H,
@@ -499,6 +499,18 @@ constexpr int kMaxLookahead = 63;
 inline bool sampling_filtered(int V, int top_k, float top_p) {
   return (top_k > 0 && top_k < V) || (top_p > 0.0f && top_p < 1.0f);
 }
+// Rows of the next forward that a sampling kernel embeds itself (the gather
+// of embed_kernel, cpu_backend.cpp:1020-1025, with the rows' digits for the
+// first q/k/v GEMM when limbs is set): row r of x takes emb[id] (ids outside
+// [0, vocab) read row 0).  Unset (x null): the forward gathers them.
+struct NextRows {
+  const float *emb = nullptr;
+  int vocab = 0, d = 0;
+  float *x = nullptr;
+  int8_t *limbs = nullptr;
+  int mpad = 0;
+  int *rexp = nullptr;
+};
 struct SpecState {
   int32_t *cur;        // [B] last committed token (generated.back())
   int32_t *cand;       // [B][k] draft candidates of this cycle
@@ -535,6 +547,9 @@ struct SpecState {
   // when set, accept_kernel also writes each sequence's accepted count and
   // its resampled / bonus token (-1 when none)
   int32_t *n_acc_out = nullptr, *tok_out = nullptr;
+  // when nd is set, drafting steps j < k - 1 embed their token as row b of
+  // the next draft forward
+  NextRows nd;
 };
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl);

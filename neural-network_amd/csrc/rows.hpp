@@ -113,6 +113,42 @@ __device__ __forceinline__ void aq_store_digits(const float (&v)[NQ][4], int s0,
   }
 }
 
+// Digits of one row for the MFMA GEMM (same rule as act_quant_kernel): the
+// row (d floats, d % 128 == 0) is in LDS, mx is the thread's max |value|;
+// NT threads reduce it through sred, then the row exponent goes to rexp and
+// the three digit planes to limbs (MFMA operand layout, planes mpad x d).
+template <int NT>
+__device__ inline void store_row_digits(const float *srow, int d, float mx,
+                                 int64_t row, int8_t *__restrict__ limbs,
+                                 int mpad, int *__restrict__ rexp,
+                                 float *sred) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sred[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) mx = fmaxf(mx, sred[w]);
+  const int e = digit_exponent(mx);
+  if (threadIdx.x == 0) rexp[row] = e;
+  const int64_t plane = (int64_t)mpad * d;
+  for (int p = threadIdx.x; p < d / 16; p += NT) {
+    const int k = p * 16;
+    v4i hi, mid, lo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int3 t = digits4(srow + k + 4 * q, e);
+      hi[q] = t.x; mid[q] = t.y; lo[q] = t.z;
+    }
+    const int64_t off = mfma_operand_offset((int)row, k, d);
+    *reinterpret_cast<v4i *>(limbs + off) = hi;
+    *reinterpret_cast<v4i *>(limbs + plane + off) = mid;
+    *reinterpret_cast<v4i *>(limbs + 2 * plane + off) = lo;
+  }
+}
+
 // quads of a row with ordinary loads
 template <int NQ>
 __device__ __forceinline__ void load_quads(const float *__restrict__ xr, int d,

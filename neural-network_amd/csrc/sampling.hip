@@ -11,6 +11,7 @@
 // Uniforms: Philox4x32-10 keyed by the seed, counter {slot, cycle, seq, 0},
 // u = (word0 >> 8) * 2^-24 -- the stream the oracle uses.
 #include "nnhip_internal.hpp"
+#include "rows.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -559,18 +560,48 @@ __device__ __forceinline__ int tiles_sample(const float *__restrict__ row,
 constexpr int kQParts = 8;
 constexpr int kQPer = (kMaxV / kQParts + kThreads - 1) / kThreads;
 
+// After drafting step j < k - 1 picked `tok` for sequence b (block-uniform):
+// row b of the next draft forward, embedded here instead of by a gather
+// launch of its own (SpecState::nd).  srow: kMaxEmbed floats of LDS, sred:
+// kWaves floats.
+constexpr int kMaxEmbed = 4096;
+__device__ void embed_row(const NextRows &n, int64_t row, int id, float *srow,
+                          float *sred) {
+  if (id < 0 || id >= n.vocab) id = 0;
+  const float *src = n.emb + (int64_t)id * n.d;
+  float *dst = n.x + row * n.d;
+  float mx = 0.f;
+  for (int i = threadIdx.x; i < n.d; i += kThreads) {
+    const float v = src[i];
+    dst[i] = v;
+    srow[i] = v;
+    mx = fmaxf(mx, fabsf(v));
+  }
+  if (n.limbs) store_row_digits<kThreads>(srow, n.d, mx, row, n.limbs, n.mpad, n.rexp, sred);
+  __syncthreads();   // srow free for the next row
+}
+__device__ void embed_next(const SpecState &s, int b, int j, int tok,
+                           float *srow, float *sred) {
+  if (j < s.k - 1 && s.nd.x) embed_row(s.nd, b, tok, srow, sred);
+}
+
 __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
     SpecState s, int j, const float *__restrict__ logits, int64_t ldl) {
   __shared__ SmallShared sh;
   __shared__ RowStats rst;
+  __shared__ float s_emb[kMaxEmbed], s_red[kWaves];
+  __shared__ int s_tok;
   const int b = blockIdx.x, part = blockIdx.y;
   if (!s.active[b]) return;
   const float2 *tl = s.dtiles + ((int64_t)b * s.k + j) * s.nt;
   if (s.T <= 0.f) {
-    if (part == 0 && threadIdx.x < 64) {
+    if (part != 0) return;
+    if (threadIdx.x < 64) {
       const int a = wave_tiles_argmax(tl, s.nt);
-      if (threadIdx.x == 0) s.cand[b * s.k + j] = a;
+      if (threadIdx.x == 0) { s.cand[b * s.k + j] = a; s_tok = a; }
     }
+    __syncthreads();
+    embed_next(s, b, j, s_tok, s_emb, s_red);
     return;
   }
   const float *row = logits + b * ldl;
@@ -597,6 +628,7 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
   const int tok = tiles_sample(row, tl, s.nt, s.tw, s.V, s.T, st,
                                uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
+  embed_next(s, b, j, tok, s_emb, s_red);
 }
 
 // ---------------------------------------------------------------------------
@@ -647,6 +679,9 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
     tok = block_sample(s.V, uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
   }
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
+  // the probability row is no longer needed: its LDS holds the embedded row
+  __syncthreads();
+  embed_next(s, b, j, tok, sh.prow, sh.f);
 }
 
 __device__ __forceinline__ int verify_rows(const SpecState &s) {
