@@ -226,7 +226,9 @@ int nnhip_quantize_w4(nnhip_ctx *ctx, const float *w, int in, int out,
  * 2 int8-digit MFMA GEMM (K % 128 == 0, N % 64 == 0), 3 MFMA GEMM with the
  * digits formed in LDS from x, 4 the same GEMM fed with digit planes
  * (3 and 4: K in {128, 256, 512, 1024}, N % 32 == 0).  The MFMA paths (2-4)
- * agree bit for bit. */
+ * agree bit for bit.  Stream-ordered: the digit planes and the codes in the
+ * MFMA operand layout go to scratch the context keeps and reuses, which
+ * grows (after draining the stream) only when a call needs more. */
 int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
                        const int8_t *codes, const float *scales,
                        const float *bias, int N, float *y, int path);
@@ -237,7 +239,8 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
  * and LN(h) into ln_out when it is not NULL.  K in {128, 256, 512, 1024},
  * N % 32 == 0.  Rows below 16 run on the GEMV with the LayerNorm as its
  * prologue (the decode path of short batches), others on the LDS-resident
- * MFMA GEMM with the LayerNorm in its prologue. */
+ * MFMA GEMM with the LayerNorm in its prologue.  Stream-ordered, with the
+ * context's scratch as nnhip_linear_w8a32. */
 int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
                                  int K, const float *gamma, const float *beta,
                                  float *ln_out, const int8_t *codes,

@@ -448,6 +448,20 @@ struct LimbScratch {
     mpad = mp;
   }
 };
+// The context's scratch for `rows` rows of K digits and an N x K code copy
+// in the operand layout; the stream drains first when a buffer must grow
+// (earlier calls may still be reading it).  Returns the digit planes' mpad.
+int ctx_scratch(nnhip_ctx *ctx, int rows, int K, int N) {
+  const int mp = (rows + 63) / 64 * 64;
+  const size_t nl = (size_t)3 * mp * K, nw = (size_t)N * K;
+  if (nl > ctx->limbs.n || (size_t)mp > ctx->rexp.n || nw > ctx->sw.n) {
+    NNHIP_CHECK(hipStreamSynchronize(ctx->c.stream));
+    ctx->limbs.ensure(nl);
+    ctx->rexp.ensure(mp);
+    ctx->sw.ensure(nw);
+  }
+  return mp;
+}
 }  // namespace
 
 int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
@@ -465,27 +479,21 @@ int nnhip_linear_w8a32(nnhip_ctx *ctx, const float *x, int rows, int K,
     if (path == 3 || path == 4) {
       NNHIP_REQUIRE(nnhip::gemm_lds_supports(rows, K, N), nnhip::kErrArg,
                     "LDS GEMM needs K in {128, 256, 512, 1024} and N % 32 == 0");
-      LimbScratch ls;
-      ls.ensure(rows, K);
-      nnhip::DevBuf<int8_t> sw((size_t)N * K);
-      nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
+      const int mpad = ctx_scratch(ctx, rows, K, N);
+      nnhip::launch_swizzle_rows(st, codes, N, K, ctx->sw.p, false);
       if (path == 4)
-        nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
+        nnhip::launch_act_quant(st, x, K, rows, K, ctx->limbs.p, mpad, ctx->rexp.p);
       nnhip::launch_gemm_lds(st, path == 4 ? nnhip::kAFromDigits : nnhip::kAFromRows,
-                             ls.limbs.p, ls.mpad, ls.rexp.p, x, K, nullptr,
-                             nullptr, nullptr, 0, rows, K, N, sw.p, scales,
+                             ctx->limbs.p, mpad, ctx->rexp.p, x, K, nullptr,
+                             nullptr, nullptr, 0, rows, K, N, ctx->sw.p, scales,
                              bias, nullptr, 0, y, N, nnhip::kEpiBias);
-      NNHIP_CHECK(hipStreamSynchronize(st));
     } else if (mfma) {
-      LimbScratch ls;
-      ls.ensure(rows, K);
-      nnhip::DevBuf<int8_t> sw((size_t)N * K);
-      nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
-      nnhip::launch_act_quant(st, x, K, rows, K, ls.limbs.p, ls.mpad, ls.rexp.p);
-      nnhip::launch_gemm_limb(st, ls.limbs.p, ls.mpad, ls.rexp.p, rows, K, N,
-                              sw.p, scales, bias, nullptr, 0, y, N,
+      const int mpad = ctx_scratch(ctx, rows, K, N);
+      nnhip::launch_swizzle_rows(st, codes, N, K, ctx->sw.p, false);
+      nnhip::launch_act_quant(st, x, K, rows, K, ctx->limbs.p, mpad, ctx->rexp.p);
+      nnhip::launch_gemm_limb(st, ctx->limbs.p, mpad, ctx->rexp.p, rows, K, N,
+                              ctx->sw.p, scales, bias, nullptr, 0, y, N,
                               nnhip::kEpiBias);
-      NNHIP_CHECK(hipStreamSynchronize(st));
     } else {
       nnhip::launch_gemv(st, x, K, rows, K, N, codes, nullptr, scales, bias,
                          nullptr, 0, y, N, nnhip::kEpiBias);
@@ -509,15 +517,13 @@ int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
       lf.g = gamma; lf.b = beta; lf.out = ln_out; lf.ldo = K;
       nnhip::launch_gemv(st, h, K, rows, K, N, codes, nullptr, scales, bias,
                          nullptr, 0, y, N, nnhip::kEpiBias, nullptr, &lf);
-      NNHIP_CHECK(hipStreamSynchronize(st));
       return;
     }
-    nnhip::DevBuf<int8_t> sw((size_t)N * K);
-    nnhip::launch_swizzle_rows(st, codes, N, K, sw.p, false);
+    ctx_scratch(ctx, 1, K, N);
+    nnhip::launch_swizzle_rows(st, codes, N, K, ctx->sw.p, false);
     nnhip::launch_gemm_lds(st, nnhip::kAFromLayerNorm, nullptr, 0, nullptr, h,
-                           K, gamma, beta, ln_out, K, rows, K, N, sw.p, scales,
+                           K, gamma, beta, ln_out, K, rows, K, N, ctx->sw.p, scales,
                            bias, nullptr, 0, y, N, nnhip::kEpiBias);
-    NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }
 

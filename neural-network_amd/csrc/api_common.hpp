@@ -11,6 +11,11 @@
 struct nnhip_ctx {
   nnhip::Ctx c;
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  // scratch of the fused entry points, reused in stream order on c.stream:
+  // digit planes and row exponents, the codes in the MFMA operand layout
+  // (grown when a call needs more, after the stream has drained)
+  nnhip::DevBuf<int8_t> limbs, sw;
+  nnhip::DevBuf<int> rexp;
 };
 struct nnhip_model {
   std::unique_ptr<nnhip::Model> m;

@@ -178,6 +178,39 @@ def linear_path(ctx, x, codes, scales, b, path):
     return dy.numpy()
 
 
+def test_linear_w8a32_scratch_reuse():
+    """nnhip_linear_w8a32 on a fresh context, calls queued back to back with
+    nothing read in between: the context's scratch grows (after the stream
+    drains) from a small call to larger ones and is reused by a small one
+    again; every output equals the same call made alone on the oracle's
+    terms."""
+    c = nnhip.Context(0)
+    cases = [(16, 128, 64, 2), (192, 1024, 1024, 2), (64, 512, 4096, 3),
+             (192, 1024, 3072, 4), (32, 512, 512, 2)]
+    keep, arrays = [], []
+    try:
+        for i, (rows, K, N, path) in enumerate(cases):
+            rng = np.random.default_rng(100 + i)
+            x = rng.standard_normal((rows, K)).astype(np.float32)
+            w = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+            b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+            codes, scales = quantize_oracle(w)
+            dx, dc = c.array(x), c.array(np.ascontiguousarray(codes.T))
+            ds, db = c.array(scales), c.array(b)
+            dy = c.array(shape=(rows, N))
+            arrays += [dx, dc, ds, db, dy]
+            call("nnhip_linear_w8a32", c.h, dx.p, rows, K, dc.p, ds.p, db.p,
+                 N, dy.p, path)
+            keep.append((x, codes, scales, b, dy))
+        for i, (x, codes, scales, b, dy) in enumerate(keep):
+            want = dense_oracle(x, codes, scales, bias=b)
+            assert_rows_close(dy.numpy(), want, 1e-4, f"scratch reuse case {i}")
+    finally:
+        for a in arrays:
+            a.free()
+        c.close()
+
+
 @pytest.mark.parametrize("rows,K,N", LDS_SHAPES)
 def test_lds_gemm_matches_digit_gemm(ctx, rows, K, N):
     """The LDS-resident GEMM (digits formed in its prologue, path 3, or read
