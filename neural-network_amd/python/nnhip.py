@@ -47,7 +47,7 @@ class View(C.Structure):
 
 def view(arr, shape=None, strides=None, offset=0):
     """A View of DeviceArray `arr`: its own shape and row-major strides, or
-    the given ones (elements)."""
+    the given ones (elements).  The view keeps `arr` alive."""
     shape = tuple(arr.shape if shape is None else shape)
     if strides is None:
         strides, acc = [], 1
@@ -55,6 +55,8 @@ def view(arr, shape=None, strides=None, offset=0):
             strides.insert(0, acc)
             acc *= n
     v = View()
+    # the view holds its array: a view alone must not outlive the memory
+    v._arr = arr
     v.data = arr.p
     v.offset = offset
     v.rank = len(shape)

@@ -142,8 +142,8 @@ def test_matmul_matches_oracle_dense(ctx, M, K, N):
     assert np.abs(got - ex).max() <= 1e-5 * np.abs(a).max() * np.abs(b).max() * K
     # transposed operands (the reference's sgemm Trans cases) and a strided
     # output give the same values
-    _, va = strided(ctx, a, (1, 0))
-    _, vb = strided(ctx, b, (1, 0))
+    ta, va = strided(ctx, a, (1, 0))
+    tb, vb = strided(ctx, b, (1, 0))
     do2 = ctx.array(shape=(M, 2 * N))
     nnhip.call("nnhip_matmul_f32", ctx.h, va, vb,
                nnhip.view(do2, (M, N), (2 * N, 2)))
