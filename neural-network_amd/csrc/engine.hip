@@ -684,9 +684,13 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
                      (T <= 0.f || !sampling_filtered(V, top_k, top_p)) &&
                      dm.lm_tiles(B);
   if (tiles) bf.dtiles.alloc((size_t)B * k * nt);
-  if (T > 0.f) bf.qprob.alloc((size_t)B * k * V);
+  // sampled drafting from tile statistics keeps each step's logits; the
+  // draft probabilities are then formed where the accept step needs them
+  // (s.qlog) instead of written out at every step
+  const bool qlog = tiles && T > 0.f;
+  if (T > 0.f && !qlog) bf.qprob.alloc((size_t)B * k * V);
   bf.tstat.alloc((size_t)B * (k + 1) * kTstat);
-  bf.dlog.alloc((size_t)B * V);
+  bf.dlog.alloc((size_t)(qlog ? k : 1) * B * V);
   bf.tlog.alloc((size_t)B * (k + 1) * V);
   bf.stats.alloc((size_t)B * kSpecStats);
   NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
@@ -701,6 +705,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
 
   SpecState s{};
   s.cur = bf.cur.p; s.cand = bf.cand.p; s.qprob = bf.qprob.p;
+  if (qlog) s.qlog = bf.dlog.p;
   s.tstat = bf.tstat.p;
   if (tiles) { s.dtiles = bf.dtiles.p; s.nt = nt; s.tw = tw; }
   s.tlen = bf.tlen.p; s.dlen = bf.dlen.p; s.gen = bf.gen.p; s.cyc = bf.cyc.p;
@@ -744,14 +749,15 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
         dts.ld = (int64_t)k * nt;
         dts.T = T;
       }
+      float *dl = bf.dlog.p + (qlog ? (size_t)j * B * V : 0);
       if (j == 0)   // {catch-up token, cur} at dlen - 1, dlen
         dm.forward(&dc, 0, bf.pair.p, 2, B, 2, bf.dlen.p, -1, bf.active.p,
-                   d_need, bf.dlog.p, true, 0, &dts);
+                   d_need, dl, true, 0, &dts);
       else
         dm.forward(&dc, 0, bf.cand.p + (j - 1), k, B, 1, bf.dlen.p, j,
-                   bf.active.p, d_need, bf.dlog.p, false, 0, &dts, true);
-      if (tiles) launch_draft_sample_tiles(st, s, j, bf.dlog.p, V);
-      else launch_draft_sample(st, s, j, bf.dlog.p, V);
+                   bf.active.p, d_need, dl, false, 0, &dts, true);
+      if (tiles) launch_draft_sample_tiles(st, s, j, dl, V);
+      else launch_draft_sample(st, s, j, dl, V);
     }
     t.forward(&tc, 0, bf.cand.p, k, B, k + 1, bf.tlen.p, 0, bf.active.p,
               t_need, bf.tlog.p, false, 0, nullptr, false, bf.cur.p);

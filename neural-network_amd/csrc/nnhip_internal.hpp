@@ -514,7 +514,13 @@ struct NextRows {
 struct SpecState {
   int32_t *cur;        // [B] last committed token (generated.back())
   int32_t *cand;       // [B][k] draft candidates of this cycle
-  float *qprob;        // [B][k][V] draft probabilities (sampled mode)
+  float *qprob;        // [B][k][V] draft probabilities (sampled mode), or
+                       // null when qlog is set
+  // the drafting steps' logits [k][B][V] (step j, sequence b at row
+  // j*B + b): with the lm head's tile statistics (dtiles) they give every
+  // draft probability, which is then computed where it is needed instead
+  // of being written out at each step (sampled mode without top-k / top-p)
+  const float *qlog = nullptr;
   float *tstat;        // [B][k+1][kTstat] verify-row statistics (accept)
   int32_t *tlen;       // [B] target cache length
   int32_t *dlen;       // [B] draft cache length

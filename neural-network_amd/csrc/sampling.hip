@@ -605,6 +605,19 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
     return;
   }
   const float *row = logits + b * ldl;
+  if (s.qlog) {
+    // the probabilities stay implicit in the logits: only the draw
+    if (threadIdx.x < 64) {
+      const RowStats st = wave_tiles_stats(tl, s.nt);
+      if (threadIdx.x == 0) rst = st;
+    }
+    __syncthreads();
+    const int tok = tiles_sample(row, tl, s.nt, s.tw, s.V, s.T, rst,
+                                 uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+    if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
+    embed_next(s, b, j, tok, s_emb, s_red);
+    return;
+  }
   // this part's entries requested while the statistics are formed
   const int chunk = (s.V + kQParts - 1) / kQParts;
   const int v0 = part * chunk, v1 = min(s.V, v0 + chunk);
@@ -721,9 +734,13 @@ __global__ __launch_bounds__(kThreads) void target_stats_kernel(
 // statistics, q from the stored draft probabilities; then sample it, or p
 // when the residual sums to zero.  The residual is sampled unnormalised:
 // the discrete distribution normalises it.
+// qrow: the draft probabilities, or with qlrow set the draft logits whose
+// probabilities are (exp(l / T - qs.mx) * qs.rsum) * qs.rfs, the values the
+// drafting step would have written
 __device__ __forceinline__ int residual_sample(
     const float *__restrict__ qrow, const float *__restrict__ tlog_row,
-    RowStats tst, int V, float T, float u, Shared &sh) {
+    RowStats tst, int V, float T, float u, Shared &sh,
+    const float *__restrict__ qlrow = nullptr, RowStats qs = RowStats{}) {
   // two halves of the thread's entries, each with its loads in flight
   constexpr int kHalf = kPer / 2;
   float loc = 0.f;
@@ -734,14 +751,15 @@ __device__ __forceinline__ int residual_sample(
     for (int i = 0; i < kHalf; ++i) {
       const int v = min((int)threadIdx.x + (hf * kHalf + i) * kThreads, V - 1);
       xt[i] = tlog_row[v];
-      xq[i] = qrow[v];
+      xq[i] = qlrow ? qlrow[v] : qrow[v];
     }
 #pragma unroll
     for (int i = 0; i < kHalf; ++i) {
       const int v = (int)threadIdx.x + (hf * kHalf + i) * kThreads;
       if (v < V) {
         const float p = prob_of(xt[i], v, T, tst);
-        const float r = fmaxf(0.0f, p - xq[i]);
+        const float q = qlrow ? (expf(scaled(xq[i], T) - qs.mx) * qs.rsum) * qs.rfs : xq[i];
+        const float r = fmaxf(0.0f, p - q);
         sh.prow[la(v)] = r;
         loc += r;
       }
@@ -781,6 +799,22 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   auto argmax_of = [&](int j) {
     return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * kTstat + 3]);
   };
+  // implicit draft probabilities (s.qlog): each drafting step's statistics
+  // from its lm-head tiles, one wave a step, as the drafting step formed them
+  __shared__ RowStats qst[kMaxLookahead];
+  const bool qimp = s.qlog != nullptr && !greedy;
+  if (qimp) {
+    const int w = threadIdx.x >> 6;
+    for (int j = w; j < M; j += kWaves) {
+      const RowStats st = wave_tiles_stats(s.dtiles + ((int64_t)b * k + j) * s.nt, s.nt);
+      if ((threadIdx.x & 63) == 0) qst[j] = st;
+    }
+    __syncthreads();
+  }
+  auto qlrow = [&](int j) { return s.qlog + ((int64_t)j * s.B + b) * V; };
+  auto q_of = [&](float l, int j) {
+    return (expf(scaled(l, s.T) - qst[j].mx) * qst[j].rsum) * qst[j].rfs;
+  };
   // the candidates' target logits and draft probabilities, the first kPre
   // positions requested at once (their loop is unrolled so that the
   // prefetched values stay in registers)
@@ -792,8 +826,13 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
       if (j < M) {
         const int c = s.cand[b * k + j];
         lc[j] = tlogits[((int64_t)b * tr + j) * V + c];
-        qcp[j] = s.qprob[((int64_t)b * k + j) * V + c];
+        qcp[j] = qimp ? qlrow(j)[c] : s.qprob[((int64_t)b * k + j) * V + c];
       }
+    }
+    if (qimp) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j)
+        if (j < M) qcp[j] = q_of(qcp[j], j);
     }
   }
   // accept test of position j given its candidate's p and q
@@ -816,7 +855,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   for (int j = kPre; j < M && rej < 0; ++j) {
     const int c = s.cand[b * k + j];
     const float lj = greedy ? 0.f : tlogits[((int64_t)b * tr + j) * V + c];
-    const float qc = greedy ? 0.f : s.qprob[((int64_t)b * k + j) * V + c];
+    const float qc = greedy ? 0.f
+                     : qimp ? q_of(qlrow(j)[c], j)
+                            : s.qprob[((int64_t)b * k + j) * V + c];
     if (!test(j, c, lj, qc)) { rej = j; break; }
     if (threadIdx.x == 0) out[nout] = c;
     ++nout;
@@ -829,8 +870,10 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     if (greedy) {
       tok = argmax_of(rej);
     } else {
-      tok = residual_sample(s.qprob + ((int64_t)b * k + rej) * V, row,
-                            stats_of(rej), V, s.T, u, sh);
+      tok = qimp ? residual_sample(nullptr, row, stats_of(rej), V, s.T, u, sh,
+                                   qlrow(rej), qst[rej])
+                 : residual_sample(s.qprob + ((int64_t)b * k + rej) * V, row,
+                                   stats_of(rej), V, s.T, u, sh);
     }
     catch_tok = tok;
   } else if (gen < s.max_new) {
@@ -976,12 +1019,12 @@ void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
 
 void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
                                const float *logits, int64_t ldl) {
-  NNHIP_REQUIRE(s.dtiles && (s.T <= 0.f || s.qprob) && s.nt <= kThreads &&
+  NNHIP_REQUIRE(s.dtiles && (s.T <= 0.f || s.qprob || s.qlog) && s.nt <= kThreads &&
                     s.tw <= kThreads && s.V <= kMaxV,
                 kErrArg, "draft sample: tile statistics missing or too many tiles");
   NNHIP_REQUIRE(s.T <= 0.f || !sampling_filtered(s.V, s.top_k, s.top_p), kErrArg,
                 "draft sample: tile statistics cannot apply top-k / top-p");
-  hipLaunchKernelGGL(draft_sample_tiles_kernel, dim3(s.B, kQParts),
+  hipLaunchKernelGGL(draft_sample_tiles_kernel, dim3(s.B, s.qlog ? 1 : kQParts),
                      dim3(kThreads), 0, st, s, j, logits, ldl);
   NNHIP_CHECK(hipGetLastError());
 }
