@@ -243,10 +243,13 @@ __device__ __forceinline__ float groups_sum(float v) {
   return v + __shfl_xor(v, 32, kWave);
 }
 
-// KV-cache rows of a launch whose rows exceed the L2 (the verify step's)
-// are streamed: non-temporal loads, so that they do not evict the weights
-// and activations held in L2 between launches.  Smaller caches (the
-// draft's, re-read by each draft step) are loaded normally and stay in L2.
+// KV-cache rows of a launch whose rows (counted up to its key bound) exceed
+// the L2s are streamed: non-temporal loads, so that they do not evict the
+// weights and activations held in L2 between launches.  At 32 sequences
+// both models' launches stream (the draft's too, although each draft step
+// re-reads its cache: loading those rows normally, so that the memory-side
+// cache could keep them between steps, measured 2.4% slower).  Launches
+// within the L2s (short contexts, batch 1) load normally.
 typedef float nnhip_f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld_stream4(const float *p) {
   const nnhip_f4 v = __builtin_nontemporal_load(reinterpret_cast<const nnhip_f4 *>(p));
