@@ -72,6 +72,11 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * rows on (default 128; process-wide).
  * "limb_k8": the digit-plane GEMM splits K over 8 waves from this K on
  * (default 1024; process-wide).
+ * "o_head_digits": 1 = for 64-wide heads the merged attention writes the
+ * output projection's digit planes itself, one exponent per (row, head),
+ * and the digit-plane GEMM scales each head's exact total by its own
+ * exponent (default); 0 = act_quant digitises the context rows with one
+ * exponent per row (process-wide).
  * "o_limb_rows": after the merged attention, the output projection of up
  * to this many rows runs as act_quant + digit-plane GEMM, taller inputs on
  * the LDS GEMM digitising the context rows (default 256; process-wide).

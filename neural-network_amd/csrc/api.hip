@@ -91,6 +91,7 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
       REQ(value >= 0, "o_limb_rows must be >= 0");
       nnhip::g_o_limb_rows = value;
     }
+    else if (std::strcmp(key, "o_head_digits") == 0) nnhip::g_o_head_digits = value != 0;
     else if (std::strcmp(key, "kv_stream") == 0) {
       REQ(value >= 0 && value <= 2, "kv_stream must be 0, 1 or 2");
       nnhip::g_kv_stream = value;

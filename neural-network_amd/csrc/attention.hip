@@ -329,7 +329,8 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
     const float *__restrict__ q, KvSrc kv, int S, int H, int Hkv, int cap,
     const int32_t *__restrict__ base, int off,
     const int32_t *__restrict__ active, int nsplit, int nqb, int kps,
-    float qscale, float *__restrict__ part, float *__restrict__ out, int nt) {
+    float qscale, float *__restrict__ part, float *__restrict__ out, int nt,
+    int8_t *__restrict__ hlimbs, int mpad, int *__restrict__ hexp) {
   constexpr int D = DL * 8;
   constexpr int NQ4 = D / 4, KPI = kWave / NQ4;   // PV: key rows per wave op
   constexpr int TPV = (kChunk + KPI - 1) / KPI;   // PV keys per lane
@@ -568,7 +569,27 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
         as += reinterpret_cast<const float *>(s_buf4[u])[i * D + dd] * f;
       }
       const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-      out[(row0 + i) * E + h * D + dd] = as * inv;
+      const float v = as * inv;
+      out[(row0 + i) * E + h * D + dd] = v;
+      if (D == kWave && hlimbs) {
+        // the output projection's digits of this head's 64 entries of the
+        // row (one per lane of this wave): the exponent of the row's head
+        // chunk, then X = rint(v 2^e) in balanced base-256 digits (the
+        // act_quant_kernel rule applied per head), at k = h D + dd
+        const float mx = wave_max_all(fabsf(v));
+        const int e = digit_exponent(mx);
+        const int X = (int)rintf(ldexpf(v, e));
+        const int lo = (int)(int8_t)(X & 0xff);
+        const int t1 = (X - lo) >> 8;
+        const int md = (int)(int8_t)(t1 & 0xff);
+        const int hi = (t1 - md) >> 8;
+        const int64_t o = mfma_operand_offset((int)(row0 + i), h * D + dd, E);
+        const int64_t plane = (int64_t)mpad * E;
+        hlimbs[o] = (int8_t)hi;
+        hlimbs[plane + o] = (int8_t)md;
+        hlimbs[2 * plane + o] = (int8_t)lo;
+        if (dd == 0) hexp[(row0 + i) * H + h] = e;
+      }
     }
     return;
   }
@@ -884,7 +905,8 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
                       int S, int H, int Hkv, int D, int cap,
                       const int32_t *base, int off, const int32_t *active,
                       int max_keys, float *part, int64_t part_elems,
-                      float *out, int8_t *limbs, int mpad, int *rexp) {
+                      float *out, int8_t *limbs, int mpad, int *rexp,
+                      int *hexp) {
   NNHIP_REQUIRE(D % 8 == 0 && D <= kMaxD, kErrArg,
                 "attention: head dim must be a multiple of 8 and <= 64");
   NNHIP_REQUIRE(!kv.q8 || (kv.ks && kv.vs), kErrArg,
@@ -904,7 +926,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
                             (g_kv_stream == 1 && kv_bytes > kL2StreamBytes));
   if (attention_merged(D, max_keys)) {
     // one workgroup per (head, sequence, query block); its waves are the key
-    // splits, merged in LDS, and the context rows are written directly
+    // splits, merged in LDS, and the context rows are written directly, with
+    // hexp also their digits per head (exponent per row and head)
+    NNHIP_REQUIRE(!hexp || (limbs && D == kWave && (H * D) % 128 == 0 && B * S <= mpad),
+                  kErrArg, "attention: head digits need D == 64, H*D % 128 == 0");
+    int8_t *hl = hexp ? limbs : nullptr;
     int kps = (max_keys + kMergedWaves - 1) / kMergedWaves;
     kps = (kps + kChunk - 1) / kChunk * kChunk;
     dim3 grid(1, H, B * nqb);
@@ -912,11 +938,11 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   if (kv.q8)                                                                  \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, W, true>), grid, dim3(kWave * W),  \
                        0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
-                       kps, qscale, nullptr, out, nt);                          \
+                       kps, qscale, nullptr, out, nt, hl, mpad, hexp);         \
   else                                                                        \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, W, false>), grid, dim3(kWave * W), \
                        0, st, q, kv, S, H, Hkv, cap, base, off, active, W, nqb, \
-                       kps, qscale, nullptr, out, nt)
+                       kps, qscale, nullptr, out, nt, hl, mpad, hexp)
 #define NNHIP_ATTN_D(SQP, W)                                                  \
   if (D == 32) { NNHIP_ATTN(SQP, 4, W); } else { NNHIP_ATTN(SQP, 8, W); }
     // many-query rows hold many registers (one workgroup of 8 waves per CU):
@@ -943,11 +969,12 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   if (kv.q8)                                                                  \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, true>), grid, dim3(kWave), 0,  \
                        st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
-                       nqb, kps, qscale, part, nullptr, nt);                  \
+                       nqb, kps, qscale, part, nullptr, nt, nullptr, 0,       \
+                       nullptr);                                              \
   else                                                                        \
     hipLaunchKernelGGL((attn_kernel<SQP, DL, 1, false>), grid, dim3(kWave), 0, \
                        st, q, kv, S, H, Hkv, cap, base, off, active, nsplit,  \
-                       nqb, kps, qscale, part, nullptr, nt)
+                       nqb, kps, qscale, part, nullptr, nt, nullptr, 0, nullptr)
 #define NNHIP_ATTN_D(SQP)                                                     \
   switch (D / 8) {                                                            \
     case 1: { NNHIP_ATTN(SQP, 1); } break;                                    \

@@ -11,6 +11,7 @@ namespace nnhip {
 int g_lds_min_rows = 128;
 int g_o_limb_rows = 256;
 int g_gemv_down_rows = 64;
+int g_o_head_digits = 1;
 
 namespace {
 
@@ -284,6 +285,8 @@ void Model::reserve(int rows, int lrows, int max_keys) {
     ws.mpad = round_up(r, 64);
     ws.limbs.alloc((size_t)kLimbs * ws.mpad * std::max(d, F));
     ws.rexp.alloc(ws.mpad);
+    ws.hexp.alloc((size_t)ws.mpad * H);
+    NNHIP_CHECK(hipMemsetAsync(ws.hexp.p, 0, ws.hexp.bytes(), ctx->stream));
     ws.ids.alloc(r);
     ws.zeros.alloc(r);
     NNHIP_CHECK(hipMemsetAsync(ws.zeros.p, 0, (size_t)r * 4, ctx->stream));
@@ -487,12 +490,23 @@ void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
     // GEMM digitising ctx in its prologue), taller inputs (prefill) use the
     // latter.  Long contexts: split attention + combine, which also writes
     // ctx's digits.
+    // Short contexts with 64-wide heads: the merged attention writes the
+    // output projection's digits itself, one exponent per (row, head), and
+    // the digit-plane GEMM scales each head's exact total by its own
+    // exponent (no act_quant launch).
     const bool merged = attention_merged(D, max_keys);
     const bool lo = !merged && (use_lds(ly.o, R) || use_limbs(ly.o, R));
+    const bool hd = merged && g_o_head_digits && R <= g_o_limb_rows &&
+                    use_limbs(ly.o, R) && D == 64 && d % 128 == 0 &&
+                    d / 64 <= kMaxHxChunks;
     launch_attention(st, ws.qrot.p, kvs, B, S, H, H, D, kv->cap, bp, off,
                      active, max_keys, ws.part.p, ws.part_elems, ws.ctx.p,
-                     lo ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p);
-    if (merged && R <= g_o_limb_rows && use_limbs(ly.o, R))
+                     lo || hd ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p,
+                     hd ? ws.hexp.p : nullptr);
+    if (hd)
+      launch_gemm_limb_hx(st, ws.limbs.p, ws.mpad, ws.hexp.p, R, d, d, ly.o.qs.p,
+                          ly.o.s.p, ly.o.b.p, ws.x.p, d, ws.h.p, d, kEpiResid);
+    else if (merged && R <= g_o_limb_rows && use_limbs(ly.o, R))
       linear(ly.o, ws.ctx.p, d, R, false, ws.x.p, d, ws.h.p, d, kEpiResid);
     else if (merged && ly.o.quant && ly.o.qs.p && R >= kLimbMinRows &&
              gemm_lds_supports(R, d, d))

@@ -43,6 +43,7 @@ struct Workspace {
   DevBuf<long long> tot;   // [rows][d] split-K totals, kept zeroed
   DevBuf<int8_t> limbs;
   DevBuf<int> rexp;
+  DevBuf<int> hexp;        // [mpad][H] per-(row, head) digit exponents
   DevBuf<int32_t> ids, zeros;
   int mpad = 0;
   int64_t part_elems = 0;

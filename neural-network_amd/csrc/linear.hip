@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(
 // are summed across waves with LDS integer atomics (exact, order-free).
 // Both operands are stored in the MFMA operand layout (mfma_operand_offset):
 // within each 128-wide K chunk, lane (r, h) supplies bytes
-// [h*64 + s*16, h*64 + s*16 + 16) of its row for MFMA step s, identically for
+// [s*32 + h*16, s*32 + h*16 + 16) of its row for MFMA step s, identically for
 // the digit operand and the weight operand, so each MFMA contracts matching
 // k indices whatever order the hardware assigns to a lane's 16 bytes, and
 // every operand load of a wave is one contiguous 1 KB block.
@@ -324,7 +324,13 @@ constexpr int kGemmMT = 32;
 
 // NSUB 32-column sub-tiles per workgroup (tile 32 x 32*NSUB); NW waves
 // split K (chunks w, w + NW, ...).
-template <int NSUB, int NW = 4>
+// HX: the digits carry one exponent per 64-wide K chunk (rexp is then
+// [M][K/64], the merged attention's per-head exponents): a 128-wide chunk's
+// MFMA steps 0-1 and 2-3 are two such chunks (mfma_operand_offset), each
+// chunk's exact integer total is scaled by its own 2^-e in double, and the
+// waves' sums are added in wave order through LDS (deterministic); one
+// rounding to float, then the bias / residual epilogue.
+template <int NSUB, int NW = 4, bool HX = false>
 __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_limb_kernel(
     const int8_t *__restrict__ limbs, int mpad, const int *__restrict__ rexp,
     int M, int K, int N, const int8_t *__restrict__ wq,
@@ -333,7 +339,10 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
     int64_t ldy, int epi, int ntm, int ntn, RopeArgs ra) {
   constexpr int NT = 32 * NSUB;
   constexpr int kThr = 64 * NW;
+  static_assert(!HX || NSUB == 1, "chunk exponents with 32-column tiles");
   __shared__ int red[kLimbs][kGemmMT][NT];
+  __shared__ double dred[HX ? NW : 1][kGemmMT][HX ? NT : 1];
+  __shared__ int s_hx[HX ? kGemmMT * kMaxHxChunks : 1];
   const int T = ntm * ntn;
   const int per = (T + 7) / 8;
   const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
@@ -362,9 +371,17 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
   for (int it = 0; it < IT; ++it) {
     const int m = m0 + ((int)threadIdx.x + it * kThr) / (NT / 2);
     const bool ok = m < M && e_cols;
-    e_ex[it] = ok ? rexp[m] : 0;
+    e_ex[it] = ok && !HX ? rexp[m] : 0;
     e_rs[it][0] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n] : 0.f;
     e_rs[it][1] = ok && epi == kEpiResid ? resid[(int64_t)m * ldr + e_n + 1] : 0.f;
+  }
+  const int nhx = K / 64;
+  if constexpr (HX) {
+    // the tile's chunk exponents (rows past M: 0)
+    for (int i = threadIdx.x; i < kGemmMT * nhx; i += kThr) {
+      const int rr = i / nhx, cc = i % nhx;
+      s_hx[i] = m0 + rr < M ? rexp[(int64_t)(m0 + rr) * nhx + cc] : 0;
+    }
   }
   __syncthreads();
 
@@ -401,10 +418,44 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
         for (int l = 0; l < kLimbs; ++l)
           acc[t][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[l][s], f.b[t][s], acc[t][l], 0, 0, 0);
   };
+  if constexpr (HX) {
+    // lane holds column (lane & 31) of rows (j >> 2) * 8 + h * 4 + (j & 3)
+    double dsum[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dsum[j] = 0.0;
+    for (int c = cb + w; c < ce; c += NW) {
+      Frag f;
+      load(c, f);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        v16i a3[kLimbs];
+#pragma unroll
+        for (int l = 0; l < kLimbs; ++l) a3[l] = v16i{};
+#pragma unroll
+        for (int s = 2 * half; s < 2 * half + 2; ++s)
+#pragma unroll
+          for (int l = 0; l < kLimbs; ++l)
+            a3[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[l][s], f.b[0][s], a3[l], 0, 0, 0);
+        const int hc = 2 * c + half;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int row = (j >> 2) * 8 + h * 4 + (j & 3);
+          // the chunk's exact total (|digit sums| < 2^21), then its scale
+          const double tot = fma((double)a3[0][j], 65536.0,
+                                 fma((double)a3[1][j], 256.0, (double)a3[2][j]));
+          dsum[j] += ldexp(tot, -s_hx[row * nhx + hc]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      dred[w][(j >> 2) * 8 + h * 4 + (j & 3)][r] = dsum[j];
+    __syncthreads();
+  }
   // ping-pong over the wave's chunks w, w+NW, w+2NW, ...: the loads of the
   // next chunk are in flight while the current chunk's MFMAs run
   Frag fa, fb;
-  int c = cb + w;
+  int c = HX ? ce : cb + w;
   if (c < ce) load(c, fa);
   while (c < ce) {
     if (c + NW < ce) load(c + NW, fb);
@@ -415,7 +466,7 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
     mma(fb);
     c += NW;
   }
-  if (cb + w < ce) {
+  if (!HX && cb + w < ce) {
 #pragma unroll
     for (int t = 0; t < NSUB; ++t)
 #pragma unroll
@@ -426,7 +477,7 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
           atomicAdd(&red[l][row][t * 32 + r], acc[t][l][j]);
         }
   }
-  __syncthreads();
+  if constexpr (!HX) __syncthreads();
   // epilogue: thread -> (row, column pair)
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
@@ -435,21 +486,31 @@ __global__ __launch_bounds__(64 * NW, NSUB == 1 && NW == 4 ? 2 : 1) void gemm_li
     const int m = m0 + row;
     if (m >= M) continue;
     const int c0 = 2 * cp;
-    long long tot[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-      tot[e] = (long long)red[0][row][c0 + e] * 65536LL +
-               (long long)red[1][row][c0 + e] * 256LL +
-               (long long)red[2][row][c0 + e];
     const int n = n0 + c0;
-    if (epi == kEpiTotals) {
-      long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
-      yt[0] = tot[0]; yt[1] = tot[1];
-      continue;
-    }
     float v[2];
-    v[0] = dequant_epilogue(tot[0], e_ex[it], e_sc0, e_bi0);
-    v[1] = dequant_epilogue(tot[1], e_ex[it], e_sc1, e_bi1);
+    if constexpr (HX) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        double dt = 0.0;
+#pragma unroll
+        for (int u = 0; u < NW; ++u) dt += dred[u][row][c0 + e];
+        v[e] = fmaf((float)dt, e == 0 ? e_sc0 : e_sc1, e == 0 ? e_bi0 : e_bi1);
+      }
+    } else {
+      long long tot[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        tot[e] = (long long)red[0][row][c0 + e] * 65536LL +
+                 (long long)red[1][row][c0 + e] * 256LL +
+                 (long long)red[2][row][c0 + e];
+      if (epi == kEpiTotals) {
+        long long *yt = reinterpret_cast<long long *>(y) + (int64_t)m * ldy + n;
+        yt[0] = tot[0]; yt[1] = tot[1];
+        continue;
+      }
+      v[0] = dequant_epilogue(tot[0], e_ex[it], e_sc0, e_bi0);
+      v[1] = dequant_epilogue(tot[1], e_ex[it], e_sc1, e_bi1);
+    }
     if (epi == kEpiSwiGLU) {
       y[(int64_t)m * ldy + n / 2] = swiglu_pair(v[0], v[1]);
     } else if (epi == kEpiRope) {
@@ -845,7 +906,7 @@ __global__ __launch_bounds__(256) void swizzle_rows_kernel(
   const int c = (int)(q % nch);
   const int64_t t = q / nch;
   const int64_t row = t * 32 + (lane & 31);
-  const int col = c * 128 + (lane >> 5) * 64 + s * 16;
+  const int col = c * 128 + s * 32 + (lane >> 5) * 16;
   if (inverse)
     *reinterpret_cast<v4i *>(dst + row * K + col) =
         *reinterpret_cast<const v4i *>(src + p * 16);
@@ -1068,6 +1129,29 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
   NNHIP_CHECK(hipGetLastError());
 }
 
+void launch_gemm_limb_hx(hipStream_t st, const int8_t *limbs, int mpad,
+                         const int *hexp, int rows, int K, int N,
+                         const int8_t *wq, const float *scale, const float *bias,
+                         const float *resid, int64_t ldr, float *y, int64_t ldy,
+                         int epi) {
+  NNHIP_REQUIRE(K % 128 == 0 && K / 64 <= kMaxHxChunks && N % 64 == 0 && rows > 0,
+                kErrArg, "gemm_limb_hx: K % 128 == 0, K <= 2048, N % 64 == 0");
+  NNHIP_REQUIRE(limbs && hexp && mpad % 64 == 0 && rows <= mpad, kErrArg,
+                "gemm_limb_hx: digit planes missing or bad mpad");
+  NNHIP_REQUIRE(epi == kEpiBias || epi == kEpiResid, kErrArg,
+                "gemm_limb_hx: bias or residual epilogue only");
+  const int ntm = (rows + kGemmMT - 1) / kGemmMT;
+  const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
+  if (K >= g_limb_k8)
+    hipLaunchKernelGGL((gemm_limb_kernel<1, 8, true>), dim3(8 * per), dim3(512), 0, st,
+                       limbs, mpad, hexp, rows, K, N, wq, scale, bias, resid,
+                       ldr, y, ldy, epi, ntm, ntn, RopeArgs{});
+  else
+    hipLaunchKernelGGL((gemm_limb_kernel<1, 4, true>), dim3(8 * per), dim3(256), 0, st,
+                       limbs, mpad, hexp, rows, K, N, wq, scale, bias, resid,
+                       ldr, y, ldy, epi, ntm, ntn, RopeArgs{});
+  NNHIP_CHECK(hipGetLastError());
+}
 
 int gemm_lds_tile_width(int K) {
   // 16 waves of 32 columns over K/KS each: 128-column blocks when KS = 4

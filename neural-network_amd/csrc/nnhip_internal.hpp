@@ -233,15 +233,17 @@ __device__ inline float swiglu_pair(float g, float u) {
 
 // MFMA operand layout of an int8 [R][K] matrix (R % 32 == 0, K % 128 == 0):
 // element (m, k) lives at
-//   [m/32][k/128][(k%64)/16][lane = ((k%128)/64)*32 + m%32][k%16],
+//   [m/32][k/128][(k%128)/32][lane = ((k%32)/16)*32 + m%32][k%16],
 // so the 16 bytes one lane feeds to one v_mfma_i32_32x32x32_i8 step are
-// contiguous and a wave's 64 lanes read one contiguous 1 KB block.  Used for
-// the weight codes of the MFMA path and for the activation digits (one
-// plane of R*K bytes per digit).
+// contiguous, a wave's 64 lanes read one contiguous 1 KB block, and step s
+// of a 128-wide chunk contracts the 32 consecutive k of [32 s, 32 s + 32)
+// (two steps cover one 64-wide attention head).  Used for the weight codes
+// of the MFMA path and for the activation digits (one plane of R*K bytes
+// per digit).
 __host__ __device__ inline int64_t mfma_operand_offset(int m, int k, int K) {
   const int nch = K / 128;
   const int c = k >> 7, kk = k & 127;
-  const int h = kk >> 6, s = (kk & 63) >> 4, byte = kk & 15;
+  const int h = (kk >> 4) & 1, s = kk >> 5, byte = kk & 15;
   const int lane = h * 32 + (m & 31);
   return ((((int64_t)(m >> 5) * nch + c) * 4 + s) * 64 + lane) * 16 + byte;
 }
@@ -287,6 +289,8 @@ extern int g_ln_split;   // LayerNorm rows of 512 / 1024 over 2 / 4 waves
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
 extern int g_gemv_down_rows; // down projection on the GEMV up to this many rows
+extern int g_o_head_digits; // 1 = the merged attention writes the output
+                            // projection's digits per head (64-wide heads)
 extern int g_o_limb_rows; // output projection after merged attention: digit
                           // planes + digit-plane GEMM up to this many rows
 extern int g_kv_stream;  // attention: non-temporal fp32 KV loads (0 never,
@@ -382,6 +386,15 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                       const int8_t *wq, const float *scale, const float *bias,
                       const float *resid, int64_t ldr, float *y, int64_t ldy,
                       int epi, const RopeArgs *ra = nullptr);
+// the same GEMM over digit planes with one exponent per 64-wide K chunk
+// (hexp [rows][K/64], as the merged attention writes them; K <= 2048), bias
+// or residual epilogue
+constexpr int kMaxHxChunks = 32;
+void launch_gemm_limb_hx(hipStream_t st, const int8_t *limbs, int mpad,
+                         const int *hexp, int rows, int K, int N,
+                         const int8_t *wq, const float *scale, const float *bias,
+                         const float *resid, int64_t ldr, float *y, int64_t ldy,
+                         int epi);
 // QuantizedDense ctor (quantization.cpp:36-86) on rows of w [N][K]: one
 // scale per row = max|w| / max_q (1 when 0), codes clamp(round(w / scale),
 // +-max_q) one per byte; max_q 127 (bits 8, INT8) or 7 (bits 4, INT4)
@@ -438,13 +451,15 @@ struct KvSrc {
 // true when launch_attention writes the context rows without the combine
 // kernel (and so without digit planes)
 bool attention_merged(int D, int max_keys);
-// returns whether the digit planes were written
+// returns whether the digit planes (one exponent per row, rexp) were
+// written; with hexp the merged attention writes the rows' digit planes with
+// one exponent per (row, head) instead, hexp [rows][H] (D == 64)
 bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
                       int S, int H, int Hkv, int D, int cap,
                       const int32_t *base, int off, const int32_t *active,
                       int max_keys, float *part, int64_t part_elems,
                       float *out, int8_t *limbs = nullptr, int mpad = 0,
-                      int *rexp = nullptr);
+                      int *rexp = nullptr, int *hexp = nullptr);
 int64_t attention_partial_elems(int B, int S, int H, int D, int max_keys);
 void launch_layernorm(hipStream_t st, const float *h, int rows, int d,
                       const float *g, const float *b, float *y,

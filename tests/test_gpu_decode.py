@@ -133,6 +133,33 @@ def test_forward_wide_vs_oracle(ctx):
     gm.free()
 
 
+# 64-wide heads, the width the output projection's per-head digits need
+HEADS = dict(vocab=512, d=512, H=8, F=1024, L=2)
+
+
+@pytest.mark.parametrize("B,S", [(32, 1), (32, 6), (4, 40)])
+def test_forward_head_digits_vs_oracle(ctx, B, S):
+    """Rows of 64-wide heads after the merged attention (the drafting and
+    verify shapes): the attention writes the output projection's digit
+    planes with one exponent per (row, head) and the digit-plane GEMM scales
+    each head's exact total by its own exponent.  Against the oracle's
+    forward (layer.cpp:1159-1216) within 1e-4 of a row, and against the
+    path with one exponent per row (act_quant; option o_head_digits = 0)."""
+    om, gm, _ = build(ctx, HEADS, 11, True, std=0.03)
+    rng = np.random.default_rng(B * 100 + S)
+    ids = rng.integers(0, 512, (B, S)).astype(np.int32)
+    got = gm.forward(ids)
+    ctx.set_option("o_head_digits", 0)
+    try:
+        per_row = gm.forward(ids)
+    finally:
+        ctx.set_option("o_head_digits", 1)
+    for b in range(B):
+        assert_rows_close(got[b], om.forward(ids[b]), 1e-4, f"forward b={b}")
+        assert_rows_close(got[b], per_row[b], 1e-5, f"per-row digits b={b}")
+    gm.free()
+
+
 @pytest.mark.parametrize("quant", [False, True])
 def test_forward_cache_truncate_vs_oracle(ctx, quant):
     om, gm, _ = build(ctx, TOY_T, 4, quant, std=0.05)
