@@ -252,17 +252,17 @@ def verify_step(ctx, t, q8=False):
 CYCLE_GEMMS = [
     # name, rows, K, N, path, kernel family, launches per cycle
     ("draft qkv", 32, 512, 1536, 8, "gemm_limb_kernel", 16),
-    ("draft o", 32, 512, 512, 8, "gemm_limb_kernel", 16),
+    ("draft o", 32, 512, 512, 9, "gemm_limb_kernel", 16),
     ("draft gate/up", 32, 512, 4096, 8, "gemm_limb_kernel", 16),
     ("draft down", 32, 2048, 512, 1, "gemv_kernel", 16),
     ("draft lm head", 32, 512, 32000, 6, "gemm_lds_kernel", 4),
     ("draft qkv (catch-up)", 64, 512, 1536, 8, "gemm_limb_kernel", 4),
-    ("draft o (catch-up)", 64, 512, 512, 8, "gemm_limb_kernel", 4),
+    ("draft o (catch-up)", 64, 512, 512, 9, "gemm_limb_kernel", 4),
     ("draft gate/up (catch-up)", 64, 512, 4096, 8, "gemm_limb_kernel", 4),
     ("draft down (catch-up)", 64, 2048, 512, 1, "gemv_kernel", 4),
     ("draft lm head (catch-up)", 32, 512, 32000, 6, "gemm_lds_kernel", 1),
     ("verify qkv", 192, 1024, 3072, 7, "gemm_lds_kernel", 12),
-    ("verify o", 192, 1024, 1024, 8, "gemm_limb_kernel", 12),
+    ("verify o", 192, 1024, 1024, 9, "gemm_limb_kernel", 12),
     ("verify gate/up", 192, 1024, 8192, 7, "gemm_lds_kernel", 12),
     ("verify down", 192, 4096, 1024, 8, "gemm_limb_kernel", 12),
     ("verify lm head", 192, 1024, 32000, 6, "gemm_lds_kernel", 1),
@@ -272,10 +272,12 @@ CYCLE_GEMMS = [
 def gemm_bytes(rows, K, N, path):
     """Algorithmic bytes of one GEMM launch: int8 codes, fp32 scale and bias
     per column, the activations as read (three int8 digit planes and an
-    exponent per row, or fp32 rows for the GEMV), fp32 outputs written (tile
+    exponent per row -- per 64-wide K chunk for path 9, the output
+    projection -- or fp32 rows for the GEMV), fp32 outputs written (tile
     statistics instead of logits are not counted: the logits are written
     too)."""
-    act = rows * K * 4 if path in (1, 3) else rows * (3 * K + 4)
+    exps = 4 * (K // 64) if path == 9 else 4
+    act = rows * K * 4 if path in (1, 3) else rows * (3 * K + exps)
     return N * K + 8 * N + act + rows * N * 4
 
 

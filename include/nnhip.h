@@ -438,7 +438,8 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V,
  * digit split included), 5 = LDS GEMM with LayerNorm in its prologue,
  * 6 = LDS GEMM over digit planes made once, with the lm head's tile
  * softmax statistics (K of 512 or 1024); the GEMM alone over digit planes
- * made once: 7 = LDS GEMM, 8 = digit-plane GEMM. */
+ * made once: 7 = LDS GEMM, 8 = digit-plane GEMM, 9 = digit-plane GEMM with
+ * one exponent per 64-wide K chunk (the output projection's; K <= 2048). */
 int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
                        int iters, int nbuf, float *ms);
 /* One TransformerDecoder::forward (layer.cpp:1159-1216) of m over B

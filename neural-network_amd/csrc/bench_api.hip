@@ -167,11 +167,13 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     nnhip::DevBuf<float> g1(K), b0(K);
     nnhip::launch_fill(st, g1.p, K, 1.f);
     nnhip::launch_fill(st, b0.p, K, 0.f);
-    NNHIP_REQUIRE(path >= 1 && path <= 8, nnhip::kErrArg, "nnhip_bench_linear: unknown path");
+    NNHIP_REQUIRE(path >= 1 && path <= 9, nnhip::kErrArg, "nnhip_bench_linear: unknown path");
     NNHIP_REQUIRE(path <= 2 || path >= 8 || nnhip::gemm_lds_supports(rows, K, N),
                   nnhip::kErrArg, "nnhip_bench_linear: shape not supported by the LDS GEMM");
-    NNHIP_REQUIRE(path != 8 || (K % 128 == 0 && N % 64 == 0), nnhip::kErrArg,
+    NNHIP_REQUIRE((path != 8 && path != 9) || (K % 128 == 0 && N % 64 == 0), nnhip::kErrArg,
                   "nnhip_bench_linear: the digit-plane GEMM needs K % 128 == 0, N % 64 == 0");
+    NNHIP_REQUIRE(path != 9 || K / 64 <= nnhip::kMaxHxChunks, nnhip::kErrArg,
+                  "nnhip_bench_linear: per-chunk exponents need K <= 2048");
     // path 6: digit planes prepared once, then the GEMM alone with the lm
     // head's tile statistics (T = 1)
     const int tw = nnhip::gemm_lds_tile_width(K);
@@ -183,9 +185,25 @@ int nnhip_bench_linear(nnhip_ctx *ctx, int rows, int K, int N, int path,
     tsa.out = tstat.p; tsa.ld = ntile; tsa.T = 1.f;
     if (path >= 6)
       nnhip::launch_act_quant(st, x.p, K, rows, K, limbs.p, mpad, rexp.p);
+    // path 9: the output projection's GEMM, one exponent per 64-wide K chunk
+    // (each row's exponent repeated over its chunks)
+    nnhip::DevBuf<int> hexp(path == 9 ? (size_t)mpad * (K / 64) : 0);
+    if (path == 9) {
+      std::vector<int> re(mpad), he((size_t)mpad * (K / 64));
+      NNHIP_CHECK(hipMemcpyAsync(re.data(), rexp.p, (size_t)mpad * 4,
+                                 hipMemcpyDeviceToHost, st));
+      NNHIP_CHECK(hipStreamSynchronize(st));
+      for (size_t i = 0; i < he.size(); ++i) he[i] = re[i / (K / 64)];
+      NNHIP_CHECK(hipMemcpyAsync(hexp.p, he.data(), he.size() * 4,
+                                 hipMemcpyHostToDevice, st));
+      NNHIP_CHECK(hipStreamSynchronize(st));
+    }
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      if (path == 8) {
+      if (path == 9) {
+        nnhip::launch_gemm_limb_hx(st, limbs.p, mpad, hexp.p, rows, K, N, WS[j].p,
+                                   S[j].p, b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
+      } else if (path == 8) {
         nnhip::launch_gemm_limb(st, limbs.p, mpad, rexp.p, rows, K, N, WS[j].p,
                                 S[j].p, b.p, nullptr, 0, y.p, N, nnhip::kEpiBias);
       } else if (path >= 3) {
