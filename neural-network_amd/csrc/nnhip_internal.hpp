@@ -127,10 +127,12 @@ __device__ inline int rope_row_pos(const RopeArgs &ra, int64_t m) {
 // Tensor::rope (tensor.cpp:1141-1173) on one pair (x_2j, x_2j+1) of output
 // column n (even) of row m at cache position pos (>= 0), with the pair's
 // cos / sin already read (unused for the v part), then the KV append of
-// layer.cpp:758-807.
+// layer.cpp:758-807.  Each product and the sum are rounded on their own, as
+// the reference's scalar code does (no fused multiply-add).
 __device__ inline void rope_store_pair_at(const RopeArgs &ra, int64_t m,
                                           int pos, int n, float xe, float xo,
                                           float c, float sn) {
+#pragma clang fp contract(off)
   const int b = (int)(m / ra.S);
   const int E = ra.H * ra.D;
   const int part = n / E, nn = n % E;
@@ -140,8 +142,10 @@ __device__ inline void rope_store_pair_at(const RopeArgs &ra, int64_t m,
     vd[0] = xe; vd[1] = xo;
     return;
   }
-  const float r0 = __fsub_rn(__fmul_rn(xe, c), __fmul_rn(xo, sn));
-  const float r1 = __fadd_rn(__fmul_rn(xe, sn), __fmul_rn(xo, c));
+  // (plain operators under contract(off): the _rn helpers are header
+  // functions whose operations the compiler may still fuse)
+  const float r0 = xe * c - xo * sn;
+  const float r1 = xe * sn + xo * c;
   float *dst = part == 0
                    ? ra.qrot + m * E + nn
                    : ra.kc + b * ra.seq_stride + ((int64_t)h * ra.cap + pos) * ra.D + 2 * j;
@@ -174,6 +178,7 @@ __device__ inline void rope_store_pair(const RopeArgs &ra, int64_t m, int n,
 // scale)), +-127), the same operations as rope_kv_q8_kernel.
 __device__ inline void rope_store_pair_q8(const RopeArgs &ra, int64_t m, int n,
                                           float xe, float xo) {
+#pragma clang fp contract(off)
   const int pos = rope_row_pos(ra, m);
   const int E = ra.H * ra.D;
   const int part = n / E, nn = n % E;
@@ -181,8 +186,8 @@ __device__ inline void rope_store_pair_q8(const RopeArgs &ra, int64_t m, int n,
   float a = xe, b = xo;
   if (part != 2) {
     const float2 cs = pos >= 0 ? rope_cos_sin(ra, pos, n) : make_float2(0.f, 0.f);
-    a = __fsub_rn(__fmul_rn(xe, cs.x), __fmul_rn(xo, cs.y));
-    b = __fadd_rn(__fmul_rn(xe, cs.y), __fmul_rn(xo, cs.x));
+    a = xe * cs.x - xo * cs.y;
+    b = xe * cs.y + xo * cs.x;
   }
   if (part == 0) {
     if (pos >= 0) { float *q = ra.qrot + m * E + nn; q[0] = a; q[1] = b; }
