@@ -15,6 +15,12 @@
 
 #include <hip/hip_runtime.h>
 
+// Every product and sum below is rounded on its own, as the reference's
+// scalar loops round them (p - q of the residual, the probabilities, the
+// tile sums): no fused multiply-add, so the decisions follow the reference's
+// arithmetic (the exponentials' own implementation is unaffected).
+#pragma clang fp contract(off)
+
 namespace nnhip {
 
 namespace {
