@@ -165,6 +165,11 @@ int nnhip_kvcache_create(nnhip_model *m, int batch, int quantized,
 int nnhip_kvcache_read_q8(const nnhip_kvcache *c, int layer, int b,
                           int8_t *kcodes, float *kscales, int8_t *vcodes,
                           float *vscales);
+/* KVCache::k / KVCache::v (layer.hpp:213-214) of one layer and sequence of
+ * an fp32 cache, its first length(b) positions: [H][len][D] each (host);
+ * k after RoPE, as the reference stores it. */
+int nnhip_kvcache_read(const nnhip_kvcache *c, int layer, int b, float *k,
+                       float *v);
 int nnhip_kvcache_free(nnhip_kvcache *c);
 int nnhip_kvcache_length(const nnhip_kvcache *c, int b, int *len);
 /* KVCache::truncate(len) (layer.cpp:67-149) for sequence b: an O(1) length

@@ -323,6 +323,28 @@ int nnhip_kvcache_read_q8(const nnhip_kvcache *c, int layer, int b,
   });
 }
 
+int nnhip_kvcache_read(const nnhip_kvcache *c, int layer, int b, float *k,
+                       float *v) {
+  return guard([&] {
+    REQ(c && k && v, "nnhip_kvcache_read: NULL argument");
+    const nnhip::KVCache &kv = *c->c;
+    REQ(!kv.q8, "nnhip_kvcache_read: the cache is quantised");
+    REQ(layer >= 0 && layer < kv.m->L && b >= 0 && b < kv.B,
+        "nnhip_kvcache_read: bad layer or sequence");
+    hipStream_t st = kv.m->ctx->stream;
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    const int H = kv.m->H, D = kv.m->D, n = kv.host_len[b];
+    const nnhip::KvSrc src = kv.src(layer, b);
+    for (int h = 0; h < H; ++h) {
+      const int64_t row0 = (int64_t)h * kv.cap;
+      NNHIP_CHECK(hipMemcpy(k + (int64_t)h * n * D, (const float *)src.k + row0 * D,
+                            (size_t)n * D * sizeof(float), hipMemcpyDeviceToHost));
+      NNHIP_CHECK(hipMemcpy(v + (int64_t)h * n * D, (const float *)src.v + row0 * D,
+                            (size_t)n * D * sizeof(float), hipMemcpyDeviceToHost));
+    }
+  });
+}
+
 int nnhip_kvcache_free(nnhip_kvcache *c) {
   return guard([&] {
     if (!c) return;

@@ -96,6 +96,7 @@ SIGNATURES = {
     "nnhip_decoder_forward": [_vp, _vp, _vp, _i, _i, _vp],
     "nnhip_kvcache_create": [_vp, _i, _i, _pp],
     "nnhip_kvcache_read_q8": [_vp, _i, _i, _vp, _vp, _vp, _vp],
+    "nnhip_kvcache_read": [_vp, _i, _i, _vp, _vp],
     "nnhip_kvcache_free": [_vp],
     "nnhip_kvcache_length": [_vp, _i, C.POINTER(C.c_int)],
     "nnhip_kvcache_truncate": [_vp, _i, _i],
@@ -424,6 +425,15 @@ class KVCache:
 
     def truncate(self, n, b=0):
         call("nnhip_kvcache_truncate", self.h, b, n)
+
+    def read(self, layer, b=0, heads=None, head_dim=None):
+        """k and v of one layer and sequence of an fp32 cache: [H][len][D]
+        each (k after RoPE)."""
+        n = self.length(b)
+        k = np.zeros((heads, n, head_dim), np.float32)
+        v = np.zeros_like(k)
+        call("nnhip_kvcache_read", self.h, layer, b, ptr(k), ptr(v))
+        return k, v
 
     def read_q8(self, layer, b=0, heads=None, head_dim=None):
         """Codes and scales of one layer and sequence of an int8 cache:

@@ -160,6 +160,48 @@ def test_forward_head_digits_vs_oracle(ctx, B, S):
     gm.free()
 
 
+@pytest.mark.parametrize("B,S", [(1, 5), (32, 1), (32, 6)])
+def test_fused_rope_append_bit_exact(ctx, B, S):
+    """The q/k/v epilogue's RoPE and KV append (tensor.cpp:1141-1173,
+    layer.cpp:758-807) bit for bit, on the GEMV (5 rows), the digit-plane
+    GEMM (32) and the LDS GEMM (192): after a forward, layer 0's cached keys
+    equal the device's own q/k/v projection of the embedded rows (the same
+    kernels with a bias epilogue, nnhip_linear_w8a32) rotated by the
+    oracle's or_rope, which rounds every product and sum on its own; the
+    cached values equal that projection."""
+    om, gm, params = build(ctx, HEADS, 13, True, std=0.03)
+    d, H = HEADS["d"], HEADS["H"]
+    D = d // H
+    rng = np.random.default_rng(B * 10 + S)
+    ids = rng.integers(0, HEADS["vocab"], (B, S)).astype(np.int32)
+    gc = nnhip.KVCache(gm, B)
+    gm.forward(ids, gc)
+    # the fused q/k/v weight of layer 0 as the forward holds it
+    parts = [gm.get_quantized(0, which, d, d) for which in (0, 1, 2)]
+    codes = np.ascontiguousarray(np.concatenate([c for c, _ in parts], axis=1).T)
+    scales = np.concatenate([sc for _, sc in parts])
+    bias = np.concatenate([params[i].ravel() for i in (2, 4, 6)])
+    x = gm.get_param(0)[ids.ravel()]
+    R = B * S
+    dx, dc = ctx.array(x), ctx.array(codes)
+    ds, db = ctx.array(scales), ctx.array(bias)
+    dy = ctx.array(shape=(R, 3 * d))
+    call = nnhip.call
+    call("nnhip_linear_w8a32", ctx.h, dx.p, R, d, dc.p, ds.p, db.p, 3 * d,
+         dy.p, 1 if R < 16 else 2)
+    y = dy.numpy()
+    for b in range(B):
+        kg, vg = gc.read(0, b, heads=H, head_dim=D)
+        rows = y[b * S:(b + 1) * S]
+        k = np.ascontiguousarray(rows[:, d:2 * d].reshape(S, H, D).transpose(1, 0, 2))
+        O.lib().or_rope(O.fptr(k), H, S, D, 0)
+        np.testing.assert_array_equal(kg, k, err_msg=f"keys b={b}")
+        v = rows[:, 2 * d:].reshape(S, H, D).transpose(1, 0, 2)
+        np.testing.assert_array_equal(vg, v, err_msg=f"values b={b}")
+    gc.free()
+    gm.free()
+
+
 @pytest.mark.parametrize("quant", [False, True])
 def test_forward_cache_truncate_vs_oracle(ctx, quant):
     om, gm, _ = build(ctx, TOY_T, 4, quant, std=0.05)
