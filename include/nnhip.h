@@ -71,7 +71,7 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * "lds_min_rows": the LDS-resident GEMM serves projections from this many
  * rows on (default 128; process-wide).
  * "limb_k8": the digit-plane GEMM splits K over 8 waves from this K on
- * (default 1024; process-wide).
+ * (default 512; process-wide).
  * "o_head_digits": 1 = for 64-wide heads the merged attention writes the
  * output projection's digit planes itself, one exponent per (row, head),
  * and the digit-plane GEMM scales each head's exact total by its own

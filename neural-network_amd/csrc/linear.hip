@@ -1085,7 +1085,7 @@ void launch_act_quant(hipStream_t st, const float *x, int64_t ldx, int rows,
   NNHIP_CHECK(hipGetLastError());
 }
 
-int g_limb_k8 = 1024;
+int g_limb_k8 = 512;
 
 // The int8 KV append in gemm_limb_kernel's epilogue needs each head's pairs
 // within one tile row's 16 (32x32 tiles) column pairs.
@@ -1115,7 +1115,9 @@ void launch_gemm_limb(hipStream_t st, const int8_t *limbs, int mpad,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
                        ldr, y, ldy, epi, ntm, ntn, rz);
   } else if (K >= g_limb_k8) {
-    // long K: 8 waves split it, half the chunks each
+    // K >= 512: 8 waves split it, half the chunks each (at K = 512 four of
+    // them have no chunk and add zeros; the epilogue is still spread over 512
+    // threads, measured faster than 4 waves)
     const int ntn = N / 32, per = (ntm * ntn + 7) / 8;
     hipLaunchKernelGGL((gemm_limb_kernel<1, 8>), dim3(8 * per), dim3(512), 0, st,
                        limbs, mpad, rexp, rows, K, N, wq, scale, bias, resid,
