@@ -26,6 +26,16 @@ nnhip_view view(const DeviceBuffer &b, size_t offset, const Shape &shape,
     throw std::runtime_error("HipBackend: more than 8 dimensions");
   if (strides.size() != shape.size())
     throw std::runtime_error("HipBackend: shape and strides differ in rank");
+  // the last element the view reaches must lie inside the buffer; an empty
+  // view reaches nothing
+  size_t last = offset;
+  bool empty = false;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == 0) empty = true;
+    else last += (shape[i] - 1) * strides[i];
+  }
+  if (!empty && (last + 1) * sizeof(float) > b.size())
+    throw std::runtime_error("HipBackend: view reaches past its buffer");
   nnhip_view v{};
   v.data = const_cast<void *>(b.data());
   v.offset = static_cast<int64_t>(offset);

@@ -1,6 +1,7 @@
 // The parts of the drop-in decoder objects (hip_nn.hpp) that use the
 // reference's compiled code: HipDecoder's constructor from a
-// TransformerDecoder and HipQuantizedDense over Tensor.
+// TransformerDecoder, HipMultiHeadAttention over Tensor and
+// HipQuantizedDense, the Tensor face of HipQuantizedDenseCore.
 #include "hip_nn.hpp"
 
 #include <algorithm>
@@ -51,130 +52,61 @@ std::shared_ptr<Tensor> HipMultiHeadAttention::forward(
                                   DataType::FP32);
 }
 
-void HipQuantizedDense::upload(const std::vector<int8_t> &codes_in_out,
-                               const std::vector<float> &scales,
-                               const std::vector<float> &bias) {
-  host_codes_ = codes_in_out;
-  host_scales_ = scales;
-  host_bias_ = bias;
-  // the device reads the codes transposed, [out][in], one per byte (INT4
-  // codes in [-7, 7] go through the int8 kernels unchanged)
-  std::vector<int8_t> t(in_ * out_);
-  for (size_t k = 0; k < in_; ++k)
-    for (size_t n = 0; n < out_; ++n) t[n * in_ + k] = codes_in_out[k * out_ + n];
-  codes_ = be_.allocate(t.size());
-  check(nnhip_h2d(be_.context(), codes_->data(), t.data(), t.size()));
-  scales_ = be_.allocate(scales.size() * sizeof(float));
-  be_.copy_host_to_device(scales.data(), *scales_, scales.size() * sizeof(float));
-  bias_ = be_.allocate(bias.size() * sizeof(float));
-  be_.copy_host_to_device(bias.data(), *bias_, bias.size() * sizeof(float));
-}
-
 HipQuantizedDense::HipQuantizedDense(HipBackend &backend,
-                                     const QuantizedDense &layer)
-    : be_(backend), type_(layer.type()) {
+                                     const QuantizedDense &layer) {
   const Shape ws = layer.weight_shape();  // [in, out]
-  in_ = ws.at(0);
-  out_ = ws.at(1);
-  // packed_weights hold the codes of [in][out]: one int8 per byte (INT8,
-  // quantization.cpp:36-66) or two 4-bit codes per byte, the even flat index
-  // in the low nibble, sign-extended on reading (INT4, quantization.cpp:
-  // 68-86, 106-122)
-  packed_ = layer.packed_weights();
-  const bool int4 = type_ == QuantizationType::INT4;
-  std::vector<int8_t> codes(in_ * out_);
-  for (size_t idx = 0; idx < codes.size(); ++idx) {
-    if (!int4) {
-      codes[idx] = static_cast<int8_t>(packed_[idx]);
-    } else {
-      const uint8_t nib = (idx % 2 == 0) ? (packed_[idx / 2] & 0x0F)
-                                         : ((packed_[idx / 2] >> 4) & 0x0F);
-      codes[idx] = (nib & 0x08) ? static_cast<int8_t>(nib | 0xF0)
-                                : static_cast<int8_t>(nib);
-    }
-  }
-  std::vector<float> b(out_, 0.0f);
+  std::vector<float> b;
   if (layer.bias()) b = layer.bias()->to_host();
-  upload(codes, layer.scales()->to_host(), b);
+  core_ = std::make_unique<HipQuantizedDenseCore>(
+      backend, layer.type(), ws.at(0), ws.at(1), layer.packed_weights(),
+      layer.scales()->to_host(), b);
 }
 
 HipQuantizedDense::HipQuantizedDense(HipBackend &backend,
                                      std::shared_ptr<Dense> float_dense,
-                                     const QuantizationConfig &config)
-    : be_(backend), type_(config.type) {
+                                     const QuantizationConfig &config) {
   const auto params = float_dense->parameters();  // weight [in, out], bias
   const Shape ws = params.at(0)->shape();
-  in_ = ws.at(0);
-  out_ = ws.at(1);
-  const std::vector<float> w = params[0]->to_host();
-  std::unique_ptr<DeviceBuffer> dw = be_.allocate(w.size() * sizeof(float));
-  be_.copy_host_to_device(w.data(), *dw, w.size() * sizeof(float));
-  std::unique_ptr<DeviceBuffer> dc = be_.allocate(in_ * out_);
-  std::unique_ptr<DeviceBuffer> ds = be_.allocate(out_ * sizeof(float));
-  const bool int4 = type_ == QuantizationType::INT4;
-  check((int4 ? nnhip_quantize_w4 : nnhip_quantize_w8)(
-      be_.context(), static_cast<const float *>(dw->data()), (int)in_, (int)out_,
-      static_cast<int8_t *>(dc->data()), static_cast<float *>(ds->data())));
-  std::vector<int8_t> t(in_ * out_);  // [out][in]
-  std::vector<float> sc(out_);
-  check(nnhip_d2h(be_.context(), t.data(), dc->data(), t.size()));
-  check(nnhip_d2h(be_.context(), sc.data(), ds->data(), sc.size() * sizeof(float)));
-  std::vector<int8_t> codes(in_ * out_);  // [in][out]
-  for (size_t k = 0; k < in_; ++k)
-    for (size_t n = 0; n < out_; ++n) codes[k * out_ + n] = t[n * in_ + k];
-  // packed_weights in the reference's layout
-  if (!int4) {
-    packed_.assign(codes.begin(), codes.end());
-  } else {
-    packed_.assign((codes.size() + 1) / 2, 0);
-    for (size_t idx = 0; idx < codes.size(); ++idx) {
-      const uint8_t v = static_cast<uint8_t>(codes[idx]) & 0x0F;
-      if (idx % 2 == 0) packed_[idx / 2] = v;
-      else packed_[idx / 2] |= static_cast<uint8_t>(v << 4);
-    }
-  }
-  std::vector<float> b(out_, 0.0f);
+  std::vector<float> b;
   if (params.size() > 1 && params[1]) b = params[1]->to_host();
-  upload(codes, sc, b);
+  core_ = std::make_unique<HipQuantizedDenseCore>(
+      backend, params[0]->to_host(), ws.at(0), ws.at(1), b, config.type);
 }
 
 std::shared_ptr<Tensor> HipQuantizedDense::scales() const {
-  return std::make_shared<Tensor>(Shape{out_}, host_scales_, &be_);
+  return std::make_shared<Tensor>(Shape{core_->out_features()}, core_->scales(),
+                                  &core_->backend());
 }
 
 std::shared_ptr<Tensor> HipQuantizedDense::bias() const {
-  return std::make_shared<Tensor>(Shape{1, out_}, host_bias_, &be_);
+  return std::make_shared<Tensor>(Shape{1, core_->out_features()}, core_->bias(),
+                                  &core_->backend());
 }
 
 std::shared_ptr<Tensor> HipQuantizedDense::dequantize_weight() const {
-  std::vector<float> w(in_ * out_);
-  for (size_t k = 0; k < in_; ++k)
-    for (size_t n = 0; n < out_; ++n)
-      w[k * out_ + n] = static_cast<float>(host_codes_[k * out_ + n]) * host_scales_[n];
-  return std::make_shared<Tensor>(Shape{in_, out_}, w, &be_);
+  return std::make_shared<Tensor>(weight_shape(), core_->dequantize_weight(),
+                                  &core_->backend());
 }
 
 std::shared_ptr<Tensor> HipQuantizedDense::forward(
     const std::shared_ptr<Tensor> &input) {
   const Shape &s = input->shape();
-  if (input->backend() != &be_ || s.empty() || s.back() != in_ ||
+  HipBackend &be = core_->backend();
+  const size_t in = core_->in_features(), out = core_->out_features();
+  if (input->backend() != &be || s.empty() || s.back() != in ||
       !is_contiguous(s, input->strides()))
     throw std::runtime_error(
         "HipQuantizedDense: input must be a contiguous HipBackend tensor "
         "whose last dimension is in_features");
-  const size_t rows = count_elements(s) / in_;
+  const size_t rows = count_elements(s) / in;
   Shape out_shape = s;
-  out_shape.back() = out_;
-  std::shared_ptr<DeviceBuffer> y(be_.allocate(rows * out_ * sizeof(float)));
+  out_shape.back() = out;
+  std::shared_ptr<DeviceBuffer> y(be.allocate(rows * out * sizeof(float)));
   const float *x =
       static_cast<const float *>(input->storage()->data()) + input->offset();
-  check(nnhip_linear_w8a32(be_.context(), x, (int)rows, (int)in_,
-                           static_cast<const int8_t *>(codes_->data()),
-                           static_cast<const float *>(scales_->data()),
-                           static_cast<const float *>(bias_->data()),
-                           (int)out_, static_cast<float *>(y->data()), 0));
+  core_->forward_device(x, rows, static_cast<float *>(y->data()));
   return std::make_shared<Tensor>(out_shape, compute_strides(out_shape), 0, y,
-                                  &be_, DataType::FP32);
+                                  &be, DataType::FP32);
 }
 
 }  // namespace nnhip_backend

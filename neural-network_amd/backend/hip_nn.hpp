@@ -168,29 +168,43 @@ class HipMhaCache {
   std::unique_ptr<DeviceBuffer> k_, v_;
 };
 
-// QuantizedDense (INT8 or INT4) with its codes and scales resident on the
-// device; forward runs on tensors whose storage belongs to `backend`.
-class HipQuantizedDense {
+// QuantizedDense (INT8 or INT4, quantization.hpp:15-41, quantization.cpp:
+// 7-147) on device pointers: the codes, scales and bias resident on the
+// device, the reference's packed_weights layout on the host.  Uses no
+// compiled reference code (hip_qdense.cpp), so programs run it without the
+// reference's sources; HipQuantizedDense is the same over Tensor.
+class HipQuantizedDenseCore {
  public:
-  // the codes and scales of a reference QuantizedDense
-  HipQuantizedDense(HipBackend &backend, const QuantizedDense &layer);
-  // QuantizedDense(float_dense, config) (quantization.cpp:7-86): the Dense's
-  // weight quantised on the device (nnhip_quantize_w8 / _w4), the same codes
-  // and scales bit for bit
-  HipQuantizedDense(HipBackend &backend, std::shared_ptr<Dense> float_dense,
-                    const QuantizationConfig &config);
-  // y [rows, out] = x [rows, in] . (codes * scales) + bias, x contiguous
-  std::shared_ptr<Tensor> forward(const std::shared_ptr<Tensor> &input);
-  // the accessors of QuantizedDense (quantization.hpp:20-31)
+  // QuantizedDense(float_dense, config) (quantization.cpp:7-86): weight
+  // [in][out] (Dense's layout) and bias [out] on the host, quantised on the
+  // device (nnhip_quantize_w8 / _w4): the reference's codes and scales bit
+  // for bit
+  HipQuantizedDenseCore(HipBackend &backend, const std::vector<float> &weight,
+                        size_t in, size_t out, const std::vector<float> &bias,
+                        QuantizationType type);
+  // the packed_weights, scales and bias of a reference QuantizedDense
+  HipQuantizedDenseCore(HipBackend &backend, QuantizationType type, size_t in,
+                        size_t out, const std::vector<uint8_t> &packed,
+                        const std::vector<float> &scales,
+                        const std::vector<float> &bias);
+  // forward (quantization.cpp:127-147) on device rows: y [rows][out] =
+  // x [rows][in] . (codes * scales) + bias, enqueued on the backend's stream
+  void forward_device(const float *x, size_t rows, float *y) const;
+  // dequantize_weight (quantization.cpp:89-125): codes * scales, [in][out]
+  [[nodiscard]] std::vector<float> dequantize_weight() const;
   [[nodiscard]] QuantizationType type() const noexcept { return type_; }
   [[nodiscard]] const std::vector<uint8_t> &packed_weights() const noexcept {
     return packed_;
   }
-  [[nodiscard]] Shape weight_shape() const { return Shape{in_, out_}; }
-  std::shared_ptr<Tensor> scales() const;  // [out] on the HipBackend
-  std::shared_ptr<Tensor> bias() const;    // [1, out] on the HipBackend
-  // dequantize_weight (quantization.cpp:89-125): codes * scales, [in, out]
-  std::shared_ptr<Tensor> dequantize_weight() const;
+  [[nodiscard]] const std::vector<float> &scales() const noexcept {
+    return host_scales_;
+  }
+  [[nodiscard]] const std::vector<float> &bias() const noexcept {
+    return host_bias_;
+  }
+  [[nodiscard]] size_t in_features() const noexcept { return in_; }
+  [[nodiscard]] size_t out_features() const noexcept { return out_; }
+  [[nodiscard]] HipBackend &backend() const noexcept { return be_; }
 
  private:
   void upload(const std::vector<int8_t> &codes_in_out,
@@ -202,6 +216,35 @@ class HipQuantizedDense {
   std::vector<int8_t> host_codes_;                        // [in][out]
   std::vector<float> host_scales_, host_bias_;
   std::unique_ptr<DeviceBuffer> codes_, scales_, bias_;  // codes [out][in]
+};
+
+// HipQuantizedDenseCore over Tensor: forward runs on tensors whose storage
+// belongs to `backend` (hip_nn.cpp, linked with the reference's sources).
+class HipQuantizedDense {
+ public:
+  // the codes and scales of a reference QuantizedDense
+  HipQuantizedDense(HipBackend &backend, const QuantizedDense &layer);
+  // QuantizedDense(float_dense, config), quantised on the device
+  HipQuantizedDense(HipBackend &backend, std::shared_ptr<Dense> float_dense,
+                    const QuantizationConfig &config);
+  // y [rows, out] = x [rows, in] . (codes * scales) + bias, x contiguous
+  std::shared_ptr<Tensor> forward(const std::shared_ptr<Tensor> &input);
+  // the accessors of QuantizedDense (quantization.hpp:20-31)
+  [[nodiscard]] QuantizationType type() const noexcept { return core_->type(); }
+  [[nodiscard]] const std::vector<uint8_t> &packed_weights() const noexcept {
+    return core_->packed_weights();
+  }
+  [[nodiscard]] Shape weight_shape() const {
+    return Shape{core_->in_features(), core_->out_features()};
+  }
+  std::shared_ptr<Tensor> scales() const;  // [out] on the HipBackend
+  std::shared_ptr<Tensor> bias() const;    // [1, out] on the HipBackend
+  // dequantize_weight (quantization.cpp:89-125): codes * scales, [in, out]
+  std::shared_ptr<Tensor> dequantize_weight() const;
+  [[nodiscard]] const HipQuantizedDenseCore &core() const noexcept { return *core_; }
+
+ private:
+  std::unique_ptr<HipQuantizedDenseCore> core_;
 };
 
 }  // namespace nnhip_backend

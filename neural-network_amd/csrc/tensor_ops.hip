@@ -348,6 +348,16 @@ bool same_shape(const TensorView &a, const TensorView &b) {
   return true;
 }
 
+// `in` broadcasts to `out` under CpuBackend's rule (right-aligned dims, each
+// equal to the output's or 1); anything else would index past `in`
+bool broadcasts_to(const TensorView &in, const TensorView &out) {
+  if (in.rank > out.rank) return false;
+  const int lead = out.rank - in.rank;
+  for (int i = 0; i < in.rank; ++i)
+    if (in.shape[i] != 1 && in.shape[i] != out.shape[lead + i]) return false;
+  return true;
+}
+
 void check_view(const TensorView &v, const char *what) {
   NNHIP_REQUIRE(v.data && v.rank >= 0 && v.rank <= kMaxRank, kErrArg,
                 std::string(what) + ": bad tensor view");
@@ -370,8 +380,8 @@ void launch_binary(hipStream_t st, int op, const TensorView &a,
                    const TensorView &b, const TensorView &out) {
   check_view(a, "binary"); check_view(b, "binary"); check_view(out, "binary");
   NNHIP_REQUIRE(op >= kOpAdd && op <= kOpLogBack, kErrArg, "binary: unknown op");
-  NNHIP_REQUIRE(a.rank <= out.rank && b.rank <= out.rank, kErrArg,
-                "binary: operand rank above the output's");
+  NNHIP_REQUIRE(broadcasts_to(a, out) && broadcasts_to(b, out), kErrArg,
+                "binary: operand shape does not broadcast to the output's");
   const int64_t n = numel(out);
   if (n == 0) return;
   if (same_shape(a, out) && same_shape(b, out) && contiguous(a) &&
@@ -390,7 +400,8 @@ void launch_unary(hipStream_t st, int op, const TensorView &in,
                   const TensorView &out) {
   check_view(in, "unary"); check_view(out, "unary");
   NNHIP_REQUIRE(op >= kOpRelu && op <= kOpLog, kErrArg, "unary: unknown op");
-  NNHIP_REQUIRE(in.rank <= out.rank, kErrArg, "unary: input rank above the output's");
+  NNHIP_REQUIRE(broadcasts_to(in, out), kErrArg,
+                "unary: input shape does not broadcast to the output's");
   const int64_t n = numel(out);
   if (n == 0) return;
   hipLaunchKernelGGL(unary_kernel, dim3(grid_for(n)), dim3(kBlock), 0, st, op,
@@ -469,7 +480,9 @@ void launch_softmax_backward(hipStream_t st, const TensorView &y,
                              int axis) {
   check_view(y, "softmax_backward"); check_view(dy, "softmax_backward");
   check_view(dx, "softmax_backward");
-  NNHIP_REQUIRE(axis >= 0 && axis < y.rank && same_shape(y, dy) && same_shape(y, dx),
+  // grad_out broadcasts against the output's shape, as in
+  // CpuBackend::softmax_backward (get_input_offset over out_shape)
+  NNHIP_REQUIRE(axis >= 0 && axis < y.rank && same_shape(y, dx) && broadcasts_to(dy, y),
                 kErrArg, "softmax_backward: bad axis or shapes");
   const int64_t n = numel(y);
   if (n == 0) return;

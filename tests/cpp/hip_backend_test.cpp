@@ -9,8 +9,10 @@
 // (or_dense, or_layernorm) and closed forms; then the decoder objects
 // HipDecoder / HipKVCache (backend/hip_nn.hpp) against the oracle's forward
 // and speculative decoding, and HipMultiHeadAttention / HipMhaCache against
-// MultiHeadAttention::forward restated with the oracle's pieces.  Needs a GPU; prints one line a check and exits
-// non-zero on the first failure.
+// MultiHeadAttention::forward restated with the oracle's pieces, and
+// HipQuantizedDenseCore against the reference's quantisation known answers
+// (tests/nn/quantization_test.cpp:6-86) and the oracle's Dense.  Needs a
+// GPU; prints one line a check and exits non-zero on the first failure.
 #include "backend/hip_backend.hpp"  // neural-network_amd/backend
 #include "backend/hip_nn.hpp"
 
@@ -305,8 +307,33 @@ void test_fill_and_unsupported(ExecutionBackend &be) {
     threw = true;
   }
   expect(threw, "maxpool2d reports it is unsupported");
-  std::printf("ok fill and unsupported ops\n");
+  // a view that reaches past its buffer is refused before any launch
+  // (Tensor never builds one; a caller's bad strides would read out of it)
+  threw = false;
+  try {
+    be.add(*a.buf, 0, Shape{5, 4}, Strides{4, 1}, *a.buf, 0, a.shape, a.strides,
+           *a.buf, 0, a.shape, a.strides);
+  } catch (const std::runtime_error &) {
+    threw = true;
+  }
+  expect(threw, "view past its buffer is refused");
+  // an operand whose shape does not broadcast to the output's ([3] against
+  // [4, 4]) is refused by the library
+  T c = make(be, {3}, {1, 2, 3});
+  threw = false;
+  try {
+    be.add(*a.buf, 0, a.shape, a.strides, *c.buf, 0, c.shape, c.strides, *a.buf,
+           0, a.shape, a.strides);
+  } catch (const std::runtime_error &) {
+    threw = true;
+  }
+  expect(threw, "non-broadcastable operand is refused");
+  ok = true;
+  for (float v : host(be, a)) ok &= v == 1.5f;
+  expect(ok, "refused ops leave the output untouched");
+  std::printf("ok fill, unsupported ops and refused views\n");
 }
+
 
 // A decoder's parameters() as host arrays in the oracle's shapes, N(0, sd)
 // from a fixed seed, loaded into a fresh oracle model as well.
@@ -558,6 +585,105 @@ void test_mha_adapter(HipBackend &hip) {
   std::printf("ok HipMultiHeadAttention / HipMhaCache vs oracle\n");
 }
 
+// HipQuantizedDenseCore (QuantizedDense on the device) against the
+// reference's own known answers (tests/nn/quantization_test.cpp:6-86) and
+// the oracle's Dense over the same codes.
+void test_quantized_dense_core(HipBackend &hip) {
+  using nnhip_backend::HipQuantizedDenseCore;
+  // SymmetricInt8 (quantization_test.cpp:6-26)
+  {
+    HipQuantizedDenseCore q(hip, {-1.27f, 0.5f, 12.7f, -6.35f}, 2, 2, {},
+                            QuantizationType::INT8);
+    expect(std::fabs(q.scales()[0] - 0.1f) < 1e-5f &&
+               std::fabs(q.scales()[1] - 0.05f) < 1e-5f,
+           "INT8 KAT scales 0.1, 0.05");
+    const std::vector<float> dq = q.dequantize_weight();
+    expect(std::fabs(dq[0] + 1.27f) < 0.05f && std::fabs(dq[1] - 0.5f) < 1e-5f &&
+               std::fabs(dq[2] - 12.7f) < 1e-5f && std::fabs(dq[3] + 6.35f) < 1e-5f,
+           "INT8 KAT dequantize_weight");
+    const auto &pk = q.packed_weights();
+    expect(pk.size() == 4 && (int8_t)pk[2] == 127 && (int8_t)pk[3] == -127 &&
+               (int8_t)pk[1] == 10,
+           "INT8 KAT packed codes");
+  }
+  // Int4Packing (quantization_test.cpp:28-45): codes -7, 3, 0, 5 at scale 1,
+  // two per byte with the even flat index in the low nibble
+  {
+    HipQuantizedDenseCore q(hip, {-7.0f, 3.0f, 0.0f, 5.0f}, 4, 1, {},
+                            QuantizationType::INT4);
+    expect(q.scales()[0] == 1.0f, "INT4 KAT scale 1");
+    const std::vector<float> dq = q.dequantize_weight();
+    expect(dq == std::vector<float>({-7.0f, 3.0f, 0.0f, 5.0f}),
+           "INT4 KAT dequantize_weight");
+    expect(q.packed_weights() == std::vector<uint8_t>({0x39, 0x50}),
+           "INT4 KAT nibble packing");
+  }
+  // QuantizedDenseForward (quantization_test.cpp:47-86): within 5% (INT8)
+  // and 70% (INT4) of the fp32 Dense, max(1, |y|) relative
+  {
+    const std::vector<float> w = {1.5f, -2.5f, 3.0f, -0.8f, 1.2f, -2.0f,
+                                  2.0f, -1.5f, 0.5f, -3.0f, 2.5f, -1.0f};
+    const std::vector<float> b = {0.5f, -0.5f, 1.0f};
+    const std::vector<float> x = {1.0f, -2.0f, 3.5f, 4.0f, -5.0f, 6.0f, 7.2f, -8.0f};
+    std::vector<float> ref(6);
+    or_dense(x.data(), 2, 4, 3, w.data(), nullptr, nullptr, b.data(), ref.data());
+    T dx = make(hip, {2, 4}, x);
+    for (int bits : {8, 4}) {
+      HipQuantizedDenseCore q(hip, w, 4, 3, b,
+                              bits == 8 ? QuantizationType::INT8 : QuantizationType::INT4);
+      T dy = make(hip, {2, 3}, {});
+      q.forward_device(static_cast<const float *>(dx.buf->data()), 2,
+                       static_cast<float *>(dy.buf->data()));
+      const std::vector<float> y = host(hip, dy);
+      double worst = 0.0;
+      for (size_t i = 0; i < 6; ++i)
+        worst = std::max(worst, std::fabs((double)y[i] - ref[i]) /
+                                    std::max(1.0, std::fabs((double)ref[i])));
+      expect(worst < (bits == 8 ? 0.05 : 0.70),
+             "QuantizedDenseForward KAT INT" + std::to_string(bits));
+    }
+  }
+  // larger shapes through the GEMV (5 rows) and the MFMA GEMMs (40, 192
+  // rows): against or_dense over the same codes and scales within 1e-4 of a
+  // row; a core rebuilt from packed_weights + scales + bias (the reference
+  // QuantizedDense's state) gives the same bytes and results
+  for (int bits : {8, 4}) {
+    const size_t in = 256, out = 384;
+    const QuantizationType qt = bits == 8 ? QuantizationType::INT8 : QuantizationType::INT4;
+    const std::vector<float> w = randn(in * out, 91u + (unsigned)bits, 0.05f);
+    const std::vector<float> b = randn(out, 92u, 0.1f);
+    HipQuantizedDenseCore q(hip, w, in, out, b, qt);
+    std::vector<int8_t> oc(in * out);
+    std::vector<float> os(out);
+    or_quantize_w(w.data(), (int64_t)in, (int64_t)out, bits, oc.data(), os.data());
+    expect(q.scales() == os, "INT" + std::to_string(bits) + " scales == oracle");
+    const std::vector<float> dq = q.dequantize_weight();
+    bool same = true;
+    for (size_t i = 0; i < in * out; ++i) same &= dq[i] == (float)oc[i] * os[i % out];
+    expect(same, "INT" + std::to_string(bits) + " dequantize_weight == codes * scales");
+    HipQuantizedDenseCore r(hip, qt, in, out, q.packed_weights(), q.scales(), q.bias());
+    expect(r.packed_weights() == q.packed_weights() && r.dequantize_weight() == dq,
+           "INT" + std::to_string(bits) + " core from packed_weights");
+    for (size_t rows : {5u, 40u, 192u}) {
+      const std::vector<float> x = randn(rows * in, 93u + (unsigned)rows);
+      std::vector<float> want(rows * out);
+      or_dense(x.data(), (int64_t)rows, (int64_t)in, (int64_t)out, nullptr,
+               oc.data(), os.data(), b.data(), want.data());
+      T dx = make(hip, {rows, in}, x);
+      T y1 = make(hip, {rows, out}, {}), y2 = make(hip, {rows, out}, {});
+      q.forward_device(static_cast<const float *>(dx.buf->data()), rows,
+                       static_cast<float *>(y1.buf->data()));
+      r.forward_device(static_cast<const float *>(dx.buf->data()), rows,
+                       static_cast<float *>(y2.buf->data()));
+      const std::vector<float> g1 = host(hip, y1), g2 = host(hip, y2);
+      expect(row_rel_err(g1, want, rows, out) <= 1e-4,
+             "INT" + std::to_string(bits) + " forward rows " + std::to_string(rows));
+      expect(g1 == g2, "INT" + std::to_string(bits) + " rebuilt core forward");
+    }
+  }
+  std::printf("ok HipQuantizedDenseCore\n");
+}
+
 }  // namespace
 
 int main() {
@@ -571,6 +697,7 @@ int main() {
     test_fill_and_unsupported(be);
     test_decoder_adapter(hip);
     test_mha_adapter(hip);
+    test_quantized_dense_core(hip);
   } catch (const std::exception &e) {
     std::printf("FAIL exception: %s\n", e.what());
     return 1;

@@ -287,3 +287,41 @@ def test_slice_backward_and_fill(ctx):
     np.testing.assert_array_equal(dgp.numpy(), want)
     nnhip.call("nnhip_fill_f32", ctx.h, dgp.p, gp.size, 2.5)
     assert (dgp.numpy() == 2.5).all()
+
+
+def test_non_broadcastable_operands_are_refused(ctx):
+    """An operand whose right-aligned dims are neither the output's nor 1
+    ([3] against [4, 5]; [2, 5] against [4, 5]) is refused with NNHIP_EARG
+    on the host, before any launch: the output keeps its contents."""
+    da = dev(ctx, np.ones(3, np.float32))
+    db = dev(ctx, np.ones((2, 5), np.float32))
+    dc = dev(ctx, np.ones((4, 5), np.float32))
+    do = ctx.array(shape=(4, 5))
+    nnhip.call("nnhip_fill_f32", ctx.h, do.p, 20, -3.0)
+    for bad in (da, db):
+        with pytest.raises(nnhip.NNHipError) as e:
+            nnhip.call("nnhip_binary_f32", ctx.h, nnhip.OP_ADD, nnhip.view(bad),
+                       nnhip.view(dc), nnhip.view(do))
+        assert e.value.code == nnhip.EARG
+        with pytest.raises(nnhip.NNHipError) as e:
+            nnhip.call("nnhip_unary_f32", ctx.h, nnhip.OP_RELU,
+                       nnhip.view(bad), nnhip.view(do))
+        assert e.value.code == nnhip.EARG
+    assert (do.numpy() == -3.0).all()
+
+
+def test_softmax_backward_broadcast_grad(ctx):
+    """CpuBackend::softmax_backward reads grad_out through its broadcast
+    offset against the output's shape (cpu_backend.cpp:585-640): a [1, L]
+    gradient against [R, L] outputs gives y * (g - sum(g * y)) per row."""
+    rng = np.random.default_rng(12)
+    R, L = 5, 33
+    y = rng.random((R, L)).astype(np.float32)
+    y /= y.sum(1, keepdims=True)
+    g = rng.standard_normal((1, L)).astype(np.float32)
+    dy_, dg, dx = dev(ctx, y), dev(ctx, g), ctx.array(shape=(R, L))
+    nnhip.call("nnhip_softmax_backward_f32", ctx.h, nnhip.view(dy_),
+               nnhip.view(dg), nnhip.view(dx), 1)
+    y64 = y.astype(np.float64)
+    want = y64 * (g - (g * y64).sum(1, keepdims=True))
+    assert np.abs(dx.numpy() - want).max() <= 1e-5 * np.abs(want).max()

@@ -5,10 +5,10 @@
   256 ids, k = 5, T = 1.0, Philox uniforms.  The device runs all 32
   sequences in lockstep with the decode loop's own kernels (draft sampling
   from the draft lm head's tile statistics, the verify rows' statistics, the
-  accept / residual kernel); a stated subset of sequences is compared with
-  the oracle's single-sequence runs (sequence index b keys the uniforms).
-  max_new is 24 instead of 128 to keep the oracle's run short; every kernel
-  and shape of the loop is the same, the contexts are shorter.
+  accept / residual kernel) over the full 128 new tokens; a stated subset
+  of six sequences (the first and the last to finish, one of median length,
+  and fixed indices) is compared with the oracle's single-sequence runs
+  (sequence index b keys the uniforms), and two sequences in greedy mode.
 * The acceptance microbenchmark at its full size: 256 sequences x k = 8 x
   V = 32000, target and draft logits N(0, 2), one accept uniform per
   position and one resample uniform per sequence, through nnhip_spec_accept
@@ -47,54 +47,93 @@ def device_and_oracle(ctx, cfg, seed, max_seq=1024):
     return gm, om
 
 
-def test_cfg4_sampled_batch32_matches_oracle(ctx):
-    B, P, new, k, T, seed = 32, 256, 24, 5, 1.0, 42
+@pytest.fixture(scope="module")
+def cfg4(ctx):
+    """The batch-32 workload as the benchmark runs it: both models, the 32
+    prompts, and the device's sampled (T = 1) and greedy runs at the full
+    128 new tokens per sequence."""
+    B, P, new, k, seed = 32, 256, 128, 5, 42
     gt, ot = device_and_oracle(ctx, CFG4_T, 1234)
     gd, od = device_and_oracle(ctx, CFG4_D, 5678)
     rng = np.random.default_rng(2024)
     prompts = rng.integers(0, CFG4_T["vocab"], (B, P)).astype(np.int32)
-    got, stats, tm = gt.generate_speculative_batch(gd, prompts, new, k, T,
-                                                   seed)
+    sampled = gt.generate_speculative_batch(gd, prompts, new, k, 1.0, seed)
+    greedy = gt.generate_speculative_batch(gd, prompts, new, k, 0.0, seed)
+    yield dict(ot=ot, od=od, prompts=prompts, new=new, k=k, seed=seed,
+               sampled=sampled, greedy=greedy)
+    gt.free(); gd.free()
+
+
+def sampled_subset(stats):
+    """The sequences compared with the oracle: the one that finishes first
+    (fewest cycles), the one that finishes last (most cycles; it runs the
+    lockstep tail alone), one of median length, and sequences 0, 13, 31."""
+    cyc = np.array([s.cycles for s in stats])
+    order = np.argsort(cyc, kind="stable")
+    first, last, mid = int(order[0]), int(order[-1]), int(order[len(order) // 2])
+    seqs = [first, last, mid]
+    for b in (0, 13, 31, 7, 22):
+        if len(seqs) >= 6:
+            break
+        if b not in seqs:
+            seqs.append(b)
+    return seqs
+
+
+def test_cfg4_sampled_batch32_device_invariants(cfg4):
+    got, stats, _ = cfg4["sampled"]
+    B, P, new = 32, 256, cfg4["new"]
     assert got.shape == (B, P + new)
-    np.testing.assert_array_equal(got[:, :P], prompts)
+    np.testing.assert_array_equal(got[:, :P], cfg4["prompts"])
     assert ((got >= 0) & (got < CFG4_T["vocab"])).all()
     for b in range(B):
         s = stats[b]
         # every cycle commits its accepted drafts plus one token
         assert s.accepted + s.resampled + s.bonus + 1 == new, b
         assert s.drafted >= s.accepted
+    # the longest sequence reaches context 256 + 128 + k in the verify
+    assert max(s.cycles for s in stats) > min(s.cycles for s in stats)
+
+
+@pytest.mark.parametrize("part", [0, 1])
+def test_cfg4_sampled_batch32_full_length_matches_oracle(cfg4, part):
+    """Six sequences over all 128 new tokens (contexts up to ~389 in the
+    verify, the lockstep tail after the first sequence finishes), each
+    against the oracle's single-sequence run keyed by its index; three per
+    test to keep each test short."""
+    got, stats, _ = cfg4["sampled"]
+    seqs = sampled_subset(stats)[3 * part:3 * part + 3]
     O.set_threads(THREADS)
+    diverged = 0
     try:
-        diverged = 0
-        for b in (0, 13, 31):
-            i = check_stream(ot, od, got[b], prompts[b], new, k, T, seed,
-                             seq=b, dev=stats[b], what=f"cfg4 b={b}")
+        for b in seqs:
+            print(f"cfg4 sampled: sequence {b} ({stats[b].cycles} cycles)",
+                  flush=True)
+            i = check_stream(cfg4["ot"], cfg4["od"], got[b], cfg4["prompts"][b],
+                             cfg4["new"], cfg4["k"], 1.0, cfg4["seed"], seq=b,
+                             dev=stats[b], what=f"cfg4 b={b}")
             diverged += i is not None
     finally:
         O.set_threads(1)
     # a divergence needs a decision within 1e-5 of its boundary: rare
     assert diverged <= 1
-    gt.free(); gd.free()
 
 
-def test_cfg4_greedy_batch32_matches_oracle(ctx):
-    """The same models in greedy mode (T = 0): exact streams."""
-    B, P, new, k = 32, 256, 12, 5
-    gt, ot = device_and_oracle(ctx, CFG4_T, 1234)
-    gd, od = device_and_oracle(ctx, CFG4_D, 5678)
-    rng = np.random.default_rng(2025)
-    prompts = rng.integers(0, CFG4_T["vocab"], (B, P)).astype(np.int32)
-    got, stats, _ = gt.generate_speculative_batch(gd, prompts, new, k, 0.0, 42)
+def test_cfg4_greedy_batch32_full_length_matches_oracle(cfg4):
+    """The same models in greedy mode (T = 0), 128 new tokens: exact
+    streams and acceptance counts for the first and last sequence."""
+    got, stats, _ = cfg4["greedy"]
     O.set_threads(THREADS)
     try:
         for b in (0, 31):
-            want, ost = O.generate_speculative(ot, od, prompts[b], new, k, 0.0,
-                                               42, seq=b)
+            print(f"cfg4 greedy: sequence {b}", flush=True)
+            want, ost = O.generate_speculative(
+                cfg4["ot"], cfg4["od"], cfg4["prompts"][b], cfg4["new"],
+                cfg4["k"], 0.0, cfg4["seed"], seq=b)
             np.testing.assert_array_equal(got[b], want)
             assert stats[b].accepted == ost.accepted
     finally:
         O.set_threads(1)
-    gt.free(); gd.free()
 
 
 def oracle_probs(rows, T):
