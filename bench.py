@@ -325,23 +325,36 @@ def roofline_gemm(fam, kern):
 def cfg3_cfg5(ctx):
     """The attention microbench (16 x 8 heads of 64, 2048 cached + 8 new
     queries, fp32) and the acceptance microbench (256 sequences x 8
-    positions x vocab 32000, T = 1), 1000 and 200 timed launches."""
+    positions x vocab 32000, T = 1), 1000 timed launches each."""
     ms = nnhip.bench_attention(ctx, 16, 8, 8, 64, 2048, iters=1000, nbuf=4)
     byt = attention_bytes(16, 8, 8, 64, 2048 + 8)
     c3 = dict(us=round(ms * 1e3, 2), bytes=byt,
               achieved_GBs=round(byt / (ms / 1e3) / 1e9, 1),
               frac=round(byt / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
-    ms5, nacc = nnhip.bench_spec_accept(ctx, 256, 8, 32000, 1.0, iters=200,
-                                        nbuf=3)
-    # algorithmic bytes: every target logit once (the softmax statistics
-    # of each position), then per sequence the target logits and draft
-    # probabilities of the one row the residual resample reads
-    b5 = 256 * 8 * 32000 * 4 + 256 * 2 * 32000 * 4
-    c5 = dict(us=round(ms5 * 1e3, 2), bytes=b5,
-              achieved_GBs=round(b5 / (ms5 / 1e3) / 1e9, 1),
-              frac=round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-              mean_accepted=round(float(np.mean(nacc)), 3))
+    c5 = cfg5_accept(ctx)
     return c3, c5
+
+
+CFG5 = dict(B=256, k=8, V=32000)
+
+
+def cfg5_accept(ctx, iters=1000):
+    """Logits in, (accepted count, resampled token) out: the draft rows'
+    tile statistics, the target rows' statistics and the accept / residual
+    kernel per launch (nnhip_spec_accept's path).  Algorithmic bytes: every
+    target and draft logit read once (dense: the kernels read every row,
+    with no early exit at the first rejection), 2 x 256 x 8 x 32000 x 4 =
+    524,288,000 B a launch."""
+    c = CFG5
+    ms5, nacc = nnhip.bench_spec_accept(ctx, c["B"], c["k"], c["V"], 1.0,
+                                        iters=iters, nbuf=3)
+    b5 = 2 * c["B"] * c["k"] * c["V"] * 4
+    return dict(us=round(ms5 * 1e3, 2), bytes=b5, iters=iters,
+                achieved_GBs=round(b5 / (ms5 / 1e3) / 1e9, 1),
+                frac=round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                mean_accepted=round(float(np.mean(nacc)), 3),
+                timed="draft tile statistics + target statistics + accept "
+                      "kernel, logits in")
 
 
 def traffic_probe():

@@ -264,8 +264,11 @@ int nnhip_layernorm_linear_w8a32(nnhip_ctx *ctx, const float *h, int rows,
  * rows64 = rows rounded up to 64) lives in one fixed 32 MiB device array per
  * GPU, held until the process ends; larger calls return NNHIP_EARG.  The
  * GEMV path (path 1, or path 0 below 16 rows) uses no scratch.  Stream-
- * ordered, no synchronisation.  Calls that overlap on one GPU (contexts on
- * different streams) race on the shared array. */
+ * ordered, no synchronisation.  The first context that calls it owns that
+ * GPU's array until nnhip_destroy: calls from any other context on the same
+ * GPU return NNHIP_EARG (two streams would race on the array).  Calls of
+ * the owning context are ordered by its stream; each call overwrites the
+ * array's contents. */
 int nnhip_linear_w8a32_noalloc(nnhip_ctx *ctx, const float *x, int rows,
                                int K, const int8_t *codes,
                                const float *scales, const float *bias, int N,

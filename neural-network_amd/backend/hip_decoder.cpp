@@ -227,13 +227,21 @@ void HipMultiHeadAttention::forward_device(const float *x, size_t B, size_t S,
     vc = fptr(*tv);
     cap = S;
   }
-  std::unique_ptr<DeviceBuffer> qkv = be_.allocate(rows * Nqkv * sizeof(float));
-  std::unique_ptr<DeviceBuffer> qrot = be_.allocate(rows * E * sizeof(float));
-  std::unique_ptr<DeviceBuffer> ctxo = be_.allocate(rows * E * sizeof(float));
-  std::unique_ptr<DeviceBuffer> pos = be_.allocate(B * sizeof(int32_t));
+  // the layer's scratch, reused in stream order; grown after the stream has
+  // drained (earlier calls may still read it)
+  if (rows > s_rows_ || B > s_B_) {
+    be_.synchronize();
+    s_rows_ = std::max(rows, s_rows_);
+    s_B_ = std::max(B, s_B_);
+    s_qkv_ = be_.allocate(s_rows_ * Nqkv * sizeof(float));
+    s_qrot_ = be_.allocate(s_rows_ * E * sizeof(float));
+    s_ctx_ = be_.allocate(s_rows_ * E * sizeof(float));
+    s_pos_ = be_.allocate(s_B_ * sizeof(int32_t));
+  }
+  DeviceBuffer *qkv = s_qkv_.get(), *qrot = s_qrot_.get(), *ctxo = s_ctx_.get();
   const std::vector<int32_t> hpos(B, (int32_t)past);
-  check(nnhip_h2d(ctx, pos->data(), hpos.data(), B * sizeof(int32_t)));
-  const int32_t *dpos = static_cast<const int32_t *>(pos->data());
+  check(nnhip_h2d(ctx, s_pos_->data(), hpos.data(), B * sizeof(int32_t)));
+  const int32_t *dpos = static_cast<const int32_t *>(s_pos_->data());
   // q | k | v rows, RoPE at the cache length and the append, attention
   if (quantized_)
     check(nnhip_linear_w8a32(ctx, x, (int)rows, (int)E, cptr(*cqkv_),
@@ -253,7 +261,7 @@ void HipMultiHeadAttention::forward_device(const float *x, size_t B, size_t S,
   else
     check(nnhip_linear_f32(ctx, fptr(*ctxo), (int)rows, (int)E, fptr(*wo_),
                            fptr(*bo_), (int)E, y));
-  be_.synchronize();  // the scratch above is freed on return
+  if (!cache) be_.synchronize();  // the temporary K / V are freed on return
   if (cache) cache->len_ += S;
 }
 

@@ -150,6 +150,10 @@ class HipMultiHeadAttention {
   // fused q | k | v: fp32 [Nqkv][E] or codes, scales, bias [Nqkv]; out: [E][E]
   std::unique_ptr<DeviceBuffer> wqkv_, wo_, cqkv_, co_, sqkv_, so_, bqkv_, bo_;
   std::vector<std::vector<float>> master_;  // parameters() as given
+  // forward scratch (q | k | v rows, rotated q, context rows, positions),
+  // kept across calls for up to s_rows_ rows of s_B_ sequences
+  std::unique_ptr<DeviceBuffer> s_qkv_, s_qrot_, s_ctx_, s_pos_;
+  size_t s_rows_ = 0, s_B_ = 0;
 };
 
 // KVCache for B sequences of one HipMultiHeadAttention: fp32 K / V

@@ -61,6 +61,7 @@ int nnhip_destroy(nnhip_ctx *ctx) {
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
     (void)hipStreamDestroy(ctx->c.stream);
+    nnhip::noalloc_release(ctx);
     delete ctx;
   });
 }
@@ -604,6 +605,36 @@ static void rope_tables(int cap, int D, std::vector<float> &hc,
     }
 }
 
+// The context's RoPE tables for head width D covering positions [0, cap):
+// built once per width (and again only when a call needs more positions,
+// after the stream has drained), so the append entry points neither compute
+// tables nor synchronise per call.
+static const nnhip_ctx::Rope &ctx_rope(nnhip_ctx *ctx, int cap, int D) {
+  nnhip_ctx::Rope *slot = nullptr;
+  for (auto &r : ctx->rope)
+    if (r.D == D) { slot = &r; break; }
+  if (!slot)
+    for (auto &r : ctx->rope)
+      if (r.D == 0) { slot = &r; break; }
+  if (!slot) slot = &ctx->rope[0];
+  if (slot->D == D && slot->n >= cap) return *slot;
+  hipStream_t st = ctx->c.stream;
+  NNHIP_CHECK(hipStreamSynchronize(st));   // earlier calls may read the old one
+  const int n = std::max(cap, slot->D == D ? 2 * slot->n : 1024);
+  std::vector<float> hc, hs;
+  rope_tables(n, D, hc, hs);
+  slot->c.alloc(hc.size());
+  slot->s.alloc(hs.size());
+  NNHIP_CHECK(hipMemcpyAsync(slot->c.p, hc.data(), hc.size() * 4,
+                             hipMemcpyHostToDevice, st));
+  NNHIP_CHECK(hipMemcpyAsync(slot->s.p, hs.data(), hs.size() * 4,
+                             hipMemcpyHostToDevice, st));
+  NNHIP_CHECK(hipStreamSynchronize(st));   // the host tables go out of scope
+  slot->D = D;
+  slot->n = n;
+  return *slot;
+}
+
 int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
                          int H, int D, const int32_t *pos, float *q_out,
                          float *kcache, float *vcache, int cap) {
@@ -612,13 +643,9 @@ int nnhip_rope_kv_append(nnhip_ctx *ctx, const float *qkv, int B, int S,
             H > 0 && D > 0 && D % 2 == 0 && cap > 0,
         "nnhip_rope_kv_append: bad argument");
     hipStream_t st = ctx->c.stream;
-    std::vector<float> hc, hs;
-    rope_tables(cap, D, hc, hs);
-    auto dc = upload(st, hc.data(), hc.size());
-    auto ds = upload(st, hs.data(), hs.size());
-    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
+    const nnhip_ctx::Rope &rt = ctx_rope(ctx, cap, D);
+    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, rt.c.p, rt.s.p,
                           q_out, kcache, vcache, cap, (int64_t)H * cap * D);
-    NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }
 
@@ -631,14 +658,10 @@ int nnhip_rope_kv_append_gqa(nnhip_ctx *ctx, const float *qkv, int B, int S,
             H > 0 && Hkv > 0 && H % Hkv == 0 && D > 0 && D % 2 == 0 && cap > 0,
         "nnhip_rope_kv_append_gqa: bad argument");
     hipStream_t st = ctx->c.stream;
-    std::vector<float> hc, hs;
-    rope_tables(cap, D, hc, hs);
-    auto dc = upload(st, hc.data(), hc.size());
-    auto ds = upload(st, hs.data(), hs.size());
-    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
+    const nnhip_ctx::Rope &rt = ctx_rope(ctx, cap, D);
+    nnhip::launch_rope_kv(st, qkv, B, S, H, D, pos, 0, nullptr, rt.c.p, rt.s.p,
                           q_out, kcache, vcache, cap, (int64_t)Hkv * cap * D,
                           Hkv);
-    NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }
 
@@ -652,12 +675,14 @@ int nnhip_attention_kq(nnhip_ctx *ctx, const float *q, const float *kcache,
     hipStream_t st = ctx->c.stream;
     const int max_keys = cap;
     const int64_t pe = nnhip::attention_partial_elems(B, S, H, D, max_keys);
-    nnhip::DevBuf<float> part(pe > 0 ? pe : 1);
+    if ((size_t)std::max<int64_t>(pe, 1) > ctx->part.n) {
+      NNHIP_CHECK(hipStreamSynchronize(st));   // earlier calls may read it
+      ctx->part.ensure((size_t)std::max<int64_t>(pe, 1));
+    }
     nnhip::KvSrc kv;
     kv.k = kcache; kv.v = vcache; kv.seq_stride = (int64_t)Hkv * cap * D;
     nnhip::launch_attention(st, q, kv, B, S, H, Hkv, D, cap, pos0, 0, nullptr,
-                            max_keys, part.p, pe, out);
-    NNHIP_CHECK(hipStreamSynchronize(st));
+                            max_keys, ctx->part.p, pe, out);
   });
 }
 
@@ -670,14 +695,10 @@ int nnhip_rope_kv_append_q8(nnhip_ctx *ctx, const float *qkv, int B, int S,
             B > 0 && S > 0 && H > 0 && D > 0 && D % 2 == 0 && D <= 64 && cap > 0,
         "nnhip_rope_kv_append_q8: bad argument");
     hipStream_t st = ctx->c.stream;
-    std::vector<float> hc, hs;
-    rope_tables(cap, D, hc, hs);
-    auto dc = upload(st, hc.data(), hc.size());
-    auto ds = upload(st, hs.data(), hs.size());
-    nnhip::launch_rope_kv_q8(st, qkv, B, S, H, D, pos, 0, nullptr, dc.p, ds.p,
-                             q_out, kcodes, kscales, vcodes, vscales, cap,
-                             (int64_t)H * cap * D, (int64_t)H * cap);
-    NNHIP_CHECK(hipStreamSynchronize(st));
+    const nnhip_ctx::Rope &rt = ctx_rope(ctx, cap, D);
+    nnhip::launch_rope_kv_q8(st, qkv, B, S, H, D, pos, 0, nullptr, rt.c.p,
+                             rt.s.p, q_out, kcodes, kscales, vcodes, vscales,
+                             cap, (int64_t)H * cap * D, (int64_t)H * cap);
   });
 }
 
@@ -733,18 +754,12 @@ int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
             n_accept && next_tok && B > 0 && k > 0 && V > 0,
         "nnhip_spec_accept: bad argument");
     hipStream_t st = ctx->c.stream;
+    // the draft rows' get_probs as the loop's drafting steps leave them:
+    // their logits and 128-column tile statistics, each probability formed
+    // where the accept step reads it
     nnhip::AcceptRows ar(B, k, V, temperature);
-    nnhip::DevBuf<float> q;
-    nnhip::DevBuf<int32_t> junk;
-    if (temperature > 0.f) {
-      // the drafting steps' get_probs of the draft rows (row_probs)
-      q.alloc((size_t)B * k * V);
-      junk.alloc((size_t)B * k);
-      nnhip::launch_sample_rows(st, dlogits, B * k, V, temperature, u_accept,
-                                junk.p, q.p);
-    }
-    ar.launch(st, tlogits, q.p, dtok, u_accept, u_resample, n_accept,
-              next_tok);
+    ar.launch_logits(st, tlogits, dlogits, dtok, u_accept, u_resample,
+                     n_accept, next_tok);
     NNHIP_CHECK(hipStreamSynchronize(st));
   });
 }

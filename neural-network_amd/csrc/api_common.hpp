@@ -16,6 +16,15 @@ struct nnhip_ctx {
   // (grown when a call needs more, after the stream has drained)
   nnhip::DevBuf<int8_t> limbs, sw;
   nnhip::DevBuf<int> rexp;
+  // RoPE cos / sin tables of the standalone append entry points, one per
+  // head width, for positions [0, n) (grown, after the stream has drained,
+  // when a call needs more positions), and the attention entry point's
+  // partial results
+  struct Rope {
+    int D = 0, n = 0;
+    nnhip::DevBuf<float> c, s;
+  } rope[4];
+  nnhip::DevBuf<float> part;
 };
 struct nnhip_model {
   std::unique_ptr<nnhip::Model> m;
@@ -30,6 +39,8 @@ void set_last_error(const std::string &msg);
 // resolves this device's copy of the fixed scratch array of
 // nnhip_linear_w8a32_noalloc (noalloc.hip); device must be current
 void noalloc_setup(int device);
+// gives up the scratch array a destroyed context owned
+void noalloc_release(const nnhip_ctx *ctx);
 
 template <typename F>
 int guard(F &&f) {

@@ -83,11 +83,13 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
   });
 }
 
-// Acceptance step of the speculative loop (target_stats_kernel +
-// accept_kernel, after a reset of the per-sequence state): B sequences x k
-// positions x V, target and draft logits N(0, 2), the draft rows' get_probs
-// formed once beforehand (the drafting steps form them in the loop), draft
-// ids drawn from them with a separate stream, one accept uniform per
+// Acceptance step of the speculative loop from logits, as
+// nnhip_spec_accept runs it: the draft rows' tile statistics
+// (row_tile_stats_kernel), the per-sequence state reset, the target rows'
+// statistics and the accept / residual kernel, timed together.  B sequences
+// x k positions x V, target and draft logits N(0, 2) (nbuf sets of each),
+// draft ids drawn from set 0's draft probabilities with a separate stream
+// beforehand (fixture preparation, not timed), one accept uniform per
 // position and one resample uniform per sequence.  n_accept (host, [B])
 // receives the accepted counts of input set 0.
 int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
@@ -98,9 +100,9 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
                   nnhip::kErrArg, "nnhip_bench_spec_accept: bad argument");
     hipStream_t st = ctx->c.stream;
     const int64_t n = (int64_t)B * k * V;
-    std::vector<nnhip::DevBuf<float>> TL(nbuf), Q(nbuf);
-    nnhip::DevBuf<float> dl(n);
-    nnhip::DevBuf<int32_t> dtok((size_t)B * k), nacc(B), next(B), junk((size_t)B * k);
+    std::vector<nnhip::DevBuf<float>> TL(nbuf), DL(nbuf);
+    nnhip::DevBuf<float> q0(n);
+    nnhip::DevBuf<int32_t> dtok((size_t)B * k), nacc(B), next(B);
     nnhip::DevBuf<float> ua((size_t)B * k), ur(B), us((size_t)B * k);
     // uniforms in [0, 1) from a fixed host xorshift stream
     std::vector<float> hu((size_t)B * k * 2 + B);
@@ -114,20 +116,19 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
     NNHIP_CHECK(hipMemcpyAsync(ur.p, hu.data() + 2 * B * k, (size_t)B * 4, hipMemcpyHostToDevice, st));
     const float Tq = T > 0.f ? T : 1.f;
     for (int i = 0; i < nbuf; ++i) {
-      TL[i].alloc(n); Q[i].alloc(n);
+      TL[i].alloc(n); DL[i].alloc(n);
       nnhip::launch_init_normal(st, TL[i].p, 1, (int)n, 0, 1, 4000 + i, 0, 2.f, 0);
-      nnhip::launch_init_normal(st, dl.p, 1, (int)n, 0, 1, 5000 + i, 0, 2.f, 0);
-      // draft probabilities; set 0's draws are the draft ids
-      nnhip::launch_sample_rows(st, dl.p, B * k, V, Tq, us.p,
-                                i == 0 ? dtok.p : junk.p, Q[i].p);
+      nnhip::launch_init_normal(st, DL[i].p, 1, (int)n, 0, 1, 5000 + i, 0, 2.f, 0);
     }
+    // set 0's draws from its draft probabilities are the draft ids
+    nnhip::launch_sample_rows(st, DL[0].p, B * k, V, Tq, us.p, dtok.p, q0.p);
     nnhip::AcceptRows ar(B, k, V, T);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      ar.launch(st, TL[j].p, Q[j].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
+      ar.launch_logits(st, TL[j].p, DL[j].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
     });
     if (n_accept) {
-      ar.launch(st, TL[0].p, Q[0].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
+      ar.launch_logits(st, TL[0].p, DL[0].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
       NNHIP_CHECK(hipMemcpyAsync(n_accept, nacc.p, (size_t)B * 4, hipMemcpyDeviceToHost, st));
       NNHIP_CHECK(hipStreamSynchronize(st));
     }

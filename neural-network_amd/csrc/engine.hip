@@ -684,7 +684,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.cur.alloc(B); bf.cand.alloc((size_t)B * k); bf.tlen.alloc(B);
   bf.dlen.alloc(B); bf.gen.alloc(B); bf.cyc.alloc(B); bf.active.alloc(B);
   bf.catchup.alloc(B); bf.catch_tok.alloc(B); bf.pair.alloc((size_t)2 * B);
-  bf.out.alloc((size_t)B * out_stride); bf.n_active.alloc(1);
+  bf.out.alloc((size_t)B * out_stride);
+  bf.n_active.alloc(2);   // n_active, n_far
   bf.prompts.alloc((size_t)B * P);
   // Drafting samples from the draft lm head's tile statistics when that lm
   // head forms them for the batch's row count; otherwise from full passes
@@ -708,7 +709,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   bf.tlog.alloc((size_t)B * (k + 1) * V);
   bf.stats.alloc((size_t)B * kSpecStats);
   NNHIP_CHECK(hipMemsetAsync(bf.stats.p, 0, bf.stats.bytes(), st));
-  NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 4, st));
+  NNHIP_CHECK(hipMemsetAsync(bf.n_active.p, 0, 8, st));
   NNHIP_CHECK(hipMemsetAsync(bf.cand.p, 0, bf.cand.bytes(), st));
   NNHIP_CHECK(hipMemsetAsync(bf.out.p, 0, bf.out.bytes(), st));
   NNHIP_CHECK(hipMemcpyAsync(bf.prompts.p, prompts, (size_t)B * P * 4,
@@ -725,7 +726,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   s.tlen = bf.tlen.p; s.dlen = bf.dlen.p; s.gen = bf.gen.p; s.cyc = bf.cyc.p;
   s.active = bf.active.p; s.catchup = bf.catchup.p;
   s.catch_tok = bf.catch_tok.p; s.pair = bf.pair.p; s.out = bf.out.p;
-  s.n_active = bf.n_active.p; s.stats = bf.stats.p;
+  s.n_active = bf.n_active.p; s.n_far = bf.n_active.p + 1;
+  s.stats = bf.stats.p;
   s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
   s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;
   s.top_k = top_k; s.top_p = top_p;
@@ -778,8 +780,9 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     launch_accept(st, s, bf.tlog.p);
   };
 
+  // per cycle parity: {n_active, n_far} after that cycle
   int32_t *h_nact = nullptr;
-  NNHIP_CHECK(hipHostMalloc((void **)&h_nact, 2 * sizeof(int32_t)));
+  NNHIP_CHECK(hipHostMalloc((void **)&h_nact, 4 * sizeof(int32_t)));
   hipEvent_t ev[2];
   NNHIP_CHECK(hipEventCreateWithFlags(&ev[0], hipEventDisableTiming));
   NNHIP_CHECK(hipEventCreateWithFlags(&ev[1], hipEventDisableTiming));
@@ -801,18 +804,32 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
         NNHIP_CHECK(hipStreamEndCapture(st, &graph));
         NNHIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
       }
-      // each cycle commits at least one token per active sequence
+      // Each cycle commits at least one and at most k + 1 tokens per active
+      // sequence.  The host reads the counts one cycle behind, so that the
+      // device never waits for it; once no sequence had more than k + 1
+      // tokens to go after cycle c - 1, cycle c may finish them all, and
+      // the host waits for its counts before it launches another (no cycle
+      // runs after the last sequence finished).
       const int max_cycles = max_new - 1;
       for (int c = 0; c < max_cycles; ++c) {
         if (exec) NNHIP_CHECK(hipGraphLaunch(exec, st));
         else cycle();
         ++launched;
-        NNHIP_CHECK(hipMemcpyAsync(&h_nact[c & 1], bf.n_active.p, 4,
+        int32_t *hc = &h_nact[2 * (c & 1)];
+        NNHIP_CHECK(hipMemcpyAsync(hc, bf.n_active.p, 8,
                                    hipMemcpyDeviceToHost, st));
         NNHIP_CHECK(hipEventRecord(ev[c & 1], st));
+        // after the first token every active sequence has max_new - 1 to go
+        bool near = c == 0 && max_new - 1 <= k + 1;
         if (c >= 1) {
+          const int32_t *hp = &h_nact[2 * ((c - 1) & 1)];
           NNHIP_CHECK(hipEventSynchronize(ev[(c - 1) & 1]));
-          if (h_nact[(c - 1) & 1] == 0) break;
+          if (hp[0] == 0) break;
+          near = hp[1] == 0;
+        }
+        if (near) {
+          NNHIP_CHECK(hipEventSynchronize(ev[c & 1]));
+          if (hc[0] == 0) break;
         }
       }
     }

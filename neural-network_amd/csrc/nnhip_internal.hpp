@@ -541,6 +541,9 @@ struct SpecState {
   // draft probability, which is then computed where it is needed instead
   // of being written out at each step (sampled mode without top-k / top-p)
   const float *qlog = nullptr;
+  // row of step j, sequence b in qlog: qlog + j*qlog_js + b*qlog_bs (0: the
+  // loop's [k][B][V] layout, js = B*V, bs = V)
+  int64_t qlog_js = 0, qlog_bs = 0;
   float *tstat;        // [B][k+1][kTstat] verify-row statistics (accept)
   int32_t *tlen;       // [B] target cache length
   int32_t *dlen;       // [B] draft cache length
@@ -553,6 +556,10 @@ struct SpecState {
                        // first draft forward
   int32_t *out;        // [B][out_stride] prompt + generated ids
   int32_t *n_active;   // [1]
+  // [1] active sequences that cannot finish within one more cycle (more than
+  // k + 1 tokens to go), or null: the host stops launching cycles once the
+  // ones it has launched are sure to finish every sequence
+  int32_t *n_far = nullptr;
   int64_t *stats;      // [B][kSpecStats] cycles, drafted, accepted, ties,
                        // resampled, bonus, and the largest target / draft
                        // cache lengths the reference's forwards reach
@@ -601,12 +608,28 @@ struct AcceptRows {
   DevBuf<int32_t> cur, tlen, dlen, gen, cyc, active, catchup, catch_tok, pair,
       out, n_active;
   DevBuf<float> tstat;
+  DevBuf<float2> dtiles;   // [B][k][nt] draft-row tile statistics
   DevBuf<int64_t> stats;
   SpecState s;
   AcceptRows(int B, int k, int V, float T);
+  // from draft probabilities qprob [B][k][V] (null in greedy mode)
   void launch(hipStream_t st, const float *tlogits, const float *qprob,
               const int32_t *cand, const float *ua, const float *ur,
               int32_t *n_acc, int32_t *tok);
+  // from draft logits dlogits [B][k][V]: their 128-column tile statistics
+  // (launch_row_tile_stats), then the accept step forms each draft
+  // probability it reads from the logit and the row's statistics, as the
+  // loop's drafting steps leave them (SpecState::qlog)
+  void launch_logits(hipStream_t st, const float *tlogits,
+                     const float *dlogits, const int32_t *cand, const float *ua,
+                     const float *ur, int32_t *n_acc, int32_t *tok);
 };
+// Softmax statistics per 128-column tile of each row of logits [rows][V]
+// (rows ldl apart), the TileStatsArgs values the LDS GEMM's lm-head epilogue
+// forms: out[r * nt + t] = (max s, sum exp(s - max)) over the tile's
+// columns, s = l / T (T > 0), or (max l, first index of the max) (T <= 0);
+// nt = ceil(V / 128).
+void launch_row_tile_stats(hipStream_t st, const float *logits, int64_t ldl,
+                           int rows, int V, float T, float2 *out);
 
 }  // namespace nnhip

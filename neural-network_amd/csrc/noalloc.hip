@@ -6,6 +6,9 @@
 // GPU the library runs on holds until the process ends.  Each device's copy
 // has its own address, resolved once per device by noalloc_setup (called by
 // nnhip_init with that device current); host code uses only that address.
+// One context at a time owns a device's array: calls from another context
+// on the same GPU (another stream, which nothing would order against the
+// owner's) are refused until the owner is destroyed.
 #include "api_common.hpp"
 
 #include <mutex>
@@ -19,6 +22,7 @@ static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
 
 std::mutex g_scratch_mu;
 void *g_scratch_dev[kMaxDevices] = {};
+const nnhip_ctx *g_scratch_owner[kMaxDevices] = {};
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
@@ -37,6 +41,12 @@ void noalloc_setup(int device) {
   g_scratch_dev[device] = p;
 }
 
+void noalloc_release(const nnhip_ctx *ctx) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  for (auto &o : g_scratch_owner)
+    if (o == ctx) o = nullptr;
+}
+
 }  // namespace nnhip
 
 using nnhip::guard;
@@ -53,12 +63,19 @@ int nnhip_linear_w8a32_noalloc(nnhip_ctx *ctx, const float *x, int rows,
     NNHIP_REQUIRE(path >= 0 && path <= 4, nnhip::kErrArg, "unknown path");
     NNHIP_CHECK(hipSetDevice(ctx->c.device));
     void *base = nullptr;
+    bool mine = false;
     {
       std::lock_guard<std::mutex> lk(g_scratch_mu);
       base = g_scratch_dev[ctx->c.device];
+      const nnhip_ctx *&owner = g_scratch_owner[ctx->c.device];
+      if (!owner) owner = ctx;
+      mine = owner == ctx;
     }
     NNHIP_REQUIRE(base, nnhip::kErrHip,
                   "nnhip_linear_w8a32_noalloc: scratch not set up for this device");
+    NNHIP_REQUIRE(mine, nnhip::kErrArg,
+                  "nnhip_linear_w8a32_noalloc: this GPU's scratch belongs to "
+                  "another context (calls on two streams would race on it)");
     hipStream_t st = ctx->c.stream;
     const bool mfma_ok = K % 128 == 0 && N % 64 == 0;
     const bool lds = path == 3 || path == 4;

@@ -477,6 +477,7 @@ __device__ __forceinline__ int draw_row(const float *row, int V, float T, float 
 // that difference of a CDF step (a tie).
 // ---------------------------------------------------------------------------
 constexpr int kTileMax = 16;   // tiles per lane of one wave: rows <= 1024 tiles
+constexpr int kTileW = 128;    // columns of a tile (the lm head's column block)
 
 // RowStats (T > 0) of a row from its nt tile statistics, by one wave
 __device__ __forceinline__ RowStats wave_tiles_stats(const float2 *__restrict__ tl,
@@ -650,6 +651,35 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
   embed_next(s, b, j, tok, s_emb, s_red);
 }
 
+// Tile statistics of rows of logits (launch_row_tile_stats): one wave per
+// 128-column tile, two columns a lane, the same operations in the same order
+// as the LDS GEMM's lm-head epilogue, so a row gives the same statistics
+// whether they come from there or from here.
+__global__ __launch_bounds__(kThreads) void row_tile_stats_kernel(
+    const float *__restrict__ logits, int64_t ldl, int V, float T, int nt,
+    float2 *__restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int tn = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t r = blockIdx.y;
+  if (tn >= nt) return;                       // whole wave
+  const int n = tn * kTileW + 2 * lane;
+  const float *row = logits + r * ldl;
+  const float l0 = n < V ? row[n] : 0.f, l1 = n + 1 < V ? row[n + 1] : 0.f;
+  if (T > 0.f) {
+    const float s0 = n < V ? scaled(l0, T) : -INFINITY;
+    const float s1 = n + 1 < V ? scaled(l1, T) : -INFINITY;
+    const float mx = wave_max_all(fmaxf(s0, s1));
+    const float e = wave_sum_all((n < V ? expf(s0 - mx) : 0.f) +
+                                 (n + 1 < V ? expf(s1 - mx) : 0.f));
+    if (lane == 0) out[r * nt + tn] = make_float2(mx, e);
+  } else {
+    const float a0 = n < V ? l0 : -INFINITY, a1 = n + 1 < V ? l1 : -INFINITY;
+    const float mx = wave_max_all(fmaxf(a0, a1));
+    const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
+    if (lane == 0) out[r * nt + tn] = make_float2(mx, __int_as_float(ix));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // First token after the prefill (layer.cpp:1500-1510): cycle 0, slot 2k.
 // ---------------------------------------------------------------------------
@@ -677,6 +707,7 @@ __global__ __launch_bounds__(kThreads) void first_token_kernel(
     const int act = s.max_new > 1 ? 1 : 0;
     s.active[b] = act;
     if (act) atomicAdd(s.n_active, 1);
+    if (act && s.n_far && s.max_new - 1 > s.k + 1) atomicAdd(s.n_far, 1);
   }
 }
 
@@ -817,7 +848,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     }
     __syncthreads();
   }
-  auto qlrow = [&](int j) { return s.qlog + ((int64_t)j * s.B + b) * V; };
+  const int64_t qjs = s.qlog_js ? s.qlog_js : (int64_t)s.B * V;
+  const int64_t qbs = s.qlog_bs ? s.qlog_bs : (int64_t)V;
+  auto qlrow = [&](int j) { return s.qlog + j * qjs + b * qbs; };
   auto q_of = [&](float l, int j) {
     return (expf(scaled(l, s.T) - qst[j].mx) * qst[j].rsum) * qst[j].rfs;
   };
@@ -930,6 +963,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
       s.catchup[b] = 0;
       atomicSub(s.n_active, 1);
     }
+    // no longer sure to need more than the next cycle
+    if (s.n_far && s.max_new - gen0 > k + 1 && s.max_new - gen <= k + 1)
+      atomicSub(s.n_far, 1);
   }
 }
 
@@ -1077,6 +1113,44 @@ AcceptRows::AcceptRows(int B, int k, int V, float T) {
   s.n_active = n_active.p; s.stats = stats.p;
   s.B = B; s.out_stride = k + 1; s.P = 0; s.max_new = k; s.k = k; s.V = V;
   s.T = T; s.trows = k; s.top_k = 0; s.top_p = 1.f;
+}
+
+void launch_row_tile_stats(hipStream_t st, const float *logits, int64_t ldl,
+                           int rows, int V, float T, float2 *out) {
+  NNHIP_REQUIRE(rows > 0 && V > 0 && ldl >= V && rows <= 65535, kErrArg,
+                "row tile statistics: bad sizes");
+  const int nt = (V + kTileW - 1) / kTileW;
+  hipLaunchKernelGGL(row_tile_stats_kernel, dim3((nt + kWaves - 1) / kWaves, rows),
+                     dim3(kThreads), 0, st, logits, ldl, V, T, nt, out);
+  NNHIP_CHECK(hipGetLastError());
+}
+
+void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
+                               const float *dlogits, const int32_t *cand,
+                               const float *ua, const float *ur, int32_t *n_acc,
+                               int32_t *tok) {
+  if (s.T <= 0.f) {   // greedy: the draft probabilities are not read
+    launch(st, tlogits, nullptr, cand, ua, ur, n_acc, tok);
+    return;
+  }
+  const int nt = (s.V + kTileW - 1) / kTileW;
+  NNHIP_REQUIRE(nt <= kTileMax * 64, kErrUnsupported,
+                "accept: more than 1024 tiles of draft statistics");
+  if (!dtiles.p) dtiles.alloc((size_t)s.B * s.k * nt);
+  launch_row_tile_stats(st, dlogits, s.V, s.B * s.k, s.V, s.T, dtiles.p);
+  SpecState a = s;
+  a.qlog = dlogits;
+  a.qlog_js = s.V;
+  a.qlog_bs = (int64_t)s.k * s.V;
+  a.dtiles = dtiles.p;
+  a.nt = nt;
+  a.tw = kTileW;
+  a.cand = const_cast<int32_t *>(cand);
+  a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
+  hipLaunchKernelGGL(accept_rows_reset_kernel, dim3((s.B + 255) / 256),
+                     dim3(256), 0, st, a);
+  NNHIP_CHECK(hipGetLastError());
+  launch_accept(st, a, tlogits);
 }
 
 void AcceptRows::launch(hipStream_t st, const float *tlogits, const float *qprob,

@@ -93,6 +93,10 @@ def test_cfg4_sampled_batch32_device_invariants(cfg4):
         assert s.drafted >= s.accepted
     # the longest sequence reaches context 256 + 128 + k in the verify
     assert max(s.cycles for s in stats) > min(s.cycles for s in stats)
+    # no cycle is launched after the last sequence finished
+    assert cfg4["sampled"][2].cycles_launched == max(s.cycles for s in stats)
+    assert cfg4["greedy"][2].cycles_launched == max(
+        s.cycles for s in cfg4["greedy"][1])
 
 
 @pytest.mark.parametrize("part", [0, 1])

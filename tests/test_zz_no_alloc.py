@@ -47,7 +47,12 @@ def test_noalloc_matches_allocating_linear(ctx, path):
 def test_noalloc_gemv_and_limit(ctx):
     want, got = linear_pair(ctx, 5, 512, 640, 0, seed=3)
     np.testing.assert_array_equal(got, want)
-    # 32000 x 1024 codes alone exceed the 32 MiB array
+    # just under the limit: 32512 x 1024 codes + 3 x 64 x 1024 digits + 64
+    # exponents = 33,489,152 of 33,554,432 bytes
+    want, got = linear_pair(ctx, 64, 1024, 32512, 2, seed=4)
+    np.testing.assert_array_equal(got, want)
+    # 32768 x 1024 codes alone fill the 32 MiB array; with the digit planes
+    # and exponents the call exceeds it
     rows, K, N = 64, 1024, 32768
     dx = ctx.array(shape=(rows, K))
     dc = ctx.array(shape=(N, K), dtype=np.int8)
@@ -59,3 +64,29 @@ def test_noalloc_gemv_and_limit(ctx):
     assert e.value.code == nnhip.EARG
     for arr in (dx, dc, ds, db, y):
         arr.free()
+
+
+def test_noalloc_refuses_a_second_context(ctx):
+    """The first context that called the entry point owns this GPU's array;
+    another context's call would run on another stream, unordered against
+    the owner's, and is refused with NNHIP_EARG (no launch)."""
+    want, got = linear_pair(ctx, 20, 256, 512, 2, seed=5)
+    np.testing.assert_array_equal(got, want)
+    other = nnhip.Context(0)
+    try:
+        rows, K, N = 20, 256, 512
+        dx = other.array(shape=(rows, K))
+        dc = other.array(shape=(N, K), dtype=np.int8)
+        ds, db = other.array(shape=(N,)), other.array(shape=(N,))
+        y = other.array(shape=(rows, N))
+        with pytest.raises(nnhip.NNHipError) as e:
+            nnhip.call("nnhip_linear_w8a32_noalloc", other.h, dx.p, rows, K,
+                       dc.p, ds.p, db.p, N, y.p, 2)
+        assert e.value.code == nnhip.EARG
+        for arr in (dx, dc, ds, db, y):
+            arr.free()
+    finally:
+        other.close()
+    # the owner keeps working
+    want, got = linear_pair(ctx, 20, 256, 512, 2, seed=6)
+    np.testing.assert_array_equal(got, want)
