@@ -163,20 +163,25 @@ TRAFFIC_NOTE = os.path.join(ROOT, "profiles", "attention_verify_traffic.md")
 GEMM_NOTE = os.path.join(ROOT, "profiles", "gemm_cycle_shapes.md")
 
 
-def measured_traffic(note=TRAFFIC_NOTE, kernel=None):
-    """HBM bytes per launch of a kernel as measured by the rocprofv3
-    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (the note's
-    traffic_bytes_per_launch line, or traffic_bytes_per_launch[kernel])."""
-    key = ("traffic_bytes_per_launch" if kernel is None
-           else f"traffic_bytes_per_launch[{kernel}]") + ":"
+def profile_value(note, key, kernel=None, cast=float):
+    """A figure recorded in a profiles/ note as a `key: value` or
+    `key[kernel]: value` line, or None."""
+    key = (key if kernel is None else f"{key}[{kernel}]") + ":"
     try:
         with open(note) as f:
             for line in f:
                 if line.startswith(key):
-                    return int(line.split(":")[1])
+                    return cast(line.split(":")[1])
     except OSError:
         pass
     return None
+
+
+def measured_traffic(note=TRAFFIC_NOTE, kernel=None):
+    """HBM bytes per launch of a kernel as measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (the note's
+    traffic_bytes_per_launch line, or traffic_bytes_per_launch[kernel])."""
+    return profile_value(note, "traffic_bytes_per_launch", kernel, int)
 
 
 def roofline_attention(ctx, w4=True, q8=False):
@@ -281,13 +286,20 @@ def gemm_bytes(rows, K, N, path):
     return N * K + 8 * N + act + rows * N * 4
 
 
+GEMM_LAUNCH_SCALE = 10
+
+
 def gemm_table(ctx):
-    """Each GEMM shape of the cycle timed alone (HIP events around 100
-    launches over 4 weight sets), its bytes and int8 MFMA rate, then per
-    kernel family the launch-weighted totals per cycle."""
+    """Each GEMM shape of the cycle timed alone (HIP events around
+    GEMM_LAUNCH_SCALE x its launches per cycle, after one warm-up launch,
+    over 4 weight sets), its bytes and int8 MFMA rate, then per kernel
+    family the launch-weighted totals per cycle.  The launch counts follow
+    the cycle's, so a kernel trace of `bench.py --gemm-probe` (which runs
+    this table) averages each family over the same mix of shapes."""
     rows_out, fam = [], {}
     for name, rows, K, N, path, kern, n in CYCLE_GEMMS:
-        ms = nnhip.bench_linear(ctx, rows, K, N, path, iters=100, nbuf=4)
+        ms = nnhip.bench_linear(ctx, rows, K, N, path,
+                                iters=GEMM_LAUNCH_SCALE * n, nbuf=4)
         us = ms * 1e3
         byt = gemm_bytes(rows, K, N, path)
         ops = 3 * 2 * rows * K * N
@@ -307,19 +319,36 @@ def gemm_table(ctx):
     return rows_out, families, fam
 
 
+DECODE_NOTE = os.path.join(ROOT, "profiles", "decode_b32_k5_kernel_stats.md")
+
+
 def roofline_gemm(fam, kern):
     """HBM roofline of one GEMM kernel family over the cycle's launches:
-    launch-weighted algorithmic bytes over launch-weighted time."""
+    launch-weighted algorithmic bytes over launch-weighted time (HIP events,
+    this run; `frac`).  Beside it, the same bytes over the family's mean
+    kernel duration in two committed kernel traces: of `bench.py
+    --gemm-probe`, which runs the same launches as this table
+    (`profile_frac`), and of the decode loop itself, where each launch
+    follows other kernels and finds less of its data in cache
+    (`in_loop_frac`)."""
     f = fam[kern]
     ach = f["bytes"] / f["us"] / 1e3
-    return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
-                unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
-                traffic=measured_traffic(GEMM_NOTE, kern),
-                kernel=kern, launches_per_cycle=f["launches"],
-                us_per_launch=round(f["us"] / f["launches"], 2),
-                bytes_per_launch=int(f["bytes"] / f["launches"]),
-                mfma_TOPS_3digit=round(f["ops"] / f["us"] / 1e6, 1),
-                mfma_frac=round(f["ops"] / f["us"] / 1e6 / INT8_PEAK_TOPS, 4))
+    byt = f["bytes"] / f["launches"]
+    out = dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
+               unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
+               traffic=measured_traffic(GEMM_NOTE, kern),
+               kernel=kern, launches_per_cycle=f["launches"],
+               us_per_launch=round(f["us"] / f["launches"], 3),
+               bytes_per_launch=int(byt),
+               mfma_TOPS_3digit=round(f["ops"] / f["us"] / 1e6, 1),
+               mfma_frac=round(f["ops"] / f["us"] / 1e6 / INT8_PEAK_TOPS, 4))
+    for tag, note, key in (("profile", GEMM_NOTE, "kernel_trace_us_per_launch"),
+                           ("in_loop", DECODE_NOTE, "in_loop_us_per_launch")):
+        us = profile_value(note, key, kern)
+        out[f"{tag}_us_per_launch"] = us
+        out[f"{tag}_frac"] = (round(byt / us / 1e3 / HBM_PEAK_GBS, 4)
+                              if us else None)
+    return out
 
 
 def cfg3_cfg5(ctx):
@@ -336,6 +365,7 @@ def cfg3_cfg5(ctx):
 
 
 CFG5 = dict(B=256, k=8, V=32000)
+CFG5_NOTE = os.path.join(ROOT, "profiles", "cfg5_accept_kernel_stats.md")
 
 
 def cfg5_accept(ctx, iters=1000):
@@ -349,12 +379,23 @@ def cfg5_accept(ctx, iters=1000):
     ms5, nacc = nnhip.bench_spec_accept(ctx, c["B"], c["k"], c["V"], 1.0,
                                         iters=iters, nbuf=3)
     b5 = 2 * c["B"] * c["k"] * c["V"] * 4
+    # the kernel trace of `bench.py --cfg5-probe` (this function alone):
+    # the mean durations of the three kernels summed per launch
+    us_prof = profile_value(CFG5_NOTE, "kernel_trace_us_per_launch")
     return dict(us=round(ms5 * 1e3, 2), bytes=b5, iters=iters,
                 achieved_GBs=round(b5 / (ms5 / 1e3) / 1e9, 1),
                 frac=round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                profile_us=us_prof,
+                profile_frac=(round(b5 / us_prof / 1e3 / HBM_PEAK_GBS, 4)
+                              if us_prof else None),
                 mean_accepted=round(float(np.mean(nacc)), 3),
                 timed="draft tile statistics + target statistics + accept "
                       "kernel, logits in")
+
+
+def cfg5_probe():
+    """For rocprofv3 --kernel-trace: the acceptance microbench alone."""
+    log(json.dumps(cfg5_accept(nnhip.Context(0))))
 
 
 def traffic_probe():
@@ -383,15 +424,17 @@ def copy_calibration():
 
 
 def gemm_probe():
-    """For rocprofv3 --pmc runs: the copy calibration, then every GEMM shape
-    of the batch-32 cycle (20 launches each, the kernel alone over digit
-    planes made once, or digitising fp32 rows for the output projections)
-    and the prefill's gate/up projection (8192 rows = 32 prompts x 256)."""
+    """For rocprofv3 runs: the copy calibration, then the GEMM table of
+    the batch-32 cycle exactly as bench.py times it (gemm_table: one
+    warm-up launch and GEMM_LAUNCH_SCALE x the cycle's launches per shape,
+    the kernel alone over digit planes made once) and the prefill's gate/up
+    projection (8192 rows = 32 prompts x 256, 21 launches)."""
     copy_calibration()
     ctx = nnhip.Context(0)
-    for name, rows, K, N, path, kern, n in CYCLE_GEMMS:
-        ms = nnhip.bench_linear(ctx, rows, K, N, path, iters=20, nbuf=4)
-        log(f"{name}: {rows}x{K}x{N} path {path} {ms * 1e3:.2f} us")
+    rows_out, families, _ = gemm_table(ctx)
+    for r in rows_out:
+        log(f"{r['name']}: {r['rows']}x{r['K']}x{r['N']} {r['us']:.2f} us")
+    log(json.dumps(families))
     ms = nnhip.bench_linear(ctx, B * P, 1024, 8192, 7, iters=20, nbuf=2)
     log(f"prefill gate/up: {B * P}x1024x8192 path 7 {ms * 1e3:.2f} us")
 
@@ -486,6 +529,9 @@ def main():
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only run the copy calibration and the cycle's GEMM "
                          "shapes (for rocprofv3 --pmc)")
+    ap.add_argument("--cfg5-probe", action="store_true",
+                    help="only run the acceptance microbench (for "
+                         "rocprofv3 --kernel-trace)")
     ap.add_argument("--gemv-probe", action="store_true",
                     help="only run the copy calibration and the batch-1 "
                          "GEMVs (for rocprofv3 --pmc)")
@@ -513,6 +559,9 @@ def main():
         return
     if a.gemv_probe:
         gemv_probe()
+        return
+    if a.cfg5_probe:
+        cfg5_probe()
         return
     ctx = nnhip.Context(0)
     if a.no_graphs:

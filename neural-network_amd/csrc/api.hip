@@ -93,6 +93,7 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
       nnhip::g_o_limb_rows = value;
     }
     else if (std::strcmp(key, "o_head_digits") == 0) nnhip::g_o_head_digits = value != 0;
+    else if (std::strcmp(key, "persistent_draft") == 0) nnhip::g_persistent_draft = value != 0;
     else if (std::strcmp(key, "kv_stream") == 0) {
       REQ(value >= 0 && value <= 2, "kv_stream must be 0, 1 or 2");
       nnhip::g_kv_stream = value;
@@ -275,6 +276,8 @@ int nnhip_decoder_forward(nnhip_model *mm, nnhip_kvcache *cache,
     if (kv) for (int b = 0; b < B; ++b) max_keys = std::max(max_keys, kv->host_len[b] + S);
     m.forward(kv, 0, d_ids.p, S, B, S, kv ? kv->len.p : nullptr, 0, nullptr,
               max_keys, d_log.p, false);
+    NNHIP_CHECK(hipStreamSynchronize(st));
+    m.check_pd();
     NNHIP_CHECK(hipMemcpyAsync(logits, d_log.p, d_log.bytes(), hipMemcpyDeviceToHost, st));
     if (kv) {
       for (int b = 0; b < B; ++b) kv->host_len[b] += S;

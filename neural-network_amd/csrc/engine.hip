@@ -10,6 +10,7 @@ namespace nnhip {
 
 int g_lds_min_rows = 128;
 int g_o_limb_rows = 256;
+int g_persistent_draft = 0;
 int g_gemv_down_rows = 64;
 int g_o_head_digits = 1;
 
@@ -300,6 +301,48 @@ void Model::reserve(int rows, int lrows, int max_keys) {
     ws.part.alloc(pe);
     ws.part_elems = pe;
   }
+  // the persistent layer kernel's state for short batches, once the option
+  // is on
+  if (g_persistent_draft && rows > pd_rows && rows <= 64 &&
+      draft_layers_supported(d, H, F, L, rows, 1)) {
+    if (!pd_nwg) {
+      int dev = 0, ncu = 0;
+      NNHIP_CHECK(hipGetDevice(&dev));
+      NNHIP_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+      pd_nwg = std::max(1, ncu);
+      pd_flags.alloc(pd_nwg);
+      pd_tflags.alloc((size_t)L * 5 * kPdFlagSlot);
+      pd_err.alloc(1);
+      NNHIP_CHECK(hipMemsetAsync(pd_flags.p, 0, pd_flags.bytes(), ctx->stream));
+      NNHIP_CHECK(hipMemsetAsync(pd_tflags.p, 0, pd_tflags.bytes(), ctx->stream));
+      NNHIP_CHECK(hipMemsetAsync(pd_err.p, 0, pd_err.bytes(), ctx->stream));
+    }
+    pd_rows = std::max(rows, 32);
+    pd_ring.alloc((size_t)L * pd_ring_layer_floats(pd_rows, d, F));
+  }
+}
+
+bool Model::use_pd(int rows, int S, const KVCache *kv) const {
+  if (!(g_persistent_draft && quantized && kv && !kv->q8 && S >= 1 && S <= 2 &&
+        rows <= pd_rows && pd_ring.p &&
+        draft_layers_supported(d, H, F, L, rows, kv->cap)))
+    return false;
+  for (const auto &ly : layers)
+    if (!ly.qkv.q.p || !ly.o.q.p || !ly.gu.q.p || !ly.down.q.p) return false;
+  return true;
+}
+
+void Model::check_pd() {
+  if (!pd_err.p) return;
+  int e = 0;
+  NNHIP_CHECK(hipMemcpy(&e, pd_err.p, 4, hipMemcpyDeviceToHost));
+  if (!e) return;
+  NNHIP_CHECK(hipMemset(pd_flags.p, 0, pd_flags.bytes()));
+  NNHIP_CHECK(hipMemset(pd_tflags.p, 0, pd_tflags.bytes()));
+  NNHIP_CHECK(hipMemset(pd_err.p, 0, pd_err.bytes()));
+  NNHIP_CHECK(hipDeviceSynchronize());
+  throw Error(kErrHip, "persistent decoder-layer kernel: a wait for another "
+                       "workgroup's tile timed out (results of that forward are invalid)");
 }
 
 bool Model::use_limbs(const Linear &ln, int rows) const {
@@ -437,19 +480,47 @@ void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
   reserve(R, logits ? (last_only ? B : R) : 0, max_keys);
   Workspace &ws = wsp;
   const int32_t *bp = base ? base : ws.zeros.p;
-  // the embedding kernel also writes the rows' digits for the first q/k/v
-  // GEMM when that is an MFMA GEMM
-  const bool emb_digits = this->emb_digits(R);
-  if (!embedded)
-    launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
-                         emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p,
-                         lead);
   // Post-norm blocks (layer.cpp:1098-1113): each LayerNorm is applied by the
   // linear that consumes it (norm1 -> ffn gate/up, norm2 -> next q/k/v or
   // the lm head), which also writes the normalised rows for the residual.
   PendingNorm norm2;            // norm2 of the previous layer, if any
   bool have_norm2 = false;
-  for (int l = 0; l < L; ++l) {
+  const bool pd = use_pd(R, S, kv);
+  // the embedding kernel also writes the rows' digits for the first q/k/v
+  // GEMM when that is an MFMA GEMM
+  const bool emb_digits = !pd && this->emb_digits(R);
+  if (!embedded)
+    launch_embed_strided(st, emb.p, V, d, ids, B, S, ids_stride, ws.x.p,
+                         emb_digits ? ws.limbs.p : nullptr, ws.mpad, ws.rexp.p,
+                         lead);
+  if (pd) {
+    // every layer in one persistent kernel; its output is the last layer's
+    // t2 before LN2, which the lm head applies
+    PdArgs pa;
+    pa.R = R; pa.S = S; pa.B = B; pa.d = d; pa.H = H; pa.D = D; pa.F = F;
+    pa.L = L; pa.cap = kv->cap; pa.off = off;
+    pa.seq_stride = kv->seq_stride();
+    pa.x0 = ws.x.p; pa.base = bp; pa.active = active;
+    pa.cosb = cosb.p; pa.sinb = sinb.p;
+    pa.out = ws.h.p; pa.ring = pd_ring.p;
+    pa.flags = pd_flags.p; pa.tflags = pd_tflags.p; pa.err = pd_err.p;
+    for (int l = 0; l < L; ++l) {
+      const LayerW &ly = layers[l];
+      const KvSrc kvs = kv->src(l, b_off);
+      PdLayer &p = pa.ly[l];
+      p.wqkv = ly.qkv.q.p; p.wo = ly.o.q.p; p.wgu = ly.gu.q.p; p.wdn = ly.down.q.p;
+      p.sqkv = ly.qkv.s.p; p.so = ly.o.s.p; p.sgu = ly.gu.s.p; p.sdn = ly.down.s.p;
+      p.bqkv = ly.qkv.b.p; p.bo = ly.o.b.p; p.bgu = ly.gu.b.p; p.bdn = ly.down.b.p;
+      p.g1 = ly.g1.p; p.b1 = ly.b1.p; p.g2 = ly.g2.p; p.b2 = ly.b2.p;
+      p.kc = (float *)kvs.k; p.vc = (float *)kvs.v;
+    }
+    launch_draft_layers(st, pa, pd_nwg);
+    norm2.h = ws.h.p; norm2.ldh = d;
+    norm2.g = layers[L - 1].g2.p; norm2.b = layers[L - 1].b2.p;
+    norm2.out = ws.x.p; norm2.ldo = d;
+    have_norm2 = true;
+  }
+  for (int l = 0; l < (pd ? 0 : L); ++l) {
     LayerW &ly = layers[l];
     const KvSrc kvs = kv->src(l, b_off);
     // the int8 append runs in the LDS GEMM's epilogue (each head's pairs on
@@ -859,6 +930,8 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
     timing->decode_ms = ms_dec;
     timing->cycles_launched = launched;
   }
+  t.check_pd();
+  dm.check_pd();
   std::vector<int64_t> hs((size_t)B * kSpecStats);
   NNHIP_CHECK(hipMemcpy(hs.data(), bf.stats.p, hs.size() * 8,
                         hipMemcpyDeviceToHost));

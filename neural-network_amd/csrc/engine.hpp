@@ -66,6 +66,18 @@ struct Model {
   // has no length check in the reference)
   void ensure_rope(int n);
   Workspace wsp;  // activations of the current forward
+  // state of the persistent decoder-layer kernel (draft_layers.hip): its
+  // ring of stage outputs for up to pd_rows rows, one flag word per
+  // workgroup (pd_nwg of them, one per CU) and the error word
+  DevBuf<float> pd_ring;
+  DevBuf<unsigned> pd_flags, pd_tflags;
+  DevBuf<int> pd_err;
+  int pd_rows = 0, pd_nwg = 0;
+  // whether a forward of `rows` rows (S per sequence) over `kv` runs its
+  // layers as that one kernel
+  bool use_pd(int rows, int S, const KVCache *kv) const;
+  // throws if a wait of that kernel timed out (and resets its state)
+  void check_pd();
 
   Model(Ctx *c, int vocab, int d_model, int heads, int d_ff, int n_layers,
         int max_seq_len);

@@ -293,6 +293,9 @@ extern int g_attn_waves; // attention: waves one launch aims for
 extern int g_ln_split;   // LayerNorm rows of 512 / 1024 over 2 / 4 waves
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
+extern int g_persistent_draft; // 1 = short batches run their decoder layers as
+                               // one persistent kernel (draft_layers.hip);
+                               // 0 (default): the per-kernel path
 extern int g_gemv_down_rows; // down projection on the GEMV up to this many rows
 extern int g_o_head_digits; // 1 = the merged attention writes the output
                             // projection's digits per head (64-wide heads)
@@ -631,5 +634,40 @@ struct AcceptRows {
 // nt = ceil(V / 128).
 void launch_row_tile_stats(hipStream_t st, const float *logits, int64_t ldl,
                            int rows, int V, float T, float2 *out);
+
+// ---------------------------------------------------------------------------
+// The decoder layers of a short batch as one persistent kernel
+// (draft_layers.hip): per-layer weights and caches, the forward's rows and
+// positions, and the kernel's own state (a ring of stage outputs, one flag
+// word per workgroup, an error word).
+// ---------------------------------------------------------------------------
+constexpr int kPdMaxLayers = 8;
+constexpr int kPdFlagSlot = 1024;       // tile flags per (layer, step)
+struct PdLayer {
+  const int8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdn = nullptr;  // codes [N][K]
+  const float *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sdn = nullptr;   // scales [N]
+  const float *bqkv = nullptr, *bo = nullptr, *bgu = nullptr, *bdn = nullptr;   // biases [N]
+  const float *g1 = nullptr, *b1 = nullptr, *g2 = nullptr, *b2 = nullptr;       // LayerNorms
+  float *kc = nullptr, *vc = nullptr;   // fp32 cache of the layer, [B][H][cap][D]
+};
+struct PdArgs {
+  int R = 0, S = 1, B = 0, d = 0, H = 0, D = 0, F = 0, L = 0, cap = 0, off = 0;
+  int64_t seq_stride = 0;               // H * cap * D
+  const float *x0 = nullptr;            // [R][d] the layer-0 input rows
+  const int32_t *base = nullptr;        // [B] position of row (b, 0) is base[b] + off
+  const int32_t *active = nullptr;      // [B] or null: 0 = the sequence is skipped
+  const float *cosb = nullptr, *sinb = nullptr;  // RoPE tables [rope_len][D/2]
+  float *out = nullptr;                 // [R][d] the last layer's output before LN2
+  float *ring = nullptr;                // L * pd_ring_layer_floats floats
+  unsigned *flags = nullptr;            // one word per workgroup: its launches
+  unsigned *tflags = nullptr;           // [L][5][kPdFlagSlot] tile done flags
+  int *err = nullptr;                   // set when a wait timed out
+  PdLayer ly[kPdMaxLayers];
+};
+__host__ __device__ inline int64_t pd_ring_layer_floats(int R, int d, int F) {
+  return (int64_t)R * (6 * d + F);
+}
+bool draft_layers_supported(int d, int H, int F, int L, int R, int cap);
+void launch_draft_layers(hipStream_t st, const PdArgs &a, int nwg);
 
 }  // namespace nnhip
