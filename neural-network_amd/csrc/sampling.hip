@@ -15,6 +15,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 // Every product and sum below is rounded on its own, as the reference's
 // scalar loops round them (p - q of the residual, the probabilities, the
 // tile sums): no fused multiply-add, so the decisions follow the reference's
@@ -169,8 +171,9 @@ __device__ __forceinline__ void load_row(const float *__restrict__ row, int V,
 }
 
 // First index of the maximum (layer.cpp:1413-1421, std::max_element).
+template <class SH>
 __device__ __forceinline__ int block_argmax(const float *__restrict__ row,
-                                            int V, Shared &sh) {
+                                            int V, SH &sh) {
   float x[kPer];
   load_row(row, V, -INFINITY, x);
   float bv = -INFINITY;
@@ -345,9 +348,9 @@ __device__ __forceinline__ void block_filter(const float (&x)[kPer], int V,
 
 // The row is held in registers (entry v = tid + kThreads i); p goes to sh.prow
 // when `to_lds`, and to gout when given.
-template <bool FILT>
+template <bool FILT, class SH>
 __device__ __forceinline__ RowStats row_pass(const float *__restrict__ row, int V, float T,
-                             Shared &sh, bool to_lds,
+                             SH &sh, bool to_lds,
                              float *__restrict__ gout, int top_k = 0,
                              float top_p = 1.f) {
   float x[kPer];
@@ -385,7 +388,9 @@ __device__ __forceinline__ RowStats row_pass(const float *__restrict__ row, int 
       const int v = threadIdx.x + i * kThreads;
       if (v < V) {
         const float p = x[i] * st.rfs;
-        if (to_lds) sh.prow[la(v)] = p;
+        if constexpr (std::is_same_v<SH, Shared>) {
+          if (to_lds) sh.prow[la(v)] = p;
+        }
         if (gout) gout[v] = p;
       }
     }
@@ -403,9 +408,9 @@ __device__ __forceinline__ RowStats row_probs(const float *__restrict__ row,
   return row_pass<FILT>(row, V, T, sh, true, gout, top_k, top_p);
 }
 
-template <bool FILT = false>
+template <bool FILT = false, class SH>
 __device__ __forceinline__ RowStats row_stats(const float *__restrict__ row,
-                                              int V, float T, Shared &sh,
+                                              int V, float T, SH &sh,
                                               int top_k = 0, float top_p = 1.f) {
   return row_pass<FILT>(row, V, T, sh, false, nullptr, top_k, top_p);
 }
@@ -651,32 +656,60 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
   embed_next(s, b, j, tok, s_emb, s_red);
 }
 
-// Tile statistics of rows of logits (launch_row_tile_stats): one wave per
-// 128-column tile, two columns a lane, the same operations in the same order
-// as the LDS GEMM's lm-head epilogue, so a row gives the same statistics
-// whether they come from there or from here.
-__global__ __launch_bounds__(kThreads) void row_tile_stats_kernel(
+// Tile statistics of rows of logits (launch_row_tile_stats): per 128-column
+// tile, two columns a lane, the same operations in the same order as the LDS
+// GEMM's lm-head epilogue, so a row gives the same statistics whether they
+// come from there or from here.  A wave takes kTileRun consecutive tiles of
+// one row and requests all of their logits (one 8-byte load a lane per tile,
+// read once: non-temporal) before it reduces the first.
+constexpr int kTileRun = 8;
+constexpr int kTileThreads = 256;
+
+template <bool PAIRS>
+__global__ __launch_bounds__(kTileThreads) void row_tile_stats_kernel(
     const float *__restrict__ logits, int64_t ldl, int V, float T, int nt,
     float2 *__restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int tn = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int t0 = (blockIdx.x * (kTileThreads / 64) + (threadIdx.x >> 6)) * kTileRun;
   const int64_t r = blockIdx.y;
-  if (tn >= nt) return;                       // whole wave
-  const int n = tn * kTileW + 2 * lane;
+  if (t0 >= nt) return;                       // whole wave
   const float *row = logits + r * ldl;
-  const float l0 = n < V ? row[n] : 0.f, l1 = n + 1 < V ? row[n + 1] : 0.f;
-  if (T > 0.f) {
-    const float s0 = n < V ? scaled(l0, T) : -INFINITY;
-    const float s1 = n + 1 < V ? scaled(l1, T) : -INFINITY;
-    const float mx = wave_max_all(fmaxf(s0, s1));
-    const float e = wave_sum_all((n < V ? expf(s0 - mx) : 0.f) +
-                                 (n + 1 < V ? expf(s1 - mx) : 0.f));
-    if (lane == 0) out[r * nt + tn] = make_float2(mx, e);
+  // PAIRS: ldl and the base are even, so a pair of columns is one aligned
+  // 8-byte word
+  typedef float pair_t __attribute__((ext_vector_type(2)));
+  pair_t v[kTileRun];
+  if (PAIRS && (t0 + kTileRun) * kTileW <= V) {   // whole run inside the row
+#pragma unroll
+    for (int i = 0; i < kTileRun; ++i)
+      v[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const pair_t *>(row + (t0 + i) * kTileW + 2 * lane));
   } else {
-    const float a0 = n < V ? l0 : -INFINITY, a1 = n + 1 < V ? l1 : -INFINITY;
-    const float mx = wave_max_all(fmaxf(a0, a1));
-    const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
-    if (lane == 0) out[r * nt + tn] = make_float2(mx, __int_as_float(ix));
+#pragma unroll
+    for (int i = 0; i < kTileRun; ++i) {
+      const int n = (t0 + i) * kTileW + 2 * lane;
+      v[i].x = n < V ? row[n] : 0.f;
+      v[i].y = n + 1 < V ? row[n + 1] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kTileRun; ++i) {
+    const int tn = t0 + i;
+    if (tn >= nt) break;                      // whole wave
+    const int n = tn * kTileW + 2 * lane;
+    const float l0 = v[i].x, l1 = v[i].y;
+    if (T > 0.f) {
+      const float s0 = n < V ? scaled(l0, T) : -INFINITY;
+      const float s1 = n + 1 < V ? scaled(l1, T) : -INFINITY;
+      const float mx = wave_max_all(fmaxf(s0, s1));
+      const float e = wave_sum_all((n < V ? expf(s0 - mx) : 0.f) +
+                                   (n + 1 < V ? expf(s1 - mx) : 0.f));
+      if (lane == 0) out[r * nt + tn] = make_float2(mx, e);
+    } else {
+      const float a0 = n < V ? l0 : -INFINITY, a1 = n + 1 < V ? l1 : -INFINITY;
+      const float mx = wave_max_all(fmaxf(a0, a1));
+      const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
+      if (lane == 0) out[r * nt + tn] = make_float2(mx, __int_as_float(ix));
+    }
   }
 }
 
@@ -743,9 +776,11 @@ __device__ __forceinline__ int verify_rows(const SpecState &s) {
 // {max, 1/sum, 1/sum(kept p1), argmax, tau, tix} (the last three as int
 // bits).
 template <bool FILT>
-__global__ __launch_bounds__(kThreads) void target_stats_kernel(
+__global__ __launch_bounds__(kThreads, FILT ? 1 : 8) void target_stats_kernel(
     SpecState s, const float *__restrict__ tlogits) {
-  __shared__ Shared sh;
+  // the row stays in registers: only the filter needs the LDS row, so the
+  // unfiltered kernel leaves room for a second workgroup on the CU
+  __shared__ std::conditional_t<FILT, Shared, SmallShared> sh;
   const int j = blockIdx.x, b = blockIdx.y;
   if (!s.active[b]) return;
   const int gen0 = s.gen[b];
@@ -1120,8 +1155,14 @@ void launch_row_tile_stats(hipStream_t st, const float *logits, int64_t ldl,
   NNHIP_REQUIRE(rows > 0 && V > 0 && ldl >= V && rows <= 65535, kErrArg,
                 "row tile statistics: bad sizes");
   const int nt = (V + kTileW - 1) / kTileW;
-  hipLaunchKernelGGL(row_tile_stats_kernel, dim3((nt + kWaves - 1) / kWaves, rows),
-                     dim3(kThreads), 0, st, logits, ldl, V, T, nt, out);
+  const int per_block = (kTileThreads / 64) * kTileRun;
+  const dim3 grid((nt + per_block - 1) / per_block, rows);
+  if (ldl % 2 == 0 && reinterpret_cast<uintptr_t>(logits) % 8 == 0)
+    hipLaunchKernelGGL(row_tile_stats_kernel<true>, grid, dim3(kTileThreads), 0, st,
+                       logits, ldl, V, T, nt, out);
+  else
+    hipLaunchKernelGGL(row_tile_stats_kernel<false>, grid, dim3(kTileThreads), 0, st,
+                       logits, ldl, V, T, nt, out);
   NNHIP_CHECK(hipGetLastError());
 }
 

@@ -672,3 +672,11 @@ def test_spec_accept_vs_oracle(ctx, T, corr):
     assert ties <= 1
     if corr > 0.9 and T > 0:
         assert n.max() >= 3          # the correlated case accepts runs
+
+
+@pytest.mark.parametrize("V", [4097, 1000, 130])
+def test_spec_accept_odd_vocab(ctx, V):
+    """Vocabularies whose rows are not 8-byte aligned (odd V: the draft
+    statistics read single columns) or end inside a run of tiles."""
+    n, ties = accept_case(ctx, 16, 4, V, 0.7, 0.9, seed=V)
+    assert ties <= 1
