@@ -135,6 +135,9 @@ def run_cfg2(ctx):
     prompt = rng.integers(0, 4096, (1, 128)).astype(np.int32)
     t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
     out, stats, tm = t.generate_speculative_batch(d, prompt, 256, 4, 0.0, 42)
+    # the same models and prompt at the headline's lookahead (k = 5)
+    t.generate_speculative_batch(d, prompt, 256, 5, 0.0, 42)
+    _, stats5, tm5 = t.generate_speculative_batch(d, prompt, 256, 5, 0.0, 42)
     # the target's GEMV at the verify shape (k + 1 = 5 rows): gate/up and
     # the lm head, int8 codes read once per launch
     gemv = {}
@@ -147,13 +150,22 @@ def run_cfg2(ctx):
     cyc = stats[0].cycles
     byt = cyc * cycle_bytes(128 + 128, 4, 1, target=CFG2_T, draft=CFG2_D)
     gbs = byt / (tm.decode_ms / 1e3) / 1e9
+    cyc5 = stats5[0].cycles
+    byt5 = cyc5 * cycle_bytes(128 + 128, 5, 1, target=CFG2_T, draft=CFG2_D)
+    gbs5 = byt5 / (tm5.decode_ms / 1e3) / 1e9
     return dict(tokens_per_s=255 / (tm.decode_ms / 1e3),
                 decode_ms=tm.decode_ms, cycles=cyc,
                 ms_per_cycle=round(tm.decode_ms / max(cyc, 1), 4),
                 accepted=stats[0].accepted,
                 loop_roofline=dict(achieved_GBs=round(gbs, 1),
                                    frac=round(gbs / HBM_PEAK_GBS, 4)),
-                gemv_verify=gemv)
+                gemv_verify=gemv,
+                k5=dict(tokens_per_s=round(255 / (tm5.decode_ms / 1e3), 1),
+                        decode_ms=round(tm5.decode_ms, 3), cycles=cyc5,
+                        ms_per_cycle=round(tm5.decode_ms / max(cyc5, 1), 4),
+                        accepted=stats5[0].accepted,
+                        loop_roofline=dict(achieved_GBs=round(gbs5, 1),
+                                           frac=round(gbs5 / HBM_PEAK_GBS, 4))))
 
 
 ATTN_SHAPE = dict(B=B, S=K_LOOK + 1, H=16, D=64, n_cached=P + NEW // 2)
