@@ -274,6 +274,204 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// int8 GEMV with 128-bit code loads: y[r][n] = epi( sum_k x[r][k] * w[n][k] ),
+// r < R (<= 8), K = 16 G with G (chunks of 16 codes per column) a power of
+// two from 16 to 256.  A workgroup (256 threads) covers NB = CPI * NIT
+// columns, CPI = 256 / G of them at a time: thread t owns chunk t % G of
+// column t / G of each of its NIT column groups, so it loads 16 codes of a
+// column with one 16-byte load, and its 16 entries of each row once, kept in
+// registers for all its columns.  Every code load is issued with the row
+// loads; the columns' scales and biases are staged in LDS first.  The R x NIT
+// partial sums of a thread are reduced over the G threads of its column
+// (within a wave: butterfly reduce-scatter over lane offsets G/2 .. 1, or
+// 32 .. 1 when G > 64, then the G / 64 waves of a column through LDS), then
+// the epilogue of gemv_kernel runs one (row, column) item per thread.
+// ---------------------------------------------------------------------------
+template <int G>
+struct Gemv16Shape {
+  static constexpr int CPI = 256 / G;                 // columns per pass
+  static constexpr int NIT = G <= 32 ? (G == 16 ? 1 : 2) : 4;
+  static constexpr int NB = CPI * NIT;                // columns per workgroup
+  static constexpr int WPC = G > 64 ? G / 64 : 1;     // waves per column
+  static constexpr int OMAX = G > 64 ? 32 : G / 2;    // first butterfly offset
+};
+
+template <int NP, int OMAX>
+__device__ __forceinline__ int gemv16_slot(int lane) {
+  int slot = 0, cnt = NP;
+#pragma unroll
+  for (int o = OMAX; o >= 1; o >>= 1)
+    if (cnt > 1) { cnt /= 2; if (lane & o) slot += cnt; }
+  return slot;
+}
+
+template <int R, int G>
+__global__ __launch_bounds__(256) void gemv16_kernel(
+    const float *__restrict__ x, int64_t ldx, int K, int N,
+    const int8_t *__restrict__ wq, const float *__restrict__ scale,
+    const float *__restrict__ bias, const float *__restrict__ resid,
+    int64_t ldr, float *__restrict__ y, int64_t ldy, int epi, int64_t row0,
+    RopeArgs ra, GemvLn lf) {
+  using SH = Gemv16Shape<G>;
+  constexpr int CPI = SH::CPI, NIT = SH::NIT, NB = SH::NB, WPC = SH::WPC;
+  constexpr int P = NIT * R;
+  constexpr int NP = P <= 1 ? 1 : P <= 2 ? 2 : P <= 4 ? 4 : P <= 8 ? 8
+                   : P <= 16 ? 16 : P <= 32 ? 32 : 64;
+  static_assert(P <= 64, "gemv16: too many partial sums per thread");
+  {
+    const int64_t g = (int64_t)blockIdx.y * R;
+    x += g * ldx;
+    if (resid) resid += g * ldr;
+    if (y) y += g * ldy;
+    if (lf.out) lf.out += g * lf.ldo;
+    row0 += g;
+  }
+  __shared__ float s_scale[NB], s_bias[NB];
+  __shared__ float red[WPC][NB][R];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int chunk = t % G, cpos = t / G;
+  const int64_t col0 = (int64_t)blockIdx.x * NB;
+  if (t < NB) {
+    const int64_t n = col0 + t;
+    s_scale[t] = n < N ? scale[n] : 0.f;
+    s_bias[t] = n < N ? bias[n] : 0.f;
+  }
+  // epilogue operands of the thread's item (row e_r, column e_c), requested
+  // first: the residual, the RoPE position and angle
+  const bool pair = epi == kEpiSwiGLU || epi == kEpiRope;
+  const int e_r = t % R, e_c = t / R;
+  const int64_t e_n = col0 + e_c;
+  const bool e_ok = t < NB * R && e_n < N && (!pair || (e_n & 1) == 0);
+  float e_rs = 0.f;
+  int e_pos = -1;
+  float2 e_cos = make_float2(0.f, 0.f);
+  if (e_ok) {
+    if (epi == kEpiResid) e_rs = resid[e_r * ldr + e_n];
+    if (epi == kEpiRope) {
+      e_pos = rope_row_pos(ra, row0 + e_r);
+      if (e_pos >= 0 && e_n / (ra.H * ra.D) != 2) e_cos = rope_cos_sin(ra, e_pos, (int)e_n);
+    }
+  }
+  // the thread's 16 entries of every row and its NIT 16-byte code chunks
+  const int k = chunk * 16;
+  float xr[R][16];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4 *>(x + r * ldx + k + 4 * q);
+      xr[r][4 * q] = v.x; xr[r][4 * q + 1] = v.y;
+      xr[r][4 * q + 2] = v.z; xr[r][4 * q + 3] = v.w;
+    }
+  v4i wc[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int64_t n = col0 + it * CPI + cpos;
+    wc[it] = n < N ? *reinterpret_cast<const v4i *>(wq + n * K + k) : v4i{0, 0, 0, 0};
+  }
+  if (lf.g) {
+#pragma clang fp contract(off)
+    // each row's mean and deviation over all K with layernorm_rows_kernel's
+    // arithmetic (every wave forms them from the whole row), then the
+    // thread's entries normalised
+    float mean[R], sd[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float q4[4][4];
+      load_quads<4>(x + r * ldx, K, lane, q4);
+      float sm = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (quad_ok(i, lane, K)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sm += q4[i][j];
+        }
+      sm = wave_sum_all(sm);
+      const float Nf = (float)K;
+      mean[r] = sm / Nf;
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (quad_ok(i, lane, K)) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) { const float df = q4[i][j] - mean[r]; sq += df * df; }
+        }
+      sq = wave_sum_all(sq);
+      sd[r] = sqrtf(sq / Nf + 1e-5f);
+    }
+    float ga[16], ba[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 gg = *reinterpret_cast<const float4 *>(lf.g + k + 4 * q);
+      const float4 bb = *reinterpret_cast<const float4 *>(lf.b + k + 4 * q);
+      ga[4 * q] = gg.x; ga[4 * q + 1] = gg.y; ga[4 * q + 2] = gg.z; ga[4 * q + 3] = gg.w;
+      ba[4 * q] = bb.x; ba[4 * q + 1] = bb.y; ba[4 * q + 2] = bb.z; ba[4 * q + 3] = bb.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xr[r][e] = (xr[r][e] - mean[r]) / sd[r] * ga[e] + ba[e];
+      if (lf.out && blockIdx.x == 0 && cpos == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4 *>(lf.out + r * lf.ldo + k + 4 * q) =
+              make_float4(xr[r][4 * q], xr[r][4 * q + 1], xr[r][4 * q + 2], xr[r][4 * q + 3]);
+      }
+    }
+  }
+  float acc[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd) {
+      const int pk = wc[it][wd];
+      float wv[4];
+      wv[0] = (float)(int8_t)(pk & 0xff);
+      wv[1] = (float)(int8_t)((pk >> 8) & 0xff);
+      wv[2] = (float)(int8_t)((pk >> 16) & 0xff);
+      wv[3] = (float)(int8_t)((pk >> 24) & 0xff);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[it * R + r] += xr[r][4 * wd + e] * wv[e];
+    }
+  }
+  rs_step<NP, NP, SH::OMAX>(acc, lane);
+  {
+    const int slot = gemv16_slot<NP, SH::OMAX>(lane);
+    // lanes of a column holding the same slot (NP < the butterfly's span)
+    // hold the same total: the first writes
+    constexpr int span = 2 * SH::OMAX;
+    const int first = (span / NP > 1) ? ((lane & (span / NP - 1)) == 0) : 1;
+    if (slot < P && first)
+      red[WPC > 1 ? w % WPC : 0][(slot / R) * CPI + cpos][slot % R] = acc[0];
+  }
+  __syncthreads();
+  if (e_ok) {
+    const int r = e_r, c = e_c;
+    const int64_t n = e_n;
+    float a = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < WPC; ++s2) a += red[s2][c][r];
+    float v = a * s_scale[c] + s_bias[c];
+    if (pair) {
+      float a1 = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < WPC; ++s2) a1 += red[s2][c + 1][r];
+      const float u = a1 * s_scale[c + 1] + s_bias[c + 1];
+      if (epi == kEpiSwiGLU) y[r * ldy + n / 2] = swiglu_pair(v, u);
+      else if (e_pos >= 0) rope_store_pair_at(ra, row0 + r, e_pos, (int)n, v, u, e_cos.x, e_cos.y);
+    } else if (epi == kEpiResid) {
+      y[r * ldy + n] = e_rs + v;
+    } else {
+      y[r * ldy + n] = v;
+    }
+  }
+}
+
 // Digits of activation rows for the MFMA GEMM: X = rint(x * 2^e) with
 // e = 22 - exponent(max|x|) per row, split into balanced base-256 digits
 // (hi, mid, lo), written in the MFMA operand layout.  WPR waves per row, each
@@ -988,12 +1186,38 @@ __global__ void fill_kernel(float *p, int64_t n, float v) {
     p[i] = v;
 }
 
+template <int R, int G>
+void gemv16_launch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
+                   const int8_t *wq, const float *scale, const float *bias,
+                   const float *resid, int64_t ldr, float *y, int64_t ldy,
+                   int epi, int64_t row0, const RopeArgs &ra, const GemvLn &lf,
+                   int groups) {
+  constexpr int NB = Gemv16Shape<G>::NB;
+  dim3 grid((N + NB - 1) / NB, groups);
+  hipLaunchKernelGGL((gemv16_kernel<R, G>), grid, dim3(256), 0, st, x, ldx, K, N,
+                     wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf);
+}
+
 template <int R>
 void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
                    const int8_t *wq, const float *wf, const float *scale,
                    const float *bias, const float *resid, int64_t ldr,
                    float *y, int64_t ldy, int epi, int64_t row0,
                    const RopeArgs &ra, const GemvLn &lf, int groups = 1) {
+  // int8 codes, K = 16 G with G a power of two in [16, 256], aligned rows:
+  // the 128-bit-load GEMV
+  if (wq && g_gemv16 && ldx % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(wq) % 16 == 0) {
+    switch (K) {
+      case 256: gemv16_launch<R, 16>(st, x, ldx, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf, groups); return;
+      case 512: gemv16_launch<R, 32>(st, x, ldx, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf, groups); return;
+      case 1024: gemv16_launch<R, 64>(st, x, ldx, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf, groups); return;
+      case 2048: gemv16_launch<R, 128>(st, x, ldx, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf, groups); return;
+      case 4096: gemv16_launch<R, 256>(st, x, ldx, K, N, wq, scale, bias, resid, ldr, y, ldy, epi, row0, ra, lf, groups); return;
+      default: break;
+    }
+  }
   int nks = K >= 1024 ? 4 : (K >= 512 ? 2 : 1);
   int cols = (4 / nks) * kGemvNC;
   dim3 grid((N + cols - 1) / cols, groups);
@@ -1012,6 +1236,8 @@ void gemv_dispatch(hipStream_t st, const float *x, int64_t ldx, int K, int N,
 // 1: allow 32x64 GEMM tiles for large grids; 0: always 32x32 (default,
 // measured faster on every decode shape).
 int g_gemm_wide = 1;
+// 1: int8 GEMVs with K of 256-4096 use 128-bit code loads (gemv16_kernel)
+int g_gemv16 = 1;
 
 void launch_gemv(hipStream_t st, const float *x, int64_t ldx, int rows, int K,
                  int N, const int8_t *wq, const float *wf, const float *scale,

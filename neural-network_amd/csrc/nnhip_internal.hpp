@@ -283,6 +283,7 @@ __device__ inline int digit_exponent(float mx) {
 }
 
 // linear.hip
+extern int g_gemv16;     // 1 = int8 GEMVs with 128-bit code loads (gemv16_kernel)
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
 extern int g_limb_k8;    // digit-plane GEMM: 8 waves split K from this K on
 // engine.hip

@@ -57,7 +57,9 @@ GEMV_SHAPES = [(1, 64, 64), (1, 256, 768), (2, 512, 1536), (3, 1024, 1024),
                # 32+ rows in 4-row groups (the draft's down projection at
                # 32 / 64 rows), and 8-row groups with a remainder launch
                (32, 512, 1536), (32, 2048, 512), (64, 2048, 512),
-               (37, 2048, 512), (64, 512, 4096)]
+               (37, 2048, 512), (64, 512, 4096),
+               # column counts that end inside a workgroup's columns
+               (3, 512, 200), (2, 2048, 36), (5, 256, 24), (1, 4096, 12)]
 
 
 @pytest.mark.parametrize("rows,K,N", GEMV_SHAPES)
