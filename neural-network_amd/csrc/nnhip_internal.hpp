@@ -283,6 +283,8 @@ __device__ inline int digit_exponent(float mx) {
 }
 
 // linear.hip
+extern int g_accept_early;  // 1 = nnhip_spec_accept forms row statistics only up
+                            // to each sequence's first rejection
 extern int g_gemv16;     // 1 = int8 GEMVs with 128-bit code loads (gemv16_kernel)
 extern int g_gemm_wide;  // GEMM tile choice (1 = 32x64 tiles allowed)
 extern int g_limb_k8;    // digit-plane GEMM: 8 waves split K from this K on
@@ -584,6 +586,9 @@ struct SpecState {
   // when set, accept_kernel also writes each sequence's accepted count and
   // its resampled / bonus token (-1 when none)
   int32_t *n_acc_out = nullptr, *tok_out = nullptr;
+  // [B] lowest position whose candidate is certainly rejected, or null: the
+  // row statistics skip the rows after it (accept_rows_stats_kernel)
+  int32_t *minrej = nullptr;
   // when nd is set, drafting steps j < k - 1 embed their token as row b of
   // the next draft forward
   NextRows nd;
@@ -613,6 +618,7 @@ struct AcceptRows {
       out, n_active;
   DevBuf<float> tstat;
   DevBuf<float2> dtiles;   // [B][k][nt] draft-row tile statistics
+  DevBuf<int32_t> minrej;  // [B] first certain rejection (early exit)
   DevBuf<int64_t> stats;
   SpecState s;
   AcceptRows(int B, int k, int V, float T);

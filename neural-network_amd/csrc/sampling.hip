@@ -665,6 +665,24 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
 constexpr int kTileRun = 8;
 constexpr int kTileThreads = 256;
 
+// One tile's statistics from a wave holding its columns n, n + 1 (n = tile
+// start + 2 lane) in l0, l1: T > 0 (max s, sum exp(s - max)) with s = l / T,
+// else (max l, first index of the max as int bits); every lane gets them.
+__device__ __forceinline__ float2 tile_stat(float l0, float l1, int n, int V, float T) {
+  if (T > 0.f) {
+    const float s0 = n < V ? scaled(l0, T) : -INFINITY;
+    const float s1 = n + 1 < V ? scaled(l1, T) : -INFINITY;
+    const float mx = wave_max_all(fmaxf(s0, s1));
+    const float e = wave_sum_all((n < V ? expf(s0 - mx) : 0.f) +
+                                 (n + 1 < V ? expf(s1 - mx) : 0.f));
+    return make_float2(mx, e);
+  }
+  const float a0 = n < V ? l0 : -INFINITY, a1 = n + 1 < V ? l1 : -INFINITY;
+  const float mx = wave_max_all(fmaxf(a0, a1));
+  const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
+  return make_float2(mx, __int_as_float(ix));
+}
+
 template <bool PAIRS>
 __global__ __launch_bounds__(kTileThreads) void row_tile_stats_kernel(
     const float *__restrict__ logits, int64_t ldl, int V, float T, int nt,
@@ -695,21 +713,8 @@ __global__ __launch_bounds__(kTileThreads) void row_tile_stats_kernel(
   for (int i = 0; i < kTileRun; ++i) {
     const int tn = t0 + i;
     if (tn >= nt) break;                      // whole wave
-    const int n = tn * kTileW + 2 * lane;
-    const float l0 = v[i].x, l1 = v[i].y;
-    if (T > 0.f) {
-      const float s0 = n < V ? scaled(l0, T) : -INFINITY;
-      const float s1 = n + 1 < V ? scaled(l1, T) : -INFINITY;
-      const float mx = wave_max_all(fmaxf(s0, s1));
-      const float e = wave_sum_all((n < V ? expf(s0 - mx) : 0.f) +
-                                   (n + 1 < V ? expf(s1 - mx) : 0.f));
-      if (lane == 0) out[r * nt + tn] = make_float2(mx, e);
-    } else {
-      const float a0 = n < V ? l0 : -INFINITY, a1 = n + 1 < V ? l1 : -INFINITY;
-      const float mx = wave_max_all(fmaxf(a0, a1));
-      const int ix = wave_min_all(a0 == mx ? n : (a1 == mx ? n + 1 : 0x7fffffff));
-      if (lane == 0) out[r * nt + tn] = make_float2(mx, __int_as_float(ix));
-    }
+    const float2 ts = tile_stat(v[i].x, v[i].y, tn * kTileW + 2 * lane, V, T);
+    if (lane == 0) out[r * nt + tn] = ts;
   }
 }
 
@@ -842,6 +847,76 @@ __device__ __forceinline__ int residual_sample(
   return block_sample(V, u, sh);
 }
 
+// The statistics of the accept step from logits (AcceptRows::launch_logits,
+// T > 0 without top-k / top-p), rows decided in order: one workgroup per
+// (verify row j, sequence b), numbered row-major (every sequence's row 0,
+// then every row 1, ...), so that the workgroups of row j mostly start after
+// those of the rows before it have finished.  A workgroup forms the target
+// row's statistics (target_stats_kernel's arithmetic) and, for a drafted
+// position, the draft row's tile statistics (row_tile_stats_kernel's) and
+// their combination (the accept step's), then tests its candidate; when the
+// candidate is rejected by a margin no rounding difference between this
+// kernel and the accept step can cross (r * q >= p * (1 + 1e-5)), it lowers
+// minrej[b] to j.  A workgroup whose sequence already has a smaller minrej
+// returns at once: the accept step, which decides every position again from
+// these statistics, stops at or before that rejection and never reads rows
+// after it (layer.cpp:1581-1630 computes p_j only until the first rejection).
+__global__ __launch_bounds__(kThreads) void accept_rows_stats_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  __shared__ SmallShared sh;
+  __shared__ float2 s_tiles[kTileMax * 64];
+  const int j = blockIdx.x / s.B, b = blockIdx.x % s.B;
+  if (!s.active[b]) return;
+  const int gen0 = s.gen[b];
+  const int M = min(s.k, s.max_new - gen0);
+  if (j > M || (j == M && gen0 + M >= s.max_new)) return;
+  if (j > 0 && __hip_atomic_load(s.minrej + b, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) < j)
+    return;
+  const int64_t r = (int64_t)b * (s.k + 1) + j;
+  const float *row = tlogits + ((int64_t)b * verify_rows(s) + j) * s.V;
+  const RowStats st = row_stats<false>(row, s.V, s.T, sh);
+  if (threadIdx.x == 0) {
+    float *ts = s.tstat + r * kTstat;
+    ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs;
+    ts[4] = __uint_as_float(st.tau); ts[5] = __int_as_float(st.tix);
+  }
+  if (j >= M) return;                         // the bonus row
+  // the draft row's tile statistics, runs of 8 tiles per wave
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const float *drow = s.qlog + j * s.qlog_js + b * s.qlog_bs;
+  float2 *dt = const_cast<float2 *>(s.dtiles) + ((int64_t)b * s.k + j) * s.nt;
+  for (int base = w * kTileRun; base < s.nt; base += kWaves * kTileRun) {
+    float2 v[kTileRun];
+#pragma unroll
+    for (int i = 0; i < kTileRun; ++i) {
+      const int n = (base + i) * kTileW + 2 * lane;
+      v[i].x = n < s.V ? drow[n] : 0.f;
+      v[i].y = n + 1 < s.V ? drow[n + 1] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kTileRun; ++i) {
+      const int tn = base + i;
+      if (tn >= s.nt) break;                  // whole wave
+      const float2 ts = tile_stat(v[i].x, v[i].y, tn * kTileW + 2 * lane, s.V, s.T);
+      if (lane == 0) { dt[tn] = ts; s_tiles[tn] = ts; }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const RowStats qs = wave_tiles_stats(s_tiles, s.nt);
+    if (threadIdx.x == 0) {
+      // (a candidate outside the vocabulary reads the last column)
+      const int c = min(max(s.cand[b * s.k + j], 0), s.V - 1);
+      const float pc = prob_of(row[c], c, s.T, st);
+      const float qc = (expf(scaled(drow[c], s.T) - qs.mx) * qs.rsum) * qs.rfs;
+      const float u = s.ua ? s.ua[(int64_t)b * s.k + j]
+                           : uniform(s.seed, s.seq0 + b, (uint32_t)s.cyc[b], s.k + j);
+      if (u * qc >= pc * (1.0f + 1e-5f)) atomicMin(s.minrej + b, j);
+    }
+  }
+}
+
 // Accept / reject, resample or bonus, rollback (layer.cpp:1581-1655), from
 // the verify rows' statistics (target_stats_kernel).  tlogits: [B][k+1][V],
 // row i = verify position i.
@@ -898,7 +973,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
       if (j < M) {
-        const int c = s.cand[b * k + j];
+        // reads clamped to the row: a candidate outside the vocabulary
+        // (only from nnhip_spec_accept's caller) reads the last column
+        const int c = min(max(s.cand[b * k + j], 0), V - 1);
         lc[j] = tlogits[((int64_t)b * tr + j) * V + c];
         qcp[j] = qimp ? qlrow(j)[c] : s.qprob[((int64_t)b * k + j) * V + c];
       }
@@ -928,10 +1005,11 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   }
   for (int j = kPre; j < M && rej < 0; ++j) {
     const int c = s.cand[b * k + j];
-    const float lj = greedy ? 0.f : tlogits[((int64_t)b * tr + j) * V + c];
+    const int cr = min(max(c, 0), V - 1);
+    const float lj = greedy ? 0.f : tlogits[((int64_t)b * tr + j) * V + cr];
     const float qc = greedy ? 0.f
-                     : qimp ? q_of(qlrow(j)[c], j)
-                            : s.qprob[((int64_t)b * k + j) * V + c];
+                     : qimp ? q_of(qlrow(j)[cr], j)
+                            : s.qprob[((int64_t)b * k + j) * V + cr];
     if (!test(j, c, lj, qc)) { rej = j; break; }
     if (threadIdx.x == 0) out[nout] = c;
     ++nout;
@@ -1026,6 +1104,7 @@ __global__ void accept_rows_reset_kernel(SpecState s) {
   if (b >= s.B) return;
   s.cur[b] = -1; s.tlen[b] = 0; s.dlen[b] = 0; s.gen[b] = 0; s.cyc[b] = 1;
   s.active[b] = 1; s.catchup[b] = 0; s.catch_tok[b] = -1;
+  if (s.minrej) s.minrej[b] = 0x7fffffff;
   for (int i = 0; i < kSpecStats; ++i) s.stats[(int64_t)b * kSpecStats + i] = 0;
 }
 
@@ -1055,6 +1134,8 @@ bool filtered(const SpecState &s) {
 }
 
 }  // namespace
+
+int g_accept_early = 1;
 
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl) {
@@ -1178,7 +1259,8 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   NNHIP_REQUIRE(nt <= kTileMax * 64, kErrUnsupported,
                 "accept: more than 1024 tiles of draft statistics");
   if (!dtiles.p) dtiles.alloc((size_t)s.B * s.k * nt);
-  launch_row_tile_stats(st, dlogits, s.V, s.B * s.k, s.V, s.T, dtiles.p);
+  const bool early = g_accept_early && !filtered(s);
+  if (!early) launch_row_tile_stats(st, dlogits, s.V, s.B * s.k, s.V, s.T, dtiles.p);
   SpecState a = s;
   a.qlog = dlogits;
   a.qlog_js = s.V;
@@ -1188,10 +1270,25 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   a.tw = kTileW;
   a.cand = const_cast<int32_t *>(cand);
   a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
+  if (early) {
+    if (!minrej.p) minrej.alloc(s.B);
+    a.minrej = minrej.p;
+  }
   hipLaunchKernelGGL(accept_rows_reset_kernel, dim3((s.B + 255) / 256),
                      dim3(256), 0, st, a);
   NNHIP_CHECK(hipGetLastError());
-  launch_accept(st, a, tlogits);
+  if (!early) {
+    launch_accept(st, a, tlogits);
+    return;
+  }
+  // rows decided in order: the statistics of the rows up to each
+  // sequence's first rejection, then the accept step
+  NNHIP_REQUIRE((int64_t)s.B * (s.k + 1) <= 0x7fffffff, kErrArg, "accept: too many rows");
+  hipLaunchKernelGGL(accept_rows_stats_kernel, dim3(s.B * (s.k + 1)), dim3(kThreads),
+                     0, st, a, tlogits);
+  NNHIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, a, tlogits);
+  NNHIP_CHECK(hipGetLastError());
 }
 
 void AcceptRows::launch(hipStream_t st, const float *tlogits, const float *qprob,
