@@ -73,6 +73,7 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
     else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
     else if (std::strcmp(key, "gemv16") == 0) nnhip::g_gemv16 = value != 0;
     else if (std::strcmp(key, "accept_early") == 0) nnhip::g_accept_early = value != 0;
+    else if (std::strcmp(key, "accept_split") == 0) nnhip::g_accept_split = value != 0;
     else if (std::strcmp(key, "lds_min_rows") == 0) {
       REQ(value >= 16, "lds_min_rows must be >= 16");
       nnhip::g_lds_min_rows = value;

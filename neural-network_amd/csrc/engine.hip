@@ -705,6 +705,8 @@ struct SpecBuffers {
   DevBuf<float> qprob, dlog, tlog, tstat;
   DevBuf<float2> dtiles;
   DevBuf<int64_t> stats;
+  DevBuf<int32_t> rec;    // the split accept step's records and chunk sums
+  DevBuf<double> chunks;
 };
 
 void check_sampling_options(int V, int top_k, float top_p) {
@@ -798,6 +800,12 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   s.active = bf.active.p; s.catchup = bf.catchup.p;
   s.catch_tok = bf.catch_tok.p; s.pair = bf.pair.p; s.out = bf.out.p;
   s.n_active = bf.n_active.p; s.n_far = bf.n_active.p + 1;
+  if (g_accept_split) {
+    bf.rec.alloc((size_t)B * kAcceptRec);
+    bf.chunks.alloc((size_t)B * kDrawChunks * 2);
+    s.rec = bf.rec.p;
+    s.chunks = bf.chunks.p;
+  }
   s.stats = bf.stats.p;
   s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
   s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;

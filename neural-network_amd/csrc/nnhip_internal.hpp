@@ -283,6 +283,8 @@ __device__ inline int digit_exponent(float mx) {
 }
 
 // linear.hip
+extern int g_accept_split;  // 1 = the accept step's draw spread over
+                            // kDrawChunks workgroups per sequence
 extern int g_accept_early;  // 1 = nnhip_spec_accept forms row statistics only up
                             // to each sequence's first rejection
 extern int g_gemv16;     // 1 = int8 GEMVs with 128-bit code loads (gemv16_kernel)
@@ -519,6 +521,10 @@ void launch_slice_backward(hipStream_t st, const TensorView &gs,
 constexpr int kTstat = 6;
 // int64 counters per sequence of SpecState::stats
 constexpr int kSpecStats = 8;
+// the split accept step (launch_accept with g_accept_split): int32 words of
+// a sequence's record, and vocabulary chunks of the draw
+constexpr int kAcceptRec = 8;
+constexpr int kDrawChunks = 16;
 // largest lookahead k of the speculative loop
 constexpr int kMaxLookahead = 63;
 // whether get_probs filters with these options (layer.cpp:1452-1472)
@@ -589,6 +595,10 @@ struct SpecState {
   // [B] lowest position whose candidate is certainly rejected, or null: the
   // row statistics skip the rows after it (accept_rows_stats_kernel)
   int32_t *minrej = nullptr;
+  // the split accept step's scratch: [B][kAcceptRec] records and
+  // [B][kDrawChunks][2] chunk sums (null: one accept_kernel per sequence)
+  int32_t *rec = nullptr;
+  double *chunks = nullptr;
   // when nd is set, drafting steps j < k - 1 embed their token as row b of
   // the next draft forward
   NextRows nd;
@@ -619,6 +629,8 @@ struct AcceptRows {
   DevBuf<float> tstat;
   DevBuf<float2> dtiles;   // [B][k][nt] draft-row tile statistics
   DevBuf<int32_t> minrej;  // [B] first certain rejection (early exit)
+  DevBuf<int32_t> rec;     // split accept step: records and chunk sums
+  DevBuf<double> chunks;
   DevBuf<int64_t> stats;
   SpecState s;
   AcceptRows(int B, int k, int V, float T);
@@ -633,6 +645,8 @@ struct AcceptRows {
   void launch_logits(hipStream_t st, const float *tlogits,
                      const float *dlogits, const int32_t *cand, const float *ua,
                      const float *ur, int32_t *n_acc, int32_t *tok);
+  // the split accept step's scratch into a (g_accept_split)
+  void attach_split(SpecState &a);
 };
 // Softmax statistics per 128-column tile of each row of logits [rows][V]
 // (rows ldl apart), the TileStatsArgs values the LDS GEMM's lm-head epilogue

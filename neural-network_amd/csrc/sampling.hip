@@ -1098,6 +1098,356 @@ __global__ __launch_bounds__(kThreads) void ar_sample_kernel(
 
 // State of the accept step run on given rows (AcceptRows): every sequence
 // drafted k candidates (gen 0 of max_new = k, so no bonus row), at cycle 1.
+// The accept step split over three launches (launch_accept with
+// g_accept_split), so that the draw from the residual (or from p for the
+// bonus) runs on many CUs instead of one per sequence:
+//  1. accept_decide_kernel (one workgroup per sequence): the accept tests of
+//     accept_kernel, the accepted candidates written out, and a record of
+//     what remains to draw;
+//  2. draw_chunks_kernel (kDrawChunks workgroups per sequence): over its
+//     chunk of the vocabulary, the double sums of the residual
+//     max(0, p - q) and of p (the weights residual_sample and fill_probs
+//     form, the same expressions);
+//  3. accept_final_kernel (one workgroup per sequence): the chunk in which
+//     u * S falls, then block_sample's crossing rule inside it (running
+//     double sums over the chunk prefix), and accept_kernel's state update.
+// Record per sequence: kind (-1 inactive, 0 nothing to draw, 1 residual,
+// 2 p of the bonus row), the rejected position (-1 none), ties, the greedy
+// token, and the implicit draft statistics of the rejected row.
+constexpr int kRec = kAcceptRec;
+
+__global__ __launch_bounds__(kThreads) void accept_decide_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  const int b = blockIdx.x;
+  int32_t *rec = s.rec + (int64_t)b * kRec;
+  if (!s.active[b]) {
+    if (threadIdx.x == 0) rec[0] = -1;
+    return;
+  }
+  const int V = s.V, k = s.k;
+  const bool greedy = s.T <= 0.f;
+  const int gen0 = s.gen[b];
+  const int M = min(k, s.max_new - gen0);
+  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const int tr = verify_rows(s);
+  int32_t *out = s.out + (int64_t)b * s.out_stride;
+  int nout = s.P + gen0;
+  int rej = -1;
+  int64_t ties = 0;
+  auto stats_of = [&](int j) {
+    const float *ts = s.tstat + ((int64_t)b * (k + 1) + j) * kTstat;
+    RowStats st = mk_stats(ts[0], ts[1], ts[2]);
+    st.tau = __float_as_uint(ts[4]);
+    st.tix = __float_as_int(ts[5]);
+    return st;
+  };
+  auto argmax_of = [&](int j) {
+    return __float_as_int(s.tstat[((int64_t)b * (k + 1) + j) * kTstat + 3]);
+  };
+  // implicit draft probabilities (s.qlog): each drafting step's statistics
+  // from its lm-head tiles, one wave a step, as the drafting step formed them
+  __shared__ RowStats qst[kMaxLookahead];
+  const bool qimp = s.qlog != nullptr && !greedy;
+  if (qimp) {
+    const int w = threadIdx.x >> 6;
+    for (int j = w; j < M; j += kWaves) {
+      const RowStats st = wave_tiles_stats(s.dtiles + ((int64_t)b * k + j) * s.nt, s.nt);
+      if ((threadIdx.x & 63) == 0) qst[j] = st;
+    }
+    __syncthreads();
+  }
+  const int64_t qjs = s.qlog_js ? s.qlog_js : (int64_t)s.B * V;
+  const int64_t qbs = s.qlog_bs ? s.qlog_bs : (int64_t)V;
+  auto qlrow = [&](int j) { return s.qlog + j * qjs + b * qbs; };
+  auto q_of = [&](float l, int j) {
+    return (expf(scaled(l, s.T) - qst[j].mx) * qst[j].rsum) * qst[j].rfs;
+  };
+  // the candidates' target logits and draft probabilities, the first kPre
+  // positions requested at once (their loop is unrolled so that the
+  // prefetched values stay in registers)
+  constexpr int kPre = 8;
+  float lc[kPre], qcp[kPre];
+  if (!greedy) {
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      if (j < M) {
+        // reads clamped to the row: a candidate outside the vocabulary
+        // (only from nnhip_spec_accept's caller) reads the last column
+        const int c = min(max(s.cand[b * k + j], 0), V - 1);
+        lc[j] = tlogits[((int64_t)b * tr + j) * V + c];
+        qcp[j] = qimp ? qlrow(j)[c] : s.qprob[((int64_t)b * k + j) * V + c];
+      }
+    }
+    if (qimp) {
+#pragma unroll
+      for (int j = 0; j < kPre; ++j)
+        if (j < M) qcp[j] = q_of(qcp[j], j);
+    }
+  }
+  // accept test of position j given its candidate's p and q
+  auto test = [&](int j, int c, float lj, float qc) {
+    if (greedy) return c == argmax_of(j);
+    const RowStats st = stats_of(j);
+    const float pc = prob_of(lj, c, s.T, st);
+    const float r = s.ua ? s.ua[(int64_t)b * k + j] : uniform(s.seed, seq, cyc, k + j);
+    if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
+    return __fmul_rn(r, qc) < pc;
+  };
+#pragma unroll
+  for (int j = 0; j < kPre; ++j) {
+    if (j >= M || rej >= 0) break;
+    const int c = s.cand[b * k + j];
+    if (!test(j, c, lc[j], qcp[j])) { rej = j; break; }
+    if (threadIdx.x == 0) out[nout] = c;
+    ++nout;
+  }
+  for (int j = kPre; j < M && rej < 0; ++j) {
+    const int c = s.cand[b * k + j];
+    const int cr = min(max(c, 0), V - 1);
+    const float lj = greedy ? 0.f : tlogits[((int64_t)b * tr + j) * V + cr];
+    const float qc = greedy ? 0.f
+                     : qimp ? q_of(qlrow(j)[cr], j)
+                            : s.qprob[((int64_t)b * k + j) * V + cr];
+    if (!test(j, c, lj, qc)) { rej = j; break; }
+    if (threadIdx.x == 0) out[nout] = c;
+    ++nout;
+  }
+  const int gen = gen0 + (rej < 0 ? M : rej);
+  if (threadIdx.x == 0) {
+    int kind = 0, tok = -1;
+    if (rej >= 0) {
+      if (greedy) tok = argmax_of(rej);
+      else kind = 1;
+    } else if (gen < s.max_new) {
+      if (greedy) tok = argmax_of(M);
+      else kind = 2;
+    }
+    rec[0] = kind;
+    rec[1] = rej;
+    rec[2] = (int)ties;
+    rec[3] = tok;
+    if (kind == 1 && qimp) {
+      rec[5] = __float_as_int(qst[rej].mx);
+      rec[6] = __float_as_int(qst[rej].rsum);
+      rec[7] = __float_as_int(qst[rej].rfs);
+    }
+  }
+}
+
+// weight of entry v of the row to draw from: the residual max(0, p - q)
+// (residual_sample's expressions) and p (fill_probs')
+__device__ __forceinline__ void draw_weights(float xt, float xq, int v, float T,
+                                             const RowStats &tst, bool implicit_q,
+                                             const RowStats &qs, float &r, float &p) {
+  p = prob_of(xt, v, T, tst);
+  const float q = implicit_q ? (expf(scaled(xq, T) - qs.mx) * qs.rsum) * qs.rfs : xq;
+  r = fmaxf(0.0f, p - q);
+}
+
+struct DrawRow {
+  const float *trow, *qrow;   // target logits; draft logits or probabilities
+  bool implicit_q;
+  RowStats tst, qs;
+};
+
+__device__ __forceinline__ DrawRow draw_row(const SpecState &s, const float *tlogits,
+                                            int b, const int32_t *rec) {
+  const int kind = rec[0], rej = rec[1];
+  const int k = s.k, V = s.V;
+  const int gen0 = s.gen[b];
+  const int M = min(k, s.max_new - gen0);
+  const int j = kind == 1 ? rej : M;
+  DrawRow d;
+  d.trow = tlogits + ((int64_t)b * verify_rows(s) + j) * V;
+  const float *ts = s.tstat + ((int64_t)b * (k + 1) + j) * kTstat;
+  d.tst = mk_stats(ts[0], ts[1], ts[2]);
+  d.tst.tau = __float_as_uint(ts[4]);
+  d.tst.tix = __float_as_int(ts[5]);
+  d.implicit_q = s.qlog != nullptr;
+  d.qrow = nullptr;
+  d.qs = mk_stats(0.f, 0.f, 0.f);
+  if (kind == 1) {
+    if (d.implicit_q) {
+      const int64_t qjs = s.qlog_js ? s.qlog_js : (int64_t)s.B * V;
+      const int64_t qbs = s.qlog_bs ? s.qlog_bs : (int64_t)V;
+      d.qrow = s.qlog + j * qjs + b * qbs;
+      d.qs = mk_stats(__int_as_float(rec[5]), __int_as_float(rec[6]), __int_as_float(rec[7]));
+    } else {
+      d.qrow = s.qprob + ((int64_t)b * k + j) * V;
+    }
+  }
+  return d;
+}
+
+constexpr int kDrawThreads = 256;
+
+__global__ __launch_bounds__(kDrawThreads) void draw_chunks_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  __shared__ double s_red[2][kDrawThreads / 64];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int32_t *rec = s.rec + (int64_t)b * kRec;
+  const int kind = rec[0];
+  if (kind <= 0) return;
+  const DrawRow d = draw_row(s, tlogits, b, rec);
+  const int V = s.V, CH = (V + kDrawChunks - 1) / kDrawChunks;
+  const int v0 = c * CH, v1 = min(V, v0 + CH);
+  constexpr int kPerT = (kMaxV / kDrawChunks + kDrawThreads - 1) / kDrawThreads;
+  float xt[kPerT], xq[kPerT];
+#pragma unroll
+  for (int i = 0; i < kPerT; ++i) {
+    const int v = min(v0 + (int)threadIdx.x + i * kDrawThreads, V - 1);
+    xt[i] = d.trow[v];
+    xq[i] = kind == 1 ? d.qrow[v] : 0.f;
+  }
+  double rs = 0.0, ps = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPerT; ++i) {
+    const int v = v0 + (int)threadIdx.x + i * kDrawThreads;
+    if (v < v1) {
+      float r, p;
+      draw_weights(xt[i], xq[i], v, s.T, d.tst, d.implicit_q, d.qs, r, p);
+      rs += (double)r;
+      ps += (double)p;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    rs += __shfl_xor(rs, o, 64);
+    ps += __shfl_xor(ps, o, 64);
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { s_red[0][w] = rs; s_red[1][w] = ps; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double tr = 0.0, tp = 0.0;
+#pragma unroll
+    for (int i = 0; i < kDrawThreads / 64; ++i) { tr += s_red[0][i]; tp += s_red[1][i]; }
+    double *out = s.chunks + ((int64_t)b * kDrawChunks + c) * 2;
+    out[0] = tr;
+    out[1] = tp;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void accept_final_kernel(
+    SpecState s, const float *__restrict__ tlogits) {
+  __shared__ SmallShared sh;
+  const int b = blockIdx.x;
+  const int32_t *rec = s.rec + (int64_t)b * kRec;
+  const int kind = rec[0];
+  if (kind < 0) return;
+  const int V = s.V, k = s.k;
+  const int gen0 = s.gen[b];
+  const int M = min(k, s.max_new - gen0);
+  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const int tstart = s.tlen[b], dstart = s.dlen[b];
+  const int rej = rec[1];
+  int32_t *out = s.out + (int64_t)b * s.out_stride;
+  const int nout = s.P + gen0 + (rej < 0 ? M : rej);
+  int gen = gen0 + (rej < 0 ? M : rej);
+  int tok = rec[3], catch_tok = -1;
+  if (kind > 0) {
+    const float u = s.ur ? s.ur[b] : uniform(s.seed, seq, cyc, 2 * k);
+    // the draw's weights: the residual, or p where the residual is all zero
+    // (residual_sample) and for the bonus row
+    const double *ch = s.chunks + (int64_t)b * kDrawChunks * 2;
+    double rtot = 0.0;
+    if (kind == 1) {
+      for (int c = 0; c < kDrawChunks; ++c) rtot += ch[2 * c];
+    }
+    const int sel = (kind == 1 && rtot > 0.0) ? 0 : 1;
+    double S = 0.0;
+    for (int c = 0; c < kDrawChunks; ++c) S += ch[2 * c + sel];
+    const double target = (double)u * S;
+    // the chunk in which the running sum reaches the target
+    int kc = kDrawChunks - 1;
+    double pre = 0.0, pk = 0.0;
+    for (int c = 0; c < kDrawChunks; ++c) {
+      const double x = ch[2 * c + sel];
+      if (pre + x >= target - 1e-12 * S) { kc = c; pk = pre; break; }
+      pre += x;
+    }
+    // block_sample inside that chunk: contiguous runs per thread, running
+    // double sums from the chunk's prefix
+    const DrawRow d = draw_row(s, tlogits, b, rec);
+    const int CH = (V + kDrawChunks - 1) / kDrawChunks;
+    const int v0 = kc * CH, v1 = min(V, v0 + CH);
+    constexpr int E = (kMaxV / kDrawChunks + kThreads - 1) / kThreads;
+    const int E_ = (CH + kThreads - 1) / kThreads;
+    const int b0 = v0 + (int)threadIdx.x * E_;
+    float wv[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int v = b0 + i;
+      wv[i] = 0.f;
+      if (i < E_ && v < v1) {
+        float r, p;
+        draw_weights(d.trow[v], kind == 1 ? d.qrow[v] : 0.f, v, s.T, d.tst,
+                     d.implicit_q, d.qs, r, p);
+        wv[i] = sel == 0 ? r : p;
+      }
+    }
+    double loc = 0.0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) loc += (double)wv[i];
+    double St;
+    double c = pk + block_excl_scan_d(loc, sh, &St);
+    int found = 0x7fffffff;
+    if (c + loc >= target - 1e-12 * S) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const int v = b0 + i;
+        c += (double)wv[i];
+        if (found == 0x7fffffff && i < E_ && v < v1 && v < V - 1 && c >= target) found = v;
+      }
+    }
+    const int r = block_min_i(found, sh);
+    tok = r != 0x7fffffff ? r : min(v1, V - 1);
+    catch_tok = kind == 1 ? tok : s.cand[b * k + M - 1];
+  } else if (tok >= 0) {
+    catch_tok = rej >= 0 ? tok : s.cand[b * k + M - 1];
+  }
+  if (threadIdx.x == 0) {
+    const int64_t ties = rec[2];
+    int64_t *st = s.stats + (int64_t)b * kSpecStats;
+    st[0] += 1;
+    st[1] += M;
+    st[2] += (rej < 0 ? M : rej);
+    st[3] += ties;
+    if (s.n_acc_out) {
+      s.n_acc_out[b] = rej < 0 ? M : rej;
+      s.tok_out[b] = tok;
+    }
+    if (tok >= 0) {
+      out[nout] = tok;
+      ++gen;
+      s.cur[b] = tok;
+      if (rej >= 0) st[4] += 1; else st[5] += 1;
+    }
+    const int keep = rej >= 0 ? rej : M;
+    s.tlen[b] = tstart + keep + 1;
+    // The draft cache keeps [generated.back(), c_0 .. c_{rej-1}] after a
+    // rejection (layer.cpp:1636) or [generated.back(), c_0 .. c_{M-2}] after
+    // full acceptance, then takes the catch-up token (layer.cpp:1639-1653);
+    // dlen is the length after that catch-up, which writes at dlen - 1.
+    if (tok >= 0) s.dlen[b] = dstart + keep + (rej >= 0 ? 2 : 1);
+    st[6] = max(st[6], (int64_t)(tstart + M + 1));
+    st[7] = max(st[7], (int64_t)max(dstart + M, tok >= 0 ? s.dlen[b] : 0));
+    s.catchup[b] = tok >= 0 ? 1 : 0;
+    s.catch_tok[b] = catch_tok;
+    s.pair[2 * b] = catch_tok;
+    s.pair[2 * b + 1] = tok;
+    s.gen[b] = gen;
+    s.cyc[b] = (int)cyc + 1;
+    if (gen >= s.max_new) {
+      s.active[b] = 0;
+      s.catchup[b] = 0;
+      atomicSub(s.n_active, 1);
+    }
+    if (s.n_far && s.max_new - gen0 > k + 1 && s.max_new - gen <= k + 1)
+      atomicSub(s.n_far, 1);
+  }
+}
+
 __global__ void accept_rows_reset_kernel(SpecState s) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b == 0) *s.n_active = s.B;
@@ -1136,6 +1486,7 @@ bool filtered(const SpecState &s) {
 }  // namespace
 
 int g_accept_early = 1;
+int g_accept_split = 1;
 
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl) {
@@ -1161,6 +1512,25 @@ void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
   NNHIP_CHECK(hipGetLastError());
 }
 
+// the accept step after the row statistics: accept_kernel, or its split
+// form when the state carries the split's scratch
+void launch_accept_step(hipStream_t st, const SpecState &s, const float *tlogits) {
+  if (s.rec && s.chunks) {
+    hipLaunchKernelGGL(accept_decide_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                       tlogits);
+    NNHIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(draw_chunks_kernel, dim3(kDrawChunks, s.B), dim3(kDrawThreads),
+                       0, st, s, tlogits);
+    NNHIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(accept_final_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                       tlogits);
+  } else {
+    hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
+                       tlogits);
+  }
+  NNHIP_CHECK(hipGetLastError());
+}
+
 void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
   NNHIP_REQUIRE(s.tstat != nullptr, kErrArg, "accept: no row statistics");
   if (filtered(s))
@@ -1170,9 +1540,7 @@ void launch_accept(hipStream_t st, const SpecState &s, const float *tlogits) {
     hipLaunchKernelGGL(target_stats_kernel<false>, dim3(s.k + 1, s.B),
                        dim3(kThreads), 0, st, s, tlogits);
   NNHIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
-                     tlogits);
-  NNHIP_CHECK(hipGetLastError());
+  launch_accept_step(st, s, tlogits);
 }
 
 void launch_draft_sample_tiles(hipStream_t st, const SpecState &s, int j,
@@ -1270,6 +1638,7 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   a.tw = kTileW;
   a.cand = const_cast<int32_t *>(cand);
   a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
+  attach_split(a);
   if (early) {
     if (!minrej.p) minrej.alloc(s.B);
     a.minrej = minrej.p;
@@ -1287,8 +1656,7 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   hipLaunchKernelGGL(accept_rows_stats_kernel, dim3(s.B * (s.k + 1)), dim3(kThreads),
                      0, st, a, tlogits);
   NNHIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(accept_kernel, dim3(s.B), dim3(kThreads), 0, st, a, tlogits);
-  NNHIP_CHECK(hipGetLastError());
+  launch_accept_step(st, a, tlogits);
 }
 
 void AcceptRows::launch(hipStream_t st, const float *tlogits, const float *qprob,
@@ -1298,10 +1666,21 @@ void AcceptRows::launch(hipStream_t st, const float *tlogits, const float *qprob
   a.qprob = const_cast<float *>(qprob);
   a.cand = const_cast<int32_t *>(cand);
   a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
+  attach_split(a);
   hipLaunchKernelGGL(accept_rows_reset_kernel, dim3((s.B + 255) / 256),
                      dim3(256), 0, st, a);
   NNHIP_CHECK(hipGetLastError());
   launch_accept(st, a, tlogits);
+}
+
+void AcceptRows::attach_split(SpecState &a) {
+  if (!g_accept_split) return;
+  if (!rec.p) {
+    rec.alloc((size_t)s.B * kAcceptRec);
+    chunks.alloc((size_t)s.B * kDrawChunks * 2);
+  }
+  a.rec = rec.p;
+  a.chunks = chunks.p;
 }
 
 }  // namespace nnhip
