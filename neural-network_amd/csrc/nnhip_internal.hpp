@@ -595,6 +595,10 @@ struct SpecState {
   // [B] lowest position whose candidate is certainly rejected, or null: the
   // row statistics skip the rows after it (accept_rows_stats_kernel)
   int32_t *minrej = nullptr;
+  // with minrej: [B][k+1] workgroups of a row done, and the verify rows'
+  // tile statistics [B][k+1][nt] (accept_tiles_kernel)
+  int32_t *rowcnt = nullptr;
+  float2 *ttiles = nullptr;
   // the split accept step's scratch: [B][kAcceptRec] records and
   // [B][kDrawChunks][2] chunk sums (null: one accept_kernel per sequence)
   int32_t *rec = nullptr;
@@ -629,6 +633,8 @@ struct AcceptRows {
   DevBuf<float> tstat;
   DevBuf<float2> dtiles;   // [B][k][nt] draft-row tile statistics
   DevBuf<int32_t> minrej;  // [B] first certain rejection (early exit)
+  DevBuf<int32_t> rowcnt;  // [B][k+1] workgroups done per row (early exit)
+  DevBuf<float2> ttiles;   // [B][k+1][nt] verify-row tile statistics
   DevBuf<int32_t> rec;     // split accept step: records and chunk sums
   DevBuf<double> chunks;
   DevBuf<int64_t> stats;

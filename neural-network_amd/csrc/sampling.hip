@@ -848,67 +848,161 @@ __device__ __forceinline__ int residual_sample(
 }
 
 // The statistics of the accept step from logits (AcceptRows::launch_logits,
-// T > 0 without top-k / top-p), rows decided in order: one workgroup per
-// (verify row j, sequence b), numbered row-major (every sequence's row 0,
-// then every row 1, ...), so that the workgroups of row j mostly start after
-// those of the rows before it have finished.  A workgroup forms the target
-// row's statistics (target_stats_kernel's arithmetic) and, for a drafted
-// position, the draft row's tile statistics (row_tile_stats_kernel's) and
-// their combination (the accept step's), then tests its candidate; when the
-// candidate is rejected by a margin no rounding difference between this
-// kernel and the accept step can cross (r * q >= p * (1 + 1e-5)), it lowers
-// minrej[b] to j.  A workgroup whose sequence already has a smaller minrej
-// returns at once: the accept step, which decides every position again from
-// these statistics, stops at or before that rejection and never reads rows
-// after it (layer.cpp:1581-1630 computes p_j only until the first rejection).
-__global__ __launch_bounds__(kThreads) void accept_rows_stats_kernel(
-    SpecState s, const float *__restrict__ tlogits) {
-  __shared__ SmallShared sh;
-  __shared__ float2 s_tiles[kTileMax * 64];
-  const int j = blockIdx.x / s.B, b = blockIdx.x % s.B;
+// T > 0 without top-k / top-p), rows decided in order.  Workgroups are
+// numbered row-major (every sequence's row 0, then every row 1, ...); each
+// takes a chunk of tiles of one verify row j of one sequence b, and forms
+// for every tile of the chunk the target row's tile statistics (max, sum of
+// exp) and, for a drafted position, the draft row's.  The last workgroup of
+// (b, j) to
+// finish (a counter per row) combines all of the row's tiles, as the accept
+// step combines a draft row's (wave_tiles_stats): the target row's
+// statistics go to tstat, and the candidate is tested; when it is rejected
+// by a margin no rounding difference between this kernel and the accept step
+// can cross (r * q >= p * (1 + 1e-5)), minrej[b] is lowered to j.  A
+// workgroup whose sequence already has a smaller minrej returns at once: the
+// accept step, which decides every position again from these statistics,
+// stops at or before that rejection and never reads rows after it
+// (layer.cpp:1581-1630 computes p_j only until the first rejection).
+// Tile statistics cross workgroups through agent-scope atomic stores and
+// loads; a workgroup's stores are complete (s_waitcnt) before it counts
+// itself, and the counting workgroups never wait for one another.  The
+// tiles here are kWideTile columns wide (one wave's: 16 logits a lane, one
+// pair of wave reductions each), and a workgroup takes kStatWaves of them.
+constexpr int kWideTile = 1024;
+constexpr int kStatWaves = 4;
+constexpr int kStatThreads = 64 * kStatWaves;
+
+// RowStats of a row from nt <= 64 tile statistics, by one wave: the
+// operations of wave_tiles_stats with one tile a lane
+__device__ __forceinline__ RowStats wave_few_tiles_stats(const float2 *tl, int nt) {
+  const int lane = threadIdx.x & 63;
+  const float2 v = tl[min(lane, nt - 1)];
+  const float mx = wave_max_all(lane < nt ? v.x : -INFINITY);
+  float e = 0.f;
+  if (lane < nt && v.x > -INFINITY) e += v.y * expf(v.x - mx);
+  e = wave_sum_all(e);
+  const float rs = 1.0f / e;
+  return mk_stats(mx, rs, 1.0f / (e * rs));
+}
+
+// (max s, sum exp(s - max)), s = l / T, of one wave's wide tile: lane l holds
+// columns n0 + 128 i + {0, 1}, n0 = tile start + 2 l, i < 8
+__device__ __forceinline__ float2 wide_stat(const float2 (&v)[kTileRun], int n0,
+                                            int V, float T) {
+  float mxl = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kTileRun; ++i) {
+    const int n = n0 + i * kTileW;
+    if (n < V) mxl = fmaxf(mxl, scaled(v[i].x, T));
+    if (n + 1 < V) mxl = fmaxf(mxl, scaled(v[i].y, T));
+  }
+  const float mx = wave_max_all(mxl);
+  float e = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTileRun; ++i) {
+    const int n = n0 + i * kTileW;
+    if (n < V) e += expf(scaled(v[i].x, T) - mx);
+    if (n + 1 < V) e += expf(scaled(v[i].y, T) - mx);
+  }
+  return make_float2(mx, wave_sum_all(e));
+}
+
+__device__ __forceinline__ void st_pair(float2 *p, float2 v) {
+  const uint64_t bits =
+      ((uint64_t)__float_as_uint(v.y) << 32) | (uint64_t)__float_as_uint(v.x);
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_pair(const float2 *p) {
+  const uint64_t bits = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
+
+template <bool PAIRS>
+__device__ __forceinline__ void load_tile_run(const float *row, int t0, int V, int lane,
+                                              float2 (&v)[kTileRun]) {
+#pragma unroll
+  for (int i = 0; i < kTileRun; ++i) {
+    const int n = (t0 + i) * kTileW + 2 * lane;
+    if (PAIRS && n + 1 < V) {
+      v[i] = *reinterpret_cast<const float2 *>(row + n);
+    } else {
+      v[i].x = n < V ? row[n] : 0.f;
+      v[i].y = n + 1 < V ? row[n + 1] : 0.f;
+    }
+  }
+}
+
+template <bool PAIRS>
+__global__ __launch_bounds__(kStatThreads, 8) void accept_tiles_kernel(
+    SpecState s, const float *__restrict__ tlogits, int nch) {
+  __shared__ float2 s_t[kMaxV / kWideTile], s_d[kMaxV / kWideTile];
+  __shared__ RowStats s_st[2];
+  __shared__ int s_last;
+  const int per_row = s.B * nch;
+  const int j = blockIdx.x / per_row, rem = blockIdx.x % per_row;
+  const int b = rem / nch, ch = rem % nch;
+  // the first certain rejection first: most workgroups of rows j >= 2 end
+  // here after one load
+  if (j > 0 && __hip_atomic_load(s.minrej + b, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) < j)
+    return;
   if (!s.active[b]) return;
   const int gen0 = s.gen[b];
   const int M = min(s.k, s.max_new - gen0);
   if (j > M || (j == M && gen0 + M >= s.max_new)) return;
-  if (j > 0 && __hip_atomic_load(s.minrej + b, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) < j)
-    return;
-  const int64_t r = (int64_t)b * (s.k + 1) + j;
-  const float *row = tlogits + ((int64_t)b * verify_rows(s) + j) * s.V;
-  const RowStats st = row_stats<false>(row, s.V, s.T, sh);
-  if (threadIdx.x == 0) {
-    float *ts = s.tstat + r * kTstat;
-    ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs;
-    ts[4] = __uint_as_float(st.tau); ts[5] = __int_as_float(st.tix);
-  }
-  if (j >= M) return;                         // the bonus row
-  // the draft row's tile statistics, runs of 8 tiles per wave
+  const bool drafted = j < M;                 // else the bonus row
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int V = s.V, nt = s.nt;
+  const float *trow = tlogits + ((int64_t)b * verify_rows(s) + j) * V;
   const float *drow = s.qlog + j * s.qlog_js + b * s.qlog_bs;
-  float2 *dt = const_cast<float2 *>(s.dtiles) + ((int64_t)b * s.k + j) * s.nt;
-  for (int base = w * kTileRun; base < s.nt; base += kWaves * kTileRun) {
-    float2 v[kTileRun];
-#pragma unroll
-    for (int i = 0; i < kTileRun; ++i) {
-      const int n = (base + i) * kTileW + 2 * lane;
-      v[i].x = n < s.V ? drow[n] : 0.f;
-      v[i].y = n + 1 < s.V ? drow[n + 1] : 0.f;
+  float2 *tt = s.ttiles + ((int64_t)b * (s.k + 1) + j) * nt;
+  float2 *dt = const_cast<float2 *>(s.dtiles) + ((int64_t)b * s.k + j) * nt;
+  const int wt = ch * kStatWaves + w;         // the wave's wide tile
+  if (wt < nt) {
+    static_assert(kWideTile == kTileRun * kTileW, "a wide tile is one run of 128-column tiles");
+    float2 tv[kTileRun], dv[kTileRun];
+    load_tile_run<PAIRS>(trow, wt * kTileRun, V, lane, tv);
+    if (drafted) load_tile_run<PAIRS>(drow, wt * kTileRun, V, lane, dv);
+    const int n0 = wt * kWideTile + 2 * lane;
+    const float2 a = wide_stat(tv, n0, V, s.T);
+    if (lane == 0) st_pair(tt + wt, a);
+    if (drafted) {
+      const float2 d = wide_stat(dv, n0, V, s.T);
+      if (lane == 0) st_pair(dt + wt, d);
     }
-#pragma unroll
-    for (int i = 0; i < kTileRun; ++i) {
-      const int tn = base + i;
-      if (tn >= s.nt) break;                  // whole wave
-      const float2 ts = tile_stat(v[i].x, v[i].y, tn * kTileW + 2 * lane, s.V, s.T);
-      if (lane == 0) { dt[tn] = ts; s_tiles[tn] = ts; }
-    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = atomicAdd(s.rowcnt + (int64_t)b * (s.k + 1) + j, 1) == nch - 1;
+  __syncthreads();
+  if (!s_last) return;
+  // the last workgroup of the row: every tile, then the row's statistics
+  for (int t = threadIdx.x; t < nt; t += kStatThreads) {
+    s_t[t] = ld_pair(tt + t);
+    if (drafted) s_d[t] = ld_pair(dt + t);
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const RowStats qs = wave_tiles_stats(s_tiles, s.nt);
-    if (threadIdx.x == 0) {
+  if (w == 0) {
+    const RowStats st = wave_few_tiles_stats(s_t, nt);
+    if (lane == 0) s_st[0] = st;
+  } else if (w == 1 && drafted) {
+    const RowStats qs = wave_few_tiles_stats(s_d, nt);
+    if (lane == 0) s_st[1] = qs;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const RowStats st = s_st[0];
+    float *ts = s.tstat + ((int64_t)b * (s.k + 1) + j) * kTstat;
+    ts[0] = st.mx; ts[1] = st.rsum; ts[2] = st.rfs;
+    ts[4] = __uint_as_float(st.tau); ts[5] = __int_as_float(st.tix);
+    if (drafted) {
+      const RowStats qs = s_st[1];
       // (a candidate outside the vocabulary reads the last column)
-      const int c = min(max(s.cand[b * s.k + j], 0), s.V - 1);
-      const float pc = prob_of(row[c], c, s.T, st);
+      const int c = min(max(s.cand[b * s.k + j], 0), V - 1);
+      const float pc = prob_of(trow[c], c, s.T, st);
       const float qc = (expf(scaled(drow[c], s.T) - qs.mx) * qs.rsum) * qs.rfs;
       const float u = s.ua ? s.ua[(int64_t)b * s.k + j]
                            : uniform(s.seed, s.seq0 + b, (uint32_t)s.cyc[b], s.k + j);
@@ -1455,6 +1549,8 @@ __global__ void accept_rows_reset_kernel(SpecState s) {
   s.cur[b] = -1; s.tlen[b] = 0; s.dlen[b] = 0; s.gen[b] = 0; s.cyc[b] = 1;
   s.active[b] = 1; s.catchup[b] = 0; s.catch_tok[b] = -1;
   if (s.minrej) s.minrej[b] = 0x7fffffff;
+  if (s.rowcnt)
+    for (int j = 0; j <= s.k; ++j) s.rowcnt[(int64_t)b * (s.k + 1) + j] = 0;
   for (int i = 0; i < kSpecStats; ++i) s.stats[(int64_t)b * kSpecStats + i] = 0;
 }
 
@@ -1640,8 +1736,18 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   a.ua = ua; a.ur = ur; a.n_acc_out = n_acc; a.tok_out = tok;
   attach_split(a);
   if (early) {
-    if (!minrej.p) minrej.alloc(s.B);
+    if (!minrej.p) {
+      minrej.alloc(s.B);
+      rowcnt.alloc((size_t)s.B * (s.k + 1));
+      ttiles.alloc((size_t)s.B * (s.k + 1) * nt);
+    }
     a.minrej = minrej.p;
+    a.rowcnt = rowcnt.p;
+    a.ttiles = ttiles.p;
+    // wide tiles: the draft probabilities the accept step forms come from
+    // these statistics
+    a.nt = (s.V + kWideTile - 1) / kWideTile;
+    a.tw = kWideTile;
   }
   hipLaunchKernelGGL(accept_rows_reset_kernel, dim3((s.B + 255) / 256),
                      dim3(256), 0, st, a);
@@ -1652,9 +1758,16 @@ void AcceptRows::launch_logits(hipStream_t st, const float *tlogits,
   }
   // rows decided in order: the statistics of the rows up to each
   // sequence's first rejection, then the accept step
-  NNHIP_REQUIRE((int64_t)s.B * (s.k + 1) <= 0x7fffffff, kErrArg, "accept: too many rows");
-  hipLaunchKernelGGL(accept_rows_stats_kernel, dim3(s.B * (s.k + 1)), dim3(kThreads),
-                     0, st, a, tlogits);
+  const int nch = (a.nt + kStatWaves - 1) / kStatWaves;
+  NNHIP_REQUIRE((int64_t)s.B * (s.k + 1) * nch <= 0x7fffffff, kErrArg, "accept: too many rows");
+  const dim3 grid(s.B * (s.k + 1) * nch);
+  if (s.V % 2 == 0 && reinterpret_cast<uintptr_t>(tlogits) % 8 == 0 &&
+      reinterpret_cast<uintptr_t>(dlogits) % 8 == 0)
+    hipLaunchKernelGGL(accept_tiles_kernel<true>, grid, dim3(kStatThreads), 0, st, a,
+                       tlogits, nch);
+  else
+    hipLaunchKernelGGL(accept_tiles_kernel<false>, grid, dim3(kStatThreads), 0, st, a,
+                       tlogits, nch);
   NNHIP_CHECK(hipGetLastError());
   launch_accept_step(st, a, tlogits);
 }
