@@ -271,12 +271,12 @@ CYCLE_GEMMS = [
     ("draft qkv", 32, 512, 1536, 8, "gemm_limb_kernel", 16),
     ("draft o", 32, 512, 512, 9, "gemm_limb_kernel", 16),
     ("draft gate/up", 32, 512, 4096, 8, "gemm_limb_kernel", 16),
-    ("draft down", 32, 2048, 512, 1, "gemv_kernel", 16),
+    ("draft down", 32, 2048, 512, 1, "gemv16_kernel", 16),
     ("draft lm head", 32, 512, 32000, 6, "gemm_lds_kernel", 4),
     ("draft qkv (catch-up)", 64, 512, 1536, 8, "gemm_limb_kernel", 4),
     ("draft o (catch-up)", 64, 512, 512, 9, "gemm_limb_kernel", 4),
     ("draft gate/up (catch-up)", 64, 512, 4096, 8, "gemm_limb_kernel", 4),
-    ("draft down (catch-up)", 64, 2048, 512, 1, "gemv_kernel", 4),
+    ("draft down (catch-up)", 64, 2048, 512, 1, "gemv16_kernel", 4),
     ("draft lm head (catch-up)", 32, 512, 32000, 6, "gemm_lds_kernel", 1),
     ("verify qkv", 192, 1024, 3072, 7, "gemm_lds_kernel", 12),
     ("verify o", 192, 1024, 1024, 9, "gemm_limb_kernel", 12),
@@ -381,28 +381,38 @@ CFG5_NOTE = os.path.join(ROOT, "profiles", "cfg5_accept_kernel_stats.md")
 
 
 def cfg5_accept(ctx, iters=1000):
-    """Logits in, (accepted count, resampled token) out: the draft rows'
-    tile statistics, the target rows' statistics and the accept / residual
-    kernel per launch (nnhip_spec_accept's path).  Algorithmic bytes: every
-    target and draft logit read once (dense: the kernels read every row,
-    with no early exit at the first rejection), 2 x 256 x 8 x 32000 x 4 =
-    524,288,000 B a launch."""
+    """Logits in, (accepted count, resampled token) out, on
+    nnhip_spec_accept's path: the state reset, the rows' statistics up to
+    each sequence's first rejection (the reference forms p_j only until the
+    first rejection, layer.cpp:1581-1630; rows after it are skipped), the
+    accept decisions, the residual draw and the state update, per launch;
+    1000 launches over 3 sets of logits, each set's draft ids drawn from its
+    own draft probabilities.  Bytes: `bytes` counts what the algorithm must
+    read, the target and draft rows up to and including each sequence's
+    first rejection (all k when every draft is accepted), 2 x V x 4 B a row,
+    from input set 0's accepted counts (the other sets are drawn the same
+    way); `dense_bytes` is every logit once, 2 x 256 x 8 x 32000 x 4 =
+    524,288,000 B, for comparison with a kernel that reads every row."""
     c = CFG5
     ms5, nacc = nnhip.bench_spec_accept(ctx, c["B"], c["k"], c["V"], 1.0,
                                         iters=iters, nbuf=3)
-    b5 = 2 * c["B"] * c["k"] * c["V"] * 4
+    rows = int(np.minimum(np.asarray(nacc) + 1, c["k"]).sum())
+    b5 = rows * 2 * c["V"] * 4
+    dense = 2 * c["B"] * c["k"] * c["V"] * 4
     # the kernel trace of `bench.py --cfg5-probe` (this function alone):
-    # the mean durations of the three kernels summed per launch
+    # the mean durations of its kernels summed per launch
     us_prof = profile_value(CFG5_NOTE, "kernel_trace_us_per_launch")
-    return dict(us=round(ms5 * 1e3, 2), bytes=b5, iters=iters,
+    return dict(us=round(ms5 * 1e3, 2), bytes=b5, rows_read=rows,
+                dense_bytes=dense, iters=iters,
                 achieved_GBs=round(b5 / (ms5 / 1e3) / 1e9, 1),
                 frac=round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                dense_equivalent_GBs=round(dense / (ms5 / 1e3) / 1e9, 1),
                 profile_us=us_prof,
                 profile_frac=(round(b5 / us_prof / 1e3 / HBM_PEAK_GBS, 4)
                               if us_prof else None),
                 mean_accepted=round(float(np.mean(nacc)), 3),
-                timed="draft tile statistics + target statistics + accept "
-                      "kernel, logits in")
+                timed="reset + row statistics up to the first rejection + "
+                      "accept decisions + residual draw, logits in")
 
 
 def cfg5_probe():

@@ -84,12 +84,12 @@ int nnhip_bench_attention(nnhip_ctx *ctx, int B, int S, int H, int D,
 }
 
 // Acceptance step of the speculative loop from logits, as
-// nnhip_spec_accept runs it: the draft rows' tile statistics
-// (row_tile_stats_kernel), the per-sequence state reset, the target rows'
-// statistics and the accept / residual kernel, timed together.  B sequences
+// nnhip_spec_accept runs it (AcceptRows::launch_logits: the state reset, the
+// rows' statistics up to each sequence's first rejection, the accept
+// step), timed together.  B sequences
 // x k positions x V, target and draft logits N(0, 2) (nbuf sets of each),
-// draft ids drawn from set 0's draft probabilities with a separate stream
-// beforehand (fixture preparation, not timed), one accept uniform per
+// each set's draft ids drawn from its draft probabilities with a separate
+// stream beforehand (fixture preparation, not timed), one accept uniform per
 // position and one resample uniform per sequence.  n_accept (host, [B])
 // receives the accepted counts of input set 0.
 int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
@@ -101,8 +101,9 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
     hipStream_t st = ctx->c.stream;
     const int64_t n = (int64_t)B * k * V;
     std::vector<nnhip::DevBuf<float>> TL(nbuf), DL(nbuf);
+    std::vector<nnhip::DevBuf<int32_t>> dtok(nbuf);
     nnhip::DevBuf<float> q0(n);
-    nnhip::DevBuf<int32_t> dtok((size_t)B * k), nacc(B), next(B);
+    nnhip::DevBuf<int32_t> nacc(B), next(B);
     nnhip::DevBuf<float> ua((size_t)B * k), ur(B), us((size_t)B * k);
     // uniforms in [0, 1) from a fixed host xorshift stream
     std::vector<float> hu((size_t)B * k * 2 + B);
@@ -120,15 +121,18 @@ int nnhip_bench_spec_accept(nnhip_ctx *ctx, int B, int k, int V, float T,
       nnhip::launch_init_normal(st, TL[i].p, 1, (int)n, 0, 1, 4000 + i, 0, 2.f, 0);
       nnhip::launch_init_normal(st, DL[i].p, 1, (int)n, 0, 1, 5000 + i, 0, 2.f, 0);
     }
-    // set 0's draws from its draft probabilities are the draft ids
-    nnhip::launch_sample_rows(st, DL[0].p, B * k, V, Tq, us.p, dtok.p, q0.p);
+    // each set's draft ids are draws from its own draft probabilities
+    for (int i = 0; i < nbuf; ++i) {
+      dtok[i].alloc((size_t)B * k);
+      nnhip::launch_sample_rows(st, DL[i].p, B * k, V, Tq, us.p, dtok[i].p, q0.p);
+    }
     nnhip::AcceptRows ar(B, k, V, T);
     *ms = time_loop(ctx, iters, [&](int i) {
       const int j = i % nbuf;
-      ar.launch_logits(st, TL[j].p, DL[j].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
+      ar.launch_logits(st, TL[j].p, DL[j].p, dtok[j].p, ua.p, ur.p, nacc.p, next.p);
     });
     if (n_accept) {
-      ar.launch_logits(st, TL[0].p, DL[0].p, dtok.p, ua.p, ur.p, nacc.p, next.p);
+      ar.launch_logits(st, TL[0].p, DL[0].p, dtok[0].p, ua.p, ur.p, nacc.p, next.p);
       NNHIP_CHECK(hipMemcpyAsync(n_accept, nacc.p, (size_t)B * 4, hipMemcpyDeviceToHost, st));
       NNHIP_CHECK(hipStreamSynchronize(st));
     }
