@@ -51,6 +51,55 @@ float or_uniform(uint64_t seed, uint32_t seq, uint32_t cycle, uint32_t slot) {
   return (float)(o[0] >> 8) * (1.0f / 16777216.0f);
 }
 
+/* std::mt19937: 624-word state, recurrence over words i, i + 1, i + 397,
+ * matrix 0x9908b0df, tempering (11, 7 / 0x9d2c5680, 15 / 0xefc60000, 18);
+ * seeding x_i = 1812433253 (x_{i-1} ^ (x_{i-1} >> 30)) + i. */
+void or_mt_seed(or_mt *g, uint32_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < 624; ++i)
+    g->mt[i] = 1812433253u * (g->mt[i - 1] ^ (g->mt[i - 1] >> 30)) + (uint32_t)i;
+  g->idx = 624;
+}
+
+static void mt_twist(or_mt *g) {
+  for (int i = 0; i < 624; ++i) {
+    const uint32_t y = (g->mt[i] & 0x80000000u) | (g->mt[(i + 1) % 624] & 0x7fffffffu);
+    g->mt[i] = g->mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+  }
+  g->idx = 0;
+}
+
+uint32_t or_mt_next(or_mt *g) {
+  if (g->idx >= 624) mt_twist(g);
+  uint32_t y = g->mt[g->idx++];
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
+/* generate_canonical<float, 24>: one output, (float)x / 2^32, kept below 1 */
+float or_mt_float(or_mt *g) {
+  const float s = (float)or_mt_next(g);
+  float r = s / 4294967296.0f;
+  if (r >= 1.0f) r = nextafterf(1.0f, 0.0f);
+  return r;
+}
+
+/* generate_canonical<double, 53>: two outputs x0 + x1 2^32 summed in double,
+ * over 2^64, kept below 1 */
+double or_mt_double(or_mt *g) {
+  double s = (double)or_mt_next(g);
+  s += (double)or_mt_next(g) * 4294967296.0;
+  double r = s / 18446744073709551616.0;
+  if (r >= 1.0) r = nextafter(1.0, 0.0);
+  return r;
+}
+
+static int g_rng = 0;
+void or_set_rng(int mode) { g_rng = mode; }
+
 /* ------------------------------------------------------------------ */
 /* Model                                                               */
 /* ------------------------------------------------------------------ */
@@ -911,10 +960,11 @@ double or_decision_margin(int reset) {
  * vectors, where discrete_distribution returns the hot index; the oracle
  * takes it directly and consumes no uniform. */
 static int draw(const float *probs, int V, int greedy, uint64_t seed,
-                uint32_t seq, uint32_t cycle, uint32_t slot) {
+                uint32_t seq, uint32_t cycle, uint32_t slot, or_mt *gen) {
   if (greedy) return or_argmax(probs, V);
   double m = 1.0;
-  int v = sample_margin(probs, V, (double)or_uniform(seed, seq, cycle, slot), &m);
+  const double u = g_rng ? or_mt_double(gen) : (double)or_uniform(seed, seq, cycle, slot);
+  int v = sample_margin(probs, V, u, &m);
   if (m < g_margin) g_margin = m;
   return v;
 }
@@ -926,9 +976,32 @@ static int draw(const float *probs, int V, int greedy, uint64_t seed,
  * u_final from max(0, p_r - q_r) normalised by its float sum, or from p_r
  * when that sum is <= 0; after full acceptance *tok is drawn from p_M when
  * has_bonus, else -1.  Returns the number of accepted candidates. */
+static int accept_step_d(const float *p, const float *q, const int32_t *cand, int M,
+                         int V, int greedy, int has_bonus, const float *u_accept,
+                         double u_final, int *tok, int64_t *ties);
+
 int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
                    int V, int greedy, int has_bonus, const float *u_accept,
                    float u_final, int *tok, int64_t *ties) {
+  return accept_step_d(p, q, cand, M, V, greedy, has_bonus, u_accept,
+                       (double)u_final, tok, ties);
+}
+
+/* the number of candidates the accept loop accepts (its decisions only) */
+static int accepted_count(const float *p, const float *q, const int32_t *cand,
+                          int M, int V, int greedy, const float *u_accept) {
+  for (int j = 0; j < M; ++j) {
+    const int c = cand[j];
+    const float *pj = p + (size_t)j * V, *qj = q + (size_t)j * V;
+    const int acc = greedy ? c == or_argmax(pj, V) : u_accept[j] * qj[c] < pj[c];
+    if (!acc) return j;
+  }
+  return M;
+}
+
+static int accept_step_d(const float *p, const float *q, const int32_t *cand, int M,
+                         int V, int greedy, int has_bonus, const float *u_accept,
+                         double u_final, int *tok, int64_t *ties) {
   *tok = -1;
   for (int j = 0; j < M; ++j) {
     int c = cand[j];
@@ -952,10 +1025,10 @@ int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
       sr += rec[v];
     }
     double m = 1.0;
-    if (sr <= 0.0f) *tok = sample_margin(pj, V, (double)u_final, &m);
+    if (sr <= 0.0f) *tok = sample_margin(pj, V, u_final, &m);
     else {
       for (int v = 0; v < V; ++v) rec[v] /= sr;
-      *tok = sample_margin(rec, V, (double)u_final, &m);
+      *tok = sample_margin(rec, V, u_final, &m);
     }
     if (m < g_margin) g_margin = m;
     free(rec);
@@ -966,7 +1039,7 @@ int or_accept_step(const float *p, const float *q, const int32_t *cand, int M,
     if (greedy) *tok = or_argmax(pm, V);
     else {
       double m = 1.0;
-      *tok = sample_margin(pm, V, (double)u_final, &m);
+      *tok = sample_margin(pm, V, u_final, &m);
       if (m < g_margin) g_margin = m;
     }
   }
@@ -1012,7 +1085,9 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
   }
   or_get_probs(tl + (size_t)(P - 1) * V, V, T, top_k, top_p, p);
   g_margin = 1.0;
-  out[n++] = draw(p, V, greedy, seed, seq, 0, 2 * k);
+  or_mt gen;
+  or_mt_seed(&gen, (uint32_t)(seed + seq));
+  out[n++] = draw(p, V, greedy, seed, seq, 0, 2 * k, &gen);
   if (g_trace) g_trace->first_margin = g_margin;
   int ngen = 1;
   uint32_t cycle = 0;
@@ -1037,7 +1112,7 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
       if (tc_i >= 0)
         memcpy(tr->dlogits + ((size_t)tc_i * k + j) * V, dl, sizeof(float) * V);
       or_get_probs(dl, V, T, top_k, top_p, q + (size_t)j * V);
-      cand[j] = draw(q + (size_t)j * V, V, greedy, seed, seq, cycle, j);
+      cand[j] = draw(q + (size_t)j * V, V, greedy, seed, seq, cycle, j, &gen);
       if (tc_i >= 0) tr->cand[(size_t)tc_i * k + j] = cand[j];
     }
     /* verify (layer.cpp:1560-1579) */
@@ -1049,12 +1124,27 @@ int or_generate_speculative(const or_model *t, const or_model *dm,
       or_get_probs(tl + (size_t)i * V, V, T, top_k, top_p, p + (size_t)i * V);
     /* accept, resample or bonus (layer.cpp:1581-1630, 1643-1647) */
     float ua[64];
-    for (int j = 0; j < M; ++j) ua[j] = greedy ? 0.0f : or_uniform(seed, seq, cycle, k + j);
-    float uf = greedy ? 0.0f : or_uniform(seed, seq, cycle, 2 * k);
+    double uf = 0.0;
+    const int has_bonus = ngen + M < max_new;
+    if (greedy) {
+      for (int j = 0; j < M; ++j) ua[j] = 0.0f;
+    } else if (g_rng) {
+      /* the reference draws r_j only for the tests it makes (up to the
+       * first rejection), then the resample or bonus: the tests' uniforms
+       * from a copy of the stream, the stream then advanced past the ones
+       * used */
+      or_mt look = gen;
+      for (int j = 0; j < M; ++j) ua[j] = or_mt_float(&look);
+      const int a = accepted_count(p, q, cand, M, V, 0, ua);
+      for (int j = 0; j < (a < M ? a + 1 : M); ++j) (void)or_mt_next(&gen);
+      if (a < M || has_bonus) uf = or_mt_double(&gen);
+    } else {
+      for (int j = 0; j < M; ++j) ua[j] = or_uniform(seed, seq, cycle, k + j);
+      uf = (double)or_uniform(seed, seq, cycle, 2 * k);
+    }
     int tok = -1;
     int64_t ties = 0;
-    int acc = or_accept_step(p, q, cand, M, V, greedy, ngen + M < max_new, ua,
-                             uf, &tok, &ties);
+    int acc = accept_step_d(p, q, cand, M, V, greedy, has_bonus, ua, uf, &tok, &ties);
     for (int j = 0; j < acc; ++j) out[n++] = cand[j];
     if (tc_i >= 0) {
       tr->acc[tc_i] = acc; tr->tok[tc_i] = tok; tr->margin[tc_i] = g_margin;
@@ -1088,7 +1178,8 @@ done:
 }
 
 /* generate_advanced (layer.cpp:1240-1380) for one sequence.  Sampled mode
- * draws u[seq][step][0]; greedy takes the first argmax. */
+ * draws u[seq][step][0] (or, with or_set_rng(1), the next double of the
+ * sequence's std::mt19937 stream); greedy takes the first argmax. */
 int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
                          int max_new, float T, int top_k, float top_p,
                          uint64_t seed, uint32_t seq, int use_cache,
@@ -1101,6 +1192,8 @@ int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
   float *lg = (float *)malloc(sizeof(float) * (size_t)total * V);
   float *pr = (float *)malloc(sizeof(float) * V);
   int rc = 0;
+  or_mt gen;
+  or_mt_seed(&gen, (uint32_t)(seed + seq));
   for (int step = 0; step < max_new; ++step) {
     int S;
     const int32_t *in;
@@ -1117,7 +1210,8 @@ int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
     if (T <= 0.0f) tok = or_argmax(last, V);
     else {
       or_get_probs(last, V, T, top_k, top_p, pr);
-      tok = or_sample(pr, V, (double)or_uniform(seed, seq, (uint32_t)step, 0));
+      tok = or_sample(pr, V, g_rng ? or_mt_double(&gen)
+                                   : (double)or_uniform(seed, seq, (uint32_t)step, 0));
     }
     out[n++] = tok;
   }

@@ -50,6 +50,28 @@ void or_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2],
 /* u[seq][cycle][slot] in [0,1): the top 24 bits of word 0, times 2^-24. */
 float or_uniform(uint64_t seed, uint32_t seq, uint32_t cycle, uint32_t slot);
 
+/* std::mt19937 (Matsumoto & Nishimura 1998, the parameters of C++
+ * [rand.predef]) and the two draws generate_speculative and
+ * generate_advanced take from it (layer.cpp:1249, 1394, 1493-1498,
+ * 1596-1597) as libstdc++ forms them: uniform_real_distribution<float>(0, 1)
+ * = generate_canonical<float, 24> (one output), and discrete_distribution's
+ * generate_canonical<double, 53> (two outputs). */
+typedef struct {
+  uint32_t mt[624];
+  int idx;
+} or_mt;
+void or_mt_seed(or_mt *g, uint32_t seed);
+uint32_t or_mt_next(or_mt *g);
+float or_mt_float(or_mt *g);
+double or_mt_double(or_mt *g);
+/* Uniform source of or_generate_speculative / or_generate_advanced:
+ * 0 = Philox slots u[seq][cycle][slot] (the default), 1 = the reference's
+ * sequential std::mt19937 stream seeded with (uint32)(seed + seq), draws in
+ * the reference's order (first token, each draft sample, each accept test
+ * up to the first rejection, the resample or bonus).  Greedy runs draw
+ * nothing (every distribution they sample is one-hot). */
+void or_set_rng(int mode);
+
 /* Model: TransformerDecoder(vocab, d, heads, d_ff, layers, max_seq_len). */
 or_model *or_model_create(int vocab, int d_model, int n_heads, int d_ff,
                           int n_layers, int max_seq_len);

@@ -104,6 +104,16 @@ def lib():
                                               C.POINTER(SpecStats)]
         L.or_set_spec_trace.argtypes = [C.POINTER(SpecTrace)]
         L.or_set_threads.argtypes = [i32]
+        L.or_set_rng.argtypes = [i32]
+        L.or_set_rng.restype = None
+        L.or_mt_seed.argtypes = [C.c_void_p, u32]
+        L.or_mt_seed.restype = None
+        L.or_mt_next.argtypes = [C.c_void_p]
+        L.or_mt_next.restype = u32
+        L.or_mt_float.argtypes = [C.c_void_p]
+        L.or_mt_float.restype = f32
+        L.or_mt_double.argtypes = [C.c_void_p]
+        L.or_mt_double.restype = C.c_double
         L.or_decision_margin.argtypes = [i32]
         L.or_decision_margin.restype = C.c_double
         L.or_generate_advanced.argtypes = [vp, ip, i32, i32, f32, i32, f32,
@@ -324,6 +334,30 @@ def generate_speculative(target, draft, prompt, max_new, k, T, seed, seq=0,
     if rc != 0:
         raise RuntimeError(f"or_generate_speculative failed: {rc}")
     return out, st
+
+
+class MT19937:
+    """The oracle's std::mt19937 (or_mt): next() raw outputs, f() the
+    uniform_real_distribution<float>(0, 1) draw, d() the
+    generate_canonical<double, 53> draw."""
+
+    def __init__(self, seed):
+        self._buf = C.create_string_buffer(624 * 4 + 8)
+        lib().or_mt_seed(self._buf, seed & 0xffffffff)
+
+    def next(self):
+        return int(lib().or_mt_next(self._buf))
+
+    def f(self):
+        return float(lib().or_mt_float(self._buf))
+
+    def d(self):
+        return float(lib().or_mt_double(self._buf))
+
+
+def set_rng(mode):
+    """0: Philox slots; 1: the reference's std::mt19937 stream (or_set_rng)."""
+    lib().or_set_rng(int(mode))
 
 
 def set_threads(n):
