@@ -56,6 +56,12 @@ const char *nnhip_last_error(void);
 int nnhip_init(int device, nnhip_ctx **out);
 int nnhip_destroy(nnhip_ctx *ctx);
 /* "graphs": 1 = replay each speculative cycle as one HIP graph (default).
+ * "rng": uniforms of nnhip_generate_speculative(_batch) and
+ * nnhip_generate_advanced(_batch) on this context: 0 = the Philox stream
+ * (default), 1 = the reference's std::mt19937 (layer.cpp:1249, 1394), one
+ * engine per sequence seeded (uint32_t)(seed + seq0 + b) -- for one
+ * sequence exactly std::mt19937 gen(seed) -- drawn in the reference's
+ * order with libstdc++'s float and double draws.
  * "gemm_wide": 1 = the int8 MFMA GEMM may use 32x64 tiles on large grids
  * (default: the prompt prefill's 8192-row down projection), 0 = always
  * 32x32 tiles (process-wide).
@@ -182,8 +188,9 @@ int nnhip_kvcache_truncate(nnhip_kvcache *c, int b, int len);
  * (layer.hpp:318-323, layer.cpp:1382-1661).  out [P + max(max_new, 1)]
  * (host) receives the prompt and the generated ids.  Uniforms come from the
  * Philox stream u[seq][cycle][slot] (slot j < k: draft sample j, k + j:
- * accept test j, 2k: resample or bonus; cycle 0 slot 2k: first token)
- * instead of std::mt19937.  temperature <= 0 is greedy.  top_k / top_p
+ * accept test j, 2k: resample or bonus; cycle 0 slot 2k: first token), or
+ * with the context option "rng" 1 from std::mt19937 as the reference draws
+ * them.  temperature <= 0 is greedy.  top_k / top_p
  * filter every get_probs as nnhip_sample_rows describes.  quantized_cache
  * != 0 gives both models int8 KV caches (KVCache(true), layer.cpp:
  * 1396-1398).  A vocabulary above 32768 returns NNHIP_EUNSUPPORTED. */
@@ -197,7 +204,8 @@ int nnhip_generate_speculative(nnhip_model *target, nnhip_model *draft,
  * reference is batch-1; this runs B of its loops in lockstep on one GPU
  * with per-sequence cache lengths).  prompts [B][P], out
  * [B][P + max(max_new, 1)], stats [B] (or NULL), timing (or NULL).
- * Sequence b uses Philox sequence index seq0 + b. */
+ * Sequence b uses Philox sequence index seq0 + b (or the mt19937 engine
+ * seeded seed + seq0 + b). */
 int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
                                      int B, const int32_t *prompts, int P,
                                      int max_new, int lookahead,
@@ -208,7 +216,8 @@ int nnhip_generate_speculative_batch(nnhip_model *target, nnhip_model *draft,
                                      nnhip_spec_timing *timing);
 /* TransformerDecoder::generate_advanced(prompt, max_new_tokens, temperature,
  * top_k, top_p, seed, use_kv_cache) (layer.hpp:310-316, layer.cpp:
- * 1240-1380); sampled mode draws u[seq][step][0]. */
+ * 1240-1380); sampled mode draws u[seq][step][0] (or, with "rng" 1, the
+ * next double of the sequence's std::mt19937). */
 int nnhip_generate_advanced(nnhip_model *m, const int32_t *prompt, int P,
                             int max_new, float temperature, int top_k,
                             float top_p, uint64_t seed, int use_kv_cache,

@@ -60,7 +60,18 @@ HipBuffer::HipBuffer(nnhip_ctx *ctx, size_t bytes) : ctx_(ctx), bytes_(bytes) {
 
 HipBuffer::~HipBuffer() { (void)nnhip_free(ctx_, ptr_); }
 
-HipBackend::HipBackend(int device) { check(nnhip_init(device, &ctx_)); }
+HipBackend::HipBackend(int device) {
+  check(nnhip_init(device, &ctx_));
+  // the decoder objects' sampled generation draws from std::mt19937 seeded
+  // with the caller's seed, as TransformerDecoder's does (layer.cpp:1249,
+  // 1394)
+  try {
+    check(nnhip_set_option(ctx_, "rng", 1));
+  } catch (...) {
+    (void)nnhip_destroy(ctx_);
+    throw;
+  }
+}
 
 HipBackend::~HipBackend() { (void)nnhip_destroy(ctx_); }
 

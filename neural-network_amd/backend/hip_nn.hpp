@@ -19,8 +19,9 @@
 //   generate_advanced (layer.hpp:310-316)        HipDecoder::generate_advanced
 //   generate_speculative (layer.hpp:318-323)     HipDecoder::generate_speculative
 //
-// Sampled generation draws from a counter-based Philox stream keyed by the
-// seed instead of std::mt19937 (greedy output is the reference's).
+// Sampled generation draws from std::mt19937 seeded with the seed, in the
+// reference's order and with libstdc++'s draws (HipBackend sets the
+// library's "rng" option to 1 on its context).
 #pragma once
 
 #include "hip_backend.hpp"

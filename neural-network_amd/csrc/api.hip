@@ -70,6 +70,10 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
   return guard([&] {
     REQ(ctx && key, "nnhip_set_option: NULL argument");
     if (std::strcmp(key, "graphs") == 0) ctx->c.use_graphs = value != 0;
+    else if (std::strcmp(key, "rng") == 0) {
+      REQ(value == 0 || value == 1, "rng must be 0 (Philox) or 1 (mt19937)");
+      ctx->c.rng = value;
+    }
     else if (std::strcmp(key, "gemm_wide") == 0) nnhip::g_gemm_wide = value;
     else if (std::strcmp(key, "gemv16") == 0) nnhip::g_gemv16 = value != 0;
     else if (std::strcmp(key, "accept_early") == 0) nnhip::g_accept_early = value != 0;

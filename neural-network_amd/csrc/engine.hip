@@ -707,7 +707,21 @@ struct SpecBuffers {
   DevBuf<int64_t> stats;
   DevBuf<int32_t> rec;    // the split accept step's records and chunk sums
   DevBuf<double> chunks;
+  DevBuf<uint32_t> mt, mt_ring, mt_rw;   // mt19937 streams (SpecState::mt)
 };
+
+// The mt19937 streams of B sequences when the context asks for them and
+// the loop samples (greedy decoding draws nothing), seeded on the stream.
+void attach_mt(Ctx *ctx, hipStream_t st, int B, float T, SpecState &s,
+               DevBuf<uint32_t> &mt, DevBuf<uint32_t> &ring,
+               DevBuf<uint32_t> &rw) {
+  if (ctx->rng != 1 || T <= 0.f) return;
+  mt.alloc((size_t)B * kMtN);
+  ring.alloc((size_t)B * kMtRing);
+  rw.alloc((size_t)B * 2);
+  s.mt = mt.p; s.mt_ring = ring.p; s.mt_rw = rw.p;
+  launch_mt_seed(st, s);
+}
 
 void check_sampling_options(int V, int top_k, float top_p) {
   NNHIP_REQUIRE(V > 0 && V <= 32768, kErrUnsupported,
@@ -810,6 +824,7 @@ void generate_speculative_batch(Model &t, Model &dm, int B,
   s.B = B; s.out_stride = out_stride; s.P = P; s.max_new = max_new;
   s.k = k; s.V = V; s.T = T; s.seed = seed; s.seq0 = seq0;
   s.top_k = top_k; s.top_p = top_p;
+  attach_mt(ctx, st, B, T, s, bf.mt, bf.mt_ring, bf.mt_rw);
   // workspace for every shape the loop uses, before any graph capture
   t.reserve(B * P, B * (k + 1), t_need);
   t.reserve(B * (k + 1), B * (k + 1), t_need);
@@ -986,6 +1001,8 @@ void generate_advanced_batch(Model &m, int B, const int32_t *prompts, int P,
   s.cur = cur.p; s.out = dout.p; s.B = B; s.out_stride = total; s.P = P;
   s.max_new = max_new; s.k = 0; s.V = m.V; s.T = T; s.seed = seed;
   s.seq0 = seq0; s.top_k = top_k; s.top_p = top_p;
+  DevBuf<uint32_t> mt, mt_ring, mt_rw;
+  attach_mt(m.ctx, st, B, T, s, mt, mt_ring, mt_rw);
   std::unique_ptr<KVCache> cache;
   if (use_cache) cache.reset(new KVCache(&m, B, std::max(total, 1)));
   for (int step = 0; step < max_new; ++step) {

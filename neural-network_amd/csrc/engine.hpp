@@ -17,6 +17,9 @@ struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   bool use_graphs = true;
+  // uniforms of the generate loops: 0 the Philox counter stream, 1 the
+  // reference's std::mt19937 per sequence (SpecState::mt)
+  int rng = 0;
 };
 
 // One Dense on the device, weight transposed to [N][K].  Fused layouts:

@@ -527,6 +527,12 @@ constexpr int kAcceptRec = 8;
 constexpr int kDrawChunks = 16;
 // largest lookahead k of the speculative loop
 constexpr int kMaxLookahead = 63;
+// std::mt19937 streams (SpecState::mt): words of the engine's state, outputs
+// a sequence's ring holds, and the fewest unread outputs a launch leaves
+// before it appends the next 624 (a cycle reads at most 3k + 2 <= 191)
+constexpr int kMtN = 624;
+constexpr int kMtRing = 1024;
+constexpr int kMtLow = kMtRing - kMtN;
 // whether get_probs filters with these options (layer.cpp:1452-1472)
 inline bool sampling_filtered(int V, int top_k, float top_p) {
   return (top_k > 0 && top_k < V) || (top_p > 0.0f && top_p < 1.0f);
@@ -603,10 +609,23 @@ struct SpecState {
   // [B][kDrawChunks][2] chunk sums (null: one accept_kernel per sequence)
   int32_t *rec = nullptr;
   double *chunks = nullptr;
+  // The reference's generator (layer.cpp:1249, 1394: one std::mt19937 per
+  // call, seeded with the seed; here sequence b's engine is seeded with
+  // seed + seq0 + b): per sequence the engine's state [B][kMtN], a ring of
+  // its tempered outputs [B][kMtRing] and the {read, write} counters
+  // [B][2].  A cycle's launches read ahead of the read counter in the
+  // reference's order -- the M drafting draws (two outputs each), the
+  // accept tests up to the first rejection (one each), then the resample or
+  // bonus draw (two) -- and the accept step advances it by what was used.
+  // Null: the Philox stream (uniform()).
+  uint32_t *mt = nullptr, *mt_ring = nullptr, *mt_rw = nullptr;
   // when nd is set, drafting steps j < k - 1 embed their token as row b of
   // the next draft forward
   NextRows nd;
 };
+// seeds SpecState::mt of every sequence and fills its ring with the first
+// 624 outputs (read counter 0)
+void launch_mt_seed(hipStream_t st, const SpecState &s);
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl);
 void launch_draft_sample(hipStream_t st, const SpecState &s, int j,

@@ -9,7 +9,9 @@
 // the logits is on-chip.  No host round trip happens per token.
 //
 // Uniforms: Philox4x32-10 keyed by the seed, counter {slot, cycle, seq, 0},
-// u = (word0 >> 8) * 2^-24 -- the stream the oracle uses.
+// u = (word0 >> 8) * 2^-24 (the oracle's default stream), or with
+// SpecState::mt set the reference's own std::mt19937 per sequence, drawn in
+// the reference's order (mt_seed_kernel, mt_commit).
 #include "nnhip_internal.hpp"
 #include "rows.hpp"
 
@@ -50,6 +52,130 @@ __device__ __forceinline__ float uniform(uint64_t seed, uint32_t seq,
     k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
   }
   return (float)(c0 >> 8) * (1.0f / 16777216.0f);
+}
+
+// ---------------------------------------------------------------------------
+// std::mt19937 (SpecState::mt), the generator generate_advanced and
+// generate_speculative draw from (layer.cpp:1249, 1394).  The engine is the
+// standard's: 624-word state, seeding x_i = 1812433253 (x_{i-1} ^
+// (x_{i-1} >> 30)) + i, twist, tempering.  Its outputs are produced 624 at a
+// time by a whole workgroup into a per-sequence ring; the draws are
+// libstdc++'s generate_canonical: a float from one output ((float)g / 2^32),
+// a double from two ((g1 + g2 2^32) / 2^64), each the largest value below 1
+// when rounding reaches 1.
+// ---------------------------------------------------------------------------
+constexpr int kMtM = 397;
+constexpr int kMtD = kMtN - kMtM;   // 227
+
+__device__ __forceinline__ uint32_t mt_mix(uint32_t cur, uint32_t nxt) {
+  const uint32_t y = (cur & 0x80000000u) | (nxt & 0x7fffffffu);
+  return (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+}
+
+__device__ __forceinline__ uint32_t mt_temper(uint32_t y) {
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  return y ^ (y >> 18);
+}
+
+// One twist of a sequence's state mt (global) and its 624 tempered outputs
+// written to ring slots wp .. wp + 623 (mod kMtRing), by a workgroup of at
+// least kMtN threads; every thread calls it.  New word i is old[i + 397] ^
+// mix(old[i], old[i + 1]) for i < 227 and new[i - 227] ^ mix(old[i],
+// old[i + 1]) after (new[0] in place of old[624]), so three phases separated
+// by barriers give the sequential recurrence's words.
+__device__ void mt_twist(uint32_t *mt, uint32_t *ring, uint32_t wp) {
+  const int i = threadIdx.x;
+  const bool on = i < kMtN;
+  const uint32_t cur = on ? mt[i] : 0u;
+  const uint32_t nxt = (on && i + 1 < kMtN) ? mt[i + 1] : 0u;
+  const uint32_t far = i < kMtD ? mt[i + kMtM] : 0u;
+  __syncthreads();   // every old word read
+  uint32_t v = 0u;
+  if (i < kMtD) {
+    v = far ^ mt_mix(cur, nxt);
+    mt[i] = v;
+  }
+  __syncthreads();
+  if (i >= kMtD && i < 2 * kMtD) {
+    v = mt[i - kMtD] ^ mt_mix(cur, nxt);
+    mt[i] = v;
+  }
+  __syncthreads();
+  if (i >= 2 * kMtD && on) {
+    v = mt[i - kMtD] ^ mt_mix(cur, i + 1 < kMtN ? nxt : mt[0]);
+    mt[i] = v;
+  }
+  if (on) ring[(wp + (uint32_t)i) & (kMtRing - 1)] = mt_temper(v);
+  __syncthreads();   // the ring's new outputs visible to the workgroup
+}
+
+__device__ __forceinline__ uint32_t mt_out(const SpecState &s, int b, uint32_t p) {
+  return s.mt_ring[(int64_t)b * kMtRing + (p & (kMtRing - 1))];
+}
+__device__ __forceinline__ double mt_double_at(const SpecState &s, int b, uint32_t p) {
+  double x = (double)mt_out(s, b, p);
+  x += (double)mt_out(s, b, p + 1) * 4294967296.0;
+  const double r = x * 0x1p-64;
+  return r >= 1.0 ? 0x1.fffffffffffffp-1 : r;
+}
+__device__ __forceinline__ float mt_float_at(const SpecState &s, int b, uint32_t p) {
+  const float r = (float)mt_out(s, b, p) * 0x1p-32f;
+  return r >= 1.0f ? 0x1.fffffep-1f : r;
+}
+
+// The uniform of sequence b's sampled draw: with the mt19937 stream the
+// double `off` outputs past the read counter, else the Philox uniform of
+// (cycle, slot).  test_u: the same for an accept test's float.
+__device__ __forceinline__ double draw_u(const SpecState &s, int b, uint32_t off,
+                                         uint32_t cyc, uint32_t slot) {
+  if (s.mt_ring) return mt_double_at(s, b, s.mt_rw[2 * b] + off);
+  return (double)uniform(s.seed, s.seq0 + b, cyc, slot);
+}
+__device__ __forceinline__ float test_u(const SpecState &s, int b, uint32_t off,
+                                        uint32_t cyc, uint32_t slot) {
+  if (s.mt_ring) return mt_float_at(s, b, s.mt_rw[2 * b] + off);
+  return uniform(s.seed, s.seq0 + b, cyc, slot);
+}
+
+// After a launch's draws for sequence b (block-uniform call, every thread):
+// the read counter advanced by `used` outputs, and when fewer than kMtLow
+// remain unread the next 624 appended.  Each thread has read the counters
+// before the barrier; the ring slots rewritten lie outside the unread ones.
+__device__ void mt_commit(const SpecState &s, int b, uint32_t used) {
+  uint32_t *rw = s.mt_rw + 2 * b;
+  const uint32_t rp = rw[0] + used, wp = rw[1];
+  __syncthreads();
+  const bool fill = wp - rp < (uint32_t)kMtLow;
+  if (fill)
+    mt_twist(s.mt + (int64_t)b * kMtN, s.mt_ring + (int64_t)b * kMtRing, wp);
+  if (threadIdx.x == 0) {
+    rw[0] = rp;
+    if (fill) rw[1] = wp + kMtN;
+  }
+}
+
+// Seeds sequence b's engine with (uint32_t)(seed + seq0 + b) -- the
+// reference's seed is an unsigned int, and the engine keeps the value mod
+// 2^32 -- and fills the ring with its first 624 outputs.
+__global__ __launch_bounds__(1024) void mt_seed_kernel(SpecState s) {
+  const int b = blockIdx.x;
+  uint32_t *mt = s.mt + (int64_t)b * kMtN;
+  if (threadIdx.x == 0) {
+    uint32_t x = (uint32_t)(s.seed + s.seq0 + (uint64_t)b);
+    mt[0] = x;
+    for (int i = 1; i < kMtN; ++i) {
+      x = 1812433253u * (x ^ (x >> 30)) + (uint32_t)i;
+      mt[i] = x;
+    }
+  }
+  __syncthreads();
+  mt_twist(mt, s.mt_ring + (int64_t)b * kMtRing, 0u);
+  if (threadIdx.x == 0) {
+    s.mt_rw[2 * b] = 0u;
+    s.mt_rw[2 * b + 1] = kMtN;
+  }
 }
 
 // Row statistics of get_probs (T > 0), see row_pass; tau / tix: the top-k /
@@ -434,7 +560,7 @@ __device__ __forceinline__ void fill_probs(const float *__restrict__ row,
 // entry 1.0): the first v whose running sum of p reaches u * S.  Each thread
 // owns a contiguous chunk; a chunk is scanned only when the crossing can lie
 // in it or before it.
-__device__ __forceinline__ int block_sample(int V, float u, Shared &sh) {
+__device__ __forceinline__ int block_sample(int V, double u, Shared &sh) {
   // the thread's chunk [b0, b0 + C) (C <= kPer), read from LDS once
   const int C = (V + kThreads - 1) / kThreads;
   const int b0 = threadIdx.x * C;
@@ -447,7 +573,7 @@ __device__ __forceinline__ int block_sample(int V, float u, Shared &sh) {
   for (int i = 0; i < kPer; ++i) loc += (double)pv[i];
   double S;
   double c = block_excl_scan_d(loc, sh, &S);
-  const double target = (double)u * S;
+  const double target = u * S;
   int found = 0x7fffffff;
   if (c + loc >= target - 1e-12 * S) {
 #pragma unroll
@@ -462,7 +588,7 @@ __device__ __forceinline__ int block_sample(int V, float u, Shared &sh) {
 }
 
 template <bool FILT>
-__device__ __forceinline__ int draw_row(const float *row, int V, float T, float u,
+__device__ __forceinline__ int draw_row(const float *row, int V, float T, double u,
                         Shared &sh, int top_k = 0, float top_p = 1.f) {
   if (T <= 0.f) return block_argmax(row, V, sh);
   row_probs<FILT>(row, V, T, sh, nullptr, top_k, top_p);
@@ -533,7 +659,7 @@ template <class SH>
 __device__ __forceinline__ int tiles_sample(const float *__restrict__ row,
                                             const float2 *__restrict__ tl,
                                             int nt, int tw, int V, float T,
-                                            RowStats st, float u, SH &sh) {
+                                            RowStats st, double u, SH &sh) {
   const int t = threadIdx.x;
   double P = 0.0;
   if (t < nt) {
@@ -543,7 +669,7 @@ __device__ __forceinline__ int tiles_sample(const float *__restrict__ row,
   }
   double S;
   const double c = block_excl_scan_d(P, sh, &S);
-  const double target = (double)u * S;
+  const double target = u * S;
   int ts = block_min_i(t < nt && P > 0.0 && c + P >= target ? t : 0x7fffffff, sh);
   if (ts == 0x7fffffff) return V - 1;
   // running sum before tile ts, broadcast
@@ -625,7 +751,7 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
     }
     __syncthreads();
     const int tok = tiles_sample(row, tl, s.nt, s.tw, s.V, s.T, rst,
-                                 uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+                                 draw_u(s, b, 2 * j, s.cyc[b], j), sh);
     if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
     embed_next(s, b, j, tok, s_emb, s_red);
     return;
@@ -651,7 +777,7 @@ __global__ __launch_bounds__(kThreads) void draft_sample_tiles_kernel(
   }
   if (part != 0) return;
   const int tok = tiles_sample(row, tl, s.nt, s.tw, s.V, s.T, st,
-                               uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+                               draw_u(s, b, 2 * j, s.cyc[b], j), sh);
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
   embed_next(s, b, j, tok, s_emb, s_red);
 }
@@ -719,15 +845,18 @@ __global__ __launch_bounds__(kTileThreads) void row_tile_stats_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// First token after the prefill (layer.cpp:1500-1510): cycle 0, slot 2k.
+// First token after the prefill (layer.cpp:1500-1510): Philox cycle 0, slot
+// 2k, or the mt19937 stream's first double.
 // ---------------------------------------------------------------------------
 template <bool FILT>
 __global__ __launch_bounds__(kThreads) void first_token_kernel(
     SpecState s, const float *__restrict__ logits, int64_t ldl) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
-  const float u = uniform(s.seed, s.seq0 + b, 0, 2 * s.k);
+  const double u = draw_u(s, b, 0, 0, 2 * s.k);
   const int tok = draw_row<FILT>(logits + b * ldl, s.V, s.T, u, sh, s.top_k, s.top_p);
+  // the draw used one double of the mt19937 stream
+  if (s.mt_ring && s.T > 0.f) mt_commit(s, b, 2);
   if (threadIdx.x == 0) {
     int32_t *out = s.out + (int64_t)b * s.out_stride;
     out[s.P] = tok;
@@ -750,7 +879,9 @@ __global__ __launch_bounds__(kThreads) void first_token_kernel(
 }
 
 // One drafting step j (layer.cpp:1541-1558): q_j = get_probs(draft logits),
-// candidate = sample_token(q_j) with u[seq][cycle][j].
+// candidate = sample_token(q_j) with u[seq][cycle][j] (Philox) or the
+// double 2j outputs past the read counter (mt19937: step j's draw follows
+// the j earlier ones of the cycle; steps j >= M draw but are not used).
 template <bool FILT>
 __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
     SpecState s, int j, const float *__restrict__ logits, int64_t ldl) {
@@ -764,7 +895,7 @@ __global__ __launch_bounds__(kThreads) void draft_sample_kernel(
   } else {
     row_probs<FILT>(row, s.V, s.T, sh, s.qprob + ((int64_t)b * s.k + j) * s.V,
                     s.top_k, s.top_p);
-    tok = block_sample(s.V, uniform(s.seed, s.seq0 + b, s.cyc[b], j), sh);
+    tok = block_sample(s.V, draw_u(s, b, 2 * j, s.cyc[b], j), sh);
   }
   if (threadIdx.x == 0) s.cand[b * s.k + j] = tok;
   // the probability row is no longer needed: its LDS holds the embedded row
@@ -816,7 +947,7 @@ __global__ __launch_bounds__(kThreads, FILT ? 1 : 8) void target_stats_kernel(
 // drafting step would have written
 __device__ __forceinline__ int residual_sample(
     const float *__restrict__ qrow, const float *__restrict__ tlog_row,
-    RowStats tst, int V, float T, float u, Shared &sh,
+    RowStats tst, int V, float T, double u, Shared &sh,
     const float *__restrict__ qlrow = nullptr, RowStats qs = RowStats{}) {
   // two halves of the thread's entries, each with its loads in flight
   constexpr int kHalf = kPer / 2;
@@ -1004,8 +1135,9 @@ __global__ __launch_bounds__(kStatThreads, 8) void accept_tiles_kernel(
       const int c = min(max(s.cand[b * s.k + j], 0), V - 1);
       const float pc = prob_of(trow[c], c, s.T, st);
       const float qc = (expf(scaled(drow[c], s.T) - qs.mx) * qs.rsum) * qs.rfs;
+      const int M = min(s.k, s.max_new - s.gen[b]);
       const float u = s.ua ? s.ua[(int64_t)b * s.k + j]
-                           : uniform(s.seed, s.seq0 + b, (uint32_t)s.cyc[b], s.k + j);
+                           : test_u(s, b, 2 * M + j, (uint32_t)s.cyc[b], s.k + j);
       if (u * qc >= pc * (1.0f + 1e-5f)) atomicMin(s.minrej + b, j);
     }
   }
@@ -1023,7 +1155,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   const bool greedy = s.T <= 0.f;
   const int gen0 = s.gen[b];
   const int M = min(k, s.max_new - gen0);
-  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const uint32_t cyc = (uint32_t)s.cyc[b];
   const int tstart = s.tlen[b], dstart = s.dlen[b];
   const int tr = verify_rows(s);
   int32_t *out = s.out + (int64_t)b * s.out_stride;
@@ -1085,7 +1217,7 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     if (greedy) return c == argmax_of(j);
     const RowStats st = stats_of(j);
     const float pc = prob_of(lj, c, s.T, st);
-    const float r = s.ua ? s.ua[(int64_t)b * k + j] : uniform(s.seed, seq, cyc, k + j);
+    const float r = s.ua ? s.ua[(int64_t)b * k + j] : test_u(s, b, 2 * M + j, cyc, k + j);
     if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
     return __fmul_rn(r, qc) < pc;
   };
@@ -1110,7 +1242,9 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
   }
   int gen = gen0 + (rej < 0 ? M : rej);
   int tok = -1, catch_tok = -1;
-  const float u = s.ur ? s.ur[b] : uniform(s.seed, seq, cyc, 2 * k);
+  // the resample / bonus draw follows the tests up to the first rejection
+  const double u = s.ur ? (double)s.ur[b]
+                        : draw_u(s, b, 2 * M + (rej >= 0 ? rej + 1 : M), cyc, 2 * k);
   if (rej >= 0) {
     const float *row = tlogits + ((int64_t)b * tr + rej) * V;
     if (greedy) {
@@ -1174,20 +1308,27 @@ __global__ __launch_bounds__(kThreads) void accept_kernel(
     if (s.n_far && s.max_new - gen0 > k + 1 && s.max_new - gen <= k + 1)
       atomicSub(s.n_far, 1);
   }
+  // the mt19937 outputs of the cycle: M drafting draws, the tests up to the
+  // first rejection, the resample or bonus draw
+  if (s.mt_ring && !greedy)
+    mt_commit(s, b, 2 * M + (rej >= 0 ? rej + 1 : M) + (tok >= 0 ? 2 : 0));
 }
 
-// generate_advanced sampling step (layer.cpp:1294-1373): u[seq][step][0].
+// generate_advanced sampling step (layer.cpp:1294-1373): u[seq][step][0]
+// (Philox) or the mt19937 stream's next double.
 template <bool FILT>
 __global__ __launch_bounds__(kThreads) void ar_sample_kernel(
     SpecState s, int step, const float *__restrict__ logits, int64_t ldl) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
-  const float u = uniform(s.seed, s.seq0 + b, (uint32_t)step, 0);
+  const double u = draw_u(s, b, 0, (uint32_t)step, 0);
   const int tok = draw_row<FILT>(logits + b * ldl, s.V, s.T, u, sh, s.top_k, s.top_p);
   if (threadIdx.x == 0) {
     s.out[(int64_t)b * s.out_stride + s.P + step] = tok;
     s.cur[b] = tok;
   }
+  // one double of the mt19937 stream per sampled token
+  if (s.mt_ring && s.T > 0.f) mt_commit(s, b, 2);
 }
 
 // State of the accept step run on given rows (AcceptRows): every sequence
@@ -1222,7 +1363,7 @@ __global__ __launch_bounds__(kThreads) void accept_decide_kernel(
   const bool greedy = s.T <= 0.f;
   const int gen0 = s.gen[b];
   const int M = min(k, s.max_new - gen0);
-  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const uint32_t cyc = (uint32_t)s.cyc[b];
   const int tr = verify_rows(s);
   int32_t *out = s.out + (int64_t)b * s.out_stride;
   int nout = s.P + gen0;
@@ -1283,7 +1424,7 @@ __global__ __launch_bounds__(kThreads) void accept_decide_kernel(
     if (greedy) return c == argmax_of(j);
     const RowStats st = stats_of(j);
     const float pc = prob_of(lj, c, s.T, st);
-    const float r = s.ua ? s.ua[(int64_t)b * k + j] : uniform(s.seed, seq, cyc, k + j);
+    const float r = s.ua ? s.ua[(int64_t)b * k + j] : test_u(s, b, 2 * M + j, cyc, k + j);
     if (fabs((double)r - (double)pc / (double)qc) < 1e-6) ++ties;
     return __fmul_rn(r, qc) < pc;
   };
@@ -1432,7 +1573,7 @@ __global__ __launch_bounds__(kThreads) void accept_final_kernel(
   const int V = s.V, k = s.k;
   const int gen0 = s.gen[b];
   const int M = min(k, s.max_new - gen0);
-  const uint32_t seq = s.seq0 + b, cyc = (uint32_t)s.cyc[b];
+  const uint32_t cyc = (uint32_t)s.cyc[b];
   const int tstart = s.tlen[b], dstart = s.dlen[b];
   const int rej = rec[1];
   int32_t *out = s.out + (int64_t)b * s.out_stride;
@@ -1440,7 +1581,8 @@ __global__ __launch_bounds__(kThreads) void accept_final_kernel(
   int gen = gen0 + (rej < 0 ? M : rej);
   int tok = rec[3], catch_tok = -1;
   if (kind > 0) {
-    const float u = s.ur ? s.ur[b] : uniform(s.seed, seq, cyc, 2 * k);
+    const double u = s.ur ? (double)s.ur[b]
+                          : draw_u(s, b, 2 * M + (rej >= 0 ? rej + 1 : M), cyc, 2 * k);
     // the draw's weights: the residual, or p where the residual is all zero
     // (residual_sample) and for the bonus row
     const double *ch = s.chunks + (int64_t)b * kDrawChunks * 2;
@@ -1540,6 +1682,9 @@ __global__ __launch_bounds__(kThreads) void accept_final_kernel(
     if (s.n_far && s.max_new - gen0 > k + 1 && s.max_new - gen <= k + 1)
       atomicSub(s.n_far, 1);
   }
+  // the mt19937 outputs of the cycle (accept_kernel)
+  if (s.mt_ring && s.T > 0.f)
+    mt_commit(s, b, 2 * M + (rej >= 0 ? rej + 1 : M) + (kind > 0 ? 2 : 0));
 }
 
 __global__ void accept_rows_reset_kernel(SpecState s) {
@@ -1583,6 +1728,13 @@ bool filtered(const SpecState &s) {
 
 int g_accept_early = 1;
 int g_accept_split = 1;
+
+void launch_mt_seed(hipStream_t st, const SpecState &s) {
+  NNHIP_REQUIRE(s.mt && s.mt_ring && s.mt_rw && s.B > 0, kErrArg,
+                "mt19937 stream: buffers not set");
+  hipLaunchKernelGGL(mt_seed_kernel, dim3(s.B), dim3(1024), 0, st, s);
+  NNHIP_CHECK(hipGetLastError());
+}
 
 void launch_first_token(hipStream_t st, const SpecState &s,
                         const float *logits, int64_t ldl) {

@@ -54,6 +54,11 @@ int or_generate_speculative(const or_model *target, const or_model *draft,
                             float top_p, uint64_t seed, int quantized_cache,
                             uint32_t seq_index, int32_t *out,
                             or_spec_stats *stats);
+int or_generate_advanced(const or_model *m, const int32_t *prompt, int P,
+                         int max_new, float temperature, int top_k,
+                         float top_p, uint64_t seed, uint32_t seq_index,
+                         int use_kv_cache, int32_t *out);
+void or_set_rng(int mode);
 void or_dense(const float *x, int64_t rows, int64_t in, int64_t out,
               const float *w, const int8_t *codes, const float *scales,
               const float *bias, float *y);
@@ -417,6 +422,28 @@ void test_decoder_adapter(HipBackend &hip) {
   const std::vector<size_t> prompt(ids.begin(), ids.begin() + 8);
   expect(t.generate_speculative(&d, prompt, 16, 3, 0.0f) == oracle_spec(ot, od, prompt, 16, 3),
          "HipDecoder::generate_speculative fp32 greedy == oracle");
+  // Sampled generation draws from std::mt19937 seeded with the seed, in the
+  // reference's order (HipBackend sets the library's "rng" option to 1): the
+  // ids of the oracle's run on that stream.  (Only a decision within fp32
+  // rounding of its boundary could part them; the models and seeds here are
+  // fixed, and none lies that close.)
+  or_set_rng(1);
+  {
+    std::vector<int32_t> p(prompt.begin(), prompt.end()), out(p.size() + 24);
+    or_spec_stats st;
+    or_generate_speculative(ot.m, od.m, p.data(), (int)p.size(), 24, 3, 1.0f,
+                            0, 1.0f, 1234, 0, 0, out.data(), &st);
+    expect(t.generate_speculative(&d, prompt, 24, 3, 1.0f, 0, 1.0f, 1234) ==
+               std::vector<size_t>(out.begin(), out.end()),
+           "HipDecoder::generate_speculative sampled == oracle on std::mt19937");
+    std::vector<int32_t> ar(p.size() + 20);
+    or_generate_advanced(ot.m, p.data(), (int)p.size(), 20, 0.9f, 0, 1.0f, 99,
+                         0, 1, ar.data());
+    expect(t.generate_advanced(prompt, 20, 0.9f, 0, 1.0f, 99, true) ==
+               std::vector<size_t>(ar.begin(), ar.end()),
+           "HipDecoder::generate_advanced sampled == oracle on std::mt19937");
+  }
+  or_set_rng(0);
   for (int bits : {8, 4}) {
     OracleModel qt(tc, 300, 0.1f), qd(dc, 400, 0.1f);
     or_model_quantize_bits(qt.m, bits);
