@@ -539,6 +539,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--no-mt19937", action="store_true",
+                    help="skip the decode loop on the reference's "
+                         "std::mt19937 generator")
     ap.add_argument("--no-kv-int8", action="store_true",
                     help="skip the secondary run with int8 KV caches "
                          "(generate_speculative(..., quantized_cache=true))")
@@ -619,6 +622,20 @@ def main():
                    "frac": round(r8["loop_GBs"] / HBM_PEAK_GBS, 4)},
                "attention": roofline_attention(ctx, q8=True),
                "verify_step": verify_step(ctx, r["models"][0], q8=True)}
+    # the same loop on the reference's generator (option "rng" 1: one
+    # std::mt19937 per sequence, drawn in the reference's order); its draws
+    # differ from the Philox stream's, so do the cycle count and acceptance
+    mt = None
+    if not a.no_mt19937:
+        ctx.set_option("rng", 1)
+        try:
+            rm = run_cfg4(ctx, 1, 1, models=r["models"])
+        finally:
+            ctx.set_option("rng", 0)
+        mt = {"value": round(rm["value"], 1), "unit": "tokens/s",
+              "decode_ms": round(rm["decode_ms"], 2), "cycles": rm["cycles"],
+              "ms_per_cycle": round(rm["decode_ms"] / rm["cycles"], 4),
+              "acceptance": round(rm["accepted"] / max(rm["drafted"], 1), 4)}
     b1 = None if a.no_batch1 else run_cfg2(ctx)
     cpu = None if a.no_cpu_baseline else cpu_baseline(r["models"])
     ms_step = r["wall_s"] / a.steps * 1e3
@@ -643,6 +660,7 @@ def main():
         "decode_ms_per_step": round(r["decode_ms"] / a.steps, 2),
         "prefill_ms": round(r["prefill_ms"], 2),
         "cycles": r["cycles"],
+        "ms_per_cycle": round(r["decode_ms"] / a.steps / r["cycles"], 4),
         "acceptance": round(r["accepted"] / max(r["drafted"], 1), 4),
         "ties": r["ties"],
         "loop_roofline": {"achieved_GBs": round(r["loop_GBs"], 1),
@@ -655,6 +673,7 @@ def main():
         "cfg3_attention": c3,
         "cfg5_accept": c5,
         "kv_int8": kv8,
+        "rng_mt19937": mt,
         "batch1": b1,
         "cpu_baseline": cpu,
     }

@@ -2,7 +2,8 @@
 
 * The batch-32 sampled speculative decode at full model size: target
   12L/1024/16h/4096/V32000 and draft 4L/512/8h/2048, int8 weights, prompts of
-  256 ids, k = 5, T = 1.0, Philox uniforms.  The device runs all 32
+  256 ids, k = 5, T = 1.0, Philox uniforms (and once more on the
+  reference's std::mt19937, two sequences compared).  The device runs all 32
   sequences in lockstep with the decode loop's own kernels (draft sampling
   from the draft lm head's tile statistics, the verify rows' statistics, the
   accept / residual kernel) over the full 128 new tokens; a stated subset
@@ -59,8 +60,16 @@ def cfg4(ctx):
     prompts = rng.integers(0, CFG4_T["vocab"], (B, P)).astype(np.int32)
     sampled = gt.generate_speculative_batch(gd, prompts, new, k, 1.0, seed)
     greedy = gt.generate_speculative_batch(gd, prompts, new, k, 0.0, seed)
+    # the same sampled run on the reference's generator (std::mt19937 per
+    # sequence, seeded seed + b)
+    ctx.set_option("rng", 1)
+    try:
+        sampled_mt = gt.generate_speculative_batch(gd, prompts, new, k, 1.0,
+                                                   seed)
+    finally:
+        ctx.set_option("rng", 0)
     yield dict(ot=ot, od=od, prompts=prompts, new=new, k=k, seed=seed,
-               sampled=sampled, greedy=greedy)
+               sampled=sampled, greedy=greedy, sampled_mt=sampled_mt)
     gt.free(); gd.free()
 
 
@@ -121,6 +130,30 @@ def test_cfg4_sampled_batch32_full_length_matches_oracle(cfg4, part):
         O.set_threads(1)
     # a divergence needs a decision within 1e-5 of its boundary: rare
     assert diverged <= 1
+
+
+def test_cfg4_mt19937_batch32_matches_oracle(cfg4):
+    """The batch-32 workload with the context option "rng" 1 (the
+    reference's std::mt19937, layer.cpp:1394): the first and the last
+    sequence to finish over all 128 new tokens against the oracle's
+    mt19937 runs (or_set_rng(1)), up to a recorded tie; the streams differ
+    from the Philox run's."""
+    got, stats, _ = cfg4["sampled_mt"]
+    assert not np.array_equal(got, cfg4["sampled"][0])
+    cyc = np.array([s.cycles for s in stats])
+    seqs = [int(np.argmin(cyc)), int(np.argmax(cyc))]
+    O.set_threads(THREADS)
+    O.set_rng(1)
+    try:
+        for b in seqs:
+            print(f"cfg4 mt19937: sequence {b} ({stats[b].cycles} cycles)",
+                  flush=True)
+            check_stream(cfg4["ot"], cfg4["od"], got[b], cfg4["prompts"][b],
+                         cfg4["new"], cfg4["k"], 1.0, cfg4["seed"], seq=b,
+                         dev=stats[b], what=f"cfg4 mt19937 b={b}")
+    finally:
+        O.set_rng(0)
+        O.set_threads(1)
 
 
 def test_cfg4_greedy_batch32_full_length_matches_oracle(cfg4):
