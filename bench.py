@@ -433,6 +433,26 @@ def traffic_probe():
         f"{attention_bytes(sh['B'], sh['S'], sh['H'], sh['D'], sh['n_cached'] + sh['S'])}")
 
 
+# the batch-32 cycle's attention launches at mid-run context: the verify
+# step (16 heads, k + 1 = 6 queries) and a drafting step (8 heads, 1 query)
+ATTN_PROBE_SHAPES = [("verify", B, K_LOOK + 1, 16, 64, P + NEW // 2),
+                     ("draft", B, 1, 8, 64, P + NEW // 2 + 30)]
+
+
+def attn_probe():
+    """For rocprofv3 --pmc runs: the verify and drafting attention
+    launches over fp32 and int8 KV rows, 50 launches each."""
+    ctx = nnhip.Context(0)
+    for name, b, s, h, d, n in ATTN_PROBE_SHAPES:
+        for q8 in (False, True):
+            ms = nnhip.bench_attention(ctx, b, s, h, d, n, iters=50, nbuf=4,
+                                       quantized=q8)
+            byt = attention_bytes(b, s, h, d, n + s, q8)
+            log(f"{name} attention {'int8' if q8 else 'fp32'} rows: "
+                f"{ms * 1e3:.2f} us, {byt} algorithmic bytes, "
+                f"{byt / (ms / 1e3) / 1e9:.1f} GB/s")
+
+
 def copy_calibration():
     """A plain device copy of 256 MiB, three times: the reference point for
     scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -554,6 +574,9 @@ def main():
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only run the copy calibration and the cycle's GEMM "
                          "shapes (for rocprofv3 --pmc)")
+    ap.add_argument("--attn-probe", action="store_true",
+                    help="only the attention launches of the cycle over fp32 "
+                         "and int8 KV rows (for rocprofv3 --pmc)")
     ap.add_argument("--cfg5-probe", action="store_true",
                     help="only run the acceptance microbench (for "
                          "rocprofv3 --kernel-trace)")
@@ -587,6 +610,9 @@ def main():
         return
     if a.cfg5_probe:
         cfg5_probe()
+        return
+    if a.attn_probe:
+        attn_probe()
         return
     ctx = nnhip.Context(0)
     if a.no_graphs:

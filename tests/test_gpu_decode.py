@@ -284,7 +284,7 @@ def test_causal_independence(ctx):
 def test_capacity_rule_matches_oracle(ctx, quant_cache):
     """The reference throws when a forward's S_past + S exceeds max_seq_len
     (layer.cpp:1171-1179), except with int8 caches, whose length it never
-    reads.  Around the boundary max_seq = P + max_new -- where
+    reads (caches[0].k is null there).  Around the boundary max_seq = P + max_new -- where
     the target fits and the draft cache, which gains one duplicate per
     rejection, may not -- the device fails (ECAPACITY) exactly when the
     oracle does, and otherwise returns the oracle's stream."""

@@ -389,7 +389,7 @@ def test_max_seq_len_throws():
 def test_int8_cache_skips_the_length_check():
     """layer.cpp:1171-1179 reads S_past from caches[0].k, which an int8
     cache leaves null: the check never fires and the cache grows past
-    max_seq_len (SURVEY Q7), while an fp32 cache throws at the same length.
+    max_seq_len, while an fp32 cache throws at the same length.
     Past max_seq_len the int8-cache forward equals a no-cache forward of
     the same ids on a model with room (attention over the dequantised
     rows within 0.08, gqa_test.cpp:213-265's bound)."""
@@ -480,7 +480,8 @@ def _trace_draft_cache(prompt, first, cycles, draft, what):
 
 @pytest.mark.parametrize("T", [1.0, 0.0])
 def test_draft_cache_duplicate_rule_hand_traced(T):
-    """The oracle's draft-side state pinned by a hand trace of
+    """The oracle's draft-side state (the draft cache after each cycle's
+    rollback and catch-up) pinned by a hand trace of
     the reference: after a rejection the draft cache holds the recovered
     token twice and later draft positions drift by one
     (layer.cpp:1541-1545, 1632-1642); after full acceptance it does not
