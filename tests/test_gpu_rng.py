@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 import oracle_py as O
+from gpu_util import nnhip
 from test_gpu_decode import TILE_D, TILE_T, TOY_D, TOY_T, check_stream, spec_pair
 
 pytestmark = pytest.mark.gpu
@@ -144,3 +145,28 @@ def test_mt_mode_leaves_greedy_and_philox_streams(ctx):
     assert not np.array_equal(runs[0][1], runs[1][1])
     check_stream(ot, od, runs[0][1], prompt, 48, 4, 1.0, 3)
     gt.free(); gd.free()
+
+
+def test_mt_generate_advanced_without_cache_and_bad_option(ctx):
+    """generate_advanced(use_kv_cache = false) draws the same doubles in the
+    same order (layer.cpp:1269-1372); an rng value other than 0 or 1 is
+    refused with NNHIP_EARG and leaves the context's stream unchanged."""
+    ot, gt, _, gd = spec_pair(ctx, TOY_T, TOY_D, 52, False, std=0.3)
+    rng = np.random.default_rng(53)
+    prompt = rng.integers(0, 256, 9).astype(np.int32)
+    ctx.set_option("rng", 1)
+    O.set_rng(1)
+    try:
+        got = gt.generate_advanced(prompt, 30, 1.0, seed=11, use_kv_cache=False)
+        want = O.generate_advanced(ot, prompt, 30, 1.0, 11, use_cache=False)
+        np.testing.assert_array_equal(got, want)
+        with pytest.raises(nnhip.NNHipError) as e:
+            ctx.set_option("rng", 2)
+        assert e.value.code == -1
+        again = gt.generate_advanced(prompt, 30, 1.0, seed=11, use_kv_cache=False)
+        np.testing.assert_array_equal(again, got)
+    finally:
+        ctx.set_option("rng", 0)
+        O.set_rng(0)
+    gt.free(); gd.free()
+
