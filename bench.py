@@ -213,7 +213,7 @@ def roofline_attention(ctx, w4=True, q8=False):
         return dict(achieved=round(ach, 1), frac=round(ach / HBM_PEAK_GBS, 4),
                     unit="GB/s", bytes_per_launch=byt,
                     us_per_launch=round(ms * 1e3, 2),
-                    kernel="attn_kernel<8, 8, 4, int8 rows>")
+                    kernel="attn_kernel<8, 8, 4, int8 rows> (scores on the int8 MFMA)")
     return dict(bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS,
                 unit="GB/s", frac=round(ach / HBM_PEAK_GBS, 4),
                 traffic=measured_traffic(),

@@ -205,6 +205,10 @@ __global__ __launch_bounds__(256) void rope_kv_q8_kernel(
 //    p ^ (g8(sub) & (SQP-1)) with g8(s) = s ^ 3 * bit2(s).
 //  * Softmax: per-query running max across chunks (online rescale), chunk
 //    probabilities written to LDS as [key][query].
+//    With int8 rows, 5-8 queries of 64 dims and merged splits (the verify
+//    step over an int8 cache), the scores are one int8 MFMA product per
+//    chunk instead: the queries in three digit planes against the K codes
+//    as stored (see MS in attn_kernel).
 //  * PV: lane (r, dq) owns dims 4dq..4dq+3 of keys c0 + r + kpi*t, with
 //    kpi = 256 / D key rows per wave instruction; the SQP probabilities of a
 //    key are one broadcast LDS read.
@@ -323,6 +327,12 @@ __device__ __forceinline__ float code_at(uint32_t w, int i) {
 // A chunk's K rows in flight: fp32 dims, or codes and the rows' scales.
 template <bool Q8> struct KChunk { float kr[4][8]; };
 template <> struct KChunk<true> { uint32_t kc[4][2]; float ks[4]; };
+// ... for the int8 MFMA scores: lane (c, hh) holds key c's codes for dims
+// [32 s + 16 hh, +16), s = 0, 1 (the B operand of two 32-dim steps), and
+// that key's scale
+typedef int attn_v4i __attribute__((ext_vector_type(4)));
+typedef int attn_v16i __attribute__((ext_vector_type(16)));
+struct KChunkMfma { attn_v4i kb[2]; float ks; };
 
 template <int SQP, int DL, int W, bool Q8>
 __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
@@ -373,12 +383,51 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
   const int r = min(lane / NQ4, KPI - 1), dq = lane % NQ4;
   const bool pv_lane = lane < KPI * NQ4;
 
-  float qv[SQP][8];
+  // int8 rows, up to 8 queries of 64 dims, merged key splits: the scores on
+  // the int8 MFMA (v_mfma_i32_32x32x32_i8).  A operand: the queries as three
+  // digit planes (act_quant's rule: one exponent e per query row, X =
+  // rint(q 2^e) in balanced base-256 digits; rows 8-31 zero); B operand: a
+  // chunk's 32 K rows' codes as stored.  Each score is the exact integer
+  // total sum_x X_x code_x, scaled by 2^-e and the K row's scale.  The
+  // softmax and the PV products are those of the other path.
+  constexpr bool MS = Q8 && SQP == 8 && DL == 8 && W > 1;
+  const int kc_ = lane & 31, hh = lane >> 5;   // MS: key / query row, half
+  float qv[MS ? 1 : SQP][8];
+  attn_v4i qa[MS ? kLimbs : 1][2];
+  int eq4[4];                                  // MS: exponents of queries 4 hh + j
+  if constexpr (MS) {
+    float f[2][16];
+    float mx = 0.f;
+    const bool qok = kc_ < nq;
+    const float *qrow = q + ((int64_t)b * S + q0 + min(kc_, nq - 1)) * E + h * D;
 #pragma unroll
-  for (int p = 0; p < SQP; ++p) {
-    const int qi = p ^ myq;
-    load_lane_dims<DL>(q + ((int64_t)b * S + q0 + min(qi, nq - 1)) * E + h * D,
-                       sub, qv[p]);
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(qrow + 32 * s2 + 16 * hh + 4 * i);
+        f[s2][4 * i] = qok ? v4.x : 0.f; f[s2][4 * i + 1] = qok ? v4.y : 0.f;
+        f[s2][4 * i + 2] = qok ? v4.z : 0.f; f[s2][4 * i + 3] = qok ? v4.w : 0.f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) mx = fmaxf(mx, fabsf(f[s2][4 * i + x]));
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const int e = digit_exponent(mx);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int3 t = digits4(&f[s2][4 * i], e);
+        qa[0][s2][i] = t.x; qa[1][s2][i] = t.y; qa[2][s2][i] = t.z;
+      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) eq4[j] = __shfl(e, 4 * hh + j, kWave);
+  } else {
+#pragma unroll
+    for (int p = 0; p < SQP; ++p) {
+      const int qi = p ^ myq;
+      load_lane_dims<DL>(q + ((int64_t)b * S + q0 + min(qi, nq - 1)) * E + h * D,
+                         sub, qv[p]);
+    }
   }
   float acc[SQP][4];
 #pragma unroll
@@ -386,6 +435,8 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
 #pragma unroll
     for (int x = 0; x < 4; ++x) acc[i][x] = 0.f;
   float m_run = -INFINITY, l_loc = 0.f;
+  // MS: running max and partial sum of queries 4 hh + j (this lane's keys)
+  float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, l4[4] = {0.f, 0.f, 0.f, 0.f};
 
   // A chunk's K and V rows are all requested before any arithmetic; rows
   // past the split end re-read the last valid row and are masked.  The
@@ -393,18 +444,28 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
   // (two register buffers, used in turn); its V rows, needed only after the
   // scores, at the start of its own turn.  An int8 row enters as
   // (float)code * scale per element, the product layer.cpp:886-887 and
-  // :932-934 form.
-  using Chunk = KChunk<Q8>;
+  // :932-934 form (the V rows always; the K rows except on the MFMA score
+  // path, whose exact integer totals are scaled once per key).
+  using Chunk = std::conditional_t<MS, KChunkMfma, KChunk<Q8>>;
   auto load_chunk = [&](int c0, Chunk &ck) {
+    if constexpr (MS) {
+      // lane (c, hh): key c0 + c's codes for dims 16 hh .. and 32 + 16 hh ..
+      const int j = min(c0 + kc_, kend - 1);
+      const int8_t *kr8 = reinterpret_cast<const int8_t *>(kb) + (int64_t)j * D + 16 * hh;
+      ck.kb[0] = *reinterpret_cast<const attn_v4i *>(kr8);
+      ck.kb[1] = *reinterpret_cast<const attn_v4i *>(kr8 + 32);
+      ck.ks = ksb[j];
+    } else {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int j = min(c0 + g + 8 * t, kend - 1);
-      if constexpr (Q8) {
-        load_lane_codes<DL>(kb + (int64_t)j * D, sub, ck.kc[t]);
-        ck.ks[t] = ksb[j];
-      } else {
-        if (nt) load_lane_dims_stream<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
-        else load_lane_dims<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+      for (int t = 0; t < 4; ++t) {
+        const int j = min(c0 + g + 8 * t, kend - 1);
+        if constexpr (Q8) {
+          load_lane_codes<DL>(kb + (int64_t)j * D, sub, ck.kc[t]);
+          ck.ks[t] = ksb[j];
+        } else {
+          if (nt) load_lane_dims_stream<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+          else load_lane_dims<DL>(kb + (int64_t)j * D, sub, ck.kr[t]);
+        }
       }
     }
   };
@@ -420,10 +481,12 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
         vw[t] = *reinterpret_cast<const uint32_t *>(vb + (int64_t)row * D + dq * 4);
         vsc[t] = vsb[row];
       }
+      if constexpr (!MS) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int x = 0; x < 8; ++x) kr[t][x] = code_at(ck.kc[t][x >> 2], x & 3) * ck.ks[t];
+          for (int x = 0; x < 8; ++x) kr[t][x] = code_at(ck.kc[t][x >> 2], x & 3) * ck.ks[t];
+      }
 #pragma unroll
       for (int t = 0; t < TPV; ++t)
         vv[t] = make_float4(code_at(vw[t], 0) * vsc[t], code_at(vw[t], 1) * vsc[t],
@@ -439,6 +502,44 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
         vv[t] = nt ? ld_stream4(pv) : *reinterpret_cast<const float4 *>(pv);
       }
     }
+    if constexpr (MS) {
+      // the chunk's scores: rows 4 hh + j (j < 4) of key c0 + c in lane
+      // (c, hh)'s accumulator entries j; the chunk maximum of each query
+      // over the 32 lanes of its half, then the online softmax as below
+      attn_v16i sacc[kLimbs];
+#pragma unroll
+      for (int l = 0; l < kLimbs; ++l) sacc[l] = attn_v16i{};
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int l = 0; l < kLimbs; ++l)
+          sacc[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa[l][s2], ck.kb[s2], sacc[l], 0, 0, 0);
+      const int key = c0 + kc_;
+      float p4[4], al4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int qq = 4 * hh + j;
+        const double tot = fma((double)sacc[0][j], 65536.0,
+                               fma((double)sacc[1][j], 256.0, (double)sacc[2][j]));
+        const bool valid = qq < nq && key < kend && key <= pos0 + qq;
+        const float scj = valid ? ((float)ldexp(tot, -eq4[j]) * ck.ks) * qscale : -INFINITY;
+        float cmj = scj;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) cmj = fmaxf(cmj, __shfl_xor(cmj, o, kWave));
+        const float mn = fmaxf(m4[j], cmj);
+        const float ms = (mn == -INFINITY) ? 0.f : mn;
+        al4[j] = __builtin_amdgcn_exp2f(m4[j] - ms);   // 0 at start
+        m4[j] = mn;
+        p4[j] = __builtin_amdgcn_exp2f(scj - ms);      // 0 if masked
+        l4[j] = l4[j] * al4[j] + p4[j];
+      }
+      *reinterpret_cast<float4 *>(s_buf + kc_ * SQP + 4 * hh) =
+          make_float4(p4[0], p4[1], p4[2], p4[3]);
+      if (kc_ == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_alpha[wv][4 * hh + j] = al4[j];
+      }
+    } else {
     // scores of this lane's query for keys c0 + g + 8t
     float sc[4], cm = -INFINITY;
 #pragma unroll
@@ -490,6 +591,7 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
     }
     l_loc = l_loc * alpha + ps;
     if (uniq && g == 0) s_alpha[wv][myq] = alpha;
+    }
     wave_lds_sync();
     float al[SQP];
 #pragma unroll
@@ -534,6 +636,16 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
     work_chunk(c0 + kChunk, cb);
   }
   const float l = groups_sum(l_loc);
+  float lq4[4];                               // MS: each query's sum over its keys
+  if constexpr (MS) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = l4[j];
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) v += __shfl_xor(v, o, kWave);
+      lq4[j] = v;
+    }
+  }
   if (pv_lane) {
 #pragma unroll
     for (int i = 0; i < SQP; ++i)
@@ -552,7 +664,18 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
       for (int rr = 0; rr < KPI; ++rr) s += s_buf[(rr * SQP + i) * D + dd];
       s_buf[i * D + dd] = s;
     }
-    if (uniq && g == 0) { s_ml[wv][myq][0] = m_run; s_ml[wv][myq][1] = l; }
+    if constexpr (MS) {
+      if (kc_ == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s_ml[wv][4 * hh + j][0] = m4[j];
+          s_ml[wv][4 * hh + j][1] = lq4[j];
+        }
+      }
+    } else if (uniq && g == 0) {
+      s_ml[wv][myq][0] = m_run;
+      s_ml[wv][myq][1] = l;
+    }
     __syncthreads();
     const int E = H * D;
     for (int t = threadIdx.x; t < nq * D; t += kWave * W) {
