@@ -280,8 +280,6 @@ void Model::reserve(int rows, int lrows, int max_keys) {
     ws.ctx.alloc((size_t)r * d); ws.h.alloc((size_t)r * d);
     ws.x1.alloc((size_t)r * d);
     ws.qkv.alloc((size_t)r * 3 * d);
-    ws.tot.alloc((size_t)r * d);
-    NNHIP_CHECK(hipMemsetAsync(ws.tot.p, 0, ws.tot.bytes(), ctx->stream));
     ws.ff.alloc((size_t)r * F);
     ws.mpad = round_up(r, 64);
     ws.limbs.alloc((size_t)kLimbs * ws.mpad * std::max(d, F));

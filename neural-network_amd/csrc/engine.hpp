@@ -43,7 +43,6 @@ struct LayerW {
 struct Workspace {
   int rows = 0, lrows = 0;
   DevBuf<float> x, qkv, qrot, ctx, h, x1, ff, logits, part;
-  DevBuf<long long> tot;   // [rows][d] split-K totals, kept zeroed
   DevBuf<int8_t> limbs;
   DevBuf<int> rexp;
   DevBuf<int> hexp;        // [mpad][H] per-(row, head) digit exponents
