@@ -349,7 +349,8 @@ int nnhip_sample_rows(nnhip_ctx *ctx, const float *logits, int B, int V,
  * [B][k], accept uniforms [B][k] (in place of the Philox slots k + j),
  * resample uniforms [B] (slot 2k).  n_accept [B]; next_tok [B] = resampled
  * id, or -1 when all k are accepted (no target row k for a bonus sample).
- * Allocates its scratch and returns with the results written. */
+ * Allocates its scratch on the first call of a (B, k, V) and keeps it in
+ * the context for the next such call; returns with the results written. */
 int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
                       const float *dlogits, const int32_t *dtok,
                       const float *u_accept, const float *u_resample, int B,

@@ -766,8 +766,15 @@ int nnhip_spec_accept(nnhip_ctx *ctx, const float *tlogits,
     hipStream_t st = ctx->c.stream;
     // the draft rows' get_probs as the loop's drafting steps leave them:
     // their logits and 128-column tile statistics, each probability formed
-    // where the accept step reads it
-    nnhip::AcceptRows ar(B, k, V, temperature);
+    // where the accept step reads it.  The state of the last call's sizes
+    // is reused (the previous call has synchronized the stream).
+    if (!ctx->accept || ctx->acc_B != B || ctx->acc_k != k || ctx->acc_V != V) {
+      ctx->accept.reset();
+      ctx->accept.reset(new nnhip::AcceptRows(B, k, V, temperature));
+      ctx->acc_B = B; ctx->acc_k = k; ctx->acc_V = V;
+    }
+    nnhip::AcceptRows &ar = *ctx->accept;
+    ar.s.T = temperature;
     ar.launch_logits(st, tlogits, dlogits, dtok, u_accept, u_resample,
                      n_accept, next_tok);
     NNHIP_CHECK(hipStreamSynchronize(st));

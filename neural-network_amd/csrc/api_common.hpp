@@ -25,6 +25,10 @@ struct nnhip_ctx {
     nnhip::DevBuf<float> c, s;
   } rope[4];
   nnhip::DevBuf<float> part;
+  // nnhip_spec_accept's state and scratch, kept for the next call of the
+  // same (B, k, V) (every call resets the state and synchronizes the stream)
+  std::unique_ptr<nnhip::AcceptRows> accept;
+  int acc_B = 0, acc_k = 0, acc_V = 0;
 };
 struct nnhip_model {
   std::unique_ptr<nnhip::Model> m;
