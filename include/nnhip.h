@@ -53,6 +53,12 @@ typedef struct {
  * 20-33): allocate, copy_host_to_device, copy_to_device,
  * copy_device_to_host; DeviceBuffer (backend.hpp:9-18) is a dev pointer. */
 const char *nnhip_last_error(void);
+/* nnhip_init makes `device` the calling thread's current device and gives
+ * the context its own stream on it.  Calls on a context launch on that
+ * stream; the scratch some of them allocate (grown on demand) is allocated
+ * on the current device, so a thread that switches devices makes the
+ * context's device current again before calling on it (nnhip_malloc,
+ * nnhip_decoder_create and nnhip_destroy select it themselves). */
 int nnhip_init(int device, nnhip_ctx **out);
 int nnhip_destroy(nnhip_ctx *ctx);
 /* "graphs": 1 = replay each speculative cycle as one HIP graph (default).
