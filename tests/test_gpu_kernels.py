@@ -676,6 +676,19 @@ def test_spec_accept_vs_oracle(ctx, T, corr):
         assert n.max() >= 3          # the correlated case accepts runs
 
 
+def test_spec_accept_kept_state_across_sizes(ctx):
+    """nnhip_spec_accept keeps its state and scratch in the context for the
+    next call of the same (B, k, V): calls of sizes A, B, A again and of A
+    at another temperature on one context each agree with the oracle, and
+    the repeated call with A's inputs gives A's first results."""
+    n1, t1 = accept_case(ctx, 24, 6, 5000, 1.0, 0.9, seed=5)
+    n2, t2 = accept_case(ctx, 8, 3, 700, 0.8, 0.9, seed=6)
+    n3, t3 = accept_case(ctx, 24, 6, 5000, 1.0, 0.9, seed=5)
+    n4, t4 = accept_case(ctx, 24, 6, 5000, 0.0, 0.9, seed=7)
+    np.testing.assert_array_equal(n1, n3)
+    assert t1 + t2 + t3 + t4 <= 2
+
+
 @pytest.mark.parametrize("V", [4097, 1000, 130])
 def test_spec_accept_odd_vocab(ctx, V):
     """Vocabularies whose rows are not 8-byte aligned (odd V: the draft
