@@ -94,6 +94,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * the LDS GEMM digitising the context rows (default 256; process-wide).
  * "gemv_down_rows": the down projection of up to this many rows runs on the
  * GEMV over the fp32 SwiGLU rows (default 64; process-wide).
+ * "gemv_ln": Linear layers on the GEMV (short rows) over a LayerNorm's
+ * output: 0 = the LayerNorm as a launch of its own before the GEMV
+ * (default), 1 = formed in the GEMV's prologue (process-wide).
  * "ln_split": 1 = LayerNorm rows of 512 / 1024 spread over 2 / 4 waves
  * (default), 0 = one wave per row (process-wide).
  * No option changes results beyond fp32 rounding order. */

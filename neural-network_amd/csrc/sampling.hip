@@ -1763,7 +1763,9 @@ void launch_draft_sample(hipStream_t st, const SpecState &s, int j,
 // the accept step after the row statistics: accept_kernel, or its split
 // form when the state carries the split's scratch
 void launch_accept_step(hipStream_t st, const SpecState &s, const float *tlogits) {
-  if (s.rec && s.chunks) {
+  // greedy decoding draws nothing: the one-launch accept step (the split
+  // form's chunk sums serve only the residual / bonus draw)
+  if (s.rec && s.chunks && s.T > 0.f) {
     hipLaunchKernelGGL(accept_decide_kernel, dim3(s.B), dim3(kThreads), 0, st, s,
                        tlogits);
     NNHIP_CHECK(hipGetLastError());

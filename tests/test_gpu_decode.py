@@ -116,6 +116,29 @@ def test_forward_vs_oracle(ctx, quant, S):
     gm.free()
 
 
+@pytest.mark.parametrize("quant", [False, True])
+def test_forward_gemv_layernorm_forms(ctx, quant):
+    """Rows on the GEMV (1 and 5 rows a sequence): the LayerNorms as
+    launches of their own before plain GEMVs (default) and in the GEMVs'
+    prologues (option gemv_ln = 1), both within 1e-4 of a row of the
+    oracle's forward and within 1e-5 of each other."""
+    om, gm, _ = build(ctx, TOY_T, 21, quant, std=0.05)
+    rng = np.random.default_rng(22)
+    for S in (1, 5):
+        ids = rng.integers(0, 256, (1, S)).astype(np.int32)
+        sep = gm.forward(ids)
+        ctx.set_option("gemv_ln", 1)
+        try:
+            pro = gm.forward(ids)
+        finally:
+            ctx.set_option("gemv_ln", 0)
+        want = om.forward(ids[0])
+        assert_rows_close(sep[0], want, 1e-4, f"separate S={S}")
+        assert_rows_close(pro[0], want, 1e-4, f"prologue S={S}")
+        assert_rows_close(sep[0], pro[0], 1e-5, f"forms S={S}")
+    gm.free()
+
+
 # one layer at the batch-32 config's width (d 1024, 16 heads, MLP 4096)
 WIDE = dict(vocab=512, d=1024, H=16, F=4096, L=1)
 
