@@ -95,8 +95,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * "gemv_down_rows": the down projection of up to this many rows runs on the
  * GEMV over the fp32 SwiGLU rows (default 64; process-wide).
  * "gemv_ln": Linear layers on the GEMV (short rows) over a LayerNorm's
- * output: 0 = the LayerNorm as a launch of its own before the GEMV
- * (default), 1 = formed in the GEMV's prologue (process-wide).
+ * output form the LayerNorm in the GEMV's prologue up to this many rows
+ * (default 2); more rows get a LayerNorm launch of their own before the
+ * GEMV (process-wide).
  * "ln_split": 1 = LayerNorm rows of 512 / 1024 spread over 2 / 4 waves
  * (default), 0 = one wave per row (process-wide).
  * No option changes results beyond fp32 rounding order. */

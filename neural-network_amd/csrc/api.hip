@@ -99,7 +99,10 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
       REQ(value >= 0, "o_limb_rows must be >= 0");
       nnhip::g_o_limb_rows = value;
     }
-    else if (std::strcmp(key, "gemv_ln") == 0) nnhip::g_gemv_ln = value != 0;
+    else if (std::strcmp(key, "gemv_ln") == 0) {
+      REQ(value >= 0, "gemv_ln must be >= 0");
+      nnhip::g_gemv_ln = value;
+    }
     else if (std::strcmp(key, "o_head_digits") == 0) nnhip::g_o_head_digits = value != 0;
     else if (std::strcmp(key, "persistent_draft") == 0) nnhip::g_persistent_draft = value != 0;
     else if (std::strcmp(key, "kv_stream") == 0) {

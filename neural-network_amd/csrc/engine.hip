@@ -13,7 +13,7 @@ int g_o_limb_rows = 256;
 int g_persistent_draft = 0;
 int g_gemv_down_rows = 64;
 int g_o_head_digits = 1;
-int g_gemv_ln = 0;
+int g_gemv_ln = 2;
 
 namespace {
 
@@ -405,10 +405,12 @@ void Model::linear_in(const Linear &ln, const float *x, int64_t ldx,
   }
   NNHIP_REQUIRE(!ts || !ts->out, kErrArg,
                 "linear_in: tile statistics need the LDS-resident GEMM");
-  // short rows: the LayerNorm in the GEMV's prologue only with g_gemv_ln
-  // (every workgroup of the GEMV forms the rows' statistics again; a
-  // LayerNorm launch before a plain GEMV measured faster in the batch-1 loop)
-  if (pn && g_gemv_ln && !use_limbs(ln, rows) && ln.K <= 1024 &&
+  // short rows: the LayerNorm in the GEMV's prologue only up to g_gemv_ln
+  // rows (every workgroup of the GEMV forms the rows' statistics again: for
+  // the batch-1 draft's one or two rows that costs less than a launch, for
+  // the verify step's five a LayerNorm launch before a plain GEMV measured
+  // faster)
+  if (pn && rows <= g_gemv_ln && !use_limbs(ln, rows) && ln.K <= 1024 &&
       ln.K % 4 == 0 && pn->ldh % 4 == 0 && (!pn->out || pn->ldo % 4 == 0)) {
     // short rows on the GEMV: the LayerNorm is its prologue
     GemvLn lf;
@@ -616,7 +618,7 @@ void Model::forward(KVCache *cache, int b_off, const int32_t *ids,
       if (last_only) { pn.h = ws.h.p + (int64_t)(S - 1) * d; pn.ldh = (int64_t)S * d; }
       linear_in(lm, nullptr, 0, &pn, rows, false, nullptr, 0, logits, ldl,
                 kEpiBias, nullptr, ts);
-    } else if (g_gemv_ln && !use_limbs(lm, rows) && d <= 1024 &&
+    } else if (rows <= g_gemv_ln && !use_limbs(lm, rows) && d <= 1024 &&
                d % 4 == 0) {
       // short rows on the GEMV: the last norm2 is its prologue
       NNHIP_REQUIRE(!ts || !ts->out, kErrArg,

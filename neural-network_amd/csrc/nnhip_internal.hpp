@@ -302,8 +302,9 @@ extern int g_persistent_draft; // 1 = short batches run their decoder layers as
                                // one persistent kernel (draft_layers.hip);
                                // 0 (default): the per-kernel path
 extern int g_gemv_down_rows; // down projection on the GEMV up to this many rows
-extern int g_gemv_ln;    // 1 = a GEMV over LN(h) forms the LayerNorm in its
-                         // prologue; 0 (default) = a LayerNorm launch before it
+extern int g_gemv_ln;    // a GEMV over LN(h) of up to this many rows (default
+                         // 2) forms the LayerNorm in its prologue; more rows
+                         // get a LayerNorm launch before it
 extern int g_o_head_digits; // 1 = the merged attention writes the output
                             // projection's digits per head (64-wide heads)
 extern int g_o_limb_rows; // output projection after merged attention: digit

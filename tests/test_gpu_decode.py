@@ -118,20 +118,21 @@ def test_forward_vs_oracle(ctx, quant, S):
 
 @pytest.mark.parametrize("quant", [False, True])
 def test_forward_gemv_layernorm_forms(ctx, quant):
-    """Rows on the GEMV (1 and 5 rows a sequence): the LayerNorms as
-    launches of their own before plain GEMVs (default) and in the GEMVs'
-    prologues (option gemv_ln = 1), both within 1e-4 of a row of the
+    """Rows on the GEMV (1, 2 and 5 rows a sequence): the LayerNorms as
+    launches of their own before plain GEMVs (option gemv_ln = 0) and in
+    the GEMVs' prologues (gemv_ln = 16), both within 1e-4 of a row of the
     oracle's forward and within 1e-5 of each other."""
     om, gm, _ = build(ctx, TOY_T, 21, quant, std=0.05)
     rng = np.random.default_rng(22)
-    for S in (1, 5):
+    for S in (1, 2, 5):
         ids = rng.integers(0, 256, (1, S)).astype(np.int32)
-        sep = gm.forward(ids)
-        ctx.set_option("gemv_ln", 1)
         try:
+            ctx.set_option("gemv_ln", 0)
+            sep = gm.forward(ids)
+            ctx.set_option("gemv_ln", 16)
             pro = gm.forward(ids)
         finally:
-            ctx.set_option("gemv_ln", 0)
+            ctx.set_option("gemv_ln", 2)
         want = om.forward(ids[0])
         assert_rows_close(sep[0], want, 1e-4, f"separate S={S}")
         assert_rows_close(pro[0], want, 1e-4, f"prologue S={S}")
