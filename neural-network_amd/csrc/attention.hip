@@ -26,6 +26,9 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kMaxQ = 8;       // queries per workgroup
+// attn_q4: launches of fewer (sequence, head) units than this take 5-8
+// queries in two blocks of 4
+constexpr int kAttnQ4MaxUnits = 64;
 constexpr int kMaxD = 64;      // head dim handled by the attention kernel
 
 // Embedding gather (cpu_backend.cpp:1020-1025): ids outside [0, vocab) read
@@ -362,7 +365,9 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
   const int g8 = sub ^ (((sub >> 2) & 1) * 3);
   const int myq = g8 & (SQP - 1);
   const bool uniq = g8 < SQP;                 // one lane per (group, query)
-  const int q0 = qb * kMaxQ;
+  // query blocks of SQP (kMaxQ whenever a launch has more than one block,
+  // except the short launches of attn_q4: blocks of 4)
+  const int q0 = qb * SQP;
   const int nq = min(SQP, S - q0);
   const int E = H * D;
   const int hk = h / (H / Hkv);
@@ -996,6 +1001,7 @@ void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
 int g_attn_waves = 4096;
 int g_kv_stream = 1;
 int g_attn_w4 = 1;
+int g_attn_q4 = 1;
 int g_ln_split = 1;
 
 // Splits of the key range: about g_attn_waves waves over the whole launch
@@ -1039,8 +1045,8 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   NNHIP_REQUIRE(!limbs || ((H * D) % 128 == 0 && B * S <= mpad), kErrArg,
                 "attention: digit output needs H*D % 128 == 0");
   if (max_keys < 1) max_keys = 1;
-  const int nqb = (S + kMaxQ - 1) / kMaxQ;
-  const int sq = S < kMaxQ ? S : kMaxQ;
+  const int nqb_all = (S + kMaxQ - 1) / kMaxQ;
+  const int sq_all = S < kMaxQ ? S : kMaxQ;
   const float qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
   // stream the fp32 rows when the launch reads more than the L2s hold
   const double kv_bytes = 2.0 * B * Hkv * (double)std::min(max_keys, cap) * D *
@@ -1050,7 +1056,13 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
   if (attention_merged(D, max_keys)) {
     // one workgroup per (head, sequence, query block); its waves are the key
     // splits, merged in LDS, and the context rows are written directly, with
-    // hexp also their digits per head (exponent per row and head)
+    // hexp also their digits per head (exponent per row and head).  A launch
+    // of few workgroups (one sequence) with 5-8 queries takes them in blocks
+    // of 4 (option attn_q4): twice the workgroups, each with half the
+    // queries' products
+    const bool q4 = g_attn_q4 && S > 4 && S <= kMaxQ && B * H < kAttnQ4MaxUnits;
+    const int nqb = q4 ? 2 : nqb_all;
+    const int sq = q4 ? 4 : sq_all;
     NNHIP_REQUIRE(!hexp || (limbs && D == kWave && (H * D) % 128 == 0 && B * S <= mpad),
                   kErrArg, "attention: head digits need D == 64, H*D % 128 == 0");
     int8_t *hl = hexp ? limbs : nullptr;
@@ -1083,6 +1095,7 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
     NNHIP_CHECK(hipGetLastError());
     return false;
   }
+  const int nqb = nqb_all, sq = sq_all;
   int kps = 0;
   const int nsplit = attention_splits(B, S, H, max_keys, &kps);
   NNHIP_REQUIRE(part_elems >= attention_partial_elems(B, S, H, D, max_keys),
