@@ -74,9 +74,9 @@ int nnhip_destroy(nnhip_ctx *ctx);
  * "attn_waves": number of (key split) waves an attention launch aims for;
  * the key range of each sequence is split accordingly (default 4096;
  * process-wide).
- * "attn_q4": 1 = an attention launch of fewer than 64 (sequence, head)
- * pairs with 5-8 queries takes them in two workgroups of 4 queries each
- * (default); 0 = one workgroup of up to 8 (process-wide).
+ * "attn_short_q": queries per workgroup of an attention launch of fewer
+ * than 64 (sequence, head) pairs (one sequence's verify step): 1 (default),
+ * 2, 4, or 8 = one workgroup for up to 8 queries (process-wide).
  * "attn_w4": attention rows of 4+ queries run in workgroups of 4 key
  * splits (two per CU) instead of 8: 1 = when a launch has 128 or more
  * workgroups (default), 2 = always, 0 = never (process-wide).

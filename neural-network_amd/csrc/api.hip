@@ -83,7 +83,11 @@ int nnhip_set_option(nnhip_ctx *ctx, const char *key, int value) {
       nnhip::g_lds_min_rows = value;
     }
     else if (std::strcmp(key, "ln_split") == 0) nnhip::g_ln_split = value;
-    else if (std::strcmp(key, "attn_q4") == 0) nnhip::g_attn_q4 = value != 0;
+    else if (std::strcmp(key, "attn_short_q") == 0) {
+      REQ(value == 1 || value == 2 || value == 4 || value == 8,
+          "attn_short_q must be 1, 2, 4 or 8");
+      nnhip::g_attn_short_q = value;
+    }
     else if (std::strcmp(key, "attn_w4") == 0) {
       REQ(value >= 0 && value <= 2, "attn_w4 must be 0, 1 or 2");
       nnhip::g_attn_w4 = value;

@@ -26,9 +26,9 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kMaxQ = 8;       // queries per workgroup
-// attn_q4: launches of fewer (sequence, head) units than this take 5-8
-// queries in two blocks of 4
-constexpr int kAttnQ4MaxUnits = 64;
+// attn_short_q: launches of fewer (sequence, head) pairs than this take
+// their queries in blocks of g_attn_short_q
+constexpr int kAttnShortUnits = 64;
 constexpr int kMaxD = 64;      // head dim handled by the attention kernel
 
 // Embedding gather (cpu_backend.cpp:1020-1025): ids outside [0, vocab) read
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kWave * W, W == 4 ? 2 : 1) void attn_kernel(
   const int myq = g8 & (SQP - 1);
   const bool uniq = g8 < SQP;                 // one lane per (group, query)
   // query blocks of SQP (kMaxQ whenever a launch has more than one block,
-  // except the short launches of attn_q4: blocks of 4)
+  // except short launches: blocks of g_attn_short_q)
   const int q0 = qb * SQP;
   const int nq = min(SQP, S - q0);
   const int E = H * D;
@@ -1001,7 +1001,7 @@ void launch_rope_kv_q8(hipStream_t st, const float *qkv, int B, int S, int H,
 int g_attn_waves = 4096;
 int g_kv_stream = 1;
 int g_attn_w4 = 1;
-int g_attn_q4 = 1;
+int g_attn_short_q = 1;
 int g_ln_split = 1;
 
 // Splits of the key range: about g_attn_waves waves over the whole launch
@@ -1057,12 +1057,15 @@ bool launch_attention(hipStream_t st, const float *q, const KvSrc &kv, int B,
     // one workgroup per (head, sequence, query block); its waves are the key
     // splits, merged in LDS, and the context rows are written directly, with
     // hexp also their digits per head (exponent per row and head).  A launch
-    // of few workgroups (one sequence) with 5-8 queries takes them in blocks
-    // of 4 (option attn_q4): twice the workgroups, each with half the
-    // queries' products
-    const bool q4 = g_attn_q4 && S > 4 && S <= kMaxQ && B * H < kAttnQ4MaxUnits;
-    const int nqb = q4 ? 2 : nqb_all;
-    const int sq = q4 ? 4 : sq_all;
+    // of few (sequence, head) pairs (one sequence's verify or catch-up step)
+    // takes its queries in blocks of g_attn_short_q (default 1): more
+    // workgroups, each with fewer queries' products, the K / V rows read
+    // once per block (from L2 after the first)
+    const int qblk = g_attn_short_q;
+    const bool short_q = qblk < kMaxQ && S > qblk && S <= kMaxQ &&
+                         B * H < kAttnShortUnits;
+    const int nqb = short_q ? (S + qblk - 1) / qblk : nqb_all;
+    const int sq = short_q ? qblk : sq_all;
     NNHIP_REQUIRE(!hexp || (limbs && D == kWave && (H * D) % 128 == 0 && B * S <= mpad),
                   kErrArg, "attention: head digits need D == 64, H*D % 128 == 0");
     int8_t *hl = hexp ? limbs : nullptr;

@@ -296,8 +296,8 @@ extern int g_lds_min_rows;  // the LDS-resident GEMM from this many rows on
 constexpr int kGemmSlots = 256;
 extern int g_attn_waves; // attention: waves one launch aims for
 extern int g_ln_split;   // LayerNorm rows of 512 / 1024 over 2 / 4 waves
-extern int g_attn_q4;    // attention: a short launch (one sequence) takes 5-8
-                         // queries in two workgroups of 4
+extern int g_attn_short_q; // attention: queries per workgroup in a launch of
+                           // few (sequence, head) pairs (1, 2, 4 or 8)
 extern int g_attn_w4;    // attention: 4-wave merged workgroups for 4+ queries
                          // (1: launches of >= 128 workgroups, 2: always)
 extern int g_persistent_draft; // 1 = short batches run their decoder layers as

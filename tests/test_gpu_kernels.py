@@ -372,6 +372,61 @@ def test_attention_kq(ctx, B, S, H, D, pos0, w4):
                           out.reshape(S, H * D), 1e-4, f"attention seq {b}")
 
 
+def attention_case(ctx, B, S, H, D, pos0, q8, seed):
+    """One attention launch (fp32 or int8 cache, H_kv = H) against the
+    oracle's or_attention / or_attention_q8."""
+    rng = np.random.default_rng(seed)
+    pos0 = np.array(pos0, np.int32)
+    cap = int(pos0.max()) + S
+    q = rng.standard_normal((B * S, H * D)).astype(np.float32)
+    dq, dp = ctx.array(q), ctx.array(pos0)
+    do = ctx.array(shape=(B * S, H * D))
+    if q8:
+        kq = rng.integers(-127, 128, (B, H, cap, D)).astype(np.int8)
+        vq = rng.integers(-127, 128, (B, H, cap, D)).astype(np.int8)
+        ks = (rng.random((B, H, cap)) * 0.03 + 0.001).astype(np.float32)
+        vs = (rng.random((B, H, cap)) * 0.03 + 0.001).astype(np.float32)
+        dkq, dvq, dks, dvs = ctx.array(kq), ctx.array(vq), ctx.array(ks), ctx.array(vs)
+        call("nnhip_attention_kq_q8", ctx.h, dq.p, dkq.p, dks.p, dvq.p, dvs.p,
+             cap, dp.p, B, S, H, H, D, do.p)
+    else:
+        k = rng.standard_normal((B, H, cap, D)).astype(np.float32)
+        v = rng.standard_normal((B, H, cap, D)).astype(np.float32)
+        dk, dv = ctx.array(k), ctx.array(v)
+        call("nnhip_attention_kq", ctx.h, dq.p, dk.p, dv.p, cap, dp.p, B, S, H, H,
+             D, do.p)
+    got = do.numpy()
+    for b in range(B):
+        St = int(pos0[b]) + S
+        qb = np.ascontiguousarray(q[b * S:(b + 1) * S].reshape(S, H, D)
+                                  .transpose(1, 0, 2))
+        if q8:
+            out = O.attention_q8(qb, kq[b, :, :St], ks[b, :, :St], vq[b, :, :St],
+                                 vs[b, :, :St])
+        else:
+            out = np.zeros((S, H, D), np.float32)
+            O.lib().or_attention(O.fptr(qb), O.fptr(np.ascontiguousarray(k[b, :, :St])),
+                                 O.fptr(np.ascontiguousarray(v[b, :, :St])), H, H, S,
+                                 St, D, 1, O.fptr(out))
+        assert_rows_close(got[b * S:(b + 1) * S].reshape(S, H * D),
+                          out.reshape(S, H * D), 1e-4, f"attention seq {b}")
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("qblk", [1, 2, 4, 8])
+def test_attention_short_launch_query_blocks(ctx, qblk, q8):
+    """A launch of few (sequence, head) pairs takes its queries in blocks of
+    the option attn_short_q (one workgroup per block): 5 and 8 queries per
+    sequence over fp32 and int8 caches against the oracle, for every block
+    size."""
+    ctx.set_option("attn_short_q", qblk)
+    try:
+        for B, S, H, pos0 in ((1, 5, 8, [300]), (2, 8, 4, [0, 411])):
+            attention_case(ctx, B, S, H, 64, pos0, q8, seed=qblk * 10 + S)
+    finally:
+        ctx.set_option("attn_short_q", 1)
+
+
 # grouped-query attention (MultiHeadAttention's num_kv_heads, layer.cpp:
 # 862-864: query head h reads kv head h / (H / H_kv)): the shapes of
 # gqa_test.cpp:115-211 (4 heads on 2 kv heads, B = 2 x 3 queries, and one
