@@ -161,10 +161,11 @@ def test_forward_wide_vs_oracle(ctx):
 HEADS = dict(vocab=512, d=512, H=8, F=1024, L=2)
 
 
-@pytest.mark.parametrize("B,S", [(32, 1), (32, 6), (4, 40)])
+@pytest.mark.parametrize("B,S", [(32, 1), (32, 6), (4, 40), (4, 6)])
 def test_forward_head_digits_vs_oracle(ctx, B, S):
     """Rows of 64-wide heads after the merged attention (the drafting and
-    verify shapes): the attention writes the output projection's digit
+    verify shapes; (4, 6) a launch of few (sequence, head) pairs, one query
+    per workgroup): the attention writes the output projection's digit
     planes with one exponent per (row, head) and the digit-plane GEMM scales
     each head's exact total by its own exponent.  Against the oracle's
     forward (layer.cpp:1159-1216) within 1e-4 of a row, and against the
